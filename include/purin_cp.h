@@ -1,0 +1,247 @@
+/*
+ * purin_cp.h -- C ABI of the MI355X Chambolle--Pock projection library
+ * (libpurin_cp.so).
+ *
+ * Plain C: opaque plan handle, device pointers passed as void*, sizes as
+ * int64_t, HIP streams as void* (hipStream_t).  No torch / JAX types.
+ * Every array argument is a device pointer in batch-major row-major layout
+ * ((B, n) means sample-major, like the reference), of the plan's dtype unless
+ * stated otherwise.  The library never frees caller buffers.
+ *
+ * Reference interfaces each entry point replaces (paths are into the
+ * reference repository, SOULS-TAMU/Purin 1.0.2):
+ *   plan_create  <- PreparedChambollePockProjection.__post_init__ +
+ *                   prepare_bounds + BoundProjection.__init__
+ *                   (src/purin/solvers/chambolle_pock/solver.py:32-65,
+ *                    src/purin/solvers/chambolle_pock/bounds.py:18-33, 320-326)
+ *   spmm         <- _batched_local_jacobian_matvec / _transpose_matvec
+ *                   (src/purin/linalg/sparse/operators.py:507-533)
+ *   solve        <- the jitted custom_vjp ``solve`` -> sparse_cp
+ *                   (src/purin/solvers/chambolle_pock/bounds.py:42-78,
+ *                    src/purin/solvers/chambolle_pock/kernels.py:178-305)
+ *   project      <- BoundProjection.solve / PreparedChambollePockProjection._solve
+ *                   (src/purin/solvers/chambolle_pock/bounds.py:170-317,
+ *                    src/purin/solvers/chambolle_pock/solver.py:277-366)
+ *   adjoint      <- custom_vjp ``bwd`` (src/purin/solvers/chambolle_pock/bounds.py:80-165)
+ *                   with _batched_restarted_gmres
+ *                   (src/purin/solvers/primal_dual_interior_point/operators.py:792-1125)
+ *
+ * Errors: entry points return PURIN_CP_OK or an error code for invalid
+ * arguments / HIP failures (the reference raises ValueError for shape and
+ * configuration errors, bounds.py:176-188, config.py:50-61).  Numerical
+ * outcomes are never errors: they are reported per sample through status,
+ * finite, converged and valid arrays, as in the reference.
+ * purin_cp_last_error() returns a message for the calling thread's last error.
+ *
+ * Threading: calls on one plan must be ordered (same stream or externally
+ * synchronised); the plan owns one workspace.  All kernels are enqueued on the
+ * given stream; project/solve/adjoint synchronise that stream only to read
+ * their device-side stop flags.
+ */
+#ifndef PURIN_CP_H
+#define PURIN_CP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PURIN_CP_ABI_VERSION 1
+
+enum purin_cp_dtype { PURIN_CP_F32 = 0, PURIN_CP_F64 = 1 };
+
+enum purin_cp_error {
+  PURIN_CP_OK = 0,
+  PURIN_CP_ERR_ARG = 1,          /* invalid argument (ValueError in the reference) */
+  PURIN_CP_ERR_HIP = 2,          /* HIP runtime error */
+  PURIN_CP_ERR_UNSUPPORTED = 3,  /* option this build does not implement */
+  PURIN_CP_ERR_NOMEM = 4         /* device allocation failed */
+};
+
+/* SolveStatus codes (src/purin/solvers/types.py:36-43). */
+enum purin_cp_status {
+  PURIN_CP_CONVERGED = 0,
+  PURIN_CP_MAX_ITERATIONS = 1,
+  PURIN_CP_LINEAR_SOLVE_FAILURE = 2,
+  PURIN_CP_NONFINITE = 3
+};
+
+typedef struct purin_cp_plan purin_cp_plan;
+
+/* The ChambollePockConfig knobs fixed at preparation
+ * (src/purin/solvers/chambolle_pock/config.py:34-48). */
+typedef struct {
+  int32_t accelerated;              /* accelerated CP update (default 0) */
+  int32_t row_scaling;              /* constraint-row normalisation (default 1) */
+  int32_t norm_bound;               /* sparse norm bound for the steps (default 1) */
+  int32_t norm_iterations;          /* power iterations for the adjoint steps (default 20) */
+  int32_t norm_seed;                /* start-vector seed (default 42) */
+  int32_t diagonal_preconditioning; /* must be 0: not implemented (returns UNSUPPORTED) */
+  double safety;                    /* step safety factor in (0,1) (default 0.95) */
+} purin_cp_options;
+
+/* Fill *opts with the reference defaults. */
+void purin_cp_default_options(purin_cp_options* opts);
+
+/*
+ * Prepare a plan for one shared constraint matrix.
+ *   rows 0..me-1        equalities      K y == rhs
+ *   rows me..me+mi-1    inequalities    K y <= rhs
+ * given as a host CSR (indptr[me+mi+1], indices, values in float64; columns
+ * ascending within a row, as the reference's row supports).  Structural zeros
+ * are kept: a row's support decides whether it is a singleton bound row.
+ * Inequality rows with exactly one stored entry are presolved into variable
+ * bounds (bounds.py:320-326); the remaining rows ("kept rows", equalities
+ * first) enter the CP iteration.
+ */
+int purin_cp_plan_create(purin_cp_plan** plan, int32_t dtype, int64_t n, int64_t me,
+                         int64_t mi, const int64_t* indptr, const int32_t* indices,
+                         const double* values, const purin_cp_options* opts);
+
+void purin_cp_plan_destroy(purin_cp_plan* plan);
+
+typedef struct {
+  int32_t dtype;
+  int64_t n, me, mi;
+  int64_t kept_rows;        /* m: rows that enter the iteration (me + general inequalities) */
+  int64_t bound_rows;       /* presolved singleton inequality rows */
+  int64_t nnz_kept;
+  double norm;              /* L used by the forward steps */
+  double tau0, sigma0;      /* initial forward steps */
+  double adjoint_norm;      /* power-iteration L of the adjoint (bounds.py:88-101) */
+  double adjoint_tau, adjoint_sigma;
+  double tolerance_factor;  /* min(1, min_i scale_i): forward tolerance = tol * factor */
+} purin_cp_plan_info;
+
+int purin_cp_plan_get_info(const purin_cp_plan* plan, purin_cp_plan_info* info);
+
+/* Host copies of the kept-row indices (int64[m], original row numbers) and
+ * their row scales (double[m], 1/||K_i||_2 or 1). */
+int purin_cp_plan_kept_rows(const purin_cp_plan* plan, int64_t* rows, double* scale);
+
+/*
+ * Optional diagonal metric (WeightedDistance, src/purin/solvers/metric.py:87-182):
+ * the plan's matrix must already be the scaled one (coefficients times
+ * 1/sqrt(D_j)); this stores sqrt(D) (host, double[n]) so that project()
+ * multiplies targets by sqrt(D) on entry and divides y by it on exit, and
+ * adjoint() applies the matching chain rule.  Pass NULL to clear.
+ */
+int purin_cp_plan_set_metric(purin_cp_plan* plan, const double* sqrt_diagonal);
+
+/* First-kernel entry: out = K x (transpose = 0; x (B,n) -> out (B,m)) or
+ * K^T x (transpose = 1; x (B,m) -> out (B,n)) over the kept rows, with the
+ * row-scaled coefficients when scaled != 0. */
+int purin_cp_spmm(purin_cp_plan* plan, void* stream, int64_t batch, int32_t transpose,
+                  int32_t scaled, const void* x, void* out);
+
+/* Per-call options of solve/project. */
+typedef struct {
+  double tolerance;        /* ChambollePockConfig.tolerance (1e-9) */
+  int64_t max_iterations;  /* ChambollePockConfig.max_iterations (10000) */
+  int32_t early_stop;      /* 1: per-sample stop test each iteration (reference
+                              semantics); 0: run exactly max_iterations */
+  int32_t check_every;     /* iterations between reads of the all-done flag (0: 32) */
+  int32_t shared_bounds;   /* 1: lower/upper (or the bound-row rhs) are the same
+                              for every sample; only sample 0 is read */
+  int32_t timing;          /* 1: bracket every iteration kernel with HIP events on
+                              the call's stream (see purin_cp_last_timing) */
+} purin_cp_solve_options;
+
+void purin_cp_default_solve_options(purin_cp_solve_options* opts);
+
+/*
+ * Bytes of the state buffer that project()/solve() fill when ``saved`` is
+ * not NULL and that adjoint() reads (the custom_vjp residuals,
+ * bounds.py:74-78).  Layout is internal; the buffer must stay untouched
+ * between the forward and the adjoint call.
+ */
+int64_t purin_cp_saved_bytes(const purin_cp_plan* plan, int64_t batch);
+
+/*
+ * The inner CP solve on the kept rows in the plan's scaled units
+ * (CPOutput of kernels.py:178-305, called as bounds.py:42-66).
+ *   rhs     (B, m) scaled kept right-hand sides
+ *   target  (B, n) candidates yhat (q = 1, c = -yhat, y0 = yhat)
+ *   dual0   (B, m) scaled initial duals, or NULL for zero
+ *   lower, upper (B, n) bounds (±inf allowed), or (n) with shared_bounds
+ *   tol     (B) per-sample tolerance, or NULL for opts->tolerance
+ *   feasible (B) uint8 or NULL; converged is ANDed with it (bounds.py:66)
+ * Outputs y (B,n), dual (B,m) scaled, iterations int32 (B), residual (B),
+ * gap (B), converged uint8 (B).
+ */
+int purin_cp_solve(purin_cp_plan* plan, void* stream, int64_t batch, const void* rhs,
+                   const void* target, const void* dual0, const void* lower,
+                   const void* upper, const void* tol, const uint8_t* feasible,
+                   const purin_cp_solve_options* opts, void* y, void* dual,
+                   int32_t* iterations, void* residual, void* gap, uint8_t* converged,
+                   void* saved);
+
+/*
+ * Full projection (BoundProjection.solve, bounds.py:170-317).
+ *   target (B, n); rhs (B, me+mi) = -[h(theta,0); g(theta,0)];
+ *   multipliers0 (B, me+mi) warm-start multipliers in original units or NULL.
+ * Outputs: y (B,n); multipliers (B, me+mi) (equalities then inequalities,
+ * bound rows included); slacks (B, mi); status int32 (B); iterations int32
+ * (B); residual (B) original-unit residual; finite uint8 (B);
+ * eligible uint8 (B) (gradient_eligible).  Any output except y may be NULL.
+ */
+int purin_cp_project(purin_cp_plan* plan, void* stream, int64_t batch, const void* target,
+                     const void* rhs, const void* multipliers0,
+                     const purin_cp_solve_options* opts, void* y, void* multipliers,
+                     void* slacks, int32_t* status, int32_t* iterations, void* residual,
+                     uint8_t* finite, uint8_t* eligible, void* saved);
+
+/* Kernel times of the last solve()/project() call made with opts.timing = 1,
+ * from HIP events recorded on that call's stream around each launch. */
+typedef struct {
+  int64_t iterations;   /* CP iterations timed */
+  double row_ms;        /* summed row-pass time */
+  double col_ms;        /* summed column-pass time */
+  double diag_ms;       /* summed residual + decide time (stop test) */
+  double loop_ms;       /* first iteration kernel start to last end */
+} purin_cp_timing;
+
+int purin_cp_last_timing(const purin_cp_plan* plan, purin_cp_timing* timing);
+
+/* GMRES and gradient policy (LinearSolverConfig / ImplicitGradientConfig,
+ * src/purin/solvers/config.py:13-16, 94). */
+typedef struct {
+  double tolerance;          /* 1e-9 */
+  double atol;               /* 0 */
+  int32_t restart;           /* 30 */
+  int32_t max_iterations;    /* 100 */
+  double adjoint_tolerance;  /* 1e-8 */
+  int32_t force_eligible;    /* 1: treat every sample as converged (benchmark of
+                                a fixed-iteration state); 0: reference rule */
+  int32_t reserved;
+} purin_cp_adjoint_options;
+
+void purin_cp_default_adjoint_options(purin_cp_adjoint_options* opts);
+
+/*
+ * Implicit VJP at the state saved by project() (or solve()).
+ *   target (B,n), rhs (B, me+mi) the same inputs as the forward call
+ *   (for solve(): rhs (B, m) scaled); cot_y (B,n) cotangent of y.
+ * Outputs g_target (B,n); g_rhs (B, me+mi) (for solve(): (B, m) scaled) or NULL;
+ * g_lower, g_upper (B,n) or NULL (solve() only: gradients w.r.t. its bounds);
+ * valid uint8 (B), info int32 (B) (0 converged, 1 not, 2 non-finite),
+ * gmres_residual (B); each may be NULL.
+ */
+int purin_cp_adjoint(purin_cp_plan* plan, void* stream, int64_t batch, const void* saved,
+                     const void* target, const void* rhs, const void* cot_y,
+                     const purin_cp_adjoint_options* opts, void* g_target, void* g_rhs,
+                     void* g_lower, void* g_upper, uint8_t* valid, int32_t* info,
+                     void* gmres_residual);
+
+/* Message of the calling thread's last error ("" if none). */
+const char* purin_cp_last_error(void);
+
+/* Build identification (ABI version, offload target). */
+const char* purin_cp_build_info(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PURIN_CP_H */

@@ -1,0 +1,116 @@
+// Shared device helpers for the CDNA4 (gfx950) Chambolle--Pock kernels.
+//
+// Internal layout: every per-sample vector is stored batch-minor, element e of
+// sample b at [e * Bp + b], with Bp the batch rounded up to whole wavefront
+// tiles.  A wavefront lane owns S consecutive samples (16 bytes: 2 doubles or
+// 4 floats), so one wave moves 1 KiB per load and the matrix entries the wave
+// walks (a row or a column of K) are wave-uniform scalar loads.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+
+namespace purin {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // 4 wavefronts
+
+template <typename T>
+struct Lane;
+template <>
+struct Lane<double> {
+  static constexpr int S = 2;
+  typedef double V __attribute__((ext_vector_type(2)));
+};
+template <>
+struct Lane<float> {
+  static constexpr int S = 4;
+  typedef float V __attribute__((ext_vector_type(4)));
+};
+
+// Samples per wavefront tile and per block tile.
+template <typename T>
+constexpr int tile_samples() {
+  return kWave * Lane<T>::S;
+}
+
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V vload(const T* p) {
+  return *reinterpret_cast<const typename Lane<T>::V*>(p);
+}
+template <typename T>
+__device__ __forceinline__ void vstore(T* p, typename Lane<T>::V v) {
+  *reinterpret_cast<typename Lane<T>::V*>(p) = v;
+}
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V vsplat(T x) {
+  typename Lane<T>::V v;
+#pragma unroll
+  for (int s = 0; s < Lane<T>::S; ++s) v[s] = x;
+  return v;
+}
+
+// NaN-propagating max/min (jnp.maximum / jnp.minimum semantics).
+template <typename T>
+__device__ __forceinline__ T maxp(T x, T y) {
+  return (x != x) ? x : ((y != y) ? y : (x > y ? x : y));
+}
+template <typename T>
+__device__ __forceinline__ T minp(T x, T y) {
+  return (x != x) ? x : ((y != y) ? y : (x < y ? x : y));
+}
+// jnp.clip(x, lo, hi) == minimum(maximum(x, lo), hi)
+template <typename T>
+__device__ __forceinline__ T clipp(T x, T lo, T hi) {
+  return minp(maxp(x, lo), hi);
+}
+__device__ __forceinline__ double absv(double x) { return __builtin_fabs(x); }
+__device__ __forceinline__ float absv(float x) { return __builtin_fabsf(x); }
+template <typename T>
+__device__ __forceinline__ bool finite(T x) {
+  return __builtin_isfinite(x);
+}
+
+// Block-wide (4 waves) combine of one value per lane-sample, in wave order.
+// ``buf`` holds kBlock*S elements of LDS.  Returns the combined value in
+// wave 0's lanes (other waves' return values are unspecified).
+template <typename T, typename Op>
+__device__ __forceinline__ typename Lane<T>::V block_combine(typename Lane<T>::V v, T* buf,
+                                                             Op op) {
+  constexpr int S = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int s = 0; s < S; ++s) buf[(wave * kWave + lane) * S + s] = v[s];
+  __syncthreads();
+  typename Lane<T>::V out = v;
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) out[s] = op(out[s], buf[(w * kWave + lane) * S + s]);
+    }
+  }
+  __syncthreads();
+  return out;
+}
+
+struct OpAdd {
+  template <typename T>
+  __device__ T operator()(T a, T b) const { return a + b; }
+};
+struct OpMax {
+  template <typename T>
+  __device__ T operator()(T a, T b) const { return maxp(a, b); }
+};
+struct OpMin {
+  template <typename T>
+  __device__ T operator()(T a, T b) const { return minp(a, b); }
+};
+
+}  // namespace purin

@@ -1,0 +1,438 @@
+// Forward drivers: purin_cp_spmm, purin_cp_solve, purin_cp_project.
+//
+// One CP iteration is two launches in fixed-iteration mode (row pass, column
+// pass) and four with the per-sample stop test (row, column, residual,
+// decide).  The per-iteration step scalars are the same for every sample
+// (shared matrix => shared norm bound and shared tau/sigma/theta schedule,
+// reference src/purin/solvers/chambolle_pock/kernels.py:209-227, 279-283), so
+// the host computes them in the plan's precision and passes them as kernel
+// arguments; nothing per-sample leaves the device inside the loop except the
+// all-done counter, read every ``check_every`` iterations.
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "kernels.hpp"
+#include "plan.hpp"
+#include "post.hpp"
+#include "forward.hpp"
+
+namespace purin {
+
+static size_t al(size_t x) { return (x + 255) & ~size_t(255); }
+
+Layout make_layout(const purin_cp_plan* p, int64_t batch) {
+  Layout L{};
+  const size_t es = elem_size(p);
+  const int64_t Bp = padded_batch(p, batch);
+  L.Bp = Bp;
+  const size_t n = p->n, m = p->m, M = p->M, mi = p->mi;
+  L.nrb = (int)((m + 4 * kRowsPerWaveEarly - 1) / (4 * kRowsPerWaveEarly));
+  L.ncb = (int)((n + 4 * kRowsPerWaveEarly - 1) / (4 * kRowsPerWaveEarly));
+  size_t o = 0;
+  auto take = [&](size_t bytes) { size_t r = o; o = al(o + bytes); return r; };
+  L.hdr = take(kSavedHeader);
+  L.Tt = take(n * Bp * es);
+  L.Y = take(n * Bp * es);
+  L.D = take(m * Bp * es);
+  L.R = take(m * Bp * es);
+  L.LO = take(n * Bp * es);
+  L.HI = take(n * Bp * es);
+  L.RF = take(M * Bp * es);
+  L.conv = take(Bp * 4);
+  L.feas = take(Bp * 4);
+  L.saved_end = o;
+  o = 0;
+  L.YB = take(n * Bp * es);
+  L.MF = take(M * Bp * es);
+  L.DF = take(M * Bp * es);
+  L.SL = take(mi * Bp * es);
+  L.colpart = take((size_t)5 * std::max(L.ncb, 1) * Bp * es);
+  L.rowpart = take((size_t)3 * std::max(L.nrb, 1) * Bp * es);
+  L.done = take(Bp * 4);
+  L.count = take(Bp * 4);
+  L.ndone = take(256);
+  L.ores = take(Bp * es);
+  L.ogap = take(Bp * es);
+  L.ofin = take(Bp * 4);
+  L.X = take(std::max(n, m) * Bp * es);  // spmm input / output staging
+  L.Z = take(std::max(n, m) * Bp * es);
+  L.ws_end = o;
+  return L;
+}
+
+// The CP loop on prepared internal arrays plus the final diagnostics.
+template <typename T>
+int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout& L, char* sv,
+                   char* ws, const purin_cp_solve_options& o, T tol_scalar, const T* tolv) {
+  const int64_t Bp = L.Bp;
+  constexpr int64_t TS = tile_samples<T>();
+  Iter<T> A{};
+  A.K = kept_matrix<T>(p, true);
+  A.Bp = Bp;
+  A.tgt = (const T*)(sv + L.Tt);
+  A.Y = (T*)(sv + L.Y);
+  A.YB = (T*)(ws + L.YB);
+  A.D = (T*)(sv + L.D);
+  A.R = (const T*)(sv + L.R);
+  A.LO = (const T*)(sv + L.LO);
+  A.HI = (const T*)(sv + L.HI);
+  A.shared_bounds = o.shared_bounds;
+  A.colpart = (T*)(ws + L.colpart);
+  A.rowpart = (T*)(ws + L.rowpart);
+  A.ncb = L.ncb;
+  A.nrb = L.nrb;
+  int32_t* done = (int32_t*)(ws + L.done);
+  int32_t* count = (int32_t*)(ws + L.count);
+  int32_t* ndone = (int32_t*)(ws + L.ndone);
+  const int m = A.K.m, n = A.K.n;
+  // y0 = ybar0 = target (kernels.py:229-231, bounds.py:59)
+  PURIN_HIP(hipMemcpyAsync(A.Y, A.tgt, (size_t)n * Bp * sizeof(T), hipMemcpyDeviceToDevice, st));
+  PURIN_HIP(hipMemcpyAsync(A.YB, A.tgt, (size_t)n * Bp * sizeof(T), hipMemcpyDeviceToDevice, st));
+
+  const bool early = o.early_stop != 0;
+  const int check = o.check_every > 0 ? o.check_every : 32;
+  const T one = T(1);
+  T tau = (T)p->tau0, sigma = (T)p->sigma0, theta = one;
+  const dim3 grow = tile_grid(Bp, TS, (m + 3) / 4);
+  const dim3 gcol = tile_grid(Bp, TS, (n + 3) / 4);
+  const dim3 gcolE = tile_grid(Bp, TS, L.ncb);
+  const dim3 gres = tile_grid(Bp, TS, std::max(L.nrb, 1));
+  const dim3 gdec((unsigned)((batch + kBlock - 1) / kBlock));
+  // optional event timing: events[3k] before the row pass, [3k+1] between the
+  // passes, [3k+2] after the column pass (and the stop test) of iteration k
+  const bool timing = o.timing != 0;
+  std::vector<hipEvent_t> ev;
+  if (timing) {
+    ev.resize((size_t)3 * o.max_iterations);
+    for (auto& e : ev) PURIN_HIP(hipEventCreate(&e));
+  }
+  std::vector<hipEvent_t> evd;  // after the column pass when the stop test runs
+  if (timing && early) {
+    evd.resize((size_t)o.max_iterations);
+    for (auto& e : evd) PURIN_HIP(hipEventCreate(&e));
+  }
+  int64_t it = 0;
+  for (; it < o.max_iterations; ++it) {
+    A.sigma = sigma;
+    A.a = one / (one + tau);  // proximal_coefficients with q = 1 (kernels.py:68-73)
+    A.delta = tau * A.a;
+    A.theta = theta;
+    if (timing) PURIN_HIP(hipEventRecord(ev[3 * it], st));
+    if (!early) {
+      if (m) k_row_pass<T, false><<<grow, kBlock, 0, st>>>(A);
+      if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 1], st));
+      k_col_pass<T, 0, kRowsPerWaveFixed><<<gcol, kBlock, 0, st>>>(A);
+    } else {
+      A.done = done;
+      if (m) k_row_pass<T, true><<<grow, kBlock, 0, st>>>(A);
+      if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 1], st));
+      k_col_pass<T, 1, kRowsPerWaveEarly><<<gcolE, kBlock, 0, st>>>(A);
+      if (timing) PURIN_HIP(hipEventRecord(evd[it], st));
+      if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres, kBlock, 0, st>>>(A);
+      k_decide<T, false><<<gdec, kBlock, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
+                                                   nullptr, nullptr, nullptr, nullptr, nullptr);
+    }
+    if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 2], st));
+    if (p->opts.accelerated) {  // kernels.py:279-283 with gamma = min q = 1
+      const T nt = one / std::sqrt(one + tau);
+      tau = nt * tau;
+      sigma = sigma / nt;
+      theta = nt;
+    }
+    if (early && ((it + 1) % check == 0)) {
+      PURIN_HIP(hipMemcpyAsync(p->pinned, ndone, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+      PURIN_HIP(hipStreamSynchronize(st));
+      if (p->pinned[0] >= batch) {
+        ++it;
+        break;
+      }
+    }
+  }
+  if (timing) {
+    PURIN_HIP(hipStreamSynchronize(st));
+    purin_cp_timing t{};
+    t.iterations = it;
+    for (int64_t k = 0; k < it; ++k) {
+      float a = 0, b = 0, c = 0;
+      PURIN_HIP(hipEventElapsedTime(&a, ev[3 * k], ev[3 * k + 1]));
+      if (early) {
+        PURIN_HIP(hipEventElapsedTime(&b, ev[3 * k + 1], evd[k]));
+        PURIN_HIP(hipEventElapsedTime(&c, evd[k], ev[3 * k + 2]));
+      } else {
+        PURIN_HIP(hipEventElapsedTime(&b, ev[3 * k + 1], ev[3 * k + 2]));
+      }
+      t.row_ms += a;
+      t.col_ms += b;
+      t.diag_ms += c;
+    }
+    float total = 0;
+    if (it > 0) PURIN_HIP(hipEventElapsedTime(&total, ev[0], ev[3 * (it - 1) + 2]));
+    t.loop_ms = total;
+    p->timing = t;
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    for (auto& e : evd) (void)hipEventDestroy(e);
+  }
+  PURIN_HIP(hipGetLastError());
+  if (!early) {
+    const int32_t cnt = (int32_t)o.max_iterations;
+    k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);
+  }
+  // final diagnostics on the returned state (kernels.py:291-305)
+  A.done = nullptr;
+  k_col_pass<T, 2, kRowsPerWaveEarly><<<gcolE, kBlock, 0, st>>>(A);
+  if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres, kBlock, 0, st>>>(A);
+  k_decide<T, true><<<gdec, kBlock, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
+                                             (const int32_t*)(sv + L.feas), (T*)(ws + L.ores),
+                                             (T*)(ws + L.ogap), (int32_t*)(sv + L.conv),
+                                             (int32_t*)(ws + L.ofin));
+  PURIN_HIP(hipGetLastError());
+  return PURIN_CP_OK;
+}
+
+template <typename T>
+static int check_layout_args(purin_cp_plan* p, int64_t batch) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  if ((p->dtype == PURIN_CP_F64) != (sizeof(T) == 8))
+    return set_error(PURIN_CP_ERR_ARG, "dtype mismatch");
+  if (batch < 1) return set_error(PURIN_CP_ERR_ARG, "batch_size and variable_size must be positive");
+  return PURIN_CP_OK;
+}
+
+template <typename T>
+static int prepare_buffers(purin_cp_plan* p, hipStream_t st, int64_t batch, void* saved,
+                           Layout* L, char** sv, char** ws) {
+  *L = make_layout(p, batch);
+  int err = PURIN_CP_OK;
+  const size_t need = L->ws_end + (saved ? 0 : L->saved_end);
+  char* base = (char*)workspace(p, need, st, &err);
+  if (!base) return err;
+  *ws = base;
+  *sv = saved ? (char*)saved : base + L->ws_end;
+  return PURIN_CP_OK;
+}
+
+template <typename T>
+static int spmm_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, int transpose, int scaled,
+                     const T* x, T* out) {
+  int rc = check_layout_args<T>(p, batch);
+  if (rc) return rc;
+  if (!x || !out) return set_error(PURIN_CP_ERR_ARG, "NULL x/out");
+  Layout L;
+  char *sv, *ws;
+  if ((rc = prepare_buffers<T>(p, st, batch, nullptr, &L, &sv, &ws))) return rc;
+  const int64_t Bp = L.Bp;
+  constexpr int64_t TS = tile_samples<T>();
+  Mat<T> K = kept_matrix<T>(p, scaled != 0);
+  T* X = (T*)(ws + L.X);
+  T* Z = (T*)(ws + L.Z);
+  const int64_t cin = transpose ? p->m : p->n, cout = transpose ? p->n : p->m;
+  to_minor<T>(st, x, batch, cin, cin, X, Bp, nullptr, 0);
+  if (!transpose) {
+    if (p->m) k_spmv_rows<T><<<tile_grid(Bp, TS, (p->m + 3) / 4), kBlock, 0, st>>>(K, Bp, X, Z);
+  } else {
+    if (p->m == 0)
+      k_fill<T><<<256, 256, 0, st>>>(Z, (int64_t)p->n * Bp, T(0));
+    else
+      k_spmv_cols<T><<<tile_grid(Bp, TS, (p->n + 3) / 4), kBlock, 0, st>>>(K, Bp, X, Z);
+  }
+  to_major<T>(st, Z, Bp, cout, out, batch, cout, nullptr, 0);
+  PURIN_HIP(hipGetLastError());
+  return PURIN_CP_OK;
+}
+
+template <typename T>
+static void write_header(hipStream_t st, char* sv, int64_t batch, int64_t Bp, int kind,
+                         int shared, const purin_cp_plan* p) {
+  k_write_header<T><<<1, 64, 0, st>>>((int64_t*)sv, batch, Bp, kind, shared, p->dtype, p->n, p->m,
+                                      p->M);
+}
+
+template <typename T>
+static int solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T* rhs,
+                      const T* target, const T* dual0, const T* lower, const T* upper,
+                      const T* tol, const uint8_t* feasible, const purin_cp_solve_options& o,
+                      T* y, T* dual, int32_t* iterations, T* residual, T* gap,
+                      uint8_t* converged, void* saved) {
+  int rc = check_layout_args<T>(p, batch);
+  if (rc) return rc;
+  if (!target || !lower || !upper || (p->m && !rhs))
+    return set_error(PURIN_CP_ERR_ARG, "NULL input array");
+  if (o.max_iterations < 1) return set_error(PURIN_CP_ERR_ARG, "max_iterations must be a positive integer");
+  Layout L;
+  char *sv, *ws;
+  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws))) return rc;
+  const int64_t Bp = L.Bp, n = p->n, m = p->m;
+  write_header<T>(st, sv, batch, Bp, 0, o.shared_bounds, p);
+  to_minor<T>(st, target, batch, n, n, (T*)(sv + L.Tt), Bp, nullptr, 0);
+  to_minor<T>(st, rhs, batch, m, m, (T*)(sv + L.R), Bp, nullptr, 0);
+  if (dual0)
+    to_minor<T>(st, dual0, batch, m, m, (T*)(sv + L.D), Bp, nullptr, 0);
+  else if (m)
+    k_fill<T><<<1024, 256, 0, st>>>((T*)(sv + L.D), m * Bp, T(0));
+  if (o.shared_bounds) {
+    PURIN_HIP(hipMemcpyAsync(sv + L.LO, lower, n * sizeof(T), hipMemcpyDeviceToDevice, st));
+    PURIN_HIP(hipMemcpyAsync(sv + L.HI, upper, n * sizeof(T), hipMemcpyDeviceToDevice, st));
+  } else {
+    to_minor<T>(st, lower, batch, n, n, (T*)(sv + L.LO), Bp, nullptr, 0);
+    to_minor<T>(st, upper, batch, n, n, (T*)(sv + L.HI), Bp, nullptr, 0);
+  }
+  k_init_flags<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(
+      batch, Bp, (int32_t*)(ws + L.done), (int32_t*)(ws + L.count), (int32_t*)(sv + L.feas),
+      feasible, (int32_t*)(ws + L.ndone));
+  // per-sample tolerance: pad to Bp in the ores scratch is not needed; the
+  // decide kernels index tol[b] only for b < batch.
+  if ((rc = run_iterations<T>(p, st, batch, L, sv, ws, o, (T)o.tolerance, tol))) return rc;
+  if (y) to_major<T>(st, (const T*)(sv + L.Y), Bp, n, y, batch, n, nullptr, 0);
+  if (dual) to_major<T>(st, (const T*)(sv + L.D), Bp, m, dual, batch, m, nullptr, 0);
+  k_finish_solve<T><<<(unsigned)((batch + 255) / 256), 256, 0, st>>>(
+      batch, (const int32_t*)(ws + L.count), (const T*)(ws + L.ores), (const T*)(ws + L.ogap),
+      (const int32_t*)(sv + L.conv), iterations, residual, gap, converged);
+  PURIN_HIP(hipGetLastError());
+  return PURIN_CP_OK;
+}
+
+template <typename T>
+static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T* target,
+                        const T* rhs, const T* mult0, const purin_cp_solve_options& o, T* y,
+                        T* mult, T* slacks, int32_t* status, int32_t* iterations, T* residual,
+                        uint8_t* finite_out, uint8_t* eligible, void* saved) {
+  int rc = check_layout_args<T>(p, batch);
+  if (rc) return rc;
+  if (!target || (p->M && !rhs)) return set_error(PURIN_CP_ERR_ARG, "NULL input array");
+  if (o.max_iterations < 1) return set_error(PURIN_CP_ERR_ARG, "max_iterations must be a positive integer");
+  if (!(o.tolerance > 0.0) || !std::isfinite(o.tolerance))
+    return set_error(PURIN_CP_ERR_ARG, "tolerance must be positive and finite");
+  Layout L;
+  char *sv, *ws;
+  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws))) return rc;
+  const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
+  constexpr int64_t TS = tile_samples<T>();
+  write_header<T>(st, sv, batch, Bp, 1, o.shared_bounds, p);
+  const T* metric = (const T*)p->metric;
+  // diagonal metric: targets scaled by sqrt(D) (metric.py:102-108), tolerance
+  // divided and residual multiplied by max(1, sqrt(max D)) (metric.py:161-165)
+  double factor = 1.0;
+  if (metric)
+    for (double s : p->metric_host) factor = std::max(factor, s);
+  const double tol_cfg = o.tolerance / factor;
+  to_minor<T>(st, target, batch, n, n, (T*)(sv + L.Tt), Bp, metric, metric ? 1 : 0);
+  T* RF = (T*)(sv + L.RF);
+  to_minor<T>(st, rhs, batch, M, M, RF, Bp, nullptr, 0);
+  T* MF = nullptr;
+  if (mult0) {
+    MF = (T*)(ws + L.MF);
+    to_minor<T>(st, mult0, batch, M, M, MF, Bp, nullptr, 0);
+  }
+  if (m)
+    k_prep_rows<T><<<2048, 256, 0, st>>>((int)m, Bp, p->dkept, (const T*)p->dscale, RF, MF,
+                                         (T*)(sv + L.R), (T*)(sv + L.D));
+  k_init_flags<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(
+      batch, Bp, (int32_t*)(ws + L.done), (int32_t*)(ws + L.count), (int32_t*)(sv + L.feas),
+      nullptr, (int32_t*)(ws + L.ndone));
+  const int64_t cols = o.shared_bounds ? 1 : Bp;
+  k_prep_bounds<T><<<2048, 256, 0, st>>>((int)n, Bp, cols, p->bptr, p->brow,
+                                         (const T*)p->dbcoef, RF, (T*)(sv + L.LO),
+                                         (T*)(sv + L.HI), (int32_t*)(sv + L.feas), batch);
+  // tolerance = tol * min(1, min_i scale_i) (bounds.py:233-236)
+  const T tol_cp = (T)tol_cfg * std::min((T)1, (T)p->tol_factor);
+  if ((rc = run_iterations<T>(p, st, batch, L, sv, ws, o, tol_cp, nullptr))) return rc;
+  // post-processing (bounds.py:247-317)
+  Post<T> P{};
+  P.K = kept_matrix<T>(p, false);
+  P.Bp = Bp;
+  P.me = p->me;
+  P.mi = p->mi;
+  P.scale = (const T*)p->dscale;
+  P.kept = p->dkept;
+  P.bptr = p->bptr;
+  P.brow = p->brow;
+  P.bcoef = (const T*)p->dbcoef;
+  P.tgt = (const T*)(sv + L.Tt);
+  P.Y = (const T*)(sv + L.Y);
+  P.D = (const T*)(sv + L.D);
+  P.RF = RF;
+  P.LO = (const T*)(sv + L.LO);
+  P.HI = (const T*)(sv + L.HI);
+  P.shared_bounds = o.shared_bounds;
+  P.DF = (T*)(ws + L.DF);
+  P.SL = (T*)(ws + L.SL);
+  P.rowpart = (T*)(ws + L.rowpart);
+  P.colpart = (T*)(ws + L.colpart);
+  P.nrb = L.nrb;
+  P.ncb = L.ncb;
+  if (m)
+    k_post_rows<T, kRowsPerWaveEarly><<<tile_grid(Bp, TS, L.nrb), kBlock, 0, st>>>(P);
+  k_post_cols<T, kRowsPerWaveEarly><<<tile_grid(Bp, TS, L.ncb), kBlock, 0, st>>>(P);
+  k_post_final<T><<<(unsigned)((batch + 255) / 256), 256, 0, st>>>(
+      P, batch, (T)tol_cfg, (T)factor, (const int32_t*)(sv + L.conv), (const T*)(ws + L.ogap),
+      (const int32_t*)(ws + L.count), status, iterations, residual, finite_out, eligible);
+  if (y) to_major<T>(st, (const T*)(sv + L.Y), Bp, n, y, batch, n, metric, metric ? 2 : 0);
+  if (mult) to_major<T>(st, (const T*)(ws + L.DF), Bp, M, mult, batch, M, nullptr, 0);
+  if (slacks) to_major<T>(st, (const T*)(ws + L.SL), Bp, p->mi, slacks, batch, p->mi, nullptr, 0);
+  PURIN_HIP(hipGetLastError());
+  return PURIN_CP_OK;
+}
+
+}  // namespace purin
+
+using namespace purin;
+
+extern "C" {
+
+int64_t purin_cp_saved_bytes(const purin_cp_plan* p, int64_t batch) {
+  if (!p || batch < 1) return -1;
+  return (int64_t)make_layout(p, batch).saved_end;
+}
+
+int purin_cp_spmm(purin_cp_plan* p, void* stream, int64_t batch, int32_t transpose,
+                  int32_t scaled, const void* x, void* out) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64)
+    return spmm_impl<double>(p, st, batch, transpose, scaled, (const double*)x, (double*)out);
+  return spmm_impl<float>(p, st, batch, transpose, scaled, (const float*)x, (float*)out);
+}
+
+int purin_cp_solve(purin_cp_plan* p, void* stream, int64_t batch, const void* rhs,
+                   const void* target, const void* dual0, const void* lower, const void* upper,
+                   const void* tol, const uint8_t* feasible, const purin_cp_solve_options* opts,
+                   void* y, void* dual, int32_t* iterations, void* residual, void* gap,
+                   uint8_t* converged, void* saved) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  purin_cp_solve_options o;
+  purin_cp_default_solve_options(&o);
+  if (opts) o = *opts;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64)
+    return solve_impl<double>(p, st, batch, (const double*)rhs, (const double*)target,
+                              (const double*)dual0, (const double*)lower, (const double*)upper,
+                              (const double*)tol, feasible, o, (double*)y, (double*)dual,
+                              iterations, (double*)residual, (double*)gap, converged, saved);
+  return solve_impl<float>(p, st, batch, (const float*)rhs, (const float*)target,
+                           (const float*)dual0, (const float*)lower, (const float*)upper,
+                           (const float*)tol, feasible, o, (float*)y, (float*)dual, iterations,
+                           (float*)residual, (float*)gap, converged, saved);
+}
+
+int purin_cp_project(purin_cp_plan* p, void* stream, int64_t batch, const void* target,
+                     const void* rhs, const void* mult0, const purin_cp_solve_options* opts,
+                     void* y, void* mult, void* slacks, int32_t* status, int32_t* iterations,
+                     void* residual, uint8_t* finite_out, uint8_t* eligible, void* saved) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  purin_cp_solve_options o;
+  purin_cp_default_solve_options(&o);
+  if (opts) o = *opts;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64)
+    return project_impl<double>(p, st, batch, (const double*)target, (const double*)rhs,
+                                (const double*)mult0, o, (double*)y, (double*)mult,
+                                (double*)slacks, status, iterations, (double*)residual,
+                                finite_out, eligible, saved);
+  return project_impl<float>(p, st, batch, (const float*)target, (const float*)rhs,
+                             (const float*)mult0, o, (float*)y, (float*)mult, (float*)slacks,
+                             status, iterations, (float*)residual, finite_out, eligible, saved);
+}
+
+}  // extern "C"

@@ -1,0 +1,492 @@
+// Batched shared-matrix Chambolle--Pock kernels for CDNA4 (gfx950).
+//
+// Layout and tiling (see common.hpp): per-sample vectors are batch-minor with
+// leading dimension Bp; a 256-thread block is 4 wavefronts; blockIdx.x picks a
+// batch tile of 64*S samples (S = 16 bytes / sizeof(T)), so when the number of
+// tiles is a multiple of 8 every tile stays on one XCD and its gathered vector
+// stays in that XCD's L2.  blockIdx.y walks rows (or columns) of K; the entries
+// of the row/column a wave processes are wave-uniform scalar loads, and the
+// batch columns are read with 16-byte-per-lane coalesced loads.
+//
+// The passes of one CP iteration (reference
+// src/purin/solvers/chambolle_pock/kernels.py:91-150 and 153-175):
+//   row pass   d+ = P(d + sigma (K ybar - r))          (K: row-scaled kept rows)
+//   col pass   y+ = clip(a y - delta K^T d+ + delta yhat, lo, hi);
+//              ybar+ = y+ + theta (y+ - y)             (+ column diagnostics)
+//   res pass   max |K y+ - r| rows, r.d+ and finite(d+) (diagnostics)
+//   decide     per-sample stop test and freeze          (kernels.py:260-278)
+#pragma once
+
+#include "common.hpp"
+
+namespace purin {
+
+template <typename T>
+struct Mat {
+  int m, n, me;
+  const int32_t* __restrict__ rptr;
+  const int32_t* __restrict__ ridx;
+  const T* __restrict__ rval;
+  const int32_t* __restrict__ cptr;
+  const int32_t* __restrict__ cidx;
+  const T* __restrict__ cval;
+};
+
+template <typename T>
+struct Iter {
+  Mat<T> K;
+  int64_t Bp;
+  const T* __restrict__ tgt;  // n x Bp
+  T* Y;                       // n x Bp
+  T* YB;                      // n x Bp
+  T* D;                       // m x Bp
+  const T* __restrict__ R;    // m x Bp (scaled kept rhs)
+  const T* __restrict__ LO;   // n x Bp, or n when shared
+  const T* __restrict__ HI;
+  int shared_bounds;
+  const int32_t* done;        // Bp, or nullptr
+  T sigma, a, delta, theta;
+  T* colpart;                 // [5][ncb][Bp]: primal, dual, stat, bound, finite
+  T* rowpart;                 // [3][nrb][Bp]: residual max, r.d, finite
+  int ncb, nrb;
+};
+
+// ---------------------------------------------------------------------------
+// row pass: d <- P(d + sigma (K ybar - r)) for samples not yet done
+// ---------------------------------------------------------------------------
+template <typename T, bool MASKED>
+__global__ __launch_bounds__(kBlock) void k_row_pass(Iter<T> A) {
+  using V = typename Lane<T>::V;
+  constexpr int S = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  V keep = vsplat<T>(T(0));
+  if (MASKED) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) keep[s] = A.done[b0 + s] ? T(1) : T(0);
+  }
+  for (int rb = blockIdx.y; rb * 4 < A.K.m; rb += gridDim.y) {
+    const int i = rb * 4 + wave;
+    if (i >= A.K.m) continue;
+    const int s0 = A.K.rptr[i], s1 = A.K.rptr[i + 1];
+    V acc = vsplat<T>(T(0));
+    for (int k = s0; k < s1; ++k) {
+      const T v = A.K.rval[k];
+      const V x = vload(A.YB + (size_t)A.K.ridx[k] * A.Bp + b0);
+      acc += v * x;
+    }
+    T* dp = A.D + (size_t)i * A.Bp + b0;
+    const V d = vload(dp);
+    const V r = vload(A.R + (size_t)i * A.Bp + b0);
+    V p = d + A.sigma * (acc - r);
+    if (i >= A.K.me) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) p[s] = maxp(p[s], T(0));
+    }
+    if (MASKED) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) p[s] = keep[s] != T(0) ? d[s] : p[s];
+    }
+    vstore(dp, p);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// column pass.  MODE 0: fixed-iteration update; 1: masked update + diagnostic
+// partials of (y+, d+); 2: no update, diagnostics of the current (y, d).
+// ---------------------------------------------------------------------------
+template <typename T, int MODE, int CPW>
+__global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
+  using V = typename Lane<T>::V;
+  constexpr int S = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  const T half = T(0.5), zero = T(0);
+  V keep = vsplat<T>(T(0));
+  if (MODE == 1) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) keep[s] = A.done[b0 + s] ? T(1) : T(0);
+  }
+  V primal = vsplat<T>(zero), dualo = vsplat<T>(zero), stat = vsplat<T>(zero),
+    bnd = vsplat<T>(zero), fin = vsplat<T>(T(1));
+  for (int cb = blockIdx.y; cb * 4 * CPW < A.K.n; cb += gridDim.y) {
+    for (int c = 0; c < CPW; ++c) {
+      const int j = (cb * 4 + wave) * CPW + c;
+      if (j >= A.K.n) break;
+      const int s0 = A.K.cptr[j], s1 = A.K.cptr[j + 1];
+      V t = vsplat<T>(zero);
+      for (int k = s0; k < s1; ++k) {
+        const T v = A.K.cval[k];
+        const V dd = vload(A.D + (size_t)A.K.cidx[k] * A.Bp + b0);
+        t += v * dd;
+      }
+      const size_t off = (size_t)j * A.Bp + b0;
+      const V y = vload(A.Y + off);
+      const V tg = vload(A.tgt + off);
+      V lo, hi;
+      if (A.shared_bounds) {
+        lo = vsplat<T>(A.LO[j]);
+        hi = vsplat<T>(A.HI[j]);
+      } else {
+        lo = vload(A.LO + off);
+        hi = vload(A.HI + off);
+      }
+      V yn;
+      if (MODE == 2) {
+        yn = y;
+      } else {
+        const V sv = A.a * y - A.delta * t + A.delta * tg;
+#pragma unroll
+        for (int s = 0; s < S; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
+        V yb = yn + A.theta * (yn - y);
+        if (MODE == 1) {
+          const V yo = y;
+          const V ybo = vload(A.YB + off);
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            if (keep[s] != zero) {
+              yn[s] = yo[s];  // frozen sample: keep state (its diagnostics are unused)
+              yb[s] = ybo[s];
+            }
+          }
+        }
+        vstore(A.Y + off, yn);
+        vstore(A.YB + off, yb);
+      }
+      if (MODE != 0) {
+        // diagnostics (kernels.py:158-174, 272-274) with q = 1, c = -yhat
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const T yv = yn[s], c = -tg[s];
+          primal[s] += half * yv * yv + c * yv;
+          const T tf = c + t[s];
+          const T mz = clipp(-tf, lo[s], hi[s]);
+          dualo[s] += half * mz * mz + tf * mz;
+          const T g = yv - clipp(yv - ((yv + c) + t[s]), lo[s], hi[s]);
+          stat[s] = maxp(stat[s], absv(g));
+          bnd[s] = maxp(bnd[s], maxp(maxp(lo[s] - yv, zero), maxp(yv - hi[s], zero)));
+          if (!finite(yv)) fin[s] = zero;
+        }
+      }
+    }
+    if (MODE != 0) {
+      __shared__ T buf[kBlock * S];
+      const V p0 = block_combine<T>(primal, buf, OpAdd());
+      const V p1 = block_combine<T>(dualo, buf, OpAdd());
+      const V p2 = block_combine<T>(stat, buf, OpMax());
+      const V p3 = block_combine<T>(bnd, buf, OpMax());
+      const V p4 = block_combine<T>(fin, buf, OpMin());
+      if (wave == 0) {
+        const size_t plane = (size_t)A.ncb * A.Bp;
+        T* base = A.colpart + (size_t)cb * A.Bp + b0;
+        vstore(base, p0);
+        vstore(base + plane, p1);
+        vstore(base + 2 * plane, p2);
+        vstore(base + 3 * plane, p3);
+        vstore(base + 4 * plane, p4);
+      }
+      primal = dualo = stat = bnd = vsplat<T>(zero);
+      fin = vsplat<T>(T(1));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// residual pass: per kept row r = K y - rhs -> |r| (eq) / max(r,0) (ineq);
+// r.d and finite(d) for the dual objective and the finiteness test.
+// ---------------------------------------------------------------------------
+template <typename T, int RPW>
+__global__ __launch_bounds__(kBlock) void k_res_pass(Iter<T> A) {
+  using V = typename Lane<T>::V;
+  constexpr int S = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  const T zero = T(0);
+  for (int rb = blockIdx.y; rb * 4 * RPW < A.K.m; rb += gridDim.y) {
+    V res = vsplat<T>(zero), rd = vsplat<T>(zero), fin = vsplat<T>(T(1));
+    for (int c = 0; c < RPW; ++c) {
+      const int i = (rb * 4 + wave) * RPW + c;
+      if (i >= A.K.m) break;
+      const int s0 = A.K.rptr[i], s1 = A.K.rptr[i + 1];
+      V acc = vsplat<T>(zero);
+      for (int k = s0; k < s1; ++k) {
+        const T v = A.K.rval[k];
+        acc += v * vload(A.Y + (size_t)A.K.ridx[k] * A.Bp + b0);
+      }
+      const size_t off = (size_t)i * A.Bp + b0;
+      const V r = vload(A.R + off);
+      const V d = vload(A.D + off);
+      const V e = acc - r;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const T v = i < A.K.me ? absv(e[s]) : maxp(e[s], zero);
+        res[s] = maxp(res[s], v);
+        rd[s] += r[s] * d[s];
+        if (!finite(d[s])) fin[s] = zero;
+      }
+    }
+    __shared__ T buf[kBlock * S];
+    const V p0 = block_combine<T>(res, buf, OpMax());
+    const V p1 = block_combine<T>(rd, buf, OpAdd());
+    const V p2 = block_combine<T>(fin, buf, OpMin());
+    if (wave == 0) {
+      const size_t plane = (size_t)A.nrb * A.Bp;
+      T* base = A.rowpart + (size_t)rb * A.Bp + b0;
+      vstore(base, p0);
+      vstore(base + plane, p1);
+      vstore(base + 2 * plane, p2);
+    }
+  }
+}
+
+// Per-sample reduction of the partials (fixed order), the stop test and the
+// freeze (kernels.py:260-278) or, when FINAL, the final convergence verdict
+// (kernels.py:291-305).
+template <typename T, bool FINAL>
+__global__ __launch_bounds__(kBlock) void k_decide(Iter<T> A, int64_t batch, T tol_scalar,
+                                                    const T* __restrict__ tolv, int32_t* done, int32_t* count,
+                                                    int32_t* ndone, const int32_t* feasible,
+                                                    T* out_res, T* out_gap, int32_t* out_conv,
+                                                    int32_t* out_fin) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  if (!FINAL && done[b]) return;
+  const T zero = T(0);
+  const T tol = tolv ? tolv[b] : tol_scalar;
+  const size_t cplane = (size_t)A.ncb * A.Bp, rplane = (size_t)A.nrb * A.Bp;
+  T primal = zero, dualo = zero, stat = zero, bnd = zero, res = zero, rd = zero;
+  bool fin = true;
+  for (int c = 0; c < A.ncb; ++c) {
+    const T* p = A.colpart + (size_t)c * A.Bp + b;
+    primal += p[0];
+    dualo += p[cplane];
+    stat = maxp(stat, p[2 * cplane]);
+    bnd = maxp(bnd, p[3 * cplane]);
+    fin = fin && p[4 * cplane] != zero;
+  }
+  bool fin_d = true;
+  for (int r = 0; r < A.nrb; ++r) {
+    const T* p = A.rowpart + (size_t)r * A.Bp + b;
+    res = maxp(res, p[0]);
+    rd += p[rplane];
+    fin_d = fin_d && p[2 * rplane] != zero;
+  }
+  const T dual_obj = dualo - rd;
+  const T gap = maxp(primal - dual_obj, zero) /
+                maxp(T(1), maxp(absv(primal), absv(dual_obj)));
+  const T residual = maxp(res, bnd);
+  if (!FINAL) {
+    count[b] += 1;
+    const bool ok = fin && fin_d && finite(gap) && residual <= tol && gap <= tol && stat <= tol;
+    if (ok) {
+      done[b] = 1;
+      atomicAdd(ndone, 1);
+    }
+  } else {
+    const bool f = fin && fin_d && finite(gap) && finite(residual);
+    const bool conv = f && residual <= tol && gap <= tol && stat <= tol &&
+                      (feasible == nullptr || feasible[b] != 0);
+    out_res[b] = maxp(residual, stat);
+    out_gap[b] = gap;
+    out_conv[b] = conv ? 1 : 0;
+    out_fin[b] = f ? 1 : 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// layout conversion
+// ---------------------------------------------------------------------------
+// dst[c * Bp + b] = src[b * ld + c] (times/divided by colmul[c]); zero padding
+// for b >= B.  mode: 0 copy, 1 multiply, 2 divide.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_to_minor(const T* __restrict__ src, int64_t B,
+                                                      int64_t C, int64_t ld, T* __restrict__ dst,
+                                                      int64_t Bp, const T* __restrict__ colmul,
+                                                      int mode) {
+  __shared__ T tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * 64, b0 = (int64_t)blockIdx.y * 64;
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t b = b0 + r, c = c0 + tx;
+    T v = T(0);
+    if (b < B && c < C) {
+      v = src[b * ld + c];
+      if (mode == 1) v = v * colmul[c];
+      else if (mode == 2) v = v / colmul[c];
+    }
+    tile[r][tx] = v;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t c = c0 + r, b = b0 + tx;
+    if (c < C && b < Bp) dst[c * Bp + b] = tile[tx][r];
+  }
+}
+
+// dst[b * ld + c] = src[c * Bp + b] (times/divided by colmul[c]) for b < B.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_to_major(const T* __restrict__ src, int64_t Bp,
+                                                      int64_t C, T* __restrict__ dst, int64_t B,
+                                                      int64_t ld, const T* __restrict__ colmul,
+                                                      int mode) {
+  __shared__ T tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * 64, b0 = (int64_t)blockIdx.y * 64;
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t c = c0 + r, b = b0 + tx;
+    T v = T(0);
+    if (c < C && b < B) {
+      v = src[c * Bp + b];
+      if (mode == 1) v = v * colmul[c];
+      else if (mode == 2) v = v / colmul[c];
+    }
+    tile[r][tx] = v;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t b = b0 + r, c = c0 + tx;
+    if (b < B && c < C) dst[b * ld + c] = tile[tx][r];
+  }
+}
+
+template <typename T>
+__global__ void k_fill(T* p, int64_t count, T v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+// Kept-row data from the full rows: R[i] = RF[kept[i]] * scale_i and
+// D[i] = MF[kept[i]] / scale_i (bounds.py:230-239).
+template <typename T>
+__global__ void k_prep_rows(int m, int64_t Bp, const int32_t* __restrict__ kept,
+                            const T* __restrict__ scale, const T* __restrict__ RF,
+                            const T* __restrict__ MF, T* __restrict__ R, T* __restrict__ D) {
+  const int64_t total = (int64_t)m * Bp;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / Bp, b = e - i * Bp;
+    const int64_t src = (int64_t)kept[i] * Bp + b;
+    R[e] = RF[src] * scale[i];
+    D[e] = MF ? MF[src] / scale[i] : T(0);
+  }
+}
+
+// Variable bounds from singleton inequality rows (bounds.py:193-209).
+// ``cols`` samples per variable: Bp (per-sample) or 1 (shared bounds, sample 0).
+template <typename T>
+__global__ void k_prep_bounds(int n, int64_t Bp, int64_t cols, const int32_t* __restrict__ bptr,
+                              const int32_t* __restrict__ brow, const T* __restrict__ bcoef,
+                              const T* __restrict__ RF, T* __restrict__ LO, T* __restrict__ HI,
+                              int32_t* feasible, int64_t batch) {
+  const int64_t total = (int64_t)n * cols;
+  const T inf = __builtin_inf();
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t j = e / cols, b = e - j * cols;
+    T lo = -inf, hi = inf;
+    bool ok = true;
+    for (int k = bptr[j]; k < bptr[j + 1]; ++k) {
+      const T c = bcoef[k];
+      const T rr = RF[(int64_t)brow[k] * Bp + b];
+      const T th = rr / (c != T(0) ? c : T(1));
+      if (c < T(0)) lo = maxp(lo, th);
+      if (c > T(0)) hi = minp(hi, th);
+      if (!(c != T(0) || rr >= T(0))) ok = false;
+    }
+    if (!(lo <= hi)) ok = false;
+    LO[e] = lo;
+    HI[e] = hi;
+    if (!ok) {
+      if (cols == 1) {
+        for (int64_t s = 0; s < batch; ++s) feasible[s] = 0;
+      } else if (b < batch) {
+        feasible[b] = 0;
+      }
+    }
+  }
+}
+
+// Plain products for the first-kernel entry point: out = K x (rows) or K^T x
+// (columns), one row/column per wave.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_spmv_rows(Mat<T> K, int64_t Bp, const T* __restrict__ X,
+                                                       T* __restrict__ out) {
+  using V = typename Lane<T>::V;
+  constexpr int S = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  for (int rb = blockIdx.y; rb * 4 < K.m; rb += gridDim.y) {
+    const int i = rb * 4 + wave;
+    if (i >= K.m) continue;
+    V acc = vsplat<T>(T(0));
+    for (int k = K.rptr[i]; k < K.rptr[i + 1]; ++k)
+      acc += K.rval[k] * vload(X + (size_t)K.ridx[k] * Bp + b0);
+    vstore(out + (size_t)i * Bp + b0, acc);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_spmv_cols(Mat<T> K, int64_t Bp, const T* __restrict__ X,
+                                                       T* __restrict__ out) {
+  using V = typename Lane<T>::V;
+  constexpr int S = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  for (int cb = blockIdx.y; cb * 4 < K.n; cb += gridDim.y) {
+    const int j = cb * 4 + wave;
+    if (j >= K.n) continue;
+    V acc = vsplat<T>(T(0));
+    for (int k = K.cptr[j]; k < K.cptr[j + 1]; ++k)
+      acc += K.cval[k] * vload(X + (size_t)K.cidx[k] * Bp + b0);
+    vstore(out + (size_t)j * Bp + b0, acc);
+  }
+}
+
+template <typename T>
+__global__ void k_write_header(int64_t* hdr, int64_t batch, int64_t Bp, int64_t kind,
+                               int64_t shared, int64_t dtype, int64_t n, int64_t m, int64_t M) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    hdr[0] = 0x5055524e43503031LL;
+    hdr[1] = batch;
+    hdr[2] = Bp;
+    hdr[3] = kind;
+    hdr[4] = shared;
+    hdr[5] = dtype;
+    hdr[6] = n;
+    hdr[7] = m;
+    hdr[8] = M;
+  }
+}
+
+template <typename T>
+__global__ void k_finish_solve(int64_t batch, const int32_t* __restrict__ count,
+                               const T* __restrict__ ores, const T* __restrict__ ogap,
+                               const int32_t* __restrict__ oconv, int32_t* iterations, T* residual,
+                               T* gap, uint8_t* converged) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  if (iterations) iterations[b] = count[b];
+  if (residual) residual[b] = ores[b];
+  if (gap) gap[b] = ogap[b];
+  if (converged) converged[b] = oconv[b] ? 1 : 0;
+}
+
+template <typename T>
+__global__ void k_init_flags(int64_t batch, int64_t Bp, int32_t* done, int32_t* count,
+                             int32_t* feasible, const uint8_t* __restrict__ feas_in,
+                             int32_t* ndone) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b == 0) *ndone = 0;
+  if (b >= Bp) return;
+  done[b] = b < batch ? 0 : 1;
+  count[b] = 0;
+  feasible[b] = b < batch ? (feas_in ? (feas_in[b] ? 1 : 0) : 1) : 0;
+}
+
+}  // namespace purin

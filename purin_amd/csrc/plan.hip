@@ -1,0 +1,431 @@
+// Plan preparation: bound presolve classification, row scaling, step sizes,
+// CSR/CSC construction and device upload.
+//
+// Mirrors the preparation in the reference (paths into SOULS-TAMU/Purin):
+//   layout / kept rows          src/purin/solvers/chambolle_pock/solver.py:44-62
+//   singleton bound rows        src/purin/solvers/chambolle_pock/bounds.py:320-326
+//   row scaling + tolerance     src/purin/solvers/chambolle_pock/bounds.py:210-236
+//   norm-bound steps            src/purin/solvers/chambolle_pock/kernels.py:209-227
+//   adjoint power iteration     src/purin/solvers/chambolle_pock/bounds.py:83-101,
+//                               src/purin/solvers/chambolle_pock/kernels.py:52-65
+// With the constraint matrix shared by the batch every one of these is a
+// property of the matrix alone, so it is computed once here, on the host, in
+// the plan's precision.
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "plan.hpp"
+
+namespace purin {
+
+static thread_local std::string g_error;
+
+int set_error(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  return set_error(PURIN_CP_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+size_t elem_size(const purin_cp_plan* p) { return p->dtype == PURIN_CP_F64 ? 8 : 4; }
+
+int64_t padded_batch(const purin_cp_plan* p, int64_t batch) {
+  const int64_t tile = p->dtype == PURIN_CP_F64 ? tile_samples<double>() : tile_samples<float>();
+  return round_up(std::max<int64_t>(batch, 1), tile);
+}
+
+void* workspace(purin_cp_plan* p, size_t bytes, hipStream_t stream, int* err, bool adjoint) {
+  *err = PURIN_CP_OK;
+  void*& buf = adjoint ? p->aws : p->ws;
+  size_t& have = adjoint ? p->aws_bytes : p->ws_bytes;
+  if (bytes <= have && buf) return buf;
+  if (buf) {
+    // kernels of an earlier call may still read the old buffer
+    hipError_t e = hipStreamSynchronize(stream);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+      *err = hip_check(e, "synchronize before workspace growth");
+      return nullptr;
+    }
+    (void)hipFree(buf);
+    buf = nullptr;
+    have = 0;
+  }
+  bytes = (size_t)round_up((int64_t)bytes, 1 << 20);
+  hipError_t e = hipMalloc(&buf, bytes);
+  if (e != hipSuccess) {
+    buf = nullptr;
+    *err = set_error(PURIN_CP_ERR_NOMEM, std::string("workspace hipMalloc: ") + hipGetErrorString(e));
+    return nullptr;
+  }
+  have = bytes;
+  return buf;
+}
+
+// splitmix64 start vector in [-1, 1) (the oracle's start_vector restates it).
+static double start_value(uint64_t seed, uint64_t j) {
+  uint64_t z = (seed << 32) + j + 0x9E3779B97F4A7C15ULL;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  z = z ^ (z >> 31);
+  return (double)(z >> 11) * 0x1.0p-53 * 2.0 - 1.0;
+}
+
+template <typename T>
+struct HostMatrix {
+  // kept rows in CSR, values in T
+  std::vector<int32_t> ptr, idx;
+  std::vector<T> val_s, val_o;
+  std::vector<int32_t> cptr, cidx;
+  std::vector<T> cval_s, cval_o;
+};
+
+template <typename T>
+static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices,
+                 const double* values) {
+  const int64_t n = p->n, me = p->me, M = p->M;
+  // --- classify rows --------------------------------------------------------
+  std::vector<std::vector<std::pair<int64_t, double>>> bounds_of(n);
+  for (int64_t r = 0; r < M; ++r) {
+    const int64_t len = indptr[r + 1] - indptr[r];
+    if (r >= me && len == 1) {
+      const int32_t j = indices[indptr[r]];
+      bounds_of[j].push_back({r, values[indptr[r]]});
+    } else {
+      p->kept.push_back(r);
+    }
+  }
+  p->m = (int64_t)p->kept.size();
+  p->bound.clear();
+  p->bvar.clear();
+  p->bcoef.clear();
+  std::vector<int32_t> bptr(n + 1, 0);
+  for (int64_t j = 0; j < n; ++j) {
+    bptr[j + 1] = bptr[j] + (int32_t)bounds_of[j].size();
+    for (auto& rc : bounds_of[j]) {
+      p->bound.push_back(rc.first);
+      p->bvar.push_back((int32_t)j);
+      p->bcoef.push_back(rc.second);
+    }
+  }
+  // --- kept CSR, row scaling (bounds.py:210-214) ------------------------------
+  HostMatrix<T> H;
+  const int64_t m = p->m;
+  H.ptr.assign(m + 1, 0);
+  std::vector<T> scale(m, T(1));
+  for (int64_t i = 0; i < m; ++i) {
+    const int64_t r = p->kept[i];
+    T sq = T(0);
+    for (int64_t k = indptr[r]; k < indptr[r + 1]; ++k) {
+      const T v = (T)values[k];
+      sq = sq + v * v;
+      H.idx.push_back(indices[k]);
+      H.val_o.push_back(v);
+    }
+    H.ptr[i + 1] = (int32_t)H.idx.size();
+    if (p->opts.row_scaling) {
+      const T norm = std::sqrt(sq);
+      scale[i] = norm > T(0) ? T(1) / std::max(norm, (T)1e-30) : T(1);
+    }
+  }
+  p->nnz = (int64_t)H.idx.size();
+  H.val_s.resize(p->nnz);
+  T min_scale = T(1);
+  for (int64_t i = 0; i < m; ++i) {
+    for (int32_t k = H.ptr[i]; k < H.ptr[i + 1]; ++k) H.val_s[k] = H.val_o[k] * scale[i];
+    min_scale = std::min(min_scale, scale[i]);
+  }
+  p->scale.assign(scale.begin(), scale.end());
+  p->tol_factor = (double)std::min(T(1), min_scale);
+  // --- CSC, increasing kept-row order per column ------------------------------
+  H.cptr.assign(n + 1, 0);
+  for (int64_t k = 0; k < p->nnz; ++k) H.cptr[H.idx[k] + 1]++;
+  for (int64_t j = 0; j < n; ++j) H.cptr[j + 1] += H.cptr[j];
+  H.cidx.resize(p->nnz);
+  H.cval_s.resize(p->nnz);
+  H.cval_o.resize(p->nnz);
+  {
+    std::vector<int32_t> fill(H.cptr.begin(), H.cptr.end() - 1);
+    for (int64_t i = 0; i < m; ++i)
+      for (int32_t k = H.ptr[i]; k < H.ptr[i + 1]; ++k) {
+        const int32_t pos = fill[H.idx[k]]++;
+        H.cidx[pos] = (int32_t)i;
+        H.cval_s[pos] = H.val_s[k];
+        H.cval_o[pos] = H.val_o[k];
+      }
+  }
+  // --- forward steps (kernels.py:209-227, norm_bound) -------------------------
+  const T safety = (T)p->opts.safety;
+  {
+    T rmax = T(0), cmax = T(0);
+    for (int64_t i = 0; i < m; ++i) {
+      T s = T(0);
+      for (int32_t k = H.ptr[i]; k < H.ptr[i + 1]; ++k) s = s + std::fabs(H.val_s[k]);
+      rmax = std::max(rmax, s);
+    }
+    for (int64_t j = 0; j < n; ++j) {
+      T s = T(0);
+      for (int32_t k = H.cptr[j]; k < H.cptr[j + 1]; ++k) s = s + std::fabs(H.cval_s[k]);
+      cmax = std::max(cmax, s);
+    }
+    T norm = std::sqrt(rmax * cmax);
+    if (!p->opts.norm_bound) norm = T(0);  // replaced by the power iteration below
+    p->L = (double)norm;
+  }
+  // --- power iteration on K^T K (kernels.py:52-65) ----------------------------
+  T Lpi;
+  {
+    std::vector<T> x(n), z(m), w(n);
+    const T eps = (T)1e-12;
+    for (int64_t j = 0; j < n; ++j) x[j] = (T)start_value((uint64_t)p->opts.norm_seed, j);
+    T nx = T(0);
+    for (int64_t j = 0; j < n; ++j) nx = nx + x[j] * x[j];
+    nx = std::sqrt(nx) + eps;
+    for (int64_t j = 0; j < n; ++j) x[j] = x[j] / nx;
+    T eig = T(0);
+    for (int it = 0; it < p->opts.norm_iterations; ++it) {
+      for (int64_t i = 0; i < m; ++i) {
+        T s = T(0);
+        for (int32_t k = H.ptr[i]; k < H.ptr[i + 1]; ++k) s = s + H.val_s[k] * x[H.idx[k]];
+        z[i] = s;
+      }
+      for (int64_t j = 0; j < n; ++j) {
+        T s = T(0);
+        for (int32_t k = H.cptr[j]; k < H.cptr[j + 1]; ++k) s = s + H.cval_s[k] * z[H.cidx[k]];
+        w[j] = s;
+      }
+      eig = T(0);
+      T nw = T(0);
+      for (int64_t j = 0; j < n; ++j) {
+        eig = eig + x[j] * w[j];
+        nw = nw + w[j] * w[j];
+      }
+      nw = std::sqrt(nw) + eps;
+      for (int64_t j = 0; j < n; ++j) x[j] = w[j] / nw;
+    }
+    Lpi = std::sqrt(std::max(eig, T(0))) + eps;
+  }
+  {
+    const T Lf = std::max(p->opts.norm_bound ? (T)p->L : Lpi, (T)1e-12);
+    p->L = (double)Lf;
+    p->sigma0 = (double)(safety / Lf);
+    p->tau0 = (double)(p->opts.accelerated ? safety / Lf : safety / (T(1) + Lf));
+    const T La = std::max(Lpi, (T)1e-12);
+    p->Ladj = (double)La;
+    p->tau_adj = (double)(safety / (T(1) + La));
+    p->sigma_adj = (double)(safety / La);
+  }
+  // --- upload -----------------------------------------------------------------
+  auto up = [&](void** dst, const void* src, size_t bytes) -> int {
+    *dst = nullptr;
+    if (bytes == 0) bytes = 16;  // keep valid pointers for empty arrays
+    hipError_t e = hipMalloc(dst, bytes);
+    if (e != hipSuccess) return set_error(PURIN_CP_ERR_NOMEM, "plan hipMalloc failed");
+    p->owned.push_back(*dst);
+    if (src) {
+      e = hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice);
+      if (e != hipSuccess) return hip_check(e, "plan upload");
+    }
+    return PURIN_CP_OK;
+  };
+  std::vector<int32_t> kept32(p->kept.begin(), p->kept.end());
+  std::vector<int32_t> brow32(p->bound.begin(), p->bound.end());
+  std::vector<T> bcoefT(p->bcoef.begin(), p->bcoef.end());
+  int rc = PURIN_CP_OK;
+#define UP(dst, vec) \
+  if ((rc = up((void**)&(dst), (vec).empty() ? nullptr : (vec).data(), (vec).size() * sizeof((vec)[0]))) != PURIN_CP_OK) return rc
+  UP(p->rptr, H.ptr);
+  UP(p->ridx, H.idx);
+  UP(p->rval_s, H.val_s);
+  UP(p->rval_o, H.val_o);
+  UP(p->cptr, H.cptr);
+  UP(p->cidx, H.cidx);
+  UP(p->cval_s, H.cval_s);
+  UP(p->cval_o, H.cval_o);
+  UP(p->dscale, scale);
+  UP(p->dkept, kept32);
+  UP(p->bptr, bptr);
+  UP(p->brow, brow32);
+  UP(p->dbcoef, bcoefT);
+#undef UP
+  return PURIN_CP_OK;
+}
+
+}  // namespace purin
+
+using namespace purin;
+
+extern "C" {
+
+void purin_cp_default_options(purin_cp_options* o) {
+  if (!o) return;
+  o->accelerated = 0;
+  o->row_scaling = 1;
+  o->norm_bound = 1;
+  o->norm_iterations = 20;
+  o->norm_seed = 42;
+  o->diagonal_preconditioning = 0;
+  o->safety = 0.95;
+}
+
+void purin_cp_default_solve_options(purin_cp_solve_options* o) {
+  if (!o) return;
+  o->tolerance = 1e-9;
+  o->max_iterations = 10000;
+  o->early_stop = 1;
+  o->check_every = 32;
+  o->shared_bounds = 0;
+  o->timing = 0;
+}
+
+void purin_cp_default_adjoint_options(purin_cp_adjoint_options* o) {
+  if (!o) return;
+  o->tolerance = 1e-9;
+  o->atol = 0.0;
+  o->restart = 30;
+  o->max_iterations = 100;
+  o->adjoint_tolerance = 1e-8;
+  o->force_eligible = 0;
+  o->reserved = 0;
+}
+
+const char* purin_cp_last_error(void) { return g_error.c_str(); }
+
+const char* purin_cp_build_info(void) {
+  return "purin_cp abi=1 target=gfx950 (CDNA4) kernels=HIP";
+}
+
+int purin_cp_plan_create(purin_cp_plan** out, int32_t dtype, int64_t n, int64_t me, int64_t mi,
+                         const int64_t* indptr, const int32_t* indices, const double* values,
+                         const purin_cp_options* opts) {
+  if (!out) return set_error(PURIN_CP_ERR_ARG, "plan pointer is NULL");
+  *out = nullptr;
+  if (dtype != PURIN_CP_F32 && dtype != PURIN_CP_F64)
+    return set_error(PURIN_CP_ERR_ARG, "dtype must be PURIN_CP_F32 or PURIN_CP_F64");
+  if (n < 1) return set_error(PURIN_CP_ERR_ARG, "batch_size and variable_size must be positive");
+  if (me < 0 || mi < 0) return set_error(PURIN_CP_ERR_ARG, "row counts must be nonnegative");
+  if (n > (1LL << 30) || me + mi > (1LL << 30))
+    return set_error(PURIN_CP_ERR_ARG, "problem too large for 32-bit indices");
+  if (!indptr) return set_error(PURIN_CP_ERR_ARG, "indptr is NULL");
+  const int64_t M = me + mi;
+  if (indptr[0] != 0) return set_error(PURIN_CP_ERR_ARG, "indptr[0] must be 0");
+  for (int64_t r = 0; r < M; ++r) {
+    if (indptr[r + 1] < indptr[r]) return set_error(PURIN_CP_ERR_ARG, "indptr must be nondecreasing");
+    for (int64_t k = indptr[r]; k < indptr[r + 1]; ++k) {
+      if (indices[k] < 0 || indices[k] >= n)
+        return set_error(PURIN_CP_ERR_ARG, "column index out of range");
+      if (k > indptr[r] && indices[k] <= indices[k - 1])
+        return set_error(PURIN_CP_ERR_ARG, "columns must be strictly ascending within a row");
+      if (!std::isfinite(values[k])) return set_error(PURIN_CP_ERR_ARG, "non-finite coefficient");
+    }
+  }
+  if (indptr[M] > (1LL << 31) - 1) return set_error(PURIN_CP_ERR_ARG, "too many nonzeros");
+  purin_cp_options o;
+  purin_cp_default_options(&o);
+  if (opts) o = *opts;
+  if (!(o.safety > 0.0 && o.safety < 1.0))
+    return set_error(PURIN_CP_ERR_ARG, "safety must be between zero and one");
+  if (o.norm_iterations < 1) return set_error(PURIN_CP_ERR_ARG, "norm_iterations must be a positive integer");
+  if (o.diagonal_preconditioning && !o.accelerated)
+    return set_error(PURIN_CP_ERR_UNSUPPORTED,
+                     "diagonal_preconditioning is not implemented by the HIP path");
+  auto* p = new purin_cp_plan();
+  p->dtype = dtype;
+  p->n = n;
+  p->me = me;
+  p->mi = mi;
+  p->M = M;
+  p->opts = o;
+  int rc = dtype == PURIN_CP_F64 ? build<double>(p, indptr, indices, values)
+                                 : build<float>(p, indptr, indices, values);
+  if (rc == PURIN_CP_OK) {
+    hipError_t e = hipHostMalloc((void**)&p->pinned, 64, hipHostMallocDefault);
+    if (e != hipSuccess) rc = hip_check(e, "hipHostMalloc");
+  }
+  if (rc != PURIN_CP_OK) {
+    purin_cp_plan_destroy(p);
+    return rc;
+  }
+  *out = p;
+  return PURIN_CP_OK;
+}
+
+void purin_cp_plan_destroy(purin_cp_plan* p) {
+  if (!p) return;
+  (void)hipDeviceSynchronize();
+  for (void* ptr : p->owned) (void)hipFree(ptr);
+  if (p->metric) (void)hipFree(p->metric);
+  if (p->ws) (void)hipFree(p->ws);
+  if (p->aws) (void)hipFree(p->aws);
+  if (p->pinned) (void)hipHostFree(p->pinned);
+  delete p;
+}
+
+int purin_cp_plan_get_info(const purin_cp_plan* p, purin_cp_plan_info* info) {
+  if (!p || !info) return set_error(PURIN_CP_ERR_ARG, "NULL argument");
+  info->dtype = p->dtype;
+  info->n = p->n;
+  info->me = p->me;
+  info->mi = p->mi;
+  info->kept_rows = p->m;
+  info->bound_rows = (int64_t)p->bound.size();
+  info->nnz_kept = p->nnz;
+  info->norm = p->L;
+  info->tau0 = p->tau0;
+  info->sigma0 = p->sigma0;
+  info->adjoint_norm = p->Ladj;
+  info->adjoint_tau = p->tau_adj;
+  info->adjoint_sigma = p->sigma_adj;
+  info->tolerance_factor = p->tol_factor;
+  return PURIN_CP_OK;
+}
+
+int purin_cp_last_timing(const purin_cp_plan* p, purin_cp_timing* t) {
+  if (!p || !t) return set_error(PURIN_CP_ERR_ARG, "NULL argument");
+  *t = p->timing;
+  return PURIN_CP_OK;
+}
+
+int purin_cp_plan_kept_rows(const purin_cp_plan* p, int64_t* rows, double* scale) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  for (int64_t i = 0; i < p->m; ++i) {
+    if (rows) rows[i] = p->kept[i];
+    if (scale) scale[i] = p->scale[i];
+  }
+  return PURIN_CP_OK;
+}
+
+int purin_cp_plan_set_metric(purin_cp_plan* p, const double* sqrt_d) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  if (p->metric) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(p->metric);
+    p->metric = nullptr;
+    p->metric_host.clear();
+  }
+  if (!sqrt_d) return PURIN_CP_OK;
+  for (int64_t j = 0; j < p->n; ++j)
+    if (!(sqrt_d[j] > 0.0) || !std::isfinite(sqrt_d[j]))
+      return set_error(PURIN_CP_ERR_ARG, "metric_diagonal must be positive and finite");
+  p->metric_host.assign(sqrt_d, sqrt_d + p->n);
+  const size_t es = elem_size(p);
+  std::vector<char> buf(p->n * es);
+  for (int64_t j = 0; j < p->n; ++j) {
+    if (p->dtype == PURIN_CP_F64)
+      reinterpret_cast<double*>(buf.data())[j] = sqrt_d[j];
+    else
+      reinterpret_cast<float*>(buf.data())[j] = (float)sqrt_d[j];
+  }
+  PURIN_HIP(hipMalloc(&p->metric, buf.size()));
+  PURIN_HIP(hipMemcpy(p->metric, buf.data(), buf.size(), hipMemcpyHostToDevice));
+  return PURIN_CP_OK;
+}
+
+}  // extern "C"

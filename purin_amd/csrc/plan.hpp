@@ -1,0 +1,77 @@
+// Plan object behind the opaque purin_cp_plan handle.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/purin_cp.h"
+#include "common.hpp"
+
+// Kernel tiling constants shared by the host drivers and the kernels.
+namespace purin {
+constexpr int kRowsPerWaveFixed = 1;  // fixed-iteration passes: one row per wave
+constexpr int kRowsPerWaveEarly = 8;  // diagnostic passes: 8 rows/columns per wave
+constexpr int kSavedHeader = 256;     // bytes of the saved-state header
+constexpr int64_t kSavedMagic = 0x5055524e43503031LL;  // "PURNCP01"
+}  // namespace purin
+
+struct purin_cp_plan {
+  int32_t dtype = PURIN_CP_F64;
+  int64_t n = 0, me = 0, mi = 0, M = 0;
+  purin_cp_options opts{};
+
+  // host-side structure
+  std::vector<int64_t> kept;       // kept row -> original row
+  std::vector<double> scale;       // per kept row, rounded to dtype
+  std::vector<int64_t> bound;      // bound rows (original index), grouped by variable
+  std::vector<int32_t> bvar;       // variable of each bound row
+  std::vector<double> bcoef;       // coefficient of each bound row
+  int64_t m = 0;                   // kept rows
+  int64_t nnz = 0;                 // nonzeros of the kept rows
+  double L = 0, tau0 = 0, sigma0 = 0;
+  double Ladj = 0, tau_adj = 0, sigma_adj = 0;
+  double tol_factor = 1;
+
+  // device copies (element type = dtype for the value arrays)
+  int32_t* rptr = nullptr;  // CSR of kept rows
+  int32_t* ridx = nullptr;
+  void* rval_s = nullptr;   // scaled coefficients
+  void* rval_o = nullptr;   // original coefficients
+  int32_t* cptr = nullptr;  // CSC of kept rows (increasing row per column)
+  int32_t* cidx = nullptr;  // kept-row index
+  void* cval_s = nullptr;
+  void* cval_o = nullptr;
+  void* dscale = nullptr;   // m
+  int32_t* dkept = nullptr; // m: original row
+  int32_t* bptr = nullptr;  // n+1: bound rows per variable
+  int32_t* brow = nullptr;  // original row of each bound row
+  void* dbcoef = nullptr;   // coefficient of each bound row
+  void* metric = nullptr;   // sqrt(D) (n) or nullptr
+  std::vector<double> metric_host;
+
+  // plan-owned workspace (grown on demand)
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  void* aws = nullptr;        // adjoint workspace
+  size_t aws_bytes = 0;
+  int32_t* pinned = nullptr;  // host-pinned flag words
+
+  std::vector<void*> owned;   // device allocations freed with the plan
+  purin_cp_timing timing{};   // last timed call
+};
+
+namespace purin {
+// thread-local error message helpers (plan.hip)
+int set_error(int code, const std::string& msg);
+int hip_check(hipError_t e, const char* what);
+int64_t padded_batch(const purin_cp_plan* p, int64_t batch);
+size_t elem_size(const purin_cp_plan* p);
+void* workspace(purin_cp_plan* p, size_t bytes, hipStream_t stream, int* err, bool adjoint = false);
+}  // namespace purin
+
+#define PURIN_HIP(call)                                        \
+  do {                                                         \
+    hipError_t e_ = (call);                                    \
+    if (e_ != hipSuccess) return purin::hip_check(e_, #call);  \
+  } while (0)

@@ -1,0 +1,212 @@
+// Post-processing of a projection on the device: dual unscaling and placement,
+// bound-multiplier recovery, original-unit residuals, slacks and status codes.
+// Reference: src/purin/solvers/chambolle_pock/bounds.py:247-317.
+#pragma once
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace purin {
+
+template <typename T>
+struct Post {
+  Mat<T> K;                      // kept rows, ORIGINAL coefficients
+  int64_t Bp, me, mi;
+  const T* __restrict__ scale;   // m
+  const int32_t* __restrict__ kept;
+  const int32_t* __restrict__ bptr;
+  const int32_t* __restrict__ brow;
+  const T* __restrict__ bcoef;
+  const T* __restrict__ tgt;     // n x Bp
+  const T* __restrict__ Y;       // n x Bp
+  const T* __restrict__ D;       // m x Bp (scaled duals)
+  const T* __restrict__ RF;      // M x Bp (original rhs)
+  const T* __restrict__ LO;
+  const T* __restrict__ HI;
+  int shared_bounds;
+  T* DF;                         // M x Bp multipliers
+  T* SL;                         // mi x Bp slacks
+  T* rowpart;                    // [2][nrb][Bp]: residual max, finite(dual)
+  T* colpart;                    // [3][ncb][Bp]: residual max (bound rows), stationarity, finite
+  int nrb, ncb;
+};
+
+// Kept rows: multiplier = d * scale (bounds.py:247), r = K y - rhs (285-289),
+// slack = max(-r, 0) for inequality rows (311).
+template <typename T, int RPW>
+__global__ __launch_bounds__(kBlock) void k_post_rows(Post<T> P) {
+  using V = typename Lane<T>::V;
+  constexpr int S = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  const T zero = T(0);
+  for (int rb = blockIdx.y; rb * 4 * RPW < P.K.m; rb += gridDim.y) {
+    V res = vsplat<T>(zero), fin = vsplat<T>(T(1));
+    for (int c = 0; c < RPW; ++c) {
+      const int i = (rb * 4 + wave) * RPW + c;
+      if (i >= P.K.m) break;
+      const int s0 = P.K.rptr[i], s1 = P.K.rptr[i + 1];
+      V acc = vsplat<T>(zero);
+      for (int k = s0; k < s1; ++k) {
+        const T v = P.K.rval[k];
+        acc += v * vload(P.Y + (size_t)P.K.ridx[k] * P.Bp + b0);
+      }
+      const int64_t row = P.kept[i];
+      const V d = vload(P.D + (size_t)i * P.Bp + b0);
+      const V full = d * P.scale[i];
+      vstore(P.DF + (size_t)row * P.Bp + b0, full);
+      const V r = acc - vload(P.RF + (size_t)row * P.Bp + b0);
+      if (row < P.me) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) res[s] = maxp(res[s], absv(r[s]));
+      } else {
+        V sl;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          res[s] = maxp(res[s], maxp(r[s], zero));
+          sl[s] = maxp(-r[s], zero);
+        }
+        vstore(P.SL + (size_t)(row - P.me) * P.Bp + b0, sl);
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        if (!finite(full[s])) fin[s] = zero;
+    }
+    __shared__ T buf[kBlock * S];
+    const V p0 = block_combine<T>(res, buf, OpMax());
+    const V p1 = block_combine<T>(fin, buf, OpMin());
+    if (wave == 0) {
+      T* base = P.rowpart + (size_t)rb * P.Bp + b0;
+      vstore(base, p0);
+      vstore(base + (size_t)P.nrb * P.Bp, p1);
+    }
+  }
+}
+
+// Variables: base stationarity y - yhat + K_kept^T dual (bounds.py:248-249),
+// bound multipliers split among tied rows (252-284), bound-row residuals and
+// slacks (285-289, 311), full stationarity (290).
+template <typename T, int CPW>
+__global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
+  using V = typename Lane<T>::V;
+  constexpr int S = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  const T zero = T(0), one = T(1);
+  for (int cb = blockIdx.y; cb * 4 * CPW < P.K.n; cb += gridDim.y) {
+    V res = vsplat<T>(zero), stat = vsplat<T>(zero), fin = vsplat<T>(one);
+    for (int c = 0; c < CPW; ++c) {
+      const int j = (cb * 4 + wave) * CPW + c;
+      if (j >= P.K.n) break;
+      const int s0 = P.K.cptr[j], s1 = P.K.cptr[j + 1];
+      V tk = vsplat<T>(zero);
+      for (int k = s0; k < s1; ++k) {
+        const int i = P.K.cidx[k];
+        const T v = P.K.cval[k];
+        tk += v * (vload(P.D + (size_t)i * P.Bp + b0) * P.scale[i]);
+      }
+      const size_t off = (size_t)j * P.Bp + b0;
+      const V y = vload(P.Y + off);
+      const V dy = y - vload(P.tgt + off);
+      const V base = dy + tk;
+      V lo, hi;
+      if (P.shared_bounds) {
+        lo = vsplat<T>(P.LO[j]);
+        hi = vsplat<T>(P.HI[j]);
+      } else {
+        lo = vload(P.LO + off);
+        hi = vload(P.HI + off);
+      }
+      const int k0 = P.bptr[j], k1 = P.bptr[j + 1];
+      V lc = vsplat<T>(zero), uc = vsplat<T>(zero);
+      for (int k = k0; k < k1; ++k) {
+        const T cf = P.bcoef[k];
+        const V rr = vload(P.RF + (size_t)P.brow[k] * P.Bp + b0);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const T th = rr[s] / (cf != zero ? cf : one);
+          lc[s] += (cf < zero && th == lo[s] && y[s] == lo[s]) ? one : zero;
+          uc[s] += (cf > zero && th == hi[s] && y[s] == hi[s]) ? one : zero;
+        }
+      }
+      V tfull = tk;
+      for (int k = k0; k < k1; ++k) {
+        const T cf = P.bcoef[k];
+        const int64_t row = P.brow[k];
+        const V rr = vload(P.RF + (size_t)row * P.Bp + b0);
+        V bd, sl;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const T th = rr[s] / (cf != zero ? cf : one);
+          const bool il = cf < zero && th == lo[s] && y[s] == lo[s];
+          const bool iu = cf > zero && th == hi[s] && y[s] == hi[s];
+          T v = il ? maxp(base[s], zero) / maxp(lc[s], one) : zero;
+          v = v + (iu ? maxp(-base[s], zero) / maxp(uc[s], one) : zero);
+          v = v / (cf != zero ? absv(cf) : one);
+          bd[s] = v;
+          tfull[s] += cf * v;
+          const T r = cf * y[s] - rr[s];
+          res[s] = maxp(res[s], maxp(r, zero));
+          sl[s] = maxp(-r, zero);
+          if (!finite(v)) fin[s] = zero;
+        }
+        vstore(P.DF + (size_t)row * P.Bp + b0, bd);
+        vstore(P.SL + (size_t)(row - P.me) * P.Bp + b0, sl);
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        stat[s] = maxp(stat[s], absv(dy[s] + tfull[s]));
+        if (!finite(y[s])) fin[s] = zero;
+      }
+    }
+    __shared__ T buf[kBlock * S];
+    const V p0 = block_combine<T>(res, buf, OpMax());
+    const V p1 = block_combine<T>(stat, buf, OpMax());
+    const V p2 = block_combine<T>(fin, buf, OpMin());
+    if (wave == 0) {
+      const size_t plane = (size_t)P.ncb * P.Bp;
+      T* base = P.colpart + (size_t)cb * P.Bp + b0;
+      vstore(base, p0);
+      vstore(base + plane, p1);
+      vstore(base + 2 * plane, p2);
+    }
+  }
+}
+
+// Per-sample verdict (bounds.py:285-305).
+template <typename T>
+__global__ void k_post_final(Post<T> P, int64_t batch, T tol_cfg, T residual_factor,
+                             const int32_t* __restrict__ cp_conv, const T* __restrict__ cp_gap,
+                             const int32_t* __restrict__ count, int32_t* status,
+                             int32_t* iterations, T* residual_out, uint8_t* finite_out,
+                             uint8_t* eligible_out) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  const T zero = T(0);
+  T res = zero, stat = zero;
+  bool fin = true;
+  for (int r = 0; r < P.nrb; ++r) {
+    const T* p = P.rowpart + (size_t)r * P.Bp + b;
+    res = maxp(res, p[0]);
+    fin = fin && p[(size_t)P.nrb * P.Bp] != zero;
+  }
+  for (int c = 0; c < P.ncb; ++c) {
+    const T* p = P.colpart + (size_t)c * P.Bp + b;
+    const size_t plane = (size_t)P.ncb * P.Bp;
+    res = maxp(res, p[0]);
+    stat = maxp(stat, p[plane]);
+    fin = fin && p[2 * plane] != zero;
+  }
+  const T residual = maxp(res, stat);
+  const bool f = fin && finite(residual) && finite(cp_gap[b]);
+  const bool conv = f && cp_conv[b] != 0 && residual <= tol_cfg;
+  if (status) status[b] = conv ? 0 : (f ? 1 : 3);
+  if (iterations) iterations[b] = count[b];
+  if (residual_out) residual_out[b] = residual * residual_factor;
+  if (finite_out) finite_out[b] = f ? 1 : 0;
+  if (eligible_out) eligible_out[b] = conv ? 1 : 0;
+}
+
+}  // namespace purin

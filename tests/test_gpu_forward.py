@@ -1,0 +1,227 @@
+"""GPU parity of the forward path: HIP kernels (through the C ABI) vs the CPU oracle.
+
+Bars (from the task): relative error <= 1e-10 in fp64 and <= 1e-4 in fp32 on
+projected points and multipliers; identical iteration counts, status codes and
+active-set masks.  Relative error is ``max|a-b| / max|b|``.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import cp as ocp
+from oracle import projection as op
+from purin_amd import workloads
+from tests import _cases
+from tests._gpu import canonical_from_workload, plan_for, rel_err, require_gpu, to_np
+
+pytestmark = pytest.mark.gpu
+
+TOL = {np.float64: 1e-10, np.float32: 1e-4}
+
+
+def _kept(canon, rhs, dtype, cfg=op.Config()):
+    return op.presolve(canon, rhs, cfg, dtype)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("scaled", [True, False])
+def test_spmm_matches_oracle(dtype, transpose, scaled):
+    torch = require_gpu()
+    w = workloads.config1(batch=37)
+    canon = canonical_from_workload(w)
+    plan = plan_for(canon, dtype=dtype)
+    rhs = np.tile(w.rhs, (37, 1)).astype(dtype)
+    pre = _kept(canon, rhs, dtype)
+    ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
+    values = pre.kept_values[0] if scaled else pre.values[pre.rows]
+    mv, tmv = ocp.operators(values, ksup, kmask, canon.n)
+    rng = np.random.default_rng(0)
+    x = rng.normal(size=(37, len(pre.rows) if transpose else canon.n)).astype(dtype)
+    want = tmv(x) if transpose else mv(x)
+    got = to_np(plan.spmm(torch.as_tensor(x), transpose=transpose, scaled=scaled))
+    assert rel_err(got, want) <= (1e-14 if dtype == np.float64 else 1e-6)
+    np.testing.assert_allclose(plan.row_scale, pre.scale[0], rtol=1e-15 if dtype == np.float64 else 1e-7)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("accelerated", [False, True])
+@pytest.mark.parametrize("early_stop", [False, True])
+def test_solve_matches_oracle(dtype, accelerated, early_stop):
+    torch = require_gpu()
+    B = 50
+    w = workloads.small_random(11, n=48, me=8, mi=20, width=4, batch=B)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+    target = w.target.astype(dtype)
+    pre = _kept(canon, rhs, dtype)
+    ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
+    iters = 400
+    tol = 1e-6 if dtype == np.float64 else 1e-4
+    want = ocp.sparse_cp(np.ones_like(target), -target, pre.kept_values[0], pre.kept_rhs, ksup,
+                         kmask, canon.me, pre.lower, pre.upper, accelerated=accelerated,
+                         max_iterations=iters, tolerance=tol, y0=target,
+                         freeze_converged=True, check_stationarity=True, norm_bound=True,
+                         early_stop=early_stop)
+    plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
+    got = plan.solve(pre.kept_rhs, target, pre.lower, pre.upper, tolerance=tol,
+                     max_iterations=iters, early_stop=early_stop, check_every=7)
+    bar = TOL[dtype]
+    assert rel_err(to_np(got.y), want.y) <= bar
+    assert rel_err(to_np(got.dual), want.dual) <= bar
+    np.testing.assert_array_equal(to_np(got.iterations), want.iterations)
+    np.testing.assert_array_equal(to_np(got.converged), want.converged)
+    # diagnostics of a nearly converged iterate sit near the rounding floor in fp32
+    dtol = dict(rtol=1e-6, atol=1e-12) if dtype == np.float64 else dict(rtol=1e-2, atol=2e-5)
+    np.testing.assert_allclose(to_np(got.residual), want.residual, **dtol)
+    np.testing.assert_allclose(to_np(got.gap), want.gap, **dtol)
+    if early_stop and not accelerated:
+        assert np.any(want.iterations < iters), "the stop test should fire for some samples"
+    # active sets: bound activity and positive inequality duals
+    y, d = to_np(got.y), to_np(got.dual)
+    np.testing.assert_array_equal(y == pre.lower, want.y == pre.lower)
+    np.testing.assert_array_equal(y == pre.upper, want.y == pre.upper)
+    np.testing.assert_array_equal(d[:, canon.me:] > 0, want.dual[:, canon.me:] > 0)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_project_config1_fixed_iterations(dtype, accelerated):
+    """Config 1 (n=64, 16+32 rows, B=32, 1000 fixed iterations) through purin_cp_project."""
+    torch = require_gpu()
+    w = workloads.config1()
+    canon = canonical_from_workload(w)
+    B = w.batch
+    rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+    target = w.target.astype(dtype)
+    cfg = op.Config(accelerated=accelerated, max_iterations=1000, early_stop=False)
+    want = op.solve(canon, target, rhs, cfg, dtype=dtype)
+    plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
+    got = plan.project(target, rhs, max_iterations=1000, early_stop=False)
+    bar = TOL[dtype]
+    assert rel_err(to_np(got.y), want.y) <= bar
+    mult = np.concatenate((want.multipliers_eq, want.multipliers_ineq), axis=1)
+    assert rel_err(to_np(got.multipliers), mult) <= bar * 10
+    assert rel_err(to_np(got.slacks), want.slacks) <= bar
+    np.testing.assert_array_equal(to_np(got.status), want.status)
+    np.testing.assert_array_equal(to_np(got.iterations), want.iterations)
+    np.testing.assert_array_equal(to_np(got.finite), want.finite)
+    np.testing.assert_array_equal(to_np(got.eligible), want.gradient_eligible)
+    np.testing.assert_allclose(to_np(got.residual), want.residual_inf_norm,
+                               **(dict(rtol=1e-5, atol=1e-13) if dtype == np.float64
+                                  else dict(rtol=1e-2, atol=2e-5)))
+    np.testing.assert_array_equal(to_np(got.multipliers)[:, canon.me:] > 0, mult[:, canon.me:] > 0)
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_project_early_stop_counts_and_statuses(shared):
+    torch = require_gpu()
+    B = 77
+    w = workloads.small_random(5, n=40, me=6, mi=14, width=3, batch=B)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (B, 1))
+    cfg = op.Config(max_iterations=3000, tolerance=1e-8)
+    want = op.solve(canon, w.target, rhs, cfg)
+    plan = plan_for(canon, dtype=np.float64)
+    got = plan.project(w.target, rhs, max_iterations=3000, tolerance=1e-8, shared_bounds=shared,
+                       check_every=16)
+    np.testing.assert_array_equal(to_np(got.iterations), want.iterations)
+    np.testing.assert_array_equal(to_np(got.status), want.status)
+    assert np.any(want.status == op.CONVERGED)
+    assert rel_err(to_np(got.y), want.y) <= 1e-10
+
+
+def _kn(canon, target, rhs, **cfgkw):
+    torch = require_gpu()
+    cfg = op.Config(**cfgkw)
+    plan = plan_for(canon, dtype=np.float64, accelerated=cfg.accelerated)
+    got = plan.project(np.asarray(target, np.float64), np.asarray(rhs, np.float64),
+                       max_iterations=cfg.max_iterations, tolerance=cfg.tolerance)
+    return got, op.solve(canon, target, rhs, cfg)
+
+
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_known_answer_affine_projection(accelerated):
+    """Reference tests/test_regression_chambolle_pock.py:25-38."""
+    got, want = _kn(_cases.sum_equals_b_u_nonneg(), [[2.0, 0.0], [-2.0, 0.0]],
+                    [[1.0, 0.0], [1.0, 0.0]], accelerated=accelerated)
+    np.testing.assert_allclose(to_np(got.y), [[1.5, -0.5], [0.0, 1.0]], atol=1e-8)
+    assert np.all(to_np(got.status) == 0)
+    assert np.max(to_np(got.residual)) <= 1e-9
+    np.testing.assert_array_equal(to_np(got.iterations), want.iterations)
+
+
+def test_known_answer_tied_bounds_multipliers_slacks():
+    """Reference tests/test_regression_cp_bound_presolve.py:13-24 (no kept rows at all)."""
+    canon, rhs = _cases.tied_scaled_bounds()
+    got, want = _kn(canon, [[-3.0, 4.0]], rhs[None])
+    np.testing.assert_allclose(to_np(got.y), [[0.0, 1.0]], atol=1e-10)
+    np.testing.assert_allclose(to_np(got.multipliers), [[1.5, 0.75, 0.0, 3.0]], atol=1e-9)
+    np.testing.assert_allclose(to_np(got.slacks), [[0.0, 0.0, 2.0, 0.0]], atol=1e-10)
+    assert to_np(got.status)[0] == 0
+
+
+def test_known_answer_status_codes():
+    """Reference tests/test_regression_chambolle_pock.py:68-85, 140-164."""
+    canon = _cases.sum_equals_b_u_nonneg()
+    got, _ = _kn(canon, [[-2.0, 0.0]], [[1.0, 0.0]], max_iterations=1)
+    assert to_np(got.status)[0] == 1 and not to_np(got.eligible)[0]
+    got, _ = _kn(canon, [[np.nan, 0.0]], [[1.0, 0.0]], max_iterations=1)
+    assert to_np(got.status)[0] == 3
+    infeasible = _cases.canonical_from_dense(np.zeros((0, 1)), [[1.0], [-1.0]], 1)
+    got, _ = _kn(infeasible, [[0.0]], [[0.0, -1.0]], max_iterations=100)
+    assert to_np(got.status)[0] == 1 and not to_np(got.eligible)[0]
+    scaled = _cases.canonical_from_dense([[1000.0, 1000.0]], [[-1.0, 0.0]], 2)
+    got, _ = _kn(scaled, [[2.0, 0.0]], [[1000.0, 0.0]])
+    assert to_np(got.eligible)[0]
+    assert abs(float(to_np(got.y).sum()) * 1000 - 1000) <= 1e-9
+
+
+def test_known_answer_no_constraints_identity():
+    """Reference tests/test_regression_chambolle_pock.py:88-95."""
+    canon = op.Canonical(n=2, me=0, rows=[], coef=[])
+    got, _ = _kn(canon, [[0.2, 0.7]], np.zeros((1, 0)))
+    np.testing.assert_allclose(to_np(got.y), [[0.2, 0.7]], atol=1e-12)
+
+
+@pytest.mark.parametrize("seed", [12, 42])
+def test_known_answer_coupled_qp(seed):
+    """Reference tests/test_regression_cp_bound_presolve.py:56-101 (exact projection instead of OSQP)."""
+    from oracle import qp as bf
+
+    rng = np.random.default_rng(seed)
+    canon, rhs = _cases.coupled_qp()
+    x = rng.normal(size=(1, 3))
+    got, want = _kn(canon, x, rhs[None])
+    K = canon.dense()
+    y_ref = bf.project_bruteforce(x[0], K[:1], rhs[:1], K[1:], rhs[1:])[0]
+    np.testing.assert_allclose(to_np(got.y)[0], y_ref, atol=2e-8)
+    mult = to_np(got.multipliers)[0]
+    np.testing.assert_allclose((to_np(got.y)[0] - x[0]) + K.T @ mult, 0.0, atol=1e-9)
+    assert to_np(got.eligible)[0]
+
+
+@pytest.mark.parametrize("batch", [1, 127, 129, 300])
+def test_ragged_batches(batch):
+    torch = require_gpu()
+    w = workloads.small_random(3, n=30, me=4, mi=10, width=3, batch=batch)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (batch, 1))
+    cfg = op.Config(max_iterations=150, early_stop=False)
+    want = op.solve(canon, w.target, rhs, cfg)
+    got = plan_for(canon, dtype=np.float64).project(w.target, rhs, max_iterations=150,
+                                                    early_stop=False)
+    assert rel_err(to_np(got.y), want.y) <= 1e-10
+    np.testing.assert_array_equal(to_np(got.status), want.status)
+
+
+def test_invalid_arguments_raise():
+    torch = require_gpu()
+    from purin_amd._lib import PurinError
+
+    canon = _cases.sum_equals_b_u_nonneg()
+    plan = plan_for(canon, dtype=np.float64)
+    with pytest.raises(ValueError):
+        plan.project(np.zeros((2, 3)), np.zeros((2, 2)))
+    with pytest.raises(PurinError):
+        plan.project(np.zeros((1, 2)), np.zeros((1, 2)), max_iterations=0)
