@@ -1,6 +1,799 @@
-// Adjoint driver (implicit VJP through the CP fixed point).
+// Implicit VJP through the CP fixed point on the device.
+//
+// Reference: custom_vjp ``bwd`` (src/purin/solvers/chambolle_pock/bounds.py:80-165)
+// and _batched_restarted_gmres
+// (src/purin/solvers/primal_dual_interior_point/operators.py:792-1125).
+//
+// The state z = (y, d, ybar) of width W = 2n + m is stored batch-minor with
+// rows [0,n) = y, [n,n+m) = d, [n+m,2n+m) = ybar.  One cp_step (theta = 1,
+// fixed-step prox from the power-iteration steps) is linearised once at the
+// saved state into masks C (clip, per variable) and D (dual projection, per
+// row); its transpose Jacobian is then one K u (row pass) and one K^T w
+// (column pass):
+//   G = gy + 2 gb,  u = C G,  w = D (gd - delta K u),
+//   pullback(gy, gd, gb) = (a u - gb, w, sigma K^T w),
+//   g_rhs = -sigma w, g_target = delta u, g_lower = Clo G, g_upper = Chi G.
+// GMRES solves (I - J^T) lambda = [cot_y * converged, 0, 0] with the
+// reference's restart cycles, two-pass classical Gram--Schmidt, Givens
+// rotations, per-sample active masks and candidate acceptance.  The
+// Gram--Schmidt passes are batched dot/update kernels over 64-row chunks; the
+// Givens/back-substitution scalars run one thread per sample.
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
 #include "forward.hpp"
+#include "kernels.hpp"
 #include "plan.hpp"
+
+namespace purin {
+
+constexpr int kChunk = 64;        // rows per Gram--Schmidt block
+constexpr int kRowsPerThread = kChunk / 4;
+constexpr int kMaxRestart = 128;  // per-sample scalar kernels keep a column in registers/scratch
+
+template <typename T>
+struct Adj {
+  Mat<T> K;  // scaled kept rows
+  int64_t Bp;
+  int n, m;
+  T a, delta, sigma;
+  const T* Cm;   // n x Bp
+  const T* Dm;   // m x Bp
+  T* U;          // n x Bp scratch (u)
+  T* Wv;         // m x Bp scratch (w)
+};
+
+// d/dx of max(x, y) and min(x, y) with JAX's balanced tie rule.
+template <typename T>
+__device__ __forceinline__ T dmax_dx(T x, T y) {
+  const T ans = maxp(x, y);
+  return x == ans ? (y == ans ? T(0.5) : T(1)) : T(0);
+}
+template <typename T>
+__device__ __forceinline__ T dmin_dx(T x, T y) {
+  const T ans = minp(x, y);
+  return x == ans ? (y == ans ? T(0.5) : T(1)) : T(0);
+}
+
+// ---------------------------------------------------------------------------
+// linearisation at z = (y, d, y): D mask and d+ (rows), then C/Clo/Chi (cols)
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_lin_rows(Adj<T> S, const T* __restrict__ Y,
+                                                     const T* __restrict__ Dd,
+                                                     const T* __restrict__ R, T* Dm, T* dplus) {
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  for (int rb = blockIdx.y; rb * 4 < S.m; rb += gridDim.y) {
+    const int i = rb * 4 + wave;
+    if (i >= S.m) continue;
+    V acc = vsplat<T>(T(0));
+    for (int k = S.K.rptr[i]; k < S.K.rptr[i + 1]; ++k)
+      acc += S.K.rval[k] * vload(Y + (size_t)S.K.ridx[k] * S.Bp + b0);
+    const size_t off = (size_t)i * S.Bp + b0;
+    const V p = vload(Dd + off) + S.sigma * (acc - vload(R + off));
+    V dm, dp;
+#pragma unroll
+    for (int s = 0; s < Sn; ++s) {
+      if (i < S.K.me) {
+        dm[s] = T(1);
+        dp[s] = p[s];
+      } else {
+        dm[s] = dmax_dx(p[s], T(0));
+        dp[s] = maxp(p[s], T(0));
+      }
+    }
+    vstore(Dm + off, dm);
+    vstore(dplus + off, dp);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_lin_cols(Adj<T> S, const T* __restrict__ Y,
+                                                     const T* __restrict__ tgt,
+                                                     const T* __restrict__ LO,
+                                                     const T* __restrict__ HI, int shared_bounds,
+                                                     const T* __restrict__ dplus, T* Cm, T* Clo,
+                                                     T* Chi) {
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  for (int cb = blockIdx.y; cb * 4 < S.n; cb += gridDim.y) {
+    const int j = cb * 4 + wave;
+    if (j >= S.n) continue;
+    V t = vsplat<T>(T(0));
+    for (int k = S.K.cptr[j]; k < S.K.cptr[j + 1]; ++k)
+      t += S.K.cval[k] * vload(dplus + (size_t)S.K.cidx[k] * S.Bp + b0);
+    const size_t off = (size_t)j * S.Bp + b0;
+    const V y = vload(Y + off);
+    const V s = S.a * y - S.delta * t + S.delta * vload(tgt + off);
+    V lo, hi;
+    if (shared_bounds) {
+      lo = vsplat<T>(LO[j]);
+      hi = vsplat<T>(HI[j]);
+    } else {
+      lo = vload(LO + off);
+      hi = vload(HI + off);
+    }
+    V c, cl, ch;
+#pragma unroll
+    for (int q = 0; q < Sn; ++q) {
+      // clip = minimum(maximum(s, lo), hi)
+      const T m1 = maxp(s[q], lo[q]);
+      const T dm1 = dmin_dx(m1, hi[q]);
+      c[q] = dm1 * dmax_dx(s[q], lo[q]);
+      cl[q] = dm1 * dmax_dx(lo[q], s[q]);
+      ch[q] = dmin_dx(hi[q], m1);
+    }
+    vstore(Cm + off, c);
+    vstore(Clo + off, cl);
+    vstore(Chi + off, ch);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// operator out = v - pullback(v) in three passes; v and out are W x Bp
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_op_cols1(Adj<T> S, const T* __restrict__ v,
+                                                     T* __restrict__ out) {
+  const int64_t total = (int64_t)S.n * S.Bp;
+  const int64_t boff = (int64_t)(S.n + S.m) * S.Bp;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const T gy = v[e], gb = v[boff + e];
+    const T u = S.Cm[e] * (gy + T(2) * gb);
+    S.U[e] = u;
+    out[e] = gy - (S.a * u - gb);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_op_rows(Adj<T> S, const T* __restrict__ v,
+                                                    T* __restrict__ out) {
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  for (int rb = blockIdx.y; rb * 4 < S.m; rb += gridDim.y) {
+    const int i = rb * 4 + wave;
+    if (i >= S.m) continue;
+    V acc = vsplat<T>(T(0));
+    for (int k = S.K.rptr[i]; k < S.K.rptr[i + 1]; ++k)
+      acc += S.K.rval[k] * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
+    const size_t off = (size_t)i * S.Bp + b0;
+    const size_t voff = (size_t)(S.n + i) * S.Bp + b0;
+    const V gd = vload(v + voff);
+    const V w = vload(S.Dm + off) * (gd - S.delta * acc);
+    vstore(S.Wv + off, w);
+    vstore(out + voff, gd - w);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_op_cols2(Adj<T> S, const T* __restrict__ v,
+                                                     T* __restrict__ out) {
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  for (int cb = blockIdx.y; cb * 4 < S.n; cb += gridDim.y) {
+    const int j = cb * 4 + wave;
+    if (j >= S.n) continue;
+    V acc = vsplat<T>(T(0));
+    for (int k = S.K.cptr[j]; k < S.K.cptr[j + 1]; ++k)
+      acc += S.K.cval[k] * vload(S.Wv + (size_t)S.K.cidx[k] * S.Bp + b0);
+    const size_t off = (size_t)(S.n + S.m + j) * S.Bp + b0;
+    vstore(out + off, vload(v + off) - S.sigma * acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// batched reductions over the W rows of a state vector
+// ---------------------------------------------------------------------------
+// MODE 0: part[i][c][b] = sum_rows V_i x                       (dots)
+// MODE 1: x <- x - sum_i h_i V_i;  part[i][c][b] = sum V_i x   (update + dots)
+// MODE 2: x <- x - sum_i h_i V_i;  part[0] = sum x^2, part[1] = finite(x)
+// MODE 3: part[0] = sum x^2                                    (norm)
+// MODE 4: part[0] = max |x|                                    (inf-norm)
+template <typename T, int MODE>
+__global__ __launch_bounds__(kBlock) void k_gs(const T* __restrict__ basis, int64_t vstride,
+                                               int nv, T* x, const T* __restrict__ h,
+                                               int64_t W, int64_t Bp, T* part, int nchunk) {
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  const int c = blockIdx.y;
+  const int64_t r0 = (int64_t)c * kChunk + wave * kRowsPerThread;
+  __shared__ T buf[kBlock * Sn];
+  V xr[kRowsPerThread];
+#pragma unroll
+  for (int r = 0; r < kRowsPerThread; ++r)
+    xr[r] = (r0 + r < W) ? vload(x + (size_t)(r0 + r) * Bp + b0) : vsplat<T>(T(0));
+  if (MODE == 1 || MODE == 2) {
+    for (int i = 0; i < nv; ++i) {
+      const V hi = vload(h + (size_t)i * Bp + b0);
+      const T* vi = basis + (size_t)i * vstride;
+#pragma unroll
+      for (int r = 0; r < kRowsPerThread; ++r)
+        if (r0 + r < W) xr[r] = xr[r] - hi * vload(vi + (size_t)(r0 + r) * Bp + b0);
+    }
+#pragma unroll
+    for (int r = 0; r < kRowsPerThread; ++r)
+      if (r0 + r < W) vstore(x + (size_t)(r0 + r) * Bp + b0, xr[r]);
+  }
+  const size_t plane = (size_t)nchunk * Bp;
+  if (MODE == 0 || MODE == 1) {
+    for (int i = 0; i < nv; ++i) {
+      const T* vi = basis + (size_t)i * vstride;
+      V acc = vsplat<T>(T(0));
+#pragma unroll
+      for (int r = 0; r < kRowsPerThread; ++r)
+        if (r0 + r < W) acc += vload(vi + (size_t)(r0 + r) * Bp + b0) * xr[r];
+      const V tot = block_combine<T>(acc, buf, OpAdd());
+      if (wave == 0) vstore(part + (size_t)i * plane + (size_t)c * Bp + b0, tot);
+    }
+  } else if (MODE == 2 || MODE == 3) {
+    V acc = vsplat<T>(T(0)), fin = vsplat<T>(T(1));
+#pragma unroll
+    for (int r = 0; r < kRowsPerThread; ++r) {
+      acc += xr[r] * xr[r];
+#pragma unroll
+      for (int s = 0; s < Sn; ++s)
+        if (!finite(xr[r][s])) fin[s] = T(0);
+    }
+    const V tot = block_combine<T>(acc, buf, OpAdd());
+    const V f = block_combine<T>(fin, buf, OpMin());
+    if (wave == 0) {
+      vstore(part + (size_t)c * Bp + b0, tot);
+      if (MODE == 2) vstore(part + plane + (size_t)c * Bp + b0, f);
+    }
+  } else {
+    V acc = vsplat<T>(T(0));
+#pragma unroll
+    for (int r = 0; r < kRowsPerThread; ++r)
+#pragma unroll
+      for (int s = 0; s < Sn; ++s) acc[s] = maxp(acc[s], absv(xr[r][s]));
+    const V tot = block_combine<T>(acc, buf, OpMax());
+    if (wave == 0) vstore(part + (size_t)c * Bp + b0, tot);
+  }
+}
+
+// out[i][b] = reduce_c part[i][c][b] in chunk order; op 0 = sum, 1 = max, 2 = min
+template <typename T>
+__global__ void k_reduce(const T* __restrict__ part, int nv, int nchunk, int64_t Bp, T* out,
+                         int op) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)nv * Bp) return;
+  const int64_t i = e / Bp, b = e - i * Bp;
+  const T* p = part + (size_t)i * nchunk * Bp + b;
+  T acc = p[0];
+  for (int c = 1; c < nchunk; ++c) {
+    const T v = p[(size_t)c * Bp];
+    acc = op == 0 ? acc + v : (op == 1 ? maxp(acc, v) : minp(acc, v));
+  }
+  out[e] = acc;
+}
+
+// elementwise helpers on W x Bp vectors
+template <typename T>
+__global__ void k_axpby(int64_t total, T* out, const T* __restrict__ a, const T* __restrict__ b,
+                        T beta) {  // out = a + beta * b
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x)
+    out[e] = a[e] + beta * b[e];
+}
+
+// V0 = r / max(beta, eps) per sample
+template <typename T>
+__global__ void k_scale_cols(int64_t total, int64_t Bp, T* out, const T* __restrict__ in,
+                             const T* __restrict__ scale, const int32_t* __restrict__ keep) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = e % Bp;
+    out[e] = (keep == nullptr || keep[b]) ? in[e] * scale[b] : T(0);
+  }
+}
+
+// x += sum_{i < row_steps[b]} coeff_i V_i
+template <typename T>
+__global__ void k_correction(int64_t total, int64_t Bp, T* x, const T* __restrict__ basis,
+                             int64_t vstride, const T* __restrict__ coeff,
+                             const int32_t* __restrict__ steps) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = e % Bp;
+    const int k = steps[b];
+    if (k == 0) continue;
+    T acc = T(0);
+    for (int i = 0; i < k; ++i) acc += coeff[(size_t)i * Bp + b] * basis[(size_t)i * vstride + e];
+    x[e] = x[e] + acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// per-sample GMRES scalars (operators.py:820-821, 873-917, 996-1091)
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Gm {
+  int64_t batch, Bp;
+  int restart;
+  T* thr;        // threshold
+  T* rinf;       // residual_inf
+  int32_t* cyc;  // cycle_active
+  int32_t* act;  // active
+  int32_t* steps;
+  int32_t* keep;
+  T* scale;
+  T* H;          // [b][(restart+1) * restart]
+  T* cs;         // [restart][Bp]
+  T* sn;
+  T* g;          // [(restart+1)][Bp]
+  T* coeff;      // [restart][Bp] (back-substitution output)
+  int32_t* counter;  // [0] active count, [1] unconverged count
+};
+
+template <typename T>
+__global__ void k_gm_thresholds(Gm<T> G, const T* __restrict__ rhs_inf, T tol, T atol) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= G.Bp) return;
+  G.thr[b] = maxp(atol, tol * rhs_inf[b]);
+  G.rinf[b] = rhs_inf[b];  // x0 = 0: rhs - matvec(0) = rhs
+}
+
+template <typename T>
+__global__ void k_gm_count_unconverged(Gm<T> G) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < G.batch && G.rinf[b] > G.thr[b]) atomicAdd(&G.counter[1], 1);
+}
+
+template <typename T>
+__global__ void k_gm_cycle_init(Gm<T> G, const T* __restrict__ beta2) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= G.Bp) return;
+  const int R = G.restart;
+  const T eps = T(1e-30);
+  const T beta = __builtin_sqrt(beta2[b]);
+  G.scale[b] = T(1) / maxp(beta, eps);
+  const int c = (b < G.batch && G.rinf[b] > G.thr[b]) ? 1 : 0;
+  G.cyc[b] = c;
+  G.act[b] = c;
+  G.steps[b] = 0;
+  for (int i = 0; i < R; ++i) {
+    G.cs[(size_t)i * G.Bp + b] = T(0);
+    G.sn[(size_t)i * G.Bp + b] = T(0);
+  }
+  for (int i = 0; i <= R; ++i) G.g[(size_t)i * G.Bp + b] = i == 0 ? beta : T(0);
+  T* Hb = G.H + (size_t)b * (R + 1) * R;
+  for (int i = 0; i < (R + 1) * R; ++i) Hb[i] = T(0);
+  if (c) atomicAdd(&G.counter[0], 1);
+}
+
+// One Arnoldi step's scalar work for iteration ``it`` (operators.py:996-1081).
+template <typename T>
+__global__ void k_gm_givens(Gm<T> G, int it, const T* __restrict__ h1, const T* __restrict__ h2,
+                            const T* __restrict__ nrm2, const T* __restrict__ fin) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= G.Bp) return;
+  const int R = G.restart;
+  const T eps = T(1e-30), brk = T(1e-14);
+  const int active = G.act[b];
+  G.keep[b] = active;
+  T col[kMaxRestart + 1];
+  for (int i = 0; i < R; ++i)
+    col[i] = i <= it ? h1[(size_t)i * G.Bp + b] + h2[(size_t)i * G.Bp + b] : T(0);
+  col[R] = T(0);
+  const T next_norm = __builtin_sqrt(nrm2[b]);
+  col[it + 1] = next_norm;
+  for (int ri = 0; ri < it; ++ri) {
+    const T c = G.cs[(size_t)ri * G.Bp + b], s = G.sn[(size_t)ri * G.Bp + b];
+    const T f = col[ri], sc = col[ri + 1];
+    col[ri] = c * f + s * sc;
+    col[ri + 1] = -s * f + c * sc;
+  }
+  const T diag = col[it], sub = col[it + 1];
+  const T rnorm = hypotv(diag, sub);
+  const T safe = maxp(rnorm, eps);
+  const T nc = rnorm > eps ? diag / safe : T(1);
+  const T ns = rnorm > eps ? sub / safe : T(0);
+  const T pc = G.g[(size_t)it * G.Bp + b], pn = G.g[(size_t)(it + 1) * G.Bp + b];
+  const T rc = nc * pc + ns * pn;
+  const T rn = -ns * pc + nc * pn;
+  if (active) {
+    G.cs[(size_t)it * G.Bp + b] = nc;
+    G.sn[(size_t)it * G.Bp + b] = ns;
+    col[it] = rnorm;
+    col[it + 1] = T(0);
+    T* Hb = G.H + (size_t)b * (R + 1) * R;
+    for (int i = 0; i <= R; ++i) Hb[(size_t)i * R + it] = col[i];
+    G.g[(size_t)it * G.Bp + b] = rc;
+    G.g[(size_t)(it + 1) * G.Bp + b] = rn;
+    G.steps[b] = it + 1;
+  }
+  const T est = absv(rn);
+  const bool finite_ok = finite(est) && finite(rnorm) && fin[b] != T(0);
+  const bool happy = next_norm <= brk;
+  const int still = (active && finite_ok && !happy && est > G.thr[b]) ? 1 : 0;
+  G.act[b] = still;
+  G.scale[b] = T(1) / maxp(next_norm, eps);
+  if (still && b < G.batch) atomicAdd(&G.counter[0], 1);
+}
+
+// Back substitution (operators.py:902-917).
+template <typename T>
+__global__ void k_gm_backsub(Gm<T> G) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= G.Bp) return;
+  const int R = G.restart;
+  const T eps = T(1e-30);
+  const T* Hb = G.H + (size_t)b * (R + 1) * R;
+  T val[kMaxRestart];
+  for (int i = 0; i < R; ++i) val[i] = T(0);
+  const int steps = G.steps[b];
+  for (int row = R - 1; row >= 0; --row) {
+    T trailing = T(0);
+    for (int cidx = 0; cidx < R; ++cidx) trailing += Hb[(size_t)row * R + cidx] * val[cidx];
+    const T num = G.g[(size_t)row * G.Bp + b] - trailing;
+    const T d = Hb[(size_t)row * R + row];
+    const T safe = absv(d) > eps ? d : T(1);
+    val[row] = row < steps ? num / safe : T(0);
+  }
+  for (int i = 0; i < R; ++i) G.coeff[(size_t)i * G.Bp + b] = val[i];
+}
+
+template <typename T>
+__global__ void k_gm_cycle_end(Gm<T> G, const T* __restrict__ cand_inf) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= G.Bp) return;
+  if (G.cyc[b]) G.rinf[b] = cand_inf[b];
+}
+
+// info / valid (operators.py:1119-1122, bounds.py:148-153) and the masked
+// cotangent weight for the final pullback.
+template <typename T>
+__global__ void k_gm_finish(Gm<T> G, const T* __restrict__ xfin, const int32_t* __restrict__ conv,
+                            T adjoint_tol, int force, T* lam_w, uint8_t* valid, int32_t* info,
+                            T* residual) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= G.Bp) return;
+  const bool fin = xfin[b] != T(0) && finite(G.rinf[b]);
+  const int code = !fin ? 2 : (G.rinf[b] <= G.thr[b] ? 0 : 1);
+  const bool eligible = b < G.batch && (force || conv[b] != 0);
+  const bool ok = eligible && fin && (code == 0 || G.rinf[b] <= adjoint_tol);
+  lam_w[b] = ok ? T(1) : T(0);
+  if (b < G.batch) {
+    if (valid) valid[b] = ok ? 1 : 0;
+    if (info) info[b] = code;
+    if (residual) residual[b] = G.rinf[b];
+  }
+}
+
+// rhs g = [cot_y * eligible, 0, 0]; cot arrives batch-minor in ``cot``
+template <typename T>
+__global__ void k_gm_rhs(int64_t n, int64_t W, int64_t Bp, int64_t batch, const T* __restrict__ cot,
+                         const int32_t* __restrict__ conv, int force, T* g) {
+  const int64_t total = W * Bp;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = e / Bp, b = e - row * Bp;
+    const bool elig = b < batch && (force || conv[b] != 0);
+    g[e] = (row < n && elig) ? cot[e] : T(0);
+  }
+}
+
+// Final pullback of lambda (masked by lam_w): outputs in internal layout, with
+// non-finite values replaced by zero (bounds.py:154-165).
+template <typename T>
+__global__ void k_final_u(Adj<T> S, const T* __restrict__ lam, const T* __restrict__ lam_w,
+                          const T* __restrict__ Clo, const T* __restrict__ Chi, T* gt, T* glo,
+                          T* ghi) {
+  const int64_t total = (int64_t)S.n * S.Bp;
+  const int64_t boff = (int64_t)(S.n + S.m) * S.Bp;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = e % S.Bp;
+    const T w = lam_w[b];
+    const T gy = w != T(0) ? lam[e] : T(0), gb = w != T(0) ? lam[boff + e] : T(0);
+    const T G = gy + T(2) * gb;
+    const T u = S.Cm[e] * G;
+    S.U[e] = u;
+    const T a = S.delta * u, l = Clo[e] * G, h = Chi[e] * G;
+    gt[e] = finite(a) ? a : T(0);
+    glo[e] = finite(l) ? l : T(0);
+    ghi[e] = finite(h) ? h : T(0);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_final_w(Adj<T> S, const T* __restrict__ lam,
+                                                    const T* __restrict__ lam_w, T* gr) {
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  for (int rb = blockIdx.y; rb * 4 < S.m; rb += gridDim.y) {
+    const int i = rb * 4 + wave;
+    if (i >= S.m) continue;
+    V acc = vsplat<T>(T(0));
+    for (int k = S.K.rptr[i]; k < S.K.rptr[i + 1]; ++k)
+      acc += S.K.rval[k] * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
+    const size_t off = (size_t)i * S.Bp + b0;
+    const V gd = vload(lam + (size_t)(S.n + i) * S.Bp + b0);
+    V out;
+#pragma unroll
+    for (int s = 0; s < Sn; ++s) {
+      const T lw = lam_w[b0 + s];
+      const T w = S.Dm[off + s] * ((lw != T(0) ? gd[s] : T(0)) - S.delta * acc[s]);
+      const T r = -S.sigma * w;
+      out[s] = finite(r) ? r : T(0);
+    }
+    vstore(gr + off, out);
+  }
+}
+
+// g_rhs in the full row space for project(): kept rows g_r * scale, bound
+// rows through their threshold (ties at a bound split evenly).
+template <typename T>
+__global__ void k_grhs_full(int m, int n, int64_t Bp, const int32_t* __restrict__ kept,
+                            const T* __restrict__ scale, const T* __restrict__ gr,
+                            const int32_t* __restrict__ bptr, const int32_t* __restrict__ brow,
+                            const T* __restrict__ bcoef, const T* __restrict__ RF,
+                            const T* __restrict__ LO, const T* __restrict__ HI, int shared_bounds,
+                            const T* __restrict__ glo, const T* __restrict__ ghi, T* out) {
+  const int64_t total_rows = (int64_t)m * Bp;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total_rows;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / Bp, b = e - i * Bp;
+    out[(int64_t)kept[i] * Bp + b] = gr[e] * scale[i];
+  }
+  const int64_t total_cols = (int64_t)n * Bp;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total_cols;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t j = e / Bp, b = e - j * Bp;
+    const T lo = shared_bounds ? LO[j] : LO[e];
+    const T hi = shared_bounds ? HI[j] : HI[e];
+    const int k0 = bptr[j], k1 = bptr[j + 1];
+    T nlo = T(0), nhi = T(0);
+    for (int k = k0; k < k1; ++k) {
+      const T c = bcoef[k];
+      const T th = RF[(int64_t)brow[k] * Bp + b] / (c != T(0) ? c : T(1));
+      if (c < T(0) && th == lo) nlo += T(1);
+      if (c > T(0) && th == hi) nhi += T(1);
+    }
+    for (int k = k0; k < k1; ++k) {
+      const T c = bcoef[k];
+      const T th = RF[(int64_t)brow[k] * Bp + b] / (c != T(0) ? c : T(1));
+      T gthr = T(0);
+      if (c < T(0) && th == lo) gthr += glo[e] / maxp(nlo, T(1));
+      if (c > T(0) && th == hi) gthr += ghi[e] / maxp(nhi, T(1));
+      const T v = c != T(0) ? gthr / c : gthr;
+      out[(int64_t)brow[k] * Bp + b] = finite(v) ? v : T(0);
+    }
+  }
+}
+
+template <typename T>
+__global__ void k_copy_i32(int64_t count, const int32_t* __restrict__ src, int32_t* dst) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < count) dst[e] = src[e];
+}
+
+static size_t al(size_t x) { return (x + 255) & ~size_t(255); }
+
+template <typename T>
+static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const void* saved,
+                        const T* cot_y, const purin_cp_adjoint_options& o, T* g_target, T* g_rhs,
+                        T* g_lower, T* g_upper, uint8_t* valid, int32_t* info, T* gres) {
+  if (!saved || !cot_y) return set_error(PURIN_CP_ERR_ARG, "NULL saved state or cotangent");
+  if (batch < 1) return set_error(PURIN_CP_ERR_ARG, "batch must be positive");
+  if (o.restart < 1 || o.max_iterations < 1)
+    return set_error(PURIN_CP_ERR_ARG, "linear iteration limits must be positive");
+  if (o.tolerance <= 0.0 || o.atol < 0.0) return set_error(PURIN_CP_ERR_ARG, "linear tolerances are invalid");
+  const Layout L = make_layout(p, batch);
+  const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
+  const int64_t W = 2 * n + m;
+  const int restart = (int)std::min<int64_t>({(int64_t)o.restart, (int64_t)o.max_iterations, W});
+  if (restart > kMaxRestart) return set_error(PURIN_CP_ERR_UNSUPPORTED, "restart above 128");
+  // header written by the forward call
+  int64_t hdr[9];
+  PURIN_HIP(hipMemcpyAsync(hdr, saved, sizeof(hdr), hipMemcpyDeviceToHost, st));
+  PURIN_HIP(hipStreamSynchronize(st));
+  if (hdr[0] != kSavedMagic || hdr[1] != batch || hdr[2] != Bp || hdr[5] != p->dtype ||
+      hdr[6] != n || hdr[7] != m)
+    return set_error(PURIN_CP_ERR_ARG, "saved state does not belong to this plan and batch");
+  const int kind = (int)hdr[3];
+  const int shared = (int)hdr[4];
+  const char* sv = (const char*)saved;
+  const T* Tt = (const T*)(sv + L.Tt);
+  const T* Y = (const T*)(sv + L.Y);
+  const T* Dd = (const T*)(sv + L.D);
+  const T* R = (const T*)(sv + L.R);
+  const T* LO = (const T*)(sv + L.LO);
+  const T* HI = (const T*)(sv + L.HI);
+  const T* RF = (const T*)(sv + L.RF);
+  const int32_t* conv = (const int32_t*)(sv + L.conv);
+  const T* metric = kind == 1 ? (const T*)p->metric : nullptr;
+
+  // workspace
+  const int nchunk = (int)((W + kChunk - 1) / kChunk);
+  const size_t es = sizeof(T);
+  const size_t vec = (size_t)W * Bp * es;
+  size_t o_ = 0;
+  auto take = [&](size_t bytes) { size_t r = o_; o_ = al(o_ + bytes); return r; };
+  const size_t oV = take(vec * (restart + 1)), oX = take(vec), oG = take(vec), oRr = take(vec),
+               oT1 = take(vec), oCm = take(n * Bp * es), oClo = take(n * Bp * es),
+               oChi = take(n * Bp * es), oDm = take(m * Bp * es), oDp = take(m * Bp * es),
+               oU = take(n * Bp * es), oWv = take(m * Bp * es),
+               oPart = take((size_t)(restart + 1) * nchunk * Bp * es),
+               oH1 = take((size_t)(restart + 1) * Bp * es), oH2 = take((size_t)(restart + 1) * Bp * es),
+               oS1 = take(Bp * es), oS2 = take(Bp * es), oThr = take(Bp * es), oRinf = take(Bp * es),
+               oCyc = take(Bp * 4), oAct = take(Bp * 4), oSteps = take(Bp * 4), oKeep = take(Bp * 4),
+               oScale = take(Bp * es), oHess = take((size_t)Bp * (restart + 1) * restart * es),
+               oCs = take((size_t)restart * Bp * es), oSn = take((size_t)restart * Bp * es),
+               oGv = take((size_t)(restart + 1) * Bp * es), oCoef = take((size_t)restart * Bp * es),
+               oCnt = take(256), oLw = take(Bp * es), oGt = take(n * Bp * es),
+               oGlo = take(n * Bp * es), oGhi = take(n * Bp * es), oGr = take(m * Bp * es),
+               oGF = take((size_t)M * Bp * es);
+  int err = PURIN_CP_OK;
+  char* ws = (char*)workspace(p, o_, st, &err, true);
+  if (!ws) return err;
+  T* Vb = (T*)(ws + oV);
+  const int64_t vstride = W * Bp;
+  T* X = (T*)(ws + oX);
+  T* Gr = (T*)(ws + oG);
+  T* Rr = (T*)(ws + oRr);
+  T* T1 = (T*)(ws + oT1);
+  T* part = (T*)(ws + oPart);
+  T* H1 = (T*)(ws + oH1);
+  T* H2 = (T*)(ws + oH2);
+  T* S1 = (T*)(ws + oS1);
+  T* S2 = (T*)(ws + oS2);
+  Gm<T> G{batch, Bp, restart, (T*)(ws + oThr), (T*)(ws + oRinf), (int32_t*)(ws + oCyc),
+          (int32_t*)(ws + oAct), (int32_t*)(ws + oSteps), (int32_t*)(ws + oKeep),
+          (T*)(ws + oScale), (T*)(ws + oHess), (T*)(ws + oCs), (T*)(ws + oSn), (T*)(ws + oGv),
+          (T*)(ws + oCoef), (int32_t*)(ws + oCnt)};
+
+  Adj<T> S{};
+  S.K = kept_matrix<T>(p, true);
+  S.Bp = Bp;
+  S.n = (int)n;
+  S.m = (int)m;
+  const T tau = (T)p->tau_adj;
+  S.sigma = (T)p->sigma_adj;
+  S.a = T(1) / (T(1) + tau);
+  S.delta = tau * S.a;
+  S.Cm = (const T*)(ws + oCm);
+  S.Dm = (const T*)(ws + oDm);
+  S.U = (T*)(ws + oU);
+  S.Wv = (T*)(ws + oWv);
+
+  constexpr int64_t TS = tile_samples<T>();
+  const dim3 grow = tile_grid(Bp, TS, (m + 3) / 4), gcol = tile_grid(Bp, TS, (n + 3) / 4);
+  const dim3 ggs((unsigned)(Bp / TS), (unsigned)nchunk);
+  const unsigned eb = 2048, sb = (unsigned)((Bp + 255) / 256);
+  const int64_t total = W * Bp;
+
+  // linearisation (bounds.py:109-129)
+  if (m) k_lin_rows<T><<<grow, kBlock, 0, st>>>(S, Y, Dd, R, (T*)(ws + oDm), (T*)(ws + oDp));
+  k_lin_cols<T><<<gcol, kBlock, 0, st>>>(S, Y, Tt, LO, HI, shared, (const T*)(ws + oDp),
+                                          (T*)(ws + oCm), (T*)(ws + oClo), (T*)(ws + oChi));
+  auto op = [&](const T* v, T* out) {
+    k_op_cols1<T><<<eb, 256, 0, st>>>(S, v, out);
+    if (m) k_op_rows<T><<<grow, kBlock, 0, st>>>(S, v, out);
+    k_op_cols2<T><<<gcol, kBlock, 0, st>>>(S, v, out);
+  };
+  auto reduce = [&](int mode_nv, T* out, int opk) {
+    k_reduce<T><<<(unsigned)((mode_nv * Bp + 255) / 256), 256, 0, st>>>(part, mode_nv, nchunk, Bp,
+                                                                         out, opk);
+  };
+  auto read_counter = [&](int idx, int32_t* val) -> int {
+    PURIN_HIP(hipMemcpyAsync(p->pinned, G.counter, 2 * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    PURIN_HIP(hipStreamSynchronize(st));
+    *val = p->pinned[idx];
+    return PURIN_CP_OK;
+  };
+  auto zero_counters = [&]() { k_fill<int32_t><<<1, 64, 0, st>>>(G.counter, 2, 0); };
+
+  // rhs g = [cot * eligible, 0, 0] (cotangent divided by sqrt(D) for a metric)
+  to_minor<T>(st, cot_y, batch, n, n, T1, Bp, metric, metric ? 2 : 0);
+  k_gm_rhs<T><<<eb, 256, 0, st>>>(n, W, Bp, batch, T1, conv, o.force_eligible, Gr);
+  // threshold = max(atol, tol * max|g|) and residual_inf = max|g - A 0| = max|g|
+  k_gs<T, 4><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Gr, nullptr, W, Bp, part, nchunk);
+  reduce(1, S1, 1);
+  k_gm_thresholds<T><<<sb, 256, 0, st>>>(G, S1, (T)o.tolerance, (T)o.atol);
+  k_fill<T><<<eb, 256, 0, st>>>(X, total, T(0));
+  PURIN_HIP(hipMemcpyAsync(Rr, Gr, vec, hipMemcpyDeviceToDevice, st));  // r = g - A(0)
+
+  int64_t completed = 0;
+  while (completed < o.max_iterations) {
+    zero_counters();
+    k_gm_count_unconverged<T><<<sb, 256, 0, st>>>(G);
+    int32_t unconverged = 0;
+    if (int rc = read_counter(1, &unconverged)) return rc;
+    if (unconverged == 0) break;
+    const int cycle_limit = (int)std::min<int64_t>(restart, o.max_iterations - completed);
+    // beta = ||r||, V0 = r / max(beta, eps)
+    k_gs<T, 3><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Rr, nullptr, W, Bp, part, nchunk);
+    reduce(1, S1, 0);
+    zero_counters();
+    k_gm_cycle_init<T><<<sb, 256, 0, st>>>(G, S1);
+    k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, Vb, Rr, G.scale, nullptr);
+    int32_t nactive = 0;
+    if (int rc = read_counter(0, &nactive)) return rc;
+    int it = 0;
+    while (it < cycle_limit && nactive > 0) {
+      T* vk = Vb + (size_t)it * vstride;
+      T* img = Vb + (size_t)(it + 1) * vstride;
+      op(vk, img);
+      // two-pass classical Gram--Schmidt over the active prefix (operators.py:834-871)
+      k_gs<T, 0><<<ggs, kBlock, 0, st>>>(Vb, vstride, it + 1, img, nullptr, W, Bp, part, nchunk);
+      reduce(it + 1, H1, 0);
+      k_gs<T, 1><<<ggs, kBlock, 0, st>>>(Vb, vstride, it + 1, img, H1, W, Bp, part, nchunk);
+      reduce(it + 1, H2, 0);
+      k_gs<T, 2><<<ggs, kBlock, 0, st>>>(Vb, vstride, it + 1, img, H2, W, Bp, part, nchunk);
+      k_reduce<T><<<sb, 256, 0, st>>>(part, 1, nchunk, Bp, S1, 0);
+      k_reduce<T><<<sb, 256, 0, st>>>(part + (size_t)nchunk * Bp, 1, nchunk, Bp, S2, 2);
+      zero_counters();
+      k_gm_givens<T><<<sb, 256, 0, st>>>(G, it, H1, H2, S1, S2);
+      k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, img, img, G.scale, G.keep);
+      ++it;
+      if (int rc = read_counter(0, &nactive)) return rc;
+    }
+    k_gm_backsub<T><<<sb, 256, 0, st>>>(G);
+    k_correction<T><<<eb, 256, 0, st>>>(total, Bp, X, Vb, vstride, G.coeff, G.steps);
+    // candidate residual r = g - A x (operators.py:1084-1091)
+    op(X, T1);
+    k_axpby<T><<<eb, 256, 0, st>>>(total, Rr, Gr, T1, T(-1));
+    k_gs<T, 4><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Rr, nullptr, W, Bp, part, nchunk);
+    reduce(1, S1, 1);
+    k_gm_cycle_end<T><<<sb, 256, 0, st>>>(G, S1);
+    completed += it;
+  }
+  // finiteness of the solution, info, valid (operators.py:1119-1122, bounds.py:148-153)
+  k_gs<T, 2><<<ggs, kBlock, 0, st>>>(Vb, vstride, 0, X, nullptr, W, Bp, part, nchunk);
+  k_reduce<T><<<sb, 256, 0, st>>>(part + (size_t)nchunk * Bp, 1, nchunk, Bp, S2, 2);
+  T* lam_w = (T*)(ws + oLw);
+  k_gm_finish<T><<<sb, 256, 0, st>>>(G, S2, conv, (T)o.adjoint_tolerance, o.force_eligible,
+                                     lam_w, valid, info, gres);
+  // final pullback of the masked lambda
+  T* gt = (T*)(ws + oGt);
+  T* glo = (T*)(ws + oGlo);
+  T* ghi = (T*)(ws + oGhi);
+  T* gr = (T*)(ws + oGr);
+  k_final_u<T><<<eb, 256, 0, st>>>(S, X, lam_w, (const T*)(ws + oClo), (const T*)(ws + oChi), gt,
+                                   glo, ghi);
+  if (m) k_final_w<T><<<grow, kBlock, 0, st>>>(S, X, lam_w, gr);
+  if (g_target) to_major<T>(st, gt, Bp, n, g_target, batch, n, metric, metric ? 1 : 0);
+  if (kind == 1) {
+    if (g_rhs && M) {
+      T* GF = (T*)(ws + oGF);
+      k_grhs_full<T><<<eb, 256, 0, st>>>((int)m, (int)n, Bp, p->dkept, (const T*)p->dscale, gr,
+                                         p->bptr, p->brow, (const T*)p->dbcoef, RF, LO, HI, shared,
+                                         glo, ghi, GF);
+      to_major<T>(st, GF, Bp, M, g_rhs, batch, M, nullptr, 0);
+    }
+  } else {
+    if (g_rhs && m) to_major<T>(st, gr, Bp, m, g_rhs, batch, m, nullptr, 0);
+  }
+  if (g_lower) to_major<T>(st, glo, Bp, n, g_lower, batch, n, nullptr, 0);
+  if (g_upper) to_major<T>(st, ghi, Bp, n, g_upper, batch, n, nullptr, 0);
+  PURIN_HIP(hipGetLastError());
+  return PURIN_CP_OK;
+}
+
+}  // namespace purin
 
 using namespace purin;
 
@@ -9,5 +802,18 @@ extern "C" int purin_cp_adjoint(purin_cp_plan* p, void* stream, int64_t batch, c
                                 const purin_cp_adjoint_options* opts, void* g_target, void* g_rhs,
                                 void* g_lower, void* g_upper, uint8_t* valid, int32_t* info,
                                 void* gmres_residual) {
-  return set_error(PURIN_CP_ERR_UNSUPPORTED, "adjoint not built yet");
+  (void)target;  // the saved state holds the forward's inputs
+  (void)rhs;
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  purin_cp_adjoint_options o;
+  purin_cp_default_adjoint_options(&o);
+  if (opts) o = *opts;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64)
+    return adjoint_impl<double>(p, st, batch, saved, (const double*)cot_y, o, (double*)g_target,
+                                (double*)g_rhs, (double*)g_lower, (double*)g_upper, valid, info,
+                                (double*)gmres_residual);
+  return adjoint_impl<float>(p, st, batch, saved, (const float*)cot_y, o, (float*)g_target,
+                             (float*)g_rhs, (float*)g_lower, (float*)g_upper, valid, info,
+                             (float*)gmres_residual);
 }

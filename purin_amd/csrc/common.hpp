@@ -69,6 +69,8 @@ template <typename T>
 __device__ __forceinline__ T clipp(T x, T lo, T hi) {
   return minp(maxp(x, lo), hi);
 }
+__device__ __forceinline__ double hypotv(double x, double y) { return ::hypot(x, y); }
+__device__ __forceinline__ float hypotv(float x, float y) { return ::hypotf(x, y); }
 __device__ __forceinline__ double absv(double x) { return __builtin_fabs(x); }
 __device__ __forceinline__ float absv(float x) { return __builtin_fabsf(x); }
 template <typename T>

@@ -1,0 +1,224 @@
+"""GPU parity of the implicit-differentiation adjoint (purin_cp_adjoint) vs the oracle.
+
+The oracle's adjoint (oracle/adjoint.py) is pinned by the reference's known
+gradients and by closed-form active-set derivatives; here the HIP GMRES is
+checked against it on the same inputs, plus the reference's known-answer
+Jacobians directly.
+
+Why the 1e-10 fp64 bar is checked at a tight GMRES tolerance: with the default
+GMRES tolerance (1e-9 relative residual) the VJP is only determined to that
+tolerance, and the oracle itself moves by 0.8-1.9e-10 when its step size is
+perturbed by one ulp (measured on these seeds).  At GMRES tolerance 1e-14 the
+oracle is reproducible to ~1e-15 under the same perturbation, so 1e-10 is a
+meaningful parity bar there.  Default-tolerance runs are compared at 1e-8.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import projection as op
+from purin_amd import workloads
+from tests import _cases
+from tests._gpu import canonical_from_workload, plan_for, rel_err, require_gpu, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_vjp(canon, target, rhs, cot, *, dtype=np.float64, accelerated=False, force=False,
+            max_iterations=10000, tolerance=1e-9, early_stop=True, metric=None):
+    require_gpu()
+    plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
+    if metric is not None:
+        plan.set_metric(metric)
+    out = plan.project(np.asarray(target, dtype), np.asarray(rhs, dtype), save=True,
+                       max_iterations=max_iterations, tolerance=tolerance, early_stop=early_stop)
+    adj = plan.adjoint(out.saved, np.asarray(target, dtype), np.asarray(rhs, dtype),
+                       np.asarray(cot, dtype), force_eligible=force)
+    return out, adj
+
+
+def jac_gpu(canon, target, rhs, **kw):
+    B, n = np.shape(target)
+    jt = np.zeros((B, n, n))
+    jr = np.zeros((B, n, np.shape(rhs)[1]))
+    for k in range(n):
+        cot = np.zeros((B, n))
+        cot[:, k] = 1.0
+        _, adj = gpu_vjp(canon, target, rhs, cot, **kw)
+        jt[:, k, :] = to_np(adj.g_target)
+        jr[:, k, :] = to_np(adj.g_rhs)
+    return jt, jr
+
+
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_known_answer_gradients(accelerated):
+    """Reference tests/test_regression_chambolle_pock.py:39-46."""
+    canon = _cases.sum_equals_b_u_nonneg()
+    target = np.array([[2.0, 0.0], [-2.0, 0.0]])
+    rhs = np.array([[1.0, 0.0], [1.0, 0.0]])
+    jt, jr = jac_gpu(canon, target, rhs, accelerated=accelerated)
+    np.testing.assert_allclose(jt[0], [[0.5, -0.5], [-0.5, 0.5]], atol=1e-8)
+    np.testing.assert_allclose(jt[1], 0, atol=1e-8)
+    np.testing.assert_allclose(jr[0][:, 0], [0.5, 0.5], atol=1e-8)
+    np.testing.assert_allclose(jr[1][:, 0], [0.0, 1.0], atol=1e-8)
+
+
+def test_known_answer_tied_bounds_zero_gradient_and_bound_row_rhs():
+    """Reference tests/test_regression_cp_bound_presolve.py:25-27, 41-52."""
+    canon, rhs = _cases.tied_scaled_bounds()
+    _, adj = gpu_vjp(canon, [[-3.0, 4.0]], rhs[None], np.ones((1, 2)))
+    np.testing.assert_allclose(to_np(adj.g_target), 0.0, atol=1e-9)
+    # a u <= b with a = 2, b = 1, x = 3  ->  dy/db = 0.5
+    single = op.Canonical(n=1, me=0, rows=[[0]], coef=[[2.0]])
+    _, adj = gpu_vjp(single, [[3.0]], [[1.0]], np.ones((1, 1)))
+    np.testing.assert_allclose(to_np(adj.g_rhs), [[0.5]], atol=1e-8)
+    infeasible = op.Canonical(n=1, me=0, rows=[[0]], coef=[[0.0]])
+    out, adj = gpu_vjp(infeasible, [[3.0]], [[-1.0]], np.ones((1, 1)))
+    assert not to_np(out.eligible)[0]
+    np.testing.assert_allclose(to_np(adj.g_target), 0.0)
+
+
+def test_known_answer_ineligible_gradient_is_zero():
+    """Reference tests/test_regression_chambolle_pock.py:68-83 (max_iterations=1)."""
+    canon = _cases.sum_equals_b_u_nonneg()
+    out, adj = gpu_vjp(canon, [[-2.0, 0.0]], [[1.0, 0.0]], np.ones((1, 2)), max_iterations=1)
+    assert not to_np(out.eligible)[0]
+    assert not to_np(adj.valid)[0]
+    np.testing.assert_allclose(to_np(adj.g_target), 0.0)
+
+
+def test_known_answer_no_constraints_unit_gradient():
+    canon = op.Canonical(n=2, me=0, rows=[], coef=[])
+    _, adj = gpu_vjp(canon, [[0.2, 0.7]], np.zeros((1, 0)), np.ones((1, 2)))
+    np.testing.assert_allclose(to_np(adj.g_target), 1.0, atol=1e-9)
+
+
+def test_known_answer_weighted_distance_jacobian():
+    """Reference tests/test_training_metric_contracts.py:63-83: WeightedDistance [1, 4]."""
+    canon = _cases.sum_equals_b()
+    D = np.array([1.0, 4.0])
+    inv = 1 / np.sqrt(D)
+    scaled = op.Canonical(canon.n, canon.me, canon.rows,
+                          [[v * inv[j] for j, v in zip(r, c)] for r, c in zip(canon.rows, canon.coef)])
+    target, rhs = np.array([[2.0, 0.0]]), np.ones((1, 1))
+    jt = np.zeros((2, 2))
+    for k in range(2):
+        cot = np.zeros((1, 2))
+        cot[0, k] = 1.0
+        out, adj = gpu_vjp(scaled, target, rhs, cot, metric=np.sqrt(D))
+        jt[k] = to_np(adj.g_target)[0]
+    np.testing.assert_allclose(to_np(out.y), [[1.2, -0.2]], atol=2e-6)
+    np.testing.assert_allclose(jt, [[0.2, -0.8], [-0.2, 0.8]], atol=2e-5)
+
+
+def _solve_state(canon, target, rhs, cfg, dtype, *, accelerated=False):
+    """GPU inner solve with a saved state, and the oracle's presolve of the same inputs."""
+    torch = require_gpu()
+    pre = op.presolve(canon, rhs, cfg, dtype)
+    plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
+    o, saved = plan.solve(pre.kept_rhs, target, pre.lower, pre.upper, tol=pre.tolerance,
+                          feasible=pre.feasible, max_iterations=cfg.max_iterations,
+                          tolerance=cfg.tolerance, early_stop=cfg.early_stop, save=True)
+    return plan, pre, o, saved
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_vjp_matches_oracle_at_the_same_state(dtype, seed):
+    """GMRES + pullback parity: the oracle linearises at the GPU's exact forward state."""
+    from oracle import adjoint as oadj
+
+    B = 40
+    w = workloads.small_random(20 + seed, n=24, me=4, mi=8, width=3, batch=B)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+    target = w.target.astype(dtype)
+    cot = np.random.default_rng(seed).normal(size=(B, canon.n)).astype(dtype)
+    tol = 1e-9 if dtype == np.float64 else 1e-5
+    tight = dict(gmres_tolerance=1e-14, gmres_max_iterations=300) if dtype == np.float64 else {}
+    cfg = op.Config(max_iterations=20000, tolerance=tol, **tight)
+    plan, pre, o, saved = _solve_state(canon, target, rhs, cfg, dtype)
+    conv = to_np(o.converged)
+    assert conv.sum() >= B // 2
+    ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
+    want = oadj.adjoint(pre.kept_values[0], ksup, kmask, canon.me, to_np(o.y), to_np(o.dual),
+                        conv, target, pre.kept_rhs, pre.lower, pre.upper, cot, cfg)
+    adj = plan.adjoint(saved, target, pre.kept_rhs, cot, bounds_grad=True, rhs_rows=plan.m,
+                       tolerance=cfg.gmres_tolerance, max_iterations=cfg.gmres_max_iterations)
+    np.testing.assert_array_equal(to_np(adj.valid), want.valid)
+    np.testing.assert_array_equal(to_np(adj.info), want.info)
+    bar = 1e-10 if dtype == np.float64 else 1e-4
+    assert rel_err(to_np(adj.g_target), want.g_target) <= bar
+    assert rel_err(to_np(adj.g_rhs), want.g_rhs) <= bar
+    assert rel_err(to_np(adj.g_lower), want.g_lower) <= bar
+    assert rel_err(to_np(adj.g_upper), want.g_upper) <= bar
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_project_vjp_matches_oracle_end_to_end(dtype):
+    """Forward + adjoint through purin_cp_project vs the oracle's own forward + adjoint.
+
+    The two forward states agree to ~1e-12, and the adjoint is defined only to the
+    GMRES tolerance (1e-9 relative residual), so the end-to-end bar is 1e-8 (fp64).
+    """
+    B = 40
+    w = workloads.small_random(25, n=24, me=4, mi=8, width=3, batch=B)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+    target = w.target.astype(dtype)
+    cot = np.random.default_rng(7).normal(size=(B, canon.n)).astype(dtype)
+    tol = 1e-9 if dtype == np.float64 else 1e-5
+    cfg = op.Config(max_iterations=20000, tolerance=tol)
+    res, gt, gr, adj_o = op.vjp(canon, target, rhs, cfg, cot, dtype=dtype)
+    out, adj = gpu_vjp(canon, target, rhs, cot, dtype=dtype, max_iterations=20000, tolerance=tol)
+    np.testing.assert_array_equal(to_np(out.eligible), res.gradient_eligible)
+    np.testing.assert_array_equal(to_np(adj.valid), adj_o.valid)
+    bar = 1e-8 if dtype == np.float64 else 1e-4
+    assert rel_err(to_np(adj.g_target), gt) <= bar
+    assert rel_err(to_np(adj.g_rhs), gr) <= bar
+
+
+def test_vjp_forced_eligible_at_fixed_iteration_state():
+    """Config-5 style: adjoint at a fixed-iteration (unconverged) state, eligibility forced."""
+    from oracle import adjoint as oadj
+
+    B = 24
+    w = workloads.small_random(31, n=32, me=6, mi=10, width=4, batch=B, accelerated=True)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (B, 1))
+    cot = np.random.default_rng(9).normal(size=(B, canon.n))
+    cfg = op.Config(accelerated=True, max_iterations=300, early_stop=False,
+                    gmres_tolerance=1e-14, gmres_max_iterations=300)
+    plan, pre, o, saved = _solve_state(canon, w.target, rhs, cfg, np.float64, accelerated=True)
+    ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
+    want = oadj.adjoint(pre.kept_values[0], ksup, kmask, canon.me, to_np(o.y), to_np(o.dual),
+                        np.ones(B, bool), w.target, pre.kept_rhs, pre.lower, pre.upper, cot, cfg)
+    adj = plan.adjoint(saved, w.target, pre.kept_rhs, cot, force_eligible=True, rhs_rows=plan.m,
+                       tolerance=1e-14, max_iterations=300)
+    np.testing.assert_array_equal(to_np(adj.info), want.info)
+    np.testing.assert_array_equal(to_np(adj.valid), want.valid)
+    # GMRES residuals sit at the rounding floor: compare them against the threshold scale
+    assert np.max(np.abs(to_np(adj.residual) - want.residual)) <= 1e-12 * np.abs(cot).max()
+    assert rel_err(to_np(adj.g_target), want.g_target) <= 1e-10
+    assert rel_err(to_np(adj.g_rhs), want.g_rhs) <= 1e-10
+
+
+def test_default_gmres_tolerance_parity():
+    """Default LinearSolverConfig (tol 1e-9, restart 30, 100 iterations): 1e-8 bar (see header)."""
+    from oracle import adjoint as oadj
+
+    B = 40
+    w = workloads.small_random(20, n=24, me=4, mi=8, width=3, batch=B)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (B, 1))
+    cot = np.random.default_rng(0).normal(size=(B, canon.n))
+    cfg = op.Config(max_iterations=20000, tolerance=1e-9)
+    plan, pre, o, saved = _solve_state(canon, w.target, rhs, cfg, np.float64)
+    ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
+    want = oadj.adjoint(pre.kept_values[0], ksup, kmask, canon.me, to_np(o.y), to_np(o.dual),
+                        to_np(o.converged), w.target, pre.kept_rhs, pre.lower, pre.upper, cot, cfg)
+    adj = plan.adjoint(saved, w.target, pre.kept_rhs, cot, rhs_rows=plan.m)
+    np.testing.assert_array_equal(to_np(adj.valid), want.valid)
+    np.testing.assert_array_equal(to_np(adj.info), want.info)
+    assert rel_err(to_np(adj.g_target), want.g_target) <= 1e-8
+    assert rel_err(to_np(adj.g_rhs), want.g_rhs) <= 1e-8
