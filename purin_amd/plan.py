@@ -247,10 +247,12 @@ class Plan:
                 max_iterations=100, adjoint_tolerance=1e-8, force_eligible=False,
                 bounds_grad=False, rhs_rows=None):
         """Implicit VJP at a saved forward state (``purin_cp_adjoint``)."""
-        batch = target.shape[0]
+        batch = cot_y.shape[0]
         rows = rhs_rows if rhs_rows is not None else self.me + self.mi
-        target = self._tensor(target, (batch, self.n), "target")
-        rhs = self._tensor(rhs, (batch, rows), "rhs")
+        # target and rhs are held by the saved state; they are accepted for interface
+        # parity with the reference's custom_vjp residuals and not re-read
+        target = None if target is None else self._tensor(target, (batch, self.n), "target")
+        rhs = None if rhs is None else self._tensor(rhs, (batch, rows), "rhs")
         cot = self._tensor(cot_y, (batch, self.n), "cotangent")
         o = _lib.default_adjoint_options()
         o.tolerance = float(tolerance)

@@ -1,0 +1,120 @@
+"""Host-side front end: canonical rows, sign conventions, configuration validation.
+
+CPU only (no kernel is launched).
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+import purin_amd as pa
+from purin_amd.problems import CanonicalRows
+
+
+def test_public_names_match_the_reference_cp_surface():
+    for name in ("Projection", "ParametricQP", "MatrixProblem", "ChambollePockConfig",
+                 "LinearSolverConfig", "ImplicitGradientConfig", "SolveStatus",
+                 "prepare_projection", "registered_methods", "Distance", "WeightedDistance"):
+        assert getattr(pa, name) is not None
+    assert pa.registered_methods() == ("chambolle-pock",)
+    assert [int(s) for s in pa.SolveStatus] == [0, 1, 2, 3, 4]
+
+
+def test_symbolic_rows_signs_and_rhs_map():
+    """``u + v == b`` and ``u >= 0``: expressions.py:298-309 sign convention."""
+    p = pa.Projection()
+    t = p.add_parameter(["b"])
+    y = p.add_variable(["u", "v"])
+    p.objective = 0.0
+    p.constraints.add(y.u + y.v == t.b, y.u >= 0, 2 * y.v <= 3 - t.b)
+    c = p.canonicalize()
+    assert (c.me, c.mi, c.n, c.parameter_size) == (1, 2, 2, 1)
+    np.testing.assert_array_equal(c.indptr, [0, 2, 3, 4])
+    np.testing.assert_array_equal(c.indices, [0, 1, 0, 1])
+    np.testing.assert_array_equal(c.values, [1.0, 1.0, -1.0, 2.0])
+    np.testing.assert_array_equal(c.rhs([[5.0]]), [[5.0, 0.0, -2.0]])
+    assert c.affine and not c.parametric_coefficients
+
+
+def test_nonlinear_and_parametric_coefficients_are_flagged():
+    p = pa.Projection()
+    y = p.add_variable(["u"])
+    p.constraints.add(y.u ** 2 <= 1)
+    assert not p.canonicalize().affine
+    q = pa.Projection()
+    a = q.add_parameter(["a"])
+    z = q.add_variable(["u", "v"])
+    q.constraints.add(a.a * z.u + z.v == 1)
+    assert q.canonicalize().parametric_coefficients
+    with pytest.raises(TypeError):
+        bool(z.u <= 1)
+
+
+def test_duplicate_symbols_rejected():
+    p = pa.Projection()
+    p.add_variable(["u"])
+    with pytest.raises(ValueError, match="Duplicate"):
+        p.add_parameter(["u"])
+
+
+def test_matrix_problem_from_bounds_row_order():
+    """Upper rows then lower rows, equalities where lower == upper (qp.py:308-398)."""
+    A = np.array([[1, 1, 1], [1, 0, 0], [0, 1, 0], [0, 0, 1], [2, -1, 0]], float)
+    m = pa.MatrixProblem.from_bounds(P=np.eye(3), q0=np.zeros(3), A=A,
+                                     lower0=[1, 0, -0.5, -np.inf, -np.inf],
+                                     upper0=[1, np.inf, np.inf, 0.7, 0.9])
+    c = m.canonicalize()
+    assert (c.me, c.mi) == (1, 4)
+    np.testing.assert_array_equal(c.rhs0, [1.0, 0.7, 0.9, 0.0, 0.5])
+    np.testing.assert_array_equal(c.values, [1, 1, 1, 1, 2, -1, -1, -1])
+
+
+def test_matrix_problem_sparse_and_dense_agree():
+    import scipy.sparse as sp
+
+    rng = np.random.default_rng(0)
+    A = rng.normal(size=(4, 6)) * (rng.uniform(size=(4, 6)) < 0.5)
+    dense = pa.ParametricQP(P=np.eye(6), q0=np.zeros(6), A_ineq=A, b_ineq0=np.ones(4)).canonicalize()
+    sparse = pa.ParametricQP(P=np.eye(6), q0=np.zeros(6), A_ineq=sp.csr_matrix(A),
+                             b_ineq0=np.ones(4)).canonicalize()
+    for f in ("indptr", "indices", "values", "rhs0"):
+        np.testing.assert_array_equal(getattr(dense, f), getattr(sparse, f))
+
+
+@pytest.mark.parametrize("kwargs,match", [
+    (dict(tolerance=0.0), "tolerance"),
+    (dict(tolerance=math.inf), "tolerance"),
+    (dict(max_iterations=0), "max_iterations"),
+    (dict(max_iterations=1.5), "max_iterations"),
+    (dict(safety=1.0), "safety"),
+    (dict(norm_iterations=0), "norm_iterations"),
+    (dict(metric_diagonal=(1.0, -1.0)), "metric_diagonal"),
+])
+def test_config_validation_messages(kwargs, match):
+    """Reference src/purin/solvers/chambolle_pock/config.py:50-61."""
+    with pytest.raises(ValueError, match=match):
+        pa.ChambollePockConfig(**kwargs)
+
+
+def test_linear_and_gradient_config_validation():
+    with pytest.raises(ValueError):
+        pa.LinearSolverConfig(restart=0)
+    with pytest.raises(ValueError):
+        pa.ImplicitGradientConfig(policy="bogus")
+    assert pa.ChambollePockConfig().linear_solver.restart == 30
+
+
+def test_cpu_backend_and_unknown_methods_are_rejected():
+    from purin_amd.projection import resolve_device
+
+    with pytest.raises(ValueError, match="cpu"):
+        resolve_device("cpu")
+    with pytest.raises(ValueError, match="Unknown projection method"):
+        pa.ProjectionMethod.normalize("admm")
+
+
+def test_canonical_rows_rhs_broadcast():
+    c = CanonicalRows(2, 1, 0, 1, np.array([0, 2]), np.array([0, 1], np.int32), np.ones(2),
+                      np.array([0.5]), np.array([[2.0]]))
+    np.testing.assert_array_equal(c.rhs([[1.0], [2.0]]), [[2.5], [4.5]])

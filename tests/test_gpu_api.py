@@ -1,0 +1,282 @@
+"""The reference's public-API CP tests, run through this build's front end on the GPU.
+
+Each test restates a reference test (cited) with the reference's expected
+values; gradients use torch autograd, whose backward is purin_cp_adjoint.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as _torch
+
+    if not _torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    return _torch
+
+
+def problem():
+    from purin_amd import Projection
+
+    p = Projection(method="chambolle-pock")
+    t = p.add_parameter(["b"])
+    y = p.add_variable(["u", "v"])
+    p.objective = 0.0
+    p.constraints.add(y.u + y.v == t.b, y.u >= 0)
+    return p
+
+
+def jac(torch, f, x):
+    return torch.autograd.functional.jacobian(f, x).cpu().numpy()
+
+
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_affine_projection_and_gradients(torch, accelerated):
+    """Reference tests/test_regression_chambolle_pock.py:25-56."""
+    from purin_amd import ChambollePockConfig, ImplicitGradientConfig, SolveStatus, prepare_projection
+
+    cfg = ChambollePockConfig(
+        accelerated=accelerated,
+        implicit_gradient=ImplicitGradientConfig(differentiate_problem_parameters=True))
+    layer = prepare_projection(problem(), method="chambolle-pock", config=cfg, batch_size=2)
+    values = torch.tensor([[2.0, 0.0], [-2.0, 0.0]], dtype=torch.float64, device="cuda")
+    theta = torch.ones((2, 1), dtype=torch.float64, device="cuda")
+    out = layer.solve(values, theta)
+    np.testing.assert_allclose(out.y.detach().cpu(), [[1.5, -0.5], [0.0, 1.0]], atol=1e-8)
+    assert np.all(out.status.cpu().numpy() == int(SolveStatus.CONVERGED))
+    assert float(out.residual_inf_norm.max()) <= cfg.tolerance
+    j = jac(torch, lambda x: layer(x, theta), values)
+    np.testing.assert_allclose(j[0, :, 0, :], [[0.5, -0.5], [-0.5, 0.5]], atol=1e-8)
+    np.testing.assert_allclose(j[1, :, 1, :], 0, atol=1e-8)
+    np.testing.assert_allclose(j[0, :, 1, :], 0, atol=1e-8)
+    d = jac(torch, lambda t: layer(values, t), theta)
+    np.testing.assert_allclose(d[0, :, 0, 0], [0.5, 0.5], atol=1e-8)
+    np.testing.assert_allclose(d[1, :, 1, 0], [0.0, 1.0], atol=1e-8)
+    eps = 1e-4
+    fd = ((layer(values, theta + eps) - layer(values, theta - eps)) / (2 * eps)).detach().cpu()
+    np.testing.assert_allclose(fd, [[0.5, 0.5], [0.0, 1.0]], atol=1e-5)
+
+
+def test_rejects_nonlinear_constraints(torch):
+    """Reference tests/test_regression_chambolle_pock.py:59-65."""
+    from purin_amd import Projection, prepare_projection
+
+    p = Projection()
+    y = p.add_variable(["u"])
+    p.objective = 0.0
+    p.constraints.add(y.u ** 2 <= 1)
+    with pytest.raises(ValueError, match="affine"):
+        prepare_projection(p, method="chambolle-pock", batch_size=1)
+
+
+def test_iteration_limit_and_nonfinite_diagnostics(torch):
+    """Reference tests/test_regression_chambolle_pock.py:68-85."""
+    from purin_amd import ChambollePockConfig, SolveStatus, prepare_projection
+
+    layer = prepare_projection(problem(), method="chambolle-pock",
+                               config=ChambollePockConfig(max_iterations=1), batch_size=1)
+    one = torch.ones((1, 1), dtype=torch.float64)
+    out = layer.solve(torch.tensor([[-2.0, 0.0]], dtype=torch.float64), one)
+    assert int(out.status[0]) == int(SolveStatus.MAX_ITERATIONS)
+    assert not bool(out.gradient_eligible[0])
+    x = torch.tensor([[-2.0, 0.0]], dtype=torch.float64, device="cuda", requires_grad=True)
+    layer(x, one).sum().backward()
+    np.testing.assert_allclose(x.grad.cpu(), 0)
+    out = layer.solve(torch.tensor([[float("nan"), 0.0]], dtype=torch.float64), one)
+    assert int(out.status[0]) == int(SolveStatus.NONFINITE)
+
+
+def test_no_constraints_and_unit_gradient(torch):
+    """Reference tests/test_regression_chambolle_pock.py:88-95."""
+    from purin_amd import Projection, prepare_projection
+
+    p = Projection()
+    p.add_variable(["u", "v"])
+    p.objective = 0.0
+    layer = prepare_projection(p, method="chambolle-pock", batch_size=1)
+    x = torch.tensor([[0.2, 0.7]], dtype=torch.float64, device="cuda", requires_grad=True)
+    np.testing.assert_allclose(layer(x).detach().cpu(), [[0.2, 0.7]], atol=1e-12)
+    layer(x).sum().backward()
+    np.testing.assert_allclose(x.grad.cpu(), 1, atol=1e-9)
+
+
+def test_inequality_only_and_warm_start_gradients(torch):
+    """Reference tests/test_regression_chambolle_pock.py:98-113."""
+    from purin_amd import Projection, prepare_projection
+
+    p = Projection()
+    y = p.add_variable(["u", "v"])
+    p.objective = 0.0
+    p.constraints.add(y.u >= 0, y.v <= 1)
+    layer = prepare_projection(p, method="chambolle-pock", batch_size=1)
+    x = torch.tensor([[-2.0, 3.0]], dtype=torch.float64)
+    out = layer.project_training(x, multipliers_ineq=torch.tensor([[0.2, 0.3]]))
+    np.testing.assert_allclose(out.y_tilde.detach().cpu(), [[0.0, 1.0]], atol=1e-8)
+    assert bool(out.forward_gradient_eligible[0])
+
+
+def test_infeasible_problem_never_claims_convergence(torch):
+    """Reference tests/test_regression_chambolle_pock.py:140-153."""
+    from purin_amd import ChambollePockConfig, Projection, SolveStatus, prepare_projection
+
+    p = Projection()
+    y = p.add_variable(["u"])
+    p.objective = 0.0
+    p.constraints.add(y.u <= 0, y.u >= 1)
+    layer = prepare_projection(p, method="chambolle-pock",
+                               config=ChambollePockConfig(max_iterations=100), batch_size=1)
+    out = layer.solve(torch.zeros((1, 1), dtype=torch.float64))
+    assert int(out.status[0]) == int(SolveStatus.MAX_ITERATIONS)
+    assert not bool(out.gradient_eligible[0])
+
+
+def test_scaled_constraints_report_original_units(torch):
+    """Reference tests/test_regression_chambolle_pock.py:156-164."""
+    from purin_amd import Projection, prepare_projection
+
+    p = Projection()
+    y = p.add_variable(["u", "v"])
+    p.objective = 0.0
+    p.constraints.add(1000 * y.u + 1000 * y.v == 1000, y.u >= 0)
+    layer = prepare_projection(p, method="chambolle-pock", batch_size=1)
+    out = layer.solve(torch.tensor([[2.0, 0.0]], dtype=torch.float64))
+    assert bool(out.gradient_eligible[0])
+    assert abs(float(out.y.sum()) * 1000 - 1000) <= layer.config.tolerance
+
+
+def test_tied_scaled_bounds_restore_duals_and_slacks(torch):
+    """Reference tests/test_regression_cp_bound_presolve.py:13-27."""
+    from purin_amd import Projection, SolveStatus, prepare_projection
+
+    p = Projection()
+    y = p.add_variable(["u", "v"])
+    p.objective = 0.0
+    p.constraints.add(y.u >= 0, 2 * y.u >= 0, y.u <= 2, y.v <= 1)
+    layer = prepare_projection(p, method="chambolle-pock", batch_size=1)
+    out = layer.solve(torch.tensor([[-3.0, 4.0]], dtype=torch.float64))
+    np.testing.assert_allclose(out.y.detach().cpu(), [[0.0, 1.0]], atol=1e-10)
+    np.testing.assert_allclose(out.multipliers_ineq.cpu(), [[1.5, 0.75, 0.0, 3.0]], atol=1e-9)
+    np.testing.assert_allclose(out.slacks.cpu(), [[0.0, 0.0, 2.0, 0.0]], atol=1e-10)
+    assert int(out.status[0]) == int(SolveStatus.CONVERGED)
+    assert layer.plan.m == 0
+    x = torch.tensor([[-3.0, 4.0]], dtype=torch.float64, device="cuda", requires_grad=True)
+    layer(x).sum().backward()
+    np.testing.assert_allclose(x.grad.cpu(), 0.0, atol=1e-9)
+
+
+@pytest.mark.parametrize("seed", [12, 42])
+def test_coupled_qp_matches_exact_projection_and_fd(torch, seed):
+    """Reference tests/test_regression_cp_bound_presolve.py:56-109 (OSQP -> exact projection)."""
+    from oracle import qp as bf
+    from purin_amd import Projection, prepare_projection
+
+    rng = np.random.default_rng(seed)
+    p = Projection()
+    y = p.add_variable(["u", "v", "w"])
+    p.objective = 0.0
+    p.constraints.add(y.u + y.v + y.w == 1, y.u >= 0, y.v >= -0.5, y.w <= 0.7,
+                      2 * y.u - y.v <= 0.9)
+    layer = prepare_projection(p, method="chambolle-pock", batch_size=1)
+    x = rng.normal(size=(1, 3))
+    matrix = np.array([[1.0, 1.0, 1.0], [-1.0, 0.0, 0.0], [0.0, -1.0, 0.0], [0.0, 0.0, 1.0],
+                       [2.0, -1.0, 0.0]])
+    upper = np.array([1.0, 0.0, 0.5, 0.7, 0.9])
+    ref = bf.project_bruteforce(x[0], matrix[:1], upper[:1], matrix[1:], upper[1:])[0]
+    out = layer.solve(torch.as_tensor(x))
+    np.testing.assert_allclose(out.y[0].detach().cpu(), ref, atol=2e-8)
+    mult = np.r_[out.multipliers_eq[0].cpu().numpy(), out.multipliers_ineq[0].cpu().numpy()]
+    np.testing.assert_allclose((out.y[0].detach().cpu().numpy() - x[0]) + matrix.T @ mult, 0.0,
+                               atol=1e-9)
+    assert bool(out.gradient_eligible[0])
+    g = torch.as_tensor(rng.normal(size=(1, 3)), device="cuda")
+    xt = torch.as_tensor(x, device="cuda").requires_grad_(True)
+    (layer(xt) * g).sum().backward()
+    for i in range(3):
+        d = np.zeros_like(x)
+        d[0, i] = 1e-4
+        fd = float(((layer(torch.as_tensor(x + d)) - layer(torch.as_tensor(x - d))) * g).sum()) / 2e-4
+        np.testing.assert_allclose(float(xt.grad[0, i]), fd, atol=2e-5)
+
+
+def make_problem(inequalities=False):
+    from purin_amd import Projection
+
+    problem = Projection()
+    pb = problem.add_parameter(["b"])
+    y = problem.add_variable(["u", "v"])
+    problem.objective = 0.0
+    problem.constraints.add(y.u + y.v == pb.b)
+    if inequalities:
+        problem.constraints.add(y.u >= 0)
+        problem.constraints.add(y.v >= 0)
+    return problem
+
+
+@pytest.mark.parametrize("dtype,atol", [("float64", 2e-6), ("float32", 5e-5)])
+def test_affine_projection_and_analytic_jacobian(torch, dtype, atol):
+    """Reference tests/test_projections.py:65-75 and .github/scripts/numerical_regression.py:23-82
+    (fp32 uses that script's settings: tolerance 1e-6, adjoint/inexact tolerance 1e-5,
+    linear-solver tolerance 1e-6)."""
+    from dataclasses import replace
+
+    from purin_amd import ChambollePockConfig, Distance, ImplicitGradientConfig, LinearSolverConfig
+
+    cfg = ChambollePockConfig(max_iterations=3000, tolerance=1e-6 if dtype == "float32" else 1e-10)
+    if dtype == "float32":
+        cfg = replace(cfg, implicit_gradient=ImplicitGradientConfig(adjoint_tolerance=1e-5,
+                                                                    inexact_tolerance=1e-5),
+                      linear_solver=LinearSolverConfig(tolerance=1e-6))
+    project = Distance(make_problem(), "chambolle-pock", cfg).prepare(batch_size=1, dtype=dtype)
+    tdt = torch.float64 if dtype == "float64" else torch.float32
+    target = torch.tensor([[0.8, 0.7]], dtype=tdt, device="cuda")
+    context = torch.ones((1, 1), dtype=tdt)
+    np.testing.assert_allclose(project(target, context).detach().cpu(), [[0.55, 0.45]], atol=atol)
+    d = jac(torch, lambda x: project(x[None, :], context)[0], target[0])
+    np.testing.assert_allclose(d, [[0.5, -0.5], [-0.5, 0.5]], atol=atol)
+
+
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_cp_variants_with_active_inequality(torch, accelerated):
+    """Reference tests/test_projections.py:78-97."""
+    from purin_amd import ChambollePockConfig, Distance
+
+    cfg = ChambollePockConfig(accelerated=accelerated, tolerance=1e-9, max_iterations=3000)
+    project = Distance(make_problem(inequalities=True), "chambolle-pock", cfg).prepare(batch_size=1)
+    np.testing.assert_allclose(
+        project(torch.tensor([[2.0, -1.0]], dtype=torch.float64),
+                torch.ones((1, 1), dtype=torch.float64)).detach().cpu(), [[1.0, 0.0]], atol=2e-6)
+
+
+def test_weighted_projection_protocol_and_gradient(torch):
+    """Reference tests/test_projections.py:121-124, tests/test_training_metric_contracts.py:63-83."""
+    from purin_amd import WeightedDistance
+
+    prepared = WeightedDistance(make_problem(), [1.0, 4.0], method="chambolle-pock").prepare(
+        batch_size=1)
+    target = torch.tensor([[2.0, 0.0]], dtype=torch.float64, device="cuda")
+    context = torch.ones((1, 1), dtype=torch.float64)
+    expected = [[1.2, -0.2]]
+    with pytest.raises(ValueError, match="warm starts"):
+        prepared.solve(target, context, initial_state=torch.tensor([[1.2, -0.2]]))
+    np.testing.assert_allclose(prepared.solve(target, context).y.detach().cpu(), expected, atol=2e-5)
+    np.testing.assert_allclose(prepared.project_training(target, context).y_tilde.detach().cpu(),
+                               expected, atol=2e-5)
+    np.testing.assert_allclose(prepared.with_info(target, context)[0].detach().cpu(), expected,
+                               atol=2e-5)
+    d = jac(torch, lambda x: prepared(x[None], context)[0], target[0])
+    np.testing.assert_allclose(d, [[0.2, -0.8], [-0.2, 0.8]], atol=2e-5)
+
+
+def test_parametric_coefficients_are_reported_unsupported(torch):
+    from purin_amd import Projection, prepare_projection
+
+    p = Projection()
+    t = p.add_parameter(["a"])
+    y = p.add_variable(["u", "v"])
+    p.constraints.add(t.a * y.u + y.v == 1)
+    with pytest.raises(NotImplementedError, match="per-sample"):
+        prepare_projection(p, method="chambolle-pock", batch_size=1)
