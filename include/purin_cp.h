@@ -146,6 +146,9 @@ typedef struct {
                               for every sample; only sample 0 is read */
   int32_t timing;          /* 1: bracket every iteration kernel with HIP events on
                               the call's stream (see purin_cp_last_timing) */
+  int32_t streaming;       /* 1: force the streaming row/column passes even when the
+                              resident on-chip kernel applies (fixed iterations) */
+  int32_t reserved;
 } purin_cp_solve_options;
 
 void purin_cp_default_solve_options(purin_cp_solve_options* opts);
@@ -200,6 +203,8 @@ typedef struct {
   double col_ms;        /* summed column-pass time */
   double diag_ms;       /* summed residual + decide time (stop test) */
   double loop_ms;       /* first iteration kernel start to last end */
+  int32_t resident;     /* 1: the iterations ran in the resident kernel (one launch) */
+  int32_t reserved;
 } purin_cp_timing;
 
 int purin_cp_last_timing(const purin_cp_plan* plan, purin_cp_timing* timing);

@@ -68,6 +68,8 @@ class SolveOptions(C.Structure):
         ("check_every", C.c_int32),
         ("shared_bounds", C.c_int32),
         ("timing", C.c_int32),
+        ("streaming", C.c_int32),
+        ("reserved", C.c_int32),
     ]
 
 
@@ -78,6 +80,8 @@ class Timing(C.Structure):
         ("col_ms", C.c_double),
         ("diag_ms", C.c_double),
         ("loop_ms", C.c_double),
+        ("resident", C.c_int32),
+        ("reserved", C.c_int32),
     ]
 
 

@@ -17,6 +17,7 @@
 #include "plan.hpp"
 #include "post.hpp"
 #include "forward.hpp"
+#include "resident.hpp"
 
 namespace purin {
 
@@ -58,8 +59,152 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch) {
   L.ofin = take(Bp * 4);
   L.X = take(std::max(n, m) * Bp * es);  // spmm input / output staging
   L.Z = take(std::max(n, m) * Bp * es);
+  if (p->res_ok) {  // resident path: slot-ordered copies of the per-sample inputs
+    const size_t Kr = (size_t)p->res_mr * kResThreads, Kc = (size_t)p->res_mc * kResThreads;
+    L.RTs = take(Kc * Bp * es);
+    L.RRs = take(Kr * Bp * es);
+    L.RD0 = take(Kr * Bp * es);
+    L.RLs = take(Kc * Bp * es);
+    L.RHs = take(Kc * Bp * es);
+  }
   L.ws_end = o;
   return L;
+}
+
+template <typename T>
+constexpr int res_tile() {
+  return sizeof(T) == 8 ? 2 : 4;  // 16 bytes of samples per gathered element
+}
+
+template <typename T, int BT, int SL>
+static int launch_resident_sl(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds) {
+  auto kern = R.shared_bounds ? k_resident<T, BT, SL, true> : k_resident<T, BT, SL, false>;
+  PURIN_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+  kern<<<dim3((unsigned)tiles), dim3(kResThreads), lds, st>>>(R);
+  return PURIN_CP_OK;
+}
+
+template <typename T>
+static int launch_resident(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slots) {
+  constexpr int BT = res_tile<T>();
+  switch (slots) {
+    case 1: return launch_resident_sl<T, BT, 1>(R, st, tiles, lds);
+    case 2: return launch_resident_sl<T, BT, 2>(R, st, tiles, lds);
+    case 4: return launch_resident_sl<T, BT, 4>(R, st, tiles, lds);
+    default: return set_error(PURIN_CP_ERR_ARG, "resident slot count out of range");
+  }
+}
+
+// LDS of the resident kernel, or 0 when the problem does not fit on chip.
+template <typename T>
+static size_t resident_lds(const purin_cp_plan* p) {
+  if (!p->res_ok) return 0;
+  // two regions (ybar and d+), each with one trailing zero slot
+  const size_t lds = (size_t)(p->n + 1 + p->m + 1) * res_tile<T>() * sizeof(T);
+  return lds <= 160 * 1024 ? lds : 0;
+}
+
+// Per-iteration step scalars (kernels.py:68-73, 279-283), cached on the device.
+template <typename T>
+static int resident_schedule(purin_cp_plan* p, int64_t iters) {
+  if (p->res_sched && p->res_sched_len == iters) return PURIN_CP_OK;
+  std::vector<T> h((size_t)4 * iters);
+  const T one = T(1);
+  T tau = (T)p->tau0, sigma = (T)p->sigma0, theta = one;
+  for (int64_t k = 0; k < iters; ++k) {
+    const T a = one / (one + tau);
+    h[4 * k] = sigma;
+    h[4 * k + 1] = a;
+    h[4 * k + 2] = tau * a;
+    h[4 * k + 3] = theta;
+    if (p->opts.accelerated) {
+      const T nt = one / std::sqrt(one + tau);
+      tau = nt * tau;
+      sigma = sigma / nt;
+      theta = nt;
+    }
+  }
+  if (p->res_sched) {
+    PURIN_HIP(hipDeviceSynchronize());
+    PURIN_HIP(hipFree(p->res_sched));
+    p->res_sched = nullptr;
+  }
+  PURIN_HIP(hipMalloc(&p->res_sched, h.size() * sizeof(T)));
+  PURIN_HIP(hipMemcpy(p->res_sched, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice));
+  p->res_sched_len = iters;
+  return PURIN_CP_OK;
+}
+
+// Fixed-iteration loop on the resident kernel; fills Y and D like the passes.
+template <typename T>
+static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char* sv, char* ws,
+                        const purin_cp_solve_options& o, size_t lds) {
+  constexpr int BT = res_tile<T>();
+  const int64_t Bp = L.Bp, tiles = Bp / BT;
+  const int Kr = p->res_mr * kResThreads, Kc = p->res_mc * kResThreads;
+  if (int rc = resident_schedule<T>(p, o.max_iterations)) return rc;
+  Res<T> R{};
+  R.n = (int)p->n;
+  R.m = (int)p->m;
+  R.me = (int)p->me;
+  R.Bp = Bp;
+  R.rowmap = p->res_rowmap;
+  R.colmap = p->res_colmap;
+  R.rslice = p->res_rslice;
+  R.cslice = p->res_cslice;
+  R.ridx = p->res_ridx;
+  R.rval = (const T*)p->res_rval;
+  R.cidx = p->res_cidx;
+  R.cval = (const T*)p->res_cval;
+  T* Ts = (T*)(ws + L.RTs);
+  T* Rs = (T*)(ws + L.RRs);
+  T* D0s = (T*)(ws + L.RD0);
+  T* Ls = (T*)(ws + L.RLs);
+  T* Hs = (T*)(ws + L.RHs);
+  const unsigned gb = 2048;
+  k_res_gather<T, BT><<<gb, 256, 0, st>>>((const T*)(sv + L.Tt), Bp, p->res_colmap, Kc, tiles, Ts);
+  k_res_gather<T, BT><<<gb, 256, 0, st>>>((const T*)(sv + L.R), Bp, p->res_rowmap, Kr, tiles, Rs);
+  k_res_gather<T, BT><<<gb, 256, 0, st>>>((const T*)(sv + L.D), Bp, p->res_rowmap, Kr, tiles, D0s);
+  if (o.shared_bounds) {
+    k_res_gather_shared<T><<<(Kc + 255) / 256, 256, 0, st>>>((const T*)(sv + L.LO), p->res_colmap, Kc, Ls);
+    k_res_gather_shared<T><<<(Kc + 255) / 256, 256, 0, st>>>((const T*)(sv + L.HI), p->res_colmap, Kc, Hs);
+  } else {
+    k_res_gather<T, BT><<<gb, 256, 0, st>>>((const T*)(sv + L.LO), Bp, p->res_colmap, Kc, tiles, Ls);
+    k_res_gather<T, BT><<<gb, 256, 0, st>>>((const T*)(sv + L.HI), Bp, p->res_colmap, Kc, tiles, Hs);
+  }
+  R.Ts = Ts;
+  R.Rs = Rs;
+  R.D0s = D0s;
+  R.Ls = Ls;
+  R.Hs = Hs;
+  R.shared_bounds = o.shared_bounds;
+  R.sched = (const T*)p->res_sched;
+  R.iters = o.max_iterations;
+  R.Y = (T*)(sv + L.Y);
+  R.D = (T*)(sv + L.D);
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (o.timing) {
+    PURIN_HIP(hipEventCreate(&e0));
+    PURIN_HIP(hipEventCreate(&e1));
+    PURIN_HIP(hipEventRecord(e0, st));
+  }
+  if (int rc = launch_resident<T>(R, st, tiles, lds, p->res_mr)) return rc;
+  PURIN_HIP(hipGetLastError());
+  if (o.timing) {
+    PURIN_HIP(hipEventRecord(e1, st));
+    PURIN_HIP(hipEventSynchronize(e1));
+    float ms = 0;
+    PURIN_HIP(hipEventElapsedTime(&ms, e0, e1));
+    purin_cp_timing t{};
+    t.iterations = o.max_iterations;
+    t.loop_ms = ms;
+    t.resident = 1;
+    p->timing = t;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+  }
+  return PURIN_CP_OK;
 }
 
 // The CP loop on prepared internal arrays plus the final diagnostics.
@@ -87,11 +232,29 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   int32_t* count = (int32_t*)(ws + L.count);
   int32_t* ndone = (int32_t*)(ws + L.ndone);
   const int m = A.K.m, n = A.K.n;
+  const bool early = o.early_stop != 0;
+  const size_t lds = resident_lds<T>(p);
+  if (!early && lds && !o.streaming) {
+    if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds)) return rc;
+    const int32_t cnt = (int32_t)o.max_iterations;
+    k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);
+    A.done = nullptr;
+    const dim3 gcolE0 = tile_grid(Bp, TS, L.ncb);
+    const dim3 gres0 = tile_grid(Bp, TS, std::max(L.nrb, 1));
+    const dim3 gdec0((unsigned)((batch + kBlock - 1) / kBlock));
+    k_col_pass<T, 2, kRowsPerWaveEarly><<<gcolE0, kBlock, 0, st>>>(A);
+    if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres0, kBlock, 0, st>>>(A);
+    k_decide<T, true><<<gdec0, kBlock, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
+                                                (const int32_t*)(sv + L.feas), (T*)(ws + L.ores),
+                                                (T*)(ws + L.ogap), (int32_t*)(sv + L.conv),
+                                                (int32_t*)(ws + L.ofin));
+    PURIN_HIP(hipGetLastError());
+    return PURIN_CP_OK;
+  }
   // y0 = ybar0 = target (kernels.py:229-231, bounds.py:59)
   PURIN_HIP(hipMemcpyAsync(A.Y, A.tgt, (size_t)n * Bp * sizeof(T), hipMemcpyDeviceToDevice, st));
   PURIN_HIP(hipMemcpyAsync(A.YB, A.tgt, (size_t)n * Bp * sizeof(T), hipMemcpyDeviceToDevice, st));
 
-  const bool early = o.early_stop != 0;
   const int check = o.check_every > 0 ? o.check_every : 32;
   const T one = T(1);
   T tau = (T)p->tau0, sigma = (T)p->sigma0, theta = one;

@@ -14,7 +14,9 @@ struct Layout {
   // saved region
   size_t hdr, Tt, Y, D, R, LO, HI, RF, conv, feas, saved_end;
   // forward workspace
-  size_t YB, MF, DF, SL, colpart, rowpart, done, count, ndone, ores, ogap, ofin, X, Z, ws_end;
+  size_t YB, MF, DF, SL, colpart, rowpart, done, count, ndone, ores, ogap, ofin, X, Z;
+  size_t RTs, RRs, RD0, RLs, RHs;  // resident path (slot-ordered inputs)
+  size_t ws_end;
 };
 
 Layout make_layout(const purin_cp_plan* p, int64_t batch);

@@ -222,6 +222,76 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
     p->tau_adj = (double)(safety / (T(1) + La));
     p->sigma_adj = (double)(safety / La);
   }
+  // --- resident schedule: slots sorted by degree, 64-lane sliced ELL ----------
+  {
+    const int64_t NT = kResThreads;
+    // one slot count for rows and columns, a power of two (1, 2, 4, 8)
+    const int64_t need = std::max<int64_t>((std::max(m, n) + NT - 1) / NT, 1);
+    int64_t slots = 1;
+    while (slots < need) slots *= 2;
+    p->res_ok = slots <= kResMaxSlots && n >= 1;
+    if (p->res_ok) {
+      p->res_mr = (int32_t)slots;
+      p->res_mc = (int32_t)slots;
+      auto slices = [&](int64_t K, int64_t count, const std::vector<int32_t>& ptr,
+                        const std::vector<int32_t>& idx, const std::vector<T>& val,
+                        int32_t zero_slot, std::vector<int32_t>& map, std::vector<int32_t>& sl,
+                        std::vector<int32_t>& eidx, std::vector<T>& eval) {
+        std::vector<int32_t> order(count);
+        for (int64_t i = 0; i < count; ++i) order[i] = (int32_t)i;
+        std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
+          return ptr[a + 1] - ptr[a] > ptr[b + 1] - ptr[b];
+        });
+        map.assign(K, -1);
+        for (int64_t k = 0; k < count; ++k) map[k] = order[k];
+        const int64_t nslice = K / 64;
+        sl.assign(2 * nslice, 0);
+        for (int64_t z = 0; z < nslice; ++z) {
+          int32_t width = 0;
+          for (int l = 0; l < 64; ++l) {
+            const int32_t r = map[z * 64 + l];
+            if (r >= 0) width = std::max(width, ptr[r + 1] - ptr[r]);
+          }
+          sl[2 * z] = (int32_t)eidx.size();
+          sl[2 * z + 1] = width;
+          for (int32_t q = 0; q < width; ++q)
+            for (int l = 0; l < 64; ++l) {
+              const int32_t r = map[z * 64 + l];
+              const bool has = r >= 0 && q < ptr[r + 1] - ptr[r];
+              eidx.push_back(has ? idx[ptr[r] + q] : zero_slot);
+              eval.push_back(has ? val[ptr[r] + q] : T(0));
+            }
+        }
+      };
+      std::vector<int32_t> rmap, cmap, rsl, csl, ridxE, cidxE;
+      std::vector<T> rvalE, cvalE;
+      slices(p->res_mr * NT, m, H.ptr, H.idx, H.val_s, (int32_t)n, rmap, rsl, ridxE, rvalE);
+      slices(p->res_mc * NT, n, H.cptr, H.cidx, H.cval_s, (int32_t)m, cmap, csl, cidxE, cvalE);
+      auto upr = [&](void** dst, const void* src, size_t bytes) -> int {
+        if (bytes == 0) bytes = 16;
+        hipError_t e = hipMalloc(dst, bytes);
+        if (e != hipSuccess) return set_error(PURIN_CP_ERR_NOMEM, "plan hipMalloc failed");
+        p->owned.push_back(*dst);
+        if (src) {
+          e = hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice);
+          if (e != hipSuccess) return hip_check(e, "plan upload");
+        }
+        return PURIN_CP_OK;
+      };
+      int rc2;
+#define UPR(dst, vec) \
+  if ((rc2 = upr((void**)&(dst), (vec).empty() ? nullptr : (vec).data(), (vec).size() * sizeof((vec)[0]))) != PURIN_CP_OK) return rc2
+      UPR(p->res_rowmap, rmap);
+      UPR(p->res_colmap, cmap);
+      UPR(p->res_rslice, rsl);
+      UPR(p->res_cslice, csl);
+      UPR(p->res_ridx, ridxE);
+      UPR(p->res_rval, rvalE);
+      UPR(p->res_cidx, cidxE);
+      UPR(p->res_cval, cvalE);
+#undef UPR
+    }
+  }
   // --- upload -----------------------------------------------------------------
   auto up = [&](void** dst, const void* src, size_t bytes) -> int {
     *dst = nullptr;
@@ -283,6 +353,8 @@ void purin_cp_default_solve_options(purin_cp_solve_options* o) {
   o->check_every = 32;
   o->shared_bounds = 0;
   o->timing = 0;
+  o->streaming = 0;
+  o->reserved = 0;
 }
 
 void purin_cp_default_adjoint_options(purin_cp_adjoint_options* o) {
@@ -364,6 +436,7 @@ void purin_cp_plan_destroy(purin_cp_plan* p) {
   if (p->metric) (void)hipFree(p->metric);
   if (p->ws) (void)hipFree(p->ws);
   if (p->aws) (void)hipFree(p->aws);
+  if (p->res_sched) (void)hipFree(p->res_sched);
   if (p->pinned) (void)hipHostFree(p->pinned);
   delete p;
 }

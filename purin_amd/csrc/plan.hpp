@@ -14,6 +14,8 @@ constexpr int kRowsPerWaveFixed = 1;  // fixed-iteration passes: one row per wav
 constexpr int kRowsPerWaveEarly = 8;  // diagnostic passes: 8 rows/columns per wave
 constexpr int kSavedHeader = 256;     // bytes of the saved-state header
 constexpr int64_t kSavedMagic = 0x5055524e43503031LL;  // "PURNCP01"
+constexpr int kResThreads = 1024;   // threads of a resident workgroup
+constexpr int kResMaxSlots = 4;     // rows / columns per thread (n, m <= 4096)
 }  // namespace purin
 
 struct purin_cp_plan {
@@ -56,6 +58,22 @@ struct purin_cp_plan {
   void* aws = nullptr;        // adjoint workspace
   size_t aws_bytes = 0;
   int32_t* pinned = nullptr;  // host-pinned flag words
+
+  // resident (on-chip) iteration schedule: degree-sorted rows/columns in
+  // 64-lane sliced-ELL slices; built when n and m fit kResMaxSlots * kResThreads
+  bool res_ok = false;
+  int32_t res_mr = 0, res_mc = 0;    // row / column slots per thread
+  int32_t* res_rowmap = nullptr;     // Kr = mr * threads: kept row of each slot or -1
+  int32_t* res_colmap = nullptr;     // Kc = mc * threads: column of each slot or -1
+  int32_t* res_rslice = nullptr;     // per 64-slot slice: {offset, width}
+  int32_t* res_cslice = nullptr;
+  int32_t* res_ridx = nullptr;       // sliced ELL entries (lane fastest); padding
+                                     // points at the zero slot (column n / row m)
+  void* res_rval = nullptr;
+  int32_t* res_cidx = nullptr;
+  void* res_cval = nullptr;
+  void* res_sched = nullptr;         // per-iteration (sigma, a, delta, theta)
+  int64_t res_sched_len = 0;
 
   std::vector<void*> owned;   // device allocations freed with the plan
   purin_cp_timing timing{};   // last timed call

@@ -174,7 +174,7 @@ class Plan:
 
     def solve(self, rhs, target, lower, upper, *, dual0=None, tol=None, feasible=None,
               tolerance=1e-9, max_iterations=10000, early_stop=True, check_every=32,
-              shared_bounds=False, save=False):
+              shared_bounds=False, save=False, streaming=False, timing=False):
         """Inner CP solve on the kept rows (``purin_cp_solve``), scaled units."""
         batch = target.shape[0]
         target = self._tensor(target, (batch, self.n), "target")
@@ -192,6 +192,8 @@ class Plan:
         o.early_stop = int(bool(early_stop))
         o.check_every = int(check_every)
         o.shared_bounds = int(bool(shared_bounds))
+        o.streaming = int(bool(streaming))
+        o.timing = int(bool(timing))
         y = self._empty(batch, self.n)
         dual = self._empty(batch, self.m)
         it = self._empty(batch, dtype=torch.int32)
@@ -213,7 +215,8 @@ class Plan:
         return {k: getattr(t, k) for k, _ in _lib.Timing._fields_}
 
     def project(self, target, rhs, *, multipliers0=None, tolerance=1e-9, max_iterations=10000,
-                early_stop=True, check_every=32, shared_bounds=False, save=False, timing=False):
+                early_stop=True, check_every=32, shared_bounds=False, save=False, timing=False,
+                streaming=False):
         """Full projection (``purin_cp_project``): BoundProjection.solve semantics."""
         batch = target.shape[0]
         M = self.me + self.mi
@@ -228,6 +231,7 @@ class Plan:
         o.check_every = int(check_every)
         o.shared_bounds = int(bool(shared_bounds))
         o.timing = int(bool(timing))
+        o.streaming = int(bool(streaming))
         y = self._empty(batch, self.n)
         mult = self._empty(batch, M)
         slacks = self._empty(batch, self.mi)

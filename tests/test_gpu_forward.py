@@ -225,3 +225,36 @@ def test_invalid_arguments_raise():
         plan.project(np.zeros((2, 3)), np.zeros((2, 2)))
     with pytest.raises(PurinError):
         plan.project(np.zeros((1, 2)), np.zeros((1, 2)), max_iterations=0)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_resident_kernel_matches_streaming_and_oracle(dtype, accelerated):
+    """The on-chip resident kernel (fixed iterations) against the streaming passes and the oracle.
+
+    Sizes cover every slot count of the resident schedule (1, 2, 4, 8 per thread).
+    """
+    torch = require_gpu()
+    for n, me, mi, width, B in ((48, 8, 20, 4, 37), (700, 100, 300, 5, 64), (1500, 300, 700, 6, 40),
+                                (4096, 1024, 2048, 8, 16)):
+        w = workloads.small_random(7 + n, n=n, me=me, mi=mi, width=width, batch=B,
+                                   accelerated=accelerated)
+        canon = canonical_from_workload(w)
+        rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+        target = w.target.astype(dtype)
+        plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
+        iters = 150
+        res = plan.project(target, rhs, max_iterations=iters, early_stop=False, timing=True)
+        assert plan.last_timing()["resident"] == 1, n
+        st = plan.project(target, rhs, max_iterations=iters, early_stop=False, streaming=True,
+                          timing=True)
+        assert plan.last_timing()["resident"] == 0
+        bar = TOL[dtype]
+        assert rel_err(to_np(res.y), to_np(st.y)) <= bar / 10
+        assert rel_err(to_np(res.multipliers), to_np(st.multipliers)) <= bar
+        np.testing.assert_array_equal(to_np(res.status), to_np(st.status))
+        sub = slice(0, 6)
+        cfg = op.Config(accelerated=accelerated, max_iterations=iters, early_stop=False)
+        want = op.solve(canon, target[sub], rhs[sub], cfg, dtype=dtype)
+        assert rel_err(to_np(res.y)[sub], want.y) <= bar, n
+        np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
