@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Throughput of the MI355X Chambolle--Pock projection on one GPU.
 
-Workload ("config2"): n = 4096 variables, 1024
+Workload (the headline configuration, "config2"): n = 4096 variables, 1024
 equality + 2048 inequality rows of 8 random columns each, box bounds [-1, 1]
 as 8192 singleton rows (presolved), batch 1024, float64, accelerated CP,
 2000 fixed iterations.  One step = one ``purin_cp_project`` call on the whole
@@ -9,9 +9,11 @@ batch (bound presolve, 2000 CP iterations, final diagnostics, dual recovery,
 statuses), with the inputs already resident in device memory.
 
 Printed: one JSON line with the driver's fields plus
-  roofline      the dominant kernel (column pass) against HBM peak, from its
-                algorithmic bytes per launch and its average duration measured
-                with HIP events on the launch stream (instrumented replay);
+  roofline      the dominant kernel (the resident CP kernel; the column pass when
+                the streaming passes run) against HBM peak: its algorithmic bytes
+                per launch over its average duration, measured with HIP events
+                on the launch stream (instrumented replay), and its HBM traffic
+                from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
   cpu_baseline  the NumPy oracle on a bounded sample of the same workload.
 """
 
@@ -65,16 +67,34 @@ def cpu_baseline(w, samples, iterations):
     }
 
 
-def traffic_from_profiles(kernel):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
+def traffic_from_profiles(kernel, batch, iterations):
+    """HBM bytes per dispatch of ``kernel`` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE runs, calibrated against a plain copy), or None when
+    the summary is absent or was taken on another workload size."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                         "traffic_config2.json")
     try:
         with open(path) as f:
             data = json.load(f)
-        return data.get(kernel)
     except (OSError, ValueError):
         return None
+    wl = data.get("workload", {})
+    if wl.get("batch") != batch or wl.get("iterations") != iterations:
+        return None
+    return data.get("hbm_bytes_per_dispatch", {}).get(kernel)
+
+
+def copy_calibration(torch, mib):
+    """A plain copy of known size: its counter readings per dispatch, divided by
+    ``mib`` MiB read and written, are the scale factors for FETCH_SIZE / WRITE_SIZE."""
+    n = mib * (1 << 20) // 8
+    src = torch.ones(n, dtype=torch.float64, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n * 8, "dispatches": 3}), flush=True)
 
 
 def main():
@@ -85,8 +105,13 @@ def main():
     ap.add_argument("--batch", type=int, default=1024)
     ap.add_argument("--iterations", type=int, default=2000)
     ap.add_argument("--cpu-samples", type=int, default=64)
-    ap.add_argument("--cpu-iterations", type=int, default=150)
+    ap.add_argument("--cpu-iterations", type=int, default=500)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-streaming", action="store_true",
+                    help="skip the streaming two-pass comparison run")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run a plain device-to-device copy of this many MiB (3 times); "
+                         "its FETCH_SIZE / WRITE_SIZE counters calibrate the traffic figures")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the batch shards across GPUs "
@@ -94,6 +119,10 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration_mib:
+        copy_calibration(torch, args.copy_calibration_mib)
+        return
 
     from purin_amd import workloads
     from purin_amd.plan import Plan
@@ -144,15 +173,17 @@ def main():
         dominant = "k_col_pass" if col_ms >= row_ms else "k_row_pass"
         dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == "k_col_pass" else (bytes_row, row_ms)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
-    traffic = traffic_from_profiles(dominant)
+    traffic = traffic_from_profiles(dominant, B, args.iterations)
     # the streaming two-pass path on the same inputs, for comparison
-    e2 = torch.cuda.Event(enable_timing=True)
-    e3 = torch.cuda.Event(enable_timing=True)
-    e2.record(stream)
-    plan.project(target, rhs, streaming=True, **kw)
-    e3.record(stream)
-    torch.cuda.synchronize()
-    streaming_ms = e2.elapsed_time(e3)
+    streaming_ms = None
+    if not args.no_streaming:
+        e2 = torch.cuda.Event(enable_timing=True)
+        e3 = torch.cuda.Event(enable_timing=True)
+        e2.record(stream)
+        plan.project(target, rhs, streaming=True, **kw)
+        e3.record(stream)
+        torch.cuda.synchronize()
+        streaming_ms = e2.elapsed_time(e3)
     line = {
         "metric": "CP projections/sec (n=4096, batch 1024, fp64) + achieved HBM GB/s % of peak",
         "value": value,

@@ -19,7 +19,7 @@ ARCH = os.environ.get("PURIN_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
-    # packed-fp32 instructions stay off (build notes)
+    # no packed-fp32 (v_pk_*_f32) instructions in the generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
