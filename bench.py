@@ -1,12 +1,15 @@
 #!/usr/bin/env python3
 """Throughput of the MI355X Chambolle--Pock projection on one GPU.
 
-Workload (the headline configuration, "config2"): n = 4096 variables, 1024
-equality + 2048 inequality rows of 8 random columns each, box bounds [-1, 1]
-as 8192 singleton rows (presolved), batch 1024, float64, accelerated CP,
-2000 fixed iterations.  One step = one ``purin_cp_project`` call on the whole
-batch (bound presolve, 2000 CP iterations, final diagnostics, dual recovery,
-statuses), with the inputs already resident in device memory.
+Default workload (the headline configuration, "config2"): n = 4096 variables,
+1024 equality + 2048 inequality rows of 8 random columns each, box bounds
+[-1, 1] as 8192 singleton rows (presolved), batch 1024, float64, accelerated
+CP, 2000 fixed iterations.  One step = one ``purin_cp_project`` call on the
+whole batch (bound presolve, 2000 CP iterations, final diagnostics, dual
+recovery, statuses), with the inputs already resident in device memory.
+``--config 3`` / ``--config 4`` measure the network-flow WeightedDistance
+(fp64, B=256, 3000 iterations) and high-batch fp32 (B=65536, 500 iterations)
+configurations the same way.
 
 Printed: one JSON line with the driver's fields plus
   roofline      the dominant kernel (the resident CP kernel; the column pass when
@@ -14,7 +17,13 @@ Printed: one JSON line with the driver's fields plus
                 per launch over its average duration, measured with HIP events
                 on the launch stream (instrumented replay), and its HBM traffic
                 from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
-  cpu_baseline  the NumPy oracle on a bounded sample of the same workload.
+  adjoint       (config2) the implicit VJP w.r.t. the candidates and b, h
+                (``purin_cp_adjoint``, cotangents N(0,1) from seed 5) at the
+                2000-iteration state with eligibility forced on, timed separately
+                from the forward;
+  cpu_baseline  the checker's C restatement of the CP loop (bit-equal to the NumPy
+                oracle) on a bounded sample of the same workload, all cores
+                (``value``) and one core (``one_core``).
 """
 
 from __future__ import annotations
@@ -30,6 +39,13 @@ import numpy as np
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 
+METRICS = {
+    2: "CP projections/sec (n=4096, batch 1024, fp64) + achieved HBM GB/s % of peak",
+    3: "CP projections/sec (network flow n=40000 edges, 10000 nodes, batch 256, fp64, "
+       "WeightedDistance) + achieved HBM GB/s % of peak",
+    4: "CP projections/sec (n=1024, batch 65536, fp32) + achieved HBM GB/s % of peak",
+}
+
 
 def _cpu_model():
     try:
@@ -42,37 +58,59 @@ def _cpu_model():
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(w, samples, iterations):
-    """NumPy oracle on the first ``samples`` samples for ``iterations`` CP iterations."""
+def weighted_values(w):
+    """CSR values with the metric change of variables (coefficients times 1/sqrt(D_j))."""
+    if w.metric is None:
+        return w.data, None
+    root = np.sqrt(np.asarray(w.metric, np.float64))
+    return w.data / root[w.indices], root
+
+
+def cpu_baseline(w, samples_one, samples_all):
+    """The C restatement of the CP loop (oracle/cp_loop.c, bit-equal to the NumPy
+    oracle) at the full iteration count: ``samples_one`` samples on one core, then
+    ``samples_all`` samples on every core this process may use (at most 16)."""
+    from oracle import cloop
     from oracle import projection as op
 
-    canon = op.Canonical(n=w.n, me=w.me, rows=w.rows(), coef=w.coefs())
-    target = np.asarray(w.target[:samples], np.float64)
-    rhs = np.tile(w.rhs, (samples, 1))
-    cfg = op.Config(accelerated=w.accelerated, max_iterations=iterations, early_stop=False)
-    t0 = time.perf_counter()
-    op.solve(canon, target, rhs, cfg)
-    dt = time.perf_counter() - t0
-    # projections/s at the full iteration count: the loop dominates and scales linearly
-    per_projection = dt / samples * (w.iterations / iterations)
+    values, root = weighted_values(w)
+    rows = [list(w.indices[w.indptr[i]:w.indptr[i + 1]]) for i in range(w.rows_total)]
+    coef = [list(values[w.indptr[i]:w.indptr[i + 1]]) for i in range(w.rows_total)]
+    canon = op.Canonical(n=w.n, me=w.me, rows=rows, coef=coef)
+    cfg = op.Config(accelerated=w.accelerated, max_iterations=w.iterations, early_stop=False)
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+
+    def leg(samples, threads):
+        target = np.asarray(w.target[:samples], w.dtype)
+        if root is not None:
+            target = target * root.astype(w.dtype)
+        rhs = np.tile(w.rhs, (samples, 1)).astype(w.dtype)
+        prep = cloop.prepare(canon, target, rhs, cfg, w.dtype)
+        _, _, seconds = cloop.run(prep, w.iterations, w.accelerated, threads=threads)
+        return samples / seconds, seconds
+
+    one, t_one = leg(samples_one, 1)
+    full, t_full = leg(samples_all, cores)
     return {
-        "value": 1.0 / per_projection,
+        "value": full,
         "unit": "projections/s",
-        "cores": 1,
+        "cores": cores,
         "kind": "port",
-        "sample": (f"NumPy/scipy oracle (oracle/projection.py), first {samples} samples x "
-                   f"{iterations} of {w.iterations} iterations, scaled linearly to "
-                   f"{w.iterations}; {dt:.1f} s on {_cpu_model()} "
-                   f"(affinity {len(os.sched_getaffinity(0))} cores, 1 used)"),
+        "sample": (f"C restatement of the CP loop (oracle/cp_loop.c, OpenMP over samples; "
+                   f"set-up by the NumPy oracle, untimed), {w.iterations} iterations: "
+                   f"{samples_all} samples on {cores} threads in {t_full:.1f} s; "
+                   f"{samples_one} samples on 1 thread in {t_one:.1f} s = {one:.2f} "
+                   f"projections/s; {_cpu_model()}"),
+        "one_core": one,
     }
 
 
-def traffic_from_profiles(kernel, batch, iterations):
+def traffic_from_profiles(config, kernel, batch, iterations):
     """HBM bytes per dispatch of ``kernel`` from the committed rocprofv3 PMC summary
     (FETCH_SIZE and WRITE_SIZE runs, calibrated against a plain copy), or None when
     the summary is absent or was taken on another workload size."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "traffic_config2.json")
+                        f"traffic_config{config}.json")
     try:
         with open(path) as f:
             data = json.load(f)
@@ -97,16 +135,45 @@ def copy_calibration(torch, mib):
     print(json.dumps({"copy_calibration_bytes": n * 8, "dispatches": 3}), flush=True)
 
 
+def adjoint_bytes(batch, ws, width, steps, restart):
+    """Algorithmic bytes of the batched GMRES: B*ws*(k+2)*W for Arnoldi step k of a
+    cycle (read v_k and the k-vector prefix once, write the new vector) plus
+    B*ws*38*W per cycle for its set-up and finish."""
+    total, done = 0, 0
+    while done < steps:
+        length = min(restart, steps - done)
+        total += sum(k + 2 for k in range(1, length + 1)) + 38
+        done += length
+    return batch * ws * width * total
+
+
+def time_calls(torch, fn, count):
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(count):
+        out = fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / count, out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--batch", type=int, default=1024)
-    ap.add_argument("--iterations", type=int, default=2000)
-    ap.add_argument("--cpu-samples", type=int, default=64)
-    ap.add_argument("--cpu-iterations", type=int, default=500)
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
+    ap.add_argument("--batch", type=int, default=None)
+    ap.add_argument("--iterations", type=int, default=None)
+    ap.add_argument("--cpu-samples", type=int, default=None,
+                    help="samples of the all-core CPU baseline leg")
+    ap.add_argument("--cpu-samples-one", type=int, default=None,
+                    help="samples of the one-core CPU baseline leg")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-adjoint", action="store_true", help="skip the adjoint leg (config2)")
     ap.add_argument("--no-streaming", action="store_true",
                     help="skip the streaming two-pass comparison run")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -127,30 +194,28 @@ def main():
     from purin_amd import workloads
     from purin_amd.plan import Plan
 
-    w = workloads.config2(args.batch)
-    w.iterations = args.iterations
+    make = {2: workloads.config2, 3: workloads.config3, 4: workloads.config4}[args.config]
+    w = make(args.batch) if args.batch else make()
+    if args.iterations:
+        w.iterations = args.iterations
     B, n = w.target.shape
-    plan = Plan(w.n, w.me, w.rows_total - w.me, w.indptr, w.indices, w.data,
-                dtype=torch.float64, accelerated=True, device="cuda:0")
+    tdtype = torch.float64 if w.dtype == np.float64 else torch.float32
+    ws = np.dtype(w.dtype).itemsize
+    values, root = weighted_values(w)
+    plan = Plan(w.n, w.me, w.rows_total - w.me, w.indptr, w.indices, values,
+                dtype=tdtype, accelerated=w.accelerated, device="cuda:0")
+    if root is not None:
+        plan.set_metric(root)
     m = plan.m
     dev = torch.device("cuda:0")
     target = torch.as_tensor(w.target, device=dev)
-    rhs = torch.as_tensor(np.tile(w.rhs, (B, 1)), device=dev)
-    kw = dict(max_iterations=args.iterations, early_stop=False, shared_bounds=True)
+    rhs = torch.as_tensor(np.tile(w.rhs, (B, 1)).astype(w.dtype), device=dev)
+    kw = dict(max_iterations=w.iterations, early_stop=False, shared_bounds=True)
+    adjoint_leg = args.config == 2 and not args.no_adjoint
 
     for _ in range(args.warmup):
         plan.project(target, rhs, **kw)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(args.steps):
-        out = plan.project(target, rhs, **kw)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_per_step = e0.elapsed_time(e1) / args.steps
+    ms_per_step, out = time_calls(torch, lambda: plan.project(target, rhs, **kw), args.steps)
     value = B / (ms_per_step / 1e3)
     status = out.status.cpu().numpy()
 
@@ -159,7 +224,6 @@ def main():
     torch.cuda.synchronize()
     tm = plan.last_timing()
     iters = max(int(tm["iterations"]), 1)
-    ws = 8
     bytes_row = B * ws * (n + 3 * m)        # gather ybar (n), read d, r (2m), write d (m)
     bytes_col = B * ws * (4 * n + m)        # gather d+ (m), read y, yhat (2n), write y, ybar (2n)
     bytes_iter = B * ws * (5 * n + 3 * m)   # the per-iteration contract figure
@@ -173,19 +237,15 @@ def main():
         dominant = "k_col_pass" if col_ms >= row_ms else "k_row_pass"
         dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == "k_col_pass" else (bytes_row, row_ms)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
-    traffic = traffic_from_profiles(dominant, B, args.iterations)
+    traffic = traffic_from_profiles(args.config, dominant, B, w.iterations)
     # the streaming two-pass path on the same inputs, for comparison
     streaming_ms = None
-    if not args.no_streaming:
-        e2 = torch.cuda.Event(enable_timing=True)
-        e3 = torch.cuda.Event(enable_timing=True)
-        e2.record(stream)
-        plan.project(target, rhs, streaming=True, **kw)
-        e3.record(stream)
-        torch.cuda.synchronize()
-        streaming_ms = e2.elapsed_time(e3)
+    if tm["resident"] and not args.no_streaming:
+        streaming_ms, _ = time_calls(
+            torch, lambda: plan.project(target, rhs, streaming=True, **kw), 1)
+
     line = {
-        "metric": "CP projections/sec (n=4096, batch 1024, fp64) + achieved HBM GB/s % of peak",
+        "metric": METRICS[args.config],
         "value": value,
         "unit": "projections/s",
         "n_gpus": 1,
@@ -195,13 +255,20 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64",
-        "data": "synthetic (config2 generator, numpy default_rng seed 2)",
+        "dtype": "f64" if ws == 8 else "f32",
+        "data": f"synthetic ({w.name} generator, numpy default_rng seed {args.config})",
         "config": {
-            "workload": "config2: n=4096, 1024 eq + 2048 ineq rows x 8 cols, 8192 bound rows, "
-                        "batch 1024, fp64, accelerated CP, fixed iterations, full projection",
+            "workload": {
+                2: "config2: n=4096, 1024 eq + 2048 ineq rows x 8 cols, 8192 bound rows, "
+                   "batch 1024, fp64, accelerated CP, fixed iterations, full projection",
+                3: "config3: node-edge incidence of 10000 nodes x 40000 edges (eq rows), "
+                   "edge bounds [0, U(1,5)], WeightedDistance D~U(0.5,2), batch 256, fp64, "
+                   "fixed-step CP, fixed iterations, full projection",
+                4: "config4: n=1024, 256 eq + 512 ineq rows x 16 cols, bounds [-2,2], "
+                   "batch 65536, fp32, accelerated CP, fixed iterations, full projection",
+            }[args.config],
             "n": n, "kept_rows": m, "bound_rows": int(plan.info.bound_rows),
-            "nnz_kept": int(plan.info.nnz_kept), "batch": B, "iterations": args.iterations,
+            "nnz_kept": int(plan.info.nnz_kept), "batch": B, "iterations": w.iterations,
             "parallelism": "1 GPU (batch-parallel)",
         },
         "roofline": {
@@ -216,7 +283,7 @@ def main():
             "avg_launch_ms": dom_ms,
         },
         "iteration": {
-            "cp_iterations_per_s": args.iterations * 1e3 / ms_per_step,
+            "cp_iterations_per_s": w.iterations * 1e3 / ms_per_step,
             "resident_kernel": bool(tm["resident"]),
             "streaming_passes_ms_per_step": streaming_ms,
             "row_pass_ms": row_ms,
@@ -228,8 +295,37 @@ def main():
         },
         "statuses": {str(k): int(v) for k, v in zip(*np.unique(status, return_counts=True))},
     }
+
+    if adjoint_leg:
+        cot = torch.as_tensor(np.random.default_rng(5).normal(0.0, 1.0, (B, n)), device=dev)
+        fwd = plan.project(target, rhs, save=True, **kw)
+        adj = dict(force_eligible=True)
+        plan.adjoint(fwd.saved, None, None, cot, **adj)       # warmup
+        adj_ms, res = time_calls(torch, lambda: plan.adjoint(fwd.saved, None, None, cot, **adj),
+                                 max(1, min(args.steps, 3)))
+        stats = plan.last_adjoint_stats()
+        width = 2 * n + m
+        abytes = adjoint_bytes(B, ws, width, stats["arnoldi_steps"], 30)
+        info = res.info.cpu().numpy()
+        line["adjoint"] = {
+            "workload": "config5: VJP w.r.t. y_hat and (b, h) on the config2 problem, cotangent "
+                        "N(0,1) seed 5, GMRES restart 30, max 100, tol 1e-9, at the "
+                        f"{w.iterations}-iteration state with gradient eligibility forced on",
+            "ms_per_vjp_batch": adj_ms,
+            "vjps_per_s": B / (adj_ms / 1e3),
+            "arnoldi_steps": stats["arnoldi_steps"],
+            "cycles": stats["cycles"],
+            "gmres_info": {str(k): int(v) for k, v in zip(*np.unique(info, return_counts=True))},
+            "algorithmic_bytes": abytes,
+            "achieved_GBs": abytes / (adj_ms / 1e3) / 1e9,
+            "frac_of_hbm_peak": abytes / (adj_ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+        }
+
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(w, args.cpu_samples, args.cpu_iterations)
+        default_sample = {2: (64, 512), 3: (4, 64), 4: (256, 4096)}[args.config]
+        one = args.cpu_samples_one or default_sample[0]
+        full = args.cpu_samples or default_sample[1]
+        line["cpu_baseline"] = cpu_baseline(w, min(one, B), min(full, B))
     print(json.dumps(line), flush=True)
 
 

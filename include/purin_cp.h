@@ -239,6 +239,18 @@ int purin_cp_adjoint(purin_cp_plan* plan, void* stream, int64_t batch, const voi
                      void* g_lower, void* g_upper, uint8_t* valid, int32_t* info,
                      void* gmres_residual);
 
+/* Work done by the last adjoint() call on this plan.  No reference counterpart
+ * (the reference's GMRES returns only per-sample info codes); it reports how
+ * many batched Arnoldi steps ran, which sets the adjoint's algorithmic bytes. */
+typedef struct {
+  int64_t arnoldi_steps;  /* Arnoldi steps run over all restart cycles (the batch
+                             steps together until its last active sample stops) */
+  int32_t cycles;         /* restart cycles started */
+  int32_t reserved;
+} purin_cp_adjoint_stats;
+
+int purin_cp_last_adjoint_stats(const purin_cp_plan* plan, purin_cp_adjoint_stats* stats);
+
 /* Message of the calling thread's last error ("" if none). */
 const char* purin_cp_last_error(void);
 

@@ -28,6 +28,7 @@ SYMBOLS = (
     "purin_cp_default_solve_options",
     "purin_cp_saved_bytes",
     "purin_cp_last_timing",
+    "purin_cp_last_adjoint_stats",
     "purin_cp_solve",
     "purin_cp_project",
     "purin_cp_default_adjoint_options",
@@ -83,6 +84,10 @@ class Timing(C.Structure):
         ("resident", C.c_int32),
         ("reserved", C.c_int32),
     ]
+
+
+class AdjointStats(C.Structure):
+    _fields_ = [("arnoldi_steps", C.c_int64), ("cycles", C.c_int32), ("reserved", C.c_int32)]
 
 
 class AdjointOptions(C.Structure):
@@ -147,6 +152,8 @@ def load(path: str = LIB_PATH):
     lib.purin_cp_project.restype = C.c_int
     lib.purin_cp_last_timing.argtypes = [vp, C.POINTER(Timing)]
     lib.purin_cp_last_timing.restype = C.c_int
+    lib.purin_cp_last_adjoint_stats.argtypes = [vp, C.POINTER(AdjointStats)]
+    lib.purin_cp_last_adjoint_stats.restype = C.c_int
     lib.purin_cp_default_adjoint_options.argtypes = [C.POINTER(AdjointOptions)]
     lib.purin_cp_default_adjoint_options.restype = None
     lib.purin_cp_adjoint.argtypes = [vp, vp, i64, vp, vp, vp, vp, C.POINTER(AdjointOptions), vp,

@@ -717,6 +717,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   PURIN_HIP(hipMemcpyAsync(Rr, Gr, vec, hipMemcpyDeviceToDevice, st));  // r = g - A(0)
 
   int64_t completed = 0;
+  p->adjoint_stats = purin_cp_adjoint_stats{};
   while (completed < o.max_iterations) {
     zero_counters();
     k_gm_count_unconverged<T><<<sb, 256, 0, st>>>(G);
@@ -724,6 +725,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     if (int rc = read_counter(1, &unconverged)) return rc;
     if (unconverged == 0) break;
     const int cycle_limit = (int)std::min<int64_t>(restart, o.max_iterations - completed);
+    ++p->adjoint_stats.cycles;
     // beta = ||r||, V0 = r / max(beta, eps)
     k_gs<T, 3><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Rr, nullptr, W, Bp, part, nchunk);
     reduce(1, S1, 0);
@@ -760,6 +762,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     reduce(1, S1, 1);
     k_gm_cycle_end<T><<<sb, 256, 0, st>>>(G, S1);
     completed += it;
+    p->adjoint_stats.arnoldi_steps += it;
   }
   // finiteness of the solution, info, valid (operators.py:1119-1122, bounds.py:148-153)
   k_gs<T, 2><<<ggs, kBlock, 0, st>>>(Vb, vstride, 0, X, nullptr, W, Bp, part, nchunk);

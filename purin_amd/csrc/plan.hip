@@ -466,6 +466,12 @@ int purin_cp_last_timing(const purin_cp_plan* p, purin_cp_timing* t) {
   return PURIN_CP_OK;
 }
 
+int purin_cp_last_adjoint_stats(const purin_cp_plan* p, purin_cp_adjoint_stats* s) {
+  if (!p || !s) return set_error(PURIN_CP_ERR_ARG, "NULL argument");
+  *s = p->adjoint_stats;
+  return PURIN_CP_OK;
+}
+
 int purin_cp_plan_kept_rows(const purin_cp_plan* p, int64_t* rows, double* scale) {
   if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
   for (int64_t i = 0; i < p->m; ++i) {

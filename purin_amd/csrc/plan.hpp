@@ -77,6 +77,7 @@ struct purin_cp_plan {
 
   std::vector<void*> owned;   // device allocations freed with the plan
   purin_cp_timing timing{};   // last timed call
+  purin_cp_adjoint_stats adjoint_stats{};  // last adjoint call
 };
 
 namespace purin {

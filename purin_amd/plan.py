@@ -214,6 +214,12 @@ class Plan:
         _lib.check(self.lib.purin_cp_last_timing(self.handle, C.byref(t)))
         return {k: getattr(t, k) for k, _ in _lib.Timing._fields_}
 
+    def last_adjoint_stats(self):
+        """Arnoldi steps and restart cycles of the last ``adjoint`` call."""
+        s = _lib.AdjointStats()
+        _lib.check(self.lib.purin_cp_last_adjoint_stats(self.handle, C.byref(s)))
+        return {"arnoldi_steps": int(s.arnoldi_steps), "cycles": int(s.cycles)}
+
     def project(self, target, rhs, *, multipliers0=None, tolerance=1e-9, max_iterations=10000,
                 early_stop=True, check_every=32, shared_bounds=False, save=False, timing=False,
                 streaming=False):
