@@ -286,6 +286,206 @@ __global__ void k_reduce(const T* __restrict__ part, int nv, int nchunk, int64_t
   out[e] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// Classical Gram--Schmidt passes over the basis prefix for nv <= NV vectors.
+//
+// A block of 4 wavefronts owns one batch tile (64 lanes x 16 bytes of samples)
+// and a contiguous range of ``rpb`` rows; each wavefront walks a quarter of it.
+// Per row a lane loads x and the prefix vectors' entries of the same row, so
+// every load is a coalesced 1 KB wavefront access and nv of them are in flight
+// per row.  Dot products accumulate in registers (one accumulator per prefix
+// vector) and are combined across the 4 wavefronts once, at the end, into
+// part[i][chunk][b].  The coefficients h (MODE 1, 2) are
+// staged in LDS once per block.
+//   MODE 0: part_i = V_i . x
+//   MODE 1: x <- x - sum_i h_i V_i;  part_i = V_i . x
+//   MODE 2: x <- x - sum_i h_i V_i;  part_0 = x . x, part_1 = finite(x)
+// The update forms sum_i h_i V_i first and subtracts it once, like the
+// reference's einsum (operators.py:845-858).
+// ---------------------------------------------------------------------------
+template <typename T, int NV, int MODE>
+__global__ __launch_bounds__(kBlock) void k_gs_pass(const T* __restrict__ basis, int64_t vstride,
+                                                    int nv, T* x, const T* __restrict__ h,
+                                                    int64_t W, int64_t Bp, T* part, int nchunk,
+                                                    int64_t rpb) {
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  const int c = blockIdx.y;
+  auto ld = [](const T* p) { return vload(p); };
+  auto st = [](T* p, V v) { vstore(p, v); };
+  __shared__ V hs[(MODE == 0) ? 1 : NV][kWave];
+  __shared__ V cb[3][kWave];
+  if (MODE != 0) {
+    for (int i = wave; i < nv; i += 4) hs[i][lane] = ld(h + (size_t)i * Bp + b0);
+    __syncthreads();
+  }
+  const int64_t rpw = (rpb + 3) / 4;
+  const int64_t r_begin = (int64_t)c * rpb + wave * rpw;
+  const int64_t r_end = std::min<int64_t>(W, std::min<int64_t>((int64_t)(c + 1) * rpb, r_begin + rpw));
+  V acc[MODE == 2 ? 1 : NV];
+#pragma unroll
+  for (int i = 0; i < (MODE == 2 ? 1 : NV); ++i) acc[i] = V(T(0));
+  V nrm = V(T(0)), fin = V(T(1));
+  for (int64_t r = r_begin; r < r_end; ++r) {
+    const size_t off = (size_t)r * Bp + b0;
+    V xr = ld(x + off);
+    if (MODE != 0) {
+      V sum = V(T(0));
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (i < nv) sum += hs[i][lane] * ld(basis + (size_t)i * vstride + off);
+      xr = xr - sum;
+      st(x + off, xr);
+    }
+    if (MODE == 2) {
+      nrm += xr * xr;
+#pragma unroll
+      for (int q = 0; q < Sn; ++q)
+        if (!finite(xr[q])) fin[q] = T(0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (i < nv) acc[i] += ld(basis + (size_t)i * vstride + off) * xr;
+    }
+  }
+  // combine the 4 wavefronts (fixed order: wave 0 + 1 + 2 + 3)
+  const size_t plane = (size_t)nchunk * Bp;
+  const size_t pout = (size_t)c * Bp + b0;
+  auto combine = [&](V v, T* dst, int op) {
+    if (wave > 0) cb[wave - 1][lane] = v;
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int w = 0; w < 3; ++w) {
+        const V o = cb[w][lane];
+        if (op == 0) {
+          v += o;
+        } else {
+#pragma unroll
+          for (int q = 0; q < Sn; ++q) v[q] = minp(v[q], o[q]);
+        }
+      }
+      st(dst, v);
+    }
+    __syncthreads();
+  };
+  if (MODE == 2) {
+    combine(nrm, part + pout, 0);
+    combine(fin, part + plane + pout, 1);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (i < nv) combine(acc[MODE == 2 ? 0 : i], part + (size_t)i * plane + pout, 0);
+  }
+}
+
+// The second Gram--Schmidt pass (x <- x - sum_i h_i V_i, then part_i = V_i . x)
+// with the prefix vectors split across the block's 4 wavefronts instead of
+// the rows: wavefront w holds V_i for i = w, w+4, ... of two rows at a time
+// (at most NV/4 per wavefront, so registers stay low), forms its share of
+// sum_i h_i V_i, and the 4 shares meet in LDS (one barrier per 2 rows, double
+// buffered).  Every wavefront then has the updated rows and dots them with
+// the prefix entries it already holds: V is read from HBM once.  Each
+// wavefront owns the dot products of its own vectors, so the partials need no
+// cross-wavefront combine.  Shares are summed in wavefront order 0+1+2+3.
+template <typename T, int NV>
+__global__ __launch_bounds__(kBlock) void k_gs_update_dots(const T* __restrict__ basis,
+                                                           int64_t vstride, int nv, T* x,
+                                                           const T* __restrict__ h, int64_t W,
+                                                           int64_t Bp, T* part, int nchunk,
+                                                           int64_t rpb) {
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  constexpr int NW = NV / 4;  // vectors per wavefront
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  const int c = blockIdx.y;
+  __shared__ V share[2][4][2][kWave];
+  V hw[NW], acc[NW];
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    const int i = wave + 4 * j;
+    hw[j] = i < nv ? vload(h + (size_t)i * Bp + b0) : vsplat<T>(T(0));
+    acc[j] = vsplat<T>(T(0));
+  }
+  const int64_t r_begin = (int64_t)c * rpb;
+  const int64_t r_end = std::min<int64_t>(W, r_begin + rpb);
+  int g = 0;
+  for (int64_t r = r_begin; r < r_end; r += 2, ++g) {
+    const bool two = r + 1 < r_end;
+    const size_t off0 = (size_t)r * Bp + b0, off1 = off0 + (size_t)Bp;
+    const V x0 = vload(x + off0);
+    const V x1 = two ? vload(x + off1) : vsplat<T>(T(0));
+    V v0[NW], v1[NW];
+    V p0 = vsplat<T>(T(0)), p1 = vsplat<T>(T(0));
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      const int i = wave + 4 * j;
+      v0[j] = vsplat<T>(T(0));
+      v1[j] = vsplat<T>(T(0));
+      if (i < nv) {
+        v0[j] = vload(basis + (size_t)i * vstride + off0);
+        if (two) v1[j] = vload(basis + (size_t)i * vstride + off1);
+      }
+      p0 += hw[j] * v0[j];
+      p1 += hw[j] * v1[j];
+    }
+    share[g & 1][wave][0][lane] = p0;
+    share[g & 1][wave][1][lane] = p1;
+    __syncthreads();
+    const V s0 = ((share[g & 1][0][0][lane] + share[g & 1][1][0][lane]) + share[g & 1][2][0][lane]) +
+                 share[g & 1][3][0][lane];
+    const V s1 = ((share[g & 1][0][1][lane] + share[g & 1][1][1][lane]) + share[g & 1][2][1][lane]) +
+                 share[g & 1][3][1][lane];
+    const V y0 = x0 - s0, y1 = x1 - s1;
+    if (wave == 0) {
+      vstore(x + off0, y0);
+      if (two) vstore(x + off1, y1);
+    }
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      acc[j] += v0[j] * y0;
+      acc[j] += v1[j] * y1;
+    }
+  }
+  const size_t plane = (size_t)nchunk * Bp;
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    const int i = wave + 4 * j;
+    if (i < nv) vstore(part + (size_t)i * plane + (size_t)c * Bp + b0, acc[j]);
+  }
+}
+
+// out[i][b] = reduce_c part[i][c][b] for c < nchunk: 4 thread groups take
+// chunks c = g mod 4 in increasing order, then groups combine 0+1+2+3.
+// op 0 = sum, 2 = min.  grid (Bp / 64, nv), block 256.
+template <typename T>
+__global__ __launch_bounds__(256) void k_reduce_chunks(const T* __restrict__ part, int nchunk,
+                                                       int64_t Bp, T* out, int op) {
+  __shared__ T buf[3][64];
+  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t b = (int64_t)blockIdx.x * 64 + lane;
+  const int i = blockIdx.y;
+  const T* p = part + (size_t)i * nchunk * Bp + b;
+  T acc = op == 0 ? T(0) : T(1);
+  bool first = true;
+  for (int c = g; c < nchunk; c += 4) {
+    const T v = p[(size_t)c * Bp];
+    acc = first ? v : (op == 0 ? acc + v : minp(acc, v));
+    first = false;
+  }
+  if (g > 0) buf[g - 1][lane] = acc;
+  __syncthreads();
+  if (g == 0) {
+    for (int w = 0; w < 3 && w + 1 < nchunk; ++w) acc = op == 0 ? acc + buf[w][lane] : minp(acc, buf[w][lane]);
+    out[(size_t)i * Bp + b] = acc;
+  }
+}
+
 // elementwise helpers on W x Bp vectors
 template <typename T>
 __global__ void k_axpby(int64_t total, T* out, const T* __restrict__ a, const T* __restrict__ b,
@@ -628,6 +828,19 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
 
   // workspace
   const int nchunk = (int)((W + kChunk - 1) / kChunk);
+  // Gram--Schmidt passes: about 1024 blocks of 4 wavefronts over the batch tiles
+  const int64_t TS0 = (int64_t)kWave * Lane<T>::S;
+  const int64_t tiles0 = Bp / TS0;
+  // at most 8 resident blocks of 4 wavefronts per CU: the partial sums need at
+  // most that many chunks per batch tile
+  int cus = 0;
+  {
+    int dev = 0;
+    PURIN_HIP(hipGetDevice(&dev));
+    PURIN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  }
+  const int nchunk2 = (int)std::max<int64_t>(
+      1, std::min<int64_t>(((int64_t)8 * cus + tiles0 - 1) / tiles0, (W + 3) / 4));
   const size_t es = sizeof(T);
   const size_t vec = (size_t)W * Bp * es;
   size_t o_ = 0;
@@ -636,7 +849,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                oT1 = take(vec), oCm = take(n * Bp * es), oClo = take(n * Bp * es),
                oChi = take(n * Bp * es), oDm = take(m * Bp * es), oDp = take(m * Bp * es),
                oU = take(n * Bp * es), oWv = take(m * Bp * es),
-               oPart = take((size_t)(restart + 1) * nchunk * Bp * es),
+               oPart = take((size_t)(restart + 1) * std::max(nchunk, nchunk2) * Bp * es),
                oH1 = take((size_t)(restart + 1) * Bp * es), oH2 = take((size_t)(restart + 1) * Bp * es),
                oS1 = take(Bp * es), oS2 = take(Bp * es), oThr = take(Bp * es), oRinf = take(Bp * es),
                oCyc = take(Bp * 4), oAct = take(Bp * 4), oSteps = take(Bp * 4), oKeep = take(Bp * 4),
@@ -705,6 +918,50 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     return PURIN_CP_OK;
   };
   auto zero_counters = [&]() { k_fill<int32_t><<<1, 64, 0, st>>>(G.counter, 2, 0); };
+  // one round of resident blocks per pass: the chunk count per batch tile is the
+  // kernel's resident block count over the tiles (so no partial second round)
+  int last_nchunk = 1;
+  auto launch_gs = [&](auto kern, int nv, T* img, const T* h) -> int {
+    int per_cu = 0;
+    PURIN_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kBlock, 0));
+    const int64_t chunks = std::max<int64_t>(
+        1, std::min<int64_t>({(int64_t)std::max(per_cu, 1) * cus / tiles0, (W + 3) / 4,
+                              (int64_t)nchunk2}));
+    const int64_t rpb = (W + chunks - 1) / chunks;
+    last_nchunk = (int)chunks;
+    kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, vstride, nv, img, h, W, Bp,
+                                                                    part, (int)chunks, rpb);
+    return PURIN_CP_OK;
+  };
+  auto gs_pass = [&](int mode, int nv, T* img, const T* h) -> int {
+#define PURIN_GS(MODE, NVB) return launch_gs(k_gs_pass<T, NVB, MODE>, nv, img, h)
+    const int bucket = nv <= 8 ? 8 : (nv <= 16 ? 16 : (nv <= 24 ? 24 : 32));
+    if (mode == 0) {
+      if (bucket == 8) PURIN_GS(0, 8);
+      if (bucket == 16) PURIN_GS(0, 16);
+      if (bucket == 24) PURIN_GS(0, 24);
+      PURIN_GS(0, 32);
+    } else if (mode == 1) {
+#define PURIN_GU(NVB) return launch_gs(k_gs_update_dots<T, NVB>, nv, img, h)
+      if (bucket == 8) PURIN_GU(8);
+      if (bucket == 16) PURIN_GU(16);
+      if (bucket == 24) PURIN_GU(24);
+      PURIN_GU(32);
+#undef PURIN_GU
+    } else {
+      if (bucket == 8) PURIN_GS(2, 8);
+      if (bucket == 16) PURIN_GS(2, 16);
+      if (bucket == 24) PURIN_GS(2, 24);
+      PURIN_GS(2, 32);
+    }
+#undef PURIN_GS
+  };
+  // reduce the chunks the last Gram--Schmidt pass wrote
+  auto reduce2 = [&](int nv, int plane_index, T* out, int opk) {
+    const size_t offset = (size_t)plane_index * last_nchunk * Bp;
+    k_reduce_chunks<T><<<dim3((unsigned)(Bp / 64), (unsigned)nv), 256, 0, st>>>(
+        part + offset, last_nchunk, Bp, out, opk);
+  };
 
   // rhs g = [cot * eligible, 0, 0] (cotangent divided by sqrt(D) for a metric)
   to_minor<T>(st, cot_y, batch, n, n, T1, Bp, metric, metric ? 2 : 0);
@@ -740,13 +997,24 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
       T* img = Vb + (size_t)(it + 1) * vstride;
       op(vk, img);
       // two-pass classical Gram--Schmidt over the active prefix (operators.py:834-871)
-      k_gs<T, 0><<<ggs, kBlock, 0, st>>>(Vb, vstride, it + 1, img, nullptr, W, Bp, part, nchunk);
-      reduce(it + 1, H1, 0);
-      k_gs<T, 1><<<ggs, kBlock, 0, st>>>(Vb, vstride, it + 1, img, H1, W, Bp, part, nchunk);
-      reduce(it + 1, H2, 0);
-      k_gs<T, 2><<<ggs, kBlock, 0, st>>>(Vb, vstride, it + 1, img, H2, W, Bp, part, nchunk);
-      k_reduce<T><<<sb, 256, 0, st>>>(part, 1, nchunk, Bp, S1, 0);
-      k_reduce<T><<<sb, 256, 0, st>>>(part + (size_t)nchunk * Bp, 1, nchunk, Bp, S2, 2);
+      const int nv = it + 1;
+      if (nv <= 32) {
+        if (int rc = gs_pass(0, nv, img, nullptr)) return rc;
+        reduce2(nv, 0, H1, 0);
+        if (int rc = gs_pass(1, nv, img, H1)) return rc;
+        reduce2(nv, 0, H2, 0);
+        if (int rc = gs_pass(2, nv, img, H2)) return rc;
+        reduce2(1, 0, S1, 0);
+        reduce2(1, 1, S2, 2);
+      } else {
+        k_gs<T, 0><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, nullptr, W, Bp, part, nchunk);
+        reduce(nv, H1, 0);
+        k_gs<T, 1><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, H1, W, Bp, part, nchunk);
+        reduce(nv, H2, 0);
+        k_gs<T, 2><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, H2, W, Bp, part, nchunk);
+        k_reduce<T><<<sb, 256, 0, st>>>(part, 1, nchunk, Bp, S1, 0);
+        k_reduce<T><<<sb, 256, 0, st>>>(part + (size_t)nchunk * Bp, 1, nchunk, Bp, S2, 2);
+      }
       zero_counters();
       k_gm_givens<T><<<sb, 256, 0, st>>>(G, it, H1, H2, S1, S2);
       k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, img, img, G.scale, G.keep);
