@@ -73,26 +73,39 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch) {
 
 template <typename T>
 constexpr int res_tile() {
-  return sizeof(T) == 8 ? 2 : 4;  // 16 bytes of samples per gathered element
+  return ResVec<T>::BT;  // 16 bytes of samples per gathered element
 }
 
-template <typename T, int BT, int SL>
-static int launch_resident_sl(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds) {
-  auto kern = R.shared_bounds ? k_resident<T, BT, SL, true> : k_resident<T, BT, SL, false>;
+template <typename T, int SLR, int SLC>
+static int launch_resident_sl(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb) {
+  auto kern = sb ? k_resident<T, SLR, SLC, true> : k_resident<T, SLR, SLC, false>;
   PURIN_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
   kern<<<dim3((unsigned)tiles), dim3(kResThreads), lds, st>>>(R);
   return PURIN_CP_OK;
 }
 
+template <typename T, int SLR>
+static int launch_resident_c(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
+                             bool sb) {
+  switch (slc) {
+    case 1: return launch_resident_sl<T, SLR, 1>(R, st, tiles, lds, sb);
+    case 2: return launch_resident_sl<T, SLR, 2>(R, st, tiles, lds, sb);
+    case 3: return launch_resident_sl<T, SLR, 3>(R, st, tiles, lds, sb);
+    case 4: return launch_resident_sl<T, SLR, 4>(R, st, tiles, lds, sb);
+    default: return set_error(PURIN_CP_ERR_ARG, "resident column slot count out of range");
+  }
+}
+
 template <typename T>
-static int launch_resident(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slots) {
-  constexpr int BT = res_tile<T>();
-  switch (slots) {
-    case 1: return launch_resident_sl<T, BT, 1>(R, st, tiles, lds);
-    case 2: return launch_resident_sl<T, BT, 2>(R, st, tiles, lds);
-    case 4: return launch_resident_sl<T, BT, 4>(R, st, tiles, lds);
-    default: return set_error(PURIN_CP_ERR_ARG, "resident slot count out of range");
+static int launch_resident(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slr,
+                           int slc, bool sb) {
+  switch (slr) {
+    case 1: return launch_resident_c<T, 1>(R, st, tiles, lds, slc, sb);
+    case 2: return launch_resident_c<T, 2>(R, st, tiles, lds, slc, sb);
+    case 3: return launch_resident_c<T, 3>(R, st, tiles, lds, slc, sb);
+    case 4: return launch_resident_c<T, 4>(R, st, tiles, lds, slc, sb);
+    default: return set_error(PURIN_CP_ERR_ARG, "resident row slot count out of range");
   }
 }
 
@@ -100,8 +113,8 @@ static int launch_resident(const Res<T>& R, hipStream_t st, int64_t tiles, size_
 template <typename T>
 static size_t resident_lds(const purin_cp_plan* p) {
   if (!p->res_ok) return 0;
-  // two regions (ybar and d+), each with one trailing zero slot
-  const size_t lds = (size_t)(p->n + 1 + p->m + 1) * res_tile<T>() * sizeof(T);
+  // Gy (n) | zero | Gd (m) | trash, 16 bytes each
+  const size_t lds = (size_t)(p->n + 1 + p->m + 1) * 16;
   return lds <= 160 * 1024 ? lds : 0;
 }
 
@@ -149,14 +162,12 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   R.m = (int)p->m;
   R.me = (int)p->me;
   R.Bp = Bp;
+  R.Kr = Kr;
+  R.Kc = Kc;
   R.rowmap = p->res_rowmap;
   R.colmap = p->res_colmap;
-  R.rslice = p->res_rslice;
-  R.cslice = p->res_cslice;
-  R.ridx = p->res_ridx;
-  R.rval = (const T*)p->res_rval;
-  R.cidx = p->res_cidx;
-  R.cval = (const T*)p->res_cval;
+  R.stream = p->res_stream;
+  R.wtab = p->res_wtab;
   T* Ts = (T*)(ws + L.RTs);
   T* Rs = (T*)(ws + L.RRs);
   T* D0s = (T*)(ws + L.RD0);
@@ -178,7 +189,6 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   R.D0s = D0s;
   R.Ls = Ls;
   R.Hs = Hs;
-  R.shared_bounds = o.shared_bounds;
   R.sched = (const T*)p->res_sched;
   R.iters = o.max_iterations;
   R.Y = (T*)(sv + L.Y);
@@ -189,7 +199,8 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     PURIN_HIP(hipEventCreate(&e1));
     PURIN_HIP(hipEventRecord(e0, st));
   }
-  if (int rc = launch_resident<T>(R, st, tiles, lds, p->res_mr)) return rc;
+  if (int rc = launch_resident<T>(R, st, tiles, lds, p->res_mr, p->res_mc,
+                                         o.shared_bounds != 0)) return rc;
   PURIN_HIP(hipGetLastError());
   if (o.timing) {
     PURIN_HIP(hipEventRecord(e1, st));

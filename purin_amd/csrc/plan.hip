@@ -222,21 +222,22 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
     p->tau_adj = (double)(safety / (T(1) + La));
     p->sigma_adj = (double)(safety / La);
   }
-  // --- resident schedule: slots sorted by degree, 64-lane sliced ELL ----------
+  // --- resident schedule: slots sorted by degree, per-wavefront chunk streams --
   {
     const int64_t NT = kResThreads;
-    // one slot count for rows and columns, a power of two (1, 2, 4, 8)
-    const int64_t need = std::max<int64_t>((std::max(m, n) + NT - 1) / NT, 1);
-    int64_t slots = 1;
-    while (slots < need) slots *= 2;
-    p->res_ok = slots <= kResMaxSlots && n >= 1;
+    const int64_t mr = std::max<int64_t>((m + NT - 1) / NT, 1);
+    const int64_t mc = std::max<int64_t>((n + NT - 1) / NT, 1);
+    // LDS: Gy (n) | zero | Gd (m) | trash, 16 bytes each
+    const bool lds_fits = (n + 1 + m + 1) * 16 <= 160 * 1024;
+    p->res_ok = mr <= kResMaxSlots && mc <= kResMaxSlots && n >= 1 && lds_fits;
     if (p->res_ok) {
-      p->res_mr = (int32_t)slots;
-      p->res_mc = (int32_t)slots;
-      auto slices = [&](int64_t K, int64_t count, const std::vector<int32_t>& ptr,
-                        const std::vector<int32_t>& idx, const std::vector<T>& val,
-                        int32_t zero_slot, std::vector<int32_t>& map, std::vector<int32_t>& sl,
-                        std::vector<int32_t>& eidx, std::vector<T>& eval) {
+      p->res_mr = (int32_t)mr;
+      p->res_mc = (int32_t)mc;
+      const uint32_t zero_off = (uint32_t)n * 16u;
+      const uint32_t gd_off = (uint32_t)(n + 1) * 16u;
+      // degree-sorted assignment of rows / columns to slots k = slot * NT + thread
+      auto assign = [&](int64_t K, int64_t count, const std::vector<int32_t>& ptr,
+                        std::vector<int32_t>& map) {
         std::vector<int32_t> order(count);
         for (int64_t i = 0; i < count; ++i) order[i] = (int32_t)i;
         std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
@@ -244,52 +245,111 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         });
         map.assign(K, -1);
         for (int64_t k = 0; k < count; ++k) map[k] = order[k];
-        const int64_t nslice = K / 64;
-        sl.assign(2 * nslice, 0);
-        for (int64_t z = 0; z < nslice; ++z) {
-          int32_t width = 0;
+      };
+      std::vector<int32_t> rmap, cmap;
+      assign(mr * NT, m, H.ptr, rmap);
+      assign(mc * NT, n, H.cptr, cmap);
+      // chunk = 64 lanes x 4 entries: u32 LDS byte offsets, then the coefficients
+      const size_t CB = 64 * 16 + 64 * 4 * sizeof(T);
+      std::vector<unsigned char> stream;
+      std::vector<int32_t> wtab(4 * 16, 0);
+      int64_t nchunks = 0;
+      auto put_chunk = [&](const uint32_t* off, const T* val) {  // off, val: [64][4]
+        const size_t at = stream.size();
+        stream.resize(at + CB);
+        std::memcpy(&stream[at], off, 64 * 16);
+        if (sizeof(T) == 8) {  // two blocks of (v0, v1) and (v2, v3) per lane
+          T* dst = reinterpret_cast<T*>(&stream[at + 1024]);
+          for (int l = 0; l < 64; ++l) {
+            dst[2 * l] = val[4 * l];
+            dst[2 * l + 1] = val[4 * l + 1];
+            dst[128 + 2 * l] = val[4 * l + 2];
+            dst[128 + 2 * l + 1] = val[4 * l + 3];
+          }
+        } else {
+          std::memcpy(&stream[at + 1024], val, 64 * 4 * sizeof(T));
+        }
+        ++nchunks;
+      };
+      bool too_wide = false;
+      // one slot of one wavefront: chunks of the 64 lanes' rows (row pass) or
+      // columns (column pass); returns the chunk count
+      auto put_slot = [&](const std::vector<int32_t>& map, int64_t z,
+                          const std::vector<int32_t>& ptr, const std::vector<int32_t>& idx,
+                          const std::vector<T>& val, uint32_t base) -> int {
+        int32_t width = 0;
+        for (int l = 0; l < 64; ++l) {
+          const int32_t r = map[z * 64 + l];
+          if (r >= 0) width = std::max(width, ptr[r + 1] - ptr[r]);
+        }
+        const int nch = (width + 3) / 4;
+        if (nch > 255) too_wide = true;
+        uint32_t off[64 * 4];
+        T v[64 * 4];
+        for (int ch = 0; ch < nch; ++ch) {
           for (int l = 0; l < 64; ++l) {
             const int32_t r = map[z * 64 + l];
-            if (r >= 0) width = std::max(width, ptr[r + 1] - ptr[r]);
-          }
-          sl[2 * z] = (int32_t)eidx.size();
-          sl[2 * z + 1] = width;
-          for (int32_t q = 0; q < width; ++q)
-            for (int l = 0; l < 64; ++l) {
-              const int32_t r = map[z * 64 + l];
+            for (int u = 0; u < 4; ++u) {
+              const int32_t q = 4 * ch + u;
               const bool has = r >= 0 && q < ptr[r + 1] - ptr[r];
-              eidx.push_back(has ? idx[ptr[r] + q] : zero_slot);
-              eval.push_back(has ? val[ptr[r] + q] : T(0));
+              off[4 * l + u] = has ? base + 16u * (uint32_t)idx[ptr[r] + q] : zero_off;
+              v[4 * l + u] = has ? val[ptr[r] + q] : T(0);
             }
+          }
+          put_chunk(off, v);
         }
+        return nch;
       };
-      std::vector<int32_t> rmap, cmap, rsl, csl, ridxE, cidxE;
-      std::vector<T> rvalE, cvalE;
-      slices(p->res_mr * NT, m, H.ptr, H.idx, H.val_s, (int32_t)n, rmap, rsl, ridxE, rvalE);
-      slices(p->res_mc * NT, n, H.cptr, H.cidx, H.cval_s, (int32_t)m, cmap, csl, cidxE, cvalE);
-      auto upr = [&](void** dst, const void* src, size_t bytes) -> int {
-        if (bytes == 0) bytes = 16;
-        hipError_t e = hipMalloc(dst, bytes);
-        if (e != hipSuccess) return set_error(PURIN_CP_ERR_NOMEM, "plan hipMalloc failed");
-        p->owned.push_back(*dst);
-        if (src) {
-          e = hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice);
-          if (e != hipSuccess) return hip_check(e, "plan upload");
+      for (int w = 0; w < 16; ++w) {
+        const int64_t first = nchunks;
+        uint32_t rc = 0, cc = 0;
+        for (int64_t r = 0; r < mr; ++r)
+          rc |= (uint32_t)put_slot(rmap, r * 16 + w, H.ptr, H.idx, H.val_s, 0u) << (8 * r);
+        for (int64_t c = 0; c < mc; ++c)
+          cc |= (uint32_t)put_slot(cmap, c * 16 + w, H.cptr, H.cidx, H.cval_s, gd_off) << (8 * c);
+        // the wrap chunk: a copy of the wave's first chunk (or zero padding),
+        // prefetched at the end of each iteration for the next one
+        if (nchunks > first) {
+          const size_t at = stream.size();
+          stream.resize(at + CB);
+          std::memcpy(&stream[at], &stream[(size_t)first * CB], CB);
+          ++nchunks;
+        } else {
+          uint32_t off[64 * 4];
+          T v[64 * 4];
+          for (int e = 0; e < 64 * 4; ++e) {
+            off[e] = zero_off;
+            v[e] = T(0);
+          }
+          put_chunk(off, v);
         }
-        return PURIN_CP_OK;
-      };
-      int rc2;
+        wtab[4 * w] = (int32_t)first;
+        wtab[4 * w + 1] = (int32_t)rc;
+        wtab[4 * w + 2] = (int32_t)cc;
+      }
+      if (too_wide || nchunks >= (int64_t)1 << 30) p->res_ok = false;
+      if (p->res_ok) {
+        p->res_stream_bytes = (int64_t)stream.size();
+        auto upr = [&](void** dst, const void* src, size_t bytes) -> int {
+          if (bytes == 0) bytes = 16;
+          hipError_t e = hipMalloc(dst, bytes);
+          if (e != hipSuccess) return set_error(PURIN_CP_ERR_NOMEM, "plan hipMalloc failed");
+          p->owned.push_back(*dst);
+          if (src) {
+            e = hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice);
+            if (e != hipSuccess) return hip_check(e, "plan upload");
+          }
+          return PURIN_CP_OK;
+        };
+        int rc2;
 #define UPR(dst, vec) \
   if ((rc2 = upr((void**)&(dst), (vec).empty() ? nullptr : (vec).data(), (vec).size() * sizeof((vec)[0]))) != PURIN_CP_OK) return rc2
-      UPR(p->res_rowmap, rmap);
-      UPR(p->res_colmap, cmap);
-      UPR(p->res_rslice, rsl);
-      UPR(p->res_cslice, csl);
-      UPR(p->res_ridx, ridxE);
-      UPR(p->res_rval, rvalE);
-      UPR(p->res_cidx, cidxE);
-      UPR(p->res_cval, cvalE);
+        UPR(p->res_rowmap, rmap);
+        UPR(p->res_colmap, cmap);
+        UPR(p->res_stream, stream);
+        UPR(p->res_wtab, wtab);
 #undef UPR
+      }
     }
   }
   // --- upload -----------------------------------------------------------------

@@ -59,19 +59,16 @@ struct purin_cp_plan {
   size_t aws_bytes = 0;
   int32_t* pinned = nullptr;  // host-pinned flag words
 
-  // resident (on-chip) iteration schedule: degree-sorted rows/columns in
-  // 64-lane sliced-ELL slices; built when n and m fit kResMaxSlots * kResThreads
+  // resident (on-chip) iteration schedule: degree-sorted rows/columns, one
+  // thread per (slot, row) and (slot, column); built when n and m fit
+  // kResMaxSlots * kResThreads and the tile's vectors fit in LDS
   bool res_ok = false;
-  int32_t res_mr = 0, res_mc = 0;    // row / column slots per thread
+  int32_t res_mr = 0, res_mc = 0;    // row / column slots per thread (1..kResMaxSlots)
   int32_t* res_rowmap = nullptr;     // Kr = mr * threads: kept row of each slot or -1
   int32_t* res_colmap = nullptr;     // Kc = mc * threads: column of each slot or -1
-  int32_t* res_rslice = nullptr;     // per 64-slot slice: {offset, width}
-  int32_t* res_cslice = nullptr;
-  int32_t* res_ridx = nullptr;       // sliced ELL entries (lane fastest); padding
-                                     // points at the zero slot (column n / row m)
-  void* res_rval = nullptr;
-  int32_t* res_cidx = nullptr;
-  void* res_cval = nullptr;
+  unsigned char* res_stream = nullptr;  // per-wavefront chunk streams of the matrix
+  int32_t* res_wtab = nullptr;       // [16][4] first chunk and packed chunk counts
+  int64_t res_stream_bytes = 0;
   void* res_sched = nullptr;         // per-iteration (sigma, a, delta, theta)
   int64_t res_sched_len = 0;
 

@@ -1,196 +1,264 @@
 // Resident fixed-iteration CP kernel: one workgroup keeps a tile of BT samples
 // on chip for every iteration of the solve.
 //
-// Per workgroup (1024 threads = 16 wavefronts):
-//   LDS      two regions, samples interleaved so a gather reads BT consecutive
-//            values with one 16-byte load:
-//              Gy[(n+1) * BT]  ybar, read by the row pass, written by the column pass
-//              Gd[(m+1) * BT]  d+,   read by the column pass, written by the row pass
-//            Entry n of Gy and entry m of Gd stay zero: padding entries of the
-//            sliced-ELL matrix point there, so the gather loops have no branches.
-//   VGPRs    y of the thread's columns and d of its rows, for the BT samples.
-//   streamed the tile's yhat and scaled rhs in slot order (coalesced; they stay in
-//            L2/MALL across iterations) and the matrix in 64-lane sliced ELL.
-// Rows and columns are assigned to (slot, thread) in decreasing-degree order so
-// the lanes of a wavefront walk rows/columns of (almost) equal length.
+// Per workgroup (1024 threads = 16 wavefronts), BT samples (2 fp64 / 4 fp32,
+// 16 bytes) interleaved so that one gathered element is one ds_read_b128:
+//   LDS      16-byte entries  Gy[0, n) | zero | Gd[0, m) | trash
+//              Gy  ybar, read by the row pass, written by the column pass
+//              Gd  d+,   read by the column pass, written by the row pass
+//              zero stays 0: padding entries of the matrix stream point there
+//              trash takes the stores of lanes that own no row / column
+//   VGPRs    per thread and slot: y of its columns, the targets yhat and the
+//            scaled right-hand sides, for the BT samples (loaded once)
+//   stream   the shared matrix, read every iteration from L2: one linear
+//            stream of chunks per wavefront (row slots, column slots, then a
+//            copy of the first chunk), a chunk being 4 entries per lane stored
+//            as {LDS byte offset of the gathered element, coefficient}.  The
+//            loads take an SGPR base and a constant lane offset, and the next
+//            chunk is always in flight while the current one is gathered,
+//            across slot, pass and iteration boundaries.
+// Rows and columns are assigned to (slot, thread) in decreasing-degree order
+// so the lanes of a wavefront walk rows / columns of (almost) equal length.
 //
 // One iteration (reference src/purin/solvers/chambolle_pock/kernels.py:91-150):
-//   row pass   d <- P(d + sigma (K ybar - r)); Gd <- d          (reads Gy only)
+//   row pass   d <- P(d + sigma (K ybar - r)); Gd <- d      (reads Gy and own Gd)
 //   barrier
 //   col pass   y+ = clip(a y - delta K^T d+ + delta yhat, lo, hi);
-//              Gy <- y+ + theta (y+ - y); y <- y+                (reads Gd only)
+//              Gy <- y+ + theta (y+ - y); y <- y+            (reads Gd only)
 //   barrier
-// Only the fixed-iteration mode runs here; the per-sample stop test uses the
-// streaming passes (kernels.hpp).
+// The arithmetic (operand order, fused multiply-adds, slot order of every
+// sum) is that of the streaming passes in kernels.hpp, so the two paths give
+// identical iterates.  Only the fixed-iteration mode runs here; the
+// per-sample stop test uses the streaming passes.
 #pragma once
 
 #include "common.hpp"
 
 namespace purin {
 
+constexpr int kResChunk = 4;      // matrix entries per lane in one stream chunk
+constexpr int kResWaves = 16;     // wavefronts of a resident workgroup
+
+template <typename T>
+struct ResVec;
+template <>
+struct ResVec<double> {
+  static constexpr int BT = 2;
+  typedef double V __attribute__((ext_vector_type(2)));
+};
+template <>
+struct ResVec<float> {
+  static constexpr int BT = 4;
+  typedef float V __attribute__((ext_vector_type(4)));
+};
+
+// Bytes of one chunk of one wavefront: the offsets block (64 lanes x 4 u32),
+// then the coefficient blocks (64 lanes x 16 bytes each; 2 for fp64, 1 for fp32).
+template <typename T>
+constexpr uint32_t res_chunk_bytes() {
+  return 64u * 16u + 64u * kResChunk * (uint32_t)sizeof(T);
+}
+
 template <typename T>
 struct Res {
   int n, m, me;
   int64_t Bp;
-  const int32_t* __restrict__ rowmap;  // [SL * NT]
-  const int32_t* __restrict__ colmap;  // [SL * NT]
-  const int32_t* __restrict__ rslice;  // per 64-slot slice {offset, width}
-  const int32_t* __restrict__ cslice;
-  const int32_t* __restrict__ ridx;    // padding points at column n (zero slot)
-  const T* __restrict__ rval;
-  const int32_t* __restrict__ cidx;    // padding points at row m (zero slot)
-  const T* __restrict__ cval;
-  const T* __restrict__ Ts;   // [tiles][SL*NT][BT] targets in slot order
-  const T* __restrict__ Rs;   // [tiles][SL*NT][BT] scaled rhs in slot order
-  const T* __restrict__ D0s;  // [tiles][SL*NT][BT] initial duals in slot order
-  const T* __restrict__ Ls;   // shared: [SL*NT]; else [tiles][SL*NT][BT]
+  int Kr, Kc;                          // slot-ordered strides: SLR*1024, SLC*1024
+  const int32_t* __restrict__ rowmap;  // [Kr] kept row of each (slot, thread) or -1
+  const int32_t* __restrict__ colmap;  // [Kc] column of each (slot, thread) or -1
+  const unsigned char* __restrict__ stream;  // the chunks
+  const int32_t* __restrict__ wtab;    // [16][4]: first chunk, row chunk counts
+                                       // (4 x u8), column chunk counts (4 x u8), 0
+  const T* __restrict__ Ts;   // [tiles][Kc][BT] targets in slot order
+  const T* __restrict__ Rs;   // [tiles][Kr][BT] scaled rhs in slot order
+  const T* __restrict__ D0s;  // [tiles][Kr][BT] initial duals in slot order
+  const T* __restrict__ Ls;   // shared: [Kc]; else [tiles][Kc][BT]
   const T* __restrict__ Hs;
-  int shared_bounds;
   const T* __restrict__ sched;  // [iters][4] = sigma, a, delta, theta
   int64_t iters;
   T* Y;  // n x Bp
   T* D;  // m x Bp
 };
 
-template <typename T, int BT>
-struct Pack;
-template <>
-struct Pack<double, 2> {
-  typedef double V __attribute__((ext_vector_type(2)));
-};
-template <>
-struct Pack<float, 4> {
-  typedef float V __attribute__((ext_vector_type(4)));
+template <typename T>
+struct Chunk {
+  uint32_t o[kResChunk];
+  T v[kResChunk];
 };
 
-// sum_q val[q] * G[idx[q]] over one sliced-ELL slice, 4 entries per step with
-// the index/value loads of a step issued before its LDS gathers.
-template <typename T, int BT>
-__device__ __forceinline__ typename Pack<T, BT>::V slice_dot(const int32_t* __restrict__ idx,
-                                                             const T* __restrict__ val,
-                                                             const typename Pack<T, BT>::V* G,
-                                                             int off, int width, int lane) {
-  using V = typename Pack<T, BT>::V;
-  V acc = V(T(0));
-  int q = 0;
-  for (; q + 4 <= width; q += 4) {
-    int j[4];
-    T v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      j[u] = idx[off + (q + u) * 64 + lane];
-      v[u] = val[off + (q + u) * 64 + lane];
-    }
-    V x[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) x[u] = G[j[u]];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) acc += v[u] * x[u];
+template <typename T>
+__device__ __forceinline__ void load_chunk(Chunk<T>& c, const unsigned char* __restrict__ base,
+                                           uint32_t lane16) {
+  const uint4 o = *reinterpret_cast<const uint4*>(base + lane16);
+  c.o[0] = o.x;
+  c.o[1] = o.y;
+  c.o[2] = o.z;
+  c.o[3] = o.w;
+  if constexpr (sizeof(T) == 8) {
+    typedef double D2 __attribute__((ext_vector_type(2)));
+    const D2 a = *reinterpret_cast<const D2*>(base + 1024u + lane16);
+    const D2 b = *reinterpret_cast<const D2*>(base + 2048u + lane16);
+    c.v[0] = a.x;
+    c.v[1] = a.y;
+    c.v[2] = b.x;
+    c.v[3] = b.y;
+  } else {
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    const F4 a = *reinterpret_cast<const F4*>(base + 1024u + lane16);
+    c.v[0] = a.x;
+    c.v[1] = a.y;
+    c.v[2] = a.z;
+    c.v[3] = a.w;
   }
-  for (; q < width; ++q) {
-    const int jj = idx[off + q * 64 + lane];
-    const T vv = val[off + q * 64 + lane];
-    acc += vv * G[jj];
+}
+
+// acc += sum over the chunk's 4 entries of coefficient * gathered element, in order
+template <typename T, typename V>
+__device__ __forceinline__ void consume_chunk(const Chunk<T>& c, const unsigned char* lds, V& acc) {
+  V x[kResChunk];
+#pragma unroll
+  for (int u = 0; u < kResChunk; ++u) x[u] = *reinterpret_cast<const V*>(lds + c.o[u]);
+#pragma unroll
+  for (int u = 0; u < kResChunk; ++u) acc += c.v[u] * x[u];
+}
+
+// Sum over the ``nch`` chunks of one slot.  On entry b0 holds (or is loading)
+// the slot's first chunk and ``pos`` indexes the next chunk of the wave's
+// stream; on exit b0 holds the chunk after the slot's last one.
+template <typename T, typename V>
+__device__ __forceinline__ V slot_sum(int nch, Chunk<T>& b0, Chunk<T>& b1, uint32_t& pos,
+                                      const unsigned char* __restrict__ stream, uint32_t lane16,
+                                      const unsigned char* lds) {
+  constexpr uint32_t CB = res_chunk_bytes<T>();
+  V acc = V(T(0));
+  for (int k = 0; k < nch; k += 2) {
+    const bool two = k + 1 < nch;
+    if (two) {
+      load_chunk(b1, stream + (size_t)pos * CB, lane16);
+      ++pos;
+    }
+    consume_chunk(b0, lds, acc);
+    load_chunk(b0, stream + (size_t)pos * CB, lane16);
+    ++pos;
+    if (two) consume_chunk(b1, lds, acc);
   }
   return acc;
 }
 
-template <typename T, int BT, int SL, bool SB>
+template <typename T, int SLR, int SLC, bool SB>
 __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   constexpr int NT = 1024;
-  using V = typename Pack<T, BT>::V;
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  V* Gy = reinterpret_cast<V*>(smem_raw);
-  V* Gd = Gy + (A.n + 1);
+  constexpr int BT = ResVec<T>::BT;
+  using V = typename ResVec<T>::V;
+  extern __shared__ __align__(16) unsigned char lds[];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int64_t tile = blockIdx.x;
+  const uint32_t lane16 = (uint32_t)lane * 16u;
   const V vzero = V(T(0));
+  const uint32_t gd_off = (uint32_t)(A.n + 1) * 16u;
+  const uint32_t trash_off = (uint32_t)(A.n + 1 + A.m) * 16u;
 
-  int ri[SL], cj[SL];
-#pragma unroll
-  for (int r = 0; r < SL; ++r) ri[r] = A.rowmap[r * NT + t];
-#pragma unroll
-  for (int c = 0; c < SL; ++c) cj[c] = A.colmap[c * NT + t];
+  const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave]);
+  const uint32_t rcnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave + 1]);
+  const uint32_t ccnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave + 2]);
 
-  const V* Ts = reinterpret_cast<const V*>(A.Ts) + tile * (int64_t)(SL * NT);
-  const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)(SL * NT);
-  const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)(SL * NT);
-  V y[SL], d[SL];
+  const V* Ts = reinterpret_cast<const V*>(A.Ts) + tile * (int64_t)A.Kc;
+  const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)A.Kr;
+  const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)A.Kr;
+
+  uint32_t soff_r[SLR], soff_c[SLC];
+  V y[SLC], tg[SLC], rr[SLR];
+  uint32_t ineq = 0;
 #pragma unroll
-  for (int c = 0; c < SL; ++c) {
-    y[c] = cj[c] >= 0 ? Ts[c * NT + t] : vzero;
-    if (cj[c] >= 0) Gy[cj[c]] = y[c];  // ybar0 = y0 = yhat
+  for (int c = 0; c < SLC; ++c) {
+    const int j = A.colmap[c * NT + t];
+    soff_c[c] = j >= 0 ? (uint32_t)j * 16u : trash_off;
+    tg[c] = j >= 0 ? Ts[c * NT + t] : vzero;
+    y[c] = tg[c];  // y0 = ybar0 = yhat (kernels.py:229-231)
+    *reinterpret_cast<V*>(lds + soff_c[c]) = y[c];
   }
 #pragma unroll
-  for (int r = 0; r < SL; ++r) {
-    d[r] = ri[r] >= 0 ? D0[r * NT + t] : vzero;
-    if (ri[r] >= 0) Gd[ri[r]] = vzero;
+  for (int r = 0; r < SLR; ++r) {
+    const int i = A.rowmap[r * NT + t];
+    soff_r[r] = i >= 0 ? gd_off + (uint32_t)i * 16u : trash_off;
+    rr[r] = i >= 0 ? Rs[r * NT + t] : vzero;
+    if (i >= A.me) ineq |= 1u << r;  // kept rows: equalities first
+    *reinterpret_cast<V*>(lds + soff_r[r]) = i >= 0 ? D0[r * NT + t] : vzero;
   }
-  if (t == 0) {
-    Gy[A.n] = vzero;
-    Gd[A.m] = vzero;
-  }
+  if (t == 0) *reinterpret_cast<V*>(lds + (uint32_t)A.n * 16u) = vzero;  // the zero slot
   __syncthreads();
 
+  constexpr uint32_t CB = res_chunk_bytes<T>();
+  Chunk<T> b0, b1;
+  load_chunk(b0, A.stream + (size_t)first * CB, lane16);
+
   for (int64_t it = 0; it < A.iters; ++it) {
-    const T sigma = A.sched[4 * it], a = A.sched[4 * it + 1];
-    const T delta = A.sched[4 * it + 2], theta = A.sched[4 * it + 3];
-    // ---- row pass (reads Gy, writes Gd) ---------------------------------------
+    // wave-uniform schedule scalars: scalar loads through the constant address space
+    const __attribute__((address_space(4))) T* sc =
+        (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
+    const T sigma = sc[0], a = sc[1], delta = sc[2], theta = sc[3];
+    uint32_t pos = first + 1;
+    // ---- row pass (reads Gy and the thread's own Gd entries, writes Gd) -------
 #pragma unroll
-    for (int r = 0; r < SL; ++r) {
-      if (ri[r] < 0) continue;
-      const int z = r * (NT / 64) + wave;
-      const V acc = slice_dot<T, BT>(A.ridx, A.rval, Gy, A.rslice[2 * z], A.rslice[2 * z + 1],
-                                     lane);
-      const V rr = Rs[r * NT + t];
-      V p = d[r] + sigma * (acc - rr);
-      if (ri[r] >= A.me) {
+    for (int r = 0; r < SLR; ++r) {
+      const int nch = (int)((rcnt >> (8 * r)) & 255u);
+      const V dold = *reinterpret_cast<const V*>(lds + soff_r[r]);
+      const V acc = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16, lds);
+      V p = dold + sigma * (acc - rr[r]);
+      if (ineq & (1u << r)) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
       }
-      d[r] = p;
-      Gd[ri[r]] = p;
+      *reinterpret_cast<V*>(lds + soff_r[r]) = p;
     }
     __syncthreads();
     // ---- column pass (reads Gd, writes Gy) --------------------------------------
 #pragma unroll
-    for (int c = 0; c < SL; ++c) {
-      if (cj[c] < 0) continue;
-      const int z = c * (NT / 64) + wave;
-      const V tt = slice_dot<T, BT>(A.cidx, A.cval, Gd, A.cslice[2 * z], A.cslice[2 * z + 1],
-                                    lane);
-      const V tg = Ts[c * NT + t];
+    for (int c = 0; c < SLC; ++c) {
+      const int nch = (int)((ccnt >> (8 * c)) & 255u);
+      // bounds are re-read each iteration (L2-resident when shared) rather
+      // than held in registers: the opaque base keeps them inside the loop
+      const T* lb = A.Ls;
+      const T* hb = A.Hs;
+      asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
       if (SB) {
-        lo = V(A.Ls[c * NT + t]);
-        hi = V(A.Hs[c * NT + t]);
+        lo = V(lb[c * NT + t]);
+        hi = V(hb[c * NT + t]);
       } else {
-        lo = reinterpret_cast<const V*>(A.Ls)[tile * (int64_t)(SL * NT) + c * NT + t];
-        hi = reinterpret_cast<const V*>(A.Hs)[tile * (int64_t)(SL * NT) + c * NT + t];
+        lo = reinterpret_cast<const V*>(lb)[tile * (int64_t)A.Kc + c * NT + t];
+        hi = reinterpret_cast<const V*>(hb)[tile * (int64_t)A.Kc + c * NT + t];
       }
-      const V sv = a * y[c] - delta * tt + delta * tg;
+      const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16, lds);
+      const V sv = a * y[c] - delta * tt + delta * tg[c];
       V yn;
 #pragma unroll
       for (int s = 0; s < BT; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
-      Gy[cj[c]] = yn + theta * (yn - y[c]);
+      *reinterpret_cast<V*>(lds + soff_c[c]) = yn + theta * (yn - y[c]);
       y[c] = yn;
     }
     __syncthreads();
   }
   // ---- hand the state to the batch-minor layout ---------------------------------
-  const int64_t b0 = tile * BT;
+  const int64_t b0s = tile * BT;
 #pragma unroll
-  for (int c = 0; c < SL; ++c)
-    if (cj[c] >= 0)
+  for (int c = 0; c < SLC; ++c) {
+    const int j = A.colmap[c * NT + t];
+    if (j >= 0)
 #pragma unroll
-      for (int s = 0; s < BT; ++s) A.Y[(int64_t)cj[c] * A.Bp + b0 + s] = y[c][s];
+      for (int s = 0; s < BT; ++s) A.Y[(int64_t)j * A.Bp + b0s + s] = y[c][s];
+  }
 #pragma unroll
-  for (int r = 0; r < SL; ++r)
-    if (ri[r] >= 0)
+  for (int r = 0; r < SLR; ++r) {
+    const int i = A.rowmap[r * NT + t];
+    if (i >= 0) {
+      const V d = *reinterpret_cast<const V*>(lds + soff_r[r]);
 #pragma unroll
-      for (int s = 0; s < BT; ++s) A.D[(int64_t)ri[r] * A.Bp + b0 + s] = d[r][s];
+      for (int s = 0; s < BT; ++s) A.D[(int64_t)i * A.Bp + b0s + s] = d[s];
+    }
+  }
 }
 
 // dst[(tile*K + k)*BT + s] = src[map[k]*Bp + tile*BT + s] (0 for empty slots)
