@@ -235,7 +235,11 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       p->res_mc = (int32_t)mc;
       const uint32_t zero_off = (uint32_t)n * 16u;
       const uint32_t gd_off = (uint32_t)(n + 1) * 16u;
-      // degree-sorted assignment of rows / columns to slots k = slot * NT + thread
+      // Rows / columns go to slots k = slot * NT + thread.  Sorted by degree,
+      // they form groups of 64 of nearly equal length (one group per slot of
+      // one wavefront).  Within each slot the groups are dealt to the
+      // wavefronts longest first to the wavefront with the least work so far,
+      // which evens out the chunks each wavefront walks between barriers.
       auto assign = [&](int64_t K, int64_t count, const std::vector<int32_t>& ptr,
                         std::vector<int32_t>& map) {
         std::vector<int32_t> order(count);
@@ -243,13 +247,31 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
           return ptr[a + 1] - ptr[a] > ptr[b + 1] - ptr[b];
         });
+        const int64_t groups = K / 64;
+        std::vector<int32_t> gch(groups, 0);  // chunks of each sorted group
+        for (int64_t g = 0; g < groups; ++g)
+          if (g * 64 < count) gch[g] = (ptr[order[g * 64] + 1] - ptr[order[g * 64]] + 3) / 4;
+        std::vector<int64_t> load(16, 0);
+        std::vector<int64_t> slice_of(groups);
+        for (int64_t slot = 0; slot < groups / 16; ++slot) {
+          std::vector<int> gs(16), ws(16);
+          for (int i = 0; i < 16; ++i) gs[i] = ws[i] = i;
+          std::stable_sort(gs.begin(), gs.end(), [&](int a, int b) {
+            return gch[slot * 16 + a] > gch[slot * 16 + b];
+          });
+          std::stable_sort(ws.begin(), ws.end(), [&](int a, int b) { return load[a] < load[b]; });
+          for (int i = 0; i < 16; ++i) {
+            slice_of[slot * 16 + gs[i]] = slot * 16 + ws[i];
+            load[ws[i]] += gch[slot * 16 + gs[i]];
+          }
+        }
         map.assign(K, -1);
-        for (int64_t k = 0; k < count; ++k) map[k] = order[k];
+        for (int64_t k = 0; k < count; ++k) map[slice_of[k / 64] * 64 + k % 64] = order[k];
       };
       std::vector<int32_t> rmap, cmap;
       assign(mr * NT, m, H.ptr, rmap);
       assign(mc * NT, n, H.cptr, cmap);
-      // chunk = 64 lanes x 4 entries: u32 LDS byte offsets, then the coefficients
+      // chunk = 64 lanes x 4 entries: u32 LDS byte addresses, then the coefficients
       const size_t CB = 64 * 16 + 64 * 4 * sizeof(T);
       std::vector<unsigned char> stream;
       std::vector<int32_t> wtab(4 * 16, 0);

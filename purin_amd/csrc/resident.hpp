@@ -13,7 +13,7 @@
 //   stream   the shared matrix, read every iteration from L2: one linear
 //            stream of chunks per wavefront (row slots, column slots, then a
 //            copy of the first chunk), a chunk being 4 entries per lane stored
-//            as {LDS byte offset of the gathered element, coefficient}.  The
+//            as {LDS byte address of the gathered element, coefficient}.  The
 //            loads take an SGPR base and a constant lane offset, and the next
 //            chunk is always in flight while the current one is gathered,
 //            across slot, pass and iteration boundaries.
@@ -52,8 +52,9 @@ struct ResVec<float> {
   typedef float V __attribute__((ext_vector_type(4)));
 };
 
-// Bytes of one chunk of one wavefront: the offsets block (64 lanes x 4 u32),
-// then the coefficient blocks (64 lanes x 16 bytes each; 2 for fp64, 1 for fp32).
+// Bytes of one chunk of one wavefront: the offsets block (64 lanes x 4 u32 LDS
+// byte addresses), then the coefficient blocks (64 lanes x 16 bytes each; 2
+// for fp64, 1 for fp32).
 template <typename T>
 constexpr uint32_t res_chunk_bytes() {
   return 64u * 16u + 64u * kResChunk * (uint32_t)sizeof(T);
@@ -86,38 +87,60 @@ struct Chunk {
   T v[kResChunk];
 };
 
+// LDS accesses by absolute byte address: the kernel declares no static LDS, so
+// its dynamic LDS starts at address 0 and the stream's offsets are addresses.
+template <typename V>
+__device__ __forceinline__ V lds_read(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) V*>(addr);
+}
+template <typename V>
+__device__ __forceinline__ void lds_write(uint32_t addr, V v) {
+  *reinterpret_cast<__attribute__((address_space(3))) V*>(addr) = v;
+}
+
+// The chunk at byte ``cbyte`` of the stream; the base is made wave-uniform
+// explicitly so the loads take an SGPR base plus the lane's 16-byte offset.
 template <typename T>
-__device__ __forceinline__ void load_chunk(Chunk<T>& c, const unsigned char* __restrict__ base,
-                                           uint32_t lane16) {
-  const uint4 o = *reinterpret_cast<const uint4*>(base + lane16);
+__device__ __forceinline__ void load_chunk(Chunk<T>& c, const unsigned char* __restrict__ stream,
+                                           uint64_t cbyte, uint32_t lane16) {
+  const uint64_t a = (uint64_t)(uintptr_t)stream + cbyte;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  const __attribute__((address_space(1))) unsigned char* base =
+      (const __attribute__((address_space(1))) unsigned char*)(((uint64_t)hi << 32) | lo);
+  typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+  typedef const __attribute__((address_space(1))) U4* U4P;
+  const U4 o = *reinterpret_cast<U4P>(base + lane16);
   c.o[0] = o.x;
   c.o[1] = o.y;
   c.o[2] = o.z;
   c.o[3] = o.w;
   if constexpr (sizeof(T) == 8) {
     typedef double D2 __attribute__((ext_vector_type(2)));
-    const D2 a = *reinterpret_cast<const D2*>(base + 1024u + lane16);
-    const D2 b = *reinterpret_cast<const D2*>(base + 2048u + lane16);
-    c.v[0] = a.x;
-    c.v[1] = a.y;
-    c.v[2] = b.x;
-    c.v[3] = b.y;
+    typedef const __attribute__((address_space(1))) D2* D2P;
+    const D2 x = *reinterpret_cast<D2P>(base + 1024u + lane16);
+    const D2 y = *reinterpret_cast<D2P>(base + 2048u + lane16);
+    c.v[0] = x.x;
+    c.v[1] = x.y;
+    c.v[2] = y.x;
+    c.v[3] = y.y;
   } else {
     typedef float F4 __attribute__((ext_vector_type(4)));
-    const F4 a = *reinterpret_cast<const F4*>(base + 1024u + lane16);
-    c.v[0] = a.x;
-    c.v[1] = a.y;
-    c.v[2] = a.z;
-    c.v[3] = a.w;
+    typedef const __attribute__((address_space(1))) F4* F4P;
+    const F4 x = *reinterpret_cast<F4P>(base + 1024u + lane16);
+    c.v[0] = x.x;
+    c.v[1] = x.y;
+    c.v[2] = x.z;
+    c.v[3] = x.w;
   }
 }
 
 // acc += sum over the chunk's 4 entries of coefficient * gathered element, in order
 template <typename T, typename V>
-__device__ __forceinline__ void consume_chunk(const Chunk<T>& c, const unsigned char* lds, V& acc) {
+__device__ __forceinline__ void consume_chunk(const Chunk<T>& c, V& acc) {
   V x[kResChunk];
 #pragma unroll
-  for (int u = 0; u < kResChunk; ++u) x[u] = *reinterpret_cast<const V*>(lds + c.o[u]);
+  for (int u = 0; u < kResChunk; ++u) x[u] = lds_read<V>(c.o[u]);
 #pragma unroll
   for (int u = 0; u < kResChunk; ++u) acc += c.v[u] * x[u];
 }
@@ -127,22 +150,30 @@ __device__ __forceinline__ void consume_chunk(const Chunk<T>& c, const unsigned 
 // stream; on exit b0 holds the chunk after the slot's last one.
 template <typename T, typename V>
 __device__ __forceinline__ V slot_sum(int nch, Chunk<T>& b0, Chunk<T>& b1, uint32_t& pos,
-                                      const unsigned char* __restrict__ stream, uint32_t lane16,
-                                      const unsigned char* lds) {
-  constexpr uint32_t CB = res_chunk_bytes<T>();
+                                      const unsigned char* __restrict__ stream, uint32_t lane16) {
+  constexpr uint64_t CB = res_chunk_bytes<T>();
   V acc = V(T(0));
   for (int k = 0; k < nch; k += 2) {
     const bool two = k + 1 < nch;
     if (two) {
-      load_chunk(b1, stream + (size_t)pos * CB, lane16);
+      load_chunk(b1, stream, pos * CB, lane16);
       ++pos;
     }
-    consume_chunk(b0, lds, acc);
-    load_chunk(b0, stream + (size_t)pos * CB, lane16);
+    consume_chunk(b0, acc);
+    load_chunk(b0, stream, pos * CB, lane16);
     ++pos;
-    if (two) consume_chunk(b1, lds, acc);
+    if (two) consume_chunk(b1, acc);
   }
   return acc;
+}
+
+// jnp.clip(x, lo, hi) for bounds that are not NaN: (x <= lo) is false for a
+// NaN x, which therefore passes through, as minimum(maximum(x, lo), hi) does;
+// ties and signed zeros resolve to the bound, as in clipp.
+template <typename T>
+__device__ __forceinline__ T clip_nonnan_bounds(T x, T lo, T hi) {
+  const T r = x <= lo ? lo : x;
+  return r >= hi ? hi : r;
 }
 
 template <typename T, int SLR, int SLC, bool SB>
@@ -150,7 +181,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   constexpr int NT = 1024;
   constexpr int BT = ResVec<T>::BT;
   using V = typename ResVec<T>::V;
-  extern __shared__ __align__(16) unsigned char lds[];
+  extern __shared__ __align__(16) unsigned char lds[];  // at LDS address 0 (no static LDS)
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -170,14 +201,19 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 
   uint32_t soff_r[SLR], soff_c[SLC];
   V y[SLC], tg[SLC], rr[SLR];
-  uint32_t ineq = 0;
+  uint32_t ineq = 0, nanb = 0;
 #pragma unroll
   for (int c = 0; c < SLC; ++c) {
     const int j = A.colmap[c * NT + t];
+#pragma unroll
+    for (int s = 0; s < BT; ++s) {
+      const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
+      if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
+    }
     soff_c[c] = j >= 0 ? (uint32_t)j * 16u : trash_off;
     tg[c] = j >= 0 ? Ts[c * NT + t] : vzero;
     y[c] = tg[c];  // y0 = ybar0 = yhat (kernels.py:229-231)
-    *reinterpret_cast<V*>(lds + soff_c[c]) = y[c];
+    lds_write<V>(soff_c[c], y[c]);
   }
 #pragma unroll
   for (int r = 0; r < SLR; ++r) {
@@ -185,14 +221,14 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
     soff_r[r] = i >= 0 ? gd_off + (uint32_t)i * 16u : trash_off;
     rr[r] = i >= 0 ? Rs[r * NT + t] : vzero;
     if (i >= A.me) ineq |= 1u << r;  // kept rows: equalities first
-    *reinterpret_cast<V*>(lds + soff_r[r]) = i >= 0 ? D0[r * NT + t] : vzero;
+    lds_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
   }
-  if (t == 0) *reinterpret_cast<V*>(lds + (uint32_t)A.n * 16u) = vzero;  // the zero slot
+  if (t == 0) lds_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
   __syncthreads();
 
   constexpr uint32_t CB = res_chunk_bytes<T>();
   Chunk<T> b0, b1;
-  load_chunk(b0, A.stream + (size_t)first * CB, lane16);
+  load_chunk(b0, A.stream, (uint64_t)first * CB, lane16);
 
   for (int64_t it = 0; it < A.iters; ++it) {
     // wave-uniform schedule scalars: scalar loads through the constant address space
@@ -204,14 +240,14 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
       const int nch = (int)((rcnt >> (8 * r)) & 255u);
-      const V dold = *reinterpret_cast<const V*>(lds + soff_r[r]);
-      const V acc = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16, lds);
+      const V dold = lds_read<V>(soff_r[r]);
+      const V acc = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
       V p = dold + sigma * (acc - rr[r]);
       if (ineq & (1u << r)) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
       }
-      *reinterpret_cast<V*>(lds + soff_r[r]) = p;
+      lds_write<V>(soff_r[r], p);
     }
     __syncthreads();
     // ---- column pass (reads Gd, writes Gy) --------------------------------------
@@ -220,23 +256,30 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       const int nch = (int)((ccnt >> (8 * c)) & 255u);
       // bounds are re-read each iteration (L2-resident when shared) rather
       // than held in registers: the opaque base keeps them inside the loop
-      const T* lb = A.Ls;
-      const T* hb = A.Hs;
+      typedef const __attribute__((address_space(1))) T* GP;
+      GP lb = (GP)A.Ls;
+      GP hb = (GP)A.Hs;
       asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
       if (SB) {
         lo = V(lb[c * NT + t]);
         hi = V(hb[c * NT + t]);
       } else {
-        lo = reinterpret_cast<const V*>(lb)[tile * (int64_t)A.Kc + c * NT + t];
-        hi = reinterpret_cast<const V*>(hb)[tile * (int64_t)A.Kc + c * NT + t];
+        typedef const __attribute__((address_space(1))) V* GV;
+        lo = ((GV)lb)[tile * (int64_t)A.Kc + c * NT + t];
+        hi = ((GV)hb)[tile * (int64_t)A.Kc + c * NT + t];
       }
-      const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16, lds);
+      const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
       const V sv = a * y[c] - delta * tt + delta * tg[c];
       V yn;
+      if (nanb & (1u << c)) {  // a NaN bound on this lane: the exact NaN-propagating clip
 #pragma unroll
-      for (int s = 0; s < BT; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
-      *reinterpret_cast<V*>(lds + soff_c[c]) = yn + theta * (yn - y[c]);
+        for (int s = 0; s < BT; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
+      } else {
+#pragma unroll
+        for (int s = 0; s < BT; ++s) yn[s] = clip_nonnan_bounds(sv[s], lo[s], hi[s]);
+      }
+      lds_write<V>(soff_c[c], yn + theta * (yn - y[c]));
       y[c] = yn;
     }
     __syncthreads();
@@ -254,7 +297,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   for (int r = 0; r < SLR; ++r) {
     const int i = A.rowmap[r * NT + t];
     if (i >= 0) {
-      const V d = *reinterpret_cast<const V*>(lds + soff_r[r]);
+      const V d = lds_read<V>(soff_r[r]);
 #pragma unroll
       for (int s = 0; s < BT; ++s) A.D[(int64_t)i * A.Bp + b0s + s] = d[s];
     }
