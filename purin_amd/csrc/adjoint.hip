@@ -31,7 +31,8 @@ namespace purin {
 
 constexpr int kChunk = 64;        // rows per Gram--Schmidt block
 constexpr int kRowsPerThread = kChunk / 4;
-constexpr int kMaxRestart = 128;  // per-sample scalar kernels keep a column in registers/scratch
+constexpr int kMaxRestart = 128;    // restart cap (Hessenberg workspace grows as restart^2)
+constexpr int kStepCheck = 8;       // Arnoldi steps between host reads of the active count
 
 template <typename T>
 struct Adj {
@@ -382,6 +383,55 @@ __global__ __launch_bounds__(kBlock) void k_gs_pass(const T* __restrict__ basis,
   }
 }
 
+// The first Gram--Schmidt pass, part_i = V_i . x, with the prefix vectors split
+// across the block's 4 wavefronts: wavefront w owns V_i for i = w, w+4, ... and
+// walks all rows of the block's chunk, loading x itself (the four loads of a
+// row hit L2 together).  Each wavefront writes the partial sums of its own
+// vectors, so there is no cross-wavefront combine; every load is a coalesced
+// 1 KB wavefront access.
+template <typename T, int NV>
+__global__ __launch_bounds__(kBlock) void k_gs_dots(const T* __restrict__ basis, int64_t vstride,
+                                                    int nv, const T* __restrict__ x, int64_t W,
+                                                    int64_t Bp, T* part, int nchunk, int64_t rpb) {
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  constexpr int NW = NV / 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  const int c = blockIdx.y;
+  // every load is issued unconditionally (a vector index past the prefix is
+  // clamped to the last vector, an L2 hit) so all NW loads of a row are in
+  // flight together; the accumulation is masked instead
+  const T* vp[NW];
+  bool own[NW];
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    own[j] = wave + 4 * j < nv;
+    vp[j] = basis + (size_t)std::min(wave + 4 * j, nv - 1) * vstride;
+  }
+  V acc[NW];
+#pragma unroll
+  for (int j = 0; j < NW; ++j) acc[j] = vsplat<T>(T(0));
+  const int64_t r_begin = (int64_t)c * rpb;
+  const int64_t r_end = std::min<int64_t>(W, r_begin + rpb);
+  for (int64_t r = r_begin; r < r_end; ++r) {
+    const size_t off = (size_t)r * Bp + b0;
+    const V xr = vload(x + off);
+    V v[NW];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) v[j] = vload(vp[j] + off);
+    __builtin_amdgcn_sched_barrier(0);  // issue all loads of the row before any FMA
+#pragma unroll
+    for (int j = 0; j < NW; ++j)
+      if (own[j]) acc[j] += v[j] * xr;
+  }
+  const size_t plane = (size_t)nchunk * Bp;
+#pragma unroll
+  for (int j = 0; j < NW; ++j)
+    if (own[j]) vstore(part + (size_t)(wave + 4 * j) * plane + (size_t)c * Bp + b0, acc[j]);
+}
+
 // The second Gram--Schmidt pass (x <- x - sum_i h_i V_i, then part_i = V_i . x)
 // with the prefix vectors split across the block's 4 wavefronts instead of
 // the rows: wavefront w holds V_i for i = w, w+4, ... of two rows at a time
@@ -536,12 +586,13 @@ struct Gm {
   int32_t* steps;
   int32_t* keep;
   T* scale;
-  T* H;          // [b][(restart+1) * restart]
+  T* H;          // [(restart+1)][restart][Bp]: H[i][j] of sample b at (i*restart + j)*Bp + b
   T* cs;         // [restart][Bp]
   T* sn;
   T* g;          // [(restart+1)][Bp]
   T* coeff;      // [restart][Bp] (back-substitution output)
-  int32_t* counter;  // [0] active count, [1] unconverged count
+  int32_t* counter;  // [0] active count at a cycle's start, [1] unconverged count
+  int32_t* stepcnt;  // [restart+1]: samples active at the start of Arnoldi step s
 };
 
 template <typename T>
@@ -575,50 +626,47 @@ __global__ void k_gm_cycle_init(Gm<T> G, const T* __restrict__ beta2) {
     G.sn[(size_t)i * G.Bp + b] = T(0);
   }
   for (int i = 0; i <= R; ++i) G.g[(size_t)i * G.Bp + b] = i == 0 ? beta : T(0);
-  T* Hb = G.H + (size_t)b * (R + 1) * R;
-  for (int i = 0; i < (R + 1) * R; ++i) Hb[i] = T(0);
-  if (c) atomicAdd(&G.counter[0], 1);
+  for (int i = 0; i < (R + 1) * R; ++i) G.H[(size_t)i * G.Bp + b] = T(0);
+  if (c) atomicAdd(&G.stepcnt[0], 1);
 }
 
 // One Arnoldi step's scalar work for iteration ``it`` (operators.py:996-1081).
+// The Hessenberg column (h1 + h2 up to row it, the new norm at row it + 1) is
+// rotated by the earlier Givens pairs in one streaming sweep that carries the
+// lower entry: rotation ri only touches rows ri and ri + 1.
 template <typename T>
 __global__ void k_gm_givens(Gm<T> G, int it, const T* __restrict__ h1, const T* __restrict__ h2,
                             const T* __restrict__ nrm2, const T* __restrict__ fin) {
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= G.Bp) return;
   const int R = G.restart;
+  const int64_t Bp = G.Bp;
   const T eps = T(1e-30), brk = T(1e-14);
   const int active = G.act[b];
   G.keep[b] = active;
-  T col[kMaxRestart + 1];
-  for (int i = 0; i < R; ++i)
-    col[i] = i <= it ? h1[(size_t)i * G.Bp + b] + h2[(size_t)i * G.Bp + b] : T(0);
-  col[R] = T(0);
   const T next_norm = __builtin_sqrt(nrm2[b]);
-  col[it + 1] = next_norm;
+  T carry = h1[b] + h2[b];  // row 0 of the column
   for (int ri = 0; ri < it; ++ri) {
-    const T c = G.cs[(size_t)ri * G.Bp + b], s = G.sn[(size_t)ri * G.Bp + b];
-    const T f = col[ri], sc = col[ri + 1];
-    col[ri] = c * f + s * sc;
-    col[ri + 1] = -s * f + c * sc;
+    const T c = G.cs[(size_t)ri * Bp + b], s = G.sn[(size_t)ri * Bp + b];
+    const T f = carry, sc = h1[(size_t)(ri + 1) * Bp + b] + h2[(size_t)(ri + 1) * Bp + b];
+    if (active) G.H[((size_t)ri * R + it) * Bp + b] = c * f + s * sc;
+    carry = -s * f + c * sc;
   }
-  const T diag = col[it], sub = col[it + 1];
+  const T diag = carry, sub = next_norm;
   const T rnorm = hypotv(diag, sub);
   const T safe = maxp(rnorm, eps);
   const T nc = rnorm > eps ? diag / safe : T(1);
   const T ns = rnorm > eps ? sub / safe : T(0);
-  const T pc = G.g[(size_t)it * G.Bp + b], pn = G.g[(size_t)(it + 1) * G.Bp + b];
+  const T pc = G.g[(size_t)it * Bp + b], pn = G.g[(size_t)(it + 1) * Bp + b];
   const T rc = nc * pc + ns * pn;
   const T rn = -ns * pc + nc * pn;
   if (active) {
-    G.cs[(size_t)it * G.Bp + b] = nc;
-    G.sn[(size_t)it * G.Bp + b] = ns;
-    col[it] = rnorm;
-    col[it + 1] = T(0);
-    T* Hb = G.H + (size_t)b * (R + 1) * R;
-    for (int i = 0; i <= R; ++i) Hb[(size_t)i * R + it] = col[i];
-    G.g[(size_t)it * G.Bp + b] = rc;
-    G.g[(size_t)(it + 1) * G.Bp + b] = rn;
+    G.cs[(size_t)it * Bp + b] = nc;
+    G.sn[(size_t)it * Bp + b] = ns;
+    G.H[((size_t)it * R + it) * Bp + b] = rnorm;
+    G.H[((size_t)(it + 1) * R + it) * Bp + b] = T(0);
+    G.g[(size_t)it * Bp + b] = rc;
+    G.g[(size_t)(it + 1) * Bp + b] = rn;
     G.steps[b] = it + 1;
   }
   const T est = absv(rn);
@@ -627,29 +675,38 @@ __global__ void k_gm_givens(Gm<T> G, int it, const T* __restrict__ h1, const T* 
   const int still = (active && finite_ok && !happy && est > G.thr[b]) ? 1 : 0;
   G.act[b] = still;
   G.scale[b] = T(1) / maxp(next_norm, eps);
-  if (still && b < G.batch) atomicAdd(&G.counter[0], 1);
+  if (still && b < G.batch) atomicAdd(&G.stepcnt[it + 1], 1);
 }
 
-// Back substitution (operators.py:902-917).
+// Back substitution (operators.py:902-917), one thread per sample in blocks of
+// 64; the partial solution stays in LDS (restart x 64 entries, dynamic), and
+// the zero entries of the trailing sum (columns at or left of the row and
+// beyond the sample's steps) are skipped.
 template <typename T>
-__global__ void k_gm_backsub(Gm<T> G) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(64) void k_gm_backsub(Gm<T> G) {
+  extern __shared__ __align__(16) unsigned char bs_raw[];
+  T* val = reinterpret_cast<T*>(bs_raw);  // [restart][64]
+  const int t = threadIdx.x;
+  const int64_t b = (int64_t)blockIdx.x * 64 + t;
   if (b >= G.Bp) return;
   const int R = G.restart;
+  const int64_t Bp = G.Bp;
   const T eps = T(1e-30);
-  const T* Hb = G.H + (size_t)b * (R + 1) * R;
-  T val[kMaxRestart];
-  for (int i = 0; i < R; ++i) val[i] = T(0);
   const int steps = G.steps[b];
   for (int row = R - 1; row >= 0; --row) {
-    T trailing = T(0);
-    for (int cidx = 0; cidx < R; ++cidx) trailing += Hb[(size_t)row * R + cidx] * val[cidx];
-    const T num = G.g[(size_t)row * G.Bp + b] - trailing;
-    const T d = Hb[(size_t)row * R + row];
-    const T safe = absv(d) > eps ? d : T(1);
-    val[row] = row < steps ? num / safe : T(0);
+    T v = T(0);
+    if (row < steps) {
+      T trailing = T(0);
+      for (int c = row + 1; c < steps; ++c)
+        trailing += G.H[((size_t)row * R + c) * Bp + b] * val[c * 64 + t];
+      const T num = G.g[(size_t)row * Bp + b] - trailing;
+      const T d = G.H[((size_t)row * R + row) * Bp + b];
+      const T safe = absv(d) > eps ? d : T(1);
+      v = num / safe;
+    }
+    val[row * 64 + t] = v;
+    G.coeff[(size_t)row * Bp + b] = v;
   }
-  for (int i = 0; i < R; ++i) G.coeff[(size_t)i * G.Bp + b] = val[i];
 }
 
 template <typename T>
@@ -806,6 +863,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   const int64_t W = 2 * n + m;
   const int restart = (int)std::min<int64_t>({(int64_t)o.restart, (int64_t)o.max_iterations, W});
   if (restart > kMaxRestart) return set_error(PURIN_CP_ERR_UNSUPPORTED, "restart above 128");
+  static_assert((kMaxRestart + 2) * 4 <= kPinnedBytes, "per-step counts must fit the pinned buffer");
   // header written by the forward call
   int64_t hdr[9];
   PURIN_HIP(hipMemcpyAsync(hdr, saved, sizeof(hdr), hipMemcpyDeviceToHost, st));
@@ -856,7 +914,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                oScale = take(Bp * es), oHess = take((size_t)Bp * (restart + 1) * restart * es),
                oCs = take((size_t)restart * Bp * es), oSn = take((size_t)restart * Bp * es),
                oGv = take((size_t)(restart + 1) * Bp * es), oCoef = take((size_t)restart * Bp * es),
-               oCnt = take(256), oLw = take(Bp * es), oGt = take(n * Bp * es),
+               oCnt = take(256), oStepCnt = take((size_t)(restart + 2) * 4), oLw = take(Bp * es), oGt = take(n * Bp * es),
                oGlo = take(n * Bp * es), oGhi = take(n * Bp * es), oGr = take(m * Bp * es),
                oGF = take((size_t)M * Bp * es);
   int err = PURIN_CP_OK;
@@ -876,7 +934,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   Gm<T> G{batch, Bp, restart, (T*)(ws + oThr), (T*)(ws + oRinf), (int32_t*)(ws + oCyc),
           (int32_t*)(ws + oAct), (int32_t*)(ws + oSteps), (int32_t*)(ws + oKeep),
           (T*)(ws + oScale), (T*)(ws + oHess), (T*)(ws + oCs), (T*)(ws + oSn), (T*)(ws + oGv),
-          (T*)(ws + oCoef), (int32_t*)(ws + oCnt)};
+          (T*)(ws + oCoef), (int32_t*)(ws + oCnt), (int32_t*)(ws + oStepCnt)};
 
   Adj<T> S{};
   S.K = kept_matrix<T>(p, true);
@@ -917,6 +975,15 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     *val = p->pinned[idx];
     return PURIN_CP_OK;
   };
+  // active counts at the start of Arnoldi steps [0, upto] of the current cycle
+  auto read_stepcnt = [&](int upto, std::vector<int32_t>& out) -> int {
+    out.resize(upto + 1);
+    PURIN_HIP(hipMemcpyAsync(p->pinned, G.stepcnt, (upto + 1) * sizeof(int32_t),
+                             hipMemcpyDeviceToHost, st));
+    PURIN_HIP(hipStreamSynchronize(st));
+    for (int i = 0; i <= upto; ++i) out[i] = p->pinned[i];
+    return PURIN_CP_OK;
+  };
   auto zero_counters = [&]() { k_fill<int32_t><<<1, 64, 0, st>>>(G.counter, 2, 0); };
   // one round of resident blocks per pass: the chunk count per batch tile is the
   // kernel's resident block count over the tiles (so no partial second round)
@@ -933,14 +1000,29 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                                                                     part, (int)chunks, rpb);
     return PURIN_CP_OK;
   };
+  // the dot pass: two blocks per CU over the batch tiles (the best measured
+  // balance of rows in flight per wavefront against blocks per CU)
+  auto launch_dots = [&](auto kern, int nv, const T* img) -> int {
+    const int64_t chunks = std::max<int64_t>(
+        1, std::min<int64_t>({(int64_t)2 * cus / tiles0, (W + 3) / 4, (int64_t)nchunk2}));
+    const int64_t rpb = (W + chunks - 1) / chunks;
+    last_nchunk = (int)chunks;
+    kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, vstride, nv, img, W, Bp,
+                                                                    part, (int)chunks, rpb);
+    return PURIN_CP_OK;
+  };
   auto gs_pass = [&](int mode, int nv, T* img, const T* h) -> int {
 #define PURIN_GS(MODE, NVB) return launch_gs(k_gs_pass<T, NVB, MODE>, nv, img, h)
     const int bucket = nv <= 8 ? 8 : (nv <= 16 ? 16 : (nv <= 24 ? 24 : 32));
     if (mode == 0) {
+#define PURIN_GD(NVB) return launch_dots(k_gs_dots<T, NVB>, nv, img)
+      // up to 8 vectors the row-split pass is faster: the vector-split one
+      // re-reads x once per wavefront, which dominates for a short prefix
       if (bucket == 8) PURIN_GS(0, 8);
-      if (bucket == 16) PURIN_GS(0, 16);
-      if (bucket == 24) PURIN_GS(0, 24);
-      PURIN_GS(0, 32);
+      if (bucket == 16) PURIN_GD(16);
+      if (bucket == 24) PURIN_GD(24);
+      PURIN_GD(32);
+#undef PURIN_GD
     } else if (mode == 1) {
 #define PURIN_GU(NVB) return launch_gs(k_gs_update_dots<T, NVB>, nv, img, h)
       if (bucket == 8) PURIN_GU(8);
@@ -986,42 +1068,57 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     // beta = ||r||, V0 = r / max(beta, eps)
     k_gs<T, 3><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Rr, nullptr, W, Bp, part, nchunk);
     reduce(1, S1, 0);
-    zero_counters();
+    k_fill<int32_t><<<1, 256, 0, st>>>(G.stepcnt, restart + 2, 0);
     k_gm_cycle_init<T><<<sb, 256, 0, st>>>(G, S1);
     k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, Vb, Rr, G.scale, nullptr);
-    int32_t nactive = 0;
-    if (int rc = read_counter(0, &nactive)) return rc;
-    int it = 0;
-    while (it < cycle_limit && nactive > 0) {
-      T* vk = Vb + (size_t)it * vstride;
-      T* img = Vb + (size_t)(it + 1) * vstride;
-      op(vk, img);
-      // two-pass classical Gram--Schmidt over the active prefix (operators.py:834-871)
-      const int nv = it + 1;
-      if (nv <= 32) {
-        if (int rc = gs_pass(0, nv, img, nullptr)) return rc;
-        reduce2(nv, 0, H1, 0);
-        if (int rc = gs_pass(1, nv, img, H1)) return rc;
-        reduce2(nv, 0, H2, 0);
-        if (int rc = gs_pass(2, nv, img, H2)) return rc;
-        reduce2(1, 0, S1, 0);
-        reduce2(1, 1, S2, 2);
-      } else {
-        k_gs<T, 0><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, nullptr, W, Bp, part, nchunk);
-        reduce(nv, H1, 0);
-        k_gs<T, 1><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, H1, W, Bp, part, nchunk);
-        reduce(nv, H2, 0);
-        k_gs<T, 2><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, H2, W, Bp, part, nchunk);
-        k_reduce<T><<<sb, 256, 0, st>>>(part, 1, nchunk, Bp, S1, 0);
-        k_reduce<T><<<sb, 256, 0, st>>>(part + (size_t)nchunk * Bp, 1, nchunk, Bp, S2, 2);
+    // Arnoldi steps.  The reference loop runs step s while s < cycle_limit and
+    // some sample is active at its start (operators.py:943-1082); a step with
+    // no active sample changes no state here (every update is masked by the
+    // active flags), so the host reads the per-step active counts only every
+    // kStepCheck steps and at the end, and takes the first empty step as the
+    // cycle's length.
+    int launched = 0;
+    std::vector<int32_t> cnt;
+    while (launched < cycle_limit) {
+      const int chunk_end = std::min(cycle_limit, launched + kStepCheck);
+      if (int rc = read_stepcnt(launched, cnt)) return rc;
+      if (cnt[launched] == 0) break;
+      for (int it = launched; it < chunk_end; ++it) {
+        T* vk = Vb + (size_t)it * vstride;
+        T* img = Vb + (size_t)(it + 1) * vstride;
+        op(vk, img);
+        // two-pass classical Gram--Schmidt over the active prefix (operators.py:834-871)
+        const int nv = it + 1;
+        if (nv <= 32) {
+          if (int rc = gs_pass(0, nv, img, nullptr)) return rc;
+          reduce2(nv, 0, H1, 0);
+          if (int rc = gs_pass(1, nv, img, H1)) return rc;
+          reduce2(nv, 0, H2, 0);
+          if (int rc = gs_pass(2, nv, img, H2)) return rc;
+          reduce2(1, 0, S1, 0);
+          reduce2(1, 1, S2, 2);
+        } else {
+          k_gs<T, 0><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, nullptr, W, Bp, part, nchunk);
+          reduce(nv, H1, 0);
+          k_gs<T, 1><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, H1, W, Bp, part, nchunk);
+          reduce(nv, H2, 0);
+          k_gs<T, 2><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, H2, W, Bp, part, nchunk);
+          k_reduce<T><<<sb, 256, 0, st>>>(part, 1, nchunk, Bp, S1, 0);
+          k_reduce<T><<<sb, 256, 0, st>>>(part + (size_t)nchunk * Bp, 1, nchunk, Bp, S2, 2);
+        }
+        k_gm_givens<T><<<sb, 256, 0, st>>>(G, it, H1, H2, S1, S2);
+        k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, img, img, G.scale, G.keep);
       }
-      zero_counters();
-      k_gm_givens<T><<<sb, 256, 0, st>>>(G, it, H1, H2, S1, S2);
-      k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, img, img, G.scale, G.keep);
-      ++it;
-      if (int rc = read_counter(0, &nactive)) return rc;
+      launched = chunk_end;
     }
-    k_gm_backsub<T><<<sb, 256, 0, st>>>(G);
+    int it = launched;
+    if (int rc = read_stepcnt(launched, cnt)) return rc;
+    for (int s2 = 0; s2 < launched; ++s2)
+      if (cnt[s2] == 0) {
+        it = s2;
+        break;
+      }
+    k_gm_backsub<T><<<(unsigned)(Bp / 64), 64, (size_t)restart * 64 * sizeof(T), st>>>(G);
     k_correction<T><<<eb, 256, 0, st>>>(total, Bp, X, Vb, vstride, G.coeff, G.steps);
     // candidate residual r = g - A x (operators.py:1084-1091)
     op(X, T1);

@@ -500,7 +500,7 @@ int purin_cp_plan_create(purin_cp_plan** out, int32_t dtype, int64_t n, int64_t 
   int rc = dtype == PURIN_CP_F64 ? build<double>(p, indptr, indices, values)
                                  : build<float>(p, indptr, indices, values);
   if (rc == PURIN_CP_OK) {
-    hipError_t e = hipHostMalloc((void**)&p->pinned, 64, hipHostMallocDefault);
+    hipError_t e = hipHostMalloc((void**)&p->pinned, kPinnedBytes, hipHostMallocDefault);
     if (e != hipSuccess) rc = hip_check(e, "hipHostMalloc");
   }
   if (rc != PURIN_CP_OK) {
