@@ -77,7 +77,8 @@ typedef struct {
   int32_t norm_bound;               /* sparse norm bound for the steps (default 1) */
   int32_t norm_iterations;          /* power iterations for the adjoint steps (default 20) */
   int32_t norm_seed;                /* start-vector seed (default 42) */
-  int32_t diagonal_preconditioning; /* must be 0: not implemented (returns UNSUPPORTED) */
+  int32_t diagonal_preconditioning; /* per-row/per-column steps when not accelerated
+                                       (kernels.py:76-88, 209-210; default 0) */
   double safety;                    /* step safety factor in (0,1) (default 0.95) */
 } purin_cp_options;
 

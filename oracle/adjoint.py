@@ -49,9 +49,9 @@ class Linearization(NamedTuple):
     mask: np.ndarray
     me: int
     n: int
-    a: np.ndarray          # (B, 1) prox inverse
-    delta: np.ndarray      # (B, 1) prox dual weight
-    sigma: np.ndarray      # (B, 1)
+    a: np.ndarray          # (B, 1) prox inverse, or (B, n) for diagonal steps
+    delta: np.ndarray      # (B, 1) prox dual weight, or (B, n)
+    sigma: np.ndarray      # (B, 1), or (B, m) for diagonal steps
     D: np.ndarray          # dual projection derivative (B, m)
     C: np.ndarray          # clip derivative w.r.t. its argument (B, n)
     Clo: np.ndarray        # clip derivative w.r.t. lower (B, n)
@@ -61,11 +61,15 @@ class Linearization(NamedTuple):
 
 
 def linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma):
-    """Masks of ``cp_step`` at ``z = (y, dual, y)`` with theta = 1 (bounds.py:109-128)."""
+    """Masks of ``cp_step`` at ``z = (y, dual, y)`` with theta = 1 (bounds.py:109-128).
+
+    ``tau``/``sigma`` are per sample ``(B,)`` or, with diagonal preconditioning,
+    per variable ``(B, n)`` and per row ``(B, m)`` (bounds.py:83-86).
+    """
     dtype = y.dtype
     n = y.shape[1]
     mv, tmv = _cp.operators(values, support, mask, n)
-    sig = sigma[:, None]
+    sig = sigma[:, None] if np.ndim(sigma) == 1 else sigma
     p = dual + sig * (mv(y) - rhs)
     _, dpi, _ = _max_grads(p[:, me:], dtype.type(0))
     D = np.concatenate((np.ones_like(p[:, :me]), dpi.astype(dtype)), axis=1)
@@ -78,8 +82,10 @@ def linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau
     C = (dm1 * ds).astype(dtype)
     Clo = (dm1 * dlo).astype(dtype)
     Chi = dhi.astype(dtype)
-    return Linearization(values, support, mask, me, n, a[:, :1], delta[:, :1], sig, D, C,
-                         Clo, Chi, y.copy(), dplus)
+    if np.ndim(tau) == 1:
+        a, delta = a[:, :1], delta[:, :1]
+    return Linearization(values, support, mask, me, n, a, delta, sig, D, C, Clo, Chi, y.copy(),
+                         dplus)
 
 
 class Pullback(NamedTuple):
@@ -104,14 +110,23 @@ def pullback(lin, gy, gd, gb):
     mv, tmv = _cp.operators(lin.values, lin.support, lin.mask, lin.n)
     G = gy + 2 * gb
     u = lin.C * G
-    w = lin.D * (gd - lin.delta * mv(u))
+    diagonal = lin.delta.shape[1] > 1 or lin.sigma.shape[1] > 1
+    if diagonal:
+        # per-variable delta and per-row sigma: delta K u -> K (delta u) and
+        # sigma K^T w -> K^T (sigma w)
+        w = lin.D * (gd - mv(lin.delta * u))
+        gz_b = tmv(lin.sigma * w)
+    else:
+        w = lin.D * (gd - lin.delta * mv(u))
+        gz_b = lin.sigma * tmv(w)
     gz_y = lin.a * u - gb
     gz_d = w
-    gz_b = lin.sigma * tmv(w)
     ybar_g = lin.ybar[:, lin.support]
     u_g = u[:, lin.support]
+    delta_g = (np.broadcast_to(lin.delta, u.shape)[:, lin.support] if diagonal
+               else lin.delta[:, :, None])
     g_values = np.where(lin.mask[None], lin.sigma[:, :, None] * w[:, :, None] * ybar_g
-                        - lin.delta[:, :, None] * lin.dplus[:, :, None] * u_g, 0)
+                        - delta_g * lin.dplus[:, :, None] * u_g, 0)
     return Pullback(gz_y, gz_d, gz_b, g_values, -lin.sigma * w, lin.delta * u,
                     lin.Clo * G, lin.Chi * G)
 
@@ -258,8 +273,6 @@ def adjoint(values, support, mask, me, y, dual, converged, target, rhs, lower, u
     batch, n = y.shape
     m = dual.shape[1]
     tau, sigma = adjoint_steps(values, support, mask, n, batch, dtype, cfg) if steps is None else steps
-    if np.ndim(tau) == 2 or np.ndim(sigma) == 2:
-        raise NotImplementedError("diagonal-metric adjoint steps are not restated")
     lin = linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma)
 
     def operator(v):

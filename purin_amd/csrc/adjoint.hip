@@ -40,6 +40,12 @@ struct Adj {
   int64_t Bp;
   int n, m;
   T a, delta, sigma;
+  // diagonal steps (bounds.py:83-86): per-column a, delta and per-row sigma
+  // replace the scalars when set.  The VJP's delta K u and sigma K^T w then
+  // read K (delta . u) and K^T (sigma . w): U and Wv hold the scaled vectors.
+  const T* a_c;    // n or nullptr
+  const T* d_c;    // n or nullptr
+  const T* sig_r;  // m or nullptr
   const T* Cm;   // n x Bp
   const T* Dm;   // m x Bp
   T* U;          // n x Bp scratch (u)
@@ -77,7 +83,8 @@ __global__ __launch_bounds__(kBlock) void k_lin_rows(Adj<T> S, const T* __restri
     for (int k = S.K.rptr[i]; k < S.K.rptr[i + 1]; ++k)
       acc += S.K.rval[k] * vload(Y + (size_t)S.K.ridx[k] * S.Bp + b0);
     const size_t off = (size_t)i * S.Bp + b0;
-    const V p = vload(Dd + off) + S.sigma * (acc - vload(R + off));
+    const T sg = S.sig_r ? S.sig_r[i] : S.sigma;
+    const V p = vload(Dd + off) + sg * (acc - vload(R + off));
     V dm, dp;
 #pragma unroll
     for (int s = 0; s < Sn; ++s) {
@@ -114,7 +121,8 @@ __global__ __launch_bounds__(kBlock) void k_lin_cols(Adj<T> S, const T* __restri
       t += S.K.cval[k] * vload(dplus + (size_t)S.K.cidx[k] * S.Bp + b0);
     const size_t off = (size_t)j * S.Bp + b0;
     const V y = vload(Y + off);
-    const V s = S.a * y - S.delta * t + S.delta * vload(tgt + off);
+    const T aj = S.a_c ? S.a_c[j] : S.a, dj = S.d_c ? S.d_c[j] : S.delta;
+    const V s = aj * y - dj * t + dj * vload(tgt + off);
     V lo, hi;
     if (shared_bounds) {
       lo = vsplat<T>(LO[j]);
@@ -151,8 +159,14 @@ __global__ __launch_bounds__(kBlock) void k_op_cols1(Adj<T> S, const T* __restri
        e += (int64_t)gridDim.x * blockDim.x) {
     const T gy = v[e], gb = v[boff + e];
     const T u = S.Cm[e] * (gy + T(2) * gb);
-    S.U[e] = u;
-    out[e] = gy - (S.a * u - gb);
+    if (S.a_c) {
+      const int64_t j = e / S.Bp;
+      S.U[e] = S.d_c[j] * u;
+      out[e] = gy - (S.a_c[j] * u - gb);
+    } else {
+      S.U[e] = u;
+      out[e] = gy - (S.a * u - gb);
+    }
   }
 }
 
@@ -173,9 +187,15 @@ __global__ __launch_bounds__(kBlock) void k_op_rows(Adj<T> S, const T* __restric
     const size_t off = (size_t)i * S.Bp + b0;
     const size_t voff = (size_t)(S.n + i) * S.Bp + b0;
     const V gd = vload(v + voff);
-    const V w = vload(S.Dm + off) * (gd - S.delta * acc);
-    vstore(S.Wv + off, w);
-    vstore(out + voff, gd - w);
+    if (S.sig_r) {
+      const V w = vload(S.Dm + off) * (gd - acc);
+      vstore(S.Wv + off, S.sig_r[i] * w);
+      vstore(out + voff, gd - w);
+    } else {
+      const V w = vload(S.Dm + off) * (gd - S.delta * acc);
+      vstore(S.Wv + off, w);
+      vstore(out + voff, gd - w);
+    }
   }
 }
 
@@ -194,7 +214,10 @@ __global__ __launch_bounds__(kBlock) void k_op_cols2(Adj<T> S, const T* __restri
     for (int k = S.K.cptr[j]; k < S.K.cptr[j + 1]; ++k)
       acc += S.K.cval[k] * vload(S.Wv + (size_t)S.K.cidx[k] * S.Bp + b0);
     const size_t off = (size_t)(S.n + S.m + j) * S.Bp + b0;
-    vstore(out + off, vload(v + off) - S.sigma * acc);
+    if (S.sig_r)
+      vstore(out + off, vload(v + off) - acc);
+    else
+      vstore(out + off, vload(v + off) - S.sigma * acc);
   }
 }
 
@@ -764,8 +787,8 @@ __global__ void k_final_u(Adj<T> S, const T* __restrict__ lam, const T* __restri
     const T gy = w != T(0) ? lam[e] : T(0), gb = w != T(0) ? lam[boff + e] : T(0);
     const T G = gy + T(2) * gb;
     const T u = S.Cm[e] * G;
-    S.U[e] = u;
-    const T a = S.delta * u, l = Clo[e] * G, h = Chi[e] * G;
+    const T a = (S.d_c ? S.d_c[e / S.Bp] : S.delta) * u, l = Clo[e] * G, h = Chi[e] * G;
+    S.U[e] = S.d_c ? a : u;
     gt[e] = finite(a) ? a : T(0);
     glo[e] = finite(l) ? l : T(0);
     ghi[e] = finite(h) ? h : T(0);
@@ -792,8 +815,9 @@ __global__ __launch_bounds__(kBlock) void k_final_w(Adj<T> S, const T* __restric
 #pragma unroll
     for (int s = 0; s < Sn; ++s) {
       const T lw = lam_w[b0 + s];
-      const T w = S.Dm[off + s] * ((lw != T(0) ? gd[s] : T(0)) - S.delta * acc[s]);
-      const T r = -S.sigma * w;
+      const T w = S.sig_r ? S.Dm[off + s] * ((lw != T(0) ? gd[s] : T(0)) - acc[s])
+                          : S.Dm[off + s] * ((lw != T(0) ? gd[s] : T(0)) - S.delta * acc[s]);
+      const T r = -(S.sig_r ? S.sig_r[i] : S.sigma) * w;
       out[s] = finite(r) ? r : T(0);
     }
     vstore(gr + off, out);
@@ -945,6 +969,11 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   S.sigma = (T)p->sigma_adj;
   S.a = T(1) / (T(1) + tau);
   S.delta = tau * S.a;
+  if (p->diag) {  // the forward's diagonal steps (bounds.py:83-86)
+    S.a_c = (const T*)p->diag_a;
+    S.d_c = (const T*)p->diag_d;
+    S.sig_r = (const T*)p->diag_sig;
+  }
   S.Cm = (const T*)(ws + oCm);
   S.Dm = (const T*)(ws + oDm);
   S.U = (T*)(ws + oU);

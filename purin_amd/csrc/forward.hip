@@ -239,13 +239,19 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   A.rowpart = (T*)(ws + L.rowpart);
   A.ncb = L.ncb;
   A.nrb = L.nrb;
+  if (p->diag) {  // diagonal steps (non-accelerated, so constant over the loop)
+    A.sig_r = (const T*)p->diag_sig;
+    A.a_c = (const T*)p->diag_a;
+    A.d_c = (const T*)p->diag_d;
+  }
   int32_t* done = (int32_t*)(ws + L.done);
   int32_t* count = (int32_t*)(ws + L.count);
   int32_t* ndone = (int32_t*)(ws + L.ndone);
   const int m = A.K.m, n = A.K.n;
   const bool early = o.early_stop != 0;
   const size_t lds = resident_lds<T>(p);
-  if (!early && lds && !o.streaming) {
+  // the resident kernel takes one schedule of scalar steps for the whole tile
+  if (!early && lds && !o.streaming && !p->diag) {
     if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds)) return rc;
     const int32_t cnt = (int32_t)o.max_iterations;
     k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);

@@ -46,6 +46,11 @@ struct Iter {
   int shared_bounds;
   const int32_t* done;        // Bp, or nullptr
   T sigma, a, delta, theta;
+  // diagonal steps (kernels.py:76-88): per-row sigma and per-column a, delta
+  // replace the scalars when set
+  const T* __restrict__ sig_r;  // m or nullptr
+  const T* __restrict__ a_c;    // n or nullptr
+  const T* __restrict__ d_c;    // n or nullptr
   T* colpart;                 // [5][ncb][Bp]: primal, dual, stat, bound, finite
   T* rowpart;                 // [3][nrb][Bp]: residual max, r.d, finite
   int ncb, nrb;
@@ -79,7 +84,8 @@ __global__ __launch_bounds__(kBlock) void k_row_pass(Iter<T> A) {
     T* dp = A.D + (size_t)i * A.Bp + b0;
     const V d = vload(dp);
     const V r = vload(A.R + (size_t)i * A.Bp + b0);
-    V p = d + A.sigma * (acc - r);
+    const T sg = A.sig_r ? A.sig_r[i] : A.sigma;
+    V p = d + sg * (acc - r);
     if (i >= A.K.me) {
 #pragma unroll
       for (int s = 0; s < S; ++s) p[s] = maxp(p[s], T(0));
@@ -137,7 +143,8 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
       if (MODE == 2) {
         yn = y;
       } else {
-        const V sv = A.a * y - A.delta * t + A.delta * tg;
+        const T aj = A.a_c ? A.a_c[j] : A.a, dj = A.d_c ? A.d_c[j] : A.delta;
+        const V sv = aj * y - dj * t + dj * tg;
 #pragma unroll
         for (int s = 0; s < S; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
         V yb = yn + A.theta * (yn - y);

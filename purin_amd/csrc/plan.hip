@@ -179,6 +179,33 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
     if (!p->opts.norm_bound) norm = T(0);  // replaced by the power iteration below
     p->L = (double)norm;
   }
+  // --- diagonal steps (kernels.py:76-88), when diagonal_preconditioning and not
+  // accelerated (kernels.py:209-210; the adjoint likewise, bounds.py:83-86):
+  // tau_j = safety / colsum_j, sigma_i = safety / rowsum_i of |K~| (a zero sum
+  // becomes 1, a positive one at least 1e-12); with q = 1 the prox coefficients
+  // are a_j = 1/(1 + tau_j), delta_j = tau_j a_j (kernels.py:68-73)
+  std::vector<T> dsig, da, dd;
+  p->diag = p->opts.diagonal_preconditioning && !p->opts.accelerated;
+  if (p->diag) {
+    dsig.resize(m);
+    da.resize(n);
+    dd.resize(n);
+    const T tiny = (T)1e-12, one = T(1);
+    for (int64_t i = 0; i < m; ++i) {
+      T s = T(0);
+      for (int32_t k = H.ptr[i]; k < H.ptr[i + 1]; ++k) s = s + std::fabs(H.val_s[k]);
+      s = s > T(0) ? std::max(s, tiny) : one;
+      dsig[i] = safety / s;
+    }
+    for (int64_t j = 0; j < n; ++j) {
+      T s = T(0);
+      for (int32_t k = H.cptr[j]; k < H.cptr[j + 1]; ++k) s = s + std::fabs(H.cval_s[k]);
+      s = s > T(0) ? std::max(s, tiny) : one;
+      const T tau = safety / s;
+      da[j] = one / (one + tau);
+      dd[j] = tau * da[j];
+    }
+  }
   // --- power iteration on K^T K (kernels.py:52-65) ----------------------------
   T Lpi;
   {
@@ -402,6 +429,11 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
   UP(p->cval_s, H.cval_s);
   UP(p->cval_o, H.cval_o);
   UP(p->dscale, scale);
+  if (p->diag) {
+    UP(p->diag_sig, dsig);
+    UP(p->diag_a, da);
+    UP(p->diag_d, dd);
+  }
   UP(p->dkept, kept32);
   UP(p->bptr, bptr);
   UP(p->brow, brow32);
@@ -487,9 +519,6 @@ int purin_cp_plan_create(purin_cp_plan** out, int32_t dtype, int64_t n, int64_t 
   if (!(o.safety > 0.0 && o.safety < 1.0))
     return set_error(PURIN_CP_ERR_ARG, "safety must be between zero and one");
   if (o.norm_iterations < 1) return set_error(PURIN_CP_ERR_ARG, "norm_iterations must be a positive integer");
-  if (o.diagonal_preconditioning && !o.accelerated)
-    return set_error(PURIN_CP_ERR_UNSUPPORTED,
-                     "diagonal_preconditioning is not implemented by the HIP path");
   auto* p = new purin_cp_plan();
   p->dtype = dtype;
   p->n = n;

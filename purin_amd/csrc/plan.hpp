@@ -51,6 +51,12 @@ struct purin_cp_plan {
   int32_t* brow = nullptr;  // original row of each bound row
   void* dbcoef = nullptr;   // coefficient of each bound row
   void* metric = nullptr;   // sqrt(D) (n) or nullptr
+  // diagonal preconditioning (non-accelerated): per-row sigma (m), per-column
+  // prox coefficients a and delta (n); nullptr when the steps are scalars
+  bool diag = false;
+  void* diag_sig = nullptr;
+  void* diag_a = nullptr;
+  void* diag_d = nullptr;
   std::vector<double> metric_host;
 
   // plan-owned workspace (grown on demand)

@@ -116,8 +116,6 @@ class PreparedChambollePockProjection:
         self.device = resolve_device(self.backend)
         self.torch_dtype = resolve_dtype(self.dtype)
         cfg = self.config
-        if cfg.diagonal_preconditioning and not cfg.accelerated:
-            raise NotImplementedError("diagonal_preconditioning is not implemented by the HIP path")
         values = c.values
         self.metric = None
         if cfg.metric_diagonal is not None and not all(v == 1.0 for v in cfg.metric_diagonal):
@@ -130,7 +128,9 @@ class PreparedChambollePockProjection:
         self.plan = Plan(c.n, c.me, c.mi, c.indptr, c.indices, values, dtype=self.torch_dtype,
                          accelerated=cfg.accelerated, row_scaling=cfg.row_scaling,
                          norm_bound=cfg.norm_bound, norm_iterations=cfg.norm_iterations,
-                         norm_seed=cfg.norm_seed, safety=cfg.safety, device=self.device)
+                         norm_seed=cfg.norm_seed, safety=cfg.safety,
+                         diagonal_preconditioning=cfg.diagonal_preconditioning,
+                         device=self.device)
         if self.metric is not None:
             root = np.sqrt(self.metric.astype(np.float64 if self.torch_dtype == torch.float64
                                               else np.float32)).astype(np.float64)

@@ -8,7 +8,9 @@ from oracle import cp
 from tests import _cases
 
 
-def _random_state(seed, n=6, m=5, me=2, B=3):
+def _random_state(seed, n=6, m=5, me=2, B=3, diagonal=False):
+    """A random CP state; ``diagonal`` gives per-variable tau and per-row sigma
+    (diagonal preconditioning, kernels.py:76-88)."""
     rng = np.random.default_rng(seed)
     K = rng.normal(size=(m, n)) * (rng.uniform(size=(m, n)) < 0.6)
     support, mask = cp.layout([tuple(np.flatnonzero(r)) for r in K], n)
@@ -19,6 +21,8 @@ def _random_state(seed, n=6, m=5, me=2, B=3):
     rhs = rng.normal(size=(B, m))
     lower, upper = -np.ones((B, n)), np.ones((B, n))
     tau, sigma = np.full(B, 0.3), np.full(B, 0.4)
+    if diagonal:
+        tau, sigma = rng.uniform(0.1, 0.5, (B, n)), rng.uniform(0.1, 0.5, (B, m))
     return values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma, rng
 
 
@@ -30,10 +34,12 @@ def _step(values, support, mask, me, z, target, rhs, lower, upper, tau, sigma, n
     return np.concatenate(out, axis=1)
 
 
+@pytest.mark.parametrize("diagonal", [False, True])
 @pytest.mark.parametrize("seed", [0, 1, 2])
-def test_pullback_matches_finite_differences(seed):
+def test_pullback_matches_finite_differences(seed, diagonal):
     """The mask-form VJP equals the transpose of the finite-difference Jacobian of cp_step."""
-    values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma, rng = _random_state(seed)
+    values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma, rng = _random_state(
+        seed, diagonal=diagonal)
     B, n = y.shape
     m = dual.shape[1]
     lin = adj.linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma)
@@ -68,8 +74,10 @@ def test_pullback_matches_finite_differences(seed):
                                        atol=1e-7, err_msg=name)
 
 
-def test_pullback_coefficient_gradient_matches_finite_differences():
-    values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma, rng = _random_state(5)
+@pytest.mark.parametrize("diagonal", [False, True])
+def test_pullback_coefficient_gradient_matches_finite_differences(diagonal):
+    values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma, rng = _random_state(
+        5, diagonal=diagonal)
     B, n = y.shape
     m = dual.shape[1]
     lin = adj.linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma)
@@ -130,10 +138,14 @@ def test_adjoint_independent_of_step_sizes():
     ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
     g = np.array([[0.3, -1.0, 0.5]])
     grads = []
-    for steps in (None, (np.array([0.05]), np.array([0.2])), (np.array([0.4]), np.array([0.5]))):
+    m = len(pre.rows)
+    diag = (np.array([[0.1, 0.3, 0.2]]), np.linspace(0.15, 0.45, m)[None])  # per-variable / row
+    for steps in (None, (np.array([0.05]), np.array([0.2])), (np.array([0.4]), np.array([0.5])),
+                  diag):
         a = adj.adjoint(pre.kept_values, ksup, kmask, canon.me, out.y, out.dual, out.converged,
                         x, pre.kept_rhs, pre.lower, pre.upper, g, cfg, steps=steps)
         assert a.valid[0]
         grads.append(a.g_target)
     np.testing.assert_allclose(grads[1], grads[0], atol=1e-8)
     np.testing.assert_allclose(grads[2], grads[0], atol=1e-8)
+    np.testing.assert_allclose(grads[3], grads[0], atol=1e-8)
