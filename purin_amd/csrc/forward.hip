@@ -258,10 +258,10 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     A.done = nullptr;
     const dim3 gcolE0 = tile_grid(Bp, TS, L.ncb);
     const dim3 gres0 = tile_grid(Bp, TS, std::max(L.nrb, 1));
-    const dim3 gdec0((unsigned)((batch + kBlock - 1) / kBlock));
+    const dim3 gdec0((unsigned)(Bp / 64));  // k_decide: 64 samples per block
     k_col_pass<T, 2, kRowsPerWaveEarly><<<gcolE0, kBlock, 0, st>>>(A);
     if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres0, kBlock, 0, st>>>(A);
-    k_decide<T, true><<<gdec0, kBlock, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
+    k_decide<T, true><<<gdec0, 64 * kDecideGroups, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
                                                 (const int32_t*)(sv + L.feas), (T*)(ws + L.ores),
                                                 (T*)(ws + L.ogap), (int32_t*)(sv + L.conv),
                                                 (int32_t*)(ws + L.ofin));
@@ -279,7 +279,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   const dim3 gcol = tile_grid(Bp, TS, (n + 3) / 4);
   const dim3 gcolE = tile_grid(Bp, TS, L.ncb);
   const dim3 gres = tile_grid(Bp, TS, std::max(L.nrb, 1));
-  const dim3 gdec((unsigned)((batch + kBlock - 1) / kBlock));
+  const dim3 gdec((unsigned)(Bp / 64));  // k_decide: 64 samples per block
   // optional event timing: events[3k] before the row pass, [3k+1] between the
   // passes, [3k+2] after the column pass (and the stop test) of iteration k
   const bool timing = o.timing != 0;
@@ -311,7 +311,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
       k_col_pass<T, 1, kRowsPerWaveEarly><<<gcolE, kBlock, 0, st>>>(A);
       if (timing) PURIN_HIP(hipEventRecord(evd[it], st));
       if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres, kBlock, 0, st>>>(A);
-      k_decide<T, false><<<gdec, kBlock, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
+      k_decide<T, false><<<gdec, 64 * kDecideGroups, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
                                                    nullptr, nullptr, nullptr, nullptr, nullptr);
     }
     if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 2], st));
@@ -363,7 +363,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   A.done = nullptr;
   k_col_pass<T, 2, kRowsPerWaveEarly><<<gcolE, kBlock, 0, st>>>(A);
   if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres, kBlock, 0, st>>>(A);
-  k_decide<T, true><<<gdec, kBlock, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
+  k_decide<T, true><<<gdec, 64 * kDecideGroups, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
                                              (const int32_t*)(sv + L.feas), (T*)(ws + L.ores),
                                              (T*)(ws + L.ogap), (int32_t*)(sv + L.conv),
                                              (int32_t*)(ws + L.ofin));

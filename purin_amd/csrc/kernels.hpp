@@ -249,38 +249,62 @@ __global__ __launch_bounds__(kBlock) void k_res_pass(Iter<T> A) {
   }
 }
 
-// Per-sample reduction of the partials (fixed order), the stop test and the
-// freeze (kernels.py:260-278) or, when FINAL, the final convergence verdict
-// (kernels.py:291-305).
+// Per-sample reduction of the partials, the stop test and the freeze
+// (kernels.py:260-278) or, when FINAL, the final convergence verdict
+// (kernels.py:291-305).  A block of kDecideGroups x 64 threads owns 64
+// samples: group g reduces the column chunks c = g, g + G, ... and the row
+// chunks likewise, in increasing order; the groups then combine in LDS in
+// group order.  Grid: Bp / 64 blocks.
+constexpr int kDecideGroups = 16;
+
 template <typename T, bool FINAL>
-__global__ __launch_bounds__(kBlock) void k_decide(Iter<T> A, int64_t batch, T tol_scalar,
-                                                    const T* __restrict__ tolv, int32_t* done, int32_t* count,
-                                                    int32_t* ndone, const int32_t* feasible,
-                                                    T* out_res, T* out_gap, int32_t* out_conv,
-                                                    int32_t* out_fin) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= batch) return;
-  if (!FINAL && done[b]) return;
+__global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
+    Iter<T> A, int64_t batch, T tol_scalar, const T* __restrict__ tolv, int32_t* done,
+    int32_t* count, int32_t* ndone, const int32_t* feasible, T* out_res, T* out_gap,
+    int32_t* out_conv, int32_t* out_fin) {
+  constexpr int G = kDecideGroups;
+  __shared__ T buf[G][64];
+  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t b = (int64_t)blockIdx.x * 64 + lane;  // < Bp by the grid
   const T zero = T(0);
-  const T tol = tolv ? tolv[b] : tol_scalar;
   const size_t cplane = (size_t)A.ncb * A.Bp, rplane = (size_t)A.nrb * A.Bp;
-  T primal = zero, dualo = zero, stat = zero, bnd = zero, res = zero, rd = zero;
-  bool fin = true;
-  for (int c = 0; c < A.ncb; ++c) {
+  T q[8] = {zero, zero, zero, zero, T(1), zero, zero, T(1)};  // primal, dual, stat, bnd, fin, res, rd, fin_d
+  for (int c = g; c < A.ncb; c += G) {
     const T* p = A.colpart + (size_t)c * A.Bp + b;
-    primal += p[0];
-    dualo += p[cplane];
-    stat = maxp(stat, p[2 * cplane]);
-    bnd = maxp(bnd, p[3 * cplane]);
-    fin = fin && p[4 * cplane] != zero;
+    q[0] += p[0];
+    q[1] += p[cplane];
+    q[2] = maxp(q[2], p[2 * cplane]);
+    q[3] = maxp(q[3], p[3 * cplane]);
+    if (p[4 * cplane] == zero) q[4] = zero;
   }
-  bool fin_d = true;
-  for (int r = 0; r < A.nrb; ++r) {
+  for (int r = g; r < A.nrb; r += G) {
     const T* p = A.rowpart + (size_t)r * A.Bp + b;
-    res = maxp(res, p[0]);
-    rd += p[rplane];
-    fin_d = fin_d && p[2 * rplane] != zero;
+    q[5] = maxp(q[5], p[0]);
+    q[6] += p[rplane];
+    if (p[2 * rplane] == zero) q[7] = zero;
   }
+  // combine the groups in order 0, 1, ..., G-1 (sum for 0, 1, 6; max for 2, 3, 5; and for 4, 7)
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    buf[g][lane] = q[k];
+    __syncthreads();
+    if (g == 0) {
+      T v = buf[0][lane];
+      for (int h = 1; h < G; ++h) {
+        const T o = buf[h][lane];
+        if (k == 0 || k == 1 || k == 6) v += o;
+        else if (k == 2 || k == 3 || k == 5) v = maxp(v, o);
+        else v = (v != zero && o != zero) ? T(1) : zero;
+      }
+      q[k] = v;
+    }
+    __syncthreads();
+  }
+  if (g != 0 || b >= batch) return;
+  if (!FINAL && done[b]) return;
+  const T tol = tolv ? tolv[b] : tol_scalar;
+  const T primal = q[0], dualo = q[1], stat = q[2], bnd = q[3], res = q[5], rd = q[6];
+  const bool fin = q[4] != zero, fin_d = q[7] != zero;
   const T dual_obj = dualo - rd;
   const T gap = maxp(primal - dual_obj, zero) /
                 maxp(T(1), maxp(absv(primal), absv(dual_obj)));
