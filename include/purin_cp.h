@@ -196,6 +196,26 @@ int purin_cp_project(purin_cp_plan* plan, void* stream, int64_t batch, const voi
                      void* slacks, int32_t* status, int32_t* iterations, void* residual,
                      uint8_t* finite, uint8_t* eligible, void* saved);
 
+/*
+ * Full projection with per-sample coefficients: the same rows and sparsity as
+ * the plan, with every sample's own coefficient values.  Replaces
+ * BoundProjection.solve when the coefficients depend on the parameters
+ * (src/purin/solvers/chambolle_pock/bounds.py:192-236: values (B, m_tot, w)
+ * from jax.vmap(_numeric_one); per-sample bounds from the bound rows'
+ * coefficients, per-sample row scales, norm bound, steps and tolerance,
+ * kernels.py:209-227).
+ *   values (B, nnz) in the plan's CSR entry order (indptr/indices given to
+ *   plan_create; the plan's own values are not used by this call).
+ * Other arguments and outputs as purin_cp_project(); opts->shared_bounds must
+ * be 0.  The saved state is for purin_cp_adjoint_values() only.
+ */
+int purin_cp_project_values(purin_cp_plan* plan, void* stream, int64_t batch,
+                            const void* values, const void* target, const void* rhs,
+                            const void* multipliers0, const purin_cp_solve_options* opts,
+                            void* y, void* multipliers, void* slacks, int32_t* status,
+                            int32_t* iterations, void* residual, uint8_t* finite,
+                            uint8_t* eligible, void* saved);
+
 /* Kernel times of the last solve()/project() call made with opts.timing = 1,
  * from HIP events recorded on that call's stream around each launch. */
 typedef struct {
@@ -239,6 +259,21 @@ int purin_cp_adjoint(purin_cp_plan* plan, void* stream, int64_t batch, const voi
                      const purin_cp_adjoint_options* opts, void* g_target, void* g_rhs,
                      void* g_lower, void* g_upper, uint8_t* valid, int32_t* info,
                      void* gmres_residual);
+
+/*
+ * Implicit VJP at the state saved by purin_cp_project_values(), with the
+ * same values (B, nnz).  The adjoint's steps are per sample, from each
+ * sample's scaled matrix (bounds.py:83-101).  Outputs as purin_cp_adjoint()
+ * plus g_values (B, nnz): the gradient w.r.t. values in the plan's CSR entry
+ * order, through the VJP of cp_step w.r.t. the scaled coefficients
+ * (bounds.py:109-141), the row scaling and the bound thresholds
+ * (bounds.py:192-236).  Each output may be NULL.
+ */
+int purin_cp_adjoint_values(purin_cp_plan* plan, void* stream, int64_t batch, const void* saved,
+                            const void* values, const void* cot_y,
+                            const purin_cp_adjoint_options* opts, void* g_target, void* g_rhs,
+                            void* g_values, uint8_t* valid, int32_t* info,
+                            void* gmres_residual);
 
 /* Work done by the last adjoint() call on this plan.  No reference counterpart
  * (the reference's GMRES returns only per-sample info codes); it reports how

@@ -154,20 +154,30 @@ def start_vector(n, seed, dtype):
     return out.astype(dtype)
 
 
+def _sum_in_order(a):
+    """Row sums of ``a`` (B, n) added in column order, each addition rounded."""
+    acc = np.zeros(a.shape[0], a.dtype)
+    for j in range(a.shape[1]):
+        acc = acc + a[:, j]
+    return acc
+
+
 def norm_estimate(mv, tmv, batch, n, dtype, iterations=20, seed=42):
     """Power iteration on ``K^T K``; kernels.py:52-65.
 
-    All samples start from the same ``start_vector`` (see its docstring).
+    All samples start from the same ``start_vector`` (see its docstring).  The
+    dot products add in index order (the HIP library's order; the reference's
+    ``jnp.sum`` leaves its reduction order to XLA).
     """
     dtype = np.dtype(dtype)
     x = np.broadcast_to(start_vector(n, seed, dtype), (batch, n)).copy()
     eps = dtype.type(1e-12)
-    x = x / (np.sqrt(np.sum(x * x, axis=1, keepdims=True)) + eps)
+    x = x / (np.sqrt(_sum_in_order(x * x))[:, None] + eps)
     eig = np.zeros(batch, dtype)
     for _ in range(iterations):
         z = tmv(mv(x))
-        eig = np.sum(x * z, axis=1)
-        x = z / (np.sqrt(np.sum(z * z, axis=1, keepdims=True)) + eps)
+        eig = _sum_in_order(x * z)
+        x = z / (np.sqrt(_sum_in_order(z * z))[:, None] + eps)
     return np.sqrt(np.maximum(eig, dtype.type(0))) + eps
 
 
@@ -297,7 +307,7 @@ def sparse_cp(q, c, values, rhs, support, mask, me, lower, upper, *,
               accelerated=False, safety=0.95, max_iterations=5000, tolerance=1e-9,
               norm_iterations=20, norm_seed=42, y0=None, dual0=None,
               freeze_converged=False, check_stationarity=False, norm_bound=False,
-              diagonal_preconditioning=False, early_stop=True, steps=None):
+              diagonal_preconditioning=False, early_stop=True, steps=None, trace=None):
     """Batched diagonal-QP CP solve; kernels.py:178-305.
 
     ``early_stop=False`` is this build's explicit fixed-iteration mode: the
@@ -305,7 +315,10 @@ def sparse_cp(q, c, values, rhs, support, mask, me, lower, upper, *,
     state with a tolerance too small to be met), so every sample runs exactly
     ``max_iterations`` iterations.  The final diagnostics (kernels.py:291-305)
     still use ``tolerance``.  ``steps`` optionally overrides the initial
-    ``(tau, sigma)``.
+    ``(tau, sigma)``.  ``trace``: a list that receives, per iteration, each
+    sample's stop-test margin ``max(residual, gap[, stationarity]) / tolerance``
+    (test diagnostics: a margin within rounding of 1 marks a sample whose stop
+    iteration rounding can move).
     """
     dtype = q.dtype
     batch, n = q.shape
@@ -339,6 +352,11 @@ def sparse_cp(q, c, values, rhs, support, mask, me, lower, upper, *,
             if check_stationarity:
                 stat = stationarity(ny, nd, q, c, lower, upper, tmv)
                 accepted = accepted & (stat <= tolerance)
+            if trace is not None:
+                worst = np.maximum(residual, gap)
+                if check_stationarity:
+                    worst = np.maximum(worst, stat)
+                trace.append(worst / tolerance)
         y = np.where(active[:, None], ny, y)
         dual = np.where(active[:, None], nd, dual)
         ybar = np.where(active[:, None], nb, ybar)

@@ -116,16 +116,22 @@ class Presolved(NamedTuple):
     tolerance: np.ndarray
 
 
-def presolve(canon, rhs, cfg, dtype):
-    """Bounds, feasibility and row scaling; bounds.py:192-236."""
+def presolve(canon, rhs, cfg, dtype, values=None):
+    """Bounds, feasibility and row scaling; bounds.py:192-236.
+
+    ``values``: per-sample coefficients ``(B, M, w)`` on ``canon``'s ELL support
+    (the reference's ``jax.vmap(_numeric_one)(theta)`` values, bounds.py:192);
+    ``None`` uses ``canon``'s shared coefficients.
+    """
     dtype = np.dtype(dtype)
-    support, mask, values = canon.ell(dtype)
+    support, mask, shared = canon.ell(dtype)
+    values = shared if values is None else np.where(mask[None], np.asarray(values, dtype), 0)
     batch = rhs.shape[0]
     bidx = np.asarray(bound_rows(canon), dtype=np.int64)
     bset = set(bidx.tolist())
     rows = np.asarray([r for r in range(len(canon.rows)) if r not in bset], dtype=np.int64)
     variables = support[bidx, 0] if len(bidx) else np.zeros(0, np.int32)
-    vals_b = np.broadcast_to(values, (batch,) + values.shape)
+    vals_b = values if values.ndim == 3 else np.broadcast_to(values, (batch,) + values.shape)
     coefficient = vals_b[:, bidx, 0] if len(bidx) else np.zeros((batch, 0), dtype)
     threshold = rhs[:, bidx] / np.where(coefficient != 0, coefficient, dtype.type(1))
     lower = np.full((batch, canon.n), -np.inf, dtype)
@@ -150,17 +156,18 @@ def presolve(canon, rhs, cfg, dtype):
 
 
 def solve(canon, target, rhs, cfg, *, dtype=np.float64, multipliers_eq=None,
-          multipliers_ineq=None, return_internal=False):
-    """``BoundProjection.solve`` (bounds.py:170-317) for shared coefficients.
+          multipliers_ineq=None, return_internal=False, values=None, trace=None):
+    """``BoundProjection.solve`` (bounds.py:170-317).
 
-    ``rhs`` is ``-[h(theta,0); g(theta,0)]`` for all ``me+mi`` rows (solver.py:132-137).
+    ``rhs`` is ``-[h(theta,0); g(theta,0)]`` for all ``me+mi`` rows (solver.py:132-137);
+    ``values`` optional per-sample coefficients ``(B, M, w)`` (see ``presolve``).
     """
     dtype = np.dtype(dtype)
     target = np.asarray(target, dtype)
     rhs = np.asarray(rhs, dtype)
     batch, n = target.shape
     me = canon.me
-    pre = presolve(canon, rhs, cfg, dtype)
+    pre = presolve(canon, rhs, cfg, dtype, values)
     eq = np.zeros((batch, me), dtype) if multipliers_eq is None else np.asarray(multipliers_eq, dtype)
     iq = (np.zeros((batch, canon.mi), dtype) if multipliers_ineq is None
           else np.asarray(multipliers_ineq, dtype))
@@ -173,7 +180,7 @@ def solve(canon, target, rhs, cfg, *, dtype=np.float64, multipliers_eq=None,
         norm_iterations=cfg.norm_iterations, norm_seed=cfg.norm_seed, y0=target,
         dual0=initial, freeze_converged=True, check_stationarity=True,
         norm_bound=cfg.norm_bound, diagonal_preconditioning=cfg.diagonal_preconditioning,
-        early_stop=cfg.early_stop)
+        early_stop=cfg.early_stop, trace=trace)
     out = out._replace(converged=out.converged & pre.feasible)
     result = recover(canon, pre, out, target, rhs, cfg)
     if return_internal:
@@ -222,28 +229,77 @@ def recover(canon, pre, out, target, rhs, cfg):
                             status, out.iterations, residual, finite, converged)
 
 
-def vjp(canon, target, rhs, cfg, cot_y, *, dtype=np.float64):
-    """Forward solve plus implicit VJP w.r.t. ``target`` and all ``rhs`` rows.
+def row_scaling_pullback(kept, mask, rhs, g_scaled, g_rhs_scaled, row_scaling):
+    """Pull gradients w.r.t. the scaled rows ``(s K, s r)`` back to ``(K, r)``.
+
+    ``s_i = 1/max(||K_i||, 1e-30)`` for a nonzero row, else 1, and 1 without
+    row scaling (bounds.py:210-214, 228-230).  Returns
+    ``g_K = s g~_K - s^3 K (sum_j g~_K K + g~_r r)`` (the second term when row
+    scaling is on and ``||K_i|| > 1e-30``; the reference's graph gives NaN for an
+    all-zero row through ``sqrt'(0)``, this restatement takes the limit 0) and
+    ``g_r = s g~_r``.
+    """
+    kept = np.where(mask[None], kept, 0)
+    norms = np.sqrt(np.sum(kept ** 2, axis=2))
+    one = kept.dtype.type(1)
+    if row_scaling:
+        scale = np.where(norms > 0, one / np.maximum(norms, kept.dtype.type(1e-30)), one)
+    else:
+        scale = np.ones_like(norms)
+    s = scale[:, :, None]
+    g_scale = np.sum(np.where(mask[None], g_scaled * kept, 0), axis=2) + g_rhs_scaled * rhs
+    chain = (norms > 1e-30) if row_scaling else np.zeros_like(norms, bool)
+    g_kept = g_scaled * s - np.where(chain[:, :, None], s ** 3 * g_scale[:, :, None] * kept, 0)
+    return np.where(mask[None], g_kept, 0), g_rhs_scaled * scale
+
+
+def vjp(canon, target, rhs, cfg, cot_y, *, dtype=np.float64, values=None,
+        return_values=False, state=None):
+    """Forward solve plus implicit VJP w.r.t. ``target``, all ``rhs`` rows and,
+    with ``return_values``, the coefficients.
 
     The adjoint is bounds.py:80-165 (``oracle.adjoint.adjoint``); the chain rule
     through the presolve follows the JAX graph of bounds.py:193-239:
-    kept rows get ``g_rscaled * scale``; a bound row's rhs gets
-    ``g_bound / coef`` through ``threshold = rhs / coef`` when it attains the
-    bound (ties split evenly: this build's choice, unpinned by the reference).
-    Returns ``(result, g_target, g_rhs, adjoint_result)``.
+    * kept rows: ``K~ = s K``, ``r~ = s r`` with ``s = 1/max(||K_i||, 1e-30)``
+      (1 for a zero row or without row scaling), so ``g_r = g_r~ s`` and
+      ``g_K = s g_K~ - s^3 K (sum_j g_K~_ij K_ij + g_r~_i r_i)`` (the second
+      term when row scaling is on and ``||K_i|| > 1e-30``; the reference's graph
+      gives NaN for an all-zero row there, through ``sqrt'(0)``, and this
+      restatement takes the limit 0);
+    * bound rows: ``threshold = rhs / c`` reaches ``lower``/``upper`` through
+      scatter max/min; a bound row's ``g_threshold`` is its variable's
+      ``g_lower``/``g_upper`` when it attains the bound (ties split evenly:
+      this build's choice, unpinned by the reference), ``g_rhs = g_thr / c``
+      and ``g_c = -g_thr rhs / c^2``.
+    Returns ``(result, g_target, g_rhs, adjoint_result)`` and, with
+    ``return_values``, ``g_values`` ``(B, M, w)`` on ``canon``'s ELL support
+    after them.  ``state = (y, scaled kept dual)`` linearises at that state
+    instead of this oracle's own solution (the forward result is still the
+    oracle's).
     """
     from oracle import adjoint as _adj
 
     dtype = np.dtype(dtype)
     target = np.asarray(target, dtype)
     rhs = np.asarray(rhs, dtype)
-    result, out, pre = solve(canon, target, rhs, cfg, dtype=dtype, return_internal=True)
+    result, out, pre = solve(canon, target, rhs, cfg, dtype=dtype, return_internal=True,
+                             values=values)
     ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
-    adj = _adj.adjoint(pre.kept_values, ksup, kmask, canon.me, out.y, out.dual,
+    y_lin, d_lin = (out.y, out.dual) if state is None else (np.asarray(state[0], dtype),
+                                                            np.asarray(state[1], dtype))
+    adj = _adj.adjoint(pre.kept_values, ksup, kmask, canon.me, y_lin, d_lin,
                        out.converged, target, pre.kept_rhs, pre.lower, pre.upper,
                        np.asarray(cot_y, dtype), cfg)
+    batch = target.shape[0]
     g_rhs = np.zeros_like(rhs)
-    g_rhs[:, pre.rows] = adj.g_rhs * pre.scale
+    vals_b = (pre.values if pre.values.ndim == 3
+              else np.broadcast_to(pre.values, (batch,) + pre.values.shape))
+    g_values = np.zeros(vals_b.shape, dtype)
+    if len(pre.rows):
+        g_kept, g_rhs[:, pre.rows] = row_scaling_pullback(
+            vals_b[:, pre.rows], kmask, rhs[:, pre.rows], adj.g_values, adj.g_rhs,
+            cfg.row_scaling)
+        g_values[:, pre.rows] = g_kept
     for k, r in enumerate(pre.bounds):
         j = pre.variables[k]
         coef = pre.coefficient[:, k]
@@ -256,5 +312,9 @@ def vjp(canon, target, rhs, cfg, cot_y, *, dtype=np.float64):
                       & (pre.threshold[:, same] == pre.upper[:, j][:, None]), axis=1)
         g_thr = (np.where(lo_hit, adj.g_lower[:, j] / np.maximum(n_lo, 1), 0)
                  + np.where(hi_hit, adj.g_upper[:, j] / np.maximum(n_hi, 1), 0))
-        g_rhs[:, r] = np.where(coef != 0, g_thr / np.where(coef != 0, coef, 1), g_thr)
+        safe = np.where(coef != 0, coef, 1)
+        g_rhs[:, r] = np.where(coef != 0, g_thr / safe, g_thr)
+        g_values[:, r, 0] = np.where(coef != 0, -g_thr * rhs[:, r] / safe ** 2, 0)
+    if return_values:
+        return result, adj.g_target, g_rhs, adj, g_values
     return result, adj.g_target, g_rhs, adj

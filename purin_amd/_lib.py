@@ -31,8 +31,10 @@ SYMBOLS = (
     "purin_cp_last_adjoint_stats",
     "purin_cp_solve",
     "purin_cp_project",
+    "purin_cp_project_values",
     "purin_cp_default_adjoint_options",
     "purin_cp_adjoint",
+    "purin_cp_adjoint_values",
     "purin_cp_last_error",
     "purin_cp_build_info",
 )
@@ -150,6 +152,9 @@ def load(path: str = LIB_PATH):
     lib.purin_cp_project.argtypes = [vp, vp, i64, vp, vp, vp, C.POINTER(SolveOptions), vp, vp, vp,
                                      i32p, i32p, vp, u8p, u8p, vp]
     lib.purin_cp_project.restype = C.c_int
+    lib.purin_cp_project_values.argtypes = [vp, vp, i64, vp, vp, vp, vp, C.POINTER(SolveOptions),
+                                            vp, vp, vp, i32p, i32p, vp, u8p, u8p, vp]
+    lib.purin_cp_project_values.restype = C.c_int
     lib.purin_cp_last_timing.argtypes = [vp, C.POINTER(Timing)]
     lib.purin_cp_last_timing.restype = C.c_int
     lib.purin_cp_last_adjoint_stats.argtypes = [vp, C.POINTER(AdjointStats)]
@@ -159,6 +164,9 @@ def load(path: str = LIB_PATH):
     lib.purin_cp_adjoint.argtypes = [vp, vp, i64, vp, vp, vp, vp, C.POINTER(AdjointOptions), vp,
                                      vp, vp, vp, u8p, i32p, vp]
     lib.purin_cp_adjoint.restype = C.c_int
+    lib.purin_cp_adjoint_values.argtypes = [vp, vp, i64, vp, vp, vp, C.POINTER(AdjointOptions),
+                                            vp, vp, vp, u8p, i32p, vp]
+    lib.purin_cp_adjoint_values.restype = C.c_int
     lib.purin_cp_last_error.argtypes = []
     lib.purin_cp_last_error.restype = C.c_char_p
     lib.purin_cp_build_info.argtypes = []

@@ -46,11 +46,41 @@ struct Adj {
   const T* a_c;    // n or nullptr
   const T* d_c;    // n or nullptr
   const T* sig_r;  // m or nullptr
+  // per-sample steps (per-sample coefficients): [Bp] scalars per sample, or
+  // with diagonal steps [n][Bp] / [m][Bp]; nullptr when shared
+  const T* a_b;
+  const T* d_b;
+  const T* sig_b;
+  const T* a_cb;
+  const T* d_cb;
+  const T* sig_rb;
+  int dg;        // 1: U and Wv hold delta . u and sigma . w (any non-scalar step)
   const T* Cm;   // n x Bp
   const T* Dm;   // m x Bp
   T* U;          // n x Bp scratch (u)
   T* Wv;         // m x Bp scratch (w)
 };
+
+// Steps of column j / row i for sample b (shared, diagonal, per-sample or
+// per-sample diagonal).
+template <typename T>
+__device__ __forceinline__ T adj_a(const Adj<T>& S, int64_t j, int64_t b) {
+  if (S.a_cb) return S.a_cb[j * S.Bp + b];
+  if (S.a_b) return S.a_b[b];
+  return S.a_c ? S.a_c[j] : S.a;
+}
+template <typename T>
+__device__ __forceinline__ T adj_d(const Adj<T>& S, int64_t j, int64_t b) {
+  if (S.d_cb) return S.d_cb[j * S.Bp + b];
+  if (S.d_b) return S.d_b[b];
+  return S.d_c ? S.d_c[j] : S.delta;
+}
+template <typename T>
+__device__ __forceinline__ T adj_sig(const Adj<T>& S, int64_t i, int64_t b) {
+  if (S.sig_rb) return S.sig_rb[i * S.Bp + b];
+  if (S.sig_b) return S.sig_b[b];
+  return S.sig_r ? S.sig_r[i] : S.sigma;
+}
 
 // d/dx of max(x, y) and min(x, y) with JAX's balanced tie rule.
 template <typename T>
@@ -81,9 +111,11 @@ __global__ __launch_bounds__(kBlock) void k_lin_rows(Adj<T> S, const T* __restri
     if (i >= S.m) continue;
     V acc = vsplat<T>(T(0));
     for (int k = S.K.rptr[i]; k < S.K.rptr[i + 1]; ++k)
-      acc += S.K.rval[k] * vload(Y + (size_t)S.K.ridx[k] * S.Bp + b0);
+      acc += row_coef(S.K, k, b0) * vload(Y + (size_t)S.K.ridx[k] * S.Bp + b0);
     const size_t off = (size_t)i * S.Bp + b0;
-    const T sg = S.sig_r ? S.sig_r[i] : S.sigma;
+    V sg;
+#pragma unroll
+    for (int s = 0; s < Sn; ++s) sg[s] = adj_sig(S, i, b0 + s);
     const V p = vload(Dd + off) + sg * (acc - vload(R + off));
     V dm, dp;
 #pragma unroll
@@ -118,10 +150,15 @@ __global__ __launch_bounds__(kBlock) void k_lin_cols(Adj<T> S, const T* __restri
     if (j >= S.n) continue;
     V t = vsplat<T>(T(0));
     for (int k = S.K.cptr[j]; k < S.K.cptr[j + 1]; ++k)
-      t += S.K.cval[k] * vload(dplus + (size_t)S.K.cidx[k] * S.Bp + b0);
+      t += col_coef(S.K, k, b0) * vload(dplus + (size_t)S.K.cidx[k] * S.Bp + b0);
     const size_t off = (size_t)j * S.Bp + b0;
     const V y = vload(Y + off);
-    const T aj = S.a_c ? S.a_c[j] : S.a, dj = S.d_c ? S.d_c[j] : S.delta;
+    V aj, dj;
+#pragma unroll
+    for (int q = 0; q < Sn; ++q) {
+      aj[q] = adj_a(S, j, b0 + q);
+      dj[q] = adj_d(S, j, b0 + q);
+    }
     const V s = aj * y - dj * t + dj * vload(tgt + off);
     V lo, hi;
     if (shared_bounds) {
@@ -159,10 +196,10 @@ __global__ __launch_bounds__(kBlock) void k_op_cols1(Adj<T> S, const T* __restri
        e += (int64_t)gridDim.x * blockDim.x) {
     const T gy = v[e], gb = v[boff + e];
     const T u = S.Cm[e] * (gy + T(2) * gb);
-    if (S.a_c) {
-      const int64_t j = e / S.Bp;
-      S.U[e] = S.d_c[j] * u;
-      out[e] = gy - (S.a_c[j] * u - gb);
+    if (S.dg) {
+      const int64_t j = e / S.Bp, b = e - j * S.Bp;
+      S.U[e] = adj_d(S, j, b) * u;
+      out[e] = gy - (adj_a(S, j, b) * u - gb);
     } else {
       S.U[e] = u;
       out[e] = gy - (S.a * u - gb);
@@ -183,13 +220,16 @@ __global__ __launch_bounds__(kBlock) void k_op_rows(Adj<T> S, const T* __restric
     if (i >= S.m) continue;
     V acc = vsplat<T>(T(0));
     for (int k = S.K.rptr[i]; k < S.K.rptr[i + 1]; ++k)
-      acc += S.K.rval[k] * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
+      acc += row_coef(S.K, k, b0) * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
     const size_t off = (size_t)i * S.Bp + b0;
     const size_t voff = (size_t)(S.n + i) * S.Bp + b0;
     const V gd = vload(v + voff);
-    if (S.sig_r) {
+    if (S.dg) {
       const V w = vload(S.Dm + off) * (gd - acc);
-      vstore(S.Wv + off, S.sig_r[i] * w);
+      V sg;
+#pragma unroll
+      for (int s = 0; s < Sn; ++s) sg[s] = adj_sig(S, i, b0 + s);
+      vstore(S.Wv + off, sg * w);
       vstore(out + voff, gd - w);
     } else {
       const V w = vload(S.Dm + off) * (gd - S.delta * acc);
@@ -212,9 +252,9 @@ __global__ __launch_bounds__(kBlock) void k_op_cols2(Adj<T> S, const T* __restri
     if (j >= S.n) continue;
     V acc = vsplat<T>(T(0));
     for (int k = S.K.cptr[j]; k < S.K.cptr[j + 1]; ++k)
-      acc += S.K.cval[k] * vload(S.Wv + (size_t)S.K.cidx[k] * S.Bp + b0);
+      acc += col_coef(S.K, k, b0) * vload(S.Wv + (size_t)S.K.cidx[k] * S.Bp + b0);
     const size_t off = (size_t)(S.n + S.m + j) * S.Bp + b0;
-    if (S.sig_r)
+    if (S.dg)
       vstore(out + off, vload(v + off) - acc);
     else
       vstore(out + off, vload(v + off) - S.sigma * acc);
@@ -787,8 +827,8 @@ __global__ void k_final_u(Adj<T> S, const T* __restrict__ lam, const T* __restri
     const T gy = w != T(0) ? lam[e] : T(0), gb = w != T(0) ? lam[boff + e] : T(0);
     const T G = gy + T(2) * gb;
     const T u = S.Cm[e] * G;
-    const T a = (S.d_c ? S.d_c[e / S.Bp] : S.delta) * u, l = Clo[e] * G, h = Chi[e] * G;
-    S.U[e] = S.d_c ? a : u;
+    const T a = adj_d(S, e / S.Bp, b) * u, l = Clo[e] * G, h = Chi[e] * G;
+    S.U[e] = S.dg ? a : u;
     gt[e] = finite(a) ? a : T(0);
     glo[e] = finite(l) ? l : T(0);
     ghi[e] = finite(h) ? h : T(0);
@@ -797,7 +837,8 @@ __global__ void k_final_u(Adj<T> S, const T* __restrict__ lam, const T* __restri
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_final_w(Adj<T> S, const T* __restrict__ lam,
-                                                    const T* __restrict__ lam_w, T* gr) {
+                                                    const T* __restrict__ lam_w, T* gr,
+                                                    T* sw) {
   using V = typename Lane<T>::V;
   constexpr int Sn = Lane<T>::S;
   const int lane = threadIdx.x & 63;
@@ -808,36 +849,99 @@ __global__ __launch_bounds__(kBlock) void k_final_w(Adj<T> S, const T* __restric
     if (i >= S.m) continue;
     V acc = vsplat<T>(T(0));
     for (int k = S.K.rptr[i]; k < S.K.rptr[i + 1]; ++k)
-      acc += S.K.rval[k] * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
+      acc += row_coef(S.K, k, b0) * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
     const size_t off = (size_t)i * S.Bp + b0;
     const V gd = vload(lam + (size_t)(S.n + i) * S.Bp + b0);
-    V out;
+    V out, swv;
 #pragma unroll
     for (int s = 0; s < Sn; ++s) {
       const T lw = lam_w[b0 + s];
-      const T w = S.sig_r ? S.Dm[off + s] * ((lw != T(0) ? gd[s] : T(0)) - acc[s])
-                          : S.Dm[off + s] * ((lw != T(0) ? gd[s] : T(0)) - S.delta * acc[s]);
-      const T r = -(S.sig_r ? S.sig_r[i] : S.sigma) * w;
-      out[s] = finite(r) ? r : T(0);
+      const T w = S.dg ? S.Dm[off + s] * ((lw != T(0) ? gd[s] : T(0)) - acc[s])
+                       : S.Dm[off + s] * ((lw != T(0) ? gd[s] : T(0)) - S.delta * acc[s]);
+      const T r = adj_sig(S, i, b0 + s) * w;
+      swv[s] = r;
+      out[s] = finite(r) ? -r : T(0);
     }
     vstore(gr + off, out);
+    if (sw) vstore(sw + off, swv);
+  }
+}
+
+// Gradient w.r.t. the coefficients of the kept rows, per sample, in the
+// caller's entry order (per-sample coefficients).  The pullback of the scaled
+// entry K~_ij = s_i K_ij is g~_ij = (sigma w)_i ybar_j - d+_i (delta u)_j
+// (the VJP of cp_step, bounds.py:109-141), cleaned of non-finite values
+// (bounds.py:155).  The row scale s_i = 1/||K_i|| (bounds.py:210-214) and the
+// scaled rhs r~_i = s_i r_i chain it to the original entries:
+//   g_ij = s_i g~_ij - s_i^3 K_ij (sum_j' g~_ij' K_ij' + g_r~_i r_i),
+// the second term only when row scaling is on and ||K_i|| > 1e-30.
+// One kept row per wavefront; sw = sigma . w, U = delta . u.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_gvals_rows(
+    Mat<T> K, int64_t Bp, const T* __restrict__ sw, const T* __restrict__ Y,
+    const T* __restrict__ U, const T* __restrict__ dplus, const T* __restrict__ gr,
+    const T* __restrict__ RVo, const T* __restrict__ SC, const T* __restrict__ RF,
+    const int32_t* __restrict__ kept, int row_scaling, const int32_t* __restrict__ kcsr,
+    T* __restrict__ GVF) {
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  const T zero = T(0);
+  for (int rb = blockIdx.y; rb * 4 < K.m; rb += gridDim.y) {
+    const int i = rb * 4 + wave;
+    if (i >= K.m) continue;
+    const size_t off = (size_t)i * Bp + b0;
+    const V swi = vload(sw + off), dpi = vload(dplus + off);
+    V gsc = vsplat<T>(zero), sq = vsplat<T>(zero);
+    const int s0 = K.rptr[i], s1 = K.rptr[i + 1];
+    for (int k = s0; k < s1; ++k) {
+      const size_t jo = (size_t)K.ridx[k] * Bp + b0;
+      const V g = swi * vload(Y + jo) - dpi * vload(U + jo);
+      const V ko = vload(RVo + (size_t)k * Bp + b0);
+#pragma unroll
+      for (int s = 0; s < Sn; ++s) gsc[s] += (finite(g[s]) ? g[s] : zero) * ko[s];
+      sq += ko * ko;
+    }
+    const V sc = vload(SC + off);
+    gsc += vload(gr + off) * vload(RF + (size_t)kept[i] * Bp + b0);
+    V c3;
+#pragma unroll
+    for (int s = 0; s < Sn; ++s)
+      c3[s] = (row_scaling && __builtin_sqrt(sq[s]) > T(1e-30)) ? sc[s] * sc[s] * sc[s] * gsc[s]
+                                                               : zero;
+    for (int k = s0; k < s1; ++k) {
+      const size_t jo = (size_t)K.ridx[k] * Bp + b0;
+      const V g = swi * vload(Y + jo) - dpi * vload(U + jo);
+      const V ko = vload(RVo + (size_t)k * Bp + b0);
+      V out;
+#pragma unroll
+      for (int s = 0; s < Sn; ++s) out[s] = sc[s] * (finite(g[s]) ? g[s] : zero) - c3[s] * ko[s];
+      vstore(GVF + (size_t)kcsr[k] * Bp + b0, out);
+    }
   }
 }
 
 // g_rhs in the full row space for project(): kept rows g_r * scale, bound
-// rows through their threshold (ties at a bound split evenly).
+// rows through their threshold (ties at a bound split evenly).  With
+// per-sample coefficients (scale_b, bcoef_b) the scales and bound
+// coefficients are per sample, and the gradient of a bound row's coefficient,
+// -g_threshold * rhs / c^2 = -g_rhs * threshold, goes to GVF[bpos[k]].
 template <typename T>
 __global__ void k_grhs_full(int m, int n, int64_t Bp, const int32_t* __restrict__ kept,
-                            const T* __restrict__ scale, const T* __restrict__ gr,
-                            const int32_t* __restrict__ bptr, const int32_t* __restrict__ brow,
-                            const T* __restrict__ bcoef, const T* __restrict__ RF,
+                            const T* __restrict__ scale, const T* __restrict__ scale_b,
+                            const T* __restrict__ gr, const int32_t* __restrict__ bptr,
+                            const int32_t* __restrict__ brow, const T* __restrict__ bcoef,
+                            const T* __restrict__ bcoef_b, const T* __restrict__ RF,
                             const T* __restrict__ LO, const T* __restrict__ HI, int shared_bounds,
-                            const T* __restrict__ glo, const T* __restrict__ ghi, T* out) {
-  const int64_t total_rows = (int64_t)m * Bp;
+                            const T* __restrict__ glo, const T* __restrict__ ghi, T* out,
+                            const int32_t* __restrict__ bpos, T* GVF) {
+  const int64_t total_rows = out ? (int64_t)m * Bp : 0;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total_rows;
        e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t i = e / Bp, b = e - i * Bp;
-    out[(int64_t)kept[i] * Bp + b] = gr[e] * scale[i];
+    out[(int64_t)kept[i] * Bp + b] = gr[e] * (scale_b ? scale_b[e] : scale[i]);
   }
   const int64_t total_cols = (int64_t)n * Bp;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total_cols;
@@ -848,19 +952,23 @@ __global__ void k_grhs_full(int m, int n, int64_t Bp, const int32_t* __restrict_
     const int k0 = bptr[j], k1 = bptr[j + 1];
     T nlo = T(0), nhi = T(0);
     for (int k = k0; k < k1; ++k) {
-      const T c = bcoef[k];
+      const T c = bcoef_b ? bcoef_b[(int64_t)k * Bp + b] : bcoef[k];
       const T th = RF[(int64_t)brow[k] * Bp + b] / (c != T(0) ? c : T(1));
       if (c < T(0) && th == lo) nlo += T(1);
       if (c > T(0) && th == hi) nhi += T(1);
     }
     for (int k = k0; k < k1; ++k) {
-      const T c = bcoef[k];
+      const T c = bcoef_b ? bcoef_b[(int64_t)k * Bp + b] : bcoef[k];
       const T th = RF[(int64_t)brow[k] * Bp + b] / (c != T(0) ? c : T(1));
       T gthr = T(0);
       if (c < T(0) && th == lo) gthr += glo[e] / maxp(nlo, T(1));
       if (c > T(0) && th == hi) gthr += ghi[e] / maxp(nhi, T(1));
       const T v = c != T(0) ? gthr / c : gthr;
-      out[(int64_t)brow[k] * Bp + b] = finite(v) ? v : T(0);
+      if (out) out[(int64_t)brow[k] * Bp + b] = finite(v) ? v : T(0);
+      if (GVF) {
+        const T gc = c != T(0) ? -v * th : T(0);
+        GVF[(int64_t)bpos[k] * Bp + b] = finite(gc) ? gc : T(0);
+      }
     }
   }
 }
@@ -876,8 +984,11 @@ static size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 template <typename T>
 static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const void* saved,
                         const T* cot_y, const purin_cp_adjoint_options& o, T* g_target, T* g_rhs,
-                        T* g_lower, T* g_upper, uint8_t* valid, int32_t* info, T* gres) {
+                        T* g_lower, T* g_upper, uint8_t* valid, int32_t* info, T* gres,
+                        const T* values = nullptr, T* g_values = nullptr,
+                        bool per_sample = false) {
   if (!saved || !cot_y) return set_error(PURIN_CP_ERR_ARG, "NULL saved state or cotangent");
+  if (per_sample && p->nnz_full && !values) return set_error(PURIN_CP_ERR_ARG, "NULL values");
   if (batch < 1) return set_error(PURIN_CP_ERR_ARG, "batch must be positive");
   if (o.restart < 1 || o.max_iterations < 1)
     return set_error(PURIN_CP_ERR_ARG, "linear iteration limits must be positive");
@@ -897,6 +1008,11 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     return set_error(PURIN_CP_ERR_ARG, "saved state does not belong to this plan and batch");
   const int kind = (int)hdr[3];
   const int shared = (int)hdr[4];
+  if (per_sample != (kind == 2))
+    return set_error(PURIN_CP_ERR_ARG, per_sample
+                                           ? "saved state is not from purin_cp_project_values"
+                                           : "saved state is from purin_cp_project_values: use "
+                                             "purin_cp_adjoint_values");
   const char* sv = (const char*)saved;
   const T* Tt = (const T*)(sv + L.Tt);
   const T* Y = (const T*)(sv + L.Y);
@@ -906,7 +1022,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   const T* HI = (const T*)(sv + L.HI);
   const T* RF = (const T*)(sv + L.RF);
   const int32_t* conv = (const int32_t*)(sv + L.conv);
-  const T* metric = kind == 1 ? (const T*)p->metric : nullptr;
+  const T* metric = kind >= 1 ? (const T*)p->metric : nullptr;
 
   // workspace
   const int nchunk = (int)((W + kChunk - 1) / kChunk);
@@ -941,6 +1057,13 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                oCnt = take(256), oStepCnt = take((size_t)(restart + 2) * 4), oLw = take(Bp * es), oGt = take(n * Bp * es),
                oGlo = take(n * Bp * es), oGhi = take(n * Bp * es), oGr = take(m * Bp * es),
                oGF = take((size_t)M * Bp * es);
+  // per-sample coefficients: the forward's per-sample arrays are rebuilt from
+  // values in a region laid out like the forward workspace, plus sigma . w and
+  // the coefficient gradient in entry order
+  const Layout Lv = per_sample ? make_layout(p, batch, true) : Layout{};
+  const size_t oPS = per_sample ? take(Lv.ws_end) : 0;
+  const size_t oSw = per_sample ? take(m * Bp * es) : 0;
+  const size_t oGV = per_sample ? take((size_t)p->nnz_full * Bp * es) : 0;
   int err = PURIN_CP_OK;
   char* ws = (char*)workspace(p, o_, st, &err, true);
   if (!ws) return err;
@@ -969,10 +1092,30 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   S.sigma = (T)p->sigma_adj;
   S.a = T(1) / (T(1) + tau);
   S.delta = tau * S.a;
-  if (p->diag) {  // the forward's diagonal steps (bounds.py:83-86)
+  PerSample<T> PS{};
+  if (per_sample) {
+    // per-sample scaled entries and the adjoint's per-sample steps: the
+    // power-iteration L of each sample's matrix (bounds.py:88-101) or its
+    // diagonal steps (bounds.py:83-86)
+    if (int rc = prepare_values<T>(p, st, batch, Lv, ws + oPS, values, T(1), true, &PS)) return rc;
+    S.K.rvb = PS.RV;
+    S.K.cvb = PS.CV;
+    S.K.vbp = Bp;
+    if (p->diag) {
+      S.a_cb = PS.a_cb;
+      S.d_cb = PS.d_cb;
+      S.sig_rb = PS.sig_rb;
+    } else {
+      S.a_b = PS.a_b;
+      S.d_b = PS.d_b;
+      S.sig_b = PS.sig_b;
+    }
+    S.dg = 1;
+  } else if (p->diag) {  // the forward's diagonal steps (bounds.py:83-86)
     S.a_c = (const T*)p->diag_a;
     S.d_c = (const T*)p->diag_d;
     S.sig_r = (const T*)p->diag_sig;
+    S.dg = 1;
   }
   S.Cm = (const T*)(ws + oCm);
   S.Dm = (const T*)(ws + oDm);
@@ -1171,16 +1314,23 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   T* gr = (T*)(ws + oGr);
   k_final_u<T><<<eb, 256, 0, st>>>(S, X, lam_w, (const T*)(ws + oClo), (const T*)(ws + oChi), gt,
                                    glo, ghi);
-  if (m) k_final_w<T><<<grow, kBlock, 0, st>>>(S, X, lam_w, gr);
+  T* sw = per_sample ? (T*)(ws + oSw) : nullptr;
+  if (m) k_final_w<T><<<grow, kBlock, 0, st>>>(S, X, lam_w, gr, sw);
   if (g_target) to_major<T>(st, gt, Bp, n, g_target, batch, n, metric, metric ? 1 : 0);
-  if (kind == 1) {
-    if (g_rhs && M) {
-      T* GF = (T*)(ws + oGF);
-      k_grhs_full<T><<<eb, 256, 0, st>>>((int)m, (int)n, Bp, p->dkept, (const T*)p->dscale, gr,
-                                         p->bptr, p->brow, (const T*)p->dbcoef, RF, LO, HI, shared,
-                                         glo, ghi, GF);
-      to_major<T>(st, GF, Bp, M, g_rhs, batch, M, nullptr, 0);
-    }
+  if (kind >= 1) {
+    T* GF = (g_rhs && M) ? (T*)(ws + oGF) : nullptr;
+    T* GV = (per_sample && g_values && p->nnz_full) ? (T*)(ws + oGV) : nullptr;
+    if (GV && m)
+      k_gvals_rows<T><<<grow, kBlock, 0, st>>>(S.K, Bp, sw, Y, S.U, (const T*)(ws + oDp), gr,
+                                              PS.RVo, PS.SC, RF, p->dkept, p->opts.row_scaling,
+                                              p->ps_kcsr, GV);
+    if (GF || (GV && !p->bound.empty()))
+      k_grhs_full<T><<<eb, 256, 0, st>>>((int)m, (int)n, Bp, p->dkept, (const T*)p->dscale,
+                                         per_sample ? PS.SC : nullptr, gr, p->bptr, p->brow,
+                                         (const T*)p->dbcoef, per_sample ? PS.BC : nullptr, RF,
+                                         LO, HI, shared, glo, ghi, GF, p->ps_bpos, GV);
+    if (GF) to_major<T>(st, GF, Bp, M, g_rhs, batch, M, nullptr, 0);
+    if (GV) to_major<T>(st, GV, Bp, p->nnz_full, g_values, batch, p->nnz_full, nullptr, 0);
   } else {
     if (g_rhs && m) to_major<T>(st, gr, Bp, m, g_rhs, batch, m, nullptr, 0);
   }
@@ -1193,6 +1343,26 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
 }  // namespace purin
 
 using namespace purin;
+
+extern "C" int purin_cp_adjoint_values(purin_cp_plan* p, void* stream, int64_t batch,
+                                       const void* saved, const void* values, const void* cot_y,
+                                       const purin_cp_adjoint_options* opts, void* g_target,
+                                       void* g_rhs, void* g_values, uint8_t* valid, int32_t* info,
+                                       void* gmres_residual) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  purin_cp_adjoint_options o;
+  purin_cp_default_adjoint_options(&o);
+  if (opts) o = *opts;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64)
+    return adjoint_impl<double>(p, st, batch, saved, (const double*)cot_y, o, (double*)g_target,
+                                (double*)g_rhs, nullptr, nullptr, valid, info,
+                                (double*)gmres_residual, (const double*)values,
+                                (double*)g_values, true);
+  return adjoint_impl<float>(p, st, batch, saved, (const float*)cot_y, o, (float*)g_target,
+                             (float*)g_rhs, nullptr, nullptr, valid, info, (float*)gmres_residual,
+                             (const float*)values, (float*)g_values, true);
+}
 
 extern "C" int purin_cp_adjoint(purin_cp_plan* p, void* stream, int64_t batch, const void* saved,
                                 const void* target, const void* rhs, const void* cot_y,

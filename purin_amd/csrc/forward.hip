@@ -18,12 +18,13 @@
 #include "post.hpp"
 #include "forward.hpp"
 #include "resident.hpp"
+#include "persample.hpp"
 
 namespace purin {
 
 static size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
-Layout make_layout(const purin_cp_plan* p, int64_t batch) {
+Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values) {
   Layout L{};
   const size_t es = elem_size(p);
   const int64_t Bp = padded_batch(p, batch);
@@ -67,9 +68,127 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch) {
     L.RLs = take(Kc * Bp * es);
     L.RHs = take(Kc * Bp * es);
   }
+  if (values) {
+    const size_t nnz = p->nnz, nb = p->bound.size();
+    L.VF = take((size_t)p->nnz_full * Bp * es);
+    L.RVo = take(nnz * Bp * es);
+    L.CVo = take(nnz * Bp * es);
+    L.RV = take(nnz * Bp * es);
+    L.CV = take(nnz * Bp * es);
+    L.BC = take(nb * Bp * es);
+    L.SC = take(m * Bp * es);
+    if (p->diag) {
+      L.SGR = take(m * Bp * es);
+      L.ACB = take(n * Bp * es);
+      L.DCB = take(n * Bp * es);
+    }
+    L.STB = take((size_t)7 * Bp * es);  // tau, sigma, a, delta, theta, tol, L
+    L.RPT = take((size_t)2 * std::max(L.nrb, 1) * Bp * es);
+    L.CPT = take((size_t)std::max(L.ncb, 1) * Bp * es);
+    L.PX = take(n * Bp * es);  // power iteration vectors and dots
+    L.PZ = take(std::max<size_t>(m, 1) * Bp * es);
+    L.PW = take(n * Bp * es);
+    L.PD = take((size_t)2 * Bp * es);
+  }
   L.ws_end = o;
   return L;
 }
+
+// Per-sample power iteration on K~^T K~ (kernels.py:52-65): every sample starts
+// from the plan's normalised start vector; returns sqrt(max(eig, 0)) + eps in Lout.
+template <typename T>
+static void ps_power(const purin_cp_plan* p, hipStream_t st, const Layout& L, char* ws,
+                     const Mat<T>& K, T* Lout) {
+  const int64_t Bp = L.Bp, n = p->n, m = p->m;
+  constexpr int64_t TS = tile_samples<T>();
+  T* X = (T*)(ws + L.PX);
+  T* Z = (T*)(ws + L.PZ);
+  T* Wv = (T*)(ws + L.PW);
+  T* eig = (T*)(ws + L.PD);
+  T* ww = eig + Bp;
+  const T eps = T(1e-12);
+  k_ps_start<T><<<1024, 256, 0, st>>>(n, Bp, (const T*)p->ps_start, X);
+  k_fill<T><<<8, 256, 0, st>>>(eig, Bp, T(0));
+  for (int it = 0; it < p->opts.norm_iterations; ++it) {
+    if (m) {
+      k_spmv_rows<T><<<tile_grid(Bp, TS, (m + 3) / 4), kBlock, 0, st>>>(K, Bp, X, Z);
+      k_spmv_cols<T><<<tile_grid(Bp, TS, (n + 3) / 4), kBlock, 0, st>>>(K, Bp, Z, Wv);
+    } else {
+      k_fill<T><<<1024, 256, 0, st>>>(Wv, n * Bp, T(0));
+    }
+    k_ps_dots<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(n, Bp, X, Wv, eig, ww);
+    k_ps_normalize<T><<<1024, 256, 0, st>>>(n, Bp, Wv, ww, eps, X);
+  }
+  k_ps_norm_final<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(Bp, eig, eps, Lout);
+}
+
+template <typename T>
+int prepare_values(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout& L, char* ws,
+                   const T* values, T tol, bool adjoint, PerSample<T>* ps) {
+  const int64_t Bp = L.Bp, n = p->n, m = p->m, nnz = p->nnz;
+  const int64_t nb = (int64_t)p->bound.size();
+  constexpr int64_t TS = tile_samples<T>();
+  T* VF = (T*)(ws + L.VF);
+  T* RVo = (T*)(ws + L.RVo);
+  T* CVo = (T*)(ws + L.CVo);
+  T* RV = (T*)(ws + L.RV);
+  T* CV = (T*)(ws + L.CV);
+  T* BC = (T*)(ws + L.BC);
+  T* SC = (T*)(ws + L.SC);
+  T* stb = (T*)(ws + L.STB);
+  T* rpart = (T*)(ws + L.RPT);
+  T* cpart = (T*)(ws + L.CPT);
+  // padded samples (b >= batch) get zero coefficients (to_minor pads with 0)
+  to_minor<T>(st, values, batch, p->nnz_full, p->nnz_full, VF, Bp, nullptr, 0);
+  if (nnz) {
+    k_gather_entries<T><<<2048, 256, 0, st>>>(VF, Bp, p->ps_kcsr, nnz, RVo);
+    k_gather_entries<T><<<2048, 256, 0, st>>>(VF, Bp, p->ps_kcsc, nnz, CVo);
+  }
+  if (nb) k_gather_entries<T><<<2048, 256, 0, st>>>(VF, Bp, p->ps_bpos, nb, BC);
+  const bool diag = p->diag;
+  const T safety = (T)p->opts.safety;
+  ps->RVo = RVo;
+  ps->CVo = CVo;
+  ps->RV = RV;
+  ps->CV = CV;
+  ps->BC = BC;
+  ps->SC = SC;
+  ps->sig_rb = diag ? (T*)(ws + L.SGR) : nullptr;
+  ps->a_cb = diag ? (T*)(ws + L.ACB) : nullptr;
+  ps->d_cb = diag ? (T*)(ws + L.DCB) : nullptr;
+  ps->tau_b = stb;
+  ps->sig_b = stb + Bp;
+  ps->a_b = stb + 2 * Bp;
+  ps->d_b = stb + 3 * Bp;
+  ps->th_b = stb + 4 * Bp;
+  ps->tol_b = stb + 5 * Bp;
+  T* Lpi = stb + 6 * Bp;
+  if (m)
+    k_ps_rows<T><<<tile_grid(Bp, TS, L.nrb), kBlock, 0, st>>>(
+        (int)m, Bp, p->rptr, RVo, p->opts.row_scaling, safety, SC, RV, ps->sig_rb, rpart, L.nrb);
+  k_ps_cols<T><<<tile_grid(Bp, TS, L.ncb), kBlock, 0, st>>>(
+      (int)n, Bp, p->cptr, p->cidx, CVo, SC, safety, CV, ps->a_cb, ps->d_cb, cpart, L.ncb);
+  // the power iteration sets L for the adjoint (bounds.py:88-101) and for the
+  // forward without the norm bound (kernels.py:211-212)
+  const bool power = !diag && (adjoint || !p->opts.norm_bound);
+  if (power) {
+    Mat<T> K = kept_matrix<T>(p, true);
+    K.rvb = RV;
+    K.cvb = CV;
+    K.vbp = Bp;
+    ps_power<T>(p, st, L, ws, K, Lpi);
+  }
+  k_ps_steps<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(
+      Bp, rpart, (int)(m ? L.nrb : 0), cpart, L.ncb, power ? Lpi : nullptr, safety,
+      adjoint ? 0 : p->opts.accelerated, tol, ps->tau_b, ps->sig_b, ps->a_b, ps->d_b, ps->th_b,
+      ps->tol_b);
+  PURIN_HIP(hipGetLastError());
+  return PURIN_CP_OK;
+}
+template int prepare_values<double>(purin_cp_plan*, hipStream_t, int64_t, const Layout&, char*,
+                                    const double*, double, bool, PerSample<double>*);
+template int prepare_values<float>(purin_cp_plan*, hipStream_t, int64_t, const Layout&, char*,
+                                   const float*, float, bool, PerSample<float>*);
 
 template <typename T>
 constexpr int res_tile() {
@@ -221,7 +340,8 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
 // The CP loop on prepared internal arrays plus the final diagnostics.
 template <typename T>
 int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout& L, char* sv,
-                   char* ws, const purin_cp_solve_options& o, T tol_scalar, const T* tolv) {
+                   char* ws, const purin_cp_solve_options& o, T tol_scalar, const T* tolv,
+                   const PerSample<T>* ps = nullptr) {
   const int64_t Bp = L.Bp;
   constexpr int64_t TS = tile_samples<T>();
   Iter<T> A{};
@@ -239,7 +359,22 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   A.rowpart = (T*)(ws + L.rowpart);
   A.ncb = L.ncb;
   A.nrb = L.nrb;
-  if (p->diag) {  // diagonal steps (non-accelerated, so constant over the loop)
+  if (ps) {  // per-sample coefficients: per-sample matrix entries and steps
+    A.K.rvb = ps->RV;
+    A.K.cvb = ps->CV;
+    A.K.vbp = Bp;
+    if (p->diag) {
+      A.sig_rb = ps->sig_rb;
+      A.a_cb = ps->a_cb;
+      A.d_cb = ps->d_cb;
+    } else {
+      A.sig_b = ps->sig_b;
+      A.a_b = ps->a_b;
+      A.d_b = ps->d_b;
+      if (p->opts.accelerated) A.th_b = ps->th_b;
+    }
+    tolv = ps->tol_b;
+  } else if (p->diag) {  // diagonal steps (non-accelerated, so constant over the loop)
     A.sig_r = (const T*)p->diag_sig;
     A.a_c = (const T*)p->diag_a;
     A.d_c = (const T*)p->diag_d;
@@ -251,7 +386,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   const bool early = o.early_stop != 0;
   const size_t lds = resident_lds<T>(p);
   // the resident kernel takes one schedule of scalar steps for the whole tile
-  if (!early && lds && !o.streaming && !p->diag) {
+  if (!early && lds && !o.streaming && !p->diag && !ps) {
     if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds)) return rc;
     const int32_t cnt = (int32_t)o.max_iterations;
     k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);
@@ -315,7 +450,10 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
                                                    nullptr, nullptr, nullptr, nullptr, nullptr);
     }
     if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 2], st));
-    if (p->opts.accelerated) {  // kernels.py:279-283 with gamma = min q = 1
+    if (p->opts.accelerated && A.th_b) {  // the same update, per sample
+      k_ps_sched<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(Bp, ps->tau_b, ps->sig_b,
+                                                                  ps->a_b, ps->d_b, ps->th_b);
+    } else if (p->opts.accelerated) {  // kernels.py:279-283 with gamma = min q = 1
       const T nt = one / std::sqrt(one + tau);
       tau = nt * tau;
       sigma = sigma / nt;
@@ -382,8 +520,8 @@ static int check_layout_args(purin_cp_plan* p, int64_t batch) {
 
 template <typename T>
 static int prepare_buffers(purin_cp_plan* p, hipStream_t st, int64_t batch, void* saved,
-                           Layout* L, char** sv, char** ws) {
-  *L = make_layout(p, batch);
+                           Layout* L, char** sv, char** ws, bool values = false) {
+  *L = make_layout(p, batch, values);
   int err = PURIN_CP_OK;
   const size_t need = L->ws_end + (saved ? 0 : L->saved_end);
   char* base = (char*)workspace(p, need, st, &err);
@@ -477,19 +615,23 @@ template <typename T>
 static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T* target,
                         const T* rhs, const T* mult0, const purin_cp_solve_options& o, T* y,
                         T* mult, T* slacks, int32_t* status, int32_t* iterations, T* residual,
-                        uint8_t* finite_out, uint8_t* eligible, void* saved) {
+                        uint8_t* finite_out, uint8_t* eligible, void* saved,
+                        const T* values = nullptr, bool per_sample = false) {
   int rc = check_layout_args<T>(p, batch);
   if (rc) return rc;
   if (!target || (p->M && !rhs)) return set_error(PURIN_CP_ERR_ARG, "NULL input array");
+  if (per_sample && p->nnz_full && !values) return set_error(PURIN_CP_ERR_ARG, "NULL values");
+  if (per_sample && o.shared_bounds)
+    return set_error(PURIN_CP_ERR_ARG, "shared_bounds needs shared coefficients");
   if (o.max_iterations < 1) return set_error(PURIN_CP_ERR_ARG, "max_iterations must be a positive integer");
   if (!(o.tolerance > 0.0) || !std::isfinite(o.tolerance))
     return set_error(PURIN_CP_ERR_ARG, "tolerance must be positive and finite");
   Layout L;
   char *sv, *ws;
-  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws))) return rc;
+  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, per_sample))) return rc;
   const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
   constexpr int64_t TS = tile_samples<T>();
-  write_header<T>(st, sv, batch, Bp, 1, o.shared_bounds, p);
+  write_header<T>(st, sv, batch, Bp, per_sample ? 2 : 1, o.shared_bounds, p);
   const T* metric = (const T*)p->metric;
   // diagonal metric: targets scaled by sqrt(D) (metric.py:102-108), tolerance
   // divided and residual multiplied by max(1, sqrt(max D)) (metric.py:161-165)
@@ -505,22 +647,38 @@ static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T
     MF = (T*)(ws + L.MF);
     to_minor<T>(st, mult0, batch, M, M, MF, Bp, nullptr, 0);
   }
+  // per-sample coefficients: scales, scaled entries, steps and tolerances
+  // tol * min(1, min_i scale_i) for every sample (bounds.py:192-236)
+  PerSample<T> PS{};
+  if (per_sample &&
+      (rc = prepare_values<T>(p, st, batch, L, ws, values, (T)tol_cfg, false, &PS)))
+    return rc;
+  const PerSample<T>* ps = per_sample ? &PS : nullptr;
   if (m)
-    k_prep_rows<T><<<2048, 256, 0, st>>>((int)m, Bp, p->dkept, (const T*)p->dscale, RF, MF,
-                                         (T*)(sv + L.R), (T*)(sv + L.D));
+    k_prep_rows<T><<<2048, 256, 0, st>>>((int)m, Bp, p->dkept, (const T*)p->dscale,
+                                         ps ? ps->SC : nullptr, RF, MF, (T*)(sv + L.R),
+                                         (T*)(sv + L.D));
   k_init_flags<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(
       batch, Bp, (int32_t*)(ws + L.done), (int32_t*)(ws + L.count), (int32_t*)(sv + L.feas),
       nullptr, (int32_t*)(ws + L.ndone));
   const int64_t cols = o.shared_bounds ? 1 : Bp;
   k_prep_bounds<T><<<2048, 256, 0, st>>>((int)n, Bp, cols, p->bptr, p->brow,
-                                         (const T*)p->dbcoef, RF, (T*)(sv + L.LO),
+                                         (const T*)p->dbcoef, ps ? ps->BC : nullptr, RF,
+                                         (T*)(sv + L.LO),
                                          (T*)(sv + L.HI), (int32_t*)(sv + L.feas), batch);
   // tolerance = tol * min(1, min_i scale_i) (bounds.py:233-236)
   const T tol_cp = (T)tol_cfg * std::min((T)1, (T)p->tol_factor);
-  if ((rc = run_iterations<T>(p, st, batch, L, sv, ws, o, tol_cp, nullptr))) return rc;
+  if ((rc = run_iterations<T>(p, st, batch, L, sv, ws, o, tol_cp, nullptr, ps))) return rc;
   // post-processing (bounds.py:247-317)
   Post<T> P{};
   P.K = kept_matrix<T>(p, false);
+  if (ps) {
+    P.K.rvb = ps->RVo;
+    P.K.cvb = ps->CVo;
+    P.K.vbp = Bp;
+    P.scale_b = ps->SC;
+    P.bcoef_b = ps->BC;
+  }
   P.Bp = Bp;
   P.me = p->me;
   P.mi = p->mi;
@@ -613,6 +771,27 @@ int purin_cp_project(purin_cp_plan* p, void* stream, int64_t batch, const void* 
   return project_impl<float>(p, st, batch, (const float*)target, (const float*)rhs,
                              (const float*)mult0, o, (float*)y, (float*)mult, (float*)slacks,
                              status, iterations, (float*)residual, finite_out, eligible, saved);
+}
+
+int purin_cp_project_values(purin_cp_plan* p, void* stream, int64_t batch, const void* values,
+                            const void* target, const void* rhs, const void* mult0,
+                            const purin_cp_solve_options* opts, void* y, void* mult,
+                            void* slacks, int32_t* status, int32_t* iterations, void* residual,
+                            uint8_t* finite_out, uint8_t* eligible, void* saved) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  purin_cp_solve_options o;
+  purin_cp_default_solve_options(&o);
+  if (opts) o = *opts;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64)
+    return project_impl<double>(p, st, batch, (const double*)target, (const double*)rhs,
+                                (const double*)mult0, o, (double*)y, (double*)mult,
+                                (double*)slacks, status, iterations, (double*)residual,
+                                finite_out, eligible, saved, (const double*)values, true);
+  return project_impl<float>(p, st, batch, (const float*)target, (const float*)rhs,
+                             (const float*)mult0, o, (float*)y, (float*)mult, (float*)slacks,
+                             status, iterations, (float*)residual, finite_out, eligible, saved,
+                             (const float*)values, true);
 }
 
 }  // extern "C"

@@ -16,10 +16,41 @@ struct Layout {
   // forward workspace
   size_t YB, MF, DF, SL, colpart, rowpart, done, count, ndone, ores, ogap, ofin, X, Z;
   size_t RTs, RRs, RD0, RLs, RHs;  // resident path (slot-ordered inputs)
+  // per-sample coefficients (values given per call): entry values in the
+  // caller's order (VF), the kept CSR / CSC entries original (RVo, CVo) and
+  // row-scaled (RV, CV), bound-row coefficients (BC), row scales (SC), steps
+  size_t VF, RVo, CVo, RV, CV, BC, SC, SGR, ACB, DCB, STB, RPT, CPT, PX, PZ, PW, PD;
   size_t ws_end;
 };
 
-Layout make_layout(const purin_cp_plan* p, int64_t batch);
+Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values = false);
+
+// Per-sample coefficient arrays prepared for one call (see persample.hpp).
+template <typename T>
+struct PerSample {
+  const T* RVo;   // [nnz][Bp] kept CSR entries, original
+  const T* CVo;   // [nnz][Bp] kept CSC entries, original
+  const T* RV;    // [nnz][Bp] row-scaled CSR
+  const T* CV;    // [nnz][Bp] row-scaled CSC
+  const T* BC;    // [nb][Bp] bound-row coefficients
+  const T* SC;    // [m][Bp] row scales
+  T* sig_rb;      // [m][Bp] diagonal sigma, or nullptr
+  T* a_cb;        // [n][Bp] diagonal prox a, or nullptr
+  T* d_cb;        // [n][Bp] diagonal prox delta, or nullptr
+  T* tau_b;       // [Bp] scalar steps (and schedule state) per sample
+  T* sig_b;
+  T* a_b;
+  T* d_b;
+  T* th_b;
+  T* tol_b;       // [Bp] stop-test tolerance
+};
+
+// Gather and prepare the per-sample arrays from values (batch-major (B, nnz_full)
+// in the plan's CSR entry order); ``adjoint`` selects the adjoint's steps
+// (power-iteration L with tau = s/(1+L), or the diagonal steps).  forward.hip.
+template <typename T>
+int prepare_values(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout& L, char* ws,
+                   const T* values, T tol, bool adjoint, PerSample<T>* ps);
 
 inline dim3 tile_grid(int64_t Bp, int64_t tile, int64_t blocks) {
   return dim3((unsigned)(Bp / tile), (unsigned)std::max<int64_t>(1, std::min<int64_t>(blocks, 65535)));
@@ -37,6 +68,9 @@ inline Mat<T> kept_matrix(const purin_cp_plan* p, bool scaled) {
   K.cptr = p->cptr;
   K.cidx = p->cidx;
   K.cval = (const T*)(scaled ? p->cval_s : p->cval_o);
+  K.rvb = nullptr;
+  K.cvb = nullptr;
+  K.vbp = 0;
   return K;
 }
 

@@ -30,7 +30,24 @@ struct Mat {
   const int32_t* __restrict__ cptr;
   const int32_t* __restrict__ cidx;
   const T* __restrict__ cval;
+  // Per-sample coefficients (parameter-dependent rows, the reference's
+  // values (B, m, w), src/purin/linalg/sparse/operators.py:515, 528): entry k
+  // of sample b at rvb[k * vbp + b] (CSR order) / cvb[k * vbp + b] (CSC
+  // order).  nullptr: the coefficients rval / cval are shared by the batch.
+  const T* __restrict__ rvb;
+  const T* __restrict__ cvb;
+  int64_t vbp;
 };
+
+// Coefficient of CSR entry k (CSC entry k) for the S samples from b0.
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V row_coef(const Mat<T>& K, int k, int64_t b0) {
+  return K.rvb ? vload(K.rvb + (size_t)k * K.vbp + b0) : vsplat<T>(K.rval[k]);
+}
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V col_coef(const Mat<T>& K, int k, int64_t b0) {
+  return K.cvb ? vload(K.cvb + (size_t)k * K.vbp + b0) : vsplat<T>(K.cval[k]);
+}
 
 template <typename T>
 struct Iter {
@@ -51,10 +68,45 @@ struct Iter {
   const T* __restrict__ sig_r;  // m or nullptr
   const T* __restrict__ a_c;    // n or nullptr
   const T* __restrict__ d_c;    // n or nullptr
+  // per-sample steps (per-sample coefficients: each sample has its own norm
+  // bound and accelerated schedule): [Bp] arrays, or with diagonal steps
+  // [m][Bp] (sigma) and [n][Bp] (a, delta); nullptr when shared
+  const T* __restrict__ sig_b;
+  const T* __restrict__ a_b;
+  const T* __restrict__ d_b;
+  const T* __restrict__ th_b;
+  const T* __restrict__ sig_rb;
+  const T* __restrict__ a_cb;
+  const T* __restrict__ d_cb;
   T* colpart;                 // [5][ncb][Bp]: primal, dual, stat, bound, finite
   T* rowpart;                 // [3][nrb][Bp]: residual max, r.d, finite
   int ncb, nrb;
 };
+
+// Step sizes of row i / column j for the S samples from b0 (shared scalar,
+// diagonal, per-sample or per-sample diagonal).
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V step_sigma(const Iter<T>& A, int i, int64_t b0) {
+  if (A.sig_rb) return vload(A.sig_rb + (size_t)i * A.Bp + b0);
+  if (A.sig_b) return vload(A.sig_b + b0);
+  return vsplat<T>(A.sig_r ? A.sig_r[i] : A.sigma);
+}
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V step_a(const Iter<T>& A, int j, int64_t b0) {
+  if (A.a_cb) return vload(A.a_cb + (size_t)j * A.Bp + b0);
+  if (A.a_b) return vload(A.a_b + b0);
+  return vsplat<T>(A.a_c ? A.a_c[j] : A.a);
+}
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V step_delta(const Iter<T>& A, int j, int64_t b0) {
+  if (A.d_cb) return vload(A.d_cb + (size_t)j * A.Bp + b0);
+  if (A.d_b) return vload(A.d_b + b0);
+  return vsplat<T>(A.d_c ? A.d_c[j] : A.delta);
+}
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V step_theta(const Iter<T>& A, int64_t b0) {
+  return A.th_b ? vload(A.th_b + b0) : vsplat<T>(A.theta);
+}
 
 // ---------------------------------------------------------------------------
 // row pass: d <- P(d + sigma (K ybar - r)) for samples not yet done
@@ -77,15 +129,13 @@ __global__ __launch_bounds__(kBlock) void k_row_pass(Iter<T> A) {
     const int s0 = A.K.rptr[i], s1 = A.K.rptr[i + 1];
     V acc = vsplat<T>(T(0));
     for (int k = s0; k < s1; ++k) {
-      const T v = A.K.rval[k];
       const V x = vload(A.YB + (size_t)A.K.ridx[k] * A.Bp + b0);
-      acc += v * x;
+      acc += row_coef(A.K, k, b0) * x;
     }
     T* dp = A.D + (size_t)i * A.Bp + b0;
     const V d = vload(dp);
     const V r = vload(A.R + (size_t)i * A.Bp + b0);
-    const T sg = A.sig_r ? A.sig_r[i] : A.sigma;
-    V p = d + sg * (acc - r);
+    V p = d + step_sigma(A, i, b0) * (acc - r);
     if (i >= A.K.me) {
 #pragma unroll
       for (int s = 0; s < S; ++s) p[s] = maxp(p[s], T(0));
@@ -124,9 +174,8 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
       const int s0 = A.K.cptr[j], s1 = A.K.cptr[j + 1];
       V t = vsplat<T>(zero);
       for (int k = s0; k < s1; ++k) {
-        const T v = A.K.cval[k];
         const V dd = vload(A.D + (size_t)A.K.cidx[k] * A.Bp + b0);
-        t += v * dd;
+        t += col_coef(A.K, k, b0) * dd;
       }
       const size_t off = (size_t)j * A.Bp + b0;
       const V y = vload(A.Y + off);
@@ -143,11 +192,11 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
       if (MODE == 2) {
         yn = y;
       } else {
-        const T aj = A.a_c ? A.a_c[j] : A.a, dj = A.d_c ? A.d_c[j] : A.delta;
+        const V aj = step_a(A, j, b0), dj = step_delta(A, j, b0);
         const V sv = aj * y - dj * t + dj * tg;
 #pragma unroll
         for (int s = 0; s < S; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
-        V yb = yn + A.theta * (yn - y);
+        V yb = yn + step_theta(A, b0) * (yn - y);
         if (MODE == 1) {
           const V yo = y;
           const V ybo = vload(A.YB + off);
@@ -219,10 +268,8 @@ __global__ __launch_bounds__(kBlock) void k_res_pass(Iter<T> A) {
       if (i >= A.K.m) break;
       const int s0 = A.K.rptr[i], s1 = A.K.rptr[i + 1];
       V acc = vsplat<T>(zero);
-      for (int k = s0; k < s1; ++k) {
-        const T v = A.K.rval[k];
-        acc += v * vload(A.Y + (size_t)A.K.ridx[k] * A.Bp + b0);
-      }
+      for (int k = s0; k < s1; ++k)
+        acc += row_coef(A.K, k, b0) * vload(A.Y + (size_t)A.K.ridx[k] * A.Bp + b0);
       const size_t off = (size_t)i * A.Bp + b0;
       const V r = vload(A.R + off);
       const V d = vload(A.D + off);
@@ -394,15 +441,17 @@ __global__ void k_fill(T* p, int64_t count, T v) {
 // D[i] = MF[kept[i]] / scale_i (bounds.py:230-239).
 template <typename T>
 __global__ void k_prep_rows(int m, int64_t Bp, const int32_t* __restrict__ kept,
-                            const T* __restrict__ scale, const T* __restrict__ RF,
-                            const T* __restrict__ MF, T* __restrict__ R, T* __restrict__ D) {
+                            const T* __restrict__ scale, const T* __restrict__ scale_b,
+                            const T* __restrict__ RF, const T* __restrict__ MF,
+                            T* __restrict__ R, T* __restrict__ D) {
   const int64_t total = (int64_t)m * Bp;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t i = e / Bp, b = e - i * Bp;
     const int64_t src = (int64_t)kept[i] * Bp + b;
-    R[e] = RF[src] * scale[i];
-    D[e] = MF ? MF[src] / scale[i] : T(0);
+    const T sc = scale_b ? scale_b[e] : scale[i];  // per-sample scales: [m][Bp]
+    R[e] = RF[src] * sc;
+    D[e] = MF ? MF[src] / sc : T(0);
   }
 }
 
@@ -411,8 +460,9 @@ __global__ void k_prep_rows(int m, int64_t Bp, const int32_t* __restrict__ kept,
 template <typename T>
 __global__ void k_prep_bounds(int n, int64_t Bp, int64_t cols, const int32_t* __restrict__ bptr,
                               const int32_t* __restrict__ brow, const T* __restrict__ bcoef,
-                              const T* __restrict__ RF, T* __restrict__ LO, T* __restrict__ HI,
-                              int32_t* feasible, int64_t batch) {
+                              const T* __restrict__ bcoef_b, const T* __restrict__ RF,
+                              T* __restrict__ LO, T* __restrict__ HI, int32_t* feasible,
+                              int64_t batch) {
   const int64_t total = (int64_t)n * cols;
   const T inf = __builtin_inf();
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
@@ -421,7 +471,7 @@ __global__ void k_prep_bounds(int n, int64_t Bp, int64_t cols, const int32_t* __
     T lo = -inf, hi = inf;
     bool ok = true;
     for (int k = bptr[j]; k < bptr[j + 1]; ++k) {
-      const T c = bcoef[k];
+      const T c = bcoef_b ? bcoef_b[(int64_t)k * Bp + b] : bcoef[k];  // per-sample: [nb][Bp]
       const T rr = RF[(int64_t)brow[k] * Bp + b];
       const T th = rr / (c != T(0) ? c : T(1));
       if (c < T(0)) lo = maxp(lo, th);
@@ -446,6 +496,7 @@ __global__ void k_prep_bounds(int n, int64_t Bp, int64_t cols, const int32_t* __
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_spmv_rows(Mat<T> K, int64_t Bp, const T* __restrict__ X,
                                                        T* __restrict__ out) {
+#pragma clang fp contract(off)  // rounded products, the oracle's and the host's order
   using V = typename Lane<T>::V;
   constexpr int S = Lane<T>::S;
   const int lane = threadIdx.x & 63;
@@ -456,7 +507,7 @@ __global__ __launch_bounds__(kBlock) void k_spmv_rows(Mat<T> K, int64_t Bp, cons
     if (i >= K.m) continue;
     V acc = vsplat<T>(T(0));
     for (int k = K.rptr[i]; k < K.rptr[i + 1]; ++k)
-      acc += K.rval[k] * vload(X + (size_t)K.ridx[k] * Bp + b0);
+      acc += row_coef(K, k, b0) * vload(X + (size_t)K.ridx[k] * Bp + b0);
     vstore(out + (size_t)i * Bp + b0, acc);
   }
 }
@@ -464,6 +515,7 @@ __global__ __launch_bounds__(kBlock) void k_spmv_rows(Mat<T> K, int64_t Bp, cons
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_spmv_cols(Mat<T> K, int64_t Bp, const T* __restrict__ X,
                                                        T* __restrict__ out) {
+#pragma clang fp contract(off)  // rounded products, the oracle's and the host's order
   using V = typename Lane<T>::V;
   constexpr int S = Lane<T>::S;
   const int lane = threadIdx.x & 63;
@@ -474,7 +526,7 @@ __global__ __launch_bounds__(kBlock) void k_spmv_cols(Mat<T> K, int64_t Bp, cons
     if (j >= K.n) continue;
     V acc = vsplat<T>(T(0));
     for (int k = K.cptr[j]; k < K.cptr[j + 1]; ++k)
-      acc += K.cval[k] * vload(X + (size_t)K.cidx[k] * Bp + b0);
+      acc += col_coef(K, k, b0) * vload(X + (size_t)K.cidx[k] * Bp + b0);
     vstore(out + (size_t)j * Bp + b0, acc);
   }
 }

@@ -120,6 +120,8 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
   const int64_t m = p->m;
   H.ptr.assign(m + 1, 0);
   std::vector<T> scale(m, T(1));
+  // entry maps into the caller's CSR order, for per-sample coefficients
+  std::vector<int32_t> kcsr, kcsc, bpos;
   for (int64_t i = 0; i < m; ++i) {
     const int64_t r = p->kept[i];
     T sq = T(0);
@@ -128,6 +130,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       sq = sq + v * v;
       H.idx.push_back(indices[k]);
       H.val_o.push_back(v);
+      kcsr.push_back((int32_t)k);
     }
     H.ptr[i + 1] = (int32_t)H.idx.size();
     if (p->opts.row_scaling) {
@@ -151,6 +154,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
   H.cidx.resize(p->nnz);
   H.cval_s.resize(p->nnz);
   H.cval_o.resize(p->nnz);
+  kcsc.resize(p->nnz);
   {
     std::vector<int32_t> fill(H.cptr.begin(), H.cptr.end() - 1);
     for (int64_t i = 0; i < m; ++i)
@@ -159,8 +163,11 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         H.cidx[pos] = (int32_t)i;
         H.cval_s[pos] = H.val_s[k];
         H.cval_o[pos] = H.val_o[k];
+        kcsc[pos] = kcsr[k];
       }
   }
+  for (int64_t r : p->bound) bpos.push_back((int32_t)indptr[r]);
+  p->nnz_full = indptr[M];
   // --- forward steps (kernels.py:209-227, norm_bound) -------------------------
   const T safety = (T)p->opts.safety;
   {
@@ -208,6 +215,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
   }
   // --- power iteration on K^T K (kernels.py:52-65) ----------------------------
   T Lpi;
+  std::vector<T> ps_start;
   {
     std::vector<T> x(n), z(m), w(n);
     const T eps = (T)1e-12;
@@ -216,6 +224,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
     for (int64_t j = 0; j < n; ++j) nx = nx + x[j] * x[j];
     nx = std::sqrt(nx) + eps;
     for (int64_t j = 0; j < n; ++j) x[j] = x[j] / nx;
+    ps_start = x;  // the normalised start vector, shared by every sample
     T eig = T(0);
     for (int it = 0; it < p->opts.norm_iterations; ++it) {
       for (int64_t i = 0; i < m; ++i) {
@@ -435,6 +444,10 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
     UP(p->diag_d, dd);
   }
   UP(p->dkept, kept32);
+  UP(p->ps_kcsr, kcsr);
+  UP(p->ps_kcsc, kcsc);
+  UP(p->ps_bpos, bpos);
+  UP(p->ps_start, ps_start);
   UP(p->bptr, bptr);
   UP(p->brow, brow32);
   UP(p->dbcoef, bcoefT);

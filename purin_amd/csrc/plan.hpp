@@ -51,6 +51,13 @@ struct purin_cp_plan {
   int32_t* brow = nullptr;  // original row of each bound row
   void* dbcoef = nullptr;   // coefficient of each bound row
   void* metric = nullptr;   // sqrt(D) (n) or nullptr
+  // per-sample coefficients: positions in the caller's CSR entry order of
+  // each kept CSR entry, each kept CSC entry and each bound row's entry
+  int64_t nnz_full = 0;
+  int32_t* ps_kcsr = nullptr;
+  int32_t* ps_kcsc = nullptr;
+  int32_t* ps_bpos = nullptr;
+  void* ps_start = nullptr;  // n: normalised power-iteration start vector
   // diagonal preconditioning (non-accelerated): per-row sigma (m), per-column
   // prox coefficients a and delta (n); nullptr when the steps are scalars
   bool diag = false;

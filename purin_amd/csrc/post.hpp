@@ -13,10 +13,12 @@ struct Post {
   Mat<T> K;                      // kept rows, ORIGINAL coefficients
   int64_t Bp, me, mi;
   const T* __restrict__ scale;   // m
+  const T* __restrict__ scale_b; // per-sample coefficients: [m][Bp] scales, else nullptr
   const int32_t* __restrict__ kept;
   const int32_t* __restrict__ bptr;
   const int32_t* __restrict__ brow;
   const T* __restrict__ bcoef;
+  const T* __restrict__ bcoef_b; // per-sample coefficients: [nb][Bp], else nullptr
   const T* __restrict__ tgt;     // n x Bp
   const T* __restrict__ Y;       // n x Bp
   const T* __restrict__ D;       // m x Bp (scaled duals)
@@ -30,6 +32,16 @@ struct Post {
   T* colpart;                    // [3][ncb][Bp]: residual max (bound rows), stationarity, finite
   int nrb, ncb;
 };
+
+// Row scale of kept row i / coefficient of bound row k for the S samples from b0.
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V post_scale(const Post<T>& P, int i, int64_t b0) {
+  return P.scale_b ? vload(P.scale_b + (size_t)i * P.Bp + b0) : vsplat<T>(P.scale[i]);
+}
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V post_bcoef(const Post<T>& P, int k, int64_t b0) {
+  return P.bcoef_b ? vload(P.bcoef_b + (size_t)k * P.Bp + b0) : vsplat<T>(P.bcoef[k]);
+}
 
 // Kept rows: multiplier = d * scale (bounds.py:247), r = K y - rhs (285-289),
 // slack = max(-r, 0) for inequality rows (311).
@@ -48,13 +60,11 @@ __global__ __launch_bounds__(kBlock) void k_post_rows(Post<T> P) {
       if (i >= P.K.m) break;
       const int s0 = P.K.rptr[i], s1 = P.K.rptr[i + 1];
       V acc = vsplat<T>(zero);
-      for (int k = s0; k < s1; ++k) {
-        const T v = P.K.rval[k];
-        acc += v * vload(P.Y + (size_t)P.K.ridx[k] * P.Bp + b0);
-      }
+      for (int k = s0; k < s1; ++k)
+        acc += row_coef(P.K, k, b0) * vload(P.Y + (size_t)P.K.ridx[k] * P.Bp + b0);
       const int64_t row = P.kept[i];
       const V d = vload(P.D + (size_t)i * P.Bp + b0);
-      const V full = d * P.scale[i];
+      const V full = d * post_scale(P, i, b0);
       vstore(P.DF + (size_t)row * P.Bp + b0, full);
       const V r = acc - vload(P.RF + (size_t)row * P.Bp + b0);
       if (row < P.me) {
@@ -104,8 +114,7 @@ __global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
       V tk = vsplat<T>(zero);
       for (int k = s0; k < s1; ++k) {
         const int i = P.K.cidx[k];
-        const T v = P.K.cval[k];
-        tk += v * (vload(P.D + (size_t)i * P.Bp + b0) * P.scale[i]);
+        tk += col_coef(P.K, k, b0) * (vload(P.D + (size_t)i * P.Bp + b0) * post_scale(P, i, b0));
       }
       const size_t off = (size_t)j * P.Bp + b0;
       const V y = vload(P.Y + off);
@@ -122,10 +131,11 @@ __global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
       const int k0 = P.bptr[j], k1 = P.bptr[j + 1];
       V lc = vsplat<T>(zero), uc = vsplat<T>(zero);
       for (int k = k0; k < k1; ++k) {
-        const T cf = P.bcoef[k];
+        const V cfv = post_bcoef(P, k, b0);
         const V rr = vload(P.RF + (size_t)P.brow[k] * P.Bp + b0);
 #pragma unroll
         for (int s = 0; s < S; ++s) {
+          const T cf = cfv[s];
           const T th = rr[s] / (cf != zero ? cf : one);
           lc[s] += (cf < zero && th == lo[s] && y[s] == lo[s]) ? one : zero;
           uc[s] += (cf > zero && th == hi[s] && y[s] == hi[s]) ? one : zero;
@@ -133,12 +143,13 @@ __global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
       }
       V tfull = tk;
       for (int k = k0; k < k1; ++k) {
-        const T cf = P.bcoef[k];
+        const V cfv = post_bcoef(P, k, b0);
         const int64_t row = P.brow[k];
         const V rr = vload(P.RF + (size_t)row * P.Bp + b0);
         V bd, sl;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
+          const T cf = cfv[s];
           const T th = rr[s] / (cf != zero ? cf : one);
           const bool il = cf < zero && th == lo[s] && y[s] == lo[s];
           const bool iu = cf > zero && th == hi[s] && y[s] == hi[s];

@@ -75,6 +75,7 @@ class AdjointOutput:
     valid: torch.Tensor
     info: torch.Tensor
     residual: torch.Tensor
+    g_values: torch.Tensor | None = None
 
 
 class Plan:
@@ -113,6 +114,7 @@ class Plan:
             values.ctypes.data_as(C.POINTER(C.c_double)), C.byref(opts)))
         self.handle = handle
         self.n, self.me, self.mi = int(n), int(me), int(mi)
+        self.nnz = int(indptr[-1])  # entries of the caller's CSR (per-sample values width)
         info = _lib.PlanInfo()
         _lib.check(self.lib.purin_cp_plan_get_info(self.handle, C.byref(info)))
         self.info = info
@@ -222,12 +224,18 @@ class Plan:
 
     def project(self, target, rhs, *, multipliers0=None, tolerance=1e-9, max_iterations=10000,
                 early_stop=True, check_every=32, shared_bounds=False, save=False, timing=False,
-                streaming=False):
-        """Full projection (``purin_cp_project``): BoundProjection.solve semantics."""
+                streaming=False, values=None):
+        """Full projection (``purin_cp_project``): BoundProjection.solve semantics.
+
+        ``values`` (B, nnz): per-sample coefficients in the plan's CSR entry order
+        (``purin_cp_project_values``); the plan's own coefficients are then unused.
+        """
         batch = target.shape[0]
         M = self.me + self.mi
         target = self._tensor(target, (batch, self.n), "y_hat")
         rhs = self._tensor(rhs, (batch, M), "rhs")
+        if values is not None:
+            values = self._tensor(values, (batch, self.nnz), "values")
         mult0 = None if multipliers0 is None else self._tensor(multipliers0, (batch, M),
                                                                "multipliers")
         o = _lib.default_solve_options()
@@ -247,6 +255,13 @@ class Plan:
         fin = self._empty(batch, dtype=torch.uint8)
         elig = self._empty(batch, dtype=torch.uint8)
         saved = self._empty(self.saved_bytes(batch), dtype=torch.uint8) if save else None
+        if values is not None:
+            _lib.check(self.lib.purin_cp_project_values(
+                self.handle, _stream(), batch, _ptr(values), _ptr(target), _ptr(rhs),
+                _ptr(mult0), C.byref(o), _ptr(y), _ptr(mult), _ptr(slacks), _i32(status),
+                _i32(it), _ptr(res), _u8(fin), _u8(elig), _ptr(saved)))
+            return ProjectOutput(y, mult, slacks, status, it, res, fin.bool(), elig.bool(),
+                                 saved)
         _lib.check(self.lib.purin_cp_project(
             self.handle, _stream(), batch, _ptr(target), _ptr(rhs), _ptr(mult0), C.byref(o),
             _ptr(y), _ptr(mult), _ptr(slacks), _i32(status), _i32(it), _ptr(res), _u8(fin),
@@ -255,8 +270,12 @@ class Plan:
 
     def adjoint(self, saved, target, rhs, cot_y, *, tolerance=1e-9, atol=0.0, restart=30,
                 max_iterations=100, adjoint_tolerance=1e-8, force_eligible=False,
-                bounds_grad=False, rhs_rows=None):
-        """Implicit VJP at a saved forward state (``purin_cp_adjoint``)."""
+                bounds_grad=False, rhs_rows=None, values=None):
+        """Implicit VJP at a saved forward state (``purin_cp_adjoint``).
+
+        ``values``: the per-sample coefficients of a ``project(..., values=...)``
+        state (``purin_cp_adjoint_values``); the result then carries ``g_values``.
+        """
         batch = cot_y.shape[0]
         rows = rhs_rows if rhs_rows is not None else self.me + self.mi
         # target and rhs are held by the saved state; they are accepted for interface
@@ -278,6 +297,13 @@ class Plan:
         valid = self._empty(batch, dtype=torch.uint8)
         info = self._empty(batch, dtype=torch.int32)
         res = self._empty(batch)
+        if values is not None:
+            values = self._tensor(values, (batch, self.nnz), "values")
+            gv = self._empty(batch, self.nnz)
+            _lib.check(self.lib.purin_cp_adjoint_values(
+                self.handle, _stream(), batch, _ptr(saved), _ptr(values), _ptr(cot), C.byref(o),
+                _ptr(gt), _ptr(gr), _ptr(gv), _u8(valid), _i32(info), _ptr(res)))
+            return AdjointOutput(gt, gr, None, None, valid.bool(), info, res, gv)
         _lib.check(self.lib.purin_cp_adjoint(
             self.handle, _stream(), batch, _ptr(saved), _ptr(target), _ptr(rhs), _ptr(cot),
             C.byref(o), _ptr(gt), _ptr(gr), _ptr(gl), _ptr(gu), _u8(valid), _i32(info),
