@@ -39,6 +39,17 @@ class CanonicalRows:
     variable_names: tuple = ()
     affine: bool = True
     parametric_coefficients: bool = False
+    # per-entry coefficient map: values(theta) = values + theta @ value_map.T,
+    # (nnz, parameter_size), when coefficients depend on parameters
+    value_map: np.ndarray | None = None
+    parameter_affine: bool = True  # rows (coefficients and rhs) affine in theta
+
+    def coefficient_values(self, theta):
+        """(B, nnz) coefficient values at theta (the plan's CSR entry order)."""
+        theta = np.asarray(theta, np.float64).reshape(-1, self.parameter_size)
+        if self.value_map is None:
+            return np.broadcast_to(self.values, (theta.shape[0], self.values.size))
+        return self.values[None, :] + theta @ self.value_map.T
 
     def rhs(self, theta):
         theta = np.asarray(theta, np.float64).reshape(-1, self.parameter_size)
@@ -308,8 +319,8 @@ class Projection:
         n, p = len(self.variable_names), len(self.parameter_names)
         eq = [c for c in self.constraints if c.kind == "eq"]
         iq = [c for c in self.constraints if c.kind == "ineq"]
-        rows, vals, rhs0, rmap = [], [], [], []
-        affine, parametric = True, False
+        rows, vals, vmaps, rhs0, rmap = [], [], [], [], []
+        affine, parametric, par_affine = True, False, True
         for c in eq + iq:
             r = c.residual
             if r.nonlinear:
@@ -317,10 +328,16 @@ class Projection:
             if r.bil:
                 parametric = True
             if r.par_nonlinear:
-                parametric = True
+                par_affine = False
             cols = sorted(r.deps)
             rows.append(cols)
             vals.append([r.var.get(j, 0.0) for j in cols])
+            for j in cols:  # coefficient of variable j: var[j] + sum_k bil[(j, k)] theta_k
+                v = np.zeros(p)
+                for (jj, k), w in r.bil.items():
+                    if jj == j:
+                        v[k] += w
+                vmaps.append(v)
             rhs0.append(-r.const)
             m = np.zeros(p)
             for k, v in r.par.items():
@@ -330,9 +347,10 @@ class Projection:
         indptr[1:] = np.cumsum([len(r) for r in rows])
         indices = np.asarray([c for r in rows for c in r], np.int32)
         values = np.asarray([v for r in vals for v in r], np.float64)
+        value_map = np.asarray(vmaps, np.float64).reshape(len(values), p) if parametric else None
         return CanonicalRows(n, len(eq), len(iq), p, indptr, indices, values,
                              np.asarray(rhs0, np.float64), np.asarray(rmap, np.float64).reshape(len(rows), p),
-                             tuple(self.variable_names), affine, parametric)
+                             tuple(self.variable_names), affine, parametric, value_map, par_affine)
 
 
 # ---------------------------------------------------------------------------

@@ -13,7 +13,9 @@ are moved to the device like ``jax.device_put``).  ``__call__`` and
 ``project_training(...).y_tilde`` are differentiable with torch autograd: the
 backward is the implicit VJP of ``purin_cp_adjoint`` w.r.t. ``y_hat`` and, when
 ``ImplicitGradientConfig.differentiate_problem_parameters`` is set, w.r.t. the
-parameters through ``rhs(theta)``.  Every computation runs in the HIP library;
+parameters through ``rhs(theta)`` and, for parameter-dependent coefficients,
+through the per-sample values ``values(theta)`` (``purin_cp_project_values`` /
+``purin_cp_adjoint_values``).  Every computation runs in the HIP library;
 ``backend="cpu"`` is rejected because this build has no CPU execution path.
 """
 
@@ -62,14 +64,20 @@ def resolve_dtype(dtype):
 
 
 class _ProjectFn(torch.autograd.Function):
-    """y = P(y_hat; rhs) with the implicit VJP of the HIP adjoint."""
+    """y = P(y_hat; rhs, values) with the implicit VJP of the HIP adjoint.
+
+    ``values`` (B, nnz) are per-sample coefficients (parameter-dependent rows)
+    or None for the plan's shared ones.
+    """
 
     @staticmethod
-    def forward(ctx, y_hat, rhs, layer, multipliers0):
-        out = layer.plan.project(y_hat, rhs, multipliers0=multipliers0, save=True,
+    def forward(ctx, y_hat, rhs, values, layer, multipliers0):
+        vals = None if values is None else values.detach().contiguous()
+        out = layer.plan.project(y_hat, rhs, multipliers0=multipliers0, save=True, values=vals,
                                  **layer._solve_kwargs())
         ctx.layer = layer
         ctx.saved_state = out.saved
+        ctx.values = vals
         ctx.shapes = (y_hat.shape, rhs.shape)
         ctx.mark_non_differentiable(out.multipliers, out.slacks, out.status, out.iterations,
                                     out.residual, out.finite, out.eligible)
@@ -80,15 +88,16 @@ class _ProjectFn(torch.autograd.Function):
     def backward(ctx, cot_y, *unused):
         layer = ctx.layer
         if cot_y is None:
-            return None, None, None, None
+            return None, None, None, None, None
         lin = layer.config.linear_solver
         adj = layer.plan.adjoint(ctx.saved_state, None, None, cot_y.contiguous(),
                                  tolerance=lin.tolerance, atol=lin.atol, restart=lin.restart,
                                  max_iterations=lin.max_iterations,
                                  adjoint_tolerance=layer.config.implicit_gradient.adjoint_tolerance,
-                                 rhs_rows=layer.plan.me + layer.plan.mi)
+                                 rhs_rows=layer.plan.me + layer.plan.mi, values=ctx.values)
         g_rhs = adj.g_rhs if ctx.needs_input_grad[1] else None
-        return adj.g_target, g_rhs, None, None
+        g_values = adj.g_values if ctx.needs_input_grad[2] else None
+        return adj.g_target, g_rhs, g_values, None, None
 
 
 @dataclass(eq=False)
@@ -106,11 +115,10 @@ class PreparedChambollePockProjection:
         if not c.affine:
             raise ValueError("chambolle-pock requires verified affine equalities and "
                              "inequalities; nonlinear or unverified constraints are unsupported")
-        if c.parametric_coefficients:
+        if not c.parameter_affine:
             raise NotImplementedError(
-                "parameter-dependent constraint coefficients (per-sample matrices) are not "
-                "supported by the shared-matrix HIP path; only right-hand sides may depend on "
-                "parameters")
+                "constraint coefficients and right-hand sides must be affine in the parameters "
+                "(products of parameters are not supported by the symbolic layer)")
         if self.batch_size < 1 or c.n < 1:
             raise ValueError("batch_size and variable_size must be positive")
         self.device = resolve_device(self.backend)
@@ -137,6 +145,16 @@ class PreparedChambollePockProjection:
             self.plan.set_metric(root)
         self._rhs0 = torch.as_tensor(c.rhs0, dtype=self.torch_dtype, device=self.device)
         self._rhs_map = torch.as_tensor(c.rhs_map, dtype=self.torch_dtype, device=self.device)
+        # parameter-dependent coefficients: values(theta) = values0 + theta @ value_map.T
+        # per sample (the reference's vmap(_numeric_one), bounds.py:192), scaled by the
+        # metric like the shared values
+        self._values0 = self._value_map = None
+        if c.parametric_coefficients:
+            vmap = np.asarray(c.value_map, np.float64)
+            if self.metric is not None:
+                vmap = vmap * (1 / np.sqrt(self.metric))[c.indices][:, None]
+            self._values0 = torch.as_tensor(values, dtype=self.torch_dtype, device=self.device)
+            self._value_map = torch.as_tensor(vmap, dtype=self.torch_dtype, device=self.device)
 
     # -- sizes (solver.py:67-85) ---------------------------------------------------
     @property
@@ -169,7 +187,7 @@ class PreparedChambollePockProjection:
                              f"got {tuple(t.shape)}")
         return t
 
-    def _rhs(self, parameters):
+    def _theta(self, parameters):
         p = self.parameter_size
         if parameters is None:
             if p:
@@ -182,7 +200,15 @@ class PreparedChambollePockProjection:
                                  f"got {tuple(theta.shape)}")
         if not self.config.implicit_gradient.differentiate_problem_parameters:
             theta = theta.detach()
+        return theta
+
+    def _rhs(self, theta):
         return self._rhs0[None, :] + theta @ self._rhs_map.T
+
+    def _values(self, theta):
+        if self._value_map is None:
+            return None
+        return self._values0[None, :] + theta @ self._value_map.T
 
     def _multipliers0(self, eq, iq):
         if eq is None and iq is None:
@@ -198,9 +224,12 @@ class PreparedChambollePockProjection:
 
     def _run(self, y_hat, parameters, multipliers_eq=None, multipliers_ineq=None):
         target = self._target(y_hat)
-        rhs = self._rhs(parameters)
+        theta = self._theta(parameters)
+        rhs = self._rhs(theta)
+        values = self._values(theta)
         mult0 = self._multipliers0(multipliers_eq, multipliers_ineq)
-        y, mult, slacks, status, iters, res, fin, elig = _ProjectFn.apply(target, rhs, self, mult0)
+        y, mult, slacks, status, iters, res, fin, elig = _ProjectFn.apply(target, rhs, values,
+                                                                          self, mult0)
         me = self.equality_size
         return ProjectionResult(y, mult[:, :me], mult[:, me:], slacks, status, iters, res, fin,
                                 elig)

@@ -51,6 +51,29 @@ def test_nonlinear_and_parametric_coefficients_are_flagged():
         bool(z.u <= 1)
 
 
+def test_parameter_dependent_coefficients_form_an_affine_value_map():
+    """``(2a + 1) u - b v <= 3 + b`` and ``a u >= 0``: per-entry values
+    values0 + theta @ value_map.T in the CSR entry order; a structural entry
+    whose constant part is zero stays in the row's support."""
+    q = pa.Projection()
+    t = q.add_parameter(["a", "b"])
+    z = q.add_variable(["u", "v"])
+    q.constraints.add((2 * t.a + 1) * z.u - t.b * z.v <= 3 + t.b, t.a * z.u >= 0)
+    c = q.canonicalize()
+    assert c.parametric_coefficients and c.parameter_affine and c.affine
+    np.testing.assert_array_equal(c.indptr, [0, 2, 3])
+    np.testing.assert_array_equal(c.indices, [0, 1, 0])
+    np.testing.assert_array_equal(c.values, [1.0, 0.0, 0.0])
+    np.testing.assert_array_equal(c.value_map, [[2.0, 0.0], [0.0, -1.0], [-1.0, 0.0]])
+    np.testing.assert_allclose(c.coefficient_values([[0.5, 2.0]]), [[2.0, -2.0, -0.5]])
+    np.testing.assert_allclose(c.rhs([[0.5, 2.0]]), [[5.0, 0.0]])
+    r = pa.Projection()
+    s = r.add_parameter(["a"])
+    w = r.add_variable(["u"])
+    r.constraints.add(w.u <= s.a * s.a)
+    assert not r.canonicalize().parameter_affine
+
+
 def test_duplicate_symbols_rejected():
     p = pa.Projection()
     p.add_variable(["u"])

@@ -271,12 +271,72 @@ def test_weighted_projection_protocol_and_gradient(torch):
     np.testing.assert_allclose(d, [[0.2, -0.8], [-0.2, 0.8]], atol=2e-5)
 
 
-def test_parametric_coefficients_are_reported_unsupported(torch):
+@pytest.mark.parametrize("diagonal", [False, True])
+def test_parameter_dependent_sparse_coefficients(torch, diagonal):
+    """Reference tests/test_regression_chambolle_pock.py:116-137 and
+    tests/test_regression_cp_diagonal_steps.py:83-112: ``a u + v == 1``; y and
+    dy/da through torch autograd (purin_cp_project_values / adjoint_values)."""
+    from purin_amd import (ChambollePockConfig, ImplicitGradientConfig, Projection,
+                           prepare_projection)
+
+    p = Projection()
+    t = p.add_parameter(["a"])
+    y = p.add_variable(["u", "v"])
+    p.objective = 0.0
+    p.constraints.add(t.a * y.u + y.v == 1)
+    cfg = ChambollePockConfig(
+        diagonal_preconditioning=diagonal,
+        implicit_gradient=ImplicitGradientConfig(differentiate_problem_parameters=True))
+    layer = prepare_projection(p, method="chambolle-pock", config=cfg, batch_size=1)
+    x = torch.tensor([[0.2, 0.3]], dtype=torch.float64, device="cuda")
+    theta = torch.tensor([[2.0]], dtype=torch.float64, device="cuda")
+
+    def expected(t):
+        a = t[0, 0]
+        return x - torch.stack([a, torch.ones_like(a)])[None] * (a * 0.2 + 0.3 - 1) / (a * a + 1)
+
+    np.testing.assert_allclose(layer(x, theta).detach().cpu(), expected(theta).cpu(), atol=1e-8)
+    np.testing.assert_allclose(jac(torch, lambda t: layer(x, t), theta),
+                               jac(torch, expected, theta), atol=2e-7)
+
+
+def test_parameter_dependent_bound_sign_zero_and_derivative(torch):
+    """Reference tests/test_regression_cp_bound_presolve.py:30-53: ``a u <= b``."""
+    from purin_amd import (ChambollePockConfig, ImplicitGradientConfig, Projection,
+                           prepare_projection)
+
+    p = Projection()
+    t = p.add_parameter(["a", "b"])
+    y = p.add_variable(["u"])
+    p.objective = 0.0
+    p.constraints.add(t.a * y.u <= t.b)
+    cfg = ChambollePockConfig(
+        implicit_gradient=ImplicitGradientConfig(differentiate_problem_parameters=True))
+    layer = prepare_projection(p, method="chambolle-pock", config=cfg, batch_size=1)
+    f64 = dict(dtype=torch.float64, device="cuda")
+    x = torch.tensor([[3.0]], **f64)
+    theta = torch.tensor([[2.0, 1.0]], **f64)
+    np.testing.assert_allclose(layer(x, theta).detach().cpu(), [[0.5]], atol=1e-10)
+    j = jac(torch, lambda z: layer(x, z), theta)
+    np.testing.assert_allclose(j[0, 0, 0], [-0.25, 0.5], atol=1e-8)
+    np.testing.assert_allclose(
+        layer(torch.tensor([[-3.0]], **f64), torch.tensor([[-2.0, 1.0]], **f64)).detach().cpu(),
+        [[-0.5]], atol=1e-10)
+    out = layer.solve(x, torch.tensor([[0.0, -1.0]], **f64))
+    assert not bool(out.gradient_eligible[0])
+    xg = x.clone().requires_grad_(True)
+    layer(xg, torch.tensor([[0.0, -1.0]], **f64)).sum().backward()
+    np.testing.assert_allclose(xg.grad.cpu(), 0.0)
+    np.testing.assert_allclose(layer(x, torch.tensor([[0.0, 1.0]], **f64)).detach().cpu(),
+                               x.cpu())
+
+
+def test_products_of_parameters_are_reported_unsupported(torch):
     from purin_amd import Projection, prepare_projection
 
     p = Projection()
     t = p.add_parameter(["a"])
     y = p.add_variable(["u", "v"])
-    p.constraints.add(t.a * y.u + y.v == 1)
-    with pytest.raises(NotImplementedError, match="per-sample"):
+    p.constraints.add(y.u + y.v == t.a * t.a)
+    with pytest.raises(NotImplementedError, match="affine in the parameters"):
         prepare_projection(p, method="chambolle-pock", batch_size=1)
