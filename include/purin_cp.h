@@ -25,6 +25,9 @@
  *   adjoint      <- custom_vjp ``bwd`` (src/purin/solvers/chambolle_pock/bounds.py:80-165)
  *                   with _batched_restarted_gmres
  *                   (src/purin/solvers/primal_dual_interior_point/operators.py:792-1125)
+ *   project_values / adjoint_values <- the same with per-sample coefficients
+ *                   (bounds.py:192-239)
+ *   qp_solve / qp_adjoint <- PreparedDiagonalQP (src/purin/solvers/diagonal_qp.py:69-319)
  *
  * Errors: entry points return PURIN_CP_OK or an error code for invalid
  * arguments / HIP failures (the reference raises ValueError for shape and
@@ -80,6 +83,11 @@ typedef struct {
   int32_t diagonal_preconditioning; /* per-row/per-column steps when not accelerated
                                        (kernels.py:76-88, 209-210; default 0) */
   double safety;                    /* step safety factor in (0,1) (default 0.95) */
+  int32_t bound_presolve;           /* 1: singleton inequality rows become variable
+                                       bounds (bounds.py:320-326; default 1); 0: every
+                                       row is kept, as the diagonal-QP layer does
+                                       (diagonal_qp.py:96-123) */
+  int32_t reserved;
 } purin_cp_options;
 
 /* Fill *opts with the reference defaults. */
@@ -216,6 +224,27 @@ int purin_cp_project_values(purin_cp_plan* plan, void* stream, int64_t batch,
                             int32_t* iterations, void* residual, uint8_t* finite,
                             uint8_t* eligible, void* saved);
 
+/*
+ * General positive diagonal QP on the plan's rows (PreparedDiagonalQP.solve,
+ * src/purin/solvers/diagonal_qp.py:222-319, through sparse_cp with general q,
+ * kernels.py:178-305):
+ *   min 0.5 y' diag(q) y + c'y  s.t.  K[:me] y == rhs[:me], K[me:] y <= rhs[me:],
+ *                                     lower <= y <= upper,
+ * every row kept (the plan must be created with bound_presolve = 0) and no
+ * metric.  q, c, lower, upper (B, n); values (B, nnz) per-sample
+ * coefficients in the plan's CSR entry order, or NULL for the plan's own;
+ * rhs (B, me+mi); y0 (B, n) or NULL for zero; dual0 (B, me+mi) or NULL.
+ * Outputs y (B, n), multipliers (B, me+mi), slacks (B, mi), status,
+ * iterations, residual (original units), finite, converged (B); each but y
+ * may be NULL.  opts->shared_bounds must be 0.
+ */
+int purin_cp_qp_solve(purin_cp_plan* plan, void* stream, int64_t batch, const void* q,
+                      const void* c, const void* values, const void* rhs, const void* lower,
+                      const void* upper, const void* y0, const void* dual0,
+                      const purin_cp_solve_options* opts, void* y, void* multipliers,
+                      void* slacks, int32_t* status, int32_t* iterations, void* residual,
+                      uint8_t* finite, uint8_t* converged, void* saved);
+
 /* Kernel times of the last solve()/project() call made with opts.timing = 1,
  * from HIP events recorded on that call's stream around each launch. */
 typedef struct {
@@ -274,6 +303,21 @@ int purin_cp_adjoint_values(purin_cp_plan* plan, void* stream, int64_t batch, co
                             const purin_cp_adjoint_options* opts, void* g_target, void* g_rhs,
                             void* g_values, uint8_t* valid, int32_t* info,
                             void* gmres_residual);
+
+/*
+ * Implicit VJP of purin_cp_qp_solve (the custom_vjp bwd of
+ * diagonal_qp.py:131-219) at its saved state, with the same q, c and values
+ * (NULL when the forward used the plan's).  cot_y (B, n); cot_dual (B, me+mi)
+ * cotangent of the multipliers, or NULL.  Outputs (each may be NULL): g_q,
+ * g_c (B, n); g_values (B, nnz); g_rhs (B, me+mi); g_lower, g_upper (B, n);
+ * valid, info, gmres_residual (B).  The row scales are constants of the
+ * derivative (stop_gradient, diagonal_qp.py:252-256).
+ */
+int purin_cp_qp_adjoint(purin_cp_plan* plan, void* stream, int64_t batch, const void* saved,
+                        const void* q, const void* c, const void* values, const void* cot_y,
+                        const void* cot_dual, const purin_cp_adjoint_options* opts, void* g_q,
+                        void* g_c, void* g_values, void* g_rhs, void* g_lower, void* g_upper,
+                        uint8_t* valid, int32_t* info, void* gmres_residual);
 
 /* Work done by the last adjoint() call on this plan.  No reference counterpart
  * (the reference's GMRES returns only per-sample info codes); it reports how

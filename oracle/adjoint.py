@@ -58,13 +58,17 @@ class Linearization(NamedTuple):
     Chi: np.ndarray        # clip derivative w.r.t. upper (B, n)
     ybar: np.ndarray       # linearization point ybar (= y)
     dplus: np.ndarray      # dual after the step at the linearization point
+    q_grad: np.ndarray = None  # (B, n) -tau a s: d(pre-clip s)/dq (general q only)
 
 
-def linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma):
+def linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma,
+              q=None, c=None):
     """Masks of ``cp_step`` at ``z = (y, dual, y)`` with theta = 1 (bounds.py:109-128).
 
     ``tau``/``sigma`` are per sample ``(B,)`` or, with diagonal preconditioning,
-    per variable ``(B, n)`` and per row ``(B, m)`` (bounds.py:83-86).
+    per variable ``(B, n)`` and per row ``(B, m)`` (bounds.py:83-86).  ``q``,
+    ``c``: a general diagonal objective (diagonal_qp.py:163-182); default
+    ``q = 1``, ``c = -target``.
     """
     dtype = y.dtype
     n = y.shape[1]
@@ -74,18 +78,23 @@ def linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau
     _, dpi, _ = _max_grads(p[:, me:], dtype.type(0))
     D = np.concatenate((np.ones_like(p[:, :me]), dpi.astype(dtype)), axis=1)
     dplus = np.concatenate((p[:, :me], np.maximum(p[:, me:], dtype.type(0))), axis=1)
-    q = np.ones_like(y)
-    a, delta, offset = _cp.proximal_coefficients(q, -target, tau)
+    general = q is not None
+    q = np.ones_like(y) if q is None else np.asarray(q, dtype)
+    c = -target if c is None else np.asarray(c, dtype)
+    a, delta, offset = _cp.proximal_coefficients(q, c, tau)
     s = a * y - delta * tmv(dplus) + offset
+    # d s / d q with a = 1/(1 + tau q), delta = tau a: -tau a s
+    q_grad = -(np.broadcast_to(tau[:, None] if np.ndim(tau) == 1 else tau, s.shape) * a * s) \
+        if general else None
     m1, ds, dlo = _max_grads(s, lower)
     _, dm1, dhi = _min_grads(m1, upper)
     C = (dm1 * ds).astype(dtype)
     Clo = (dm1 * dlo).astype(dtype)
     Chi = dhi.astype(dtype)
-    if np.ndim(tau) == 1:
-        a, delta = a[:, :1], delta[:, :1]
+    if np.ndim(tau) == 1 and not general:
+        a, delta = a[:, :1], delta[:, :1]  # q = 1: one prox coefficient per sample
     return Linearization(values, support, mask, me, n, a, delta, sig, D, C, Clo, Chi, y.copy(),
-                         dplus)
+                         dplus, q_grad)
 
 
 class Pullback(NamedTuple):
@@ -97,6 +106,7 @@ class Pullback(NamedTuple):
     g_target: np.ndarray
     g_lower: np.ndarray
     g_upper: np.ndarray
+    g_q: np.ndarray = None  # general q only: -tau a u s
 
 
 def pullback(lin, gy, gd, gb):
@@ -128,7 +138,7 @@ def pullback(lin, gy, gd, gb):
     g_values = np.where(lin.mask[None], lin.sigma[:, :, None] * w[:, :, None] * ybar_g
                         - delta_g * lin.dplus[:, :, None] * u_g, 0)
     return Pullback(gz_y, gz_d, gz_b, g_values, -lin.sigma * w, lin.delta * u,
-                    lin.Clo * G, lin.Chi * G)
+                    lin.Clo * G, lin.Chi * G, None if lin.q_grad is None else lin.q_grad * u)
 
 
 def batched_restarted_gmres(matvec, rhs, *, tolerance, absolute_tolerance, restart,
@@ -251,6 +261,7 @@ class AdjointResult(NamedTuple):
     lam: np.ndarray
     tau: np.ndarray
     sigma: np.ndarray
+    g_q: np.ndarray = None
 
 
 def adjoint_steps(values, support, mask, n, batch, dtype, cfg):
@@ -267,20 +278,28 @@ def adjoint_steps(values, support, mask, n, batch, dtype, cfg):
 
 
 def adjoint(values, support, mask, me, y, dual, converged, target, rhs, lower, upper,
-            cot_y, cfg, steps=None):
-    """Custom-VJP backward of the CP solve; bounds.py:80-165 (solver.py:186-272)."""
+            cot_y, cfg, steps=None, q=None, c=None, cot_dual=None):
+    """Custom-VJP backward of the CP solve; bounds.py:80-165 (solver.py:186-272).
+
+    With ``q``, ``c`` (and optionally ``cot_dual``, the dual's cotangent) it is
+    the general diagonal QP's backward, diagonal_qp.py:131-219; the caller
+    then passes its ``steps``.  ``g_target`` is ``delta u``; the QP's
+    ``g_c`` is its negative.
+    """
     dtype = y.dtype
     batch, n = y.shape
     m = dual.shape[1]
     tau, sigma = adjoint_steps(values, support, mask, n, batch, dtype, cfg) if steps is None else steps
-    lin = linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma)
+    lin = linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma,
+                    q=q, c=c)
 
     def operator(v):
         pb = pullback(lin, v[:, :n], v[:, n:n + m], v[:, n + m:])
         return v - np.concatenate((pb.gy, pb.gd, pb.gbar), axis=1)
 
-    g = np.concatenate((np.where(converged[:, None], cot_y, 0).astype(dtype),
-                        np.zeros_like(dual), np.zeros_like(y)), axis=1)
+    gd0 = np.zeros_like(dual) if cot_dual is None else np.asarray(cot_dual, dtype)
+    g = np.concatenate((np.asarray(cot_y, dtype), gd0, np.zeros_like(y)), axis=1)
+    g = np.where(converged[:, None], g, 0).astype(dtype)
     lam, info, residual, _ = batched_restarted_gmres(
         operator, g, tolerance=cfg.gmres_tolerance, absolute_tolerance=cfg.gmres_atol,
         restart=cfg.gmres_restart, max_iterations=cfg.gmres_max_iterations)
@@ -294,4 +313,4 @@ def adjoint(values, support, mask, me, y, dual, converged, target, rhs, lower, u
 
     return AdjointResult(clean(pb.g_values), clean(pb.g_rhs), clean(pb.g_target),
                          clean(pb.g_lower), clean(pb.g_upper), valid, info, residual, lam,
-                         tau, sigma)
+                         tau, sigma, None if pb.g_q is None else clean(pb.g_q))

@@ -32,9 +32,11 @@ SYMBOLS = (
     "purin_cp_solve",
     "purin_cp_project",
     "purin_cp_project_values",
+    "purin_cp_qp_solve",
     "purin_cp_default_adjoint_options",
     "purin_cp_adjoint",
     "purin_cp_adjoint_values",
+    "purin_cp_qp_adjoint",
     "purin_cp_last_error",
     "purin_cp_build_info",
 )
@@ -49,6 +51,8 @@ class Options(C.Structure):
         ("norm_seed", C.c_int32),
         ("diagonal_preconditioning", C.c_int32),
         ("safety", C.c_double),
+        ("bound_presolve", C.c_int32),
+        ("reserved", C.c_int32),
     ]
 
 
@@ -155,6 +159,10 @@ def load(path: str = LIB_PATH):
     lib.purin_cp_project_values.argtypes = [vp, vp, i64, vp, vp, vp, vp, C.POINTER(SolveOptions),
                                             vp, vp, vp, i32p, i32p, vp, u8p, u8p, vp]
     lib.purin_cp_project_values.restype = C.c_int
+    lib.purin_cp_qp_solve.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp, vp, vp,
+                                      C.POINTER(SolveOptions), vp, vp, vp, i32p, i32p, vp, u8p,
+                                      u8p, vp]
+    lib.purin_cp_qp_solve.restype = C.c_int
     lib.purin_cp_last_timing.argtypes = [vp, C.POINTER(Timing)]
     lib.purin_cp_last_timing.restype = C.c_int
     lib.purin_cp_last_adjoint_stats.argtypes = [vp, C.POINTER(AdjointStats)]
@@ -167,6 +175,10 @@ def load(path: str = LIB_PATH):
     lib.purin_cp_adjoint_values.argtypes = [vp, vp, i64, vp, vp, vp, C.POINTER(AdjointOptions),
                                             vp, vp, vp, u8p, i32p, vp]
     lib.purin_cp_adjoint_values.restype = C.c_int
+    lib.purin_cp_qp_adjoint.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp,
+                                        C.POINTER(AdjointOptions), vp, vp, vp, vp, vp, vp, u8p,
+                                        i32p, vp]
+    lib.purin_cp_qp_adjoint.restype = C.c_int
     lib.purin_cp_last_error.argtypes = []
     lib.purin_cp_last_error.restype = C.c_char_p
     lib.purin_cp_build_info.argtypes = []

@@ -26,6 +26,7 @@
 #include "forward.hpp"
 #include "kernels.hpp"
 #include "plan.hpp"
+#include "persample.hpp"
 
 namespace purin {
 
@@ -55,6 +56,14 @@ struct Adj {
   const T* d_cb;
   const T* sig_rb;
   int dg;        // 1: U and Wv hold delta . u and sigma . w (any non-scalar step)
+  // general diagonal QP (diagonal_qp.py:131-219): q, c [n][Bp]; the prox
+  // a = 1/(1 + tau q), delta = tau a is formed from tau per sample (tau_b) or
+  // per variable (tau_cb); Spre keeps the pre-clip value for the q gradient
+  const T* Q;
+  const T* Cc;
+  const T* tau_b;
+  const T* tau_cb;
+  T* Spre;
   const T* Cm;   // n x Bp
   const T* Dm;   // m x Bp
   T* U;          // n x Bp scratch (u)
@@ -64,13 +73,19 @@ struct Adj {
 // Steps of column j / row i for sample b (shared, diagonal, per-sample or
 // per-sample diagonal).
 template <typename T>
+__device__ __forceinline__ T adj_tau(const Adj<T>& S, int64_t j, int64_t b) {
+  return S.tau_cb ? S.tau_cb[j * S.Bp + b] : S.tau_b[b];
+}
+template <typename T>
 __device__ __forceinline__ T adj_a(const Adj<T>& S, int64_t j, int64_t b) {
+  if (S.Q) return T(1) / (T(1) + adj_tau(S, j, b) * S.Q[j * S.Bp + b]);
   if (S.a_cb) return S.a_cb[j * S.Bp + b];
   if (S.a_b) return S.a_b[b];
   return S.a_c ? S.a_c[j] : S.a;
 }
 template <typename T>
 __device__ __forceinline__ T adj_d(const Adj<T>& S, int64_t j, int64_t b) {
+  if (S.Q) return adj_tau(S, j, b) * adj_a(S, j, b);
   if (S.d_cb) return S.d_cb[j * S.Bp + b];
   if (S.d_b) return S.d_b[b];
   return S.d_c ? S.d_c[j] : S.delta;
@@ -159,7 +174,15 @@ __global__ __launch_bounds__(kBlock) void k_lin_cols(Adj<T> S, const T* __restri
       aj[q] = adj_a(S, j, b0 + q);
       dj[q] = adj_d(S, j, b0 + q);
     }
-    const V s = aj * y - dj * t + dj * vload(tgt + off);
+    V s;
+    if (S.Q) {  // offset -delta c (kernels.py:68-73)
+      const V cv = vload(S.Cc + off);
+#pragma unroll
+      for (int q = 0; q < Sn; ++q) s[q] = aj[q] * y[q] - dj[q] * t[q] + (-dj[q] * cv[q]);
+      vstore(S.Spre + off, s);
+    } else {
+      s = aj * y - dj * t + dj * vload(tgt + off);
+    }
     V lo, hi;
     if (shared_bounds) {
       lo = vsplat<T>(LO[j]);
@@ -800,24 +823,34 @@ __global__ void k_gm_finish(Gm<T> G, const T* __restrict__ xfin, const int32_t* 
 }
 
 // rhs g = [cot_y * eligible, 0, 0]; cot arrives batch-minor in ``cot``
+// With cotd (the general QP's dual cotangent, diagonal_qp.py:197-200), the
+// rows n..n+m of g are cotd * eligible.
 template <typename T>
-__global__ void k_gm_rhs(int64_t n, int64_t W, int64_t Bp, int64_t batch, const T* __restrict__ cot,
+__global__ void k_gm_rhs(int64_t n, int64_t m, int64_t W, int64_t Bp, int64_t batch,
+                         const T* __restrict__ cot, const T* __restrict__ cotd,
                          const int32_t* __restrict__ conv, int force, T* g) {
   const int64_t total = W * Bp;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = e / Bp, b = e - row * Bp;
     const bool elig = b < batch && (force || conv[b] != 0);
-    g[e] = (row < n && elig) ? cot[e] : T(0);
+    T v = T(0);
+    if (row < n)
+      v = cot[e];
+    else if (cotd && row < n + m)
+      v = cotd[e - n * Bp];
+    g[e] = elig ? v : T(0);
   }
 }
 
 // Final pullback of lambda (masked by lam_w): outputs in internal layout, with
 // non-finite values replaced by zero (bounds.py:154-165).
+// General QP: gt receives g_c = -delta u and gq g_q = -tau a u s, with s the
+// pre-clip value (d s / d q = -tau a s for a = 1/(1 + tau q), delta = tau a).
 template <typename T>
 __global__ void k_final_u(Adj<T> S, const T* __restrict__ lam, const T* __restrict__ lam_w,
                           const T* __restrict__ Clo, const T* __restrict__ Chi, T* gt, T* glo,
-                          T* ghi) {
+                          T* ghi, T* gq) {
   const int64_t total = (int64_t)S.n * S.Bp;
   const int64_t boff = (int64_t)(S.n + S.m) * S.Bp;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
@@ -829,7 +862,14 @@ __global__ void k_final_u(Adj<T> S, const T* __restrict__ lam, const T* __restri
     const T u = S.Cm[e] * G;
     const T a = adj_d(S, e / S.Bp, b) * u, l = Clo[e] * G, h = Chi[e] * G;
     S.U[e] = S.dg ? a : u;
-    gt[e] = finite(a) ? a : T(0);
+    if (S.Q) {
+      const int64_t j = e / S.Bp;
+      const T g = -(adj_tau(S, j, b) * adj_a(S, j, b) * u * S.Spre[e]);
+      gq[e] = finite(g) ? g : T(0);
+      gt[e] = finite(a) ? -a : T(0);
+    } else {
+      gt[e] = finite(a) ? a : T(0);
+    }
     glo[e] = finite(l) ? l : T(0);
     ghi[e] = finite(h) ? h : T(0);
   }
@@ -981,14 +1021,25 @@ __global__ void k_copy_i32(int64_t count, const int32_t* __restrict__ src, int32
 
 static size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Inputs and extra outputs of the general diagonal QP's VJP (diagonal_qp.py:131-219).
+template <typename T>
+struct QPAdjArgs {
+  const T* q;         // (B, n)
+  const T* c;         // (B, n)
+  const T* cot_dual;  // (B, M) cotangent of the multipliers, or nullptr
+  T* g_q;             // (B, n) or nullptr
+};
+
 template <typename T>
 static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const void* saved,
                         const T* cot_y, const purin_cp_adjoint_options& o, T* g_target, T* g_rhs,
                         T* g_lower, T* g_upper, uint8_t* valid, int32_t* info, T* gres,
                         const T* values = nullptr, T* g_values = nullptr,
-                        bool per_sample = false) {
+                        bool per_sample = false, const QPAdjArgs<T>* qa = nullptr) {
   if (!saved || !cot_y) return set_error(PURIN_CP_ERR_ARG, "NULL saved state or cotangent");
-  if (per_sample && p->nnz_full && !values) return set_error(PURIN_CP_ERR_ARG, "NULL values");
+  if (per_sample && !qa && p->nnz_full && !values)
+    return set_error(PURIN_CP_ERR_ARG, "NULL values");
+  if (qa && (!qa->q || !qa->c)) return set_error(PURIN_CP_ERR_ARG, "NULL q or c");
   if (batch < 1) return set_error(PURIN_CP_ERR_ARG, "batch must be positive");
   if (o.restart < 1 || o.max_iterations < 1)
     return set_error(PURIN_CP_ERR_ARG, "linear iteration limits must be positive");
@@ -1008,7 +1059,11 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     return set_error(PURIN_CP_ERR_ARG, "saved state does not belong to this plan and batch");
   const int kind = (int)hdr[3];
   const int shared = (int)hdr[4];
-  if (per_sample != (kind == 2))
+  if (qa ? kind != 3 : kind == 3)
+    return set_error(PURIN_CP_ERR_ARG, qa ? "saved state is not from purin_cp_qp_solve"
+                                          : "saved state is from purin_cp_qp_solve: use "
+                                            "purin_cp_qp_adjoint");
+  if (!qa && per_sample != (kind == 2))
     return set_error(PURIN_CP_ERR_ARG, per_sample
                                            ? "saved state is not from purin_cp_project_values"
                                            : "saved state is from purin_cp_project_values: use "
@@ -1022,7 +1077,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   const T* HI = (const T*)(sv + L.HI);
   const T* RF = (const T*)(sv + L.RF);
   const int32_t* conv = (const int32_t*)(sv + L.conv);
-  const T* metric = kind >= 1 ? (const T*)p->metric : nullptr;
+  const T* metric = (kind == 1 || kind == 2) ? (const T*)p->metric : nullptr;
 
   // workspace
   const int nchunk = (int)((W + kChunk - 1) / kChunk);
@@ -1064,6 +1119,10 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   const size_t oPS = per_sample ? take(Lv.ws_end) : 0;
   const size_t oSw = per_sample ? take(m * Bp * es) : 0;
   const size_t oGV = per_sample ? take((size_t)p->nnz_full * Bp * es) : 0;
+  const size_t oSp = qa ? take(n * Bp * es) : 0;    // pre-clip values (q gradient)
+  const size_t oGq = qa ? take(n * Bp * es) : 0;    // g_q
+  const size_t oCd = (qa && qa->cot_dual) ? take((size_t)std::max<int64_t>(M, 1) * Bp * es) : 0;
+  const size_t oCds = (qa && qa->cot_dual) ? take((size_t)std::max<int64_t>(m, 1) * Bp * es) : 0;
   int err = PURIN_CP_OK;
   char* ws = (char*)workspace(p, o_, st, &err, true);
   if (!ws) return err;
@@ -1093,11 +1152,42 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   S.a = T(1) / (T(1) + tau);
   S.delta = tau * S.a;
   PerSample<T> PS{};
-  if (per_sample) {
+  if (qa) {
+    // the QP's q, c and per-sample steps: diagonal steps, or tau = s/(max q + L),
+    // sigma = s/L with L from the norm bound or the power iteration
+    // (diagonal_qp.py:137-160)
+    char* wq = ws + oPS;
+    T* QQ = (T*)(wq + Lv.QQ);
+    T* QC = (T*)(wq + Lv.QC);
+    T* qmax = (T*)(wq + Lv.QS);
+    to_minor<T>(st, qa->q, batch, n, n, QQ, Bp, nullptr, 0);
+    to_minor<T>(st, qa->c, batch, n, n, QC, Bp, nullptr, 0);
+    k_qp_stats<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(n, Bp, batch, QQ, LO, HI, qmax,
+                                                              qmax + Bp, nullptr);
+    if (int rc = prepare_values<T>(p, st, batch, Lv, wq, values, T(1), kQPAdjoint, qmax,
+                                   qmax + Bp, &PS))
+      return rc;
+    S.K.rvb = PS.RV;
+    S.K.cvb = PS.CV;
+    S.K.vbp = Bp;
+    S.Q = QQ;
+    S.Cc = QC;
+    S.Spre = (T*)(ws + oSp);
+    if (p->diag) {
+      S.tau_cb = PS.tau_cb;
+      S.sig_rb = PS.sig_rb;
+    } else {
+      S.tau_b = PS.tau_b;
+      S.sig_b = PS.sig_b;
+    }
+    S.dg = 1;
+  } else if (per_sample) {
     // per-sample scaled entries and the adjoint's per-sample steps: the
     // power-iteration L of each sample's matrix (bounds.py:88-101) or its
     // diagonal steps (bounds.py:83-86)
-    if (int rc = prepare_values<T>(p, st, batch, Lv, ws + oPS, values, T(1), true, &PS)) return rc;
+    if (int rc = prepare_values<T>(p, st, batch, Lv, ws + oPS, values, T(1), kProjectAdjoint,
+                                   nullptr, nullptr, &PS))
+      return rc;
     S.K.rvb = PS.RV;
     S.K.cvb = PS.CV;
     S.K.vbp = Bp;
@@ -1219,7 +1309,17 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
 
   // rhs g = [cot * eligible, 0, 0] (cotangent divided by sqrt(D) for a metric)
   to_minor<T>(st, cot_y, batch, n, n, T1, Bp, metric, metric ? 2 : 0);
-  k_gm_rhs<T><<<eb, 256, 0, st>>>(n, W, Bp, batch, T1, conv, o.force_eligible, Gr);
+  // the QP's dual cotangent w.r.t. the scaled dual: cot_dual * scale (the
+  // returned multipliers are dual * scale, diagonal_qp.py:274)
+  T* cotd = nullptr;
+  if (qa && qa->cot_dual && m) {
+    T* CD = (T*)(ws + oCd);
+    cotd = (T*)(ws + oCds);
+    to_minor<T>(st, qa->cot_dual, batch, M, M, CD, Bp, nullptr, 0);
+    k_prep_rows<T><<<2048, 256, 0, st>>>((int)m, Bp, p->dkept, (const T*)p->dscale, PS.SC, CD,
+                                         nullptr, cotd, nullptr);
+  }
+  k_gm_rhs<T><<<eb, 256, 0, st>>>(n, m, W, Bp, batch, T1, cotd, conv, o.force_eligible, Gr);
   // threshold = max(atol, tol * max|g|) and residual_inf = max|g - A 0| = max|g|
   k_gs<T, 4><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Gr, nullptr, W, Bp, part, nchunk);
   reduce(1, S1, 1);
@@ -1312,8 +1412,10 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   T* glo = (T*)(ws + oGlo);
   T* ghi = (T*)(ws + oGhi);
   T* gr = (T*)(ws + oGr);
+  T* gq = qa ? (T*)(ws + oGq) : nullptr;
   k_final_u<T><<<eb, 256, 0, st>>>(S, X, lam_w, (const T*)(ws + oClo), (const T*)(ws + oChi), gt,
-                                   glo, ghi);
+                                   glo, ghi, gq);
+  if (qa && qa->g_q) to_major<T>(st, gq, Bp, n, qa->g_q, batch, n, nullptr, 0);
   T* sw = per_sample ? (T*)(ws + oSw) : nullptr;
   if (m) k_final_w<T><<<grow, kBlock, 0, st>>>(S, X, lam_w, gr, sw);
   if (g_target) to_major<T>(st, gt, Bp, n, g_target, batch, n, metric, metric ? 1 : 0);
@@ -1322,8 +1424,8 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     T* GV = (per_sample && g_values && p->nnz_full) ? (T*)(ws + oGV) : nullptr;
     if (GV && m)
       k_gvals_rows<T><<<grow, kBlock, 0, st>>>(S.K, Bp, sw, Y, S.U, (const T*)(ws + oDp), gr,
-                                              PS.RVo, PS.SC, RF, p->dkept, p->opts.row_scaling,
-                                              p->ps_kcsr, GV);
+                                              PS.RVo, PS.SC, RF, p->dkept,
+                                              qa ? 0 : p->opts.row_scaling, p->ps_kcsr, GV);
     if (GF || (GV && !p->bound.empty()))
       k_grhs_full<T><<<eb, 256, 0, st>>>((int)m, (int)n, Bp, p->dkept, (const T*)p->dscale,
                                          per_sample ? PS.SC : nullptr, gr, p->bptr, p->brow,
@@ -1343,6 +1445,33 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
 }  // namespace purin
 
 using namespace purin;
+
+extern "C" int purin_cp_qp_adjoint(purin_cp_plan* p, void* stream, int64_t batch,
+                                   const void* saved, const void* q, const void* c,
+                                   const void* values, const void* cot_y, const void* cot_dual,
+                                   const purin_cp_adjoint_options* opts, void* g_q, void* g_c,
+                                   void* g_values, void* g_rhs, void* g_lower, void* g_upper,
+                                   uint8_t* valid, int32_t* info, void* gmres_residual) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  purin_cp_adjoint_options o;
+  purin_cp_default_adjoint_options(&o);
+  if (opts) o = *opts;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64) {
+    const QPAdjArgs<double> qa{(const double*)q, (const double*)c, (const double*)cot_dual,
+                               (double*)g_q};
+    return adjoint_impl<double>(p, st, batch, saved, (const double*)cot_y, o, (double*)g_c,
+                                (double*)g_rhs, (double*)g_lower, (double*)g_upper, valid, info,
+                                (double*)gmres_residual, (const double*)values,
+                                (double*)g_values, true, &qa);
+  }
+  const QPAdjArgs<float> qa{(const float*)q, (const float*)c, (const float*)cot_dual,
+                            (float*)g_q};
+  return adjoint_impl<float>(p, st, batch, saved, (const float*)cot_y, o, (float*)g_c,
+                             (float*)g_rhs, (float*)g_lower, (float*)g_upper, valid, info,
+                             (float*)gmres_residual, (const float*)values, (float*)g_values, true,
+                             &qa);
+}
 
 extern "C" int purin_cp_adjoint_values(purin_cp_plan* p, void* stream, int64_t batch,
                                        const void* saved, const void* values, const void* cot_y,

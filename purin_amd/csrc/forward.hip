@@ -89,6 +89,9 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values) {
     L.PZ = take(std::max<size_t>(m, 1) * Bp * es);
     L.PW = take(n * Bp * es);
     L.PD = take((size_t)2 * Bp * es);
+    L.QQ = take(n * Bp * es);
+    L.QC = take(n * Bp * es);
+    L.QS = take((size_t)2 * Bp * es);
   }
   L.ws_end = o;
   return L;
@@ -124,7 +127,10 @@ static void ps_power(const purin_cp_plan* p, hipStream_t st, const Layout& L, ch
 
 template <typename T>
 int prepare_values(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout& L, char* ws,
-                   const T* values, T tol, bool adjoint, PerSample<T>* ps) {
+                   const T* values, T tol, int mode, const T* qmax, const T* qmin,
+                   PerSample<T>* ps) {
+  const bool adjoint = mode == kProjectAdjoint || mode == kQPAdjoint;
+  const bool qp = mode == kQPForward || mode == kQPAdjoint;
   const int64_t Bp = L.Bp, n = p->n, m = p->m, nnz = p->nnz;
   const int64_t nb = (int64_t)p->bound.size();
   constexpr int64_t TS = tile_samples<T>();
@@ -139,7 +145,13 @@ int prepare_values(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   T* rpart = (T*)(ws + L.RPT);
   T* cpart = (T*)(ws + L.CPT);
   // padded samples (b >= batch) get zero coefficients (to_minor pads with 0)
-  to_minor<T>(st, values, batch, p->nnz_full, p->nnz_full, VF, Bp, nullptr, 0);
+  if (values) {
+    to_minor<T>(st, values, batch, p->nnz_full, p->nnz_full, VF, Bp, nullptr, 0);
+  } else {
+    if (p->nnz != p->nnz_full)
+      return set_error(PURIN_CP_ERR_ARG, "shared values need a plan that keeps every row");
+    k_bcast_entries<T><<<2048, 256, 0, st>>>((const T*)p->rval_o, p->nnz_full, Bp, batch, VF);
+  }
   if (nnz) {
     k_gather_entries<T><<<2048, 256, 0, st>>>(VF, Bp, p->ps_kcsr, nnz, RVo);
     k_gather_entries<T><<<2048, 256, 0, st>>>(VF, Bp, p->ps_kcsc, nnz, CVo);
@@ -154,8 +166,9 @@ int prepare_values(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   ps->BC = BC;
   ps->SC = SC;
   ps->sig_rb = diag ? (T*)(ws + L.SGR) : nullptr;
-  ps->a_cb = diag ? (T*)(ws + L.ACB) : nullptr;
-  ps->d_cb = diag ? (T*)(ws + L.DCB) : nullptr;
+  ps->a_cb = (diag && !qp) ? (T*)(ws + L.ACB) : nullptr;
+  ps->d_cb = (diag && !qp) ? (T*)(ws + L.DCB) : nullptr;
+  ps->tau_cb = (diag && qp) ? (T*)(ws + L.ACB) : nullptr;
   ps->tau_b = stb;
   ps->sig_b = stb + Bp;
   ps->a_b = stb + 2 * Bp;
@@ -167,10 +180,11 @@ int prepare_values(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     k_ps_rows<T><<<tile_grid(Bp, TS, L.nrb), kBlock, 0, st>>>(
         (int)m, Bp, p->rptr, RVo, p->opts.row_scaling, safety, SC, RV, ps->sig_rb, rpart, L.nrb);
   k_ps_cols<T><<<tile_grid(Bp, TS, L.ncb), kBlock, 0, st>>>(
-      (int)n, Bp, p->cptr, p->cidx, CVo, SC, safety, CV, ps->a_cb, ps->d_cb, cpart, L.ncb);
-  // the power iteration sets L for the adjoint (bounds.py:88-101) and for the
-  // forward without the norm bound (kernels.py:211-212)
-  const bool power = !diag && (adjoint || !p->opts.norm_bound);
+      (int)n, Bp, p->cptr, p->cidx, CVo, SC, safety, CV, ps->a_cb, ps->d_cb, ps->tau_cb, cpart,
+      L.ncb);
+  // the power iteration sets L for the projection's adjoint (bounds.py:88-101)
+  // and wherever the norm bound is off (kernels.py:211-212, diagonal_qp.py:148-157)
+  const bool power = !diag && (mode == kProjectAdjoint || !p->opts.norm_bound);
   if (power) {
     Mat<T> K = kept_matrix<T>(p, true);
     K.rvb = RV;
@@ -180,15 +194,17 @@ int prepare_values(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   }
   k_ps_steps<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(
       Bp, rpart, (int)(m ? L.nrb : 0), cpart, L.ncb, power ? Lpi : nullptr, safety,
-      adjoint ? 0 : p->opts.accelerated, tol, ps->tau_b, ps->sig_b, ps->a_b, ps->d_b, ps->th_b,
-      ps->tol_b);
+      adjoint ? 0 : p->opts.accelerated, tol, qp ? qmax : nullptr, qp ? qmin : nullptr, ps->tau_b,
+      ps->sig_b, ps->a_b, ps->d_b, ps->th_b, ps->tol_b);
   PURIN_HIP(hipGetLastError());
   return PURIN_CP_OK;
 }
 template int prepare_values<double>(purin_cp_plan*, hipStream_t, int64_t, const Layout&, char*,
-                                    const double*, double, bool, PerSample<double>*);
+                                    const double*, double, int, const double*, const double*,
+                                    PerSample<double>*);
 template int prepare_values<float>(purin_cp_plan*, hipStream_t, int64_t, const Layout&, char*,
-                                   const float*, float, bool, PerSample<float>*);
+                                   const float*, float, int, const float*, const float*,
+                                   PerSample<float>*);
 
 template <typename T>
 constexpr int res_tile() {
@@ -341,7 +357,7 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
 template <typename T>
 int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout& L, char* sv,
                    char* ws, const purin_cp_solve_options& o, T tol_scalar, const T* tolv,
-                   const PerSample<T>* ps = nullptr) {
+                   const PerSample<T>* ps = nullptr, const QPRun<T>* qp = nullptr) {
   const int64_t Bp = L.Bp;
   constexpr int64_t TS = tile_samples<T>();
   Iter<T> A{};
@@ -367,13 +383,20 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
       A.sig_rb = ps->sig_rb;
       A.a_cb = ps->a_cb;
       A.d_cb = ps->d_cb;
+      A.tau_cb = ps->tau_cb;
     } else {
       A.sig_b = ps->sig_b;
       A.a_b = ps->a_b;
       A.d_b = ps->d_b;
+      A.tau_b = ps->tau_b;
       if (p->opts.accelerated) A.th_b = ps->th_b;
     }
     tolv = ps->tol_b;
+    if (qp) {  // general q, c: the column pass forms the prox from tau and q
+      A.Q = qp->Q;
+      A.Cc = qp->Cc;
+      A.tgt = nullptr;
+    }
   } else if (p->diag) {  // diagonal steps (non-accelerated, so constant over the loop)
     A.sig_r = (const T*)p->diag_sig;
     A.a_c = (const T*)p->diag_a;
@@ -386,7 +409,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   const bool early = o.early_stop != 0;
   const size_t lds = resident_lds<T>(p);
   // the resident kernel takes one schedule of scalar steps for the whole tile
-  if (!early && lds && !o.streaming && !p->diag && !ps) {
+  if (!early && lds && !o.streaming && !p->diag && !ps && !qp) {
     if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds)) return rc;
     const int32_t cnt = (int32_t)o.max_iterations;
     k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);
@@ -403,9 +426,13 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     PURIN_HIP(hipGetLastError());
     return PURIN_CP_OK;
   }
-  // y0 = ybar0 = target (kernels.py:229-231, bounds.py:59)
-  PURIN_HIP(hipMemcpyAsync(A.Y, A.tgt, (size_t)n * Bp * sizeof(T), hipMemcpyDeviceToDevice, st));
-  PURIN_HIP(hipMemcpyAsync(A.YB, A.tgt, (size_t)n * Bp * sizeof(T), hipMemcpyDeviceToDevice, st));
+  if (qp) {  // y0 is in Y already (the caller's or zero); ybar0 = y0 (kernels.py:229-231)
+    PURIN_HIP(hipMemcpyAsync(A.YB, A.Y, (size_t)n * Bp * sizeof(T), hipMemcpyDeviceToDevice, st));
+  } else {  // y0 = ybar0 = target (kernels.py:229-231, bounds.py:59)
+    PURIN_HIP(hipMemcpyAsync(A.Y, A.tgt, (size_t)n * Bp * sizeof(T), hipMemcpyDeviceToDevice, st));
+    PURIN_HIP(hipMemcpyAsync(A.YB, A.tgt, (size_t)n * Bp * sizeof(T), hipMemcpyDeviceToDevice, st));
+  }
+  const T* qgam = qp ? qp->gamma : nullptr;
 
   const int check = o.check_every > 0 ? o.check_every : 32;
   const T one = T(1);
@@ -451,7 +478,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     }
     if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 2], st));
     if (p->opts.accelerated && A.th_b) {  // the same update, per sample
-      k_ps_sched<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(Bp, ps->tau_b, ps->sig_b,
+      k_ps_sched<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(Bp, qgam, ps->tau_b, ps->sig_b,
                                                                   ps->a_b, ps->d_b, ps->th_b);
     } else if (p->opts.accelerated) {  // kernels.py:279-283 with gamma = min q = 1
       const T nt = one / std::sqrt(one + tau);
@@ -651,7 +678,8 @@ static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T
   // tol * min(1, min_i scale_i) for every sample (bounds.py:192-236)
   PerSample<T> PS{};
   if (per_sample &&
-      (rc = prepare_values<T>(p, st, batch, L, ws, values, (T)tol_cfg, false, &PS)))
+      (rc = prepare_values<T>(p, st, batch, L, ws, values, (T)tol_cfg, kProjectForward, nullptr,
+                              nullptr, &PS)))
     return rc;
   const PerSample<T>* ps = per_sample ? &PS : nullptr;
   if (m)
@@ -713,11 +741,141 @@ static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T
   return PURIN_CP_OK;
 }
 
+// General positive diagonal QP (PreparedDiagonalQP.solve, diagonal_qp.py:222-319):
+// min 0.5 y'Qy + c'y over the plan's rows (every row kept) and bounds
+// lower <= y <= upper, per-sample q, c, values, rhs and bounds.
+template <typename T>
+static int qp_solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T* q, const T* c,
+                         const T* values, const T* rhs, const T* lower, const T* upper,
+                         const T* y0, const T* dual0, const purin_cp_solve_options& o, T* y,
+                         T* mult, T* slacks, int32_t* status, int32_t* iterations, T* residual,
+                         uint8_t* finite_out, uint8_t* converged_out, void* saved) {
+  int rc = check_layout_args<T>(p, batch);
+  if (rc) return rc;
+  if (!q || !c || !lower || !upper || (p->M && !rhs))
+    return set_error(PURIN_CP_ERR_ARG, "NULL input array");
+  if (p->opts.bound_presolve)
+    return set_error(PURIN_CP_ERR_ARG,
+                     "the diagonal-QP entry needs a plan created with bound_presolve = 0");
+  if (p->metric)
+    return set_error(PURIN_CP_ERR_ARG, "QPData.q already defines the quadratic metric");
+  if (o.max_iterations < 1) return set_error(PURIN_CP_ERR_ARG, "max_iterations must be a positive integer");
+  if (!(o.tolerance > 0.0) || !std::isfinite(o.tolerance))
+    return set_error(PURIN_CP_ERR_ARG, "tolerance must be positive and finite");
+  if (o.shared_bounds) return set_error(PURIN_CP_ERR_ARG, "the diagonal QP takes per-sample bounds");
+  Layout L;
+  char *sv, *ws;
+  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, true))) return rc;
+  const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
+  constexpr int64_t TS = tile_samples<T>();
+  write_header<T>(st, sv, batch, Bp, 3, 0, p);
+  T* QQ = (T*)(ws + L.QQ);
+  T* QC = (T*)(ws + L.QC);
+  T* qmax = (T*)(ws + L.QS);
+  T* qmin = qmax + Bp;
+  T* RF = (T*)(sv + L.RF);
+  to_minor<T>(st, q, batch, n, n, QQ, Bp, nullptr, 0);
+  to_minor<T>(st, c, batch, n, n, QC, Bp, nullptr, 0);
+  to_minor<T>(st, lower, batch, n, n, (T*)(sv + L.LO), Bp, nullptr, 0);
+  to_minor<T>(st, upper, batch, n, n, (T*)(sv + L.HI), Bp, nullptr, 0);
+  to_minor<T>(st, rhs, batch, M, M, RF, Bp, nullptr, 0);
+  if (y0)
+    to_minor<T>(st, y0, batch, n, n, (T*)(sv + L.Y), Bp, nullptr, 0);
+  else
+    k_fill<T><<<1024, 256, 0, st>>>((T*)(sv + L.Y), n * Bp, T(0));
+  T* MF = nullptr;
+  if (dual0) {
+    MF = (T*)(ws + L.MF);
+    to_minor<T>(st, dual0, batch, M, M, MF, Bp, nullptr, 0);
+  }
+  k_init_flags<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(
+      batch, Bp, (int32_t*)(ws + L.done), (int32_t*)(ws + L.count), (int32_t*)(sv + L.feas),
+      nullptr, (int32_t*)(ws + L.ndone));
+  // valid = all(q > 0) & all(lower <= upper) ANDs into convergence (diagonal_qp.py:120-123)
+  k_qp_stats<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(
+      n, Bp, batch, QQ, (const T*)(sv + L.LO), (const T*)(sv + L.HI), qmax, qmin,
+      (int32_t*)(sv + L.feas));
+  PerSample<T> PS{};
+  if ((rc = prepare_values<T>(p, st, batch, L, ws, values, (T)o.tolerance, kQPForward, qmax, qmin,
+                              &PS)))
+    return rc;
+  // scaled rhs and initial dual / scale (diagonal_qp.py:257-273)
+  if (m)
+    k_prep_rows<T><<<2048, 256, 0, st>>>((int)m, Bp, p->dkept, (const T*)p->dscale, PS.SC, RF, MF,
+                                         (T*)(sv + L.R), (T*)(sv + L.D));
+  const QPRun<T> qr{QQ, QC, qmin};
+  if ((rc = run_iterations<T>(p, st, batch, L, sv, ws, o, (T)o.tolerance, nullptr, &PS, &qr)))
+    return rc;
+  // original-unit residual, status and slacks (diagonal_qp.py:276-319)
+  Post<T> P{};
+  P.K = kept_matrix<T>(p, false);
+  P.K.rvb = PS.RVo;
+  P.K.cvb = PS.CVo;
+  P.K.vbp = Bp;
+  P.scale_b = PS.SC;
+  P.Q = QQ;
+  P.Cc = QC;
+  P.Bp = Bp;
+  P.me = p->me;
+  P.mi = p->mi;
+  P.scale = (const T*)p->dscale;
+  P.kept = p->dkept;
+  P.bptr = p->bptr;
+  P.brow = p->brow;
+  P.bcoef = (const T*)p->dbcoef;
+  P.Y = (const T*)(sv + L.Y);
+  P.D = (const T*)(sv + L.D);
+  P.RF = RF;
+  P.LO = (const T*)(sv + L.LO);
+  P.HI = (const T*)(sv + L.HI);
+  P.DF = (T*)(ws + L.DF);
+  P.SL = (T*)(ws + L.SL);
+  P.rowpart = (T*)(ws + L.rowpart);
+  P.colpart = (T*)(ws + L.colpart);
+  P.nrb = L.nrb;
+  P.ncb = L.ncb;
+  if (m)
+    k_post_rows<T, kRowsPerWaveEarly><<<tile_grid(Bp, TS, L.nrb), kBlock, 0, st>>>(P);
+  k_post_cols<T, kRowsPerWaveEarly><<<tile_grid(Bp, TS, L.ncb), kBlock, 0, st>>>(P);
+  k_post_final<T><<<(unsigned)((batch + 255) / 256), 256, 0, st>>>(
+      P, batch, (T)o.tolerance, T(1), (const int32_t*)(sv + L.conv), (const T*)(ws + L.ogap),
+      (const int32_t*)(ws + L.count), status, iterations, residual, finite_out, converged_out);
+  if (y) to_major<T>(st, (const T*)(sv + L.Y), Bp, n, y, batch, n, nullptr, 0);
+  if (mult) to_major<T>(st, (const T*)(ws + L.DF), Bp, M, mult, batch, M, nullptr, 0);
+  if (slacks) to_major<T>(st, (const T*)(ws + L.SL), Bp, p->mi, slacks, batch, p->mi, nullptr, 0);
+  PURIN_HIP(hipGetLastError());
+  return PURIN_CP_OK;
+}
+
 }  // namespace purin
 
 using namespace purin;
 
 extern "C" {
+
+int purin_cp_qp_solve(purin_cp_plan* p, void* stream, int64_t batch, const void* q, const void* c,
+                      const void* values, const void* rhs, const void* lower, const void* upper,
+                      const void* y0, const void* dual0, const purin_cp_solve_options* opts,
+                      void* y, void* mult, void* slacks, int32_t* status, int32_t* iterations,
+                      void* residual, uint8_t* finite_out, uint8_t* converged, void* saved) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  purin_cp_solve_options o;
+  purin_cp_default_solve_options(&o);
+  if (opts) o = *opts;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64)
+    return qp_solve_impl<double>(p, st, batch, (const double*)q, (const double*)c,
+                                 (const double*)values, (const double*)rhs, (const double*)lower,
+                                 (const double*)upper, (const double*)y0, (const double*)dual0, o,
+                                 (double*)y, (double*)mult, (double*)slacks, status, iterations,
+                                 (double*)residual, finite_out, converged, saved);
+  return qp_solve_impl<float>(p, st, batch, (const float*)q, (const float*)c, (const float*)values,
+                              (const float*)rhs, (const float*)lower, (const float*)upper,
+                              (const float*)y0, (const float*)dual0, o, (float*)y, (float*)mult,
+                              (float*)slacks, status, iterations, (float*)residual, finite_out,
+                              converged, saved);
+}
+
 
 int64_t purin_cp_saved_bytes(const purin_cp_plan* p, int64_t batch) {
   if (!p || batch < 1) return -1;

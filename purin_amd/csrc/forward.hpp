@@ -20,6 +20,7 @@ struct Layout {
   // caller's order (VF), the kept CSR / CSC entries original (RVo, CVo) and
   // row-scaled (RV, CV), bound-row coefficients (BC), row scales (SC), steps
   size_t VF, RVo, CVo, RV, CV, BC, SC, SGR, ACB, DCB, STB, RPT, CPT, PX, PZ, PW, PD;
+  size_t QQ, QC, QS;  // general QP: q, c (n x Bp) and per-sample max q, min q
   size_t ws_end;
 };
 
@@ -37,6 +38,7 @@ struct PerSample {
   T* sig_rb;      // [m][Bp] diagonal sigma, or nullptr
   T* a_cb;        // [n][Bp] diagonal prox a, or nullptr
   T* d_cb;        // [n][Bp] diagonal prox delta, or nullptr
+  T* tau_cb;      // [n][Bp] diagonal tau (general-q QP), or nullptr
   T* tau_b;       // [Bp] scalar steps (and schedule state) per sample
   T* sig_b;
   T* a_b;
@@ -45,12 +47,31 @@ struct PerSample {
   T* tol_b;       // [Bp] stop-test tolerance
 };
 
+// General diagonal QP objective (diagonal_qp.py): q, c [n][Bp] and the
+// per-sample gamma = min q of the accelerated schedule (kernels.py:228, 279).
+template <typename T>
+struct QPRun {
+  const T* Q;
+  const T* Cc;
+  const T* gamma;
+};
+
+// Which steps prepare_values computes.
+enum ValuesMode {
+  kProjectForward = 0,  // kernels.py:209-227 with q = 1 (norm bound or power iteration)
+  kProjectAdjoint = 1,  // bounds.py:83-101: power-iteration L, tau = s/(1 + L)
+  kQPForward = 2,       // kernels.py:209-227 with a general diagonal q
+  kQPAdjoint = 3,       // diagonal_qp.py:137-160: norm bound or power L, tau = s/(max q + L)
+};
+
 // Gather and prepare the per-sample arrays from values (batch-major (B, nnz_full)
-// in the plan's CSR entry order); ``adjoint`` selects the adjoint's steps
-// (power-iteration L with tau = s/(1+L), or the diagonal steps).  forward.hip.
+// in the plan's CSR entry order; nullptr: the plan's own values for every
+// sample, plans that keep every row only).  qmax / qmin: per-sample extremes
+// of a general q (QP modes).  forward.hip.
 template <typename T>
 int prepare_values(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout& L, char* ws,
-                   const T* values, T tol, bool adjoint, PerSample<T>* ps);
+                   const T* values, T tol, int mode, const T* qmax, const T* qmin,
+                   PerSample<T>* ps);
 
 inline dim3 tile_grid(int64_t Bp, int64_t tile, int64_t blocks) {
   return dim3((unsigned)(Bp / tile), (unsigned)std::max<int64_t>(1, std::min<int64_t>(blocks, 65535)));

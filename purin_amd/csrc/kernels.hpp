@@ -78,6 +78,14 @@ struct Iter {
   const T* __restrict__ sig_rb;
   const T* __restrict__ a_cb;
   const T* __restrict__ d_cb;
+  // general diagonal QP (diagonal_qp.py, kernels.py:68-73, 153-175): objective
+  // 0.5 q y^2 + c y with per-sample q, c [n][Bp] replacing q = 1, c = -yhat;
+  // the prox coefficients a = 1/(1 + tau q), delta = tau a and the offset
+  // -delta c are formed from tau per sample [Bp] or per variable [n][Bp]
+  const T* __restrict__ Q;
+  const T* __restrict__ Cc;
+  const T* __restrict__ tau_b;
+  const T* __restrict__ tau_cb;
   T* colpart;                 // [5][ncb][Bp]: primal, dual, stat, bound, finite
   T* rowpart;                 // [3][nrb][Bp]: residual max, r.d, finite
   int ncb, nrb;
@@ -179,7 +187,13 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
       }
       const size_t off = (size_t)j * A.Bp + b0;
       const V y = vload(A.Y + off);
-      const V tg = vload(A.tgt + off);
+      V tg, qv, cv;  // projection: yhat; general QP: q and c
+      if (A.Q) {
+        qv = vload(A.Q + off);
+        cv = vload(A.Cc + off);
+      } else {
+        tg = vload(A.tgt + off);
+      }
       V lo, hi;
       if (A.shared_bounds) {
         lo = vsplat<T>(A.LO[j]);
@@ -192,8 +206,20 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
       if (MODE == 2) {
         yn = y;
       } else {
-        const V aj = step_a(A, j, b0), dj = step_delta(A, j, b0);
-        const V sv = aj * y - dj * t + dj * tg;
+        V sv;
+        if (A.Q) {
+          const V tau = A.tau_cb ? vload(A.tau_cb + off) : vload(A.tau_b + b0);
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            const T aj = T(1) / (T(1) + tau[s] * qv[s]);
+            const T dj = tau[s] * aj;
+            const T oj = -dj * cv[s];
+            sv[s] = aj * y[s] - dj * t[s] + oj;
+          }
+        } else {
+          const V aj = step_a(A, j, b0), dj = step_delta(A, j, b0);
+          sv = aj * y - dj * t + dj * tg;
+        }
 #pragma unroll
         for (int s = 0; s < S; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
         V yb = yn + step_theta(A, b0) * (yn - y);
@@ -211,7 +237,21 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
         vstore(A.Y + off, yn);
         vstore(A.YB + off, yb);
       }
-      if (MODE != 0) {
+      if (MODE != 0 && A.Q) {
+        // diagnostics (kernels.py:158-174, 272-274) with general q, c
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const T yv = yn[s], q = qv[s], c = cv[s];
+          primal[s] += half * q * yv * yv + c * yv;
+          const T tf = c + t[s];
+          const T mz = q > T(1e-12) ? clipp(-tf / q, lo[s], hi[s]) : (tf >= zero ? lo[s] : hi[s]);
+          dualo[s] += half * q * (mz * mz) + tf * mz;
+          const T g = yv - clipp(yv - ((q * yv + c) + t[s]), lo[s], hi[s]);
+          stat[s] = maxp(stat[s], absv(g));
+          bnd[s] = maxp(bnd[s], maxp(maxp(lo[s] - yv, zero), maxp(yv - hi[s], zero)));
+          if (!finite(yv)) fin[s] = zero;
+        }
+      } else if (MODE != 0) {
         // diagnostics (kernels.py:158-174, 272-274) with q = 1, c = -yhat
 #pragma unroll
         for (int s = 0; s < S; ++s) {
@@ -451,7 +491,7 @@ __global__ void k_prep_rows(int m, int64_t Bp, const int32_t* __restrict__ kept,
     const int64_t src = (int64_t)kept[i] * Bp + b;
     const T sc = scale_b ? scale_b[e] : scale[i];  // per-sample scales: [m][Bp]
     R[e] = RF[src] * sc;
-    D[e] = MF ? MF[src] / sc : T(0);
+    if (D) D[e] = MF ? MF[src] / sc : T(0);
   }
 }
 

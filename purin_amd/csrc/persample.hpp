@@ -26,6 +26,18 @@ __global__ void k_gather_entries(const T* __restrict__ src, int64_t Bp,
   }
 }
 
+// dst[k * Bp + b] = src[k] for b < batch, 0 for the padding
+template <typename T>
+__global__ void k_bcast_entries(const T* __restrict__ src, int64_t K, int64_t Bp, int64_t batch,
+                                T* __restrict__ dst) {
+  const int64_t total = K * Bp;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t k = e / Bp, b = e - k * Bp;
+    dst[e] = b < batch ? src[k] : T(0);
+  }
+}
+
 // Per kept row (one row per wavefront, lanes over samples): the row norm and
 // scale (bounds.py:210-214; 1 without row scaling or for an empty row), the
 // scaled values RV = RVo * scale, the absolute row sum of RV (the norm bound,
@@ -107,7 +119,8 @@ __global__ __launch_bounds__(kBlock) void k_ps_cols(int n, int64_t Bp, const int
                                                     const int32_t* __restrict__ cidx,
                                                     const T* __restrict__ CVo, const T* __restrict__ SC,
                                                     T safety, T* __restrict__ CV, T* __restrict__ a_cb,
-                                                    T* __restrict__ d_cb, T* __restrict__ part, int ncb) {
+                                                    T* __restrict__ d_cb, T* __restrict__ tau_cb,
+                                                    T* __restrict__ part, int ncb) {
 #pragma clang fp contract(off)
   using V = typename Lane<T>::V;
   constexpr int S = Lane<T>::S;
@@ -127,17 +140,21 @@ __global__ __launch_bounds__(kBlock) void k_ps_cols(int n, int64_t Bp, const int
 #pragma unroll
         for (int s = 0; s < S; ++s) cs[s] += absv(v[s]);
       }
-      if (a_cb) {
-        V av, dv;
+      if (a_cb || tau_cb) {
+        V av, dv, tv;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           const T c2 = cs[s] > zero ? maxp(cs[s], T(1e-12)) : one;
           const T tau = safety / c2;
+          tv[s] = tau;
           av[s] = one / (one + tau);
           dv[s] = tau * av[s];
         }
-        vstore(a_cb + (size_t)j * Bp + b0, av);
-        vstore(d_cb + (size_t)j * Bp + b0, dv);
+        if (a_cb) {
+          vstore(a_cb + (size_t)j * Bp + b0, av);
+          vstore(d_cb + (size_t)j * Bp + b0, dv);
+        }
+        if (tau_cb) vstore(tau_cb + (size_t)j * Bp + b0, tv);
       }
 #pragma unroll
       for (int s = 0; s < S; ++s) cmax[s] = maxp(cmax[s], cs[s]);
@@ -148,15 +165,18 @@ __global__ __launch_bounds__(kBlock) void k_ps_cols(int n, int64_t Bp, const int
   }
 }
 
-// Per-sample steps (one thread per sample; kernels.py:209-227 with q = 1):
+// Per-sample steps (one thread per sample; kernels.py:209-227):
 // L = max(sqrt(max rowsum * max colsum), 1e-12) from the block partials (or
 // the power-iteration estimate Lpi when given), sigma = s/L,
-// tau = s/L (accelerated) or s/(1 + L), a = 1/(1 + tau), delta = tau a,
-// theta = 1; the tolerance tol * min(1, min_i scale_i) (bounds.py:233-236).
+// tau = s/L (accelerated and min q > 0) or s/(max q + L), a = 1/(1 + tau),
+// delta = tau a (the prox of q = 1), theta = 1; the tolerance
+// tol * min(1, min_i scale_i) (bounds.py:233-236).  qmax / qmin: per-sample
+// max and min of a general diagonal q, or nullptr for q = 1.
 template <typename T>
 __global__ void k_ps_steps(int64_t Bp, const T* __restrict__ rpart, int nrb,
                            const T* __restrict__ cpart, int ncb, const T* __restrict__ Lpi,
-                           T safety, int accelerated, T tol, T* tau_b, T* sig_b, T* a_b, T* d_b,
+                           T safety, int accelerated, T tol, const T* __restrict__ qmax,
+                           const T* __restrict__ qmin, T* tau_b, T* sig_b, T* a_b, T* d_b,
                            T* th_b, T* tol_b) {
 #pragma clang fp contract(off)
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -171,7 +191,8 @@ __global__ void k_ps_steps(int64_t Bp, const T* __restrict__ rpart, int nrb,
   const T norm = Lpi ? Lpi[b] : (T)__builtin_sqrt(rmax * cmax);
   const T L = maxp(norm, T(1e-12));
   const T sigma = safety / L;
-  const T tau = accelerated ? safety / L : safety / (one + L);
+  const T qhi = qmax ? qmax[b] : one, qlo = qmin ? qmin[b] : one;
+  const T tau = (accelerated && qlo > T(0)) ? safety / L : safety / (qhi + L);
   tau_b[b] = tau;
   sig_b[b] = sigma;
   a_b[b] = one / (one + tau);
@@ -180,17 +201,19 @@ __global__ void k_ps_steps(int64_t Bp, const T* __restrict__ rpart, int nrb,
   tol_b[b] = tol * minp(one, smin);
 }
 
-// The accelerated update after an iteration (kernels.py:279-283, gamma = 1):
-// nu = 1/sqrt(1 + tau); tau <- nu tau; sigma <- sigma / nu; theta <- nu; and
-// the prox coefficients of the new tau.
+// The accelerated update after an iteration (kernels.py:279-283):
+// nu = 1/sqrt(1 + gamma tau) with gamma = min q (1 when gam is nullptr);
+// tau <- nu tau; sigma <- sigma / nu; theta <- nu; and the prox
+// coefficients of q = 1 for the new tau.
 template <typename T>
-__global__ void k_ps_sched(int64_t Bp, T* tau_b, T* sig_b, T* a_b, T* d_b, T* th_b) {
+__global__ void k_ps_sched(int64_t Bp, const T* __restrict__ gam, T* tau_b, T* sig_b, T* a_b,
+                           T* d_b, T* th_b) {
 #pragma clang fp contract(off)
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= Bp) return;
   const T one = T(1);
   const T tau = tau_b[b];
-  const T nu = one / (T)__builtin_sqrt(one + tau);
+  const T nu = one / (T)__builtin_sqrt(one + (gam ? gam[b] : one) * tau);
   const T nt = nu * tau;
   tau_b[b] = nt;
   sig_b[b] = sig_b[b] / nu;
@@ -241,6 +264,28 @@ __global__ void k_ps_start(int64_t n, int64_t Bp, const T* __restrict__ start, T
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x)
     x[e] = start[e / Bp];
+}
+
+// Per sample of a general diagonal QP (one thread per sample, coalesced over
+// the batch): max_j q, min_j q, and valid = all(q > 0) & all(lower <= upper)
+// (diagonal_qp.py:120-123) into feas[b] for b < batch (0 beyond).
+template <typename T>
+__global__ void k_qp_stats(int64_t n, int64_t Bp, int64_t batch, const T* __restrict__ Q,
+                           const T* __restrict__ LO, const T* __restrict__ HI, T* qmax, T* qmin,
+                           int32_t* feas) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= Bp) return;
+  T hi = Q[b], lo = Q[b];
+  bool ok = true;
+  for (int64_t j = 0; j < n; ++j) {
+    const T q = Q[j * Bp + b];
+    hi = maxp(hi, q);
+    lo = minp(lo, q);
+    ok = ok && q > T(0) && LO[j * Bp + b] <= HI[j * Bp + b];
+  }
+  qmax[b] = hi;
+  qmin[b] = lo;
+  if (feas) feas[b] = (b < batch && ok) ? 1 : 0;
 }
 
 // L[b] = sqrt(max(eig[b], 0)) + eps

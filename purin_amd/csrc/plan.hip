@@ -95,7 +95,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
   std::vector<std::vector<std::pair<int64_t, double>>> bounds_of(n);
   for (int64_t r = 0; r < M; ++r) {
     const int64_t len = indptr[r + 1] - indptr[r];
-    if (r >= me && len == 1) {
+    if (r >= me && len == 1 && p->opts.bound_presolve) {
       const int32_t j = indices[indptr[r]];
       bounds_of[j].push_back({r, values[indptr[r]]});
     } else {
@@ -470,6 +470,8 @@ void purin_cp_default_options(purin_cp_options* o) {
   o->norm_seed = 42;
   o->diagonal_preconditioning = 0;
   o->safety = 0.95;
+  o->bound_presolve = 1;
+  o->reserved = 0;
 }
 
 void purin_cp_default_solve_options(purin_cp_solve_options* o) {

@@ -19,6 +19,10 @@ struct Post {
   const int32_t* __restrict__ brow;
   const T* __restrict__ bcoef;
   const T* __restrict__ bcoef_b; // per-sample coefficients: [nb][Bp], else nullptr
+  // general diagonal QP (diagonal_qp.py:276-319): q, c [n][Bp]; stationarity
+  // is max |y - clip(y - (q y + c + K^T dual), lo, hi)| and there are no bound rows
+  const T* __restrict__ Q;
+  const T* __restrict__ Cc;
   const T* __restrict__ tgt;     // n x Bp
   const T* __restrict__ Y;       // n x Bp
   const T* __restrict__ D;       // m x Bp (scaled duals)
@@ -118,8 +122,6 @@ __global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
       }
       const size_t off = (size_t)j * P.Bp + b0;
       const V y = vload(P.Y + off);
-      const V dy = y - vload(P.tgt + off);
-      const V base = dy + tk;
       V lo, hi;
       if (P.shared_bounds) {
         lo = vsplat<T>(P.LO[j]);
@@ -128,6 +130,18 @@ __global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
         lo = vload(P.LO + off);
         hi = vload(P.HI + off);
       }
+      if (P.Q) {
+        const V q = vload(P.Q + off), cc = vload(P.Cc + off);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const T g = y[s] - clipp(y[s] - ((q[s] * y[s] + cc[s]) + tk[s]), lo[s], hi[s]);
+          stat[s] = maxp(stat[s], absv(g));
+          if (!finite(y[s])) fin[s] = zero;
+        }
+        continue;
+      }
+      const V dy = y - vload(P.tgt + off);
+      const V base = dy + tk;
       const int k0 = P.bptr[j], k1 = P.bptr[j + 1];
       V lc = vsplat<T>(zero), uc = vsplat<T>(zero);
       for (int k = k0; k < k1; ++k) {
@@ -211,7 +225,8 @@ __global__ void k_post_final(Post<T> P, int64_t batch, T tol_cfg, T residual_fac
     fin = fin && p[2 * plane] != zero;
   }
   const T residual = maxp(res, stat);
-  const bool f = fin && finite(residual) && finite(cp_gap[b]);
+  // the QP's finiteness omits the gap (diagonal_qp.py:291-295)
+  const bool f = fin && finite(residual) && (P.Q || finite(cp_gap[b]));
   const bool conv = f && cp_conv[b] != 0 && residual <= tol_cfg;
   if (status) status[b] = conv ? 0 : (f ? 1 : 3);
   if (iterations) iterations[b] = count[b];

@@ -78,12 +78,39 @@ class AdjointOutput:
     g_values: torch.Tensor | None = None
 
 
+@dataclass
+class QPOutput:
+    y: torch.Tensor
+    multipliers: torch.Tensor
+    slacks: torch.Tensor
+    status: torch.Tensor
+    iterations: torch.Tensor
+    residual: torch.Tensor
+    finite: torch.Tensor
+    converged: torch.Tensor
+    saved: torch.Tensor | None
+
+
+@dataclass
+class QPAdjointOutput:
+    g_q: torch.Tensor
+    g_c: torch.Tensor
+    g_values: torch.Tensor
+    g_rhs: torch.Tensor
+    g_lower: torch.Tensor
+    g_upper: torch.Tensor
+    valid: torch.Tensor
+    info: torch.Tensor
+    residual: torch.Tensor
+
+
 class Plan:
     """A prepared shared-matrix CP plan (``purin_cp_plan_create``)."""
 
     def __init__(self, n, me, mi, indptr, indices, values, *, dtype=torch.float64,
                  accelerated=False, row_scaling=True, norm_bound=True, norm_iterations=20,
-                 norm_seed=42, safety=0.95, diagonal_preconditioning=False, device="cuda"):
+                 norm_seed=42, safety=0.95, diagonal_preconditioning=False, device="cuda",
+                 bound_presolve=True):
         self.lib = _lib.load()
         self.code, self.dtype = _dtype_code(dtype)
         device = torch.device(device)
@@ -105,6 +132,7 @@ class Plan:
         opts.norm_seed = int(norm_seed)
         opts.safety = float(safety)
         opts.diagonal_preconditioning = int(bool(diagonal_preconditioning))
+        opts.bound_presolve = int(bool(bound_presolve))
         handle = C.c_void_p()
         torch.cuda.set_device(self.device)
         _lib.check(self.lib.purin_cp_plan_create(
@@ -267,6 +295,73 @@ class Plan:
             _ptr(y), _ptr(mult), _ptr(slacks), _i32(status), _i32(it), _ptr(res), _u8(fin),
             _u8(elig), _ptr(saved)))
         return ProjectOutput(y, mult, slacks, status, it, res, fin.bool(), elig.bool(), saved)
+
+    def qp_solve(self, q, c, rhs, lower, upper, *, values=None, y0=None, dual0=None,
+                 tolerance=1e-9, max_iterations=10000, early_stop=True, check_every=32,
+                 save=False, timing=False):
+        """General diagonal QP (``purin_cp_qp_solve``): PreparedDiagonalQP.solve
+        semantics on a plan created with ``bound_presolve=False``."""
+        batch = q.shape[0]
+        M = self.me + self.mi
+        q = self._tensor(q, (batch, self.n), "q")
+        c = self._tensor(c, (batch, self.n), "c")
+        rhs = self._tensor(rhs, (batch, M), "rhs")
+        lower = self._tensor(lower, (batch, self.n), "lower")
+        upper = self._tensor(upper, (batch, self.n), "upper")
+        values = None if values is None else self._tensor(values, (batch, self.nnz), "values")
+        y0 = None if y0 is None else self._tensor(y0, (batch, self.n), "initial_y")
+        dual0 = None if dual0 is None else self._tensor(dual0, (batch, M), "initial_dual")
+        o = _lib.default_solve_options()
+        o.tolerance = float(tolerance)
+        o.max_iterations = int(max_iterations)
+        o.early_stop = int(bool(early_stop))
+        o.check_every = int(check_every)
+        o.timing = int(bool(timing))
+        y = self._empty(batch, self.n)
+        mult = self._empty(batch, M)
+        slacks = self._empty(batch, self.mi)
+        status = self._empty(batch, dtype=torch.int32)
+        it = self._empty(batch, dtype=torch.int32)
+        res = self._empty(batch)
+        fin = self._empty(batch, dtype=torch.uint8)
+        conv = self._empty(batch, dtype=torch.uint8)
+        saved = self._empty(self.saved_bytes(batch), dtype=torch.uint8) if save else None
+        _lib.check(self.lib.purin_cp_qp_solve(
+            self.handle, _stream(), batch, _ptr(q), _ptr(c), _ptr(values), _ptr(rhs),
+            _ptr(lower), _ptr(upper), _ptr(y0), _ptr(dual0), C.byref(o), _ptr(y), _ptr(mult),
+            _ptr(slacks), _i32(status), _i32(it), _ptr(res), _u8(fin), _u8(conv), _ptr(saved)))
+        return QPOutput(y, mult, slacks, status, it, res, fin.bool(), conv.bool(), saved)
+
+    def qp_adjoint(self, saved, q, c, cot_y, *, values=None, cot_dual=None, tolerance=1e-9,
+                   atol=0.0, restart=30, max_iterations=100, adjoint_tolerance=1e-8,
+                   force_eligible=False):
+        """Implicit VJP of ``qp_solve`` (``purin_cp_qp_adjoint``)."""
+        batch = cot_y.shape[0]
+        M = self.me + self.mi
+        q = self._tensor(q, (batch, self.n), "q")
+        c = self._tensor(c, (batch, self.n), "c")
+        values = None if values is None else self._tensor(values, (batch, self.nnz), "values")
+        cot = self._tensor(cot_y, (batch, self.n), "cotangent")
+        cotd = None if cot_dual is None else self._tensor(cot_dual, (batch, M), "dual cotangent")
+        o = _lib.default_adjoint_options()
+        o.tolerance = float(tolerance)
+        o.atol = float(atol)
+        o.restart = int(restart)
+        o.max_iterations = int(max_iterations)
+        o.adjoint_tolerance = float(adjoint_tolerance)
+        o.force_eligible = int(bool(force_eligible))
+        gq, gc = self._empty(batch, self.n), self._empty(batch, self.n)
+        gv = self._empty(batch, self.nnz)
+        gr = self._empty(batch, M)
+        gl, gu = self._empty(batch, self.n), self._empty(batch, self.n)
+        valid = self._empty(batch, dtype=torch.uint8)
+        info = self._empty(batch, dtype=torch.int32)
+        res = self._empty(batch)
+        _lib.check(self.lib.purin_cp_qp_adjoint(
+            self.handle, _stream(), batch, _ptr(saved), _ptr(q), _ptr(c), _ptr(values), _ptr(cot),
+            _ptr(cotd), C.byref(o), _ptr(gq), _ptr(gc), _ptr(gv), _ptr(gr), _ptr(gl), _ptr(gu),
+            _u8(valid), _i32(info), _ptr(res)))
+        return QPAdjointOutput(gq, gc, gv, gr, gl, gu, valid.bool(), info, res)
 
     def adjoint(self, saved, target, rhs, cot_y, *, tolerance=1e-9, atol=0.0, restart=30,
                 max_iterations=100, adjoint_tolerance=1e-8, force_eligible=False,
