@@ -141,3 +141,22 @@ def test_canonical_rows_rhs_broadcast():
     c = CanonicalRows(2, 1, 0, 1, np.array([0, 2]), np.array([0, 1], np.int32), np.ones(2),
                       np.array([0.5]), np.array([[2.0]]))
     np.testing.assert_array_equal(c.rhs([[1.0], [2.0]]), [[2.5], [4.5]])
+
+
+def test_invalid_qp_structures():
+    """Reference tests/test_diagonal_qp.py:109-137 (the parts that need no GPU)."""
+    from purin_amd.diagonal_qp import QPStructure, dense_qp_data
+
+    for args in [(0,), (2, ((0, 0),)), (2, ((2,),)), (2, ((-1,),))]:
+        with pytest.raises(ValueError):
+            QPStructure(*args)
+    structure = QPStructure(2)
+    with pytest.raises(ValueError):
+        structure.prepare(batch_size=0)
+    with pytest.raises(ValueError):
+        structure.prepare(batch_size=1,
+                          config=pa.ChambollePockConfig(metric_diagonal=(1.0, 1.0)))
+    with pytest.raises(ValueError):
+        dense_qp_data(np.ones(2), np.ones(2), np.empty((0, 2)), [], np.empty((0, 2)), [], -1, 1)
+    s = QPStructure(3, ((0, 2),), ((1,), (0, 1, 2)))
+    assert s.rows == ((0, 2), (1,), (0, 1, 2))

@@ -1,0 +1,91 @@
+"""The reference's diagonal-QP tests through this build's front end
+(purin_amd/diagonal_qp.py) on the GPU; gradients use torch autograd, whose
+backward is purin_cp_qp_adjoint."""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as _torch
+
+    if not _torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    return _torch
+
+
+@pytest.mark.parametrize("accelerated", [False, True])
+@pytest.mark.parametrize("scaling", [False, True])
+def test_diagonal_qp_value_and_coefficient_gradient(torch, accelerated, scaling):
+    """Reference tests/test_diagonal_qp.py:13-48."""
+    from purin_amd import ChambollePockConfig
+    from purin_amd.diagonal_qp import dense_qp_data
+
+    f64 = dict(dtype=torch.float64, device="cuda")
+    structure, data = dense_qp_data(
+        torch.tensor([[2.0, 4.0]], **f64), torch.tensor([[-2.0, -4.0]], **f64),
+        torch.ones((1, 1, 2), **f64), torch.tensor([1.0], **f64), torch.empty((0, 2), **f64),
+        torch.empty(0, **f64), -np.inf, np.inf)
+    config = ChambollePockConfig(accelerated=accelerated, row_scaling=scaling, tolerance=1e-9,
+                                 max_iterations=3000)
+    solver = structure.prepare(batch_size=1, config=config)
+    result = solver.solve(data)
+    np.testing.assert_allclose(result.y.detach().cpu(), [[1 / 3, 2 / 3]], atol=1e-8)
+    assert float(result.residual_inf_norm[0]) < 1e-8
+    expected = -np.diag([0.5, 0.25]) + np.outer([0.5, 0.25], [0.5, 0.25]) / 0.75
+    actual = torch.autograd.functional.jacobian(
+        lambda c: solver.solve(data._replace(c=c[None, :])).y[0], data.c[0])
+    np.testing.assert_allclose(actual.cpu(), expected, atol=1e-7)
+    warm = solver.solve(data, initial_y=result.y, initial_dual=result.multipliers_eq)
+    np.testing.assert_allclose(warm.y.detach().cpu(), result.y.detach().cpu(), atol=1e-8)
+    with pytest.raises(ValueError):
+        solver.solve(data._replace(q=torch.ones((2, 2), **f64)))
+    with pytest.raises(ValueError):
+        solver.solve(data, initial_y=torch.zeros((2, 2), **f64))
+    with pytest.raises(ValueError):
+        solver.solve(data, initial_dual=torch.zeros((2, 1), **f64))
+
+
+def test_every_input_is_differentiable(torch):
+    """Gradients w.r.t. q, c, values, rhs, lower and upper, and through the
+    multipliers, against central differences of the forward (one active bound,
+    one equality, one inequality)."""
+    from purin_amd import ChambollePockConfig
+    from purin_amd.diagonal_qp import QPData, QPStructure
+
+    f64 = dict(dtype=torch.float64, device="cuda")
+    structure = QPStructure(3, ((0, 1, 2),), ((0, 2),))
+    cfg = ChambollePockConfig(tolerance=1e-12, max_iterations=100000)
+    solver = structure.prepare(batch_size=1, config=cfg)
+    base = QPData(torch.tensor([[1.0, 2.0, 1.5]], **f64), torch.tensor([[-1.0, 0.5, -2.0]], **f64),
+                  torch.tensor([[[1.0, 1.0, 1.0], [1.0, 2.0, 0.0]]], **f64),
+                  torch.tensor([[1.0, 0.8]], **f64), torch.tensor([[-1.0, -0.1, -1.0]], **f64),
+                  torch.tensor([[1.0, 1.0, 1.0]], **f64))
+    w_y = torch.tensor([[0.3, -1.2, 0.7]], **f64)
+    w_m = torch.tensor([[0.5, -0.4]], **f64)
+
+    def f(*xs):
+        r = solver.solve(QPData(*xs))
+        return (r.y * w_y).sum() + (torch.cat((r.multipliers_eq, r.multipliers_ineq), 1)
+                                    * w_m).sum()
+
+    inputs = [x.clone().requires_grad_(True) for x in base]
+    r = solver.solve(QPData(*inputs))
+    assert int(r.status[0]) == 0
+    f(*inputs).backward()
+    h = 1e-6
+    for k, x in enumerate(base):
+        flat = x.reshape(-1)
+        for j in range(flat.numel()):
+            if k == 2 and j == 5:  # padding slot of the second row: no coefficient
+                continue
+            up = [t.clone() for t in base]
+            dn = [t.clone() for t in base]
+            up[k].reshape(-1)[j] += h
+            dn[k].reshape(-1)[j] -= h
+            want = float((f(*up) - f(*dn)) / (2 * h))
+            got = float(inputs[k].grad.reshape(-1)[j])
+            assert abs(got - want) <= 2e-6, (k, j, got, want)
