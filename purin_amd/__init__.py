@@ -28,6 +28,10 @@ _EXPORTS = {
     "WeightedDistance": ("projection", "WeightedDistance"),
     "ChambollePockProjection": ("projection", "ChambollePockProjection"),
     "Plan": ("plan", "Plan"),
+    "FunctionalProblem": ("local_quadratic", "FunctionalProblem"),
+    "LocalQuadratic": ("local_quadratic", "LocalQuadratic"),
+    "QPStructure": ("diagonal_qp", "QPStructure"),
+    "QPData": ("diagonal_qp", "QPData"),
 }
 __all__ = list(_EXPORTS)
 

@@ -160,3 +160,39 @@ def test_invalid_qp_structures():
         dense_qp_data(np.ones(2), np.ones(2), np.empty((0, 2)), [], np.empty((0, 2)), [], -1, 1)
     s = QPStructure(3, ((0, 2),), ((1,), (0, 1, 2)))
     assert s.rows == ((0, 2), (1,), (0, 1, 2))
+
+
+def _local_problem():
+    import torch
+
+    return pa.FunctionalProblem(
+        parameter_size=1, variable_size=2,
+        objective=lambda p, y: 0.5 * torch.sum(torch.tensor([2.0, 4.0], dtype=y.dtype,
+                                                            device=y.device)
+                                               * (y - 1) ** 2),
+        equalities=lambda p, y: torch.stack([torch.sum(y) - p[0]]), equality_size=1,
+        inequalities=lambda p, y: torch.stack([-y[0]]), inequality_size=1)
+
+
+def test_local_quadratic_coefficients():
+    """Reference tests/test_diagonal_qp.py:53-76 (the builder, on the CPU)."""
+    import torch
+
+    definition = pa.LocalQuadratic(_local_problem(), lower=lambda p: torch.zeros(2), upper=2.0)
+    compiled = definition.compile()
+    context = torch.ones((1, 1), dtype=torch.float64)
+    anchor = torch.tensor([[0.4, 0.5]], dtype=torch.float64)
+    data = compiled.build(context, anchor)
+    np.testing.assert_allclose(data.q, [[2.0, 4.0]])
+    np.testing.assert_allclose(data.c, [[-2.0, -4.0]])
+    np.testing.assert_allclose(data.rhs, [[1.0, 0.0]])
+    np.testing.assert_allclose(data.lower, [[0.0, 0.0]])
+    np.testing.assert_allclose(data.upper, [[2.0, 2.0]])
+    for badcontext, badanchor in [(context[0], anchor), (context, anchor[0]),
+                                  (torch.ones((2, 1)), anchor), (torch.ones((1, 2)), anchor),
+                                  (context, torch.ones((1, 3)))]:
+        with pytest.raises(ValueError):
+            compiled.build(badcontext, badanchor)
+    for kwargs in [dict(rho=0), dict(diagonal_floor=-1), dict(rho=np.inf)]:
+        with pytest.raises(ValueError):
+            pa.LocalQuadratic(_local_problem(), **kwargs)

@@ -89,3 +89,34 @@ def test_every_input_is_differentiable(torch):
             want = float((f(*up) - f(*dn)) / (2 * h))
             got = float(inputs[k].grad.reshape(-1)[j])
             assert abs(got - want) <= 2e-6, (k, j, got, want)
+
+
+def test_local_quadratic_training_protocol(torch):
+    """Reference tests/test_diagonal_qp.py:53-106: the prepared local QP solves to
+    [1/3, 2/3] through solve, __call__, with_info and project_training."""
+    import purin_amd as pa
+    from tests.test_frontend import _local_problem
+
+    definition = pa.LocalQuadratic(
+        _local_problem(), lower=lambda p: torch.zeros(2, dtype=p.dtype, device=p.device),
+        upper=2.0, config=pa.ChambollePockConfig(tolerance=1e-9, max_iterations=3000))
+    f64 = dict(dtype=torch.float64, device="cuda")
+    context = torch.ones((1, 1), **f64)
+    anchor = torch.tensor([[0.4, 0.5]], **f64)
+    prepared = definition.prepare(batch_size=1)
+    result = prepared.solve(anchor, context)
+    np.testing.assert_allclose(result.y.detach().cpu(), [[1 / 3, 2 / 3]], atol=1e-8)
+    np.testing.assert_allclose(prepared(anchor, context).detach().cpu(),
+                               result.y.detach().cpu(), atol=1e-8)
+    np.testing.assert_allclose(prepared.with_info(anchor, context)[0].detach().cpu(),
+                               result.y.detach().cpu(), atol=1e-8)
+    for kwargs in [{}, {"multipliers_eq": result.multipliers_eq,
+                        "multipliers_ineq": result.multipliers_ineq}]:
+        np.testing.assert_allclose(
+            prepared.project_training(anchor, context, **kwargs).y_tilde.detach().cpu(),
+            result.y.detach().cpu(), atol=1e-8)
+    # the context (the equality's rhs) is differentiable through the local QP:
+    # y = argmin over u + v = p of the quadratic; dy/dp = Q^-1 1 / (1'Q^-1 1) = [2/3, 1/3]
+    ctx = context.clone().requires_grad_(True)
+    jac = torch.autograd.functional.jacobian(lambda p: prepared(anchor, p)[0], ctx)
+    np.testing.assert_allclose(jac.reshape(2).cpu(), [2 / 3, 1 / 3], atol=1e-7)
