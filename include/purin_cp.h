@@ -245,6 +245,25 @@ int purin_cp_qp_solve(purin_cp_plan* plan, void* stream, int64_t batch, const vo
                       void* slacks, int32_t* status, int32_t* iterations, void* residual,
                       uint8_t* finite, uint8_t* converged, void* saved);
 
+/*
+ * The dense CP adapter's forward (solve_dense, chambolle_pock/dense.py:26-105,
+ * as called by dense_layer.py:13-134 after any equilibration): the diagonal
+ * QP of purin_cp_qp_solve with the adapter's policy -- the factored prox
+ * a ((y - tau K^T d) - tau c) (kernels.py:140-142), no freezing of accepted
+ * samples (all iterate until the last is accepted), no stationarity in the
+ * stop test, power-iteration steps.  The plan keeps every row
+ * (bound_presolve = 0) with row_scaling = 0, norm_bound = 0 and
+ * diagonal_preconditioning = 0; dense matrices are rows over all n columns
+ * (a packed inequality_support gives those rows its columns).
+ * Inputs as purin_cp_qp_solve.  Outputs y (B, n), multipliers (B, me+mi)
+ * (lambda then mu), iterations (B); each but y may be NULL.
+ */
+int purin_cp_dense_solve(purin_cp_plan* plan, void* stream, int64_t batch, const void* q,
+                         const void* c, const void* values, const void* rhs, const void* lower,
+                         const void* upper, const void* y0, const void* dual0,
+                         const purin_cp_solve_options* opts, void* y, void* multipliers,
+                         int32_t* iterations, void* saved);
+
 /* Kernel times of the last solve()/project() call made with opts.timing = 1,
  * from HIP events recorded on that call's stream around each launch. */
 typedef struct {

@@ -62,7 +62,7 @@ class Linearization(NamedTuple):
 
 
 def linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau, sigma,
-              q=None, c=None):
+              q=None, c=None, factored_proximal=False):
     """Masks of ``cp_step`` at ``z = (y, dual, y)`` with theta = 1 (bounds.py:109-128).
 
     ``tau``/``sigma`` are per sample ``(B,)`` or, with diagonal preconditioning,
@@ -82,7 +82,11 @@ def linearize(values, support, mask, me, y, dual, target, rhs, lower, upper, tau
     q = np.ones_like(y) if q is None else np.asarray(q, dtype)
     c = -target if c is None else np.asarray(c, dtype)
     a, delta, offset = _cp.proximal_coefficients(q, c, tau)
-    s = a * y - delta * tmv(dplus) + offset
+    if factored_proximal:  # the dense adapter's arithmetic (kernels.py:140-142)
+        step = tau[:, None] if np.ndim(tau) == 1 else tau
+        s = a * ((y - step * tmv(dplus)) - step * c)
+    else:
+        s = a * y - delta * tmv(dplus) + offset
     # d s / d q with a = 1/(1 + tau q), delta = tau a: -tau a s
     q_grad = -(np.broadcast_to(tau[:, None] if np.ndim(tau) == 1 else tau, s.shape) * a * s) \
         if general else None

@@ -247,10 +247,11 @@ def clip(x, lower, upper):
 
 
 def cp_step(state, q, c, rhs, lower, upper, mv, tmv, me, tau, sigma, theta,
-            proximal=None, return_pre_clip=False):
+            proximal=None, return_pre_clip=False, factored_proximal=False):
     """One CP primal/dual update plus extrapolation; kernels.py:91-150.
 
-    (``factored_proximal=False`` branch, the one on the projection path.)
+    ``factored_proximal`` selects the dense adapter's arithmetic
+    ``inverse * ((y - tau K^T d) - tau c)`` (kernels.py:140-142).
     """
     y, dual, ybar = state
     dual_step = sigma[:, None] if sigma.ndim == 1 else sigma
@@ -261,7 +262,11 @@ def cp_step(state, q, c, rhs, lower, upper, mv, tmv, me, tau, sigma, theta,
     inverse, dual_weight, offset = (
         proximal_coefficients(q, c, tau) if proximal is None else proximal
     )
-    pre = inverse * y - dual_weight * tmv(next_dual) + offset
+    if factored_proximal:
+        step = tau[:, None] if tau.ndim == 1 else tau
+        pre = inverse * ((y - step * tmv(next_dual)) - step * c)
+    else:
+        pre = inverse * y - dual_weight * tmv(next_dual) + offset
     next_y = clip(pre, lower, upper)
     th = theta[:, None]
     out = (next_y, next_dual, next_y + th * (next_y - y))
@@ -307,7 +312,8 @@ def sparse_cp(q, c, values, rhs, support, mask, me, lower, upper, *,
               accelerated=False, safety=0.95, max_iterations=5000, tolerance=1e-9,
               norm_iterations=20, norm_seed=42, y0=None, dual0=None,
               freeze_converged=False, check_stationarity=False, norm_bound=False,
-              diagonal_preconditioning=False, early_stop=True, steps=None, trace=None):
+              diagonal_preconditioning=False, early_stop=True, steps=None, trace=None,
+              factored_proximal=False):
     """Batched diagonal-QP CP solve; kernels.py:178-305.
 
     ``early_stop=False`` is this build's explicit fixed-iteration mode: the
@@ -342,7 +348,8 @@ def sparse_cp(q, c, values, rhs, support, mask, me, lower, upper, *,
     iteration = 0
     while iteration < max_iterations and not np.all(done):
         ny, nd, nb = cp_step((y, dual, ybar), q, c, rhs, lower, upper, mv, tmv, me,
-                             tau, sigma, theta, proximal=proximal)
+                             tau, sigma, theta, proximal=proximal,
+                             factored_proximal=factored_proximal)
         active = ~done if freeze_converged else np.ones_like(done)
         if early_stop:
             residual, gap = diagnostics(ny, nd, q, c, rhs, lower, upper, mv, tmv, me)

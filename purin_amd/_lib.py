@@ -33,6 +33,7 @@ SYMBOLS = (
     "purin_cp_project",
     "purin_cp_project_values",
     "purin_cp_qp_solve",
+    "purin_cp_dense_solve",
     "purin_cp_default_adjoint_options",
     "purin_cp_adjoint",
     "purin_cp_adjoint_values",
@@ -163,6 +164,9 @@ def load(path: str = LIB_PATH):
                                       C.POINTER(SolveOptions), vp, vp, vp, i32p, i32p, vp, u8p,
                                       u8p, vp]
     lib.purin_cp_qp_solve.restype = C.c_int
+    lib.purin_cp_dense_solve.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp, vp, vp,
+                                         C.POINTER(SolveOptions), vp, vp, i32p, vp]
+    lib.purin_cp_dense_solve.restype = C.c_int
     lib.purin_cp_last_timing.argtypes = [vp, C.POINTER(Timing)]
     lib.purin_cp_last_timing.restype = C.c_int
     lib.purin_cp_last_adjoint_stats.argtypes = [vp, C.POINTER(AdjointStats)]

@@ -396,6 +396,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
       A.Q = qp->Q;
       A.Cc = qp->Cc;
       A.tgt = nullptr;
+      A.factored = A.nofreeze = A.nostat = qp->dense;
     }
   } else if (p->diag) {  // diagonal steps (non-accelerated, so constant over the loop)
     A.sig_r = (const T*)p->diag_sig;
@@ -405,6 +406,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   int32_t* done = (int32_t*)(ws + L.done);
   int32_t* count = (int32_t*)(ws + L.count);
   int32_t* ndone = (int32_t*)(ws + L.ndone);
+  int32_t* snap = ndone + 1;  // accepted count at the start of the iteration (no freezing)
   const int m = A.K.m, n = A.K.n;
   const bool early = o.early_stop != 0;
   const size_t lds = resident_lds<T>(p);
@@ -466,6 +468,20 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
       if (m) k_row_pass<T, false><<<grow, kBlock, 0, st>>>(A);
       if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 1], st));
       k_col_pass<T, 0, kRowsPerWaveFixed><<<gcol, kBlock, 0, st>>>(A);
+    } else if (A.nofreeze) {
+      // every sample iterates until the last is accepted; the kernels return
+      // at once from the iteration after that (the host reads the count lazily)
+      A.done = done;
+      A.stop = snap;
+      A.nstop = batch;
+      k_snap<<<1, 64, 0, st>>>(ndone, snap);
+      if (m) k_row_pass<T, false><<<grow, kBlock, 0, st>>>(A);
+      if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 1], st));
+      k_col_pass<T, 1, kRowsPerWaveEarly><<<gcolE, kBlock, 0, st>>>(A);
+      if (timing) PURIN_HIP(hipEventRecord(evd[it], st));
+      if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres, kBlock, 0, st>>>(A);
+      k_decide<T, false><<<gdec, 64 * kDecideGroups, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
+                                                   nullptr, nullptr, nullptr, nullptr, nullptr);
     } else {
       A.done = done;
       if (m) k_row_pass<T, true><<<grow, kBlock, 0, st>>>(A);
@@ -526,6 +542,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   }
   // final diagnostics on the returned state (kernels.py:291-305)
   A.done = nullptr;
+  A.stop = nullptr;
   k_col_pass<T, 2, kRowsPerWaveEarly><<<gcolE, kBlock, 0, st>>>(A);
   if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres, kBlock, 0, st>>>(A);
   k_decide<T, true><<<gdec, 64 * kDecideGroups, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
@@ -749,7 +766,8 @@ static int qp_solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const 
                          const T* values, const T* rhs, const T* lower, const T* upper,
                          const T* y0, const T* dual0, const purin_cp_solve_options& o, T* y,
                          T* mult, T* slacks, int32_t* status, int32_t* iterations, T* residual,
-                         uint8_t* finite_out, uint8_t* converged_out, void* saved) {
+                         uint8_t* finite_out, uint8_t* converged_out, void* saved,
+                         int dense = 0) {
   int rc = check_layout_args<T>(p, batch);
   if (rc) return rc;
   if (!q || !c || !lower || !upper || (p->M && !rhs))
@@ -757,6 +775,10 @@ static int qp_solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const 
   if (p->opts.bound_presolve)
     return set_error(PURIN_CP_ERR_ARG,
                      "the diagonal-QP entry needs a plan created with bound_presolve = 0");
+  if (dense && (p->opts.row_scaling || p->opts.norm_bound || p->opts.diagonal_preconditioning))
+    return set_error(PURIN_CP_ERR_ARG,
+                     "the dense adapter needs a plan with row_scaling = 0, norm_bound = 0 and "
+                     "diagonal_preconditioning = 0 (dense.py:85-106)");
   if (p->metric)
     return set_error(PURIN_CP_ERR_ARG, "QPData.q already defines the quadratic metric");
   if (o.max_iterations < 1) return set_error(PURIN_CP_ERR_ARG, "max_iterations must be a positive integer");
@@ -768,7 +790,7 @@ static int qp_solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const 
   if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, true))) return rc;
   const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
   constexpr int64_t TS = tile_samples<T>();
-  write_header<T>(st, sv, batch, Bp, 3, 0, p);
+  write_header<T>(st, sv, batch, Bp, dense ? 4 : 3, 0, p);
   T* QQ = (T*)(ws + L.QQ);
   T* QC = (T*)(ws + L.QC);
   T* qmax = (T*)(ws + L.QS);
@@ -803,7 +825,7 @@ static int qp_solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const 
   if (m)
     k_prep_rows<T><<<2048, 256, 0, st>>>((int)m, Bp, p->dkept, (const T*)p->dscale, PS.SC, RF, MF,
                                          (T*)(sv + L.R), (T*)(sv + L.D));
-  const QPRun<T> qr{QQ, QC, qmin};
+  const QPRun<T> qr{QQ, QC, qmin, dense};
   if ((rc = run_iterations<T>(p, st, batch, L, sv, ws, o, (T)o.tolerance, nullptr, &PS, &qr)))
     return rc;
   // original-unit residual, status and slacks (diagonal_qp.py:276-319)
@@ -852,6 +874,28 @@ static int qp_solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const 
 using namespace purin;
 
 extern "C" {
+
+int purin_cp_dense_solve(purin_cp_plan* p, void* stream, int64_t batch, const void* q,
+                         const void* c, const void* values, const void* rhs, const void* lower,
+                         const void* upper, const void* y0, const void* dual0,
+                         const purin_cp_solve_options* opts, void* y, void* mult,
+                         int32_t* iterations, void* saved) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  purin_cp_solve_options o;
+  purin_cp_default_solve_options(&o);
+  if (opts) o = *opts;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64)
+    return qp_solve_impl<double>(p, st, batch, (const double*)q, (const double*)c,
+                                 (const double*)values, (const double*)rhs, (const double*)lower,
+                                 (const double*)upper, (const double*)y0, (const double*)dual0, o,
+                                 (double*)y, (double*)mult, nullptr, nullptr, iterations, nullptr,
+                                 nullptr, nullptr, saved, 1);
+  return qp_solve_impl<float>(p, st, batch, (const float*)q, (const float*)c, (const float*)values,
+                              (const float*)rhs, (const float*)lower, (const float*)upper,
+                              (const float*)y0, (const float*)dual0, o, (float*)y, (float*)mult,
+                              nullptr, nullptr, iterations, nullptr, nullptr, nullptr, saved, 1);
+}
 
 int purin_cp_qp_solve(purin_cp_plan* p, void* stream, int64_t batch, const void* q, const void* c,
                       const void* values, const void* rhs, const void* lower, const void* upper,

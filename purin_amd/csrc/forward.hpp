@@ -54,6 +54,7 @@ struct QPRun {
   const T* Q;
   const T* Cc;
   const T* gamma;
+  int dense;  // the dense adapter's policy (factored prox, no freezing, no stationarity)
 };
 
 // Which steps prepare_values computes.

@@ -86,6 +86,16 @@ struct Iter {
   const T* __restrict__ Cc;
   const T* __restrict__ tau_b;
   const T* __restrict__ tau_cb;
+  // dense adapter policy (chambolle_pock/dense.py:85-106): factored prox
+  // a ((y - tau K^T d) - tau c) (kernels.py:140-142), no freezing of accepted
+  // samples (freeze_converged=False: every sample keeps iterating and
+  // counting until all are done) and no stationarity in the stop test
+  int factored, nofreeze, nostat;
+  // without freezing the loop must stop at the iteration where the last
+  // sample is accepted (kernels.py:238-240); the passes and the stop test
+  // return at once when *stop (the accepted count) has reached nstop
+  const int32_t* stop;
+  int64_t nstop;
   T* colpart;                 // [5][ncb][Bp]: primal, dual, stat, bound, finite
   T* rowpart;                 // [3][nrb][Bp]: residual max, r.d, finite
   int ncb, nrb;
@@ -121,6 +131,7 @@ __device__ __forceinline__ typename Lane<T>::V step_theta(const Iter<T>& A, int6
 // ---------------------------------------------------------------------------
 template <typename T, bool MASKED>
 __global__ __launch_bounds__(kBlock) void k_row_pass(Iter<T> A) {
+  if (A.stop && *A.stop >= A.nstop) return;
   using V = typename Lane<T>::V;
   constexpr int S = Lane<T>::S;
   const int lane = threadIdx.x & 63;
@@ -162,6 +173,7 @@ __global__ __launch_bounds__(kBlock) void k_row_pass(Iter<T> A) {
 // ---------------------------------------------------------------------------
 template <typename T, int MODE, int CPW>
 __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
+  if (MODE != 2 && A.stop && *A.stop >= A.nstop) return;
   using V = typename Lane<T>::V;
   constexpr int S = Lane<T>::S;
   const int lane = threadIdx.x & 63;
@@ -212,9 +224,13 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
 #pragma unroll
           for (int s = 0; s < S; ++s) {
             const T aj = T(1) / (T(1) + tau[s] * qv[s]);
-            const T dj = tau[s] * aj;
-            const T oj = -dj * cv[s];
-            sv[s] = aj * y[s] - dj * t[s] + oj;
+            if (A.factored) {
+              sv[s] = aj * ((y[s] - tau[s] * t[s]) - tau[s] * cv[s]);
+            } else {
+              const T dj = tau[s] * aj;
+              const T oj = -dj * cv[s];
+              sv[s] = aj * y[s] - dj * t[s] + oj;
+            }
           }
         } else {
           const V aj = step_a(A, j, b0), dj = step_delta(A, j, b0);
@@ -228,7 +244,7 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
           const V ybo = vload(A.YB + off);
 #pragma unroll
           for (int s = 0; s < S; ++s) {
-            if (keep[s] != zero) {
+            if (keep[s] != zero && !A.nofreeze) {
               yn[s] = yo[s];  // frozen sample: keep state (its diagnostics are unused)
               yb[s] = ybo[s];
             }
@@ -295,6 +311,7 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
 // ---------------------------------------------------------------------------
 template <typename T, int RPW>
 __global__ __launch_bounds__(kBlock) void k_res_pass(Iter<T> A) {
+  if (A.stop && *A.stop >= A.nstop) return;
   using V = typename Lane<T>::V;
   constexpr int S = Lane<T>::S;
   const int lane = threadIdx.x & 63;
@@ -349,6 +366,7 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
     Iter<T> A, int64_t batch, T tol_scalar, const T* __restrict__ tolv, int32_t* done,
     int32_t* count, int32_t* ndone, const int32_t* feasible, T* out_res, T* out_gap,
     int32_t* out_conv, int32_t* out_fin) {
+  if (!FINAL && A.stop && *A.stop >= A.nstop) return;
   constexpr int G = kDecideGroups;
   __shared__ T buf[G][64];
   const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
@@ -388,7 +406,10 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
     __syncthreads();
   }
   if (g != 0 || b >= batch) return;
-  if (!FINAL && done[b]) return;
+  if (!FINAL && done[b]) {
+    if (A.nofreeze) count[b] += 1;  // accepted samples keep iterating (and counting)
+    return;
+  }
   const T tol = tolv ? tolv[b] : tol_scalar;
   const T primal = q[0], dualo = q[1], stat = q[2], bnd = q[3], res = q[5], rd = q[6];
   const bool fin = q[4] != zero, fin_d = q[7] != zero;
@@ -398,16 +419,17 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
   const T residual = maxp(res, bnd);
   if (!FINAL) {
     count[b] += 1;
-    const bool ok = fin && fin_d && finite(gap) && residual <= tol && gap <= tol && stat <= tol;
+    const bool ok = fin && fin_d && finite(gap) && residual <= tol && gap <= tol &&
+                    (A.nostat || stat <= tol);
     if (ok) {
       done[b] = 1;
       atomicAdd(ndone, 1);
     }
   } else {
     const bool f = fin && fin_d && finite(gap) && finite(residual);
-    const bool conv = f && residual <= tol && gap <= tol && stat <= tol &&
+    const bool conv = f && residual <= tol && gap <= tol && (A.nostat || stat <= tol) &&
                       (feasible == nullptr || feasible[b] != 0);
-    out_res[b] = maxp(residual, stat);
+    out_res[b] = A.nostat ? residual : maxp(residual, stat);
     out_gap[b] = gap;
     out_conv[b] = conv ? 1 : 0;
     out_fin[b] = f ? 1 : 0;
@@ -598,6 +620,11 @@ __global__ void k_finish_solve(int64_t batch, const int32_t* __restrict__ count,
   if (residual) residual[b] = ores[b];
   if (gap) gap[b] = ogap[b];
   if (converged) converged[b] = oconv[b] ? 1 : 0;
+}
+
+// *snap = *src (one word): the accepted count at the start of an iteration
+static __global__ void k_snap(const int32_t* __restrict__ src, int32_t* snap) {
+  if (threadIdx.x == 0) *snap = *src;
 }
 
 template <typename T>

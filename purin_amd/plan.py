@@ -332,6 +332,37 @@ class Plan:
             _ptr(slacks), _i32(status), _i32(it), _ptr(res), _u8(fin), _u8(conv), _ptr(saved)))
         return QPOutput(y, mult, slacks, status, it, res, fin.bool(), conv.bool(), saved)
 
+    def dense_solve(self, q, c, rhs, lower, upper, *, values=None, y0=None, dual0=None,
+                    tolerance=1e-9, max_iterations=5000, early_stop=True, check_every=32,
+                    save=False):
+        """The dense adapter's forward (``purin_cp_dense_solve``, solve_dense
+        semantics) on a plan with bound_presolve, row_scaling, norm_bound and
+        diagonal_preconditioning off.  Returns (y, multipliers, iterations, saved)."""
+        batch = q.shape[0]
+        M = self.me + self.mi
+        q = self._tensor(q, (batch, self.n), "q")
+        c = self._tensor(c, (batch, self.n), "c")
+        rhs = self._tensor(rhs, (batch, M), "rhs")
+        lower = self._tensor(lower, (batch, self.n), "lower")
+        upper = self._tensor(upper, (batch, self.n), "upper")
+        values = None if values is None else self._tensor(values, (batch, self.nnz), "values")
+        y0 = None if y0 is None else self._tensor(y0, (batch, self.n), "y0")
+        dual0 = None if dual0 is None else self._tensor(dual0, (batch, M), "dual0")
+        o = _lib.default_solve_options()
+        o.tolerance = float(tolerance)
+        o.max_iterations = int(max_iterations)
+        o.early_stop = int(bool(early_stop))
+        o.check_every = int(check_every)
+        y = self._empty(batch, self.n)
+        mult = self._empty(batch, M)
+        it = self._empty(batch, dtype=torch.int32)
+        saved = self._empty(self.saved_bytes(batch), dtype=torch.uint8) if save else None
+        _lib.check(self.lib.purin_cp_dense_solve(
+            self.handle, _stream(), batch, _ptr(q), _ptr(c), _ptr(values), _ptr(rhs),
+            _ptr(lower), _ptr(upper), _ptr(y0), _ptr(dual0), C.byref(o), _ptr(y), _ptr(mult),
+            _i32(it), _ptr(saved)))
+        return y, mult, it, saved
+
     def qp_adjoint(self, saved, q, c, cot_y, *, values=None, cot_dual=None, tolerance=1e-9,
                    atol=0.0, restart=30, max_iterations=100, adjoint_tolerance=1e-8,
                    force_eligible=False):
