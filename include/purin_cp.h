@@ -338,6 +338,25 @@ int purin_cp_qp_adjoint(purin_cp_plan* plan, void* stream, int64_t batch, const 
                         void* g_c, void* g_values, void* g_rhs, void* g_lower, void* g_upper,
                         uint8_t* valid, int32_t* info, void* gmres_residual);
 
+/*
+ * The dense layer's backward (dense_implicit.py:160-210 with
+ * autodiff/fixed_point.py:8-40) at the state saved by purin_cp_dense_solve:
+ * BiCGSTAB (jax.scipy.sparse.linalg.bicgstab, jax 0.6.2) on
+ * (I - J_z^T) v = [cot_y, cot_dual, 0] over the whole batch as one vector,
+ * tolerance opts->tolerance (the reference uses 1e-6) and at most
+ * opts->max_iterations iterations (adjoint_iters, 50 there), with the step
+ * sizes and the prox inverse frozen -- so g_q is zero -- and no convergence
+ * masking.  Outputs (each may be NULL): g_q, g_c (B, n); g_values (B, nnz);
+ * g_rhs (B, me+mi); g_lower, g_upper (B, n).  purin_cp_last_adjoint_stats
+ * reports the BiCGSTAB iterations (arnoldi_steps) and its final counter
+ * (cycles: the iterations, or -10 / -11 at a breakdown).
+ */
+int purin_cp_dense_adjoint(purin_cp_plan* plan, void* stream, int64_t batch, const void* saved,
+                           const void* q, const void* c, const void* values, const void* cot_y,
+                           const void* cot_dual, const purin_cp_adjoint_options* opts, void* g_q,
+                           void* g_c, void* g_values, void* g_rhs, void* g_lower,
+                           void* g_upper);
+
 /* Work done by the last adjoint() call on this plan.  No reference counterpart
  * (the reference's GMRES returns only per-sample info codes); it reports how
  * many batched Arnoldi steps ran, which sets the adjoint's algorithmic bytes. */

@@ -38,6 +38,7 @@ SYMBOLS = (
     "purin_cp_adjoint",
     "purin_cp_adjoint_values",
     "purin_cp_qp_adjoint",
+    "purin_cp_dense_adjoint",
     "purin_cp_last_error",
     "purin_cp_build_info",
 )
@@ -183,6 +184,9 @@ def load(path: str = LIB_PATH):
                                         C.POINTER(AdjointOptions), vp, vp, vp, vp, vp, vp, u8p,
                                         i32p, vp]
     lib.purin_cp_qp_adjoint.restype = C.c_int
+    lib.purin_cp_dense_adjoint.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp,
+                                           C.POINTER(AdjointOptions), vp, vp, vp, vp, vp, vp]
+    lib.purin_cp_dense_adjoint.restype = C.c_int
     lib.purin_cp_last_error.argtypes = []
     lib.purin_cp_last_error.restype = C.c_char_p
     lib.purin_cp_build_info.argtypes = []

@@ -64,6 +64,7 @@ struct Adj {
   const T* tau_b;
   const T* tau_cb;
   T* Spre;
+  int factored;  // the dense adapter's prox arithmetic a ((y - tau t) - tau c)
   const T* Cm;   // n x Bp
   const T* Dm;   // m x Bp
   T* U;          // n x Bp scratch (u)
@@ -175,10 +176,17 @@ __global__ __launch_bounds__(kBlock) void k_lin_cols(Adj<T> S, const T* __restri
       dj[q] = adj_d(S, j, b0 + q);
     }
     V s;
-    if (S.Q) {  // offset -delta c (kernels.py:68-73)
+    if (S.Q) {  // offset -delta c (kernels.py:68-73), or the factored form (140-142)
       const V cv = vload(S.Cc + off);
 #pragma unroll
-      for (int q = 0; q < Sn; ++q) s[q] = aj[q] * y[q] - dj[q] * t[q] + (-dj[q] * cv[q]);
+      for (int q = 0; q < Sn; ++q) {
+        if (S.factored) {
+          const T tau = adj_tau(S, j, b0 + q);
+          s[q] = aj[q] * ((y[q] - tau * t[q]) - tau * cv[q]);
+        } else {
+          s[q] = aj[q] * y[q] - dj[q] * t[q] + (-dj[q] * cv[q]);
+        }
+      }
       vstore(S.Spre + off, s);
     } else {
       s = aj * y - dj * t + dj * vload(tgt + off);
@@ -864,8 +872,10 @@ __global__ void k_final_u(Adj<T> S, const T* __restrict__ lam, const T* __restri
     S.U[e] = S.dg ? a : u;
     if (S.Q) {
       const int64_t j = e / S.Bp;
-      const T g = -(adj_tau(S, j, b) * adj_a(S, j, b) * u * S.Spre[e]);
-      gq[e] = finite(g) ? g : T(0);
+      if (gq) {
+        const T g = -(adj_tau(S, j, b) * adj_a(S, j, b) * u * S.Spre[e]);
+        gq[e] = finite(g) ? g : T(0);
+      }
       gt[e] = finite(a) ? -a : T(0);
     } else {
       gt[e] = finite(a) ? a : T(0);
@@ -1021,6 +1031,107 @@ __global__ void k_copy_i32(int64_t count, const int32_t* __restrict__ src, int32
 
 static size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
+// ---------------------------------------------------------------------------
+// BiCGSTAB over the whole batch as one vector (the dense layer's
+// fixed_point_pullback, src/purin/autodiff/fixed_point.py:8-40, with
+// jax.scipy.sparse.linalg.bicgstab of jax 0.6.2: van der Vorst's BiCGSTAB,
+// rho = alpha = omega = 1 and rhat = p = q = r0 initially, the early exit
+// when |s|^2 < atol2, breakdown codes -10 (rho = 0) and -11 (alpha or
+// omega = 0), atol2 = max(tol^2 |b|^2, atol^2)).  Dot products over all
+// W x Bp entries (padding is zero) in a fixed two-level order; the scalars
+// live in the device array sc[].
+// ---------------------------------------------------------------------------
+constexpr int kBiBlocks = 1024;
+enum BiSlot { kBS = 0, kAtol2, kRho, kAlpha, kOmega, kRho_, kAlpha_, kOmega_, kBeta, kSS, kTS,
+              kTT, kRQ, kRS, kK, kSlots };
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_bi_dot(const T* __restrict__ x, const T* __restrict__ y,
+                                                int64_t total, T* part) {
+  __shared__ T buf[256];
+  T acc = T(0);
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x)
+    acc += x[e] * y[e];
+  buf[threadIdx.x] = acc;
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if ((int)threadIdx.x < h) buf[threadIdx.x] += buf[threadIdx.x + h];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = buf[0];
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_bi_sum(const T* __restrict__ part, int np, T* sc,
+                                                int slot) {
+  __shared__ T buf[256];
+  T acc = T(0);
+  for (int i = threadIdx.x; i < np; i += blockDim.x) acc += part[i];
+  buf[threadIdx.x] = acc;
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if ((int)threadIdx.x < h) buf[threadIdx.x] += buf[threadIdx.x + h];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) sc[slot] = buf[0];
+}
+
+// op: 0 start (atol2, rho = alpha = omega = 1, k = 0), 1 beta, 2 alpha_, 3 omega_,
+// 4 the iteration's end (k, and rho/alpha/omega <- the new values)
+template <typename T>
+__global__ void k_bi_scalar(T* sc, int op, T tol, T atol) {
+  if (threadIdx.x != 0) return;
+  const T one = T(1);
+  if (op == 0) {
+    sc[kAtol2] = maxp(tol * tol * sc[kBS], atol * atol);
+    sc[kRho] = sc[kAlpha] = sc[kOmega] = one;
+    sc[kK] = T(0);
+  } else if (op == 1) {
+    sc[kBeta] = sc[kRho_] / sc[kRho] * sc[kAlpha] / sc[kOmega];
+  } else if (op == 2) {
+    sc[kAlpha_] = sc[kRho_] / sc[kRQ];
+  } else if (op == 3) {
+    sc[kOmega_] = sc[kTS] / sc[kTT];
+  } else {
+    T k = (sc[kOmega_] == T(0) || sc[kAlpha_] == T(0)) ? T(-11) : sc[kK] + one;
+    if (sc[kRho_] == T(0)) k = T(-10);
+    sc[kK] = k;
+    sc[kRho] = sc[kRho_];
+    sc[kAlpha] = sc[kAlpha_];
+    sc[kOmega] = sc[kOmega_];
+  }
+}
+
+// mode 0: p = r + beta (p - omega q); 1: s = r - alpha_ q;
+// 2: x, r update with the early exit
+template <typename T>
+__global__ void k_bi_vec(int mode, int64_t total, const T* __restrict__ sc, T* x, T* r, T* p,
+                         const T* __restrict__ q, T* s, const T* __restrict__ t) {
+  const T beta = sc[kBeta], omega = sc[kOmega], alpha_ = sc[kAlpha_], omega_ = sc[kOmega_];
+  const bool early = sc[kSS] < sc[kAtol2];
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    if (mode == 0) {
+      p[e] = r[e] + beta * (p[e] - omega * q[e]);
+    } else if (mode == 1) {
+      s[e] = r[e] - alpha_ * q[e];
+    } else if (early) {
+      x[e] = x[e] + alpha_ * p[e];
+      r[e] = s[e];
+    } else {
+      x[e] = x[e] + (alpha_ * p[e] + omega_ * s[e]);
+      r[e] = s[e] - omega_ * t[e];
+    }
+  }
+}
+
+template <typename T>
+__global__ void k_fill_weights(int64_t batch, int64_t Bp, T* w) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < Bp) w[b] = b < batch ? T(1) : T(0);
+}
+
 // Inputs and extra outputs of the general diagonal QP's VJP (diagonal_qp.py:131-219).
 template <typename T>
 struct QPAdjArgs {
@@ -1028,6 +1139,9 @@ struct QPAdjArgs {
   const T* c;         // (B, n)
   const T* cot_dual;  // (B, M) cotangent of the multipliers, or nullptr
   T* g_q;             // (B, n) or nullptr
+  int dense;          // the dense layer's backward (dense_implicit.py:198-209):
+                      // BiCGSTAB over the batch, frozen prox (no q gradient),
+                      // no convergence masking
 };
 
 template <typename T>
@@ -1047,7 +1161,10 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   const Layout L = make_layout(p, batch);
   const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
   const int64_t W = 2 * n + m;
-  const int restart = (int)std::min<int64_t>({(int64_t)o.restart, (int64_t)o.max_iterations, W});
+  // the dense layer's BiCGSTAB keeps its five work vectors in the basis slots
+  const int restart = (qa && qa->dense)
+                          ? 5
+                          : (int)std::min<int64_t>({(int64_t)o.restart, (int64_t)o.max_iterations, W});
   if (restart > kMaxRestart) return set_error(PURIN_CP_ERR_UNSUPPORTED, "restart above 128");
   static_assert((kMaxRestart + 2) * 4 <= kPinnedBytes, "per-step counts must fit the pinned buffer");
   // header written by the forward call
@@ -1059,10 +1176,13 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     return set_error(PURIN_CP_ERR_ARG, "saved state does not belong to this plan and batch");
   const int kind = (int)hdr[3];
   const int shared = (int)hdr[4];
-  if (qa ? kind != 3 : kind == 3)
-    return set_error(PURIN_CP_ERR_ARG, qa ? "saved state is not from purin_cp_qp_solve"
-                                          : "saved state is from purin_cp_qp_solve: use "
-                                            "purin_cp_qp_adjoint");
+  const bool dense = qa && qa->dense;
+  if (dense ? kind != 4 : (qa ? kind != 3 : kind >= 3))
+    return set_error(PURIN_CP_ERR_ARG,
+                     dense ? "saved state is not from purin_cp_dense_solve"
+                           : (qa ? "saved state is not from purin_cp_qp_solve"
+                                 : "saved state is from purin_cp_qp_solve or purin_cp_dense_solve: "
+                                   "use purin_cp_qp_adjoint or purin_cp_dense_adjoint"));
   if (!qa && per_sample != (kind == 2))
     return set_error(PURIN_CP_ERR_ARG, per_sample
                                            ? "saved state is not from purin_cp_project_values"
@@ -1119,6 +1239,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   const size_t oPS = per_sample ? take(Lv.ws_end) : 0;
   const size_t oSw = per_sample ? take(m * Bp * es) : 0;
   const size_t oGV = per_sample ? take((size_t)p->nnz_full * Bp * es) : 0;
+  const size_t oBi = (qa && qa->dense) ? take((size_t)(kBiBlocks + kSlots) * es) : 0;
   const size_t oSp = qa ? take(n * Bp * es) : 0;    // pre-clip values (q gradient)
   const size_t oGq = qa ? take(n * Bp * es) : 0;    // g_q
   const size_t oCd = (qa && qa->cot_dual) ? take((size_t)std::max<int64_t>(M, 1) * Bp * es) : 0;
@@ -1173,6 +1294,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     S.Q = QQ;
     S.Cc = QC;
     S.Spre = (T*)(ws + oSp);
+    S.factored = qa->dense;
     if (p->diag) {
       S.tau_cb = PS.tau_cb;
       S.sig_rb = PS.sig_rb;
@@ -1319,7 +1441,60 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     k_prep_rows<T><<<2048, 256, 0, st>>>((int)m, Bp, p->dkept, (const T*)p->dscale, PS.SC, CD,
                                          nullptr, cotd, nullptr);
   }
-  k_gm_rhs<T><<<eb, 256, 0, st>>>(n, m, W, Bp, batch, T1, cotd, conv, o.force_eligible, Gr);
+  k_gm_rhs<T><<<eb, 256, 0, st>>>(n, m, W, Bp, batch, T1, cotd, conv,
+                                  dense ? 1 : o.force_eligible, Gr);
+  T* lam_w = (T*)(ws + oLw);
+  p->adjoint_stats = purin_cp_adjoint_stats{};
+  if (dense) {
+    // BiCGSTAB on (I - J^T) v = g over the whole batch (fixed_point.py:8-40)
+    T* bpart = (T*)(ws + oBi);
+    T* bsc = bpart + kBiBlocks;
+    T* RH = Vb;
+    T* Pv = Vb + vstride;
+    T* Qv = Vb + 2 * vstride;
+    T* Sv = Vb + 3 * vstride;
+    T* Tv = Vb + 4 * vstride;
+    auto dot = [&](const T* x, const T* y, int slot) {
+      k_bi_dot<T><<<kBiBlocks, 256, 0, st>>>(x, y, total, bpart);
+      k_bi_sum<T><<<1, 256, 0, st>>>(bpart, kBiBlocks, bsc, slot);
+    };
+    auto bi_vec = [&](int mode) {
+      k_bi_vec<T><<<eb, 256, 0, st>>>(mode, total, bsc, X, Rr, Pv, Qv, Sv, Tv);
+    };
+    dot(Gr, Gr, kBS);
+    k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 0, (T)o.tolerance, (T)o.atol);
+    k_fill<T><<<eb, 256, 0, st>>>(X, total, T(0));
+    // r0 = b - A(0) = b; rhat = p = q = r0
+    for (T* dst : {Rr, RH, Pv, Qv})
+      PURIN_HIP(hipMemcpyAsync(dst, Gr, vec, hipMemcpyDeviceToDevice, st));
+    int64_t iters = 0;
+    T* host = (T*)p->pinned;
+    for (;;) {
+      dot(Rr, Rr, kRS);
+      PURIN_HIP(hipMemcpyAsync(host, bsc, kSlots * sizeof(T), hipMemcpyDeviceToHost, st));
+      PURIN_HIP(hipStreamSynchronize(st));
+      const T rs = host[kRS], atol2 = host[kAtol2], kk = host[kK];
+      if (!(rs > atol2 && kk < (T)o.max_iterations && kk >= T(0))) break;
+      dot(RH, Rr, kRho_);
+      k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 1, T(0), T(0));
+      bi_vec(0);
+      op(Pv, Qv);
+      dot(RH, Qv, kRQ);
+      k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 2, T(0), T(0));
+      bi_vec(1);
+      dot(Sv, Sv, kSS);
+      op(Sv, Tv);
+      dot(Tv, Sv, kTS);
+      dot(Tv, Tv, kTT);
+      k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 3, T(0), T(0));
+      bi_vec(2);
+      k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 4, T(0), T(0));
+      ++iters;
+    }
+    p->adjoint_stats.arnoldi_steps = iters;
+    p->adjoint_stats.cycles = (int32_t)host[kK];  // iterations, or -10 / -11 at breakdown
+    k_fill_weights<T><<<sb, 256, 0, st>>>(batch, Bp, lam_w);
+  } else {
   // threshold = max(atol, tol * max|g|) and residual_inf = max|g - A 0| = max|g|
   k_gs<T, 4><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Gr, nullptr, W, Bp, part, nchunk);
   reduce(1, S1, 1);
@@ -1328,7 +1503,6 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   PURIN_HIP(hipMemcpyAsync(Rr, Gr, vec, hipMemcpyDeviceToDevice, st));  // r = g - A(0)
 
   int64_t completed = 0;
-  p->adjoint_stats = purin_cp_adjoint_stats{};
   while (completed < o.max_iterations) {
     zero_counters();
     k_gm_count_unconverged<T><<<sb, 256, 0, st>>>(G);
@@ -1404,18 +1578,23 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   // finiteness of the solution, info, valid (operators.py:1119-1122, bounds.py:148-153)
   k_gs<T, 2><<<ggs, kBlock, 0, st>>>(Vb, vstride, 0, X, nullptr, W, Bp, part, nchunk);
   k_reduce<T><<<sb, 256, 0, st>>>(part + (size_t)nchunk * Bp, 1, nchunk, Bp, S2, 2);
-  T* lam_w = (T*)(ws + oLw);
   k_gm_finish<T><<<sb, 256, 0, st>>>(G, S2, conv, (T)o.adjoint_tolerance, o.force_eligible,
                                      lam_w, valid, info, gres);
+  }
   // final pullback of the masked lambda
   T* gt = (T*)(ws + oGt);
   T* glo = (T*)(ws + oGlo);
   T* ghi = (T*)(ws + oGhi);
   T* gr = (T*)(ws + oGr);
-  T* gq = qa ? (T*)(ws + oGq) : nullptr;
+  T* gq = (qa && !dense) ? (T*)(ws + oGq) : nullptr;  // the dense layer's prox is frozen
   k_final_u<T><<<eb, 256, 0, st>>>(S, X, lam_w, (const T*)(ws + oClo), (const T*)(ws + oChi), gt,
                                    glo, ghi, gq);
-  if (qa && qa->g_q) to_major<T>(st, gq, Bp, n, qa->g_q, batch, n, nullptr, 0);
+  if (qa && qa->g_q) {
+    if (gq)
+      to_major<T>(st, gq, Bp, n, qa->g_q, batch, n, nullptr, 0);
+    else
+      k_fill<T><<<eb, 256, 0, st>>>(qa->g_q, batch * n, T(0));
+  }
   T* sw = per_sample ? (T*)(ws + oSw) : nullptr;
   if (m) k_final_w<T><<<grow, kBlock, 0, st>>>(S, X, lam_w, gr, sw);
   if (g_target) to_major<T>(st, gt, Bp, n, g_target, batch, n, metric, metric ? 1 : 0);
@@ -1446,6 +1625,32 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
 
 using namespace purin;
 
+extern "C" int purin_cp_dense_adjoint(purin_cp_plan* p, void* stream, int64_t batch,
+                                      const void* saved, const void* q, const void* c,
+                                      const void* values, const void* cot_y,
+                                      const void* cot_dual, const purin_cp_adjoint_options* opts,
+                                      void* g_q, void* g_c, void* g_values, void* g_rhs,
+                                      void* g_lower, void* g_upper) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  purin_cp_adjoint_options o;
+  purin_cp_default_adjoint_options(&o);
+  if (opts) o = *opts;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64) {
+    const QPAdjArgs<double> qa{(const double*)q, (const double*)c, (const double*)cot_dual,
+                               (double*)g_q, 1};
+    return adjoint_impl<double>(p, st, batch, saved, (const double*)cot_y, o, (double*)g_c,
+                                (double*)g_rhs, (double*)g_lower, (double*)g_upper, nullptr,
+                                nullptr, nullptr, (const double*)values, (double*)g_values, true,
+                                &qa);
+  }
+  const QPAdjArgs<float> qa{(const float*)q, (const float*)c, (const float*)cot_dual,
+                            (float*)g_q, 1};
+  return adjoint_impl<float>(p, st, batch, saved, (const float*)cot_y, o, (float*)g_c,
+                             (float*)g_rhs, (float*)g_lower, (float*)g_upper, nullptr, nullptr,
+                             nullptr, (const float*)values, (float*)g_values, true, &qa);
+}
+
 extern "C" int purin_cp_qp_adjoint(purin_cp_plan* p, void* stream, int64_t batch,
                                    const void* saved, const void* q, const void* c,
                                    const void* values, const void* cot_y, const void* cot_dual,
@@ -1459,14 +1664,14 @@ extern "C" int purin_cp_qp_adjoint(purin_cp_plan* p, void* stream, int64_t batch
   hipStream_t st = (hipStream_t)stream;
   if (p->dtype == PURIN_CP_F64) {
     const QPAdjArgs<double> qa{(const double*)q, (const double*)c, (const double*)cot_dual,
-                               (double*)g_q};
+                               (double*)g_q, 0};
     return adjoint_impl<double>(p, st, batch, saved, (const double*)cot_y, o, (double*)g_c,
                                 (double*)g_rhs, (double*)g_lower, (double*)g_upper, valid, info,
                                 (double*)gmres_residual, (const double*)values,
                                 (double*)g_values, true, &qa);
   }
   const QPAdjArgs<float> qa{(const float*)q, (const float*)c, (const float*)cot_dual,
-                            (float*)g_q};
+                            (float*)g_q, 0};
   return adjoint_impl<float>(p, st, batch, saved, (const float*)cot_y, o, (float*)g_c,
                              (float*)g_rhs, (float*)g_lower, (float*)g_upper, valid, info,
                              (float*)gmres_residual, (const float*)values, (float*)g_values, true,

@@ -363,6 +363,29 @@ class Plan:
             _i32(it), _ptr(saved)))
         return y, mult, it, saved
 
+    def dense_adjoint(self, saved, q, c, cot_y, *, values=None, cot_dual=None, tolerance=1e-6,
+                      max_iterations=50):
+        """The dense layer's backward (``purin_cp_dense_adjoint``): BiCGSTAB over the
+        batch with the frozen prox.  Returns a QPAdjointOutput (valid/info None)."""
+        batch = cot_y.shape[0]
+        M = self.me + self.mi
+        q = self._tensor(q, (batch, self.n), "q")
+        c = self._tensor(c, (batch, self.n), "c")
+        values = None if values is None else self._tensor(values, (batch, self.nnz), "values")
+        cot = self._tensor(cot_y, (batch, self.n), "cotangent")
+        cotd = None if cot_dual is None else self._tensor(cot_dual, (batch, M), "dual cotangent")
+        o = _lib.default_adjoint_options()
+        o.tolerance = float(tolerance)
+        o.max_iterations = int(max_iterations)
+        gq, gc = self._empty(batch, self.n), self._empty(batch, self.n)
+        gv = self._empty(batch, self.nnz)
+        gr = self._empty(batch, M)
+        gl, gu = self._empty(batch, self.n), self._empty(batch, self.n)
+        _lib.check(self.lib.purin_cp_dense_adjoint(
+            self.handle, _stream(), batch, _ptr(saved), _ptr(q), _ptr(c), _ptr(values), _ptr(cot),
+            _ptr(cotd), C.byref(o), _ptr(gq), _ptr(gc), _ptr(gv), _ptr(gr), _ptr(gl), _ptr(gu)))
+        return QPAdjointOutput(gq, gc, gv, gr, gl, gu, None, None, None)
+
     def qp_adjoint(self, saved, q, c, cot_y, *, values=None, cot_dual=None, tolerance=1e-9,
                    atol=0.0, restart=30, max_iterations=100, adjoint_tolerance=1e-8,
                    force_eligible=False):
