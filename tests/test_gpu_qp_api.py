@@ -120,3 +120,87 @@ def test_local_quadratic_training_protocol(torch):
     ctx = context.clone().requires_grad_(True)
     jac = torch.autograd.functional.jacobian(lambda p: prepared(anchor, p)[0], ctx)
     np.testing.assert_allclose(jac.reshape(2).cpu(), [2 / 3, 1 / 3], atol=1e-7)
+
+
+@pytest.mark.parametrize("accelerated", [False, True])
+@pytest.mark.parametrize("equilibrate", [False, True])
+def test_dense_cp_matches_analytic_equality_qp(torch, accelerated, equilibrate):
+    """Reference tests/test_dense_cp.py:20-49 through purin_amd.dense (the
+    derivative through the equilibration by torch autograd)."""
+    from purin_amd.dense import solve_dense_implicit
+
+    f64 = dict(dtype=torch.float64, device="cuda")
+    q = torch.tensor([[2.0, 4.0]], **f64)
+    c = torch.tensor([[-2.0, -4.0]], **f64)
+    A = torch.ones((1, 1, 2), **f64)
+    b = torch.ones((1, 1), **f64)
+    C = torch.tensor([[[-1.0, 0.0]]], **f64)
+    d = torch.zeros((1, 1), **f64)
+    lo = torch.zeros((1, 2), **f64)
+    hi = torch.ones((1, 2), **f64) * 2
+    kw = dict(accelerated=accelerated, equilibrate=equilibrate, tolerance=1e-13,
+              max_iterations=20000)
+    actual = solve_dense_implicit(q, c, A, b, C, d, lo, hi, **kw)
+    np.testing.assert_allclose(actual[0].detach().cpu(), [[1 / 3, 2 / 3]], atol=1e-6)
+    warm = solve_dense_implicit(q, c, A, b, C, d, lo, hi, y0=actual[0], lambda0=actual[1],
+                                mu0=actual[2], **kw)
+    np.testing.assert_allclose(warm[0].detach().cpu(), actual[0].detach().cpu(), atol=1e-6)
+    derivative = torch.autograd.functional.jacobian(
+        lambda lin: solve_dense_implicit(q, lin, A, b, C, d, lo, hi, **kw)[0], c)
+    expected = -np.diag([0.5, 0.25]) + np.outer([0.5, 0.25], [0.5, 0.25]) / 0.75
+    np.testing.assert_allclose(derivative[0, :, 0, :].cpu(), expected, atol=1e-6)
+
+
+def test_dense_empty_constraints(torch):
+    """Reference tests/test_dense_cp.py:52-73."""
+    from purin_amd.dense import solve_dense_implicit
+
+    f64 = dict(dtype=torch.float64, device="cuda")
+    y = solve_dense_implicit(torch.ones((1, 2), **f64), torch.tensor([[-1.0, -2.0]], **f64),
+                             torch.zeros((1, 0, 2), **f64), torch.zeros((1, 0), **f64),
+                             torch.zeros((1, 0, 2), **f64), torch.zeros((1, 0), **f64),
+                             torch.zeros((1, 2), **f64), torch.ones((1, 2), **f64) * 3,
+                             equilibrate=True, tolerance=1e-14)[0]
+    np.testing.assert_allclose(y.cpu(), [[1.0, 2.0]], atol=1e-6)
+
+
+def test_dense_packed_support_and_gradients(torch):
+    """inequality_support (sparse_layer.py:44-122) gives the same solution as the
+    dense rows with those entries; gradients against central differences."""
+    from purin_amd.dense import solve_dense_implicit
+
+    f64 = dict(dtype=torch.float64, device="cuda")
+    rng = np.random.default_rng(8)
+    n = 4
+    q = torch.tensor(rng.uniform(1, 2, (1, n)), **f64)
+    c = torch.tensor(rng.normal(size=(1, n)), **f64)
+    A = torch.tensor(rng.normal(size=(1, 1, n)), **f64)
+    b = torch.tensor([[0.2]], **f64)
+    support = ((0, 2), (1, 3))
+    C = torch.zeros((1, 2, n), **f64)
+    C[0, 0, [0, 2]] = torch.tensor([1.0, -0.5], **f64)
+    C[0, 1, [1, 3]] = torch.tensor([0.7, 1.2], **f64)
+    d = torch.tensor([[0.1, 0.05]], **f64)
+    lo, hi = -torch.ones((1, n), **f64), torch.ones((1, n), **f64)
+    kw = dict(tolerance=1e-12, max_iterations=50000, adjoint_iterations=500)
+    dense = solve_dense_implicit(q, c, A, b, C, d, lo, hi, **kw)
+    packed = solve_dense_implicit(q, c, A, b, C, d, lo, hi, inequality_support=support, **kw)
+    np.testing.assert_allclose(packed[0].detach().cpu(), dense[0].detach().cpu(), atol=1e-9)
+    w = torch.tensor(rng.normal(size=(1, n)), **f64)
+    cc = c.clone().requires_grad_(True)
+    dd = d.clone().requires_grad_(True)
+    (solve_dense_implicit(q, cc, A, b, C, dd, lo, hi, inequality_support=support, **kw)[0]
+     * w).sum().backward()
+    h = 1e-6
+    for x, g in ((c, cc.grad), (d, dd.grad)):
+        for j in range(x.shape[1]):
+            up, dn = x.clone(), x.clone()
+            up[0, j] += h
+            dn[0, j] -= h
+            args_up = (up, d) if x is c else (c, up)
+            args_dn = (dn, d) if x is c else (c, dn)
+            f = lambda cv, dv: float((solve_dense_implicit(q, cv, A, b, C, dv, lo, hi,
+                                                           inequality_support=support, **kw)[0]
+                                      * w).sum())
+            want = (f(*args_up) - f(*args_dn)) / (2 * h)
+            assert abs(float(g[0, j]) - want) <= 1e-5, (j, float(g[0, j]), want)
