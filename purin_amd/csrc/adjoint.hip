@@ -250,6 +250,7 @@ __global__ __launch_bounds__(kBlock) void k_op_rows(Adj<T> S, const T* __restric
     const int i = rb * 4 + wave;
     if (i >= S.m) continue;
     V acc = vsplat<T>(T(0));
+#pragma unroll 4
     for (int k = S.K.rptr[i]; k < S.K.rptr[i + 1]; ++k)
       acc += row_coef(S.K, k, b0) * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
     const size_t off = (size_t)i * S.Bp + b0;

@@ -147,6 +147,8 @@ __global__ __launch_bounds__(kBlock) void k_row_pass(Iter<T> A) {
     if (i >= A.K.m) continue;
     const int s0 = A.K.rptr[i], s1 = A.K.rptr[i + 1];
     V acc = vsplat<T>(T(0));
+    // unrolled: four independent gathers in flight per wave (rows are short)
+#pragma unroll 4
     for (int k = s0; k < s1; ++k) {
       const V x = vload(A.YB + (size_t)A.K.ridx[k] * A.Bp + b0);
       acc += row_coef(A.K, k, b0) * x;
@@ -325,6 +327,7 @@ __global__ __launch_bounds__(kBlock) void k_res_pass(Iter<T> A) {
       if (i >= A.K.m) break;
       const int s0 = A.K.rptr[i], s1 = A.K.rptr[i + 1];
       V acc = vsplat<T>(zero);
+#pragma unroll 4
       for (int k = s0; k < s1; ++k)
         acc += row_coef(A.K, k, b0) * vload(A.Y + (size_t)A.K.ridx[k] * A.Bp + b0);
       const size_t off = (size_t)i * A.Bp + b0;
