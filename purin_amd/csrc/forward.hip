@@ -748,7 +748,7 @@ static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T
   if (m)
     k_post_rows<T, kRowsPerWaveEarly><<<tile_grid(Bp, TS, L.nrb), kBlock, 0, st>>>(P);
   k_post_cols<T, kRowsPerWaveEarly><<<tile_grid(Bp, TS, L.ncb), kBlock, 0, st>>>(P);
-  k_post_final<T><<<(unsigned)((batch + 255) / 256), 256, 0, st>>>(
+  k_post_final<T><<<(unsigned)(Bp / 64), 64 * kDecideGroups, 0, st>>>(
       P, batch, (T)tol_cfg, (T)factor, (const int32_t*)(sv + L.conv), (const T*)(ws + L.ogap),
       (const int32_t*)(ws + L.count), status, iterations, residual, finite_out, eligible);
   if (y) to_major<T>(st, (const T*)(sv + L.Y), Bp, n, y, batch, n, metric, metric ? 2 : 0);
@@ -859,7 +859,7 @@ static int qp_solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const 
   if (m)
     k_post_rows<T, kRowsPerWaveEarly><<<tile_grid(Bp, TS, L.nrb), kBlock, 0, st>>>(P);
   k_post_cols<T, kRowsPerWaveEarly><<<tile_grid(Bp, TS, L.ncb), kBlock, 0, st>>>(P);
-  k_post_final<T><<<(unsigned)((batch + 255) / 256), 256, 0, st>>>(
+  k_post_final<T><<<(unsigned)(Bp / 64), 64 * kDecideGroups, 0, st>>>(
       P, batch, (T)o.tolerance, T(1), (const int32_t*)(sv + L.conv), (const T*)(ws + L.ogap),
       (const int32_t*)(ws + L.count), status, iterations, residual, finite_out, converged_out);
   if (y) to_major<T>(st, (const T*)(sv + L.Y), Bp, n, y, batch, n, nullptr, 0);

@@ -200,30 +200,50 @@ __global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
   }
 }
 
-// Per-sample verdict (bounds.py:285-305).
+// Per-sample verdict (bounds.py:285-305).  A block of kDecideGroups x 64
+// threads owns 64 samples: group g takes the row and column chunks c = g,
+// g + G, ...; the groups combine in LDS (max and "and": order-independent).
+// Grid: Bp / 64 blocks.
 template <typename T>
-__global__ void k_post_final(Post<T> P, int64_t batch, T tol_cfg, T residual_factor,
-                             const int32_t* __restrict__ cp_conv, const T* __restrict__ cp_gap,
-                             const int32_t* __restrict__ count, int32_t* status,
-                             int32_t* iterations, T* residual_out, uint8_t* finite_out,
-                             uint8_t* eligible_out) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= batch) return;
+__global__ __launch_bounds__(64 * kDecideGroups) void k_post_final(
+    Post<T> P, int64_t batch, T tol_cfg, T residual_factor, const int32_t* __restrict__ cp_conv,
+    const T* __restrict__ cp_gap, const int32_t* __restrict__ count, int32_t* status,
+    int32_t* iterations, T* residual_out, uint8_t* finite_out, uint8_t* eligible_out) {
+  constexpr int G = kDecideGroups;
+  __shared__ T buf[G][64];
+  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t b = (int64_t)blockIdx.x * 64 + lane;  // < Bp by the grid
   const T zero = T(0);
-  T res = zero, stat = zero;
-  bool fin = true;
-  for (int r = 0; r < P.nrb; ++r) {
+  T q[3] = {zero, zero, T(1)};  // residual, stationarity, finite
+  for (int r = g; r < P.nrb; r += G) {
     const T* p = P.rowpart + (size_t)r * P.Bp + b;
-    res = maxp(res, p[0]);
-    fin = fin && p[(size_t)P.nrb * P.Bp] != zero;
+    q[0] = maxp(q[0], p[0]);
+    if (p[(size_t)P.nrb * P.Bp] == zero) q[2] = zero;
   }
-  for (int c = 0; c < P.ncb; ++c) {
+  const size_t plane = (size_t)P.ncb * P.Bp;
+  for (int c = g; c < P.ncb; c += G) {
     const T* p = P.colpart + (size_t)c * P.Bp + b;
-    const size_t plane = (size_t)P.ncb * P.Bp;
-    res = maxp(res, p[0]);
-    stat = maxp(stat, p[plane]);
-    fin = fin && p[2 * plane] != zero;
+    q[0] = maxp(q[0], p[0]);
+    q[1] = maxp(q[1], p[plane]);
+    if (p[2 * plane] == zero) q[2] = zero;
   }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    buf[g][lane] = q[k];
+    __syncthreads();
+    if (g == 0) {
+      T v = buf[0][lane];
+      for (int h = 1; h < G; ++h) {
+        const T o = buf[h][lane];
+        v = k < 2 ? maxp(v, o) : ((v != zero && o != zero) ? T(1) : zero);
+      }
+      q[k] = v;
+    }
+    __syncthreads();
+  }
+  if (g != 0 || b >= batch) return;
+  const T res = q[0], stat = q[1];
+  const bool fin = q[2] != zero;
   const T residual = maxp(res, stat);
   // the QP's finiteness omits the gap (diagonal_qp.py:291-295)
   const bool f = fin && finite(residual) && (P.Q || finite(cp_gap[b]));
