@@ -163,6 +163,127 @@ def adjoint_streamed_bytes(batch, ws, n, m, steps, restart):
     return batch * ws * W * total
 
 
+MODES = {
+    "values": "CP projections/sec with per-sample coefficients (config2 rows, values (B, nnz) "
+              "per sample, batch 1024, fp64) + achieved HBM GB/s % of peak",
+    "qp": "diagonal-QP solves/sec (config2 general rows, box [-1,1], per-sample q, c, batch "
+          "1024, fp64) + achieved HBM GB/s % of peak",
+    "dense": "dense-adapter solves/sec (n=256, 32 eq + 96 ineq dense rows per sample, batch "
+             "4096, fp64) + achieved HBM GB/s % of peak",
+}
+
+
+def run_mode(args, torch):
+    """The widened paths on config2-sized data: per-sample coefficients
+    (purin_cp_project_values), the general diagonal QP (purin_cp_qp_solve) and the
+    dense adapter (purin_cp_dense_solve).  Streaming passes; the roofline is the
+    dominant pass with its algorithmic bytes, which include the per-sample
+    coefficients each pass reads (B * ws * nnz)."""
+    from purin_amd import workloads
+    from purin_amd.plan import Plan
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(7)
+    ws = 8
+    if args.mode in ("values", "qp"):
+        w = workloads.config2(args.batch or 1024)
+        iters = args.iterations or w.iterations
+        B = w.target.shape[0]
+        if args.mode == "values":
+            plan = Plan(w.n, w.me, w.rows_total - w.me, w.indptr, w.indices, w.data,
+                        dtype=torch.float64, accelerated=True, device="cuda:0")
+            scale = 1.0 + 0.1 * rng.uniform(-1.0, 1.0, (B, w.indptr[-1]))
+            values = torch.as_tensor(w.data[None, :] * scale, device=dev)
+            target = torch.as_tensor(w.target, device=dev)
+            rhs = torch.as_tensor(np.tile(w.rhs, (B, 1)), device=dev)
+            kw = dict(max_iterations=iters, early_stop=False)
+            call = lambda timing=False: plan.project(target, rhs, values=values, timing=timing,
+                                                     **kw)
+            extra_n = 0
+        else:
+            general = w.me + int(w.info["mi_general"])
+            indptr = w.indptr[:general + 1]
+            nnz = int(indptr[-1])
+            plan = Plan(w.n, w.me, general - w.me, indptr, w.indices[:nnz], w.data[:nnz],
+                        dtype=torch.float64, accelerated=True, bound_presolve=False,
+                        device="cuda:0")
+            q = torch.as_tensor(rng.uniform(0.5, 2.0, (B, w.n)), device=dev)
+            c = -q * torch.as_tensor(w.target, device=dev)
+            rhs = torch.as_tensor(np.tile(w.rhs[:general], (B, 1)), device=dev)
+            lo = torch.full((B, w.n), -1.0, dtype=torch.float64, device=dev)
+            hi = torch.full((B, w.n), 1.0, dtype=torch.float64, device=dev)
+            call = lambda timing=False: plan.qp_solve(q, c, rhs, lo, hi, max_iterations=iters,
+                                                      early_stop=False, timing=timing)
+            extra_n = 1  # q and c replace the candidates: one more n-vector per iteration
+        n, m, nnz = w.n, plan.m, int(plan.info.nnz_kept)
+        workload = {"values": "config2 rows and sparsity, per-sample values = shared values x "
+                              "(1 + 0.1 U(-1,1)) (seed 7), batch 1024, fp64, accelerated CP, "
+                              f"{iters} fixed iterations, full projection",
+                    "qp": "config2's 3072 general rows (shared coefficients, read per sample), "
+                          "box [-1,1], q ~ U(0.5,2), c = -q yhat (seed 7), batch 1024, fp64, "
+                          f"accelerated CP, {iters} fixed iterations"}[args.mode]
+    else:
+        B = args.batch or 4096
+        n, me, mi = 256, 32, 96
+        iters = args.iterations or 500
+        A = rng.normal(size=(B, me, n))
+        C = rng.normal(size=(B, mi, n))
+        x0 = rng.uniform(-0.3, 0.3, (B, n))
+        b = np.einsum("bmn,bn->bm", A, x0)
+        d = np.einsum("bmn,bn->bm", C, x0) + rng.uniform(0.1, 1.0, (B, mi))
+        rows = [list(range(n))] * (me + mi)
+        indptr = np.zeros(me + mi + 1, np.int64)
+        indptr[1:] = np.cumsum([n] * (me + mi))
+        plan = Plan(n, me, mi, indptr, np.tile(np.arange(n, dtype=np.int32), me + mi),
+                    np.ones(indptr[-1]), dtype=torch.float64, bound_presolve=False,
+                    row_scaling=False, norm_bound=False, device="cuda:0")
+        values = torch.as_tensor(np.concatenate((A, C), axis=1).reshape(B, -1), device=dev)
+        q = torch.as_tensor(rng.uniform(0.5, 2.0, (B, n)), device=dev)
+        c = torch.as_tensor(rng.normal(size=(B, n)), device=dev)
+        rhs = torch.as_tensor(np.concatenate((b, d), axis=1), device=dev)
+        lo = torch.full((B, n), -1.0, dtype=torch.float64, device=dev)
+        hi = torch.full((B, n), 1.0, dtype=torch.float64, device=dev)
+        call = lambda timing=False: plan.dense_solve(q, c, rhs, lo, hi, values=values,
+                                                     max_iterations=iters, early_stop=False,
+                                                     timing=timing)
+        m, nnz, extra_n = me + mi, int(indptr[-1]), 1
+        workload = (f"dense adapter: n={n}, {me} eq + {mi} ineq dense rows per sample N(0,1), "
+                    f"feasible rhs, box [-1,1], q ~ U(0.5,2), c ~ N(0,1) (seed 7), batch {B}, "
+                    f"fp64, fixed-step CP, {iters} fixed iterations")
+    for _ in range(args.warmup):
+        call()
+    ms_per_step, _ = time_calls(torch, call, args.steps)
+    call(True)
+    torch.cuda.synchronize()
+    tm = plan.last_timing()
+    it = max(int(tm["iterations"]), 1)
+    row_ms, col_ms = tm["row_ms"] / it, tm["col_ms"] / it
+    bytes_row = B * ws * (n + 3 * m + nnz)                # gather ybar, d, r, d+ and the row entries
+    bytes_col = B * ws * ((4 + extra_n) * n + m + nnz)    # y, yhat (or q, c), writes, gather d+, entries
+    dominant = "k_col_pass" if col_ms >= row_ms else "k_row_pass"
+    dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == "k_col_pass" else (bytes_row, row_ms)
+    achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+    bytes_iter = B * ws * ((5 + extra_n) * n + 3 * m + 2 * nnz)
+    iter_ms = tm["loop_ms"] / it
+    line = {
+        "metric": MODES[args.mode], "value": B / (ms_per_step / 1e3),
+        "unit": "solves/s" if args.mode != "values" else "projections/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+        "data": "synthetic (numpy default_rng)",
+        "config": {"workload": workload, "n": n, "rows": m, "nnz": nnz, "batch": B,
+                   "iterations": iters, "parallelism": "1 GPU (batch-parallel)"},
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None, "bytes_per_launch": dom_bytes, "avg_launch_ms": dom_ms},
+        "iteration": {"row_pass_ms": row_ms, "col_pass_ms": col_ms, "iteration_ms": iter_ms,
+                      "algorithmic_bytes": bytes_iter,
+                      "achieved_GBs": bytes_iter / (iter_ms / 1e3) / 1e9,
+                      "frac_of_hbm_peak": bytes_iter / (iter_ms / 1e3) / 1e9 / HBM_PEAK_GBS},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def time_calls(torch, fn, count):
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
@@ -182,6 +303,9 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
+    ap.add_argument("--mode", default="project", choices=("project", "values", "qp", "dense"),
+                    help="project: the headline (default); values / qp / dense: the widened "
+                         "paths (per-sample coefficients, diagonal QP, dense adapter)")
     ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--iterations", type=int, default=None)
     ap.add_argument("--cpu-samples", type=int, default=None,
@@ -205,6 +329,10 @@ def main():
 
     if args.copy_calibration_mib:
         copy_calibration(torch, args.copy_calibration_mib)
+        return
+
+    if args.mode != "project":
+        run_mode(args, torch)
         return
 
     from purin_amd import workloads

@@ -334,7 +334,7 @@ class Plan:
 
     def dense_solve(self, q, c, rhs, lower, upper, *, values=None, y0=None, dual0=None,
                     tolerance=1e-9, max_iterations=5000, early_stop=True, check_every=32,
-                    save=False):
+                    save=False, timing=False):
         """The dense adapter's forward (``purin_cp_dense_solve``, solve_dense
         semantics) on a plan with bound_presolve, row_scaling, norm_bound and
         diagonal_preconditioning off.  Returns (y, multipliers, iterations, saved)."""
@@ -353,6 +353,7 @@ class Plan:
         o.max_iterations = int(max_iterations)
         o.early_stop = int(bool(early_stop))
         o.check_every = int(check_every)
+        o.timing = int(bool(timing))
         y = self._empty(batch, self.n)
         mult = self._empty(batch, M)
         it = self._empty(batch, dtype=torch.int32)
