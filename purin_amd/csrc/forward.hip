@@ -212,8 +212,10 @@ constexpr int res_tile() {
 }
 
 template <typename T, int SLR, int SLC>
-static int launch_resident_sl(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb) {
-  auto kern = sb ? k_resident<T, SLR, SLC, true> : k_resident<T, SLR, SLC, false>;
+static int launch_resident_sl(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
+                              bool early) {
+  auto kern = early ? (sb ? k_resident_early<T, SLR, SLC, true> : k_resident_early<T, SLR, SLC, false>)
+                    : (sb ? k_resident<T, SLR, SLC, true> : k_resident<T, SLR, SLC, false>);
   PURIN_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
   kern<<<dim3((unsigned)tiles), dim3(kResThreads), lds, st>>>(R);
@@ -222,34 +224,35 @@ static int launch_resident_sl(const Res<T>& R, hipStream_t st, int64_t tiles, si
 
 template <typename T, int SLR>
 static int launch_resident_c(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
-                             bool sb) {
+                             bool sb, bool early) {
   switch (slc) {
-    case 1: return launch_resident_sl<T, SLR, 1>(R, st, tiles, lds, sb);
-    case 2: return launch_resident_sl<T, SLR, 2>(R, st, tiles, lds, sb);
-    case 3: return launch_resident_sl<T, SLR, 3>(R, st, tiles, lds, sb);
-    case 4: return launch_resident_sl<T, SLR, 4>(R, st, tiles, lds, sb);
+    case 1: return launch_resident_sl<T, SLR, 1>(R, st, tiles, lds, sb, early);
+    case 2: return launch_resident_sl<T, SLR, 2>(R, st, tiles, lds, sb, early);
+    case 3: return launch_resident_sl<T, SLR, 3>(R, st, tiles, lds, sb, early);
+    case 4: return launch_resident_sl<T, SLR, 4>(R, st, tiles, lds, sb, early);
     default: return set_error(PURIN_CP_ERR_ARG, "resident column slot count out of range");
   }
 }
 
 template <typename T>
 static int launch_resident(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slr,
-                           int slc, bool sb) {
+                           int slc, bool sb, bool early) {
   switch (slr) {
-    case 1: return launch_resident_c<T, 1>(R, st, tiles, lds, slc, sb);
-    case 2: return launch_resident_c<T, 2>(R, st, tiles, lds, slc, sb);
-    case 3: return launch_resident_c<T, 3>(R, st, tiles, lds, slc, sb);
-    case 4: return launch_resident_c<T, 4>(R, st, tiles, lds, slc, sb);
+    case 1: return launch_resident_c<T, 1>(R, st, tiles, lds, slc, sb, early);
+    case 2: return launch_resident_c<T, 2>(R, st, tiles, lds, slc, sb, early);
+    case 3: return launch_resident_c<T, 3>(R, st, tiles, lds, slc, sb, early);
+    case 4: return launch_resident_c<T, 4>(R, st, tiles, lds, slc, sb, early);
     default: return set_error(PURIN_CP_ERR_ARG, "resident row slot count out of range");
   }
 }
 
-// LDS of the resident kernel, or 0 when the problem does not fit on chip.
+// LDS of the resident kernel (the early-stop one: with its partials), or 0
+// when the problem does not fit on chip.
 template <typename T>
-static size_t resident_lds(const purin_cp_plan* p) {
+static size_t resident_lds(const purin_cp_plan* p, bool early = false) {
   if (!p->res_ok) return 0;
   // Gy (n) | zero | Gd (m) | trash, 16 bytes each
-  const size_t lds = (size_t)(p->n + 1 + p->m + 1) * 16;
+  const size_t lds = (size_t)(p->n + 1 + p->m + 1) * 16 + (early ? kResEarlyExtra : 0);
   return lds <= 160 * 1024 ? lds : 0;
 }
 
@@ -284,10 +287,13 @@ static int resident_schedule(purin_cp_plan* p, int64_t iters) {
   return PURIN_CP_OK;
 }
 
-// Fixed-iteration loop on the resident kernel; fills Y and D like the passes.
+// The CP loop on the resident kernel; fills Y and D like the passes (and, with
+// early stop, the per-sample done flags and iteration counts).
 template <typename T>
 static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char* sv, char* ws,
-                        const purin_cp_solve_options& o, size_t lds) {
+                        const purin_cp_solve_options& o, size_t lds, bool early = false,
+                        int64_t batch = 0, T tol = T(0), const T* tolv = nullptr,
+                        int32_t* done = nullptr, int32_t* count = nullptr) {
   constexpr int BT = res_tile<T>();
   const int64_t Bp = L.Bp, tiles = Bp / BT;
   const int Kr = p->res_mr * kResThreads, Kc = p->res_mc * kResThreads;
@@ -301,8 +307,13 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   R.Kc = Kc;
   R.rowmap = p->res_rowmap;
   R.colmap = p->res_colmap;
-  R.stream = p->res_stream;
-  R.wtab = p->res_wtab;
+  R.stream = early ? p->res_stream_e : p->res_stream;
+  R.wtab = early ? p->res_wtab_e : p->res_wtab;
+  R.batch = batch;
+  R.tol = tol;
+  R.tolv = tolv;
+  R.done = done;
+  R.count = count;
   T* Ts = (T*)(ws + L.RTs);
   T* Rs = (T*)(ws + L.RRs);
   T* D0s = (T*)(ws + L.RD0);
@@ -335,7 +346,7 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     PURIN_HIP(hipEventRecord(e0, st));
   }
   if (int rc = launch_resident<T>(R, st, tiles, lds, p->res_mr, p->res_mc,
-                                         o.shared_bounds != 0)) return rc;
+                                  o.shared_bounds != 0, early)) return rc;
   PURIN_HIP(hipGetLastError());
   if (o.timing) {
     PURIN_HIP(hipEventRecord(e1, st));
@@ -409,12 +420,15 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   int32_t* snap = ndone + 1;  // accepted count at the start of the iteration (no freezing)
   const int m = A.K.m, n = A.K.n;
   const bool early = o.early_stop != 0;
-  const size_t lds = resident_lds<T>(p);
+  const size_t lds = resident_lds<T>(p, early);
   // the resident kernel takes one schedule of scalar steps for the whole tile
-  if (!early && lds && !o.streaming && !p->diag && !ps && !qp) {
-    if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds)) return rc;
-    const int32_t cnt = (int32_t)o.max_iterations;
-    k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);
+  if (lds && !o.streaming && !p->diag && !ps && !qp) {
+    if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds, early, batch, tol_scalar, tolv, done,
+                                 count)) return rc;
+    if (!early) {
+      const int32_t cnt = (int32_t)o.max_iterations;
+      k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);
+    }
     A.done = nullptr;
     const dim3 gcolE0 = tile_grid(Bp, TS, L.ncb);
     const dim3 gres0 = tile_grid(Bp, TS, std::max(L.nrb, 1));

@@ -79,6 +79,12 @@ struct Res {
   int64_t iters;
   T* Y;  // n x Bp
   T* D;  // m x Bp
+  // early-stop kernel only: the per-sample stop test and its outputs
+  int64_t batch;
+  T tol;                       // tolerance, or per sample from tolv [Bp] when set
+  const T* __restrict__ tolv;
+  int32_t* done;               // [Bp] accepted (1) or not (0)
+  int32_t* count;              // [Bp] iterations committed
 };
 
 template <typename T>
@@ -300,6 +306,335 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       const V d = lds_read<V>(soff_r[r]);
 #pragma unroll
       for (int s = 0; s < BT; ++s) A.D[(int64_t)i * A.Bp + b0s + s] = d[s];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Early-stop variant (freeze_converged and the stop test of kernels.py:228-290
+// with check_stationarity, bounds.py:61-62).  The tile's samples stop
+// independently: a sample accepted at iteration k keeps the state of
+// iteration k (its later updates are masked and not counted), and the
+// workgroup returns when all its samples are accepted or the iterations run
+// out.  Per iteration:
+//   row pass      as above, masked to the active samples
+//   barrier
+//   column pass   as above, masked; Gy <- y+ (for the residual sweep), ybar+
+//                 kept in registers; column diagnostics of (y+, K^T d+):
+//                 primal, dual objective terms, max(stationarity, bound
+//                 violation), finiteness (kernels.py:153-175, 272-274)
+//   barrier
+//   residual      the row chunks again, gathering y+: max |K y+ - r| (eq) /
+//                 max(K y+ - r, 0) (ineq), r . d+, finiteness of d+; every
+//                 partial is summed within 16-lane rows by DPP and written to LDS
+//   barrier
+//   Gy <- ybar+; wavefront 0 combines the 64 row partials of each quantity in
+//                 a fixed order and applies the stop test of each sample
+//   barrier
+// The step arithmetic is the fixed kernel's (and the streaming passes'), so
+// the iterates of a sample are identical up to its stop; the diagnostics are
+// summed in another (fixed) order than the streaming stop test's.
+// LDS: the fixed kernel's, then [16 waves][4 rows][kResQ] partials and the
+// active mask.
+constexpr int kResQ = 5;  // primal, dual terms, r.d, max(res, bound, stat), finite
+constexpr uint32_t kResEarlyExtra = 16u * 4u * kResQ * 16u + 16u;
+
+// One DPP move of a 32- or 64-bit value (all lanes active, full row/bank masks).
+template <int CTRL, typename T>
+__device__ __forceinline__ T dpp_move(T v) {
+  if constexpr (sizeof(T) == 8) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const uint32_t hi =
+        (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else {
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF,
+                                                             0xF, false));
+  }
+}
+
+// Combine the 16 lanes of each DPP row; lane 0 of the row holds
+// ((q0 op q3) op (q2 op q1)) of its four quads q (each quad combined pairwise).
+template <typename T, typename Op>
+__device__ __forceinline__ T row16_combine(T v, Op op) {
+  v = op(v, dpp_move<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = op(v, dpp_move<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = op(v, dpp_move<0x124>(v));  // row_ror:4
+  v = op(v, dpp_move<0x128>(v));  // row_ror:8
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T read_lane(T v, int l) {
+  if constexpr (sizeof(T) == 8) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+  }
+}
+
+template <typename T, int SLR, int SLC, bool SB>
+__global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
+  constexpr int NT = 1024;
+  constexpr int BT = ResVec<T>::BT;
+  using V = typename ResVec<T>::V;
+  extern __shared__ __align__(16) unsigned char lds[];  // at LDS address 0 (no static LDS)
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int64_t tile = blockIdx.x;
+  const uint32_t lane16 = (uint32_t)lane * 16u;
+  const V vzero = V(T(0));
+  const T zero = T(0), half = T(0.5);
+  const uint32_t gd_off = (uint32_t)(A.n + 1) * 16u;
+  const uint32_t trash_off = (uint32_t)(A.n + 1 + A.m) * 16u;
+  const uint32_t red_off = trash_off + 16u;
+  const uint32_t flag_off = red_off + 16u * 4u * kResQ * 16u;
+
+  const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave]);
+  const uint32_t rcnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave + 1]);
+  const uint32_t ccnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave + 2]);
+
+  const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)A.Kr;
+  const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)A.Kr;
+
+  // registers: y and ybar of the thread's columns; the targets and the scaled
+  // right-hand sides are re-read each iteration (L2) to leave room for the
+  // diagnostics
+  uint32_t soff_r[SLR], soff_c[SLC];
+  V y[SLC], yb[SLC];
+  uint32_t ineq = 0, nanb = 0, rvalid = 0, cvalid = 0;
+#pragma unroll
+  for (int c = 0; c < SLC; ++c) {
+    const int j = A.colmap[c * NT + t];
+#pragma unroll
+    for (int s = 0; s < BT; ++s) {
+      const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
+      if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
+    }
+    if (j >= 0) cvalid |= 1u << c;
+    soff_c[c] = j >= 0 ? (uint32_t)j * 16u : trash_off;
+    y[c] = j >= 0 ? reinterpret_cast<const V*>(A.Ts)[tile * (int64_t)A.Kc + c * NT + t] : vzero;
+    yb[c] = y[c];  // y0 = ybar0 = yhat (kernels.py:229-231)
+    lds_write<V>(soff_c[c], y[c]);
+  }
+#pragma unroll
+  for (int r = 0; r < SLR; ++r) {
+    const int i = A.rowmap[r * NT + t];
+    if (i >= 0) rvalid |= 1u << r;
+    soff_r[r] = i >= 0 ? gd_off + (uint32_t)i * 16u : trash_off;
+    if (i >= A.me) ineq |= 1u << r;  // kept rows: equalities first
+    lds_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
+  }
+  if (t == 0) lds_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
+  // samples of the tile: the padding samples beyond the batch never run
+  const int64_t bs0 = tile * BT;
+  uint32_t act = 0;
+#pragma unroll
+  for (int s = 0; s < BT; ++s)
+    if (bs0 + s < A.batch) act |= 1u << s;
+  int32_t cnt[BT];
+#pragma unroll
+  for (int s = 0; s < BT; ++s) cnt[s] = 0;
+  __syncthreads();
+
+  constexpr uint32_t CB = res_chunk_bytes<T>();
+  Chunk<T> b0, b1;
+  load_chunk(b0, A.stream, (uint64_t)first * CB, lane16);
+
+  for (int64_t it = 0; it < A.iters && act != 0u; ++it) {
+    const __attribute__((address_space(4))) T* sc =
+        (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
+    const T sigma = sc[0], a = sc[1], delta = sc[2], theta = sc[3];
+    uint32_t pos = first + 1;
+    // the slot-ordered rhs (zero on empty slots) through an opaque base, so the
+    // loads stay inside the loop
+    typedef const __attribute__((address_space(1))) V* GV;
+    GV rb = (GV)Rs;
+    asm volatile("" : "+s"(rb));
+    // ---- row pass, masked ------------------------------------------------------
+#pragma unroll
+    for (int r = 0; r < SLR; ++r) {
+      const int nch = (int)((rcnt >> (8 * r)) & 255u);
+      const V rr = rb[r * NT + t];
+      const V dold = lds_read<V>(soff_r[r]);
+      const V acc = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      V p = dold + sigma * (acc - rr);
+      if (ineq & (1u << r)) {
+#pragma unroll
+        for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
+      }
+#pragma unroll
+      for (int s = 0; s < BT; ++s)
+        if (!(act & (1u << s))) p[s] = dold[s];
+      lds_write<V>(soff_r[r], p);
+    }
+    __syncthreads();
+    // ---- column pass, masked, with the column diagnostics --------------------------
+    V qp = vzero, qd = vzero, qm = vzero;
+    uint32_t bad = 0;  // bit s: a non-finite y+ or d+ of sample s
+#pragma unroll
+    for (int c = 0; c < SLC; ++c) {
+      const int nch = (int)((ccnt >> (8 * c)) & 255u);
+      typedef const __attribute__((address_space(1))) T* GP;
+      GP lb = (GP)A.Ls;
+      GP hb = (GP)A.Hs;
+      GP tb = (GP)A.Ts;
+      asm volatile("" : "+s"(lb), "+s"(hb), "+s"(tb));
+      V lo, hi;
+      if (SB) {
+        lo = V(lb[c * NT + t]);
+        hi = V(hb[c * NT + t]);
+      } else {
+        lo = ((GV)lb)[tile * (int64_t)A.Kc + c * NT + t];
+        hi = ((GV)hb)[tile * (int64_t)A.Kc + c * NT + t];
+      }
+      const V tg = ((GV)tb)[tile * (int64_t)A.Kc + c * NT + t];
+      const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      const V sv = a * y[c] - delta * tt + delta * tg;
+      V yn;
+      if (nanb & (1u << c)) {
+#pragma unroll
+        for (int s = 0; s < BT; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
+      } else {
+#pragma unroll
+        for (int s = 0; s < BT; ++s) yn[s] = clip_nonnan_bounds(sv[s], lo[s], hi[s]);
+      }
+      const V ybn = yn + theta * (yn - y[c]);
+#pragma unroll
+      for (int s = 0; s < BT; ++s) {
+        if (act & (1u << s)) {
+          yb[c][s] = ybn[s];
+        } else {
+          yn[s] = y[c][s];
+        }
+      }
+      if (cvalid & (1u << c)) {  // diagnostics with q = 1, c = -yhat (kernels.py:158-174, 272-274)
+#pragma unroll
+        for (int s = 0; s < BT; ++s) {
+          const T yv = yn[s], cq = -tg[s];
+          qp[s] += half * yv * yv + cq * yv;
+          const T tf = cq + tt[s];
+          const T mz = clipp(-tf, lo[s], hi[s]);
+          qd[s] += half * mz * mz + tf * mz;
+          const T g = yv - clipp(yv - ((yv + cq) + tt[s]), lo[s], hi[s]);
+          qm[s] = maxp(qm[s], absv(g));
+          qm[s] = maxp(qm[s], maxp(maxp(lo[s] - yv, zero), maxp(yv - hi[s], zero)));
+          if (!finite(yv)) bad |= 1u << s;
+        }
+      }
+      lds_write<V>(soff_c[c], yn);  // y+ for the residual sweep
+      y[c] = yn;
+    }
+    __syncthreads();
+    // ---- residual sweep (reads Gy = y+ and the thread's own Gd) ------------------
+    V qr = vzero;
+#pragma unroll
+    for (int r = 0; r < SLR; ++r) {
+      const int nch = (int)((rcnt >> (8 * r)) & 255u);
+      const V rr = rb[r * NT + t];
+      const V acc = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      const V d = lds_read<V>(soff_r[r]);
+      if (rvalid & (1u << r)) {  // kernels.py:158-166
+#pragma unroll
+        for (int s = 0; s < BT; ++s) {
+          const T e = acc[s] - rr[s];
+          qm[s] = maxp(qm[s], (ineq & (1u << r)) ? maxp(e, zero) : absv(e));
+          qr[s] += rr[s] * d[s];
+          if (!finite(d[s])) bad |= 1u << s;
+        }
+      }
+    }
+    // 16-lane row partials to LDS, [wave][row][q]; finiteness by wavefront vote
+    {
+      const uint32_t at = red_off + (uint32_t)((wave * 4 + (lane >> 4)) * kResQ) * 16u;
+      const bool lead = (lane & 15) == 0;
+      V f;
+#pragma unroll
+      for (int s = 0; s < BT; ++s) {
+        qp[s] = row16_combine(qp[s], OpAdd());
+        f[s] = __ballot((bad >> s) & 1u) ? zero : T(1);
+      }
+      if (lead) lds_write<V>(at, qp);
+#pragma unroll
+      for (int s = 0; s < BT; ++s) qd[s] = row16_combine(qd[s], OpAdd());
+      if (lead) lds_write<V>(at + 16u, qd);
+#pragma unroll
+      for (int s = 0; s < BT; ++s) qr[s] = row16_combine(qr[s], OpAdd());
+      if (lead) lds_write<V>(at + 32u, qr);
+#pragma unroll
+      for (int s = 0; s < BT; ++s) qm[s] = row16_combine(qm[s], OpMax());
+      if (lead) {
+        lds_write<V>(at + 48u, qm);
+        lds_write<V>(at + 64u, f);
+      }
+    }
+    __syncthreads();
+    // ---- ybar+ back into Gy; the stop test ---------------------------------------
+#pragma unroll
+    for (int c = 0; c < SLC; ++c) lds_write<V>(soff_c[c], yb[c]);
+#pragma unroll
+    for (int s = 0; s < BT; ++s)
+      if (act & (1u << s)) ++cnt[s];
+    if (wave == 0) {
+      // lane l holds partial (wave l / 4, row l % 4): combined within DPP
+      // rows, then the 4 rows in order
+      const uint32_t at = red_off + (uint32_t)(lane * kResQ) * 16u;
+      uint32_t accept = 0;
+#pragma unroll
+      for (int s = 0; s < BT; ++s) {
+        T tot[kResQ];
+#pragma unroll
+        for (int q = 0; q < kResQ; ++q) {
+          T x = lds_read<V>(at + 16u * (uint32_t)q)[s];
+          if (q < 3) x = row16_combine(x, OpAdd());
+          else if (q == 3) x = row16_combine(x, OpMax());
+          else x = row16_combine(x, OpMin());
+          const T r0 = read_lane(x, 0), r1 = read_lane(x, 16), r2 = read_lane(x, 32),
+                  r3 = read_lane(x, 48);
+          if (q < 3) tot[q] = ((r0 + r1) + r2) + r3;
+          else if (q == 3) tot[q] = maxp(maxp(maxp(r0, r1), r2), r3);
+          else tot[q] = minp(minp(minp(r0, r1), r2), r3);
+        }
+        // kernels.py:167-175, 260-278
+        const T tol = A.tolv ? (bs0 + s < A.batch ? A.tolv[bs0 + s] : T(0)) : A.tol;
+        const T primal = tot[0], dual_obj = tot[1] - tot[2];
+        const T gap = maxp(primal - dual_obj, zero) /
+                      maxp(T(1), maxp(absv(primal), absv(dual_obj)));
+        const bool ok = tot[4] != zero && finite(gap) && tot[3] <= tol && gap <= tol;
+        if (ok && (act & (1u << s))) accept |= 1u << s;
+      }
+      if (lane == 0) lds_write<uint32_t>(flag_off, act & ~accept);
+    }
+    __syncthreads();
+    act = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_read<uint32_t>(flag_off));
+  }
+  // ---- hand the state to the batch-minor layout ---------------------------------
+#pragma unroll
+  for (int c = 0; c < SLC; ++c) {
+    const int j = A.colmap[c * NT + t];
+    if (j >= 0)
+#pragma unroll
+      for (int s = 0; s < BT; ++s) A.Y[(int64_t)j * A.Bp + bs0 + s] = y[c][s];
+  }
+#pragma unroll
+  for (int r = 0; r < SLR; ++r) {
+    const int i = A.rowmap[r * NT + t];
+    if (i >= 0) {
+      const V d = lds_read<V>(soff_r[r]);
+#pragma unroll
+      for (int s = 0; s < BT; ++s) A.D[(int64_t)i * A.Bp + bs0 + s] = d[s];
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < BT; ++s) {
+    if (t == s) {
+      A.count[bs0 + s] = cnt[s];
+      A.done[bs0 + s] = (bs0 + s < A.batch && !(act & (1u << s))) ? 1 : 0;
     }
   }
 }

@@ -258,3 +258,51 @@ def test_resident_kernel_matches_streaming_and_oracle(dtype, accelerated):
         want = op.solve(canon, target[sub], rhs[sub], cfg, dtype=dtype)
         assert rel_err(to_np(res.y)[sub], want.y) <= bar, n
         np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_resident_early_stop_matches_streaming_and_oracle(dtype, accelerated):
+    """Early stop on the resident kernel (each workgroup stops when its samples
+    are accepted; accepted samples keep their state and count) against the
+    streaming passes and the oracle.  The step arithmetic is the same on both
+    paths, so a sample that stops at the same iteration has the same iterate
+    bit for bit; the stop tests sum the objective terms in different fixed
+    orders, so in fp32 a sample whose margin sits on the tolerance may stop
+    one iteration apart (at most 1 in 10; fp64 counts are identical)."""
+    torch = require_gpu()
+    tol = (1e-6 if dtype == np.float64 else 1e-3) if not accelerated else 1e-4
+    stopped = 0
+    for n, me, mi, width, B in ((48, 8, 20, 4, 37), (700, 100, 300, 5, 64), (1500, 300, 700, 6, 40),
+                                (4096, 1024, 2048, 8, 16)):
+        w = workloads.small_random(3 + n, n=n, me=me, mi=mi, width=width, batch=B,
+                                   accelerated=accelerated)
+        canon = canonical_from_workload(w)
+        rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+        target = w.target.astype(dtype)
+        plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
+        kw = dict(max_iterations=2000, early_stop=True, tolerance=tol, timing=True)
+        res = plan.project(target, rhs, **kw)
+        assert plan.last_timing()["resident"] == 1, n
+        st = plan.project(target, rhs, streaming=True, **kw)
+        assert plan.last_timing()["resident"] == 0
+        it_r, it_s = to_np(res.iterations), to_np(st.iterations)
+        same = it_r == it_s
+        if dtype == np.float64:
+            np.testing.assert_array_equal(it_r, it_s)
+        else:
+            assert (~same).sum() * 10 <= B, (n, it_r[~same], it_s[~same])
+            assert np.all(np.abs(it_r - it_s) <= 1)
+        np.testing.assert_array_equal(to_np(res.y)[same], to_np(st.y)[same])
+        np.testing.assert_array_equal(to_np(res.multipliers)[same], to_np(st.multipliers)[same])
+        np.testing.assert_array_equal(to_np(res.status)[same], to_np(st.status)[same])
+        stopped += int(np.sum(it_r < kw["max_iterations"]))
+        if dtype == np.float64:
+            sub = slice(0, 6)
+            cfg = op.Config(accelerated=accelerated, max_iterations=kw["max_iterations"],
+                            tolerance=tol)
+            want = op.solve(canon, target[sub], rhs[sub], cfg, dtype=dtype)
+            np.testing.assert_array_equal(it_r[sub], want.iterations)
+            np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
+            assert rel_err(to_np(res.y)[sub], want.y) <= TOL[dtype], n
+    assert stopped > 0  # the stop test fired
