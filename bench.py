@@ -149,16 +149,16 @@ def adjoint_bytes(batch, ws, width, steps, restart):
 
 def adjoint_streamed_bytes(batch, ws, n, m, steps, restart):
     """Bytes the adjoint's kernels stream by construction, in vectors of W = 2n + m
-    rows of B samples.  Per Arnoldi step with a k-vector prefix: the three
-    Gram-Schmidt passes read the prefix three times, read x three times and
-    write it twice (3k + 5), the operator moves about 4 and the normalisation 2.
+    rows of B samples.  Per Arnoldi step with a k-vector prefix: the dot pass
+    reads the prefix and the image (k + 1), the update-and-dot pass reads them
+    again and writes the next raw vector (k + 2), and the operator moves about 4.
     Per cycle: the correction reads the prefix once, and the residual,
     acceptance and norms move about 40."""
     W = 2 * n + m
     total, done = 0, 0
     while done < steps:
         length = min(restart, steps - done)
-        total += sum(3 * k + 5 + 4 + 2 for k in range(1, length + 1)) + length + 40
+        total += sum(2 * k + 3 + 4 for k in range(1, length + 1)) + length + 40
         done += length
     return batch * ws * W * total
 

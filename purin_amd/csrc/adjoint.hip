@@ -15,9 +15,12 @@
 //   g_rhs = -sigma w, g_target = delta u, g_lower = Clo G, g_upper = Chi G.
 // GMRES solves (I - J^T) lambda = [cot_y * converged, 0, 0] with the
 // reference's restart cycles, two-pass classical Gram--Schmidt, Givens
-// rotations, per-sample active masks and candidate acceptance.  The
-// Gram--Schmidt passes are batched dot/update kernels over 64-row chunks; the
-// Givens/back-substitution scalars run one thread per sample.
+// rotations, per-sample active masks and candidate acceptance.  The basis is
+// kept raw (vectors Z with an upper-triangular map to the orthonormal ones,
+// see k_gm_tri), so each Arnoldi step makes two passes over it: a read-only
+// dot pass and one update-and-dot pass that writes the next raw vector.  The
+// per-sample scalars (chunk sums, triangular products, Givens rotations,
+// back-substitution) run on the device.
 
 #include <algorithm>
 #include <cmath>
@@ -65,6 +68,7 @@ struct Adj {
   const T* tau_cb;
   T* Spre;
   int factored;  // the dense adapter's prox arithmetic a ((y - tau t) - tau c)
+  const T* vsc;  // [Bp] per-sample scale of the operator's input, or nullptr
   const T* Cm;   // n x Bp
   const T* Dm;   // m x Bp
   T* U;          // n x Bp scratch (u)
@@ -225,10 +229,18 @@ __global__ __launch_bounds__(kBlock) void k_op_cols1(Adj<T> S, const T* __restri
   const int64_t boff = (int64_t)(S.n + S.m) * S.Bp;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
-    const T gy = v[e], gb = v[boff + e];
+    int64_t j = 0, b = 0;
+    if (S.vsc || S.dg) {
+      j = e / S.Bp;
+      b = e - j * S.Bp;
+    }
+    T gy = v[e], gb = v[boff + e];
+    if (S.vsc) {
+      gy *= S.vsc[b];
+      gb *= S.vsc[b];
+    }
     const T u = S.Cm[e] * (gy + T(2) * gb);
     if (S.dg) {
-      const int64_t j = e / S.Bp, b = e - j * S.Bp;
       S.U[e] = adj_d(S, j, b) * u;
       out[e] = gy - (adj_a(S, j, b) * u - gb);
     } else {
@@ -255,7 +267,8 @@ __global__ __launch_bounds__(kBlock) void k_op_rows(Adj<T> S, const T* __restric
       acc += row_coef(S.K, k, b0) * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
     const size_t off = (size_t)i * S.Bp + b0;
     const size_t voff = (size_t)(S.n + i) * S.Bp + b0;
-    const V gd = vload(v + voff);
+    V gd = vload(v + voff);
+    if (S.vsc) gd = gd * vload(S.vsc + b0);
     if (S.dg) {
       const V w = vload(S.Dm + off) * (gd - acc);
       V sg;
@@ -286,10 +299,12 @@ __global__ __launch_bounds__(kBlock) void k_op_cols2(Adj<T> S, const T* __restri
     for (int k = S.K.cptr[j]; k < S.K.cptr[j + 1]; ++k)
       acc += col_coef(S.K, k, b0) * vload(S.Wv + (size_t)S.K.cidx[k] * S.Bp + b0);
     const size_t off = (size_t)(S.n + S.m + j) * S.Bp + b0;
+    V gb = vload(v + off);
+    if (S.vsc) gb = gb * vload(S.vsc + b0);
     if (S.dg)
-      vstore(out + off, vload(v + off) - acc);
+      vstore(out + off, gb - acc);
     else
-      vstore(out + off, vload(v + off) - S.sigma * acc);
+      vstore(out + off, gb - S.sigma * acc);
   }
 }
 
@@ -301,6 +316,7 @@ __global__ __launch_bounds__(kBlock) void k_op_cols2(Adj<T> S, const T* __restri
 // MODE 2: x <- x - sum_i h_i V_i;  part[0] = sum x^2, part[1] = finite(x)
 // MODE 3: part[0] = sum x^2                                    (norm)
 // MODE 4: part[0] = max |x|                                    (inf-norm)
+// MODE 5: MODE 1, and part[nv] = sum x^2
 template <typename T, int MODE>
 __global__ __launch_bounds__(kBlock) void k_gs(const T* __restrict__ basis, int64_t vstride,
                                                int nv, T* x, const T* __restrict__ h,
@@ -317,7 +333,7 @@ __global__ __launch_bounds__(kBlock) void k_gs(const T* __restrict__ basis, int6
 #pragma unroll
   for (int r = 0; r < kRowsPerThread; ++r)
     xr[r] = (r0 + r < W) ? vload(x + (size_t)(r0 + r) * Bp + b0) : vsplat<T>(T(0));
-  if (MODE == 1 || MODE == 2) {
+  if (MODE == 1 || MODE == 2 || MODE == 5) {
     for (int i = 0; i < nv; ++i) {
       const V hi = vload(h + (size_t)i * Bp + b0);
       const T* vi = basis + (size_t)i * vstride;
@@ -330,7 +346,7 @@ __global__ __launch_bounds__(kBlock) void k_gs(const T* __restrict__ basis, int6
       if (r0 + r < W) vstore(x + (size_t)(r0 + r) * Bp + b0, xr[r]);
   }
   const size_t plane = (size_t)nchunk * Bp;
-  if (MODE == 0 || MODE == 1) {
+  if (MODE == 0 || MODE == 1 || MODE == 5) {
     for (int i = 0; i < nv; ++i) {
       const T* vi = basis + (size_t)i * vstride;
       V acc = vsplat<T>(T(0));
@@ -339,6 +355,13 @@ __global__ __launch_bounds__(kBlock) void k_gs(const T* __restrict__ basis, int6
         if (r0 + r < W) acc += vload(vi + (size_t)(r0 + r) * Bp + b0) * xr[r];
       const V tot = block_combine<T>(acc, buf, OpAdd());
       if (wave == 0) vstore(part + (size_t)i * plane + (size_t)c * Bp + b0, tot);
+    }
+    if (MODE == 5) {
+      V acc = vsplat<T>(T(0));
+#pragma unroll
+      for (int r = 0; r < kRowsPerThread; ++r) acc += xr[r] * xr[r];
+      const V tot = block_combine<T>(acc, buf, OpAdd());
+      if (wave == 0) vstore(part + (size_t)nv * plane + (size_t)c * Bp + b0, tot);
     }
   } else if (MODE == 2 || MODE == 3) {
     V acc = vsplat<T>(T(0)), fin = vsplat<T>(T(1));
@@ -383,98 +406,53 @@ __global__ void k_reduce(const T* __restrict__ part, int nv, int nchunk, int64_t
 }
 
 // ---------------------------------------------------------------------------
-// Classical Gram--Schmidt passes over the basis prefix for nv <= NV vectors.
-//
-// A block of 4 wavefronts owns one batch tile (64 lanes x 16 bytes of samples)
-// and a contiguous range of ``rpb`` rows; each wavefront walks a quarter of it.
-// Per row a lane loads x and the prefix vectors' entries of the same row, so
-// every load is a coalesced 1 KB wavefront access and nv of them are in flight
-// per row.  Dot products accumulate in registers (one accumulator per prefix
-// vector) and are combined across the 4 wavefronts once, at the end, into
-// part[i][chunk][b].  The coefficients h (MODE 1, 2) are
-// staged in LDS once per block.
-//   MODE 0: part_i = V_i . x
-//   MODE 1: x <- x - sum_i h_i V_i;  part_i = V_i . x
-//   MODE 2: x <- x - sum_i h_i V_i;  part_0 = x . x, part_1 = finite(x)
-// The update forms sum_i h_i V_i first and subtracts it once, like the
-// reference's einsum (operators.py:845-858).
+// The dot pass part_i = V_i . x for a short prefix (nv <= NV <= 8), split by
+// rows: a block of 4 wavefronts owns one batch tile (64 lanes x 16 bytes of
+// samples) and a contiguous range of ``rpb`` rows, and each wavefront walks a
+// quarter of it.  Per row a lane loads x and the prefix vectors' entries of the
+// same row (coalesced 1 KB wavefront accesses, nv of them in flight per row).
+// The dot products accumulate in registers and are combined across the 4
+// wavefronts once, at the end (wave 0 + 1 + 2 + 3), into part[i][chunk][b].
 // ---------------------------------------------------------------------------
-template <typename T, int NV, int MODE>
-__global__ __launch_bounds__(kBlock) void k_gs_pass(const T* __restrict__ basis, int64_t vstride,
-                                                    int nv, T* x, const T* __restrict__ h,
-                                                    int64_t W, int64_t Bp, T* part, int nchunk,
-                                                    int64_t rpb) {
+template <typename T, int NV>
+__global__ __launch_bounds__(kBlock) void k_gs_dots_rows(const T* __restrict__ basis,
+                                                         int64_t vstride, int nv,
+                                                         const T* __restrict__ x, int64_t W,
+                                                         int64_t Bp, T* part, int nchunk,
+                                                         int64_t rpb) {
   using V = typename Lane<T>::V;
-  constexpr int Sn = Lane<T>::S;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Lane<T>::S;
   const int c = blockIdx.y;
-  auto ld = [](const T* p) { return vload(p); };
-  auto st = [](T* p, V v) { vstore(p, v); };
-  __shared__ V hs[(MODE == 0) ? 1 : NV][kWave];
   __shared__ V cb[3][kWave];
-  if (MODE != 0) {
-    for (int i = wave; i < nv; i += 4) hs[i][lane] = ld(h + (size_t)i * Bp + b0);
-    __syncthreads();
-  }
   const int64_t rpw = (rpb + 3) / 4;
   const int64_t r_begin = (int64_t)c * rpb + wave * rpw;
   const int64_t r_end = std::min<int64_t>(W, std::min<int64_t>((int64_t)(c + 1) * rpb, r_begin + rpw));
-  V acc[MODE == 2 ? 1 : NV];
+  V acc[NV];
 #pragma unroll
-  for (int i = 0; i < (MODE == 2 ? 1 : NV); ++i) acc[i] = V(T(0));
-  V nrm = V(T(0)), fin = V(T(1));
+  for (int i = 0; i < NV; ++i) acc[i] = V(T(0));
   for (int64_t r = r_begin; r < r_end; ++r) {
     const size_t off = (size_t)r * Bp + b0;
-    V xr = ld(x + off);
-    if (MODE != 0) {
-      V sum = V(T(0));
+    const V xr = vload(x + off);
 #pragma unroll
-      for (int i = 0; i < NV; ++i)
-        if (i < nv) sum += hs[i][lane] * ld(basis + (size_t)i * vstride + off);
-      xr = xr - sum;
-      st(x + off, xr);
-    }
-    if (MODE == 2) {
-      nrm += xr * xr;
-#pragma unroll
-      for (int q = 0; q < Sn; ++q)
-        if (!finite(xr[q])) fin[q] = T(0);
-    } else {
-#pragma unroll
-      for (int i = 0; i < NV; ++i)
-        if (i < nv) acc[i] += ld(basis + (size_t)i * vstride + off) * xr;
-    }
+    for (int i = 0; i < NV; ++i)
+      if (i < nv) acc[i] += vload(basis + (size_t)i * vstride + off) * xr;
   }
-  // combine the 4 wavefronts (fixed order: wave 0 + 1 + 2 + 3)
   const size_t plane = (size_t)nchunk * Bp;
   const size_t pout = (size_t)c * Bp + b0;
-  auto combine = [&](V v, T* dst, int op) {
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (i >= nv) continue;
+    V v = acc[i];
     if (wave > 0) cb[wave - 1][lane] = v;
     __syncthreads();
     if (wave == 0) {
 #pragma unroll
-      for (int w = 0; w < 3; ++w) {
-        const V o = cb[w][lane];
-        if (op == 0) {
-          v += o;
-        } else {
-#pragma unroll
-          for (int q = 0; q < Sn; ++q) v[q] = minp(v[q], o[q]);
-        }
-      }
-      st(dst, v);
+      for (int w = 0; w < 3; ++w) v += cb[w][lane];
+      vstore(part + (size_t)i * plane + pout, v);
     }
     __syncthreads();
-  };
-  if (MODE == 2) {
-    combine(nrm, part + pout, 0);
-    combine(fin, part + plane + pout, 1);
-  } else {
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (i < nv) combine(acc[MODE == 2 ? 0 : i], part + (size_t)i * plane + pout, 0);
   }
 }
 
@@ -527,7 +505,8 @@ __global__ __launch_bounds__(kBlock) void k_gs_dots(const T* __restrict__ basis,
     if (own[j]) vstore(part + (size_t)(wave + 4 * j) * plane + (size_t)c * Bp + b0, acc[j]);
 }
 
-// The second Gram--Schmidt pass (x <- x - sum_i h_i V_i, then part_i = V_i . x)
+// The second Gram--Schmidt pass (x <- x - sum_i h_i V_i, then part_i = V_i . x
+// for i < nv and part_nv = x . x)
 // with the prefix vectors split across the block's 4 wavefronts instead of
 // the rows: wavefront w holds V_i for i = w, w+4, ... of two rows at a time
 // (at most NV/4 per wavefront, so registers stay low), forms its share of
@@ -550,7 +529,7 @@ __global__ __launch_bounds__(kBlock) void k_gs_update_dots(const T* __restrict__
   const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
   const int c = blockIdx.y;
   __shared__ V share[2][4][2][kWave];
-  V hw[NW], acc[NW];
+  V hw[NW], acc[NW], nrm = vsplat<T>(T(0));
 #pragma unroll
   for (int j = 0; j < NW; ++j) {
     const int i = wave + 4 * j;
@@ -589,7 +568,11 @@ __global__ __launch_bounds__(kBlock) void k_gs_update_dots(const T* __restrict__
     const V y0 = x0 - s0, y1 = x1 - s1;
     if (wave == 0) {
       vstore(x + off0, y0);
-      if (two) vstore(x + off1, y1);
+      nrm += y0 * y0;
+      if (two) {
+        vstore(x + off1, y1);
+        nrm += y1 * y1;
+      }
     }
 #pragma unroll
     for (int j = 0; j < NW; ++j) {
@@ -603,32 +586,7 @@ __global__ __launch_bounds__(kBlock) void k_gs_update_dots(const T* __restrict__
     const int i = wave + 4 * j;
     if (i < nv) vstore(part + (size_t)i * plane + (size_t)c * Bp + b0, acc[j]);
   }
-}
-
-// out[i][b] = reduce_c part[i][c][b] for c < nchunk: 4 thread groups take
-// chunks c = g mod 4 in increasing order, then groups combine 0+1+2+3.
-// op 0 = sum, 2 = min.  grid (Bp / 64, nv), block 256.
-template <typename T>
-__global__ __launch_bounds__(256) void k_reduce_chunks(const T* __restrict__ part, int nchunk,
-                                                       int64_t Bp, T* out, int op) {
-  __shared__ T buf[3][64];
-  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
-  const int64_t b = (int64_t)blockIdx.x * 64 + lane;
-  const int i = blockIdx.y;
-  const T* p = part + (size_t)i * nchunk * Bp + b;
-  T acc = op == 0 ? T(0) : T(1);
-  bool first = true;
-  for (int c = g; c < nchunk; c += 4) {
-    const T v = p[(size_t)c * Bp];
-    acc = first ? v : (op == 0 ? acc + v : minp(acc, v));
-    first = false;
-  }
-  if (g > 0) buf[g - 1][lane] = acc;
-  __syncthreads();
-  if (g == 0) {
-    for (int w = 0; w < 3 && w + 1 < nchunk; ++w) acc = op == 0 ? acc + buf[w][lane] : minp(acc, buf[w][lane]);
-    out[(size_t)i * Bp + b] = acc;
-  }
+  if (wave == 0) vstore(part + (size_t)nv * plane + (size_t)c * Bp + b0, nrm);
 }
 
 // elementwise helpers on W x Bp vectors
@@ -688,6 +646,14 @@ struct Gm {
   T* coeff;      // [restart][Bp] (back-substitution output)
   int32_t* counter;  // [0] active count at a cycle's start, [1] unconverged count
   int32_t* stepcnt;  // [restart+1]: samples active at the start of Arnoldi step s
+  // raw-basis map (k_gm_tri): v_j = sum_{i<=j} Z_i Tm[i][j]
+  T* Tm;   // [(restart+1)][(restart+1)][Bp], upper triangular
+  T* Hu;   // [(restart+1)][restart][Bp]: the unrotated Hessenberg matrix
+  T* U2;   // [restart+1][Bp]: g2 / nu of the last step
+  T* G1;   // [restart+1][Bp]: V^T y of the current step
+  T* Q1;   // [restart+1][Bp]: Tm G1, the first projection's coefficients on Z
+  T* Cg;   // [restart+1][Bp]: the lagged correction c of the current step
+  T* Wc;   // [restart][Bp]: Tm coeff, the cycle's correction on Z
 };
 
 template <typename T>
@@ -722,55 +688,166 @@ __global__ void k_gm_cycle_init(Gm<T> G, const T* __restrict__ beta2) {
   }
   for (int i = 0; i <= R; ++i) G.g[(size_t)i * G.Bp + b] = i == 0 ? beta : T(0);
   for (int i = 0; i < (R + 1) * R; ++i) G.H[(size_t)i * G.Bp + b] = T(0);
+  G.Tm[b] = T(1);  // Z_0 = r / beta is stored normalised
   if (c) atomicAdd(&G.stepcnt[0], 1);
 }
 
-// One Arnoldi step's scalar work for iteration ``it`` (operators.py:996-1081).
-// The Hessenberg column (h1 + h2 up to row it, the new norm at row it + 1) is
-// rotated by the earlier Givens pairs in one streaming sweep that carries the
-// lower entry: rotation ri only touches rows ri and ri + 1.
-template <typename T>
-__global__ void k_gm_givens(Gm<T> G, int it, const T* __restrict__ h1, const T* __restrict__ h2,
-                            const T* __restrict__ nrm2, const T* __restrict__ fin) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= G.Bp) return;
-  const int R = G.restart;
+// One Arnoldi step's per-sample algebra on the raw basis (operators.py:834-871,
+// 996-1081).
+//
+// Basis slot i holds a raw vector Z_i.  The orthonormal Arnoldi vectors are
+// v_j = sum_{i<=j} Z_i Tm[i][j], with Tm upper triangular: Z_0 = v_0, and
+// Z_{j+1} is the image of step j after one projection, so the off-diagonal
+// entries of Tm are of the order of the rounding error.  Step ``it`` applies
+// the operator to Z_it Tm[it][it], giving y, and then runs
+//   pass A   p = Z^T y                                  (reads the prefix)
+//   MODE 1   g1 = Tm^T p (= V^T y),  q1 = Tm g1         (V g1 = Z q1)
+//   pass B   y1 = y - Z q1 stored as Z_{it+1},  p2 = Z^T y1,  |y1|^2
+//   MODE 2   g2 = Tm^T p2 (= V^T y1), the Hessenberg column, the Givens
+//            step, and column it+1 of Tm: v_{it+1} = (y1 - V g2) / nu.
+// This is the reference's two-pass classical Gram--Schmidt: the image is
+// projected on the prefix twice, each time with dot products taken against
+// the vector being corrected.  The second subtraction is carried by Tm
+// instead of a third pass over the basis, and the operator reads the raw
+// vector, so
+//  * Z_it Tm[it][it] = v_it + V u with u = g2 / nu of step it - 1, and
+//    A V = V Hu (Hu: the unrotated Hessenberg matrix), give
+//    A v_it = y - V c with c = Hu[0..it][0..it-1] u;
+//  * the column is h = g1 + g2 - c, and h[it+1] = |y1 - V g2| =
+//    sqrt(|y1|^2 - |g2|^2), as y1 - V g2 is orthogonal to V;
+//  * the rotations, the stop test (residual estimate, finiteness, happy
+//    breakdown at 1e-14) and the masking by the step's active flag are the
+//    reference's.  Tm's new column is zero for a sample inactive at the
+//    step's start, as the reference keeps a zero basis vector there.
+// A block owns 64 samples (one per lane) and 16 wavefronts, which split the
+// planes of the chunk reduction and the rows or columns of the triangular
+// products; LDS holds the reduced planes P[R+2][64] and the coefficients
+// Gv[R+1][64] (dynamic, (2R + 3) * 64 elements).
+template <typename T, int MODE>
+__global__ __launch_bounds__(1024) void k_gm_tri(Gm<T> G, int it, const T* __restrict__ part,
+                                                 int nchunk) {
+  extern __shared__ __align__(16) unsigned char tri_raw[];
+  const int R = G.restart, R1 = R + 1;
+  T* P = reinterpret_cast<T*>(tri_raw);  // [R + 2][64]
+  T* Gv = P + (size_t)(R + 2) * 64;      // [R + 1][64]
+  __shared__ T s_inv[64];
+  __shared__ int s_keep[64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int64_t Bp = G.Bp;
-  const T eps = T(1e-30), brk = T(1e-14);
-  const int active = G.act[b];
-  G.keep[b] = active;
-  const T next_norm = __builtin_sqrt(nrm2[b]);
-  T carry = h1[b] + h2[b];  // row 0 of the column
-  for (int ri = 0; ri < it; ++ri) {
-    const T c = G.cs[(size_t)ri * Bp + b], s = G.sn[(size_t)ri * Bp + b];
-    const T f = carry, sc = h1[(size_t)(ri + 1) * Bp + b] + h2[(size_t)(ri + 1) * Bp + b];
-    if (active) G.H[((size_t)ri * R + it) * Bp + b] = c * f + s * sc;
-    carry = -s * f + c * sc;
+  const int64_t b = (int64_t)blockIdx.x * 64 + lane;
+  const int nv = it + 1;
+  const int planes = MODE == 1 ? nv : nv + 1;
+  const size_t plane = (size_t)nchunk * Bp;
+  // the pass's chunk partials, summed in chunk order
+  for (int i = wave; i < planes; i += 16) {
+    const T* pp = part + (size_t)i * plane + b;
+    T acc = pp[0];
+    for (int c = 1; c < nchunk; ++c) acc += pp[(size_t)c * Bp];
+    P[i * 64 + lane] = acc;
   }
-  const T diag = carry, sub = next_norm;
-  const T rnorm = hypotv(diag, sub);
-  const T safe = maxp(rnorm, eps);
-  const T nc = rnorm > eps ? diag / safe : T(1);
-  const T ns = rnorm > eps ? sub / safe : T(0);
-  const T pc = G.g[(size_t)it * Bp + b], pn = G.g[(size_t)(it + 1) * Bp + b];
-  const T rc = nc * pc + ns * pn;
-  const T rn = -ns * pc + nc * pn;
-  if (active) {
-    G.cs[(size_t)it * Bp + b] = nc;
-    G.sn[(size_t)it * Bp + b] = ns;
-    G.H[((size_t)it * R + it) * Bp + b] = rnorm;
-    G.H[((size_t)(it + 1) * R + it) * Bp + b] = T(0);
-    G.g[(size_t)it * Bp + b] = rc;
-    G.g[(size_t)(it + 1) * Bp + b] = rn;
-    G.steps[b] = it + 1;
+  __syncthreads();
+  const T* Tm = G.Tm + b;
+  const size_t tcol = (size_t)Bp, trow = (size_t)R1 * Bp;  // Tm[i][j] at i * trow + j * tcol
+  for (int j = wave; j < nv; j += 16) {
+    T acc = T(0);
+    for (int i = 0; i <= j; ++i) acc += Tm[i * trow + j * tcol] * P[i * 64 + lane];
+    Gv[j * 64 + lane] = acc;
+    if (MODE == 1) {
+      G.G1[(size_t)j * Bp + b] = acc;
+    } else {
+      // c_j = sum_k Hu[j][k] u_k, k in [max(j - 1, 0), it - 1] (Hu is upper Hessenberg)
+      T cj = T(0);
+      for (int k = j > 0 ? j - 1 : 0; k < it; ++k)
+        cj += G.Hu[((size_t)j * R + k) * Bp + b] * G.U2[(size_t)k * Bp + b];
+      G.Cg[(size_t)j * Bp + b] = cj;
+    }
   }
-  const T est = absv(rn);
-  const bool finite_ok = finite(est) && finite(rnorm) && fin[b] != T(0);
-  const bool happy = next_norm <= brk;
-  const int still = (active && finite_ok && !happy && est > G.thr[b]) ? 1 : 0;
-  G.act[b] = still;
-  G.scale[b] = T(1) / maxp(next_norm, eps);
-  if (still && b < G.batch) atomicAdd(&G.stepcnt[it + 1], 1);
+  __syncthreads();
+  if (MODE == 1) {
+    for (int i = wave; i < nv; i += 16) {
+      T acc = T(0);
+      for (int j = i; j < nv; ++j) acc += Tm[i * trow + j * tcol] * Gv[j * 64 + lane];
+      G.Q1[(size_t)i * Bp + b] = acc;
+    }
+    return;
+  }
+  if (wave == 0) {
+    const T eps = T(1e-30), brk = T(1e-14);
+    const int active = G.act[b];
+    G.keep[b] = active;
+    T ss = T(0);
+    for (int j = 0; j < nv; ++j) ss += Gv[j * 64 + lane] * Gv[j * 64 + lane];
+    const T d2 = P[nv * 64 + lane] - ss;
+    const T next_norm = d2 < T(0) ? T(0) : __builtin_sqrt(d2);  // NaN stays NaN
+    auto col = [&](int i) {
+      return (G.G1[(size_t)i * Bp + b] + Gv[i * 64 + lane]) - G.Cg[(size_t)i * Bp + b];
+    };
+    T carry = col(0);
+    if (active) G.Hu[(size_t)it * Bp + b] = carry;
+    for (int ri = 0; ri < it; ++ri) {
+      const T c = G.cs[(size_t)ri * Bp + b], s = G.sn[(size_t)ri * Bp + b];
+      const T f = carry, sc = col(ri + 1);
+      if (active) {
+        G.Hu[((size_t)(ri + 1) * R + it) * Bp + b] = sc;
+        G.H[((size_t)ri * R + it) * Bp + b] = c * f + s * sc;
+      }
+      carry = -s * f + c * sc;
+    }
+    const T diag = carry, sub = next_norm;
+    const T rnorm = hypotv(diag, sub);
+    const T safe = maxp(rnorm, eps);
+    const T nc = rnorm > eps ? diag / safe : T(1);
+    const T ns = rnorm > eps ? sub / safe : T(0);
+    const T pc = G.g[(size_t)it * Bp + b], pn = G.g[(size_t)(it + 1) * Bp + b];
+    const T rc = nc * pc + ns * pn;
+    const T rn = -ns * pc + nc * pn;
+    const T inv = T(1) / maxp(next_norm, eps);
+    if (active) {
+      G.Hu[((size_t)(it + 1) * R + it) * Bp + b] = next_norm;
+      G.cs[(size_t)it * Bp + b] = nc;
+      G.sn[(size_t)it * Bp + b] = ns;
+      G.H[((size_t)it * R + it) * Bp + b] = rnorm;
+      G.H[((size_t)(it + 1) * R + it) * Bp + b] = T(0);
+      G.g[(size_t)it * Bp + b] = rc;
+      G.g[(size_t)(it + 1) * Bp + b] = rn;
+      G.steps[b] = it + 1;
+    }
+    const T est = absv(rn);
+    // |y1|^2 is finite exactly when y1 and hence (y1 - V g2) / nu are
+    const bool finite_ok = finite(est) && finite(rnorm) && finite(P[nv * 64 + lane]);
+    const bool happy = next_norm <= brk;
+    const int still = (active && finite_ok && !happy && est > G.thr[b]) ? 1 : 0;
+    G.act[b] = still;
+    G.Tm[(size_t)(it + 1) * trow + (size_t)(it + 1) * tcol + b] = active ? inv : T(0);
+    s_inv[lane] = inv;
+    s_keep[lane] = active;
+    if (still && b < G.batch) atomicAdd(&G.stepcnt[it + 1], 1);
+  }
+  __syncthreads();
+  // column it + 1 of Tm: v_{it+1} = (Z_{it+1} - Z Tm g2) / nu, and u = g2 / nu
+  const T inv = s_inv[lane];
+  const bool keep = s_keep[lane] != 0;
+  for (int i = wave; i < nv; i += 16) {
+    T acc = T(0);
+    for (int j = i; j < nv; ++j) acc += Tm[i * trow + j * tcol] * Gv[j * 64 + lane];
+    G.Tm[(size_t)i * trow + (size_t)(it + 1) * tcol + b] = keep ? -(acc * inv) : T(0);
+    G.U2[(size_t)i * Bp + b] = keep ? Gv[i * 64 + lane] * inv : T(0);
+  }
+}
+
+// The cycle's correction on the raw basis: x += sum_{j < steps} coeff_j v_j =
+// sum_i Z_i Wc_i with Wc_i = sum_{i <= j < steps} Tm[i][j] coeff_j.
+template <typename T>
+__global__ void k_gm_tcoef(Gm<T> G) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int i = blockIdx.y;
+  if (b >= G.Bp) return;
+  const int steps = G.steps[b];
+  const size_t trow = (size_t)(G.restart + 1) * G.Bp;
+  T acc = T(0);
+  for (int j = i; j < steps; ++j) acc += G.Tm[i * trow + (size_t)j * G.Bp + b] * G.coeff[(size_t)j * G.Bp + b];
+  G.Wc[(size_t)i * G.Bp + b] = acc;
 }
 
 // Back substitution (operators.py:902-917), one thread per sample in blocks of
@@ -1224,7 +1301,6 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                oChi = take(n * Bp * es), oDm = take(m * Bp * es), oDp = take(m * Bp * es),
                oU = take(n * Bp * es), oWv = take(m * Bp * es),
                oPart = take((size_t)(restart + 1) * std::max(nchunk, nchunk2) * Bp * es),
-               oH1 = take((size_t)(restart + 1) * Bp * es), oH2 = take((size_t)(restart + 1) * Bp * es),
                oS1 = take(Bp * es), oS2 = take(Bp * es), oThr = take(Bp * es), oRinf = take(Bp * es),
                oCyc = take(Bp * 4), oAct = take(Bp * 4), oSteps = take(Bp * 4), oKeep = take(Bp * 4),
                oScale = take(Bp * es), oHess = take((size_t)Bp * (restart + 1) * restart * es),
@@ -1232,7 +1308,12 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                oGv = take((size_t)(restart + 1) * Bp * es), oCoef = take((size_t)restart * Bp * es),
                oCnt = take(256), oStepCnt = take((size_t)(restart + 2) * 4), oLw = take(Bp * es), oGt = take(n * Bp * es),
                oGlo = take(n * Bp * es), oGhi = take(n * Bp * es), oGr = take(m * Bp * es),
-               oGF = take((size_t)M * Bp * es);
+               oGF = take((size_t)M * Bp * es),
+               oTm = take((size_t)(restart + 1) * (restart + 1) * Bp * es),
+               oHu = take((size_t)(restart + 1) * restart * Bp * es),
+               oU2 = take((size_t)(restart + 1) * Bp * es), oG1 = take((size_t)(restart + 1) * Bp * es),
+               oQ1 = take((size_t)(restart + 1) * Bp * es), oCg = take((size_t)(restart + 1) * Bp * es),
+               oWc = take((size_t)restart * Bp * es);
   // per-sample coefficients: the forward's per-sample arrays are rebuilt from
   // values in a region laid out like the forward workspace, plus sigma . w and
   // the coefficient gradient in entry order
@@ -1255,14 +1336,14 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   T* Rr = (T*)(ws + oRr);
   T* T1 = (T*)(ws + oT1);
   T* part = (T*)(ws + oPart);
-  T* H1 = (T*)(ws + oH1);
-  T* H2 = (T*)(ws + oH2);
   T* S1 = (T*)(ws + oS1);
   T* S2 = (T*)(ws + oS2);
   Gm<T> G{batch, Bp, restart, (T*)(ws + oThr), (T*)(ws + oRinf), (int32_t*)(ws + oCyc),
           (int32_t*)(ws + oAct), (int32_t*)(ws + oSteps), (int32_t*)(ws + oKeep),
           (T*)(ws + oScale), (T*)(ws + oHess), (T*)(ws + oCs), (T*)(ws + oSn), (T*)(ws + oGv),
-          (T*)(ws + oCoef), (int32_t*)(ws + oCnt), (int32_t*)(ws + oStepCnt)};
+          (T*)(ws + oCoef), (int32_t*)(ws + oCnt), (int32_t*)(ws + oStepCnt),
+          (T*)(ws + oTm), (T*)(ws + oHu), (T*)(ws + oU2), (T*)(ws + oG1), (T*)(ws + oQ1),
+          (T*)(ws + oCg), (T*)(ws + oWc)};
 
   Adj<T> S{};
   S.K = kept_matrix<T>(p, true);
@@ -1345,10 +1426,13 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   if (m) k_lin_rows<T><<<grow, kBlock, 0, st>>>(S, Y, Dd, R, (T*)(ws + oDm), (T*)(ws + oDp));
   k_lin_cols<T><<<gcol, kBlock, 0, st>>>(S, Y, Tt, LO, HI, shared, (const T*)(ws + oDp),
                                           (T*)(ws + oCm), (T*)(ws + oClo), (T*)(ws + oChi));
-  auto op = [&](const T* v, T* out) {
+  // out = A (vsc . v), vsc a per-sample scale or nullptr
+  auto op = [&](const T* v, T* out, const T* vsc) {
+    S.vsc = vsc;
     k_op_cols1<T><<<eb, 256, 0, st>>>(S, v, out);
     if (m) k_op_rows<T><<<grow, kBlock, 0, st>>>(S, v, out);
     k_op_cols2<T><<<gcol, kBlock, 0, st>>>(S, v, out);
+    S.vsc = nullptr;
   };
   auto reduce = [&](int mode_nv, T* out, int opk) {
     k_reduce<T><<<(unsigned)((mode_nv * Bp + 255) / 256), 256, 0, st>>>(part, mode_nv, nchunk, Bp,
@@ -1373,15 +1457,29 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   // one round of resident blocks per pass: the chunk count per batch tile is the
   // kernel's resident block count over the tiles (so no partial second round)
   int last_nchunk = 1;
-  auto launch_gs = [&](auto kern, int nv, T* img, const T* h) -> int {
+  auto resident_chunks = [&](auto kern, int64_t* chunks) -> int {
     int per_cu = 0;
     PURIN_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kBlock, 0));
-    const int64_t chunks = std::max<int64_t>(
+    *chunks = std::max<int64_t>(
         1, std::min<int64_t>({(int64_t)std::max(per_cu, 1) * cus / tiles0, (W + 3) / 4,
                               (int64_t)nchunk2}));
+    return PURIN_CP_OK;
+  };
+  auto launch_gs = [&](auto kern, int nv, T* img, const T* h) -> int {
+    int64_t chunks = 1;
+    if (int rc = resident_chunks(kern, &chunks)) return rc;
     const int64_t rpb = (W + chunks - 1) / chunks;
     last_nchunk = (int)chunks;
     kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, vstride, nv, img, h, W, Bp,
+                                                                    part, (int)chunks, rpb);
+    return PURIN_CP_OK;
+  };
+  auto launch_rows = [&](auto kern, int nv, const T* img) -> int {
+    int64_t chunks = 1;
+    if (int rc = resident_chunks(kern, &chunks)) return rc;
+    const int64_t rpb = (W + chunks - 1) / chunks;
+    last_nchunk = (int)chunks;
+    kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, vstride, nv, img, W, Bp,
                                                                     part, (int)chunks, rpb);
     return PURIN_CP_OK;
   };
@@ -1396,38 +1494,22 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                                                                     part, (int)chunks, rpb);
     return PURIN_CP_OK;
   };
+  // pass A (mode 0): part_i = Z_i . y; pass B (mode 1): y <- y - sum_i h_i Z_i,
+  // part_i = Z_i . y, part_nv = y . y
   auto gs_pass = [&](int mode, int nv, T* img, const T* h) -> int {
-#define PURIN_GS(MODE, NVB) return launch_gs(k_gs_pass<T, NVB, MODE>, nv, img, h)
     const int bucket = nv <= 8 ? 8 : (nv <= 16 ? 16 : (nv <= 24 ? 24 : 32));
     if (mode == 0) {
-#define PURIN_GD(NVB) return launch_dots(k_gs_dots<T, NVB>, nv, img)
       // up to 8 vectors the row-split pass is faster: the vector-split one
       // re-reads x once per wavefront, which dominates for a short prefix
-      if (bucket == 8) PURIN_GS(0, 8);
-      if (bucket == 16) PURIN_GD(16);
-      if (bucket == 24) PURIN_GD(24);
-      PURIN_GD(32);
-#undef PURIN_GD
-    } else if (mode == 1) {
-#define PURIN_GU(NVB) return launch_gs(k_gs_update_dots<T, NVB>, nv, img, h)
-      if (bucket == 8) PURIN_GU(8);
-      if (bucket == 16) PURIN_GU(16);
-      if (bucket == 24) PURIN_GU(24);
-      PURIN_GU(32);
-#undef PURIN_GU
-    } else {
-      if (bucket == 8) PURIN_GS(2, 8);
-      if (bucket == 16) PURIN_GS(2, 16);
-      if (bucket == 24) PURIN_GS(2, 24);
-      PURIN_GS(2, 32);
+      if (bucket == 8) return launch_rows(k_gs_dots_rows<T, 8>, nv, img);
+      if (bucket == 16) return launch_dots(k_gs_dots<T, 16>, nv, img);
+      if (bucket == 24) return launch_dots(k_gs_dots<T, 24>, nv, img);
+      return launch_dots(k_gs_dots<T, 32>, nv, img);
     }
-#undef PURIN_GS
-  };
-  // reduce the chunks the last Gram--Schmidt pass wrote
-  auto reduce2 = [&](int nv, int plane_index, T* out, int opk) {
-    const size_t offset = (size_t)plane_index * last_nchunk * Bp;
-    k_reduce_chunks<T><<<dim3((unsigned)(Bp / 64), (unsigned)nv), 256, 0, st>>>(
-        part + offset, last_nchunk, Bp, out, opk);
+    if (bucket == 8) return launch_gs(k_gs_update_dots<T, 8>, nv, img, h);
+    if (bucket == 16) return launch_gs(k_gs_update_dots<T, 16>, nv, img, h);
+    if (bucket == 24) return launch_gs(k_gs_update_dots<T, 24>, nv, img, h);
+    return launch_gs(k_gs_update_dots<T, 32>, nv, img, h);
   };
 
   // rhs g = [cot * eligible, 0, 0] (cotangent divided by sqrt(D) for a metric)
@@ -1479,12 +1561,12 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
       dot(RH, Rr, kRho_);
       k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 1, T(0), T(0));
       bi_vec(0);
-      op(Pv, Qv);
+      op(Pv, Qv, nullptr);
       dot(RH, Qv, kRQ);
       k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 2, T(0), T(0));
       bi_vec(1);
       dot(Sv, Sv, kSS);
-      op(Sv, Tv);
+      op(Sv, Tv, nullptr);
       dot(Tv, Sv, kTS);
       dot(Tv, Tv, kTT);
       k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 3, T(0), T(0));
@@ -1503,6 +1585,12 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   k_fill<T><<<eb, 256, 0, st>>>(X, total, T(0));
   PURIN_HIP(hipMemcpyAsync(Rr, Gr, vec, hipMemcpyDeviceToDevice, st));  // r = g - A(0)
 
+  const dim3 tri_grid((unsigned)(Bp / 64));
+  const size_t tri_lds = (size_t)(2 * restart + 3) * 64 * es;
+  PURIN_HIP(hipFuncSetAttribute((const void*)k_gm_tri<T, 1>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)tri_lds));
+  PURIN_HIP(hipFuncSetAttribute((const void*)k_gm_tri<T, 2>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)tri_lds));
   int64_t completed = 0;
   while (completed < o.max_iterations) {
     zero_counters();
@@ -1531,30 +1619,28 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
       if (int rc = read_stepcnt(launched, cnt)) return rc;
       if (cnt[launched] == 0) break;
       for (int it = launched; it < chunk_end; ++it) {
-        T* vk = Vb + (size_t)it * vstride;
+        // slot it holds Z_it; y = A (Z_it Tm[it][it]) goes to slot it + 1, where
+        // pass B turns it into Z_{it+1}
+        T* zk = Vb + (size_t)it * vstride;
         T* img = Vb + (size_t)(it + 1) * vstride;
-        op(vk, img);
-        // two-pass classical Gram--Schmidt over the active prefix (operators.py:834-871)
         const int nv = it + 1;
+        op(zk, img, G.Tm + ((size_t)it * (restart + 1) + it) * Bp);
+        int nch = nchunk;
         if (nv <= 32) {
           if (int rc = gs_pass(0, nv, img, nullptr)) return rc;
-          reduce2(nv, 0, H1, 0);
-          if (int rc = gs_pass(1, nv, img, H1)) return rc;
-          reduce2(nv, 0, H2, 0);
-          if (int rc = gs_pass(2, nv, img, H2)) return rc;
-          reduce2(1, 0, S1, 0);
-          reduce2(1, 1, S2, 2);
+          nch = last_nchunk;
         } else {
           k_gs<T, 0><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, nullptr, W, Bp, part, nchunk);
-          reduce(nv, H1, 0);
-          k_gs<T, 1><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, H1, W, Bp, part, nchunk);
-          reduce(nv, H2, 0);
-          k_gs<T, 2><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, H2, W, Bp, part, nchunk);
-          k_reduce<T><<<sb, 256, 0, st>>>(part, 1, nchunk, Bp, S1, 0);
-          k_reduce<T><<<sb, 256, 0, st>>>(part + (size_t)nchunk * Bp, 1, nchunk, Bp, S2, 2);
         }
-        k_gm_givens<T><<<sb, 256, 0, st>>>(G, it, H1, H2, S1, S2);
-        k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, img, img, G.scale, G.keep);
+        k_gm_tri<T, 1><<<tri_grid, 1024, tri_lds, st>>>(G, it, part, nch);
+        nch = nchunk;
+        if (nv <= 32) {
+          if (int rc = gs_pass(1, nv, img, G.Q1)) return rc;
+          nch = last_nchunk;
+        } else {
+          k_gs<T, 5><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, G.Q1, W, Bp, part, nchunk);
+        }
+        k_gm_tri<T, 2><<<tri_grid, 1024, tri_lds, st>>>(G, it, part, nch);
       }
       launched = chunk_end;
     }
@@ -1566,9 +1652,10 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
         break;
       }
     k_gm_backsub<T><<<(unsigned)(Bp / 64), 64, (size_t)restart * 64 * sizeof(T), st>>>(G);
-    k_correction<T><<<eb, 256, 0, st>>>(total, Bp, X, Vb, vstride, G.coeff, G.steps);
+    k_gm_tcoef<T><<<dim3((unsigned)((Bp + 255) / 256), (unsigned)restart), 256, 0, st>>>(G);
+    k_correction<T><<<eb, 256, 0, st>>>(total, Bp, X, Vb, vstride, G.Wc, G.steps);
     // candidate residual r = g - A x (operators.py:1084-1091)
-    op(X, T1);
+    op(X, T1, nullptr);
     k_axpby<T><<<eb, 256, 0, st>>>(total, Rr, Gr, T1, T(-1));
     k_gs<T, 4><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Rr, nullptr, W, Bp, part, nchunk);
     reduce(1, S1, 1);
