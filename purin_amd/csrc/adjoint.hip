@@ -719,40 +719,53 @@ __global__ void k_gm_cycle_init(Gm<T> G, const T* __restrict__ beta2) {
 //    breakdown at 1e-14) and the masking by the step's active flag are the
 //    reference's.  Tm's new column is zero for a sample inactive at the
 //    step's start, as the reference keeps a zero basis vector there.
-// A block owns 64 samples (one per lane) and 16 wavefronts, which split the
-// planes of the chunk reduction and the rows or columns of the triangular
-// products; LDS holds the reduced planes P[R+2][64] and the coefficients
-// Gv[R+1][64] (dynamic, (2R + 3) * 64 elements).
+// A block of 16 wavefronts owns kTriS = 16 samples: lane l of a wavefront
+// serves sample l mod 16 as worker 4 w + l / 16 (64 workers per sample).  The
+// chunk sums split each plane's chunks into 4 interleaved quarters summed in
+// chunk order and combined as (q0 + q1) + (q2 + q3); the workers then split
+// the outputs of the triangular products, and one lane per sample runs the
+// Givens step from LDS.  LDS (dynamic, (5R + 4) * kTriS elements): the reduced
+// planes P[R+2], the coefficients Gv[R+1], the Hessenberg column Col[R+1] and
+// the rotations Cs[R], Sn[R], each over the block's samples.
+constexpr int kTriS = 16;
+
 template <typename T, int MODE>
 __global__ __launch_bounds__(1024) void k_gm_tri(Gm<T> G, int it, const T* __restrict__ part,
                                                  int nchunk) {
   extern __shared__ __align__(16) unsigned char tri_raw[];
   const int R = G.restart, R1 = R + 1;
-  T* P = reinterpret_cast<T*>(tri_raw);  // [R + 2][64]
-  T* Gv = P + (size_t)(R + 2) * 64;      // [R + 1][64]
-  __shared__ T s_inv[64];
-  __shared__ int s_keep[64];
+  T* P = reinterpret_cast<T*>(tri_raw);  // [R + 2][kTriS]
+  T* Gv = P + (size_t)(R + 2) * kTriS;   // [R + 1][kTriS]
+  T* Col = Gv + (size_t)(R + 1) * kTriS; // [R + 1][kTriS]
+  T* Cs = Col + (size_t)(R + 1) * kTriS; // [R][kTriS]
+  T* Sn = Cs + (size_t)R * kTriS;        // [R][kTriS]
+  __shared__ T s_inv[kTriS];
+  __shared__ int s_keep[kTriS];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int sl = lane & (kTriS - 1), q = lane >> 4;
+  const int worker = wave * 4 + q;
   const int64_t Bp = G.Bp;
-  const int64_t b = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t b = (int64_t)blockIdx.x * kTriS + sl;
   const int nv = it + 1;
   const int planes = MODE == 1 ? nv : nv + 1;
   const size_t plane = (size_t)nchunk * Bp;
-  // the pass's chunk partials, summed in chunk order
   for (int i = wave; i < planes; i += 16) {
     const T* pp = part + (size_t)i * plane + b;
-    T acc = pp[0];
-    for (int c = 1; c < nchunk; ++c) acc += pp[(size_t)c * Bp];
-    P[i * 64 + lane] = acc;
+    T acc = T(0);
+    for (int c = q; c < nchunk; c += 4) acc += pp[(size_t)c * Bp];
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    if (q == 0) P[i * kTriS + sl] = acc;
   }
   __syncthreads();
   const T* Tm = G.Tm + b;
   const size_t tcol = (size_t)Bp, trow = (size_t)R1 * Bp;  // Tm[i][j] at i * trow + j * tcol
-  for (int j = wave; j < nv; j += 16) {
+  const int active = MODE == 2 ? G.act[b] : 0;
+  for (int j = worker; j < nv; j += 64) {
     T acc = T(0);
-    for (int i = 0; i <= j; ++i) acc += Tm[i * trow + j * tcol] * P[i * 64 + lane];
-    Gv[j * 64 + lane] = acc;
+    for (int i = 0; i <= j; ++i) acc += Tm[i * trow + j * tcol] * P[i * kTriS + sl];
+    Gv[j * kTriS + sl] = acc;
     if (MODE == 1) {
       G.G1[(size_t)j * Bp + b] = acc;
     } else {
@@ -760,38 +773,39 @@ __global__ __launch_bounds__(1024) void k_gm_tri(Gm<T> G, int it, const T* __res
       T cj = T(0);
       for (int k = j > 0 ? j - 1 : 0; k < it; ++k)
         cj += G.Hu[((size_t)j * R + k) * Bp + b] * G.U2[(size_t)k * Bp + b];
-      G.Cg[(size_t)j * Bp + b] = cj;
+      const T col = (G.G1[(size_t)j * Bp + b] + acc) - cj;
+      Col[j * kTriS + sl] = col;
+      if (active) G.Hu[((size_t)j * R + it) * Bp + b] = col;
+    }
+  }
+  if (MODE == 2) {
+    for (int j = worker; j < it; j += 64) {
+      Cs[j * kTriS + sl] = G.cs[(size_t)j * Bp + b];
+      Sn[j * kTriS + sl] = G.sn[(size_t)j * Bp + b];
     }
   }
   __syncthreads();
   if (MODE == 1) {
-    for (int i = wave; i < nv; i += 16) {
+    for (int i = worker; i < nv; i += 64) {
       T acc = T(0);
-      for (int j = i; j < nv; ++j) acc += Tm[i * trow + j * tcol] * Gv[j * 64 + lane];
+      for (int j = i; j < nv; ++j) acc += Tm[i * trow + j * tcol] * Gv[j * kTriS + sl];
       G.Q1[(size_t)i * Bp + b] = acc;
     }
     return;
   }
-  if (wave == 0) {
+  if (worker == 0) {
     const T eps = T(1e-30), brk = T(1e-14);
-    const int active = G.act[b];
     G.keep[b] = active;
     T ss = T(0);
-    for (int j = 0; j < nv; ++j) ss += Gv[j * 64 + lane] * Gv[j * 64 + lane];
-    const T d2 = P[nv * 64 + lane] - ss;
+    for (int j = 0; j < nv; ++j) ss += Gv[j * kTriS + sl] * Gv[j * kTriS + sl];
+    const T n1 = P[nv * kTriS + sl];
+    const T d2 = n1 - ss;
     const T next_norm = d2 < T(0) ? T(0) : __builtin_sqrt(d2);  // NaN stays NaN
-    auto col = [&](int i) {
-      return (G.G1[(size_t)i * Bp + b] + Gv[i * 64 + lane]) - G.Cg[(size_t)i * Bp + b];
-    };
-    T carry = col(0);
-    if (active) G.Hu[(size_t)it * Bp + b] = carry;
+    T carry = Col[sl];
     for (int ri = 0; ri < it; ++ri) {
-      const T c = G.cs[(size_t)ri * Bp + b], s = G.sn[(size_t)ri * Bp + b];
-      const T f = carry, sc = col(ri + 1);
-      if (active) {
-        G.Hu[((size_t)(ri + 1) * R + it) * Bp + b] = sc;
-        G.H[((size_t)ri * R + it) * Bp + b] = c * f + s * sc;
-      }
+      const T c = Cs[ri * kTriS + sl], s = Sn[ri * kTriS + sl];
+      const T f = carry, sc = Col[(ri + 1) * kTriS + sl];
+      if (active) G.H[((size_t)ri * R + it) * Bp + b] = c * f + s * sc;
       carry = -s * f + c * sc;
     }
     const T diag = carry, sub = next_norm;
@@ -814,25 +828,25 @@ __global__ __launch_bounds__(1024) void k_gm_tri(Gm<T> G, int it, const T* __res
       G.steps[b] = it + 1;
     }
     const T est = absv(rn);
-    // |y1|^2 is finite exactly when y1 and hence (y1 - V g2) / nu are
-    const bool finite_ok = finite(est) && finite(rnorm) && finite(P[nv * 64 + lane]);
+    // |y1|^2 is finite exactly when y1, and hence (y1 - V g2) / nu, is
+    const bool finite_ok = finite(est) && finite(rnorm) && finite(n1);
     const bool happy = next_norm <= brk;
     const int still = (active && finite_ok && !happy && est > G.thr[b]) ? 1 : 0;
     G.act[b] = still;
     G.Tm[(size_t)(it + 1) * trow + (size_t)(it + 1) * tcol + b] = active ? inv : T(0);
-    s_inv[lane] = inv;
-    s_keep[lane] = active;
+    s_inv[sl] = inv;
+    s_keep[sl] = active;
     if (still && b < G.batch) atomicAdd(&G.stepcnt[it + 1], 1);
   }
   __syncthreads();
   // column it + 1 of Tm: v_{it+1} = (Z_{it+1} - Z Tm g2) / nu, and u = g2 / nu
-  const T inv = s_inv[lane];
-  const bool keep = s_keep[lane] != 0;
-  for (int i = wave; i < nv; i += 16) {
+  const T inv = s_inv[sl];
+  const bool keep = s_keep[sl] != 0;
+  for (int i = worker; i < nv; i += 64) {
     T acc = T(0);
-    for (int j = i; j < nv; ++j) acc += Tm[i * trow + j * tcol] * Gv[j * 64 + lane];
+    for (int j = i; j < nv; ++j) acc += Tm[i * trow + j * tcol] * Gv[j * kTriS + sl];
     G.Tm[(size_t)i * trow + (size_t)(it + 1) * tcol + b] = keep ? -(acc * inv) : T(0);
-    G.U2[(size_t)i * Bp + b] = keep ? Gv[i * 64 + lane] * inv : T(0);
+    G.U2[(size_t)i * Bp + b] = keep ? Gv[i * kTriS + sl] * inv : T(0);
   }
 }
 
@@ -1465,9 +1479,11 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                               (int64_t)nchunk2}));
     return PURIN_CP_OK;
   };
+  // the update-and-dot pass: two blocks per CU over the batch tiles (as fast
+  // as more, and fewer chunk partials for the per-sample reduction)
   auto launch_gs = [&](auto kern, int nv, T* img, const T* h) -> int {
-    int64_t chunks = 1;
-    if (int rc = resident_chunks(kern, &chunks)) return rc;
+    const int64_t chunks = std::max<int64_t>(
+        1, std::min<int64_t>({(int64_t)2 * cus / tiles0, (W + 3) / 4, (int64_t)nchunk2}));
     const int64_t rpb = (W + chunks - 1) / chunks;
     last_nchunk = (int)chunks;
     kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, vstride, nv, img, h, W, Bp,
@@ -1585,8 +1601,8 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   k_fill<T><<<eb, 256, 0, st>>>(X, total, T(0));
   PURIN_HIP(hipMemcpyAsync(Rr, Gr, vec, hipMemcpyDeviceToDevice, st));  // r = g - A(0)
 
-  const dim3 tri_grid((unsigned)(Bp / 64));
-  const size_t tri_lds = (size_t)(2 * restart + 3) * 64 * es;
+  const dim3 tri_grid((unsigned)(Bp / kTriS));
+  const size_t tri_lds = (size_t)(5 * restart + 4) * kTriS * es;
   PURIN_HIP(hipFuncSetAttribute((const void*)k_gm_tri<T, 1>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)tri_lds));
   PURIN_HIP(hipFuncSetAttribute((const void*)k_gm_tri<T, 2>,
