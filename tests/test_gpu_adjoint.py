@@ -222,3 +222,44 @@ def test_default_gmres_tolerance_parity():
     np.testing.assert_array_equal(to_np(adj.info), want.info)
     assert rel_err(to_np(adj.g_target), want.g_target) <= 1e-8
     assert rel_err(to_np(adj.g_rhs), want.g_rhs) <= 1e-8
+
+
+@pytest.mark.parametrize("dtype,restart", [(np.float64, 3), (np.float64, 45), (np.float32, 45)])
+def test_vjp_restart_lengths(dtype, restart):
+    """GMRES restart lengths other than the default: many short cycles (3), and a
+    prefix beyond the 32-vector kernels (45), which takes the generic
+    Gram-Schmidt passes.  Both against the oracle at the same saved state."""
+    from oracle import adjoint as oadj
+
+    B = 24
+    w = workloads.small_random(41, n=40, me=6, mi=12, width=4, batch=B, accelerated=True)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+    target = w.target.astype(dtype)
+    cot = np.random.default_rng(13).normal(size=(B, canon.n)).astype(dtype)
+    # fp32 cannot reach 1e-9: every sample stops at the iteration limit (info 1)
+    gtol, gmax = (1e-14, 300) if dtype == np.float64 else (1e-9, 100)
+    cfg = op.Config(accelerated=True, max_iterations=400, early_stop=False,
+                    gmres_tolerance=gtol, gmres_restart=restart, gmres_max_iterations=gmax)
+    plan, pre, o, saved = _solve_state(canon, target, rhs, cfg, dtype, accelerated=True)
+    ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
+    want = oadj.adjoint(pre.kept_values[0], ksup, kmask, canon.me, to_np(o.y), to_np(o.dual),
+                        np.ones(B, bool), target, pre.kept_rhs, pre.lower, pre.upper, cot, cfg)
+    adj = plan.adjoint(saved, target, pre.kept_rhs, cot, force_eligible=True, rhs_rows=plan.m,
+                       tolerance=gtol, restart=restart, max_iterations=gmax)
+    np.testing.assert_array_equal(to_np(adj.info), want.info)
+    np.testing.assert_array_equal(to_np(adj.valid), want.valid)
+    if dtype == np.float64:
+        # converged samples to 1e-10; a sample that restarted GMRES(3) leaves at
+        # the iteration limit (residual ~1e-11) is fixed only to about that
+        # residual times the conditioning, and is held to 1e-8
+        conv = want.info == 0
+        assert conv.sum() >= B // 2
+        gt, gr = to_np(adj.g_target), to_np(adj.g_rhs)
+        assert rel_err(gt[conv], want.g_target[conv]) <= 1e-10
+        assert rel_err(gr[conv], want.g_rhs[conv]) <= 1e-10
+        assert rel_err(gt, want.g_target) <= 1e-8
+        assert rel_err(gr, want.g_rhs) <= 1e-8
+    else:
+        assert rel_err(to_np(adj.g_target), want.g_target) <= 1e-4
+        assert rel_err(to_np(adj.g_rhs), want.g_rhs) <= 1e-4
