@@ -225,27 +225,35 @@ __global__ __launch_bounds__(kBlock) void k_lin_cols(Adj<T> S, const T* __restri
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_op_cols1(Adj<T> S, const T* __restrict__ v,
                                                      T* __restrict__ out) {
-  const int64_t total = (int64_t)S.n * S.Bp;
-  const int64_t boff = (int64_t)(S.n + S.m) * S.Bp;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    int64_t j = 0, b = 0;
-    if (S.vsc || S.dg) {
-      j = e / S.Bp;
-      b = e - j * S.Bp;
-    }
-    T gy = v[e], gb = v[boff + e];
+  using V = typename Lane<T>::V;
+  constexpr int Sn = Lane<T>::S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * Sn;
+  const V sc = S.vsc ? vload(S.vsc + b0) : vsplat<T>(T(1));
+  for (int cb = blockIdx.y; cb * 4 < S.n; cb += gridDim.y) {
+    const int j = cb * 4 + wave;
+    if (j >= S.n) continue;
+    const size_t off = (size_t)j * S.Bp + b0;
+    const size_t boff = (size_t)(S.n + S.m + j) * S.Bp + b0;
+    V gy = vload(v + off), gb = vload(v + boff);
     if (S.vsc) {
-      gy *= S.vsc[b];
-      gb *= S.vsc[b];
+      gy = gy * sc;
+      gb = gb * sc;
     }
-    const T u = S.Cm[e] * (gy + T(2) * gb);
+    const V u = vload(S.Cm + off) * (gy + T(2) * gb);
     if (S.dg) {
-      S.U[e] = adj_d(S, j, b) * u;
-      out[e] = gy - (adj_a(S, j, b) * u - gb);
+      V du, o;
+#pragma unroll
+      for (int s = 0; s < Sn; ++s) {
+        du[s] = adj_d(S, j, b0 + s) * u[s];
+        o[s] = gy[s] - (adj_a(S, j, b0 + s) * u[s] - gb[s]);
+      }
+      vstore(S.U + off, du);
+      vstore(out + off, o);
     } else {
-      S.U[e] = u;
-      out[e] = gy - (S.a * u - gb);
+      vstore(S.U + off, u);
+      vstore(out + off, gy - (S.a * u - gb));
     }
   }
 }
@@ -1443,7 +1451,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   // out = A (vsc . v), vsc a per-sample scale or nullptr
   auto op = [&](const T* v, T* out, const T* vsc) {
     S.vsc = vsc;
-    k_op_cols1<T><<<eb, 256, 0, st>>>(S, v, out);
+    k_op_cols1<T><<<gcol, kBlock, 0, st>>>(S, v, out);
     if (m) k_op_rows<T><<<grow, kBlock, 0, st>>>(S, v, out);
     k_op_cols2<T><<<gcol, kBlock, 0, st>>>(S, v, out);
     S.vsc = nullptr;

@@ -116,7 +116,7 @@ def test_dense_adjoint_matches_oracle_at_the_same_state(with_dual_cotangent, tol
     gradients agree to 1e-9; at the reference's 1e-6 the unconverged iterate
     depends on the rounding of the global dot products (summed in another
     order), and agrees to 10 x that tolerance.  The iteration counts agree to
-    one (the last stop test can flip under rounding)."""
+    two (the last stop test moves with the operator's rounding)."""
     require_gpu()
     q, c, A, b, C, d, lo, hi = _problem(53, B=8, n=10, me=2, mi=4)
     B, n = q.shape
@@ -135,8 +135,10 @@ def test_dense_adjoint_matches_oracle_at_the_same_state(with_dual_cotangent, tol
                              cot_dual=cotd if with_dual_cotangent else None, tolerance=tol,
                              max_iterations=iters)
     stats = plan.last_adjoint_stats()
-    # the stop test |r|^2 <= atol2 can flip by one iteration under rounding
-    assert abs(stats["arnoldi_steps"] - want[5]) <= 1 and want[5] > 0
+    # the first iteration under the stop threshold moves with the operator's
+    # rounding: with unit-roundoff noise on each operator output the oracle's
+    # own count spans 59-61 here (10 noise seeds, tolerance 1e-12)
+    assert abs(stats["arnoldi_steps"] - want[5]) <= 2 and want[5] > 0
     np.testing.assert_array_equal(to_np(got.g_q), 0.0)
     for name, w in (("g_c", want[0]), ("g_values", want[1].reshape(B, -1)), ("g_rhs", want[2]),
                     ("g_lower", want[3]), ("g_upper", want[4])):
