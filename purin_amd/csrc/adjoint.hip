@@ -69,6 +69,7 @@ struct Adj {
   T* Spre;
   int factored;  // the dense adapter's prox arithmetic a ((y - tau t) - tau c)
   const T* vsc;  // [Bp] per-sample scale of the operator's input, or nullptr
+  int64_t ldv;   // row stride of the operator's input and output (Bp, or a basis slot's)
   const T* Cm;   // n x Bp
   const T* Dm;   // m x Bp
   T* U;          // n x Bp scratch (u)
@@ -235,8 +236,9 @@ __global__ __launch_bounds__(kBlock) void k_op_cols1(Adj<T> S, const T* __restri
     const int j = cb * 4 + wave;
     if (j >= S.n) continue;
     const size_t off = (size_t)j * S.Bp + b0;
-    const size_t boff = (size_t)(S.n + S.m + j) * S.Bp + b0;
-    V gy = vload(v + off), gb = vload(v + boff);
+    const size_t voff = (size_t)j * S.ldv + b0;
+    const size_t boff = (size_t)(S.n + S.m + j) * S.ldv + b0;
+    V gy = vload(v + voff), gb = vload(v + boff);
     if (S.vsc) {
       gy = gy * sc;
       gb = gb * sc;
@@ -250,10 +252,10 @@ __global__ __launch_bounds__(kBlock) void k_op_cols1(Adj<T> S, const T* __restri
         o[s] = gy[s] - (adj_a(S, j, b0 + s) * u[s] - gb[s]);
       }
       vstore(S.U + off, du);
-      vstore(out + off, o);
+      vstore(out + voff, o);
     } else {
       vstore(S.U + off, u);
-      vstore(out + off, gy - (S.a * u - gb));
+      vstore(out + voff, gy - (S.a * u - gb));
     }
   }
 }
@@ -274,7 +276,7 @@ __global__ __launch_bounds__(kBlock) void k_op_rows(Adj<T> S, const T* __restric
     for (int k = S.K.rptr[i]; k < S.K.rptr[i + 1]; ++k)
       acc += row_coef(S.K, k, b0) * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
     const size_t off = (size_t)i * S.Bp + b0;
-    const size_t voff = (size_t)(S.n + i) * S.Bp + b0;
+    const size_t voff = (size_t)(S.n + i) * S.ldv + b0;
     V gd = vload(v + voff);
     if (S.vsc) gd = gd * vload(S.vsc + b0);
     if (S.dg) {
@@ -306,7 +308,7 @@ __global__ __launch_bounds__(kBlock) void k_op_cols2(Adj<T> S, const T* __restri
     V acc = vsplat<T>(T(0));
     for (int k = S.K.cptr[j]; k < S.K.cptr[j + 1]; ++k)
       acc += col_coef(S.K, k, b0) * vload(S.Wv + (size_t)S.K.cidx[k] * S.Bp + b0);
-    const size_t off = (size_t)(S.n + S.m + j) * S.Bp + b0;
+    const size_t off = (size_t)(S.n + S.m + j) * S.ldv + b0;
     V gb = vload(v + off);
     if (S.vsc) gb = gb * vload(S.vsc + b0);
     if (S.dg)
@@ -328,7 +330,8 @@ __global__ __launch_bounds__(kBlock) void k_op_cols2(Adj<T> S, const T* __restri
 template <typename T, int MODE>
 __global__ __launch_bounds__(kBlock) void k_gs(const T* __restrict__ basis, int64_t vstride,
                                                int nv, T* x, const T* __restrict__ h,
-                                               int64_t W, int64_t Bp, T* part, int nchunk) {
+                                               int64_t W, int64_t Bp, T* part, int nchunk,
+                                               int64_t ld) {
   using V = typename Lane<T>::V;
   constexpr int Sn = Lane<T>::S;
   const int lane = threadIdx.x & 63;
@@ -340,18 +343,18 @@ __global__ __launch_bounds__(kBlock) void k_gs(const T* __restrict__ basis, int6
   V xr[kRowsPerThread];
 #pragma unroll
   for (int r = 0; r < kRowsPerThread; ++r)
-    xr[r] = (r0 + r < W) ? vload(x + (size_t)(r0 + r) * Bp + b0) : vsplat<T>(T(0));
+    xr[r] = (r0 + r < W) ? vload(x + (size_t)(r0 + r) * ld + b0) : vsplat<T>(T(0));
   if (MODE == 1 || MODE == 2 || MODE == 5) {
     for (int i = 0; i < nv; ++i) {
       const V hi = vload(h + (size_t)i * Bp + b0);
       const T* vi = basis + (size_t)i * vstride;
 #pragma unroll
       for (int r = 0; r < kRowsPerThread; ++r)
-        if (r0 + r < W) xr[r] = xr[r] - hi * vload(vi + (size_t)(r0 + r) * Bp + b0);
+        if (r0 + r < W) xr[r] = xr[r] - hi * vload(vi + (size_t)(r0 + r) * ld + b0);
     }
 #pragma unroll
     for (int r = 0; r < kRowsPerThread; ++r)
-      if (r0 + r < W) vstore(x + (size_t)(r0 + r) * Bp + b0, xr[r]);
+      if (r0 + r < W) vstore(x + (size_t)(r0 + r) * ld + b0, xr[r]);
   }
   const size_t plane = (size_t)nchunk * Bp;
   if (MODE == 0 || MODE == 1 || MODE == 5) {
@@ -360,7 +363,7 @@ __global__ __launch_bounds__(kBlock) void k_gs(const T* __restrict__ basis, int6
       V acc = vsplat<T>(T(0));
 #pragma unroll
       for (int r = 0; r < kRowsPerThread; ++r)
-        if (r0 + r < W) acc += vload(vi + (size_t)(r0 + r) * Bp + b0) * xr[r];
+        if (r0 + r < W) acc += vload(vi + (size_t)(r0 + r) * ld + b0) * xr[r];
       const V tot = block_combine<T>(acc, buf, OpAdd());
       if (wave == 0) vstore(part + (size_t)i * plane + (size_t)c * Bp + b0, tot);
     }
@@ -427,7 +430,7 @@ __global__ __launch_bounds__(kBlock) void k_gs_dots_rows(const T* __restrict__ b
                                                          int64_t vstride, int nv,
                                                          const T* __restrict__ x, int64_t W,
                                                          int64_t Bp, T* part, int nchunk,
-                                                         int64_t rpb) {
+                                                         int64_t rpb, int64_t ld) {
   using V = typename Lane<T>::V;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -441,7 +444,7 @@ __global__ __launch_bounds__(kBlock) void k_gs_dots_rows(const T* __restrict__ b
 #pragma unroll
   for (int i = 0; i < NV; ++i) acc[i] = V(T(0));
   for (int64_t r = r_begin; r < r_end; ++r) {
-    const size_t off = (size_t)r * Bp + b0;
+    const size_t off = (size_t)r * ld + b0;
     const V xr = vload(x + off);
 #pragma unroll
     for (int i = 0; i < NV; ++i)
@@ -473,7 +476,7 @@ __global__ __launch_bounds__(kBlock) void k_gs_dots_rows(const T* __restrict__ b
 template <typename T, int NV>
 __global__ __launch_bounds__(kBlock) void k_gs_dots(const T* __restrict__ basis, int64_t vstride,
                                                     int nv, const T* __restrict__ x, int64_t W,
-                                                    int64_t Bp, T* part, int nchunk, int64_t rpb) {
+                                                    int64_t Bp, T* part, int nchunk, int64_t rpb, int64_t ld) {
   using V = typename Lane<T>::V;
   constexpr int Sn = Lane<T>::S;
   constexpr int NW = NV / 4;
@@ -497,7 +500,7 @@ __global__ __launch_bounds__(kBlock) void k_gs_dots(const T* __restrict__ basis,
   const int64_t r_begin = (int64_t)c * rpb;
   const int64_t r_end = std::min<int64_t>(W, r_begin + rpb);
   for (int64_t r = r_begin; r < r_end; ++r) {
-    const size_t off = (size_t)r * Bp + b0;
+    const size_t off = (size_t)r * ld + b0;
     const V xr = vload(x + off);
     V v[NW];
 #pragma unroll
@@ -528,7 +531,7 @@ __global__ __launch_bounds__(kBlock) void k_gs_update_dots(const T* __restrict__
                                                            int64_t vstride, int nv, T* x,
                                                            const T* __restrict__ h, int64_t W,
                                                            int64_t Bp, T* part, int nchunk,
-                                                           int64_t rpb) {
+                                                           int64_t rpb, int64_t ld) {
   using V = typename Lane<T>::V;
   constexpr int Sn = Lane<T>::S;
   constexpr int NW = NV / 4;  // vectors per wavefront
@@ -549,7 +552,7 @@ __global__ __launch_bounds__(kBlock) void k_gs_update_dots(const T* __restrict__
   int g = 0;
   for (int64_t r = r_begin; r < r_end; r += 2, ++g) {
     const bool two = r + 1 < r_end;
-    const size_t off0 = (size_t)r * Bp + b0, off1 = off0 + (size_t)Bp;
+    const size_t off0 = (size_t)r * ld + b0, off1 = off0 + (size_t)ld;
     const V x0 = vload(x + off0);
     const V x1 = two ? vload(x + off1) : vsplat<T>(T(0));
     V v0[NW], v1[NW];
@@ -608,27 +611,30 @@ __global__ void k_axpby(int64_t total, T* out, const T* __restrict__ a, const T*
 
 // V0 = r / max(beta, eps) per sample
 template <typename T>
-__global__ void k_scale_cols(int64_t total, int64_t Bp, T* out, const T* __restrict__ in,
-                             const T* __restrict__ scale, const int32_t* __restrict__ keep) {
+__global__ void k_scale_cols(int64_t total, int64_t Bp, T* out, int64_t ldo,
+                             const T* __restrict__ in, const T* __restrict__ scale,
+                             const int32_t* __restrict__ keep) {
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = e % Bp;
-    out[e] = (keep == nullptr || keep[b]) ? in[e] * scale[b] : T(0);
+    const int64_t row = e / Bp, b = e - row * Bp;
+    out[row * ldo + b] = (keep == nullptr || keep[b]) ? in[e] * scale[b] : T(0);
   }
 }
 
-// x += sum_{i < row_steps[b]} coeff_i V_i
+// x += sum_{i < row_steps[b]} coeff_i V_i, with V_i at basis + i * vstride and
+// row stride ld
 template <typename T>
 __global__ void k_correction(int64_t total, int64_t Bp, T* x, const T* __restrict__ basis,
-                             int64_t vstride, const T* __restrict__ coeff,
+                             int64_t vstride, int64_t ld, const T* __restrict__ coeff,
                              const int32_t* __restrict__ steps) {
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = e % Bp;
+    const int64_t row = e / Bp, b = e - row * Bp;
     const int k = steps[b];
     if (k == 0) continue;
+    const T* vr = basis + row * ld + b;
     T acc = T(0);
-    for (int i = 0; i < k; ++i) acc += coeff[(size_t)i * Bp + b] * basis[(size_t)i * vstride + e];
+    for (int i = 0; i < k; ++i) acc += coeff[(size_t)i * Bp + b] * vr[(size_t)i * vstride];
     x[e] = x[e] + acc;
   }
 }
@@ -1352,7 +1358,11 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   char* ws = (char*)workspace(p, o_, st, &err, true);
   if (!ws) return err;
   T* Vb = (T*)(ws + oV);
+  // GMRES basis: slot i, row r, sample b at r * zld + i * zs + b (the rows of all
+  // slots interleaved, so a pass over the prefix reads one contiguous run per
+  // row); the dense BiCGSTAB keeps contiguous vectors of vstride elements
   const int64_t vstride = W * Bp;
+  const int64_t zs = Bp, zld = (int64_t)(restart + 1) * Bp;
   T* X = (T*)(ws + oX);
   T* Gr = (T*)(ws + oG);
   T* Rr = (T*)(ws + oRr);
@@ -1370,6 +1380,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   Adj<T> S{};
   S.K = kept_matrix<T>(p, true);
   S.Bp = Bp;
+  S.ldv = Bp;
   S.n = (int)n;
   S.m = (int)m;
   const T tau = (T)p->tau_adj;
@@ -1449,12 +1460,14 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   k_lin_cols<T><<<gcol, kBlock, 0, st>>>(S, Y, Tt, LO, HI, shared, (const T*)(ws + oDp),
                                           (T*)(ws + oCm), (T*)(ws + oClo), (T*)(ws + oChi));
   // out = A (vsc . v), vsc a per-sample scale or nullptr
-  auto op = [&](const T* v, T* out, const T* vsc) {
+  auto op = [&](const T* v, T* out, const T* vsc, int64_t ldv) {
     S.vsc = vsc;
+    S.ldv = ldv;
     k_op_cols1<T><<<gcol, kBlock, 0, st>>>(S, v, out);
     if (m) k_op_rows<T><<<grow, kBlock, 0, st>>>(S, v, out);
     k_op_cols2<T><<<gcol, kBlock, 0, st>>>(S, v, out);
     S.vsc = nullptr;
+    S.ldv = Bp;
   };
   auto reduce = [&](int mode_nv, T* out, int opk) {
     k_reduce<T><<<(unsigned)((mode_nv * Bp + 255) / 256), 256, 0, st>>>(part, mode_nv, nchunk, Bp,
@@ -1494,8 +1507,8 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
         1, std::min<int64_t>({(int64_t)2 * cus / tiles0, (W + 3) / 4, (int64_t)nchunk2}));
     const int64_t rpb = (W + chunks - 1) / chunks;
     last_nchunk = (int)chunks;
-    kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, vstride, nv, img, h, W, Bp,
-                                                                    part, (int)chunks, rpb);
+    kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, zs, nv, img, h, W, Bp,
+                                                                    part, (int)chunks, rpb, zld);
     return PURIN_CP_OK;
   };
   auto launch_rows = [&](auto kern, int nv, const T* img) -> int {
@@ -1503,8 +1516,8 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     if (int rc = resident_chunks(kern, &chunks)) return rc;
     const int64_t rpb = (W + chunks - 1) / chunks;
     last_nchunk = (int)chunks;
-    kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, vstride, nv, img, W, Bp,
-                                                                    part, (int)chunks, rpb);
+    kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, zs, nv, img, W, Bp,
+                                                                    part, (int)chunks, rpb, zld);
     return PURIN_CP_OK;
   };
   // the dot pass: two blocks per CU over the batch tiles (the best measured
@@ -1514,8 +1527,8 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
         1, std::min<int64_t>({(int64_t)2 * cus / tiles0, (W + 3) / 4, (int64_t)nchunk2}));
     const int64_t rpb = (W + chunks - 1) / chunks;
     last_nchunk = (int)chunks;
-    kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, vstride, nv, img, W, Bp,
-                                                                    part, (int)chunks, rpb);
+    kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, zs, nv, img, W, Bp,
+                                                                    part, (int)chunks, rpb, zld);
     return PURIN_CP_OK;
   };
   // pass A (mode 0): part_i = Z_i . y; pass B (mode 1): y <- y - sum_i h_i Z_i,
@@ -1585,12 +1598,12 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
       dot(RH, Rr, kRho_);
       k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 1, T(0), T(0));
       bi_vec(0);
-      op(Pv, Qv, nullptr);
+      op(Pv, Qv, nullptr, Bp);
       dot(RH, Qv, kRQ);
       k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 2, T(0), T(0));
       bi_vec(1);
       dot(Sv, Sv, kSS);
-      op(Sv, Tv, nullptr);
+      op(Sv, Tv, nullptr, Bp);
       dot(Tv, Sv, kTS);
       dot(Tv, Tv, kTT);
       k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 3, T(0), T(0));
@@ -1603,7 +1616,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     k_fill_weights<T><<<sb, 256, 0, st>>>(batch, Bp, lam_w);
   } else {
   // threshold = max(atol, tol * max|g|) and residual_inf = max|g - A 0| = max|g|
-  k_gs<T, 4><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Gr, nullptr, W, Bp, part, nchunk);
+  k_gs<T, 4><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Gr, nullptr, W, Bp, part, nchunk, Bp);
   reduce(1, S1, 1);
   k_gm_thresholds<T><<<sb, 256, 0, st>>>(G, S1, (T)o.tolerance, (T)o.atol);
   k_fill<T><<<eb, 256, 0, st>>>(X, total, T(0));
@@ -1625,11 +1638,11 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     const int cycle_limit = (int)std::min<int64_t>(restart, o.max_iterations - completed);
     ++p->adjoint_stats.cycles;
     // beta = ||r||, V0 = r / max(beta, eps)
-    k_gs<T, 3><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Rr, nullptr, W, Bp, part, nchunk);
+    k_gs<T, 3><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Rr, nullptr, W, Bp, part, nchunk, Bp);
     reduce(1, S1, 0);
     k_fill<int32_t><<<1, 256, 0, st>>>(G.stepcnt, restart + 2, 0);
     k_gm_cycle_init<T><<<sb, 256, 0, st>>>(G, S1);
-    k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, Vb, Rr, G.scale, nullptr);
+    k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, Vb, zld, Rr, G.scale, nullptr);
     // Arnoldi steps.  The reference loop runs step s while s < cycle_limit and
     // some sample is active at its start (operators.py:943-1082); a step with
     // no active sample changes no state here (every update is masked by the
@@ -1645,16 +1658,16 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
       for (int it = launched; it < chunk_end; ++it) {
         // slot it holds Z_it; y = A (Z_it Tm[it][it]) goes to slot it + 1, where
         // pass B turns it into Z_{it+1}
-        T* zk = Vb + (size_t)it * vstride;
-        T* img = Vb + (size_t)(it + 1) * vstride;
+        T* zk = Vb + (size_t)it * zs;
+        T* img = Vb + (size_t)(it + 1) * zs;
         const int nv = it + 1;
-        op(zk, img, G.Tm + ((size_t)it * (restart + 1) + it) * Bp);
+        op(zk, img, G.Tm + ((size_t)it * (restart + 1) + it) * Bp, zld);
         int nch = nchunk;
         if (nv <= 32) {
           if (int rc = gs_pass(0, nv, img, nullptr)) return rc;
           nch = last_nchunk;
         } else {
-          k_gs<T, 0><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, nullptr, W, Bp, part, nchunk);
+          k_gs<T, 0><<<ggs, kBlock, 0, st>>>(Vb, zs, nv, img, nullptr, W, Bp, part, nchunk, zld);
         }
         k_gm_tri<T, 1><<<tri_grid, 1024, tri_lds, st>>>(G, it, part, nch);
         nch = nchunk;
@@ -1662,7 +1675,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
           if (int rc = gs_pass(1, nv, img, G.Q1)) return rc;
           nch = last_nchunk;
         } else {
-          k_gs<T, 5><<<ggs, kBlock, 0, st>>>(Vb, vstride, nv, img, G.Q1, W, Bp, part, nchunk);
+          k_gs<T, 5><<<ggs, kBlock, 0, st>>>(Vb, zs, nv, img, G.Q1, W, Bp, part, nchunk, zld);
         }
         k_gm_tri<T, 2><<<tri_grid, 1024, tri_lds, st>>>(G, it, part, nch);
       }
@@ -1677,18 +1690,18 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
       }
     k_gm_backsub<T><<<(unsigned)(Bp / 64), 64, (size_t)restart * 64 * sizeof(T), st>>>(G);
     k_gm_tcoef<T><<<dim3((unsigned)((Bp + 255) / 256), (unsigned)restart), 256, 0, st>>>(G);
-    k_correction<T><<<eb, 256, 0, st>>>(total, Bp, X, Vb, vstride, G.Wc, G.steps);
+    k_correction<T><<<eb, 256, 0, st>>>(total, Bp, X, Vb, zs, zld, G.Wc, G.steps);
     // candidate residual r = g - A x (operators.py:1084-1091)
-    op(X, T1, nullptr);
+    op(X, T1, nullptr, Bp);
     k_axpby<T><<<eb, 256, 0, st>>>(total, Rr, Gr, T1, T(-1));
-    k_gs<T, 4><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Rr, nullptr, W, Bp, part, nchunk);
+    k_gs<T, 4><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Rr, nullptr, W, Bp, part, nchunk, Bp);
     reduce(1, S1, 1);
     k_gm_cycle_end<T><<<sb, 256, 0, st>>>(G, S1);
     completed += it;
     p->adjoint_stats.arnoldi_steps += it;
   }
   // finiteness of the solution, info, valid (operators.py:1119-1122, bounds.py:148-153)
-  k_gs<T, 2><<<ggs, kBlock, 0, st>>>(Vb, vstride, 0, X, nullptr, W, Bp, part, nchunk);
+  k_gs<T, 2><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, X, nullptr, W, Bp, part, nchunk, Bp);
   k_reduce<T><<<sb, 256, 0, st>>>(part + (size_t)nchunk * Bp, 1, nchunk, Bp, S2, 2);
   k_gm_finish<T><<<sb, 256, 0, st>>>(G, S2, conv, (T)o.adjoint_tolerance, o.force_eligible,
                                      lam_w, valid, info, gres);
