@@ -178,7 +178,8 @@ def run_mode(args, torch):
     (purin_cp_project_values), the general diagonal QP (purin_cp_qp_solve) and the
     dense adapter (purin_cp_dense_solve).  Streaming passes; the roofline is the
     dominant pass with its algorithmic bytes, which include the per-sample
-    coefficients each pass reads (B * ws * nnz)."""
+    coefficients each pass reads (B * ws * nnz) where the coefficients are per
+    sample (values, dense); the QP here uses the plan's shared coefficients."""
     from purin_amd import workloads
     from purin_amd.plan import Plan
 
@@ -216,10 +217,12 @@ def run_mode(args, torch):
                                                       early_stop=False, timing=timing)
             extra_n = 1  # q and c replace the candidates: one more n-vector per iteration
         n, m, nnz = w.n, plan.m, int(plan.info.nnz_kept)
+        # the QP with the plan's own coefficients reads one shared copy of them
+        coef_nnz = 0 if args.mode == "qp" else nnz
         workload = {"values": "config2 rows and sparsity, per-sample values = shared values x "
                               "(1 + 0.1 U(-1,1)) (seed 7), batch 1024, fp64, accelerated CP, "
                               f"{iters} fixed iterations, full projection",
-                    "qp": "config2's 3072 general rows (shared coefficients, read per sample), "
+                    "qp": "config2's 3072 general rows (the plan's shared coefficients), "
                           "box [-1,1], q ~ U(0.5,2), c = -q yhat (seed 7), batch 1024, fp64, "
                           f"accelerated CP, {iters} fixed iterations"}[args.mode]
     else:
@@ -247,6 +250,7 @@ def run_mode(args, torch):
                                                      max_iterations=iters, early_stop=False,
                                                      timing=timing)
         m, nnz, extra_n = me + mi, int(indptr[-1]), 1
+        coef_nnz = nnz
         workload = (f"dense adapter: n={n}, {me} eq + {mi} ineq dense rows per sample N(0,1), "
                     f"feasible rhs, box [-1,1], q ~ U(0.5,2), c ~ N(0,1) (seed 7), batch {B}, "
                     f"fp64, fixed-step CP, {iters} fixed iterations")
@@ -258,12 +262,12 @@ def run_mode(args, torch):
     tm = plan.last_timing()
     it = max(int(tm["iterations"]), 1)
     row_ms, col_ms = tm["row_ms"] / it, tm["col_ms"] / it
-    bytes_row = B * ws * (n + 3 * m + nnz)                # gather ybar, d, r, d+ and the row entries
-    bytes_col = B * ws * ((4 + extra_n) * n + m + nnz)    # y, yhat (or q, c), writes, gather d+, entries
+    bytes_row = B * ws * (n + 3 * m + coef_nnz)               # gather ybar, d, r, d+, per-sample entries
+    bytes_col = B * ws * ((4 + extra_n) * n + m + coef_nnz)   # y, yhat (or q, c), writes, gather d+, entries
     dominant = "k_col_pass" if col_ms >= row_ms else "k_row_pass"
     dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == "k_col_pass" else (bytes_row, row_ms)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
-    bytes_iter = B * ws * ((5 + extra_n) * n + 3 * m + 2 * nnz)
+    bytes_iter = B * ws * ((5 + extra_n) * n + 3 * m + 2 * coef_nnz)
     iter_ms = tm["loop_ms"] / it
     line = {
         "metric": MODES[args.mode], "value": B / (ms_per_step / 1e3),

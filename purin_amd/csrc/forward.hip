@@ -75,6 +75,8 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values) {
     L.CVo = take(nnz * Bp * es);
     L.RV = take(nnz * Bp * es);
     L.CV = take(nnz * Bp * es);
+    L.RVs = take(std::max<size_t>(nnz, 1) * es);
+    L.CVs = take(std::max<size_t>(nnz, 1) * es);
     L.BC = take(nb * Bp * es);
     L.SC = take(m * Bp * es);
     if (p->diag) {
@@ -123,6 +125,13 @@ static void ps_power(const purin_cp_plan* p, hipStream_t st, const Layout& L, ch
     k_ps_normalize<T><<<1024, 256, 0, st>>>(n, Bp, Wv, ww, eps, X);
   }
   k_ps_norm_final<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(Bp, eig, eps, Lout);
+}
+
+// dst[k] = src[k][0]: sample 0's entry of each row of a [count][Bp] array
+template <typename T>
+__global__ void k_sample0(const T* __restrict__ src, int64_t Bp, int64_t count, T* dst) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k < count) dst[k] = src[k * Bp];
 }
 
 template <typename T>
@@ -196,6 +205,19 @@ int prepare_values(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
       Bp, rpart, (int)(m ? L.nrb : 0), cpart, L.ncb, power ? Lpi : nullptr, safety,
       adjoint ? 0 : p->opts.accelerated, tol, qp ? qmax : nullptr, qp ? qmin : nullptr, ps->tau_b,
       ps->sig_b, ps->a_b, ps->d_b, ps->th_b, ps->tol_b);
+  // with the plan's own coefficients every sample's scaled entries are the same
+  // (the same broadcast values through the same per-sample arithmetic), so the
+  // iterations can read one shared copy instead of B per-sample copies
+  ps->RVs = ps->CVs = nullptr;
+  if (!values && nnz) {
+    T* RVs = (T*)(ws + L.RVs);
+    T* CVs = (T*)(ws + L.CVs);
+    const unsigned g = (unsigned)((nnz + 255) / 256);
+    k_sample0<T><<<g, 256, 0, st>>>(RV, Bp, nnz, RVs);
+    k_sample0<T><<<g, 256, 0, st>>>(CV, Bp, nnz, CVs);
+    ps->RVs = RVs;
+    ps->CVs = CVs;
+  }
   PURIN_HIP(hipGetLastError());
   return PURIN_CP_OK;
 }
@@ -387,9 +409,14 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   A.ncb = L.ncb;
   A.nrb = L.nrb;
   if (ps) {  // per-sample coefficients: per-sample matrix entries and steps
-    A.K.rvb = ps->RV;
-    A.K.cvb = ps->CV;
-    A.K.vbp = Bp;
+    if (ps->RVs) {  // the plan's own coefficients: one shared copy
+      A.K.rval = ps->RVs;
+      A.K.cval = ps->CVs;
+    } else {
+      A.K.rvb = ps->RV;
+      A.K.cvb = ps->CV;
+      A.K.vbp = Bp;
+    }
     if (p->diag) {
       A.sig_rb = ps->sig_rb;
       A.a_cb = ps->a_cb;

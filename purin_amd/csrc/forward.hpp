@@ -20,6 +20,7 @@ struct Layout {
   // caller's order (VF), the kept CSR / CSC entries original (RVo, CVo) and
   // row-scaled (RV, CV), bound-row coefficients (BC), row scales (SC), steps
   size_t VF, RVo, CVo, RV, CV, BC, SC, SGR, ACB, DCB, STB, RPT, CPT, PX, PZ, PW, PD;
+  size_t RVs, CVs;    // [nnz] the scaled CSR / CSC entries when every sample has the plan's
   size_t QQ, QC, QS;  // general QP: q, c (n x Bp) and per-sample max q, min q
   size_t ws_end;
 };
@@ -33,6 +34,8 @@ struct PerSample {
   const T* CVo;   // [nnz][Bp] kept CSC entries, original
   const T* RV;    // [nnz][Bp] row-scaled CSR
   const T* CV;    // [nnz][Bp] row-scaled CSC
+  const T* RVs;   // [nnz] row-scaled CSR shared by every sample (the plan's own
+  const T* CVs;   //   coefficients: sample 0's entries of RV / CV), or nullptr
   const T* BC;    // [nb][Bp] bound-row coefficients
   const T* SC;    // [m][Bp] row scales
   T* sig_rb;      // [m][Bp] diagonal sigma, or nullptr

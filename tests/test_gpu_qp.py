@@ -123,9 +123,12 @@ def test_qp_step_variants_match_oracle(dtype, mode):
     np.testing.assert_array_equal(to_np(got.status), want.status)
 
 
-def test_qp_shared_values_and_warm_start():
+@pytest.mark.parametrize("early_stop", [False, True])
+def test_qp_shared_values_and_warm_start(early_stop):
     """values = None uses the plan's coefficients for every sample; a warm start
-    (y0, dual0) enters the iteration like the oracle's (diagonal_qp.py:240-273)."""
+    (y0, dual0) enters the iteration like the oracle's (diagonal_qp.py:240-273).
+    The shared path reads one copy of the scaled entries, the same bits as every
+    sample's copy when the values are passed per sample, so the two agree exactly."""
     require_gpu()
     rows, me, mi, n, support, mask, data = _problem(43, B=17)
     shared = data.values[0]
@@ -141,17 +144,20 @@ def test_qp_shared_values_and_warm_start():
     indices = np.asarray([c for r in rows for c in r], np.int32)
     plan = Plan(n, me, mi, indptr, indices, shared[mask], dtype=torch.float64,
                 bound_presolve=False, device="cuda")
-    cfg = Config(max_iterations=300, early_stop=False)
+    iters = 2000 if early_stop else 300
+    cfg = Config(max_iterations=iters, early_stop=early_stop)
     y0 = np.random.default_rng(2).uniform(-0.5, 0.5, (17, n))
     d0 = np.random.default_rng(3).normal(size=(17, me + mi))
     d0[:, me:] = np.abs(d0[:, me:])
     want = dq.solve(support, mask, me, data, cfg, y0=y0, dual0=d0)
     got = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, y0=y0, dual0=d0,
-                        max_iterations=300, early_stop=False)
+                        max_iterations=iters, early_stop=early_stop)
     assert rel_err(to_np(got.y), want.y) <= 1e-10
     got2 = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, y0=y0, dual0=d0,
-                         values=data.values[:, mask], max_iterations=300, early_stop=False)
-    assert rel_err(to_np(got2.y), to_np(got.y)) <= 1e-13
+                         values=data.values[:, mask], max_iterations=iters,
+                         early_stop=early_stop)
+    np.testing.assert_array_equal(to_np(got2.y), to_np(got.y))
+    np.testing.assert_array_equal(to_np(got2.iterations), to_np(got.iterations))
 
 
 @pytest.mark.parametrize("mode", ["scalar", "diagonal"])
