@@ -1403,9 +1403,14 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     if (int rc = prepare_values<T>(p, st, batch, Lv, wq, values, T(1), kQPAdjoint, qmax,
                                    qmax + Bp, &PS))
       return rc;
-    S.K.rvb = PS.RV;
-    S.K.cvb = PS.CV;
-    S.K.vbp = Bp;
+    if (PS.RVs) {  // the plan's own coefficients: one shared copy of the scaled entries
+      S.K.rval = PS.RVs;
+      S.K.cval = PS.CVs;
+    } else {
+      S.K.rvb = PS.RV;
+      S.K.cvb = PS.CV;
+      S.K.vbp = Bp;
+    }
     S.Q = QQ;
     S.Cc = QC;
     S.Spre = (T*)(ws + oSp);

@@ -193,6 +193,44 @@ def test_qp_vjp_matches_oracle_at_the_same_state(mode):
     assert np.abs(to_np(adj.g_q)).max() > 1e-3
 
 
+@pytest.mark.parametrize("mode", ["scalar", "diagonal"])
+def test_qp_adjoint_shared_values_equal_per_sample(mode):
+    """The QP's VJP with the plan's own coefficients (values = None: one shared
+    copy of the scaled entries) equals, bit for bit, the VJP with those
+    coefficients passed per sample."""
+    require_gpu()
+    rows, me, mi, n, support, mask, data = _problem(45, n=16, me=2, mi=5, width=3, B=20)
+    shared = data.values[0]
+    data = data._replace(values=np.broadcast_to(shared, data.values.shape).copy())
+    x0 = np.random.default_rng(6).uniform(-0.4, 0.4, (20, n))
+    data = data._replace(rhs=np.einsum("mw,bmw->bm", shared, x0[:, support]) + np.concatenate(
+        (np.zeros((20, me)), np.full((20, mi), 0.3)), axis=1))
+    kw = dict(diagonal_preconditioning=True) if mode == "diagonal" else {}
+    from purin_amd.plan import Plan
+    import torch
+
+    indptr = np.zeros(len(rows) + 1, np.int64)
+    indptr[1:] = np.cumsum([len(r) for r in rows])
+    indices = np.asarray([c for r in rows for c in r], np.int32)
+    plan = Plan(n, me, mi, indptr, indices, shared[mask], dtype=torch.float64,
+                bound_presolve=False, device="cuda", **kw)
+    rng = np.random.default_rng(7)
+    cot = rng.normal(size=(20, n))
+    cot_dual = rng.normal(size=(20, me + mi))
+    outs = []
+    for vals in (None, data.values[:, mask]):
+        fwd = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, values=vals,
+                            tolerance=1e-9, max_iterations=20000, save=True)
+        adj = plan.qp_adjoint(fwd.saved, data.q, data.c, cot, values=vals, cot_dual=cot_dual,
+                              tolerance=1e-12, max_iterations=200)
+        outs.append((fwd, adj))
+    (f0, a0), (f1, a1) = outs
+    np.testing.assert_array_equal(to_np(f0.y), to_np(f1.y))
+    for name in ("g_q", "g_c", "g_rhs", "g_lower", "g_upper"):
+        np.testing.assert_array_equal(to_np(getattr(a0, name)), to_np(getattr(a1, name)), name)
+    np.testing.assert_array_equal(to_np(a0.info), to_np(a1.info))
+
+
 @pytest.mark.parametrize("accelerated", [False, True])
 @pytest.mark.parametrize("scaling", [False, True])
 def test_qp_known_answer(accelerated, scaling):
