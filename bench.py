@@ -262,12 +262,13 @@ def run_mode(args, torch):
     tm = plan.last_timing()
     it = max(int(tm["iterations"]), 1)
     row_ms, col_ms = tm["row_ms"] / it, tm["col_ms"] / it
+    # these entry points take per-sample bounds: the column pass reads lower and upper (2n)
     bytes_row = B * ws * (n + 3 * m + coef_nnz)               # gather ybar, d, r, d+, per-sample entries
-    bytes_col = B * ws * ((4 + extra_n) * n + m + coef_nnz)   # y, yhat (or q, c), writes, gather d+, entries
+    bytes_col = B * ws * ((6 + extra_n) * n + m + coef_nnz)   # y, yhat (or q, c), bounds, writes, d+, entries
     dominant = "k_col_pass" if col_ms >= row_ms else "k_row_pass"
     dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == "k_col_pass" else (bytes_row, row_ms)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
-    bytes_iter = B * ws * ((5 + extra_n) * n + 3 * m + 2 * coef_nnz)
+    bytes_iter = B * ws * ((7 + extra_n) * n + 3 * m + 2 * coef_nnz)
     iter_ms = tm["loop_ms"] / it
     line = {
         "metric": MODES[args.mode], "value": B / (ms_per_step / 1e3),
