@@ -1398,7 +1398,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     T* qmax = (T*)(wq + Lv.QS);
     to_minor<T>(st, qa->q, batch, n, n, QQ, Bp, nullptr, 0);
     to_minor<T>(st, qa->c, batch, n, n, QC, Bp, nullptr, 0);
-    k_qp_stats<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(n, Bp, batch, QQ, LO, HI, qmax,
+    k_qp_stats<T><<<(unsigned)(Bp / 64), 1024, 0, st>>>(n, Bp, batch, QQ, LO, HI, qmax,
                                                               qmax + Bp, nullptr);
     if (int rc = prepare_values<T>(p, st, batch, Lv, wq, values, T(1), kQPAdjoint, qmax,
                                    qmax + Bp, &PS))

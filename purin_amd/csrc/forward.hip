@@ -84,7 +84,9 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values) {
       L.ACB = take(n * Bp * es);
       L.DCB = take(n * Bp * es);
     }
-    L.STB = take((size_t)7 * Bp * es);  // tau, sigma, a, delta, theta, tol, L
+    // tau, sigma, a, delta, theta, tol, L, then the schedule's second buffer
+    // (tau, sigma, a, delta, theta)
+    L.STB = take((size_t)12 * Bp * es);
     L.RPT = take((size_t)2 * std::max(L.nrb, 1) * Bp * es);
     L.CPT = take((size_t)std::max(L.ncb, 1) * Bp * es);
     L.PX = take(n * Bp * es);  // power iteration vectors and dots
@@ -476,6 +478,25 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     PURIN_HIP(hipMemcpyAsync(A.YB, A.tgt, (size_t)n * Bp * sizeof(T), hipMemcpyDeviceToDevice, st));
   }
   const T* qgam = qp ? qp->gamma : nullptr;
+  // per-sample accelerated schedule: two buffers of [5][Bp] (tau, sigma, a,
+  // delta, theta); the passes read ``cur`` and the column pass writes the next
+  // iteration's values into ``nxt``
+  T* cur = nullptr;
+  T* nxt = nullptr;
+  auto set_steps = [&]() {
+    A.tau_b = cur;
+    A.sig_b = cur + Bp;
+    A.a_b = cur + 2 * Bp;
+    A.d_b = cur + 3 * Bp;
+    A.th_b = cur + 4 * Bp;
+    A.sch_next = nxt;
+    A.gam = qgam;
+  };
+  if (ps && p->opts.accelerated && A.th_b) {
+    cur = ps->tau_b;           // [5][Bp] from the steps prepared for iteration 0
+    nxt = ps->tau_b + 7 * Bp;  // after tol and L
+    set_steps();
+  }
 
   const int check = o.check_every > 0 ? o.check_every : 32;
   const T one = T(1);
@@ -534,9 +555,11 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
                                                    nullptr, nullptr, nullptr, nullptr, nullptr);
     }
     if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 2], st));
-    if (p->opts.accelerated && A.th_b) {  // the same update, per sample
-      k_ps_sched<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(Bp, qgam, ps->tau_b, ps->sig_b,
-                                                                  ps->a_b, ps->d_b, ps->th_b);
+    if (p->opts.accelerated && A.th_b) {
+      // the same update, per sample: the column pass wrote the next steps into
+      // the other buffer; swap (kernels.py:279-283)
+      std::swap(cur, nxt);
+      set_steps();
     } else if (p->opts.accelerated) {  // kernels.py:279-283 with gamma = min q = 1
       const T nt = one / std::sqrt(one + tau);
       tau = nt * tau;
@@ -855,7 +878,7 @@ static int qp_solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const 
       batch, Bp, (int32_t*)(ws + L.done), (int32_t*)(ws + L.count), (int32_t*)(sv + L.feas),
       nullptr, (int32_t*)(ws + L.ndone));
   // valid = all(q > 0) & all(lower <= upper) ANDs into convergence (diagonal_qp.py:120-123)
-  k_qp_stats<T><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(
+  k_qp_stats<T><<<(unsigned)(Bp / 64), 1024, 0, st>>>(
       n, Bp, batch, QQ, (const T*)(sv + L.LO), (const T*)(sv + L.HI), qmax, qmin,
       (int32_t*)(sv + L.feas));
   PerSample<T> PS{};

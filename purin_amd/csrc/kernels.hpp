@@ -86,6 +86,11 @@ struct Iter {
   const T* __restrict__ Cc;
   const T* __restrict__ tau_b;
   const T* __restrict__ tau_cb;
+  // per-sample accelerated schedule: the column pass writes the next
+  // iteration's tau, sigma, a, delta, theta ([5][Bp] at sch_next) from this
+  // iteration's; gamma = min q per sample ([Bp]; nullptr: 1)
+  T* sch_next;
+  const T* __restrict__ gam;
   // dense adapter policy (chambolle_pock/dense.py:85-106): factored prox
   // a ((y - tau K^T d) - tau c) (kernels.py:140-142), no freezing of accepted
   // samples (freeze_converged=False: every sample keeps iterating and
@@ -100,6 +105,24 @@ struct Iter {
   T* rowpart;                 // [3][nrb][Bp]: residual max, r.d, finite
   int ncb, nrb;
 };
+
+// The accelerated update after an iteration (kernels.py:279-283) for one
+// sample: nu = 1/sqrt(1 + gamma tau); tau <- nu tau; sigma <- sigma / nu;
+// theta <- nu; and the prox coefficients a = 1/(1 + tau), delta = tau a of
+// q = 1 for the new tau.  Every product and quotient is rounded.
+template <typename T>
+__device__ __forceinline__ void sched_next(T gamma, T tau, T sig, T* out, int64_t Bp, int64_t b) {
+#pragma clang fp contract(off)
+  const T one = T(1);
+  const T nu = one / (T)__builtin_sqrt(one + gamma * tau);
+  const T nt = nu * tau;
+  const T a = one / (one + nt);
+  out[b] = nt;
+  out[Bp + b] = sig / nu;
+  out[2 * Bp + b] = a;
+  out[3 * Bp + b] = nt * a;
+  out[4 * Bp + b] = nu;
+}
 
 // Step sizes of row i / column j for the S samples from b0 (shared scalar,
 // diagonal, per-sample or per-sample diagonal).
@@ -182,6 +205,14 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
   const T half = T(0.5), zero = T(0);
+  // the per-sample schedule advances for every sample (done or not), once per
+  // tile: wavefront 0 of the tile's first column block
+  if (MODE != 2 && A.sch_next && blockIdx.y == 0 && wave == 0) {
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      sched_next(A.gam ? A.gam[b0 + s] : T(1), A.tau_b[b0 + s], A.sig_b[b0 + s], A.sch_next,
+                 A.Bp, b0 + s);
+  }
   V keep = vsplat<T>(T(0));
   if (MODE == 1) {
 #pragma unroll

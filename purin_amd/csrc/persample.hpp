@@ -201,28 +201,6 @@ __global__ void k_ps_steps(int64_t Bp, const T* __restrict__ rpart, int nrb,
   tol_b[b] = tol * minp(one, smin);
 }
 
-// The accelerated update after an iteration (kernels.py:279-283):
-// nu = 1/sqrt(1 + gamma tau) with gamma = min q (1 when gam is nullptr);
-// tau <- nu tau; sigma <- sigma / nu; theta <- nu; and the prox
-// coefficients of q = 1 for the new tau.
-template <typename T>
-__global__ void k_ps_sched(int64_t Bp, const T* __restrict__ gam, T* tau_b, T* sig_b, T* a_b,
-                           T* d_b, T* th_b) {
-#pragma clang fp contract(off)
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= Bp) return;
-  const T one = T(1);
-  const T tau = tau_b[b];
-  const T nu = one / (T)__builtin_sqrt(one + (gam ? gam[b] : one) * tau);
-  const T nt = nu * tau;
-  tau_b[b] = nt;
-  sig_b[b] = sig_b[b] / nu;
-  th_b[b] = nu;
-  const T a = one / (one + nt);
-  a_b[b] = a;
-  d_b[b] = nt * a;
-}
-
 // Per-sample sums over the rows of two vectors (batch-minor, R rows), one
 // thread per sample adding in row order with every product rounded (no fused
 // multiply-add), the order the oracle's norm estimate and the plan's host
@@ -266,26 +244,44 @@ __global__ void k_ps_start(int64_t n, int64_t Bp, const T* __restrict__ start, T
     x[e] = start[e / Bp];
 }
 
-// Per sample of a general diagonal QP (one thread per sample, coalesced over
-// the batch): max_j q, min_j q, and valid = all(q > 0) & all(lower <= upper)
-// (diagonal_qp.py:120-123) into feas[b] for b < batch (0 beyond).
+// Per sample of a general diagonal QP: max_j q, min_j q, and valid =
+// all(q > 0) & all(lower <= upper) (diagonal_qp.py:120-123) into feas[b] for
+// b < batch (0 beyond).  Grid Bp / 64 blocks of 1024 threads.
 template <typename T>
-__global__ void k_qp_stats(int64_t n, int64_t Bp, int64_t batch, const T* __restrict__ Q,
-                           const T* __restrict__ LO, const T* __restrict__ HI, T* qmax, T* qmin,
-                           int32_t* feas) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= Bp) return;
+__global__ __launch_bounds__(1024) void k_qp_stats(int64_t n, int64_t Bp, int64_t batch,
+                                                  const T* __restrict__ Q,
+                                                  const T* __restrict__ LO,
+                                                  const T* __restrict__ HI, T* qmax, T* qmin,
+                                                  int32_t* feas) {
+  // a block owns 64 samples (one per lane); its 16 wavefronts take the columns
+  // j = w, w + 16, ... and meet in LDS (max, min and the AND do not depend on
+  // the order in which they combine)
+  __shared__ T s_hi[16][64], s_lo[16][64];
+  __shared__ int s_ok[16][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t b = (int64_t)blockIdx.x * 64 + lane;
   T hi = Q[b], lo = Q[b];
   bool ok = true;
-  for (int64_t j = 0; j < n; ++j) {
+  for (int64_t j = w; j < n; j += 16) {
     const T q = Q[j * Bp + b];
     hi = maxp(hi, q);
     lo = minp(lo, q);
     ok = ok && q > T(0) && LO[j * Bp + b] <= HI[j * Bp + b];
   }
-  qmax[b] = hi;
-  qmin[b] = lo;
-  if (feas) feas[b] = (b < batch && ok) ? 1 : 0;
+  s_hi[w][lane] = hi;
+  s_lo[w][lane] = lo;
+  s_ok[w][lane] = ok ? 1 : 0;
+  __syncthreads();
+  if (w == 0) {
+    for (int k = 1; k < 16; ++k) {
+      hi = maxp(hi, s_hi[k][lane]);
+      lo = minp(lo, s_lo[k][lane]);
+      ok = ok && s_ok[k][lane] != 0;
+    }
+    qmax[b] = hi;
+    qmin[b] = lo;
+    if (feas) feas[b] = (b < batch && ok) ? 1 : 0;
+  }
 }
 
 // L[b] = sqrt(max(eig[b], 0)) + eps
