@@ -402,11 +402,12 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)A.Kr;
   const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)A.Kr;
 
-  // registers: y and ybar of the thread's columns; the targets and the scaled
+  // registers: y of the thread's columns; the targets and the scaled
   // right-hand sides are re-read each iteration (L2) to leave room for the
-  // diagnostics
+  // diagnostics.  ybar+ is formed after the residual sweep from y+ (the
+  // thread's own Gy entry, which the sweep gathers) and the old y.
   uint32_t soff_r[SLR], soff_c[SLC];
-  V y[SLC], yb[SLC];
+  V y[SLC];
   uint32_t ineq = 0, nanb = 0, rvalid = 0, cvalid = 0;
 #pragma unroll
   for (int c = 0; c < SLC; ++c) {
@@ -419,8 +420,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     if (j >= 0) cvalid |= 1u << c;
     soff_c[c] = j >= 0 ? (uint32_t)j * 16u : trash_off;
     y[c] = j >= 0 ? reinterpret_cast<const V*>(A.Ts)[tile * (int64_t)A.Kc + c * NT + t] : vzero;
-    yb[c] = y[c];  // y0 = ybar0 = yhat (kernels.py:229-231)
-    lds_write<V>(soff_c[c], y[c]);
+    lds_write<V>(soff_c[c], y[c]);  // y0 = ybar0 = yhat (kernels.py:229-231)
   }
 #pragma unroll
   for (int r = 0; r < SLR; ++r) {
@@ -504,15 +504,9 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) yn[s] = clip_nonnan_bounds(sv[s], lo[s], hi[s]);
       }
-      const V ybn = yn + theta * (yn - y[c]);
 #pragma unroll
-      for (int s = 0; s < BT; ++s) {
-        if (act & (1u << s)) {
-          yb[c][s] = ybn[s];
-        } else {
-          yn[s] = y[c][s];
-        }
-      }
+      for (int s = 0; s < BT; ++s)
+        if (!(act & (1u << s))) yn[s] = y[c][s];  // a frozen sample keeps its state
       if (cvalid & (1u << c)) {  // diagnostics with q = 1, c = -yhat (kernels.py:158-174, 272-274)
 #pragma unroll
         for (int s = 0; s < BT; ++s) {
@@ -527,9 +521,18 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
           if (!finite(yv)) bad |= 1u << s;
         }
       }
-      lds_write<V>(soff_c[c], yn);  // y+ for the residual sweep
-      y[c] = yn;
+      lds_write<V>(soff_c[c], yn);  // y+ for the residual sweep; y[c] keeps the old y
     }
+    // the column sums' 16-lane row partials go to LDS now ([wave][row][q]), so
+    // they are not held through the sweep
+    const uint32_t red_at = red_off + (uint32_t)((wave * 4 + (lane >> 4)) * kResQ) * 16u;
+    const bool red_lead = (lane & 15) == 0;
+#pragma unroll
+    for (int s = 0; s < BT; ++s) qp[s] = row16_combine(qp[s], OpAdd());
+    if (red_lead) lds_write<V>(red_at, qp);
+#pragma unroll
+    for (int s = 0; s < BT; ++s) qd[s] = row16_combine(qd[s], OpAdd());
+    if (red_lead) lds_write<V>(red_at + 16u, qd);
     __syncthreads();
     // ---- residual sweep (reads Gy = y+ and the thread's own Gd) ------------------
     V qr = vzero;
@@ -549,34 +552,30 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         }
       }
     }
-    // 16-lane row partials to LDS, [wave][row][q]; finiteness by wavefront vote
+    // the sweep's 16-lane row partials to LDS; finiteness by wavefront vote
     {
-      const uint32_t at = red_off + (uint32_t)((wave * 4 + (lane >> 4)) * kResQ) * 16u;
-      const bool lead = (lane & 15) == 0;
       V f;
 #pragma unroll
-      for (int s = 0; s < BT; ++s) {
-        qp[s] = row16_combine(qp[s], OpAdd());
-        f[s] = __ballot((bad >> s) & 1u) ? zero : T(1);
-      }
-      if (lead) lds_write<V>(at, qp);
-#pragma unroll
-      for (int s = 0; s < BT; ++s) qd[s] = row16_combine(qd[s], OpAdd());
-      if (lead) lds_write<V>(at + 16u, qd);
+      for (int s = 0; s < BT; ++s) f[s] = __ballot((bad >> s) & 1u) ? zero : T(1);
 #pragma unroll
       for (int s = 0; s < BT; ++s) qr[s] = row16_combine(qr[s], OpAdd());
-      if (lead) lds_write<V>(at + 32u, qr);
+      if (red_lead) lds_write<V>(red_at + 32u, qr);
 #pragma unroll
       for (int s = 0; s < BT; ++s) qm[s] = row16_combine(qm[s], OpMax());
-      if (lead) {
-        lds_write<V>(at + 48u, qm);
-        lds_write<V>(at + 64u, f);
+      if (red_lead) {
+        lds_write<V>(red_at + 48u, qm);
+        lds_write<V>(red_at + 64u, f);
       }
     }
     __syncthreads();
-    // ---- ybar+ back into Gy; the stop test ---------------------------------------
+    // ---- ybar+ = y+ + theta (y+ - y) into Gy (kernels.py:149; a frozen sample has
+    // y+ = y, so its Gy entry, which no output reads, becomes y); the stop test --
 #pragma unroll
-    for (int c = 0; c < SLC; ++c) lds_write<V>(soff_c[c], yb[c]);
+    for (int c = 0; c < SLC; ++c) {
+      const V yn = lds_read<V>(soff_c[c]);
+      lds_write<V>(soff_c[c], yn + theta * (yn - y[c]));
+      y[c] = yn;
+    }
 #pragma unroll
     for (int s = 0; s < BT; ++s)
       if (act & (1u << s)) ++cnt[s];
