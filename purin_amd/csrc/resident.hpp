@@ -319,8 +319,8 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 // out.  Per iteration:
 //   row pass      as above, masked to the active samples
 //   barrier
-//   column pass   as above, masked; Gy <- y+ (for the residual sweep), ybar+
-//                 kept in registers; column diagnostics of (y+, K^T d+):
+//   column pass   as above, masked; Gy <- y+ (for the residual sweep); column
+//                 diagnostics of (y+, K^T d+), their sums to LDS:
 //                 primal, dual objective terms, max(stationarity, bound
 //                 violation), finiteness (kernels.py:153-175, 272-274)
 //   barrier
@@ -328,16 +328,17 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 //                 max(K y+ - r, 0) (ineq), r . d+, finiteness of d+; every
 //                 partial is summed within 16-lane rows by DPP and written to LDS
 //   barrier
-//   Gy <- ybar+; wavefront 0 combines the 64 row partials of each quantity in
-//                 a fixed order and applies the stop test of each sample
+//   Gy <- ybar+ (from y+ and the old y); wavefront k combines the 64 row
+//                 partials of (sample, quantity) k in a fixed order
 //   barrier
+//   every wavefront applies the stop test of each sample to the totals
 // The step arithmetic is the fixed kernel's (and the streaming passes'), so
 // the iterates of a sample are identical up to its stop; the diagnostics are
 // summed in another (fixed) order than the streaming stop test's.
 // LDS: the fixed kernel's, then [16 waves][4 rows][kResQ] partials and the
-// active mask.
+// [BT][kResQ] totals.
 constexpr int kResQ = 5;  // primal, dual terms, r.d, max(res, bound, stat), finite
-constexpr uint32_t kResEarlyExtra = 16u * 4u * kResQ * 16u + 16u;
+constexpr uint32_t kResEarlyExtra = 16u * 4u * kResQ * 16u + 128u;
 
 // One DPP move of a 32- or 64-bit value (all lanes active, full row/bank masks).
 template <int CTRL, typename T>
@@ -393,7 +394,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const uint32_t gd_off = (uint32_t)(A.n + 1) * 16u;
   const uint32_t trash_off = (uint32_t)(A.n + 1 + A.m) * 16u;
   const uint32_t red_off = trash_off + 16u;
-  const uint32_t flag_off = red_off + 16u * 4u * kResQ * 16u;
+  const uint32_t tot_off = red_off + 16u * 4u * kResQ * 16u;  // [BT][kResQ] totals
 
   const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave]);
   const uint32_t rcnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave + 1]);
@@ -579,27 +580,38 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
 #pragma unroll
     for (int s = 0; s < BT; ++s)
       if (act & (1u << s)) ++cnt[s];
-    if (wave == 0) {
-      // lane l holds partial (wave l / 4, row l % 4): combined within DPP
-      // rows, then the 4 rows in order
-      const uint32_t at = red_off + (uint32_t)(lane * kResQ) * 16u;
+    // the (sample, quantity) totals, one per wavefront (BT * kResQ of them): lane
+    // l holds partial (wave l / 4, row l % 4), combined within DPP rows, then
+    // the 4 rows in order
+    for (int k = wave; k < BT * kResQ; k += kResWaves) {
+      const int s = k / kResQ, q = k - s * kResQ;
+      const V pv = lds_read<V>(red_off + (uint32_t)(lane * kResQ + q) * 16u);
+      T x = pv[0];
+#pragma unroll
+      for (int u = 1; u < BT; ++u)
+        if (s == u) x = pv[u];
+      if (q < 3) x = row16_combine(x, OpAdd());
+      else if (q == 3) x = row16_combine(x, OpMax());
+      else x = row16_combine(x, OpMin());
+      const T r0 = read_lane(x, 0), r1 = read_lane(x, 16), r2 = read_lane(x, 32),
+              r3 = read_lane(x, 48);
+      T tot;
+      if (q < 3) tot = ((r0 + r1) + r2) + r3;
+      else if (q == 3) tot = maxp(maxp(maxp(r0, r1), r2), r3);
+      else tot = minp(minp(minp(r0, r1), r2), r3);
+      if (lane == 0) lds_write<T>(tot_off + (uint32_t)(k * sizeof(T)), tot);
+    }
+    __syncthreads();
+    // every wavefront applies the stop test to the same totals (the same
+    // decision everywhere; kernels.py:167-175, 260-278)
+    {
       uint32_t accept = 0;
 #pragma unroll
       for (int s = 0; s < BT; ++s) {
         T tot[kResQ];
 #pragma unroll
-        for (int q = 0; q < kResQ; ++q) {
-          T x = lds_read<V>(at + 16u * (uint32_t)q)[s];
-          if (q < 3) x = row16_combine(x, OpAdd());
-          else if (q == 3) x = row16_combine(x, OpMax());
-          else x = row16_combine(x, OpMin());
-          const T r0 = read_lane(x, 0), r1 = read_lane(x, 16), r2 = read_lane(x, 32),
-                  r3 = read_lane(x, 48);
-          if (q < 3) tot[q] = ((r0 + r1) + r2) + r3;
-          else if (q == 3) tot[q] = maxp(maxp(maxp(r0, r1), r2), r3);
-          else tot[q] = minp(minp(minp(r0, r1), r2), r3);
-        }
-        // kernels.py:167-175, 260-278
+        for (int q = 0; q < kResQ; ++q)
+          tot[q] = lds_read<T>(tot_off + (uint32_t)((s * kResQ + q) * sizeof(T)));
         const T tol = A.tolv ? (bs0 + s < A.batch ? A.tolv[bs0 + s] : T(0)) : A.tol;
         const T primal = tot[0], dual_obj = tot[1] - tot[2];
         const T gap = maxp(primal - dual_obj, zero) /
@@ -607,10 +619,8 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         const bool ok = tot[4] != zero && finite(gap) && tot[3] <= tol && gap <= tol;
         if (ok && (act & (1u << s))) accept |= 1u << s;
       }
-      if (lane == 0) lds_write<uint32_t>(flag_off, act & ~accept);
+      act = (uint32_t)__builtin_amdgcn_readfirstlane((int)(act & ~accept));
     }
-    __syncthreads();
-    act = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_read<uint32_t>(flag_off));
   }
   // ---- hand the state to the batch-minor layout ---------------------------------
 #pragma unroll
