@@ -612,12 +612,11 @@ __global__ void k_axpby(int64_t total, T* out, const T* __restrict__ a, const T*
 // V0 = r / max(beta, eps) per sample
 template <typename T>
 __global__ void k_scale_cols(int64_t total, int64_t Bp, T* out, int64_t ldo,
-                             const T* __restrict__ in, const T* __restrict__ scale,
-                             const int32_t* __restrict__ keep) {
+                             const T* __restrict__ in, const T* __restrict__ scale) {
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = e / Bp, b = e - row * Bp;
-    out[row * ldo + b] = (keep == nullptr || keep[b]) ? in[e] * scale[b] : T(0);
+    out[row * ldo + b] = in[e] * scale[b];
   }
 }
 
@@ -651,7 +650,6 @@ struct Gm {
   int32_t* cyc;  // cycle_active
   int32_t* act;  // active
   int32_t* steps;
-  int32_t* keep;
   T* scale;
   T* H;          // [(restart+1)][restart][Bp]: H[i][j] of sample b at (i*restart + j)*Bp + b
   T* cs;         // [restart][Bp]
@@ -809,7 +807,6 @@ __global__ __launch_bounds__(1024) void k_gm_tri(Gm<T> G, int it, const T* __res
   }
   if (worker == 0) {
     const T eps = T(1e-30), brk = T(1e-14);
-    G.keep[b] = active;
     T ss = T(0);
     for (int j = 0; j < nv; ++j) ss += Gv[j * kTriS + sl] * Gv[j * kTriS + sl];
     const T n1 = P[nv * kTriS + sl];
@@ -1330,7 +1327,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                oU = take(n * Bp * es), oWv = take(m * Bp * es),
                oPart = take((size_t)(restart + 1) * std::max(nchunk, nchunk2) * Bp * es),
                oS1 = take(Bp * es), oS2 = take(Bp * es), oThr = take(Bp * es), oRinf = take(Bp * es),
-               oCyc = take(Bp * 4), oAct = take(Bp * 4), oSteps = take(Bp * 4), oKeep = take(Bp * 4),
+               oCyc = take(Bp * 4), oAct = take(Bp * 4), oSteps = take(Bp * 4),
                oScale = take(Bp * es), oHess = take((size_t)Bp * (restart + 1) * restart * es),
                oCs = take((size_t)restart * Bp * es), oSn = take((size_t)restart * Bp * es),
                oGv = take((size_t)(restart + 1) * Bp * es), oCoef = take((size_t)restart * Bp * es),
@@ -1371,7 +1368,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   T* S1 = (T*)(ws + oS1);
   T* S2 = (T*)(ws + oS2);
   Gm<T> G{batch, Bp, restart, (T*)(ws + oThr), (T*)(ws + oRinf), (int32_t*)(ws + oCyc),
-          (int32_t*)(ws + oAct), (int32_t*)(ws + oSteps), (int32_t*)(ws + oKeep),
+          (int32_t*)(ws + oAct), (int32_t*)(ws + oSteps),
           (T*)(ws + oScale), (T*)(ws + oHess), (T*)(ws + oCs), (T*)(ws + oSn), (T*)(ws + oGv),
           (T*)(ws + oCoef), (int32_t*)(ws + oCnt), (int32_t*)(ws + oStepCnt),
           (T*)(ws + oTm), (T*)(ws + oHu), (T*)(ws + oU2), (T*)(ws + oG1), (T*)(ws + oQ1),
@@ -1647,7 +1644,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     reduce(1, S1, 0);
     k_fill<int32_t><<<1, 256, 0, st>>>(G.stepcnt, restart + 2, 0);
     k_gm_cycle_init<T><<<sb, 256, 0, st>>>(G, S1);
-    k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, Vb, zld, Rr, G.scale, nullptr);
+    k_scale_cols<T><<<eb, 256, 0, st>>>(total, Bp, Vb, zld, Rr, G.scale);
     // Arnoldi steps.  The reference loop runs step s while s < cycle_limit and
     // some sample is active at its start (operators.py:943-1082); a step with
     // no active sample changes no state here (every update is masked by the
