@@ -1522,11 +1522,13 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                                                                     part, (int)chunks, rpb, zld);
     return PURIN_CP_OK;
   };
-  // the dot pass: two blocks per CU over the batch tiles (the best measured
-  // balance of rows in flight per wavefront against blocks per CU)
+  // the dot pass: two blocks per CU over the batch tiles, one from 16 prefix
+  // vectors on (as fast, with each wavefront holding 4+ vectors' loads in
+  // flight, and half the chunk partials for the per-sample reduction)
   auto launch_dots = [&](auto kern, int nv, const T* img) -> int {
+    const int64_t per_cu = nv >= 16 ? 1 : 2;
     const int64_t chunks = std::max<int64_t>(
-        1, std::min<int64_t>({(int64_t)2 * cus / tiles0, (W + 3) / 4, (int64_t)nchunk2}));
+        1, std::min<int64_t>({per_cu * cus / tiles0, (W + 3) / 4, (int64_t)nchunk2}));
     const int64_t rpb = (W + chunks - 1) / chunks;
     last_nchunk = (int)chunks;
     kern<<<dim3((unsigned)tiles0, (unsigned)chunks), kBlock, 0, st>>>(Vb, zs, nv, img, W, Bp,
