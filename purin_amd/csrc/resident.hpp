@@ -509,14 +509,17 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       for (int s = 0; s < BT; ++s)
         if (!(act & (1u << s))) yn[s] = y[c][s];  // a frozen sample keeps its state
       if (cvalid & (1u << c)) {  // diagnostics with q = 1, c = -yhat (kernels.py:158-174, 272-274)
+        // the clip of non-NaN bounds is the two-compare form (clipp's result)
+        const bool fast = !(nanb & (1u << c));
 #pragma unroll
         for (int s = 0; s < BT; ++s) {
           const T yv = yn[s], cq = -tg[s];
           qp[s] += half * yv * yv + cq * yv;
           const T tf = cq + tt[s];
-          const T mz = clipp(-tf, lo[s], hi[s]);
+          const T mz = fast ? clip_nonnan_bounds(-tf, lo[s], hi[s]) : clipp(-tf, lo[s], hi[s]);
           qd[s] += half * mz * mz + tf * mz;
-          const T g = yv - clipp(yv - ((yv + cq) + tt[s]), lo[s], hi[s]);
+          const T xs = yv - ((yv + cq) + tt[s]);
+          const T g = yv - (fast ? clip_nonnan_bounds(xs, lo[s], hi[s]) : clipp(xs, lo[s], hi[s]));
           qm[s] = maxp(qm[s], absv(g));
           qm[s] = maxp(qm[s], maxp(maxp(lo[s] - yv, zero), maxp(yv - hi[s], zero)));
           if (!finite(yv)) bad |= 1u << s;
