@@ -765,6 +765,7 @@ __global__ __launch_bounds__(1024) void k_gm_tri(Gm<T> G, int it, const T* __res
   for (int i = wave; i < planes; i += 16) {
     const T* pp = part + (size_t)i * plane + b;
     T acc = T(0);
+#pragma unroll 8
     for (int c = q; c < nchunk; c += 4) acc += pp[(size_t)c * Bp];
     acc += __shfl_xor(acc, 16);
     acc += __shfl_xor(acc, 32);
@@ -776,6 +777,7 @@ __global__ __launch_bounds__(1024) void k_gm_tri(Gm<T> G, int it, const T* __res
   const int active = MODE == 2 ? G.act[b] : 0;
   for (int j = worker; j < nv; j += 64) {
     T acc = T(0);
+#pragma unroll 8
     for (int i = 0; i <= j; ++i) acc += Tm[i * trow + j * tcol] * P[i * kTriS + sl];
     Gv[j * kTriS + sl] = acc;
     if (MODE == 1) {
@@ -783,6 +785,7 @@ __global__ __launch_bounds__(1024) void k_gm_tri(Gm<T> G, int it, const T* __res
     } else {
       // c_j = sum_k Hu[j][k] u_k, k in [max(j - 1, 0), it - 1] (Hu is upper Hessenberg)
       T cj = T(0);
+#pragma unroll 8
       for (int k = j > 0 ? j - 1 : 0; k < it; ++k)
         cj += G.Hu[((size_t)j * R + k) * Bp + b] * G.U2[(size_t)k * Bp + b];
       const T col = (G.G1[(size_t)j * Bp + b] + acc) - cj;
@@ -800,6 +803,7 @@ __global__ __launch_bounds__(1024) void k_gm_tri(Gm<T> G, int it, const T* __res
   if (MODE == 1) {
     for (int i = worker; i < nv; i += 64) {
       T acc = T(0);
+#pragma unroll 8
       for (int j = i; j < nv; ++j) acc += Tm[i * trow + j * tcol] * Gv[j * kTriS + sl];
       G.Q1[(size_t)i * Bp + b] = acc;
     }
@@ -855,6 +859,7 @@ __global__ __launch_bounds__(1024) void k_gm_tri(Gm<T> G, int it, const T* __res
   const bool keep = s_keep[sl] != 0;
   for (int i = worker; i < nv; i += 64) {
     T acc = T(0);
+#pragma unroll 8
     for (int j = i; j < nv; ++j) acc += Tm[i * trow + j * tcol] * Gv[j * kTriS + sl];
     G.Tm[(size_t)i * trow + (size_t)(it + 1) * tcol + b] = keep ? -(acc * inv) : T(0);
     G.U2[(size_t)i * Bp + b] = keep ? Gv[i * kTriS + sl] * inv : T(0);
