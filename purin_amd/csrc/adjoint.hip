@@ -876,6 +876,7 @@ __global__ void k_gm_tcoef(Gm<T> G) {
   const int steps = G.steps[b];
   const size_t trow = (size_t)(G.restart + 1) * G.Bp;
   T acc = T(0);
+#pragma unroll 8
   for (int j = i; j < steps; ++j) acc += G.Tm[i * trow + (size_t)j * G.Bp + b] * G.coeff[(size_t)j * G.Bp + b];
   G.Wc[(size_t)i * G.Bp + b] = acc;
 }
@@ -899,6 +900,7 @@ __global__ __launch_bounds__(64) void k_gm_backsub(Gm<T> G) {
     T v = T(0);
     if (row < steps) {
       T trailing = T(0);
+#pragma unroll 8
       for (int c = row + 1; c < steps; ++c)
         trailing += G.H[((size_t)row * R + c) * Bp + b] * val[c * 64 + t];
       const T num = G.g[(size_t)row * Bp + b] - trailing;
