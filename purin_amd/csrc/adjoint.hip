@@ -306,6 +306,7 @@ __global__ __launch_bounds__(kBlock) void k_op_cols2(Adj<T> S, const T* __restri
     const int j = cb * 4 + wave;
     if (j >= S.n) continue;
     V acc = vsplat<T>(T(0));
+#pragma unroll 4
     for (int k = S.K.cptr[j]; k < S.K.cptr[j + 1]; ++k)
       acc += col_coef(S.K, k, b0) * vload(S.Wv + (size_t)S.K.cidx[k] * S.Bp + b0);
     const size_t off = (size_t)(S.n + S.m + j) * S.ldv + b0;
