@@ -277,17 +277,17 @@ __global__ __launch_bounds__(kBlock) void k_op_rows(Adj<T> S, const T* __restric
       acc += row_coef(S.K, k, b0) * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
     const size_t off = (size_t)i * S.Bp + b0;
     const size_t voff = (size_t)(S.n + i) * S.ldv + b0;
-    V gd = vload(v + voff);
+    V gd = vload_once(v + voff);
     if (S.vsc) gd = gd * vload(S.vsc + b0);
     if (S.dg) {
-      const V w = vload(S.Dm + off) * (gd - acc);
+      const V w = vload_once(S.Dm + off) * (gd - acc);
       V sg;
 #pragma unroll
       for (int s = 0; s < Sn; ++s) sg[s] = adj_sig(S, i, b0 + s);
       vstore(S.Wv + off, sg * w);
       vstore(out + voff, gd - w);
     } else {
-      const V w = vload(S.Dm + off) * (gd - S.delta * acc);
+      const V w = vload_once(S.Dm + off) * (gd - S.delta * acc);
       vstore(S.Wv + off, w);
       vstore(out + voff, gd - w);
     }

@@ -43,6 +43,12 @@ template <typename T>
 __device__ __forceinline__ typename Lane<T>::V vload(const T* p) {
   return *reinterpret_cast<const typename Lane<T>::V*>(p);
 }
+// Load of a value read once: marked nontemporal so it does not displace gathered
+// vectors from L2.
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V vload_once(const T* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const typename Lane<T>::V*>(p));
+}
 template <typename T>
 __device__ __forceinline__ void vstore(T* p, typename Lane<T>::V v) {
   *reinterpret_cast<typename Lane<T>::V*>(p) = v;
