@@ -39,7 +39,11 @@
  * Threading: calls on one plan must be ordered (same stream or externally
  * synchronised); the plan owns one workspace.  All kernels are enqueued on the
  * given stream; project/solve/adjoint synchronise that stream only to read
- * their device-side stop flags.
+ * their device-side stop flags.  A workspace that must grow is replaced
+ * stream-ordered (hipMallocAsync / hipFreeAsync on the call's stream), and so
+ * is the resident kernel's step schedule for a call of more than 65536
+ * iterations; no entry point synchronises the device or other streams
+ * (plan creation, destruction and set_metric are set-up calls and may).
  */
 #ifndef PURIN_CP_H
 #define PURIN_CP_H

@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <string>
 #include <vector>
 
 #include "kernels.hpp"
@@ -24,7 +25,7 @@ namespace purin {
 
 static size_t al(size_t x) { return (x + 255) & ~size_t(255); }
 
-Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values) {
+Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values, int extras) {
   Layout L{};
   const size_t es = elem_size(p);
   const int64_t Bp = padded_batch(p, batch);
@@ -47,7 +48,7 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values) {
   L.saved_end = o;
   o = 0;
   L.YB = take(n * Bp * es);
-  L.MF = take(M * Bp * es);
+  L.MF = (extras & kLayoutWarm) ? take(M * Bp * es) : 0;
   L.DF = take(M * Bp * es);
   L.SL = take(mi * Bp * es);
   L.colpart = take((size_t)5 * std::max(L.ncb, 1) * Bp * es);
@@ -58,8 +59,10 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values) {
   L.ores = take(Bp * es);
   L.ogap = take(Bp * es);
   L.ofin = take(Bp * 4);
-  L.X = take(std::max(n, m) * Bp * es);  // spmm input / output staging
-  L.Z = take(std::max(n, m) * Bp * es);
+  if (extras & kLayoutSpmm) {  // spmm input / output staging
+    L.X = take(std::max(n, m) * Bp * es);
+    L.Z = take(std::max(n, m) * Bp * es);
+  }
   if (p->res_ok) {  // resident path: slot-ordered copies of the per-sample inputs
     const size_t Kr = (size_t)p->res_mr * kResThreads, Kc = (size_t)p->res_mc * kResThreads;
     L.RTs = take(Kc * Bp * es);
@@ -280,37 +283,6 @@ static size_t resident_lds(const purin_cp_plan* p, bool early = false) {
   return lds <= 160 * 1024 ? lds : 0;
 }
 
-// Per-iteration step scalars (kernels.py:68-73, 279-283), cached on the device.
-template <typename T>
-static int resident_schedule(purin_cp_plan* p, int64_t iters) {
-  if (p->res_sched && p->res_sched_len == iters) return PURIN_CP_OK;
-  std::vector<T> h((size_t)4 * iters);
-  const T one = T(1);
-  T tau = (T)p->tau0, sigma = (T)p->sigma0, theta = one;
-  for (int64_t k = 0; k < iters; ++k) {
-    const T a = one / (one + tau);
-    h[4 * k] = sigma;
-    h[4 * k + 1] = a;
-    h[4 * k + 2] = tau * a;
-    h[4 * k + 3] = theta;
-    if (p->opts.accelerated) {
-      const T nt = one / std::sqrt(one + tau);
-      tau = nt * tau;
-      sigma = sigma / nt;
-      theta = nt;
-    }
-  }
-  if (p->res_sched) {
-    PURIN_HIP(hipDeviceSynchronize());
-    PURIN_HIP(hipFree(p->res_sched));
-    p->res_sched = nullptr;
-  }
-  PURIN_HIP(hipMalloc(&p->res_sched, h.size() * sizeof(T)));
-  PURIN_HIP(hipMemcpy(p->res_sched, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice));
-  p->res_sched_len = iters;
-  return PURIN_CP_OK;
-}
-
 // The CP loop on the resident kernel; fills Y and D like the passes (and, with
 // early stop, the per-sample done flags and iteration counts).
 template <typename T>
@@ -321,7 +293,9 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   constexpr int BT = res_tile<T>();
   const int64_t Bp = L.Bp, tiles = Bp / BT;
   const int Kr = p->res_mr * kResThreads, Kc = p->res_mc * kResThreads;
-  if (int rc = resident_schedule<T>(p, o.max_iterations)) return rc;
+  // the step schedule built with the plan covers kSchedCapacity iterations;
+  // a longer call grows it stream-ordered
+  if (int rc = ensure_schedule(p, o.max_iterations, st, false)) return rc;
   Res<T> R{};
   R.n = (int)p->n;
   R.m = (int)p->m;
@@ -626,10 +600,11 @@ static int check_layout_args(purin_cp_plan* p, int64_t batch) {
   return PURIN_CP_OK;
 }
 
+// This call's buffers: the plan workspace (grown stream-ordered).
 template <typename T>
 static int prepare_buffers(purin_cp_plan* p, hipStream_t st, int64_t batch, void* saved,
-                           Layout* L, char** sv, char** ws, bool values = false) {
-  *L = make_layout(p, batch, values);
+                           Layout* L, char** sv, char** ws, bool values = false, int extras = 0) {
+  *L = make_layout(p, batch, values, extras);
   int err = PURIN_CP_OK;
   const size_t need = L->ws_end + (saved ? 0 : L->saved_end);
   char* base = (char*)workspace(p, need, st, &err);
@@ -647,7 +622,8 @@ static int spmm_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, int transp
   if (!x || !out) return set_error(PURIN_CP_ERR_ARG, "NULL x/out");
   Layout L;
   char *sv, *ws;
-  if ((rc = prepare_buffers<T>(p, st, batch, nullptr, &L, &sv, &ws))) return rc;
+  if ((rc = prepare_buffers<T>(p, st, batch, nullptr, &L, &sv, &ws, false, kLayoutSpmm)))
+    return rc;
   const int64_t Bp = L.Bp;
   constexpr int64_t TS = tile_samples<T>();
   Mat<T> K = kept_matrix<T>(p, scaled != 0);
@@ -736,7 +712,9 @@ static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T
     return set_error(PURIN_CP_ERR_ARG, "tolerance must be positive and finite");
   Layout L;
   char *sv, *ws;
-  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, per_sample))) return rc;
+  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, per_sample,
+                               mult0 ? kLayoutWarm : 0)))
+    return rc;
   const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
   constexpr int64_t TS = tile_samples<T>();
   write_header<T>(st, sv, batch, Bp, per_sample ? 2 : 1, o.shared_bounds, p);
@@ -851,7 +829,8 @@ static int qp_solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const 
   if (o.shared_bounds) return set_error(PURIN_CP_ERR_ARG, "the diagonal QP takes per-sample bounds");
   Layout L;
   char *sv, *ws;
-  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, true))) return rc;
+  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, true, dual0 ? kLayoutWarm : 0)))
+    return rc;
   const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
   constexpr int64_t TS = tile_samples<T>();
   write_header<T>(st, sv, batch, Bp, dense ? 4 : 3, 0, p);

@@ -25,7 +25,11 @@ struct Layout {
   size_t ws_end;
 };
 
-Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values = false);
+// Optional parts of the forward workspace.
+constexpr int kLayoutSpmm = 1;  // X, Z: purin_cp_spmm's batch-minor staging
+constexpr int kLayoutWarm = 2;  // MF: warm-start multipliers / duals in batch-minor layout
+
+Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values = false, int extras = 0);
 
 // Per-sample coefficient arrays prepared for one call (see persample.hpp).
 template <typename T>

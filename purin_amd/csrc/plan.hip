@@ -46,27 +46,110 @@ void* workspace(purin_cp_plan* p, size_t bytes, hipStream_t stream, int* err, bo
   void*& buf = adjoint ? p->aws : p->ws;
   size_t& have = adjoint ? p->aws_bytes : p->ws_bytes;
   if (bytes <= have && buf) return buf;
-  if (buf) {
-    // kernels of an earlier call may still read the old buffer
-    hipError_t e = hipStreamSynchronize(stream);
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
-      *err = hip_check(e, "synchronize before workspace growth");
-      return nullptr;
-    }
-    (void)hipFree(buf);
-    buf = nullptr;
-    have = 0;
-  }
+  // Stream-ordered growth: the new buffer is usable by work enqueued after it
+  // on ``stream``, and the old one is released once the stream's earlier
+  // kernels (which may still read it) are done.  No host or device-wide sync.
   bytes = (size_t)round_up((int64_t)bytes, 1 << 20);
-  hipError_t e = hipMalloc(&buf, bytes);
+  void* nb = nullptr;
+  hipError_t e = hipMallocAsync(&nb, bytes, stream);
   if (e != hipSuccess) {
-    buf = nullptr;
-    *err = set_error(PURIN_CP_ERR_NOMEM, std::string("workspace hipMalloc: ") + hipGetErrorString(e));
+    *err = set_error(PURIN_CP_ERR_NOMEM, std::string("workspace hipMallocAsync: ") + hipGetErrorString(e));
     return nullptr;
   }
+  if (buf) {
+    e = hipFreeAsync(buf, stream);
+    if (e != hipSuccess) {
+      (void)hipFreeAsync(nb, stream);
+      *err = hip_check(e, "workspace hipFreeAsync");
+      return nullptr;
+    }
+  }
+  buf = nb;
   have = bytes;
   return buf;
+}
+
+// Per-iteration step scalars (sigma, a, delta, theta) of the shared scalar
+// schedule, in the plan's precision: the prox coefficients with q = 1
+// (kernels.py:68-73) and, when accelerated, the update of kernels.py:279-283
+// with gamma = min q = 1.  The streaming driver (forward.hip, run_iterations)
+// performs the same operations in the same order on its host loop variables.
+template <typename T>
+static std::vector<T> step_schedule(const purin_cp_plan* p, int64_t iters) {
+  std::vector<T> h((size_t)4 * iters);
+  const T one = T(1);
+  T tau = (T)p->tau0, sigma = (T)p->sigma0, theta = one;
+  for (int64_t k = 0; k < iters; ++k) {
+    const T a = one / (one + tau);
+    h[4 * k] = sigma;
+    h[4 * k + 1] = a;
+    h[4 * k + 2] = tau * a;
+    h[4 * k + 3] = theta;
+    if (p->opts.accelerated) {
+      const T nt = one / std::sqrt(one + tau);
+      tau = nt * tau;
+      sigma = sigma / nt;
+      theta = nt;
+    }
+  }
+  return h;
+}
+
+int ensure_schedule(purin_cp_plan* p, int64_t iters, hipStream_t stream, bool at_create) {
+  if (p->res_sched && p->res_sched_len >= iters) return PURIN_CP_OK;
+  const int64_t len = std::max(iters, p->res_sched_len * 2);
+  const size_t es = elem_size(p);
+  const size_t bytes = (size_t)4 * len * es;
+  if (at_create) {
+    std::vector<unsigned char> h(bytes);
+    if (p->dtype == PURIN_CP_F64) {
+      auto v = step_schedule<double>(p, len);
+      std::memcpy(h.data(), v.data(), bytes);
+    } else {
+      auto v = step_schedule<float>(p, len);
+      std::memcpy(h.data(), v.data(), bytes);
+    }
+    // a stream-ordered allocation like the grown ones, so that every schedule
+    // buffer is released the same way (hipFreeAsync)
+    void* d = nullptr;
+    hipError_t e = hipMallocAsync(&d, bytes, nullptr);
+    if (e != hipSuccess) return set_error(PURIN_CP_ERR_NOMEM, "schedule hipMallocAsync failed");
+    e = hipMemcpyAsync(d, h.data(), bytes, hipMemcpyHostToDevice, nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+      (void)hipFreeAsync(d, nullptr);
+      return hip_check(e, "schedule upload");
+    }
+    p->res_sched = d;
+    p->res_sched_len = len;
+    return PURIN_CP_OK;
+  }
+  // a longer call: a new pinned staging copy (kept until the plan is destroyed,
+  // so no host buffer is reused while a copy from it may be pending) and a
+  // stream-ordered replacement of the device buffer
+  void* staging = nullptr;
+  hipError_t e = hipHostMalloc(&staging, bytes, hipHostMallocDefault);
+  if (e != hipSuccess) return set_error(PURIN_CP_ERR_NOMEM, "schedule hipHostMalloc failed");
+  p->sched_staging.push_back(staging);
+  if (p->dtype == PURIN_CP_F64) {
+    auto v = step_schedule<double>(p, len);
+    std::memcpy(staging, v.data(), bytes);
+  } else {
+    auto v = step_schedule<float>(p, len);
+    std::memcpy(staging, v.data(), bytes);
+  }
+  void* d = nullptr;
+  e = hipMallocAsync(&d, bytes, stream);
+  if (e != hipSuccess) return set_error(PURIN_CP_ERR_NOMEM, "schedule hipMallocAsync failed");
+  e = hipMemcpyAsync(d, staging, bytes, hipMemcpyHostToDevice, stream);
+  if (e != hipSuccess) return hip_check(e, "schedule upload");
+  if (p->res_sched) {
+    e = hipFreeAsync(p->res_sched, stream);
+    if (e != hipSuccess) return hip_check(e, "schedule hipFreeAsync");
+  }
+  p->res_sched = d;
+  p->res_sched_len = len;
+  return PURIN_CP_OK;
 }
 
 // splitmix64 start vector in [-1, 1) (the oracle's start_vector restates it).
@@ -567,12 +650,21 @@ int purin_cp_plan_create(purin_cp_plan** out, int32_t dtype, int64_t n, int64_t 
   p->mi = mi;
   p->M = M;
   p->opts = o;
+  {
+    hipError_t e = hipGetDevice(&p->device);
+    if (e != hipSuccess) {
+      delete p;
+      return hip_check(e, "hipGetDevice");
+    }
+  }
   int rc = dtype == PURIN_CP_F64 ? build<double>(p, indptr, indices, values)
                                  : build<float>(p, indptr, indices, values);
   if (rc == PURIN_CP_OK) {
     hipError_t e = hipHostMalloc((void**)&p->pinned, kPinnedBytes, hipHostMallocDefault);
     if (e != hipSuccess) rc = hip_check(e, "hipHostMalloc");
   }
+  // the resident kernel's step schedule, for calls of up to kSchedCapacity iterations
+  if (rc == PURIN_CP_OK && p->res_ok) rc = ensure_schedule(p, kSchedCapacity, nullptr, true);
   if (rc != PURIN_CP_OK) {
     purin_cp_plan_destroy(p);
     return rc;
@@ -586,9 +678,12 @@ void purin_cp_plan_destroy(purin_cp_plan* p) {
   (void)hipDeviceSynchronize();
   for (void* ptr : p->owned) (void)hipFree(ptr);
   if (p->metric) (void)hipFree(p->metric);
-  if (p->ws) (void)hipFree(p->ws);
-  if (p->aws) (void)hipFree(p->aws);
-  if (p->res_sched) (void)hipFree(p->res_sched);
+  // the workspaces (and a grown schedule) are stream-ordered allocations
+  if (p->ws) (void)hipFreeAsync(p->ws, nullptr);
+  if (p->aws) (void)hipFreeAsync(p->aws, nullptr);
+  if (p->res_sched) (void)hipFreeAsync(p->res_sched, nullptr);
+  (void)hipDeviceSynchronize();
+  for (void* h : p->sched_staging) (void)hipHostFree(h);
   if (p->pinned) (void)hipHostFree(p->pinned);
   delete p;
 }

@@ -17,6 +17,10 @@ constexpr int64_t kSavedMagic = 0x5055524e43503031LL;  // "PURNCP01"
 constexpr int kResThreads = 1024;   // threads of a resident workgroup
 constexpr int kResMaxSlots = 4;     // rows / columns per thread (n, m <= 4096)
 constexpr int kPinnedBytes = 4096;  // host-pinned flag words: counters and per-step counts
+// Iterations of the step schedule built with the plan (the schedule of k
+// iterations is a prefix of any longer one, so calls up to this count read it
+// as it is; longer calls extend it stream-ordered).
+constexpr int64_t kSchedCapacity = int64_t(1) << 16;
 }  // namespace purin
 
 struct purin_cp_plan {
@@ -86,7 +90,10 @@ struct purin_cp_plan {
   int32_t* res_wtab_e = nullptr;
   int64_t res_stream_bytes = 0;
   void* res_sched = nullptr;         // per-iteration (sigma, a, delta, theta)
-  int64_t res_sched_len = 0;
+  int64_t res_sched_len = 0;         // iterations the schedule holds
+  std::vector<void*> sched_staging;  // pinned host copies of grown schedules (freed with the plan)
+
+  int device = 0;             // the device the plan was created on (its buffers live there)
 
   std::vector<void*> owned;   // device allocations freed with the plan
   purin_cp_timing timing{};   // last timed call
@@ -100,6 +107,10 @@ int hip_check(hipError_t e, const char* what);
 int64_t padded_batch(const purin_cp_plan* p, int64_t batch);
 size_t elem_size(const purin_cp_plan* p);
 void* workspace(purin_cp_plan* p, size_t bytes, hipStream_t stream, int* err, bool adjoint = false);
+// Make the resident step schedule hold at least ``iters`` iterations: built on
+// the host and uploaded synchronously at plan creation (at_create), or grown
+// stream-ordered on ``stream`` (pinned staging, hipMallocAsync / hipFreeAsync).
+int ensure_schedule(purin_cp_plan* p, int64_t iters, hipStream_t stream, bool at_create);
 }  // namespace purin
 
 #define PURIN_HIP(call)                                        \
