@@ -209,6 +209,37 @@ int purin_cp_project(purin_cp_plan* plan, void* stream, int64_t batch, const voi
                      uint8_t* finite, uint8_t* eligible, void* saved);
 
 /*
+ * The same projection as purin_cp_project(), for callers that cannot allocate
+ * device memory during the call (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference:
+ * it exists for those callers.  It runs the same kernels on the same inputs
+ * and outputs, with the call's working buffers (and the saved state when
+ * ``saved`` is NULL) in one static device array of
+ * PURIN_CP_NOALLOC_SCRATCH_BYTES per GPU, which each GPU the library runs on
+ * holds until the process ends.  It calls no hipMalloc / hipFree or other
+ * allocating routine.
+ * Limits (each a PURIN_CP_ERR_ARG with a message, nothing launched):
+ *   - the call's buffers must fit the scratch array (at the config-2 shape,
+ *     n = 4096 with 3072 kept rows in fp64, a batch of up to 128 samples);
+ *   - opts->max_iterations must not exceed the step schedule the plan built
+ *     at creation (65536 iterations) when the resident kernel runs;
+ *   - opts->timing must be 0;
+ *   - the current device must be the plan's.
+ * Every call on one GPU shares that GPU's array, which keeps the last call's
+ * contents (the kernels clear what must start at zero): calls that overlap on
+ * one GPU -- on different streams, or from different threads or plans --
+ * race, and must be ordered by the caller.  A saved state written into the
+ * array (saved == NULL) is not kept for an adjoint call.
+ */
+#define PURIN_CP_NOALLOC_SCRATCH_BYTES (128LL << 20)
+
+int purin_cp_project_noalloc(purin_cp_plan* plan, void* stream, int64_t batch,
+                             const void* target, const void* rhs, const void* multipliers0,
+                             const purin_cp_solve_options* opts, void* y, void* multipliers,
+                             void* slacks, int32_t* status, int32_t* iterations, void* residual,
+                             uint8_t* finite, uint8_t* eligible, void* saved);
+
+/*
  * Full projection with per-sample coefficients: the same rows and sparsity as
  * the plan, with every sample's own coefficient values.  Replaces
  * BoundProjection.solve when the coefficients depend on the parameters

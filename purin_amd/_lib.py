@@ -14,6 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libpurin_cp.so")
 
 F32, F64 = 0, 1
+NOALLOC_SCRATCH_BYTES = 128 << 20  # PURIN_CP_NOALLOC_SCRATCH_BYTES
 OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM = 0, 1, 2, 3, 4
 
 # every symbol the header declares (checked by tests/test_abi.py)
@@ -31,6 +32,7 @@ SYMBOLS = (
     "purin_cp_last_adjoint_stats",
     "purin_cp_solve",
     "purin_cp_project",
+    "purin_cp_project_noalloc",
     "purin_cp_project_values",
     "purin_cp_qp_solve",
     "purin_cp_dense_solve",
@@ -158,6 +160,8 @@ def load(path: str = LIB_PATH):
     lib.purin_cp_project.argtypes = [vp, vp, i64, vp, vp, vp, C.POINTER(SolveOptions), vp, vp, vp,
                                      i32p, i32p, vp, u8p, u8p, vp]
     lib.purin_cp_project.restype = C.c_int
+    lib.purin_cp_project_noalloc.argtypes = lib.purin_cp_project.argtypes
+    lib.purin_cp_project_noalloc.restype = C.c_int
     lib.purin_cp_project_values.argtypes = [vp, vp, i64, vp, vp, vp, vp, C.POINTER(SolveOptions),
                                             vp, vp, vp, i32p, i32p, vp, u8p, u8p, vp]
     lib.purin_cp_project_values.restype = C.c_int

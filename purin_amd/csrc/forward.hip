@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -289,12 +290,17 @@ template <typename T>
 static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char* sv, char* ws,
                         const purin_cp_solve_options& o, size_t lds, bool early = false,
                         int64_t batch = 0, T tol = T(0), const T* tolv = nullptr,
-                        int32_t* done = nullptr, int32_t* count = nullptr) {
+                        int32_t* done = nullptr, int32_t* count = nullptr, bool noalloc = false) {
   constexpr int BT = res_tile<T>();
   const int64_t Bp = L.Bp, tiles = Bp / BT;
   const int Kr = p->res_mr * kResThreads, Kc = p->res_mc * kResThreads;
   // the step schedule built with the plan covers kSchedCapacity iterations;
-  // a longer call grows it stream-ordered
+  // a longer call grows it stream-ordered (not in the no-allocation entry)
+  if (noalloc && o.max_iterations > p->res_sched_len)
+    return set_error(PURIN_CP_ERR_ARG,
+                     "max_iterations exceeds the plan's step schedule (" +
+                         std::to_string(p->res_sched_len) +
+                         " iterations) in the no-allocation entry point");
   if (int rc = ensure_schedule(p, o.max_iterations, st, false)) return rc;
   Res<T> R{};
   R.n = (int)p->n;
@@ -366,7 +372,8 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
 template <typename T>
 int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout& L, char* sv,
                    char* ws, const purin_cp_solve_options& o, T tol_scalar, const T* tolv,
-                   const PerSample<T>* ps = nullptr, const QPRun<T>* qp = nullptr) {
+                   const PerSample<T>* ps = nullptr, const QPRun<T>* qp = nullptr,
+                   bool noalloc = false) {
   const int64_t Bp = L.Bp;
   constexpr int64_t TS = tile_samples<T>();
   Iter<T> A{};
@@ -427,7 +434,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   // the resident kernel takes one schedule of scalar steps for the whole tile
   if (lds && !o.streaming && !p->diag && !ps && !qp) {
     if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds, early, batch, tol_scalar, tolv, done,
-                                 count)) return rc;
+                                 count, noalloc)) return rc;
     if (!early) {
       const int32_t cnt = (int32_t)o.max_iterations;
       k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);
@@ -600,15 +607,66 @@ static int check_layout_args(purin_cp_plan* p, int64_t batch) {
   return PURIN_CP_OK;
 }
 
-// This call's buffers: the plan workspace (grown stream-ordered).
+// Scratch of the no-allocation projection entry (purin_cp_project_noalloc):
+// the plan workspace (and the saved state when the caller passes none) of one
+// call, in a static device array that every GPU the library runs on holds
+// until the process ends.  Host code never uses the array's name as an
+// address: scratch_init_device() looks up each device's own copy once (with
+// that device current) and keeps the pointer per device.
+constexpr size_t kScratchBytes = (size_t)PURIN_CP_NOALLOC_SCRATCH_BYTES;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kScratchDevices] = {};
+
+int scratch_init_device(int device) {
+  if (device < 0 || device >= kScratchDevices)
+    return set_error(PURIN_CP_ERR_UNSUPPORTED, "device ordinal beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return PURIN_CP_OK;
+  int cur = -1;
+  PURIN_HIP(hipGetDevice(&cur));
+  if (cur != device) PURIN_HIP(hipSetDevice(device));
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (cur != device) (void)hipSetDevice(cur);
+  if (e != hipSuccess) return hip_check(e, "hipGetSymbolAddress(scratch)");
+  if (!ptr) return set_error(PURIN_CP_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+  g_scratch_ptr[device] = ptr;
+  return PURIN_CP_OK;
+}
+
+// This call's buffers: the plan workspace (grown stream-ordered) or, for the
+// no-allocation entry, the device's scratch array.
 template <typename T>
 static int prepare_buffers(purin_cp_plan* p, hipStream_t st, int64_t batch, void* saved,
-                           Layout* L, char** sv, char** ws, bool values = false, int extras = 0) {
+                           Layout* L, char** sv, char** ws, bool values = false, int extras = 0,
+                           bool noalloc = false) {
   *L = make_layout(p, batch, values, extras);
   int err = PURIN_CP_OK;
   const size_t need = L->ws_end + (saved ? 0 : L->saved_end);
-  char* base = (char*)workspace(p, need, st, &err);
-  if (!base) return err;
+  char* base = nullptr;
+  if (noalloc) {
+    int cur = -1;
+    PURIN_HIP(hipGetDevice(&cur));
+    if (cur != p->device)
+      return set_error(PURIN_CP_ERR_ARG, "the plan was created on device " +
+                                             std::to_string(p->device) +
+                                             ", not the current device " + std::to_string(cur));
+    if (need > kScratchBytes)
+      return set_error(PURIN_CP_ERR_ARG,
+                       "batch too large for the no-allocation entry point: the call needs " +
+                           std::to_string(need) + " bytes of scratch, the maximum is " +
+                           std::to_string(kScratchBytes));
+    {
+      std::lock_guard<std::mutex> lock(g_scratch_mu);
+      base = (char*)g_scratch_ptr[p->device];
+    }
+    if (!base) return set_error(PURIN_CP_ERR_HIP, "no scratch address for this device");
+  } else {
+    base = (char*)workspace(p, need, st, &err);
+    if (!base) return err;
+  }
   *ws = base;
   *sv = saved ? (char*)saved : base + L->ws_end;
   return PURIN_CP_OK;
@@ -700,7 +758,7 @@ static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T
                         const T* rhs, const T* mult0, const purin_cp_solve_options& o, T* y,
                         T* mult, T* slacks, int32_t* status, int32_t* iterations, T* residual,
                         uint8_t* finite_out, uint8_t* eligible, void* saved,
-                        const T* values = nullptr, bool per_sample = false) {
+                        const T* values = nullptr, bool per_sample = false, bool noalloc = false) {
   int rc = check_layout_args<T>(p, batch);
   if (rc) return rc;
   if (!target || (p->M && !rhs)) return set_error(PURIN_CP_ERR_ARG, "NULL input array");
@@ -712,8 +770,15 @@ static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T
     return set_error(PURIN_CP_ERR_ARG, "tolerance must be positive and finite");
   Layout L;
   char *sv, *ws;
+  if (noalloc && o.timing)
+    return set_error(PURIN_CP_ERR_ARG, "timing is not available in the no-allocation entry point");
+  if (noalloc && p->res_ok && o.max_iterations > p->res_sched_len)
+    return set_error(PURIN_CP_ERR_ARG,
+                     "max_iterations exceeds the plan's step schedule (" +
+                         std::to_string(p->res_sched_len) +
+                         " iterations) in the no-allocation entry point");
   if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, per_sample,
-                               mult0 ? kLayoutWarm : 0)))
+                               mult0 ? kLayoutWarm : 0, noalloc)))
     return rc;
   const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
   constexpr int64_t TS = tile_samples<T>();
@@ -755,7 +820,8 @@ static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T
                                          (T*)(sv + L.HI), (int32_t*)(sv + L.feas), batch);
   // tolerance = tol * min(1, min_i scale_i) (bounds.py:233-236)
   const T tol_cp = (T)tol_cfg * std::min((T)1, (T)p->tol_factor);
-  if ((rc = run_iterations<T>(p, st, batch, L, sv, ws, o, tol_cp, nullptr, ps))) return rc;
+  if ((rc = run_iterations<T>(p, st, batch, L, sv, ws, o, tol_cp, nullptr, ps, nullptr, noalloc)))
+    return rc;
   // post-processing (bounds.py:247-317)
   Post<T> P{};
   P.K = kept_matrix<T>(p, false);
@@ -1016,6 +1082,27 @@ int purin_cp_project(purin_cp_plan* p, void* stream, int64_t batch, const void* 
   return project_impl<float>(p, st, batch, (const float*)target, (const float*)rhs,
                              (const float*)mult0, o, (float*)y, (float*)mult, (float*)slacks,
                              status, iterations, (float*)residual, finite_out, eligible, saved);
+}
+
+int purin_cp_project_noalloc(purin_cp_plan* p, void* stream, int64_t batch, const void* target,
+                             const void* rhs, const void* mult0,
+                             const purin_cp_solve_options* opts, void* y, void* mult,
+                             void* slacks, int32_t* status, int32_t* iterations, void* residual,
+                             uint8_t* finite_out, uint8_t* eligible, void* saved) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
+  purin_cp_solve_options o;
+  purin_cp_default_solve_options(&o);
+  if (opts) o = *opts;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->dtype == PURIN_CP_F64)
+    return project_impl<double>(p, st, batch, (const double*)target, (const double*)rhs,
+                                (const double*)mult0, o, (double*)y, (double*)mult,
+                                (double*)slacks, status, iterations, (double*)residual,
+                                finite_out, eligible, saved, nullptr, false, true);
+  return project_impl<float>(p, st, batch, (const float*)target, (const float*)rhs,
+                             (const float*)mult0, o, (float*)y, (float*)mult, (float*)slacks,
+                             status, iterations, (float*)residual, finite_out, eligible, saved,
+                             nullptr, false, true);
 }
 
 int purin_cp_project_values(purin_cp_plan* p, void* stream, int64_t batch, const void* values,

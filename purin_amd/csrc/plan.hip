@@ -665,6 +665,8 @@ int purin_cp_plan_create(purin_cp_plan** out, int32_t dtype, int64_t n, int64_t 
   }
   // the resident kernel's step schedule, for calls of up to kSchedCapacity iterations
   if (rc == PURIN_CP_OK && p->res_ok) rc = ensure_schedule(p, kSchedCapacity, nullptr, true);
+  // this device's address of the no-allocation entry's scratch array
+  if (rc == PURIN_CP_OK) rc = scratch_init_device(p->device);
   if (rc != PURIN_CP_OK) {
     purin_cp_plan_destroy(p);
     return rc;

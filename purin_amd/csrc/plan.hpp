@@ -111,6 +111,9 @@ void* workspace(purin_cp_plan* p, size_t bytes, hipStream_t stream, int* err, bo
 // the host and uploaded synchronously at plan creation (at_create), or grown
 // stream-ordered on ``stream`` (pinned staging, hipMallocAsync / hipFreeAsync).
 int ensure_schedule(purin_cp_plan* p, int64_t iters, hipStream_t stream, bool at_create);
+// The no-allocation entry's scratch (forward.hip): look up this device's copy
+// of the static array once, with the device current.
+int scratch_init_device(int device);
 }  // namespace purin
 
 #define PURIN_HIP(call)                                        \

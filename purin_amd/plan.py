@@ -252,11 +252,14 @@ class Plan:
 
     def project(self, target, rhs, *, multipliers0=None, tolerance=1e-9, max_iterations=10000,
                 early_stop=True, check_every=32, shared_bounds=False, save=False, timing=False,
-                streaming=False, values=None):
+                streaming=False, values=None, noalloc=False):
         """Full projection (``purin_cp_project``): BoundProjection.solve semantics.
 
         ``values`` (B, nnz): per-sample coefficients in the plan's CSR entry order
         (``purin_cp_project_values``); the plan's own coefficients are then unused.
+        ``noalloc``: run ``purin_cp_project_noalloc`` (the library allocates no
+        device memory during the call; its buffers sit in a static per-GPU
+        scratch array of ``_lib.NOALLOC_SCRATCH_BYTES``).
         """
         batch = target.shape[0]
         M = self.me + self.mi
@@ -284,13 +287,16 @@ class Plan:
         elig = self._empty(batch, dtype=torch.uint8)
         saved = self._empty(self.saved_bytes(batch), dtype=torch.uint8) if save else None
         if values is not None:
+            if noalloc:
+                raise ValueError("the no-allocation entry takes the plan's own coefficients")
             _lib.check(self.lib.purin_cp_project_values(
                 self.handle, _stream(), batch, _ptr(values), _ptr(target), _ptr(rhs),
                 _ptr(mult0), C.byref(o), _ptr(y), _ptr(mult), _ptr(slacks), _i32(status),
                 _i32(it), _ptr(res), _u8(fin), _u8(elig), _ptr(saved)))
             return ProjectOutput(y, mult, slacks, status, it, res, fin.bool(), elig.bool(),
                                  saved)
-        _lib.check(self.lib.purin_cp_project(
+        entry = self.lib.purin_cp_project_noalloc if noalloc else self.lib.purin_cp_project
+        _lib.check(entry(
             self.handle, _stream(), batch, _ptr(target), _ptr(rhs), _ptr(mult0), C.byref(o),
             _ptr(y), _ptr(mult), _ptr(slacks), _i32(status), _i32(it), _ptr(res), _u8(fin),
             _u8(elig), _ptr(saved)))
