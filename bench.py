@@ -12,18 +12,32 @@ recovery, statuses), with the inputs already resident in device memory.
 configurations the same way.
 
 Printed: one JSON line with the driver's fields plus
-  roofline      the dominant kernel (the resident CP kernel; the column pass when
-                the streaming passes run) against HBM peak: its algorithmic bytes
-                per launch over its average duration, measured with HIP events
-                on the launch stream (instrumented replay), and its HBM traffic
-                from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
+  roofline      the dominant kernel against the resource that bounds it.  The
+                resident CP kernel keeps the iterate on chip, so HBM does not
+                bound it: its bound is the L2 -> CU stream of the shared matrix
+                (chunk-stream bytes per launch over the launch's duration, HIP
+                events on the launch stream) against the best rate the
+                ``k_probe_stream`` ceiling probe (libpurin_probe.so) reaches at
+                the same launch shape, measured in the same run; ``lds`` gives
+                its LDS bytes against the ``k_probe_lds`` ceiling, and ``hbm``
+                the algorithmic state bytes against the 8 TB/s HBM peak (context
+                only).  For the streaming passes (config 3) the bound is HBM.
+                ``traffic`` is the HBM bytes per launch from the committed
+                rocprofv3 FETCH_SIZE / WRITE_SIZE summary;
+  per_sample_bounds  the same projection with per-sample bounds (the kernels a
+                caller whose bound rows depend on the parameters runs);
+  purin_api     the same projection through the PURIN-API front end
+                (``Distance(problem).prepare(batch_size=...)``), which picks the
+                shared-bounds kernels itself for constant bound rows;
   adjoint       (config2) the implicit VJP w.r.t. the candidates and b, h
                 (``purin_cp_adjoint``, cotangents N(0,1) from seed 5) at the
                 2000-iteration state with eligibility forced on, timed separately
                 from the forward;
   cpu_baseline  the checker's C restatement of the CP loop (bit-equal to the NumPy
-                oracle) on a bounded sample of the same workload, all cores
-                (``value``) and one core (``one_core``).
+                oracle) on a bounded sample of the same workload, on the threads
+                this process may use (``value``) and one core (``one_core``);
+  cpu_baseline_adjoint  the NumPy oracle's GMRES pullback (the checker) on a
+                bounded sample of the config5 VJP, one thread.
 """
 
 from __future__ import annotations
@@ -38,6 +52,8 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+PROBE_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "purin_amd",
+                         "libpurin_probe.so")
 
 METRICS = {
     2: "CP projections/sec (n=4096, batch 1024, fp64) + achieved HBM GB/s % of peak",
@@ -78,7 +94,8 @@ def cpu_baseline(w, samples_one, samples_all):
     coef = [list(values[w.indptr[i]:w.indptr[i + 1]]) for i in range(w.rows_total)]
     canon = op.Canonical(n=w.n, me=w.me, rows=rows, coef=coef)
     cfg = op.Config(accelerated=w.accelerated, max_iterations=w.iterations, early_stop=False)
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    affinity = len(os.sched_getaffinity(0))
+    cores = cpu_threads()
 
     def leg(samples, threads):
         target = np.asarray(w.target[:samples], w.dtype)
@@ -98,10 +115,61 @@ def cpu_baseline(w, samples_one, samples_all):
         "kind": "port",
         "sample": (f"C restatement of the CP loop (oracle/cp_loop.c, OpenMP over samples; "
                    f"set-up by the NumPy oracle, untimed), {w.iterations} iterations: "
-                   f"{samples_all} samples on {cores} threads in {t_full:.1f} s; "
-                   f"{samples_one} samples on 1 thread in {t_one:.1f} s = {one:.2f} "
-                   f"projections/s; {_cpu_model()}"),
+                   f"{samples_all} samples on {cores} threads (every core of this "
+                   f"process's CPU set: {affinity} in the affinity mask"
+                   + (f", OMP_NUM_THREADS={os.environ['OMP_NUM_THREADS']}"
+                      if os.environ.get("OMP_NUM_THREADS") else "")
+                   + f") in {t_full:.1f} s; {samples_one} samples on 1 thread in {t_one:.1f} s "
+                   f"= {one:.2f} projections/s; {_cpu_model()}"),
         "one_core": one,
+        "affinity_cores": affinity,
+    }
+
+
+def cpu_threads():
+    """Threads for the all-core CPU leg: every core in this process's affinity
+    mask, or fewer when OMP_NUM_THREADS caps the process (the GPU box sets it to
+    the box's CPU share)."""
+    cores = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        cores = min(cores, int(env))
+    return max(1, cores)
+
+
+def cpu_baseline_adjoint(w, plan, out_y, out_dual, lower, upper, rhs_k, samples):
+    """The NumPy oracle's implicit VJP (bounds.py:80-165 with the CGS2 GMRES of
+    operators.py:792-1125; the checker of the GPU adjoint) on ``samples`` samples
+    of the config5 workload, linearised at the same forward state, one thread."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import adjoint as oadj
+    from oracle import projection as op
+
+    cfg = op.Config(accelerated=True, max_iterations=w.iterations, early_stop=False)
+    one = op.Canonical(n=w.n, me=w.me, rows=w.rows(), coef=w.coefs())
+    pre = op.presolve(one, w.rhs[None, :], cfg, np.float64)
+    ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
+    sub = np.arange(samples)
+    args = (pre.kept_values[0], ksup, kmask, w.me, out_y[sub], out_dual[sub],
+            np.ones(samples, bool), w.target[sub], rhs_k[sub],
+            np.broadcast_to(lower, (samples, w.n)), np.broadcast_to(upper, (samples, w.n)),
+            w.cotangent[sub], cfg)
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        res = oadj.adjoint(*args)
+        seconds = time.perf_counter() - t0
+    info = np.asarray(res.info)
+    return {
+        "value": samples / seconds,
+        "unit": "VJPs/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"NumPy oracle adjoint (oracle/adjoint.py: mask-form pullback, batched CGS2 "
+                   f"GMRES restart 30, max 100, tol 1e-9) on {samples} samples of the config5 "
+                   f"VJP at the {w.iterations}-iteration state, eligibility forced, one thread, "
+                   f"in {seconds:.1f} s (GMRES info {dict(zip(*np.unique(info, return_counts=True)))}); "
+                   f"{_cpu_model()}"),
     }
 
 
@@ -133,6 +201,61 @@ def copy_calibration(torch, mib):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes": n * 8, "dispatches": 3}), flush=True)
+
+
+def probe_ceilings(torch, groups, lds_bytes, stream_bytes_iter):
+    """Best rates (GB/s) of the ceiling probes (libpurin_probe.so) at the resident
+    kernel's launch shape: ``groups`` workgroups of 1024 threads.  The L2 -> CU
+    chunk stream is probed with the kernel's per-wavefront stream length and its
+    dynamic LDS (one workgroup per CU) and with 64 KiB (two per CU), 1, 2 and 4
+    chunks in flight; LDS reads with 1 to 8 conflict-free ds_read_b128 in flight.
+    Each variant: one warm-up launch, then the mean of 3 timed launches (HIP
+    events on the current stream)."""
+    import ctypes as C
+
+    lib = C.CDLL(PROBE_LIB)
+    vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int32
+    lib.purin_probe_stream.argtypes = [vp, vp, i64, i64, i32, i32, i32, i32, i32, vp, i64,
+                                       C.POINTER(C.c_double)]
+    lib.purin_probe_lds.argtypes = [vp, i32, i32, i32, i32, i32, vp, i64, C.POINTER(C.c_double)]
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dev = torch.device("cuda:0")
+    sink = torch.zeros(1024, dtype=torch.int32, device=dev)
+    chunk = 3072
+    wave_chunks = max(4, int(round(stream_bytes_iter / 16 / chunk / 4)) * 4)
+    buf = torch.zeros(16 * wave_chunks * chunk, dtype=torch.uint8, device=dev)
+    per_iter = groups * 16 * wave_chunks * chunk
+    iters = max(1, int(300e9 // per_iter))
+    ms = C.c_double()
+    l2 = []
+    for lds in sorted({int(lds_bytes), 65536}):
+        for unroll in (1, 2, 4):
+            for reps in (1, 3):
+                rc = lib.purin_probe_stream(stream, C.c_void_p(buf.data_ptr()), buf.numel(),
+                                            wave_chunks, iters, groups, lds, unroll, reps,
+                                            C.c_void_p(sink.data_ptr()), sink.numel() * 4,
+                                            C.byref(ms))
+                if rc != 0:
+                    raise RuntimeError(f"purin_probe_stream failed ({rc})")
+            l2.append({"lds_bytes": lds, "unroll": unroll, "ms": ms.value,
+                       "GBs": per_iter * iters / (ms.value / 1e3) / 1e9})
+    lds_rates = []
+    lds_iter = groups * 1024 * 16
+    for lds in sorted({max(int(lds_bytes), 65536), 65536}):
+        for unroll in (1, 2, 4, 8):
+            it = max(1, int(600e9 // (lds_iter * unroll)))
+            for reps in (1, 3):
+                rc = lib.purin_probe_lds(stream, it, groups, lds, unroll, reps,
+                                         C.c_void_p(sink.data_ptr()), sink.numel() * 4,
+                                         C.byref(ms))
+                if rc != 0:
+                    raise RuntimeError(f"purin_probe_lds failed ({rc})")
+            lds_rates.append({"lds_bytes": lds, "unroll": unroll, "ms": ms.value,
+                              "GBs": lds_iter * unroll * it / (ms.value / 1e3) / 1e9})
+    best_l2 = max(l2, key=lambda r: r["GBs"])
+    best_lds = max(lds_rates, key=lambda r: r["GBs"])
+    return {"l2": best_l2, "lds": best_lds, "l2_all": l2, "lds_all": lds_rates,
+            "wave_chunks": wave_chunks, "groups": groups}
 
 
 def adjoint_bytes(batch, ws, width, steps, restart):
@@ -289,6 +412,39 @@ def run_mode(args, torch):
     print(json.dumps(line), flush=True)
 
 
+def purin_api_timing(torch, w, values, root, target, steps):
+    """One projection through the PURIN-API front end (``Distance`` /
+    ``WeightedDistance`` over a ``MatrixProblem`` of the workload's rows), timed
+    per call with the inputs on the device."""
+    import scipy.sparse as sp
+
+    from purin_amd.config import ChambollePockConfig
+    from purin_amd.problems import MatrixProblem
+    from purin_amd.projection import Distance, WeightedDistance
+
+    me, M = w.me, w.rows_total
+    A = sp.csr_matrix((w.data, w.indices, w.indptr), shape=(M, w.n))
+    problem = MatrixProblem(P=sp.identity(w.n, format="csr"), q0=np.zeros(w.n), A_eq=A[:me],
+                            b_eq0=w.rhs[:me], A_ineq=A[me:], b_ineq0=w.rhs[me:])
+    cfg = ChambollePockConfig(accelerated=w.accelerated, max_iterations=w.iterations,
+                              early_stop=False)
+    B = w.target.shape[0]
+    tdtype = torch.float64 if w.dtype == np.float64 else torch.float32
+    if w.metric is not None:
+        layer = WeightedDistance(problem, tuple(np.asarray(w.metric, np.float64)),
+                                 config=cfg).prepare(batch_size=B, dtype=tdtype)
+    else:
+        layer = Distance(problem, config=cfg).prepare(batch_size=B, dtype=tdtype)
+    y_hat = torch.as_tensor(w.target, device="cuda:0")
+    with torch.no_grad():
+        layer(y_hat)
+        ms, _ = time_calls(torch, lambda: layer(y_hat), steps)
+    return {"ms_per_step": ms, "value": B / (ms / 1e3), "unit": "projections/s",
+            "shared_bounds": layer.shared_bounds,
+            "what": "Distance(MatrixProblem(rows), ChambollePockConfig(accelerated, "
+                    "max_iterations, early_stop=False)).prepare(batch_size=B)(y_hat)"}
+
+
 def time_calls(torch, fn, count):
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
@@ -317,6 +473,8 @@ def main():
                     help="samples of the all-core CPU baseline leg")
     ap.add_argument("--cpu-samples-one", type=int, default=None,
                     help="samples of the one-core CPU baseline leg")
+    ap.add_argument("--cpu-adjoint-samples", type=int, default=32,
+                    help="samples of the one-thread CPU adjoint leg (config2)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-adjoint", action="store_true", help="skip the adjoint leg (config2)")
     ap.add_argument("--no-streaming", action="store_true",
@@ -387,11 +545,77 @@ def main():
         dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == "k_col_pass" else (bytes_row, row_ms)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
     traffic = traffic_from_profiles(args.config, dominant, B, w.iterations)
+    if tm["resident"]:
+        # The iterate stays on chip: what the launch moves is the shared matrix's
+        # chunk streams from L2 (every tile re-reads them each iteration) and the
+        # LDS gathers.  Price it against the probes' ceilings at the same shape.
+        info = plan.info
+        bt = 2 if ws == 8 else 4                        # samples per workgroup (16 bytes)
+        tiles = -(-B // (64 * bt)) * 64                 # the padded batch's tiles
+        l2_bytes = tiles * iters * int(info.resident_stream_bytes)
+        entries = int(info.resident_stream_bytes) // (12 if ws == 8 else 8)
+        lds_iter = 16 * (entries + 2 * int(info.resident_row_slots) + int(info.resident_col_slots))
+        lds_launch = tiles * iters * lds_iter
+        lds_alloc = (n + 1 + m + 1) * 16
+        ceil = probe_ceilings(torch, tiles, lds_alloc, int(info.resident_stream_bytes))
+        l2_rate = l2_bytes / (dom_ms / 1e3) / 1e9
+        lds_rate = lds_launch / (dom_ms / 1e3) / 1e9
+        roofline = {
+            "bound": "l2",
+            "kernel": dominant,
+            "achieved": l2_rate,
+            "peak": ceil["l2"]["GBs"],
+            "unit": "GB/s",
+            "frac": l2_rate / ceil["l2"]["GBs"],
+            "traffic": traffic,
+            "bytes_per_launch": l2_bytes,
+            "avg_launch_ms": dom_ms,
+            "what": "L2 -> CU bytes of the shared matrix's chunk streams: "
+                    f"{int(info.resident_stream_bytes)} B per workgroup per iteration x "
+                    f"{tiles} workgroups x {iters} iterations",
+            "peak_source": "measured in this run: best rate of the k_probe_stream ceiling probe "
+                           f"(libpurin_probe.so) at {tiles} workgroups of 1024 threads, "
+                           f"{ceil['wave_chunks']} 3072-byte chunks per wavefront per pass, "
+                           f"{ceil['l2']['unroll']} in flight, {ceil['l2']['lds_bytes']} B LDS",
+            "lds": {"achieved": lds_rate, "peak": ceil["lds"]["GBs"],
+                    "frac": lds_rate / ceil["lds"]["GBs"], "bytes_per_launch": lds_launch,
+                    "what": f"16 B per gathered entry ({entries} per workgroup per iteration, "
+                            "padding included) + the slots' own entries (2 per row, 1 per "
+                            "column)",
+                    "peak_source": "measured in this run: best rate of k_probe_lds "
+                                   "(conflict-free ds_read_b128)"},
+            "hbm": {"achieved": achieved, "peak": HBM_PEAK_GBS, "frac": achieved / HBM_PEAK_GBS,
+                    "bytes_per_launch": dom_bytes,
+                    "note": "algorithmic state bytes B*ws*(5n+3m) per iteration; they stay "
+                            "on chip, so this exceeds the HBM peak and does not bound the "
+                            "kernel (context only)"},
+            "probes": {"l2": ceil["l2_all"], "lds": ceil["lds_all"]},
+        }
+    else:
+        roofline = {
+            "bound": "hbm",
+            "kernel": dominant,
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "bytes_per_launch": dom_bytes,
+            "avg_launch_ms": dom_ms,
+        }
     # the streaming two-pass path on the same inputs, for comparison
     streaming_ms = None
     if tm["resident"] and not args.no_streaming:
         streaming_ms, _ = time_calls(
             torch, lambda: plan.project(target, rhs, streaming=True, **kw), 1)
+    # per-sample bounds: the kernels of a caller whose bound rows depend on theta
+    kw_ps = dict(kw, shared_bounds=False)
+    plan.project(target, rhs, **kw_ps)
+    ps_ms, ps_out = time_calls(torch, lambda: plan.project(target, rhs, **kw_ps), args.steps)
+    same = bool(torch.equal(ps_out.y, out.y))
+    # the PURIN-API front end on the same problem (constant bound rows: it
+    # selects the shared-bounds kernels by itself)
+    api = purin_api_timing(torch, w, values, root, target, args.steps)
 
     line = {
         "metric": METRICS[args.config],
@@ -420,17 +644,16 @@ def main():
             "nnz_kept": int(plan.info.nnz_kept), "batch": B, "iterations": w.iterations,
             "parallelism": "1 GPU (batch-parallel)",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": dominant,
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": traffic,
-            "bytes_per_launch": dom_bytes,
-            "avg_launch_ms": dom_ms,
+        "roofline": roofline,
+        "per_sample_bounds": {
+            "ms_per_step": ps_ms,
+            "value": B / (ps_ms / 1e3),
+            "unit": "projections/s",
+            "y_bit_identical_to_shared": same,
+            "what": "the same purin_cp_project call with shared_bounds = 0 (lower/upper read "
+                    "per sample: the kernels of bound rows whose rhs depends on theta)",
         },
+        "purin_api": api,
         "iteration": {
             "cp_iterations_per_s": w.iterations * 1e3 / ms_per_step,
             "resident_kernel": bool(tm["resident"]),
@@ -508,6 +731,22 @@ def main():
         one = args.cpu_samples_one or default_sample[0]
         full = args.cpu_samples or default_sample[1]
         line["cpu_baseline"] = cpu_baseline(w, min(one, B), min(full, B))
+        if adjoint_leg:
+            # the checker's adjoint on the first samples, linearised at the GPU's
+            # forward state of the same samples (samples are independent)
+            from oracle import projection as op
+
+            k = min(args.cpu_adjoint_samples, B)
+            cfg = op.Config(accelerated=True, max_iterations=w.iterations, early_stop=False)
+            one_c = op.Canonical(n=w.n, me=w.me, rows=w.rows(), coef=w.coefs())
+            pre = op.presolve(one_c, w.rhs[None, :], cfg, np.float64)
+            rhs_k = np.tile(pre.kept_rhs, (k, 1))
+            w.cotangent = np.random.default_rng(5).normal(0.0, 1.0, (B, n))
+            st = plan.solve(rhs_k, w.target[:k], pre.lower[0], pre.upper[0],
+                            max_iterations=w.iterations, early_stop=False, shared_bounds=True)
+            line["cpu_baseline_adjoint"] = cpu_baseline_adjoint(
+                w, plan, st.y.cpu().numpy(), st.dual.cpu().numpy(), pre.lower[0], pre.upper[0],
+                rhs_k, k)
     print(json.dumps(line), flush=True)
 
 

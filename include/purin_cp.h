@@ -125,6 +125,16 @@ typedef struct {
   double adjoint_norm;      /* power-iteration L of the adjoint (bounds.py:88-101) */
   double adjoint_tau, adjoint_sigma;
   double tolerance_factor;  /* min(1, min_i scale_i): forward tolerance = tol * factor */
+  /* Measurement figures of the resident (on-chip) kernel, 0 when it does not
+   * apply (no reference counterpart): the bytes of the shared matrix's chunk
+   * streams one workgroup (one tile of samples) reads from L2 per iteration in
+   * the fixed-iteration and the early-stop kernels, and the row and column
+   * slots of a workgroup (each slot reads or writes its own 16-byte LDS entry
+   * once per pass). */
+  int64_t resident_stream_bytes;
+  int64_t resident_stream_bytes_early;
+  int64_t resident_row_slots;
+  int64_t resident_col_slots;
 } purin_cp_plan_info;
 
 int purin_cp_plan_get_info(const purin_cp_plan* plan, purin_cp_plan_info* info);

@@ -68,6 +68,8 @@ class PlanInfo(C.Structure):
         ("norm", C.c_double), ("tau0", C.c_double), ("sigma0", C.c_double),
         ("adjoint_norm", C.c_double), ("adjoint_tau", C.c_double), ("adjoint_sigma", C.c_double),
         ("tolerance_factor", C.c_double),
+        ("resident_stream_bytes", C.c_int64), ("resident_stream_bytes_early", C.c_int64),
+        ("resident_row_slots", C.c_int64), ("resident_col_slots", C.c_int64),
     ]
 
 

@@ -2,7 +2,8 @@
 
 The library is the product: the C ABI of ``include/purin_cp.h``.  It is built
 here, into ``purin_amd/``, so that the built ``.so`` travels with the source
-tree to the GPU machine.
+tree to the GPU machine.  ``libpurin_probe.so`` (``include/purin_probe.h``)
+holds the ceiling probes that ``bench.py`` times beside the resident kernel.
 """
 
 from __future__ import annotations
@@ -15,6 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libpurin_cp.so")
 SOURCES = ["plan.hip", "forward.hip", "adjoint.hip"]
+PROBE_LIB = os.path.join(HERE, "libpurin_probe.so")
+PROBE_SOURCES = ["probe.hip"]
 ARCH = os.environ.get("PURIN_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
@@ -25,21 +28,26 @@ FLAGS = [
 ]
 
 
-def sources():
-    return [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+def sources(names=SOURCES):
+    return [os.path.join(CSRC, s) for s in names if os.path.exists(os.path.join(CSRC, s))]
 
 
-def build(verbose: bool = False) -> str:
+def _hipcc(srcs, out, verbose):
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = LIB + ".tmp"
-    cmd = [hipcc, *FLAGS, *sources(), "-o", tmp]
+    tmp = out + ".tmp"
+    cmd = [hipcc, *FLAGS, *srcs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError("hipcc failed building libpurin_cp.so")
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"hipcc failed building {os.path.basename(out)}")
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    _hipcc(sources(), LIB, verbose)
+    _hipcc(sources(PROBE_SOURCES), PROBE_LIB, verbose)
     return LIB
 
 

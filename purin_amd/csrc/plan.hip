@@ -481,6 +481,17 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
           return (int64_t)total;
         };
         stream_e.reserve(stream.size() * 2);
+        // matrix-stream bytes one workgroup reads per iteration: every
+        // wavefront's row and column chunks (the early-stop kernel walks the
+        // row chunks twice)
+        int64_t fixed_chunks = 0, early_chunks = 0;
+        for (int w = 0; w < 16; ++w) {
+          const int64_t rch = chunks_of(wtab[4 * w + 1]), cch = chunks_of(wtab[4 * w + 2]);
+          fixed_chunks += rch + cch;
+          early_chunks += 2 * rch + cch;
+        }
+        p->res_iter_bytes = fixed_chunks * (int64_t)CB;
+        p->res_iter_bytes_e = early_chunks * (int64_t)CB;
         for (int w = 0; w < 16; ++w) {
           const int64_t first = wtab[4 * w], rch = chunks_of(wtab[4 * w + 1]),
                         cch = chunks_of(wtab[4 * w + 2]);
@@ -706,6 +717,10 @@ int purin_cp_plan_get_info(const purin_cp_plan* p, purin_cp_plan_info* info) {
   info->adjoint_tau = p->tau_adj;
   info->adjoint_sigma = p->sigma_adj;
   info->tolerance_factor = p->tol_factor;
+  info->resident_stream_bytes = p->res_ok ? p->res_iter_bytes : 0;
+  info->resident_stream_bytes_early = p->res_ok ? p->res_iter_bytes_e : 0;
+  info->resident_row_slots = p->res_ok ? (int64_t)p->res_mr * kResThreads : 0;
+  info->resident_col_slots = p->res_ok ? (int64_t)p->res_mc * kResThreads : 0;
   return PURIN_CP_OK;
 }
 

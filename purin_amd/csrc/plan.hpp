@@ -89,6 +89,8 @@ struct purin_cp_plan {
   unsigned char* res_stream_e = nullptr;  // the early-stop kernel's streams (rows, columns, rows)
   int32_t* res_wtab_e = nullptr;
   int64_t res_stream_bytes = 0;
+  int64_t res_iter_bytes = 0;        // matrix-stream bytes a workgroup reads per iteration
+  int64_t res_iter_bytes_e = 0;      // the same for the early-stop kernel
   void* res_sched = nullptr;         // per-iteration (sigma, a, delta, theta)
   int64_t res_sched_len = 0;         // iterations the schedule holds
   std::vector<void*> sched_staging;  // pinned host copies of grown schedules (freed with the plan)

@@ -153,22 +153,34 @@ __device__ __forceinline__ void consume_chunk(const Chunk<T>& c, V& acc) {
 
 // Sum over the ``nch`` chunks of one slot.  On entry b0 holds (or is loading)
 // the slot's first chunk and ``pos`` indexes the next chunk of the wave's
-// stream; on exit b0 holds the chunk after the slot's last one.
+// stream; on exit b0 holds the chunk after the slot's last one.  The chunks
+// are taken in pairs by a loop whose every pass issues the same loads (the
+// next chunk into b1, then the one after into b0), so the compiler waits only
+// for the chunk being consumed (the later chunk stays in flight); an odd last
+// chunk is consumed after the loop.  Summation order: the slot's chunks in
+// stream order, entries in order.
 template <typename T, typename V>
 __device__ __forceinline__ V slot_sum(int nch, Chunk<T>& b0, Chunk<T>& b1, uint32_t& pos,
                                       const unsigned char* __restrict__ stream, uint32_t lane16) {
   constexpr uint64_t CB = res_chunk_bytes<T>();
   V acc = V(T(0));
-  for (int k = 0; k < nch; k += 2) {
-    const bool two = k + 1 < nch;
-    if (two) {
-      load_chunk(b1, stream, pos * CB, lane16);
-      ++pos;
-    }
+  int k = 0;
+  for (; k + 1 < nch; k += 2) {
+    load_chunk(b1, stream, pos * CB, lane16);
+    ++pos;
+    // keep the load ahead of the consumption it overlaps (the scheduler would
+    // otherwise sink it, leaving one chunk in flight)
+    __builtin_amdgcn_sched_barrier(0);
     consume_chunk(b0, acc);
     load_chunk(b0, stream, pos * CB, lane16);
     ++pos;
-    if (two) consume_chunk(b1, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    consume_chunk(b1, acc);
+  }
+  if (k < nch) {
+    consume_chunk(b0, acc);
+    load_chunk(b0, stream, pos * CB, lane16);
+    ++pos;
   }
   return acc;
 }
@@ -206,7 +218,10 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)A.Kr;
 
   uint32_t soff_r[SLR], soff_c[SLC];
-  V y[SLC], tg[SLC], rr[SLR];
+  // the targets stay in registers except in the variant with four row and
+  // four column slots and per-sample bounds, which would spill them
+  constexpr bool kHoldTarget = SB || SLR + SLC < 8;
+  V y[SLC], tg[kHoldTarget ? SLC : 1], rr[SLR];
   uint32_t ineq = 0, nanb = 0;
 #pragma unroll
   for (int c = 0; c < SLC; ++c) {
@@ -217,8 +232,9 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
     }
     soff_c[c] = j >= 0 ? (uint32_t)j * 16u : trash_off;
-    tg[c] = j >= 0 ? Ts[c * NT + t] : vzero;
-    y[c] = tg[c];  // y0 = ybar0 = yhat (kernels.py:229-231)
+    const V t0 = j >= 0 ? Ts[c * NT + t] : vzero;
+    if constexpr (kHoldTarget) tg[c] = t0;
+    y[c] = t0;  // y0 = ybar0 = yhat (kernels.py:229-231)
     lds_write<V>(soff_c[c], y[c]);
   }
 #pragma unroll
@@ -261,8 +277,10 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
     for (int c = 0; c < SLC; ++c) {
       const int nch = (int)((ccnt >> (8 * c)) & 255u);
       // bounds are re-read each iteration (L2-resident when shared) rather
-      // than held in registers: the opaque base keeps them inside the loop
+      // than held in registers: the opaque base keeps them inside the loop;
+      // they are loaded before the gathers, which hide their latency
       typedef const __attribute__((address_space(1))) T* GP;
+      typedef const __attribute__((address_space(1))) V* GV;
       GP lb = (GP)A.Ls;
       GP hb = (GP)A.Hs;
       asm volatile("" : "+s"(lb), "+s"(hb));
@@ -271,12 +289,20 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
         lo = V(lb[c * NT + t]);
         hi = V(hb[c * NT + t]);
       } else {
-        typedef const __attribute__((address_space(1))) V* GV;
         lo = ((GV)lb)[tile * (int64_t)A.Kc + c * NT + t];
         hi = ((GV)hb)[tile * (int64_t)A.Kc + c * NT + t];
       }
+      V tgc;
+      if constexpr (kHoldTarget) {
+        tgc = tg[c];
+      } else {  // re-read (L2) in the largest per-sample-bounds variant: registers
+        typedef const __attribute__((address_space(1))) V* GVT;
+        GVT tb = (GVT)A.Ts;
+        asm volatile("" : "+s"(tb));
+        tgc = tb[tile * (int64_t)A.Kc + c * NT + t];
+      }
       const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
-      const V sv = a * y[c] - delta * tt + delta * tg[c];
+      const V sv = a * y[c] - delta * tt + delta * tgc;
       V yn;
       if (nanb & (1u << c)) {  // a NaN bound on this lane: the exact NaN-propagating clip
 #pragma unroll
@@ -485,17 +511,19 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       GP lb = (GP)A.Ls;
       GP hb = (GP)A.Hs;
       GP tb = (GP)A.Ts;
-      asm volatile("" : "+s"(lb), "+s"(hb), "+s"(tb));
       V lo, hi;
       if (SB) {
+        asm volatile("" : "+s"(lb), "+s"(hb), "+s"(tb));
         lo = V(lb[c * NT + t]);
         hi = V(hb[c * NT + t]);
-      } else {
+      }
+      const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      if (!SB) {  // per-sample bounds after the gathers (register pressure)
+        asm volatile("" : "+s"(lb), "+s"(hb), "+s"(tb));
         lo = ((GV)lb)[tile * (int64_t)A.Kc + c * NT + t];
         hi = ((GV)hb)[tile * (int64_t)A.Kc + c * NT + t];
       }
       const V tg = ((GV)tb)[tile * (int64_t)A.Kc + c * NT + t];
-      const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
       const V sv = a * y[c] - delta * tt + delta * tg;
       V yn;
       if (nanb & (1u << c)) {

@@ -63,6 +63,31 @@ def resolve_dtype(dtype):
     raise ValueError(f"dtype must be float32 or float64; got {dtype!r}")
 
 
+def constant_rows(c):
+    """Rows whose right-hand side does not depend on the parameters (a zero row
+    of ``rhs_map``)."""
+    rhs_map = np.asarray(c.rhs_map, np.float64)
+    if rhs_map.size == 0:  # no rows, or no parameters
+        return np.ones(len(c.rhs0), bool)
+    return ~np.any(rhs_map.reshape(len(c.rhs0), -1) != 0.0, axis=1)
+
+
+def bounds_are_shared(c):
+    """True when every sample gets the same variable bounds: the bound rows
+    (inequality rows with one stored entry, presolved into bounds,
+    bounds.py:320-326) all have constant right-hand sides and the coefficients
+    are shared, so lower = max rhs/coef and upper = min rhs/coef
+    (bounds.py:193-209) are the same for the whole batch.  The plan then reads
+    one copy of the bounds (``shared_bounds``), which selects the on-chip
+    kernels' broadcast-bounds variant; the results are identical either way."""
+    if c.parametric_coefficients:
+        return False
+    lengths = np.diff(np.asarray(c.indptr, np.int64))
+    bound_rows = np.zeros(len(lengths), bool)
+    bound_rows[c.me:] = lengths[c.me:] == 1
+    return bool(np.all(constant_rows(c)[bound_rows]))
+
+
 class _ProjectFn(torch.autograd.Function):
     """y = P(y_hat; rhs, values) with the implicit VJP of the HIP adjoint.
 
@@ -145,6 +170,11 @@ class PreparedChambollePockProjection:
             self.plan.set_metric(root)
         self._rhs0 = torch.as_tensor(c.rhs0, dtype=self.torch_dtype, device=self.device)
         self._rhs_map = torch.as_tensor(c.rhs_map, dtype=self.torch_dtype, device=self.device)
+        # rows whose right-hand side does not involve the parameters keep their
+        # constant value for every sample (the reference evaluates them as
+        # constants, so a non-finite theta does not reach them)
+        self._const_rows = torch.as_tensor(constant_rows(c), device=self.device)
+        self.shared_bounds = bounds_are_shared(c)
         # parameter-dependent coefficients: values(theta) = values0 + theta @ value_map.T
         # per sample (the reference's vmap(_numeric_one), bounds.py:192), scaled by the
         # metric like the shared values
@@ -176,7 +206,7 @@ class PreparedChambollePockProjection:
     # -- helpers -------------------------------------------------------------------
     def _solve_kwargs(self):
         return dict(tolerance=self.config.tolerance, max_iterations=self.config.max_iterations,
-                    early_stop=self.config.early_stop)
+                    early_stop=self.config.early_stop, shared_bounds=self.shared_bounds)
 
     def _target(self, y_hat):
         t = torch.as_tensor(y_hat).to(device=self.device, dtype=self.torch_dtype)
@@ -203,7 +233,7 @@ class PreparedChambollePockProjection:
         return theta
 
     def _rhs(self, theta):
-        return self._rhs0[None, :] + theta @ self._rhs_map.T
+        return torch.where(self._const_rows, self._rhs0, self._rhs0[None, :] + theta @ self._rhs_map.T)
 
     def _values(self, theta):
         if self._value_map is None:

@@ -196,3 +196,35 @@ def test_local_quadratic_coefficients():
     for kwargs in [dict(rho=0), dict(diagonal_floor=-1), dict(rho=np.inf)]:
         with pytest.raises(ValueError):
             pa.LocalQuadratic(_local_problem(), **kwargs)
+
+
+def test_front_end_shares_bounds_only_when_every_bound_row_is_constant():
+    """Singleton inequality rows are the presolved bounds (bounds.py:320-326);
+    their thresholds rhs/coef (bounds.py:193-209) are the same for every sample
+    when no bound row's rhs depends on theta and the coefficients are shared."""
+    from purin_amd.projection import bounds_are_shared, constant_rows
+
+    p = pa.Projection()
+    t = p.add_parameter(["b"])
+    y = p.add_variable(["u", "v"])
+    p.constraints.add(y.u + y.v == t.b, y.u >= 0, 2 * y.v <= 3, y.u - y.v <= t.b)
+    c = p.canonicalize()
+    np.testing.assert_array_equal(constant_rows(c), [False, True, True, False])
+    assert bounds_are_shared(c)          # the two-entry row may depend on theta
+    q = pa.Projection()
+    s = q.add_parameter(["b"])
+    z = q.add_variable(["u", "v"])
+    q.constraints.add(z.u + z.v == 1, z.u >= s.b)   # a bound row that moves with theta
+    assert not bounds_are_shared(q.canonicalize())
+    r = pa.Projection()
+    a = r.add_parameter(["a"])
+    x = r.add_variable(["u", "v"])
+    r.constraints.add(a.a * x.u + x.v == 1, x.u >= 0)  # per-sample coefficients
+    assert not bounds_are_shared(r.canonicalize())
+    m = pa.MatrixProblem(P=np.eye(2), q0=np.zeros(2), A_ineq=np.array([[1.0, 0.0], [0.0, 2.0]]),
+                         b_ineq0=np.ones(2), b_ineq_parameter_map=np.array([[0.0], [1.0]]))
+    assert not bounds_are_shared(m.canonicalize())
+    empty = pa.Projection()
+    empty.add_variable(["u", "v"])
+    assert bounds_are_shared(empty.canonicalize())  # no rows at all
+    assert constant_rows(empty.canonicalize()).shape == (0,)

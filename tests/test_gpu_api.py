@@ -340,3 +340,67 @@ def test_products_of_parameters_are_reported_unsupported(torch):
     p.constraints.add(y.u + y.v == t.a * t.a)
     with pytest.raises(NotImplementedError, match="affine in the parameters"):
         prepare_projection(p, method="chambolle-pock", batch_size=1)
+
+
+@pytest.mark.parametrize("early_stop", [False, True])
+def test_front_end_runs_the_resident_kernel_with_shared_bounds(torch, early_stop):
+    """A config2-shaped problem through the PURIN API: its bound rows are
+    constant, so the front end passes shared_bounds and the call runs the
+    resident kernel; the result (y, multipliers, statuses, iterations,
+    residuals, the VJP) is bit-identical to the per-sample-bounds call."""
+    import scipy.sparse as sp
+
+    from purin_amd import ChambollePockConfig, Distance
+    from purin_amd import workloads
+
+    w = workloads.small_random(31, n=900, me=120, mi=300, width=6, batch=70, accelerated=True,
+                               target_sd=0.2)
+    me, M = w.me, w.rows_total
+    A = sp.csr_matrix((w.data, w.indices, w.indptr), shape=(M, w.n))
+    from purin_amd import MatrixProblem
+
+    pa_problem = MatrixProblem(
+        P=sp.identity(w.n, format="csr"), q0=np.zeros(w.n), A_eq=A[:me], b_eq0=w.rhs[:me],
+        A_ineq=A[me:], b_ineq0=w.rhs[me:])
+    cfg = ChambollePockConfig(accelerated=True, max_iterations=500, early_stop=early_stop,
+                              tolerance=1e-3)
+    layer = Distance(pa_problem, config=cfg).prepare(batch_size=w.batch)
+    assert layer.shared_bounds
+    y_hat = torch.as_tensor(w.target, device="cuda").requires_grad_(True)
+    out = layer.solve(y_hat)
+    cot = torch.as_tensor(np.random.default_rng(3).normal(size=w.target.shape), device="cuda")
+    (g_api,) = torch.autograd.grad(out.y, y_hat, cot)
+    plan = layer.plan
+    rhs = torch.as_tensor(np.tile(w.rhs, (w.batch, 1)), device="cuda")
+    kw = dict(max_iterations=500, early_stop=early_stop, tolerance=1e-3)
+    shared = plan.project(y_hat.detach(), rhs, shared_bounds=True, timing=True, save=True, **kw)
+    assert plan.last_timing()["resident"] == 1
+    per = plan.project(y_hat.detach(), rhs, shared_bounds=False, timing=True, save=True, **kw)
+    assert plan.last_timing()["resident"] == 1
+    if early_stop:  # the stop test fired for some samples (about 380-530 iterations)
+        assert np.any(per.iterations.cpu().numpy() < 500)
+    for a, b in ((out.y, shared.y), (shared.y, per.y), (shared.multipliers, per.multipliers),
+                 (shared.status, per.status), (shared.iterations, per.iterations),
+                 (shared.residual, per.residual), (shared.eligible, per.eligible)):
+        assert torch.equal(a.detach(), b)
+    ga = plan.adjoint(shared.saved, None, None, cot, force_eligible=True)
+    gb = plan.adjoint(per.saved, None, None, cot, force_eligible=True)
+    assert torch.equal(ga.g_target, gb.g_target) and torch.equal(ga.g_rhs, gb.g_rhs)
+    eligible = shared.eligible.bool()
+    assert torch.equal(g_api[eligible], plan.adjoint(shared.saved, None, None, cot).g_target[eligible])
+
+
+def test_front_end_per_sample_bounds_when_a_bound_row_moves(torch):
+    """``u >= b`` with b a parameter: the bound rows differ per sample, so the
+    front end keeps per-sample bounds, and each sample gets its own bound."""
+    from purin_amd import ChambollePockConfig, Projection, prepare_projection
+
+    p = Projection()
+    t = p.add_parameter(["b"])
+    y = p.add_variable(["u", "v"])
+    p.constraints.add(y.u + y.v == 1, y.u >= t.b)
+    layer = prepare_projection(p, config=ChambollePockConfig(), batch_size=2)
+    assert not layer.shared_bounds
+    out = layer.solve(torch.tensor([[0.0, 0.0], [0.0, 0.0]], dtype=torch.float64, device="cuda"),
+                      torch.tensor([[0.2], [0.8]], dtype=torch.float64, device="cuda"))
+    np.testing.assert_allclose(out.y.cpu().numpy(), [[0.5, 0.5], [0.8, 0.2]], atol=1e-8)
