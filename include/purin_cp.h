@@ -414,6 +414,16 @@ typedef struct {
 
 int purin_cp_last_adjoint_stats(const purin_cp_plan* plan, purin_cp_adjoint_stats* stats);
 
+/* Per-sample Arnoldi steps (summed over restart cycles) of the last GMRES
+ * adjoint call (adjoint / adjoint_values / qp_adjoint) on this plan: the
+ * reference's row_iterations, _batched_restarted_gmres(..., return_iterations=True)
+ * (src/purin/solvers/primal_dual_interior_point/operators.py:1092-1097, 1121-1123).
+ * Copies ``batch`` int32 values (batch must be that call's) into the device
+ * array ``iterations``, stream-ordered on ``stream``.  The values live in the
+ * plan's adjoint workspace until its next adjoint call. */
+int purin_cp_last_adjoint_iterations(const purin_cp_plan* plan, void* stream, int64_t batch,
+                                     int32_t* iterations);
+
 /* Message of the calling thread's last error ("" if none). */
 const char* purin_cp_last_error(void);
 

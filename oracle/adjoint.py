@@ -266,6 +266,7 @@ class AdjointResult(NamedTuple):
     tau: np.ndarray
     sigma: np.ndarray
     g_q: np.ndarray = None
+    iterations: np.ndarray = None  # per-sample Arnoldi steps (operators.py:1092-1097)
 
 
 def adjoint_steps(values, support, mask, n, batch, dtype, cfg):
@@ -304,7 +305,7 @@ def adjoint(values, support, mask, me, y, dual, converged, target, rhs, lower, u
     gd0 = np.zeros_like(dual) if cot_dual is None else np.asarray(cot_dual, dtype)
     g = np.concatenate((np.asarray(cot_y, dtype), gd0, np.zeros_like(y)), axis=1)
     g = np.where(converged[:, None], g, 0).astype(dtype)
-    lam, info, residual, _ = batched_restarted_gmres(
+    lam, info, residual, iterations = batched_restarted_gmres(
         operator, g, tolerance=cfg.gmres_tolerance, absolute_tolerance=cfg.gmres_atol,
         restart=cfg.gmres_restart, max_iterations=cfg.gmres_max_iterations)
     valid = (converged & np.all(np.isfinite(lam), axis=1) & np.isfinite(residual)
@@ -317,4 +318,4 @@ def adjoint(values, support, mask, me, y, dual, converged, target, rhs, lower, u
 
     return AdjointResult(clean(pb.g_values), clean(pb.g_rhs), clean(pb.g_target),
                          clean(pb.g_lower), clean(pb.g_upper), valid, info, residual, lam,
-                         tau, sigma, None if pb.g_q is None else clean(pb.g_q))
+                         tau, sigma, None if pb.g_q is None else clean(pb.g_q), iterations)

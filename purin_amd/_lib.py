@@ -30,6 +30,7 @@ SYMBOLS = (
     "purin_cp_saved_bytes",
     "purin_cp_last_timing",
     "purin_cp_last_adjoint_stats",
+    "purin_cp_last_adjoint_iterations",
     "purin_cp_solve",
     "purin_cp_project",
     "purin_cp_project_noalloc",
@@ -178,6 +179,8 @@ def load(path: str = LIB_PATH):
     lib.purin_cp_last_timing.restype = C.c_int
     lib.purin_cp_last_adjoint_stats.argtypes = [vp, C.POINTER(AdjointStats)]
     lib.purin_cp_last_adjoint_stats.restype = C.c_int
+    lib.purin_cp_last_adjoint_iterations.argtypes = [vp, vp, i64, i32p]
+    lib.purin_cp_last_adjoint_iterations.restype = C.c_int
     lib.purin_cp_default_adjoint_options.argtypes = [C.POINTER(AdjointOptions)]
     lib.purin_cp_default_adjoint_options.restype = None
     lib.purin_cp_adjoint.argtypes = [vp, vp, i64, vp, vp, vp, vp, C.POINTER(AdjointOptions), vp,

@@ -667,6 +667,7 @@ struct Gm {
   T* Q1;   // [restart+1][Bp]: Tm G1, the first projection's coefficients on Z
   T* Cg;   // [restart+1][Bp]: the lagged correction c of the current step
   T* Wc;   // [restart][Bp]: Tm coeff, the cycle's correction on Z
+  int32_t* total;  // [Bp]: Arnoldi steps over all cycles (operators.py:1092-1097)
 };
 
 template <typename T>
@@ -919,6 +920,7 @@ __global__ void k_gm_cycle_end(Gm<T> G, const T* __restrict__ cand_inf) {
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= G.Bp) return;
   if (G.cyc[b]) G.rinf[b] = cand_inf[b];
+  G.total[b] += G.steps[b];  // total_row_iterations + row_steps (0 when inactive)
 }
 
 // info / valid (operators.py:1119-1122, bounds.py:148-153) and the masked
@@ -1346,7 +1348,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                oHu = take((size_t)(restart + 1) * restart * Bp * es),
                oU2 = take((size_t)(restart + 1) * Bp * es), oG1 = take((size_t)(restart + 1) * Bp * es),
                oQ1 = take((size_t)(restart + 1) * Bp * es), oCg = take((size_t)(restart + 1) * Bp * es),
-               oWc = take((size_t)restart * Bp * es);
+               oWc = take((size_t)restart * Bp * es), oTot = take(Bp * 4);
   // per-sample coefficients: the forward's per-sample arrays are rebuilt from
   // values in a region laid out like the forward workspace, plus sigma . w and
   // the coefficient gradient in entry order
@@ -1380,7 +1382,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
           (T*)(ws + oScale), (T*)(ws + oHess), (T*)(ws + oCs), (T*)(ws + oSn), (T*)(ws + oGv),
           (T*)(ws + oCoef), (int32_t*)(ws + oCnt), (int32_t*)(ws + oStepCnt),
           (T*)(ws + oTm), (T*)(ws + oHu), (T*)(ws + oU2), (T*)(ws + oG1), (T*)(ws + oQ1),
-          (T*)(ws + oCg), (T*)(ws + oWc)};
+          (T*)(ws + oCg), (T*)(ws + oWc), (int32_t*)(ws + oTot)};
 
   Adj<T> S{};
   S.K = kept_matrix<T>(p, true);
@@ -1577,6 +1579,8 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                                   dense ? 1 : o.force_eligible, Gr);
   T* lam_w = (T*)(ws + oLw);
   p->adjoint_stats = purin_cp_adjoint_stats{};
+  p->adj_steps = nullptr;  // set by the GMRES path below
+  p->adj_steps_batch = 0;
   if (dense) {
     // BiCGSTAB on (I - J^T) v = g over the whole batch (fixed_point.py:8-40)
     T* bpart = (T*)(ws + oBi);
@@ -1641,6 +1645,9 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   PURIN_HIP(hipFuncSetAttribute((const void*)k_gm_tri<T, 2>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)tri_lds));
   int64_t completed = 0;
+  k_fill<int32_t><<<sb, 256, 0, st>>>(G.total, Bp, 0);
+  p->adj_steps = G.total;  // read by purin_cp_last_adjoint_iterations
+  p->adj_steps_batch = batch;
   while (completed < o.max_iterations) {
     zero_counters();
     k_gm_count_unconverged<T><<<sb, 256, 0, st>>>(G);

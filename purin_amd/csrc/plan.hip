@@ -736,6 +736,18 @@ int purin_cp_last_adjoint_stats(const purin_cp_plan* p, purin_cp_adjoint_stats* 
   return PURIN_CP_OK;
 }
 
+int purin_cp_last_adjoint_iterations(const purin_cp_plan* p, void* stream, int64_t batch,
+                                     int32_t* iterations) {
+  if (!p || !iterations) return set_error(PURIN_CP_ERR_ARG, "NULL argument");
+  if (!p->adj_steps)
+    return set_error(PURIN_CP_ERR_ARG, "no GMRES adjoint call has run on this plan");
+  if (batch != p->adj_steps_batch)
+    return set_error(PURIN_CP_ERR_ARG, "batch differs from the last adjoint call's");
+  PURIN_HIP(hipMemcpyAsync(iterations, p->adj_steps, (size_t)batch * sizeof(int32_t),
+                           hipMemcpyDeviceToDevice, (hipStream_t)stream));
+  return PURIN_CP_OK;
+}
+
 int purin_cp_plan_kept_rows(const purin_cp_plan* p, int64_t* rows, double* scale) {
   if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan");
   for (int64_t i = 0; i < p->m; ++i) {

@@ -100,6 +100,8 @@ struct purin_cp_plan {
   std::vector<void*> owned;   // device allocations freed with the plan
   purin_cp_timing timing{};   // last timed call
   purin_cp_adjoint_stats adjoint_stats{};  // last adjoint call
+  int32_t* adj_steps = nullptr;  // per-sample Arnoldi steps of the last GMRES adjoint (in aws)
+  int64_t adj_steps_batch = 0;
 };
 
 namespace purin {

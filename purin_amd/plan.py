@@ -250,6 +250,13 @@ class Plan:
         _lib.check(self.lib.purin_cp_last_adjoint_stats(self.handle, C.byref(s)))
         return {"arnoldi_steps": int(s.arnoldi_steps), "cycles": int(s.cycles)}
 
+    def last_adjoint_iterations(self, batch):
+        """Per-sample Arnoldi steps of the last GMRES ``adjoint`` call (int32 (B,))."""
+        out = self._empty(int(batch), dtype=torch.int32)
+        _lib.check(self.lib.purin_cp_last_adjoint_iterations(self.handle, _stream(), int(batch),
+                                                             _i32(out)))
+        return out
+
     def project(self, target, rhs, *, multipliers0=None, tolerance=1e-9, max_iterations=10000,
                 early_stop=True, check_every=32, shared_bounds=False, save=False, timing=False,
                 streaming=False, values=None, noalloc=False):
