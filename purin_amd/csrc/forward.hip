@@ -311,8 +311,8 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   R.Kc = Kc;
   R.rowmap = p->res_rowmap;
   R.colmap = p->res_colmap;
-  R.stream = early ? p->res_stream_e : p->res_stream;
-  R.wtab = early ? p->res_wtab_e : p->res_wtab;
+  R.stream = p->res_stream;  // both kernels walk the same chunk streams
+  R.wtab = p->res_wtab;
   R.batch = batch;
   R.tol = tol;
   R.tolv = tolv;

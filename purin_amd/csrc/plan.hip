@@ -469,40 +469,19 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         wtab[4 * w + 2] = (int32_t)cc;
       }
       if (too_wide || nchunks >= (int64_t)1 << 30) p->res_ok = false;
-      // The early-stop kernel's streams: per wavefront the row chunks, the
-      // column chunks, the row chunks again (the residual sweep K y+ of the
-      // stop test) and the wrap chunk, copied from the streams above.
-      std::vector<unsigned char> stream_e;
-      std::vector<int32_t> wtab_e(wtab);
       if (p->res_ok) {
+        // matrix-stream bytes one workgroup reads per iteration: every
+        // wavefront's row and column chunks (the early-stop kernel reads the
+        // same, plus one closing row sweep per launch)
         auto chunks_of = [](int32_t packed) {
           int total = 0;
           for (int k = 0; k < 4; ++k) total += (packed >> (8 * k)) & 255;
           return (int64_t)total;
         };
-        stream_e.reserve(stream.size() * 2);
-        // matrix-stream bytes one workgroup reads per iteration: every
-        // wavefront's row and column chunks (the early-stop kernel walks the
-        // row chunks twice)
-        int64_t fixed_chunks = 0, early_chunks = 0;
-        for (int w = 0; w < 16; ++w) {
-          const int64_t rch = chunks_of(wtab[4 * w + 1]), cch = chunks_of(wtab[4 * w + 2]);
-          fixed_chunks += rch + cch;
-          early_chunks += 2 * rch + cch;
-        }
-        p->res_iter_bytes = fixed_chunks * (int64_t)CB;
-        p->res_iter_bytes_e = early_chunks * (int64_t)CB;
-        for (int w = 0; w < 16; ++w) {
-          const int64_t first = wtab[4 * w], rch = chunks_of(wtab[4 * w + 1]),
-                        cch = chunks_of(wtab[4 * w + 2]);
-          wtab_e[4 * w] = (int32_t)(stream_e.size() / CB);
-          const unsigned char* f = stream.data() + (size_t)first * CB;
-          stream_e.insert(stream_e.end(), f, f + (size_t)(rch + cch) * CB);
-          stream_e.insert(stream_e.end(), f, f + (size_t)rch * CB);
-          const unsigned char* wrap = f + (size_t)(rch + cch) * CB;
-          stream_e.insert(stream_e.end(), wrap, wrap + CB);
-        }
-        if ((int64_t)(stream_e.size() / CB) >= (int64_t)1 << 30) p->res_ok = false;
+        int64_t chunks = 0;
+        for (int w = 0; w < 16; ++w) chunks += chunks_of(wtab[4 * w + 1]) + chunks_of(wtab[4 * w + 2]);
+        p->res_iter_bytes = chunks * (int64_t)CB;
+        p->res_iter_bytes_e = p->res_iter_bytes;
       }
       if (p->res_ok) {
         p->res_stream_bytes = (int64_t)stream.size();
@@ -524,8 +503,6 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         UPR(p->res_colmap, cmap);
         UPR(p->res_stream, stream);
         UPR(p->res_wtab, wtab);
-        UPR(p->res_stream_e, stream_e);
-        UPR(p->res_wtab_e, wtab_e);
 #undef UPR
       }
     }

@@ -86,8 +86,6 @@ struct purin_cp_plan {
   int32_t* res_colmap = nullptr;     // Kc = mc * threads: column of each slot or -1
   unsigned char* res_stream = nullptr;  // per-wavefront chunk streams of the matrix
   int32_t* res_wtab = nullptr;       // [16][4] first chunk and packed chunk counts
-  unsigned char* res_stream_e = nullptr;  // the early-stop kernel's streams (rows, columns, rows)
-  int32_t* res_wtab_e = nullptr;
   int64_t res_stream_bytes = 0;
   int64_t res_iter_bytes = 0;        // matrix-stream bytes a workgroup reads per iteration
   int64_t res_iter_bytes_e = 0;      // the same for the early-stop kernel

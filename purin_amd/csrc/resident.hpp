@@ -342,29 +342,40 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 // independently: a sample accepted at iteration k keeps the state of
 // iteration k (its later updates are masked and not counted), and the
 // workgroup returns when all its samples are accepted or the iterations run
-// out.  Per iteration:
-//   row pass      as above, masked to the active samples
+// out.  It walks the fixed kernel's chunk streams, two sweeps per iteration,
+// with Gy holding the iterate y itself (not ybar):
+//   row update    commit d+ where the sample is active: the candidate
+//                   P(d + sigma (K ybar - r)) formed by the previous residual
+//                   sweep, with K ybar = (1 + theta) K y - theta K y_prev
+//                   (ybar = y + theta (y - y_prev), kernels.py:149; the first
+//                   iteration's ybar is y): no gathers, no global loads
 //   barrier
-//   column pass   as above, masked; Gy <- y+ (for the residual sweep); column
-//                 diagnostics of (y+, K^T d+), their sums to LDS:
-//                 primal, dual objective terms, max(stationarity, bound
-//                 violation), finiteness (kernels.py:153-175, 272-274)
+//   column pass   gathers Gd: y+ where active, Gy <- y+; the column
+//                   diagnostics (primal and dual objective terms,
+//                   stationarity and bound violation, kernels.py:153-175,
+//                   272-274): the primal sum over 16-lane rows by DPP to
+//                   LDS, the others kept per thread
 //   barrier
-//   residual      the row chunks again, gathering y+: max |K y+ - r| (eq) /
-//                 max(K y+ - r, 0) (ineq), r . d+, finiteness of d+; every
-//                 partial is summed within 16-lane rows by DPP and written to LDS
+//   residual      gathers Gy = y+: K y+, max |K y+ - r| (eq) /
+//                   max(K y+ - r, 0) (ineq) and r . d+ (kernels.py:158-166)
+//                   folded into the thread's dual terms and maxima, summed
+//                   over 16-lane rows by DPP, to LDS; the next iteration's
+//                   candidate duals
 //   barrier
-//   Gy <- ybar+ (from y+ and the old y); wavefront k combines the 64 row
-//                 partials of (sample, quantity) k in a fixed order
+//   decision      wavefront s combines sample s's 64 partials of each total
+//                   in one fixed order and applies the stop test
+//                   (kernels.py:167-175, 260-278); the verdicts go through LDS
 //   barrier
-//   every wavefront applies the stop test of each sample to the totals
-// The step arithmetic is the fixed kernel's (and the streaming passes'), so
-// the iterates of a sample are identical up to its stop; the diagnostics are
-// summed in another (fixed) order than the streaming stop test's.
-// LDS: the fixed kernel's, then [16 waves][4 rows][kResQ] partials and the
-// [BT][kResQ] totals.
-constexpr int kResQ = 5;  // primal, dual terms, r.d, max(res, bound, stat), finite
-constexpr uint32_t kResEarlyExtra = 16u * 4u * kResQ * 16u + 128u;
+// The residual is exact; K ybar comes from the linear relation above, so the
+// iterates differ from the fixed kernel's (which gathers ybar) by rounding.
+// A non-finite y+ or d+ makes the primal or the dual sum non-finite, so the
+// gap is not finite and the sample is not accepted (the finiteness flag of
+// kernels.py:172).  On lanes whose bounds are not NaN, y+ lies in [lo, hi]
+// (bound violation 0) and the stationarity clip equals the dual term's.
+// LDS: the fixed kernel's, then the partials [16 waves][4 rows][kResQ] and
+// the BT verdicts.
+constexpr int kResQ = 3;  // primal; dual objective (terms - r.d); max(stationarity, residual)
+constexpr uint32_t kResEarlyExtra = 16u * 4u * kResQ * 16u + 16u;
 
 // One DPP move of a 32- or 64-bit value (all lanes active, full row/bank masks).
 template <int CTRL, typename T>
@@ -380,6 +391,13 @@ __device__ __forceinline__ T dpp_move(T v) {
                                                              0xF, false));
   }
 }
+
+// max that ignores a NaN operand (v_max_f64 / v_max_f32): for maxima whose
+// NaN cases the caller has already turned into an infinity or a non-finite sum
+struct OpFMax {
+  template <typename T>
+  __device__ T operator()(T a, T b) const { return __builtin_fmax(a, b); }
+};
 
 // Combine the 16 lanes of each DPP row; lane 0 of the row holds
 // ((q0 op q3) op (q2 op q1)) of its four quads q (each quad combined pairwise).
@@ -416,11 +434,11 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const int64_t tile = blockIdx.x;
   const uint32_t lane16 = (uint32_t)lane * 16u;
   const V vzero = V(T(0));
-  const T zero = T(0), half = T(0.5);
+  const T zero = T(0), half = T(0.5), inf = T(__builtin_inf());
   const uint32_t gd_off = (uint32_t)(A.n + 1) * 16u;
   const uint32_t trash_off = (uint32_t)(A.n + 1 + A.m) * 16u;
   const uint32_t red_off = trash_off + 16u;
-  const uint32_t tot_off = red_off + 16u * 4u * kResQ * 16u;  // [BT][kResQ] totals
+  const uint32_t dec_off = red_off + 16u * 4u * kResQ * 16u;  // [BT] verdicts
 
   const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave]);
   const uint32_t rcnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave + 1]);
@@ -429,12 +447,12 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)A.Kr;
   const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)A.Kr;
 
-  // registers: y of the thread's columns; the targets and the scaled
-  // right-hand sides are re-read each iteration (L2) to leave room for the
-  // diagnostics.  ybar+ is formed after the residual sweep from y+ (the
-  // thread's own Gy entry, which the sweep gathers) and the old y.
+  // registers: per row slot K y of the current iterate and the candidate
+  // dual of the next row update.  y lives in Gy (each thread reads its own
+  // entries); the targets and the scaled right-hand sides are re-read each
+  // iteration (L2), ahead of the gathers that hide their latency.
   uint32_t soff_r[SLR], soff_c[SLC];
-  V y[SLC];
+  V ky[SLR], dn[SLR];
   uint32_t ineq = 0, nanb = 0, rvalid = 0, cvalid = 0;
 #pragma unroll
   for (int c = 0; c < SLC; ++c) {
@@ -446,8 +464,9 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     }
     if (j >= 0) cvalid |= 1u << c;
     soff_c[c] = j >= 0 ? (uint32_t)j * 16u : trash_off;
-    y[c] = j >= 0 ? reinterpret_cast<const V*>(A.Ts)[tile * (int64_t)A.Kc + c * NT + t] : vzero;
-    lds_write<V>(soff_c[c], y[c]);  // y0 = ybar0 = yhat (kernels.py:229-231)
+    // y0 = ybar0 = yhat (kernels.py:229-231)
+    lds_write<V>(soff_c[c],
+                 j >= 0 ? reinterpret_cast<const V*>(A.Ts)[tile * (int64_t)A.Kc + c * NT + t] : vzero);
   }
 #pragma unroll
   for (int r = 0; r < SLR; ++r) {
@@ -467,43 +486,52 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   int32_t cnt[BT];
 #pragma unroll
   for (int s = 0; s < BT; ++s) cnt[s] = 0;
+  const uint32_t red_at = red_off + (uint32_t)((wave * 4 + (lane >> 4)) * kResQ) * 16u;
+  const bool red_lead = (lane & 15) == 0;
   __syncthreads();
 
   constexpr uint32_t CB = res_chunk_bytes<T>();
   Chunk<T> b0, b1;
   load_chunk(b0, A.stream, (uint64_t)first * CB, lane16);
-
-  for (int64_t it = 0; it < A.iters && act != 0u; ++it) {
-    const __attribute__((address_space(4))) T* sc =
-        (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
-    const T sigma = sc[0], a = sc[1], delta = sc[2], theta = sc[3];
-    uint32_t pos = first + 1;
-    // the slot-ordered rhs (zero on empty slots) through an opaque base, so the
-    // loads stay inside the loop
-    typedef const __attribute__((address_space(1))) V* GV;
-    GV rb = (GV)Rs;
-    asm volatile("" : "+s"(rb));
-    // ---- row pass, masked ------------------------------------------------------
+  uint32_t pos = first + 1;
+  typedef const __attribute__((address_space(1))) V* GV;
+  // K y0 (= K ybar0) by one row sweep, and the first candidate duals; b0 then
+  // holds the first column chunk
+  {
+    const T sigma0 = A.sched[0];
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
       const int nch = (int)((rcnt >> (8 * r)) & 255u);
-      const V rr = rb[r * NT + t];
-      const V dold = lds_read<V>(soff_r[r]);
-      const V acc = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
-      V p = dold + sigma * (acc - rr);
+      const V rr = Rs[r * NT + t];
+      ky[r] = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      V p = lds_read<V>(soff_r[r]) + sigma0 * (ky[r] - rr);
       if (ineq & (1u << r)) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
       }
+      dn[r] = p;
+    }
+  }
+
+  for (int64_t it = 0; it < A.iters && act != 0u; ++it) {
+    const __attribute__((address_space(4))) T* sc =
+        (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
+    const T a = sc[1], delta = sc[2], theta = sc[3];
+    // ---- row update: commit the candidate duals where the sample is active ----------
 #pragma unroll
-      for (int s = 0; s < BT; ++s)
-        if (!(act & (1u << s))) p[s] = dold[s];
+    for (int r = 0; r < SLR; ++r) {
+      V p = dn[r];
+      if (act != (1u << BT) - 1u) {
+        const V dold = lds_read<V>(soff_r[r]);
+#pragma unroll
+        for (int s = 0; s < BT; ++s)
+          if (!(act & (1u << s))) p[s] = dold[s];
+      }
       lds_write<V>(soff_r[r], p);
     }
     __syncthreads();
-    // ---- column pass, masked, with the column diagnostics --------------------------
-    V qp = vzero, qd = vzero, qm = vzero;
-    uint32_t bad = 0;  // bit s: a non-finite y+ or d+ of sample s
+    // ---- column pass, masked, with the column diagnostics ------------------------------
+    V qp = vzero, qd = vzero, qc = vzero;
 #pragma unroll
     for (int c = 0; c < SLC; ++c) {
       const int nch = (int)((ccnt >> (8 * c)) & 255u);
@@ -511,20 +539,22 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       GP lb = (GP)A.Ls;
       GP hb = (GP)A.Hs;
       GP tb = (GP)A.Ts;
+      // the target (per tile, beyond L2) ahead of the gathers that hide its
+      // latency; the bounds after them (register pressure)
+      asm volatile("" : "+s"(tb));
+      const V tg = ((GV)tb)[tile * (int64_t)A.Kc + c * NT + t];
+      const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
       if (SB) {
-        asm volatile("" : "+s"(lb), "+s"(hb), "+s"(tb));
         lo = V(lb[c * NT + t]);
         hi = V(hb[c * NT + t]);
-      }
-      const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
-      if (!SB) {  // per-sample bounds after the gathers (register pressure)
-        asm volatile("" : "+s"(lb), "+s"(hb), "+s"(tb));
+      } else {
         lo = ((GV)lb)[tile * (int64_t)A.Kc + c * NT + t];
         hi = ((GV)hb)[tile * (int64_t)A.Kc + c * NT + t];
       }
-      const V tg = ((GV)tb)[tile * (int64_t)A.Kc + c * NT + t];
-      const V sv = a * y[c] - delta * tt + delta * tg;
+      const V yo = lds_read<V>(soff_c[c]);
+      const V sv = a * yo - delta * tt + delta * tg;
       V yn;
       if (nanb & (1u << c)) {
 #pragma unroll
@@ -533,41 +563,61 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) yn[s] = clip_nonnan_bounds(sv[s], lo[s], hi[s]);
       }
+      if (act != (1u << BT) - 1u) {
 #pragma unroll
-      for (int s = 0; s < BT; ++s)
-        if (!(act & (1u << s))) yn[s] = y[c][s];  // a frozen sample keeps its state
+        for (int s = 0; s < BT; ++s)
+          if (!(act & (1u << s))) yn[s] = yo[s];  // a frozen sample keeps its state
+      }
       if (cvalid & (1u << c)) {  // diagnostics with q = 1, c = -yhat (kernels.py:158-174, 272-274)
-        // the clip of non-NaN bounds is the two-compare form (clipp's result)
-        const bool fast = !(nanb & (1u << c));
+        if (!(nanb & (1u << c))) {
+          // Bounds without NaN (the usual lane): y+ is a clip to [lo, hi], so
+          // its bound violation is 0; y - (y + c + K^T d) = -c - K^T d, so the
+          // stationarity clip is the dual term's clip m.  A non-finite y+
+          // makes the primal sum non-finite, which the stop test rejects
+          // through the gap (kernels.py:172's finiteness).
 #pragma unroll
-        for (int s = 0; s < BT; ++s) {
-          const T yv = yn[s], cq = -tg[s];
-          qp[s] += half * yv * yv + cq * yv;
-          const T tf = cq + tt[s];
-          const T mz = fast ? clip_nonnan_bounds(-tf, lo[s], hi[s]) : clipp(-tf, lo[s], hi[s]);
-          qd[s] += half * mz * mz + tf * mz;
-          const T xs = yv - ((yv + cq) + tt[s]);
-          const T g = yv - (fast ? clip_nonnan_bounds(xs, lo[s], hi[s]) : clipp(xs, lo[s], hi[s]));
-          qm[s] = maxp(qm[s], absv(g));
-          qm[s] = maxp(qm[s], maxp(maxp(lo[s] - yv, zero), maxp(yv - hi[s], zero)));
-          if (!finite(yv)) bad |= 1u << s;
+          for (int s = 0; s < BT; ++s) {
+            const T yv = yn[s], cq = -tg[s];
+            qp[s] += half * yv * yv + cq * yv;
+            const T tf = cq + tt[s];
+            const T mz = __builtin_fmin(__builtin_fmax(-tf, lo[s]), hi[s]);
+            qd[s] += half * mz * mz + tf * mz;
+            qc[s] = __builtin_fmax(qc[s], absv(yv - mz));
+          }
+        } else {  // a NaN bound on this lane: the reference's expressions, NaN-propagating
+#pragma unroll
+          for (int s = 0; s < BT; ++s) {
+            const T yv = yn[s], cq = -tg[s];
+            qp[s] += half * yv * yv + cq * yv;
+            const T tf = cq + tt[s];
+            const T mz = clipp(-tf, lo[s], hi[s]);
+            qd[s] += half * mz * mz + tf * mz;
+            const T xs = yv - ((yv + cq) + tt[s]);
+            T g = maxp(absv(yv - clipp(xs, lo[s], hi[s])),
+                       maxp(maxp(lo[s] - yv, zero), maxp(yv - hi[s], zero)));
+            if (!finite(g)) g = inf;
+            qc[s] = __builtin_fmax(qc[s], g);
+          }
         }
       }
-      lds_write<V>(soff_c[c], yn);  // y+ for the residual sweep; y[c] keeps the old y
+      lds_write<V>(soff_c[c], yn);  // Gy <- y+
     }
-    // the column sums' 16-lane row partials go to LDS now ([wave][row][q]), so
-    // they are not held through the sweep
-    const uint32_t red_at = red_off + (uint32_t)((wave * 4 + (lane >> 4)) * kResQ) * 16u;
-    const bool red_lead = (lane & 15) == 0;
 #pragma unroll
     for (int s = 0; s < BT; ++s) qp[s] = row16_combine(qp[s], OpAdd());
     if (red_lead) lds_write<V>(red_at, qp);
-#pragma unroll
-    for (int s = 0; s < BT; ++s) qd[s] = row16_combine(qd[s], OpAdd());
-    if (red_lead) lds_write<V>(red_at + 16u, qd);
+    // qd and qc stay in registers: the sweep folds its own terms into them
     __syncthreads();
-    // ---- residual sweep (reads Gy = y+ and the thread's own Gd) ------------------
-    V qr = vzero;
+    // ---- residual sweep (gathers Gy = y+; own Gd entries = d+) ---------------------
+    pos = first + 1;  // b0 holds the copy of the stream's first (row) chunk
+    // the next iteration's sigma (the candidates are formed only when it runs)
+    const bool more = it + 1 < A.iters;
+    const T sigma_n = more ? A.sched[4 * (it + 1)] : zero;
+    // the slot-ordered rhs (zero on empty slots) through an opaque base, so the
+    // loads stay inside the loop
+    GV rb = (GV)Rs;
+    asm volatile("" : "+s"(rb));
+    const T tp1 = T(1) + theta;
+    V qr = qd, qm = qc;  // the thread's dual terms and maxima of both passes
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
       const int nch = (int)((rcnt >> (8 * r)) & 255u);
@@ -575,91 +625,85 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       const V acc = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
       const V d = lds_read<V>(soff_r[r]);
       if (rvalid & (1u << r)) {  // kernels.py:158-166
+        // e = K y+ - r; equality rows |e|, inequality rows max(e, 0): max(e, w e)
+        // with w = -1 / 0.  d * 0 is NaN for a non-finite d: it makes the
+        // dual sum, and so the gap, non-finite (kernels.py:172's finiteness).
+        const T w = (ineq & (1u << r)) ? zero : T(-1);
 #pragma unroll
         for (int s = 0; s < BT; ++s) {
           const T e = acc[s] - rr[s];
-          qm[s] = maxp(qm[s], (ineq & (1u << r)) ? maxp(e, zero) : absv(e));
-          qr[s] += rr[s] * d[s];
-          if (!finite(d[s])) bad |= 1u << s;
+          qm[s] = __builtin_fmax(qm[s], __builtin_fmax(e, w * e));
+          qr[s] = (qr[s] - rr[s] * d[s]) - d[s] * zero;
         }
       }
-    }
-    // the sweep's 16-lane row partials to LDS; finiteness by wavefront vote
-    {
-      V f;
+      if (more) {  // d+ of the next iteration from K ybar = (1 + theta) K y+ - theta K y
+        V p = d + sigma_n * ((tp1 * acc - theta * ky[r]) - rr);
+        if (ineq & (1u << r)) {
 #pragma unroll
-      for (int s = 0; s < BT; ++s) f[s] = __ballot((bad >> s) & 1u) ? zero : T(1);
-#pragma unroll
-      for (int s = 0; s < BT; ++s) qr[s] = row16_combine(qr[s], OpAdd());
-      if (red_lead) lds_write<V>(red_at + 32u, qr);
-#pragma unroll
-      for (int s = 0; s < BT; ++s) qm[s] = row16_combine(qm[s], OpMax());
-      if (red_lead) {
-        lds_write<V>(red_at + 48u, qm);
-        lds_write<V>(red_at + 64u, f);
+          for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
+        }
+        dn[r] = p;
       }
+      ky[r] = acc;
     }
+#pragma unroll
+    for (int s = 0; s < BT; ++s) qr[s] = row16_combine(qr[s], OpAdd());
+    if (red_lead) lds_write<V>(red_at + 16u, qr);
+#pragma unroll
+    for (int s = 0; s < BT; ++s) qm[s] = row16_combine(qm[s], OpFMax());
+    if (red_lead) lds_write<V>(red_at + 32u, qm);
     __syncthreads();
-    // ---- ybar+ = y+ + theta (y+ - y) into Gy (kernels.py:149; a frozen sample has
-    // y+ = y, so its Gy entry, which no output reads, becomes y); the stop test --
-#pragma unroll
-    for (int c = 0; c < SLC; ++c) {
-      const V yn = lds_read<V>(soff_c[c]);
-      lds_write<V>(soff_c[c], yn + theta * (yn - y[c]));
-      y[c] = yn;
-    }
-#pragma unroll
-    for (int s = 0; s < BT; ++s)
-      if (act & (1u << s)) ++cnt[s];
-    // the (sample, quantity) totals, one per wavefront (BT * kResQ of them): lane
-    // l holds partial (wave l / 4, row l % 4), combined within DPP rows, then
-    // the 4 rows in order
-    for (int k = wave; k < BT * kResQ; k += kResWaves) {
-      const int s = k / kResQ, q = k - s * kResQ;
-      const V pv = lds_read<V>(red_off + (uint32_t)(lane * kResQ + q) * 16u);
-      T x = pv[0];
+    // ---- the stop test of sample s, on wavefront s: lane l combines partial l
+    // (wave l/4, DPP row l%4) in one fixed order; the verdicts go through LDS
+    if (wave < BT) {
+      const uint32_t pl = red_off + (uint32_t)(lane * kResQ) * 16u;
+      const V pp = lds_read<V>(pl), pd = lds_read<V>(pl + 16u), pm = lds_read<V>(pl + 32u);
+      T vp = pp[0], vd = pd[0], vm = pm[0];
 #pragma unroll
       for (int u = 1; u < BT; ++u)
-        if (s == u) x = pv[u];
-      if (q < 3) x = row16_combine(x, OpAdd());
-      else if (q == 3) x = row16_combine(x, OpMax());
-      else x = row16_combine(x, OpMin());
-      const T r0 = read_lane(x, 0), r1 = read_lane(x, 16), r2 = read_lane(x, 32),
-              r3 = read_lane(x, 48);
-      T tot;
-      if (q < 3) tot = ((r0 + r1) + r2) + r3;
-      else if (q == 3) tot = maxp(maxp(maxp(r0, r1), r2), r3);
-      else tot = minp(minp(minp(r0, r1), r2), r3);
-      if (lane == 0) lds_write<T>(tot_off + (uint32_t)(k * sizeof(T)), tot);
+        if (wave == u) {
+          vp = pp[u];
+          vd = pd[u];
+          vm = pm[u];
+        }
+      const T xp = row16_combine(vp, OpAdd());
+      const T xd = row16_combine(vd, OpAdd());
+      const T xm = row16_combine(vm, OpFMax());
+      const T primal =
+          ((read_lane(xp, 0) + read_lane(xp, 16)) + read_lane(xp, 32)) + read_lane(xp, 48);
+      const T dual_obj =
+          ((read_lane(xd, 0) + read_lane(xd, 16)) + read_lane(xd, 32)) + read_lane(xd, 48);
+      const T mx = __builtin_fmax(
+          __builtin_fmax(__builtin_fmax(read_lane(xm, 0), read_lane(xm, 16)), read_lane(xm, 32)),
+          read_lane(xm, 48));
+      const int64_t b = bs0 + wave;
+      const T tol = A.tolv ? (b < A.batch ? A.tolv[b] : T(0)) : A.tol;
+      const T gap = maxp(primal - dual_obj, zero) / maxp(T(1), maxp(absv(primal), absv(dual_obj)));
+      const bool ok = finite(gap) && mx <= tol && gap <= tol;
+      if (lane == 0) lds_write<uint32_t>(dec_off + 4u * (uint32_t)wave, ok ? 1u : 0u);
     }
     __syncthreads();
-    // every wavefront applies the stop test to the same totals (the same
-    // decision everywhere; kernels.py:167-175, 260-278)
     {
       uint32_t accept = 0;
 #pragma unroll
       for (int s = 0; s < BT; ++s) {
-        T tot[kResQ];
-#pragma unroll
-        for (int q = 0; q < kResQ; ++q)
-          tot[q] = lds_read<T>(tot_off + (uint32_t)((s * kResQ + q) * sizeof(T)));
-        const T tol = A.tolv ? (bs0 + s < A.batch ? A.tolv[bs0 + s] : T(0)) : A.tol;
-        const T primal = tot[0], dual_obj = tot[1] - tot[2];
-        const T gap = maxp(primal - dual_obj, zero) /
-                      maxp(T(1), maxp(absv(primal), absv(dual_obj)));
-        const bool ok = tot[4] != zero && finite(gap) && tot[3] <= tol && gap <= tol;
-        if (ok && (act & (1u << s))) accept |= 1u << s;
+        if (lds_read<uint32_t>(dec_off + 4u * (uint32_t)s) && (act & (1u << s))) accept |= 1u << s;
+        if (act & (1u << s)) ++cnt[s];  // this iteration ran for the sample
       }
       act = (uint32_t)__builtin_amdgcn_readfirstlane((int)(act & ~accept));
     }
+    // b0 holds the first column chunk again and pos follows it; the partials
+    // are rewritten only after the next barrier
   }
   // ---- hand the state to the batch-minor layout ---------------------------------
 #pragma unroll
   for (int c = 0; c < SLC; ++c) {
     const int j = A.colmap[c * NT + t];
-    if (j >= 0)
+    if (j >= 0) {
+      const V yv = lds_read<V>(soff_c[c]);
 #pragma unroll
-      for (int s = 0; s < BT; ++s) A.Y[(int64_t)j * A.Bp + bs0 + s] = y[c][s];
+      for (int s = 0; s < BT; ++s) A.Y[(int64_t)j * A.Bp + bs0 + s] = yv[s];
+    }
   }
 #pragma unroll
   for (int r = 0; r < SLR; ++r) {

