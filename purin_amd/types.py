@@ -7,25 +7,26 @@ from typing import Any, NamedTuple
 
 
 class ProjectionMethod(str, Enum):
-    """Projection backends; this build implements Chambolle--Pock only."""
+    """Which projection solver to run; only Chambolle--Pock exists in this build."""
 
     CHAMBOLLE_POCK = "chambolle-pock"
 
     @classmethod
     def normalize(cls, value):
+        """Accept a member or its name in any case/padding; raise ValueError otherwise
+        (the reference raises for unknown names too, types.py:22-33)."""
         if isinstance(value, cls):
             return value
-        try:
-            return cls(str(value).strip().lower())
-        except ValueError as error:
-            supported = ", ".join(item.value for item in cls)
-            raise ValueError(
-                f"Unknown projection method {value!r}. Supported methods: {supported}."
-            ) from error
+        key = str(value).strip().lower()
+        for member in cls:
+            if member.value == key:
+                return member
+        names = ", ".join(m.value for m in cls)
+        raise ValueError(f"Unknown projection method {value!r}; this build supports: {names}.")
 
 
 class SolveStatus(IntEnum):
-    """Backend-neutral solver termination status."""
+    """Why a solve stopped; the integer codes are part of the result interface."""
 
     CONVERGED = 0
     MAX_ITERATIONS = 1
@@ -35,7 +36,7 @@ class SolveStatus(IntEnum):
 
 
 class ProjectionResult(NamedTuple):
-    """Complete fixed-shape projection result."""
+    """Every output of one batched projection, each with a fixed shape."""
 
     y: Any
     multipliers_eq: Any
@@ -49,7 +50,7 @@ class ProjectionResult(NamedTuple):
 
 
 class ProjectionInfo(NamedTuple):
-    """Lightweight diagnostics returned by ``with_info``."""
+    """Per-sample forward diagnostics that ``with_info`` returns beside y."""
 
     forward_status_codes: Any
     forward_iterations: Any
@@ -63,7 +64,7 @@ class ProjectionInfo(NamedTuple):
 
 
 class ProjectionTrainingOutput(NamedTuple):
-    """Projected primal/latent-dual state used by the training frontend."""
+    """The training front end's output: the projected point, its multipliers and forward diagnostics."""
 
     y_tilde: Any
     multipliers_eq: Any
