@@ -53,6 +53,22 @@ template <typename T>
 __device__ __forceinline__ void vstore(T* p, typename Lane<T>::V v) {
   *reinterpret_cast<typename Lane<T>::V*>(p) = v;
 }
+// Store of a value not read again by this kernel: nontemporal, like vload_once.
+template <typename T>
+__device__ __forceinline__ void vstore_once(T* p, typename Lane<T>::V v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<typename Lane<T>::V*>(p));
+}
+// A load or store of a streamed vector: nontemporal when NT.
+template <bool NT, typename T>
+__device__ __forceinline__ typename Lane<T>::V vload_s(const T* p) {
+  if constexpr (NT) return vload_once(p);
+  else return vload(p);
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void vstore_s(T* p, typename Lane<T>::V v) {
+  if constexpr (NT) vstore_once(p, v);
+  else vstore(p, v);
+}
 template <typename T>
 __device__ __forceinline__ typename Lane<T>::V vsplat(T x) {
   typename Lane<T>::V v;

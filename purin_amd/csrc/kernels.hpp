@@ -196,7 +196,10 @@ __global__ __launch_bounds__(kBlock) void k_row_pass(Iter<T> A) {
 // column pass.  MODE 0: fixed-iteration update; 1: masked update + diagnostic
 // partials of (y+, d+); 2: no update, diagnostics of the current (y, d).
 // ---------------------------------------------------------------------------
-template <typename T, int MODE, int CPW>
+// NT: the per-column streams (y, yhat or q and c, per-sample bounds, and the
+// stores of y and ybar) are nontemporal, for problems whose per-iteration
+// vectors exceed the caches: the gathered rows of d+ then keep L2 and MALL.
+template <typename T, int MODE, int CPW, bool NT = false>
 __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
   if (MODE != 2 && A.stop && *A.stop >= A.nstop) return;
   using V = typename Lane<T>::V;
@@ -231,21 +234,21 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
         t += col_coef(A.K, k, b0) * dd;
       }
       const size_t off = (size_t)j * A.Bp + b0;
-      const V y = vload(A.Y + off);
+      const V y = vload_s<NT>(A.Y + off);
       V tg, qv, cv;  // projection: yhat; general QP: q and c
       if (A.Q) {
-        qv = vload(A.Q + off);
-        cv = vload(A.Cc + off);
+        qv = vload_s<NT>(A.Q + off);
+        cv = vload_s<NT>(A.Cc + off);
       } else {
-        tg = vload(A.tgt + off);
+        tg = vload_s<NT>(A.tgt + off);
       }
       V lo, hi;
       if (A.shared_bounds) {
         lo = vsplat<T>(A.LO[j]);
         hi = vsplat<T>(A.HI[j]);
       } else {
-        lo = vload(A.LO + off);
-        hi = vload(A.HI + off);
+        lo = vload_s<NT>(A.LO + off);
+        hi = vload_s<NT>(A.HI + off);
       }
       V yn;
       if (MODE == 2) {
@@ -283,8 +286,8 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
             }
           }
         }
-        vstore(A.Y + off, yn);
-        vstore(A.YB + off, yb);
+        vstore_s<NT>(A.Y + off, yn);
+        vstore_s<NT>(A.YB + off, yb);
       }
       if (MODE != 0 && A.Q) {
         // diagnostics (kernels.py:158-174, 272-274) with general q, c

@@ -204,3 +204,36 @@ def test_full_size_adjoint_at_the_same_state():
     assert len(np.unique(want6.iterations)) > 1
     np.testing.assert_array_equal(steps6[sub], want6.iterations)
     np.testing.assert_array_equal(to_np(adj6.info)[sub], want6.info)
+
+
+def test_full_size_default_stopping_rule_matches_oracle_fixture():
+    """config5's forward: config2 under the reference's default stopping rule
+    (tolerance 1e-9, at most 10000 accelerated iterations, early stop;
+    kernels.py:228-305).  The oracle leaves samples 0, 511 and 1023 at the
+    iteration limit (tests/golden/config2_converged.npz, written by
+    tests/golden/make_config2_converged.py); the GPU, on the whole batch, must
+    agree on their status, iteration count, residual and iterate.  No sample of
+    the batch converges, so none is gradient-eligible (bounds.py:148-153): the
+    config5 VJP at this forward is zero by the reference's own rule."""
+    require_gpu()
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                        "config2_converged.npz")
+    with np.load(path, allow_pickle=False) as f:
+        g = {k: f[k] for k in f.files}
+    w = workloads.config2()
+    B = w.target.shape[0]
+    p, _, _ = full_plan(w)
+    rhs = np.tile(w.rhs, (B, 1))
+    out = p.project(w.target, rhs, max_iterations=10000, early_stop=True, tolerance=1e-9,
+                    shared_bounds=True, save=True)
+    s = g["samples"]
+    status, iters = to_np(out.status), to_np(out.iterations)
+    np.testing.assert_array_equal(status[s], g["status"])
+    np.testing.assert_array_equal(iters[s], g["iterations"])
+    assert rel_err(to_np(out.y)[s], g["y"]) <= 1e-10
+    # the residual is a small difference (~1e-8): relative agreement to 1e-3
+    res = to_np(out.residual)[s]
+    assert np.all(np.abs(res - g["residual"]) <= 1e-3 * np.abs(g["residual"]))
+    assert np.all(status == 1) and int(to_np(out.eligible).sum()) == 0
