@@ -311,6 +311,8 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   R.Kc = Kc;
   R.rowmap = p->res_rowmap;
   R.colmap = p->res_colmap;
+  R.rowent = p->res_rowent;
+  R.colent = p->res_colent;
   R.stream = p->res_stream;  // both kernels walk the same chunk streams
   R.wtab = p->res_wtab;
   R.batch = batch;

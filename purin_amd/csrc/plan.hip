@@ -170,6 +170,118 @@ struct HostMatrix {
   std::vector<T> cval_s, cval_o;
 };
 
+// LDS placement of the resident kernels' vectors.  A ds_read_b128 or
+// ds_write_b128 serves 16 consecutive lanes at a time and is free of bank
+// conflicts when their 16-byte entries differ mod 16 (lanes on one entry are a
+// broadcast).  Each gather step of the row pass reads, per quarter wavefront,
+// the entries of 16 columns; a step of the column pass those of 16 rows; a
+// quarter's own-entry reads and writes touch its 16 rows or columns.  Those
+// sets are the groups (gptr/gmem: distinct entities per group; entities are
+// columns [0, n), the zero entry n, rows n + 1 + [0, m)).  The entries of the
+// columns and of the rows are permuted among themselves (so every entry class
+// keeps its size and the LDS image its length) by a greedy swap search that
+// lowers the number of same-class pairs summed over the groups; ent[e] is
+// entity e's entry.  The search is deterministic (fixed seed) and bounded.
+static void lds_placement(int64_t n, int64_t m, const std::vector<int32_t>& gptr,
+                          const std::vector<int32_t>& gmem, std::vector<int32_t>& ent) {
+  const int64_t E = n + 1 + m;
+  const int64_t G = (int64_t)gptr.size() - 1;
+  ent.resize(E);
+  for (int64_t e = 0; e < E; ++e) ent[e] = (int32_t)e;
+  if (G <= 0) return;
+  std::vector<int32_t> eptr(E + 1, 0), egrp(gmem.size());
+  for (int32_t e : gmem) eptr[e + 1]++;
+  for (int64_t e = 0; e < E; ++e) eptr[e + 1] += eptr[e];
+  {
+    std::vector<int32_t> fill(eptr.begin(), eptr.end() - 1);
+    for (int64_t g = 0; g < G; ++g)
+      for (int32_t k = gptr[g]; k < gptr[g + 1]; ++k) egrp[fill[gmem[k]]++] = (int32_t)g;
+  }
+  std::vector<uint16_t> cnt((size_t)G * 16, 0);
+  for (int64_t g = 0; g < G; ++g)
+    for (int32_t k = gptr[g]; k < gptr[g + 1]; ++k) cnt[(size_t)g * 16 + (ent[gmem[k]] & 15)]++;
+  auto in_group = [&](int32_t g, int32_t e) {
+    for (int32_t k = gptr[g]; k < gptr[g + 1]; ++k)
+      if (gmem[k] == e) return true;
+    return false;
+  };
+  auto conflicted = [&](int32_t a) {
+    const int ca = ent[a] & 15;
+    for (int32_t k = eptr[a]; k < eptr[a + 1]; ++k)
+      if (cnt[(size_t)egrp[k] * 16 + ca] > 1) return true;
+    return false;
+  };
+  // change of the pair count when a and b exchange entries
+  auto delta = [&](int32_t a, int32_t b) {
+    const int ca = ent[a] & 15, cb = ent[b] & 15;
+    int d = 0;
+    for (int32_t k = eptr[a]; k < eptr[a + 1]; ++k) {
+      const int32_t g = egrp[k];
+      if (!in_group(g, b)) d += (int)cnt[(size_t)g * 16 + cb] - ((int)cnt[(size_t)g * 16 + ca] - 1);
+    }
+    for (int32_t k = eptr[b]; k < eptr[b + 1]; ++k) {
+      const int32_t g = egrp[k];
+      if (!in_group(g, a)) d += (int)cnt[(size_t)g * 16 + ca] - ((int)cnt[(size_t)g * 16 + cb] - 1);
+    }
+    return d;
+  };
+  auto swap_entries = [&](int32_t a, int32_t b) {
+    const int ca = ent[a] & 15, cb = ent[b] & 15;
+    for (int32_t k = eptr[a]; k < eptr[a + 1]; ++k) {
+      const int32_t g = egrp[k];
+      if (in_group(g, b)) continue;
+      cnt[(size_t)g * 16 + ca]--;
+      cnt[(size_t)g * 16 + cb]++;
+    }
+    for (int32_t k = eptr[b]; k < eptr[b + 1]; ++k) {
+      const int32_t g = egrp[k];
+      if (in_group(g, a)) continue;
+      cnt[(size_t)g * 16 + cb]--;
+      cnt[(size_t)g * 16 + ca]++;
+    }
+    std::swap(ent[a], ent[b]);
+  };
+  uint64_t rng = 0x9E3779B97F4A7C15ull;
+  auto next = [&]() {
+    rng ^= rng << 13;
+    rng ^= rng >> 7;
+    rng ^= rng << 17;
+    return rng;
+  };
+  constexpr int kSweeps = 12, kCandidates = 32;
+  const int64_t kinds[2][2] = {{0, n}, {n + 1, n + 1 + m}};
+  std::vector<int32_t> order;
+  for (int sweep = 0; sweep < kSweeps; ++sweep) {
+    int64_t swaps = 0;
+    for (const auto& kind : kinds) {
+      const int64_t lo = kind[0], span = kind[1] - kind[0];
+      if (span < 2) continue;
+      order.resize(span);
+      for (int64_t e = 0; e < span; ++e) order[e] = (int32_t)(lo + e);
+      for (int64_t e = span - 1; e > 0; --e) std::swap(order[e], order[next() % (e + 1)]);
+      for (int32_t a : order) {
+        if (!conflicted(a)) continue;
+        int best = 0;
+        int32_t pick = -1;
+        for (int c = 0; c < kCandidates; ++c) {
+          const int32_t b = (int32_t)(lo + (int64_t)(next() % span));
+          if ((ent[b] & 15) == (ent[a] & 15)) continue;
+          const int d = delta(a, b);
+          if (d < best) {
+            best = d;
+            pick = b;
+          }
+        }
+        if (pick >= 0) {
+          swap_entries(a, pick);
+          ++swaps;
+        }
+      }
+    }
+    if (swaps == 0) break;
+  }
+}
+
 template <typename T>
 static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices,
                  const double* values) {
@@ -353,7 +465,6 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       p->res_mr = (int32_t)mr;
       p->res_mc = (int32_t)mc;
       const uint32_t zero_off = (uint32_t)n * 16u;
-      const uint32_t gd_off = (uint32_t)(n + 1) * 16u;
       // Rows / columns go to slots k = slot * NT + thread.  Sorted by degree,
       // they form groups of 64 of nearly equal length (one group per slot of
       // one wavefront).  Within each slot the groups are dealt to the
@@ -390,6 +501,55 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       std::vector<int32_t> rmap, cmap;
       assign(mr * NT, m, H.ptr, rmap);
       assign(mc * NT, n, H.cptr, cmap);
+      // LDS entries: columns in [0, n), the zero entry n, rows in n + 1 + [0, m),
+      // placed to spread each quarter wavefront's accesses over the 16 entry
+      // classes (lds_placement)
+      std::vector<int32_t> ent;
+      {
+        std::vector<int32_t> gptr(1, 0), gmem;
+        auto add_group = [&](const int32_t* mem, int count) {
+          const size_t at = gmem.size();
+          for (int k = 0; k < count; ++k) {
+            bool seen = false;
+            for (size_t q = at; q < gmem.size(); ++q) seen |= gmem[q] == mem[k];
+            if (!seen) gmem.push_back(mem[k]);
+          }
+          if (gmem.size() - at > 1) gptr.push_back((int32_t)gmem.size());
+          else gmem.resize(at);  // a single entity cannot conflict
+        };
+        // slot z of a pass: lanes l own map[z * 64 + l]; the gathered entity of
+        // step s is ent_of(idx[ptr[r] + s]), or the zero entry past the row's end
+        auto slot_groups = [&](const std::vector<int32_t>& map, int64_t z,
+                               const std::vector<int32_t>& ptr, const std::vector<int32_t>& idx,
+                               int32_t own_base, int32_t gather_base) {
+          int32_t width = 0;
+          for (int l = 0; l < 64; ++l) {
+            const int32_t r = map[z * 64 + l];
+            if (r >= 0) width = std::max(width, ptr[r + 1] - ptr[r]);
+          }
+          const int steps = (width + 3) / 4 * 4;
+          int32_t mem[16];
+          for (int q = 0; q < 4; ++q) {
+            int cnt = 0;
+            for (int l = 16 * q; l < 16 * q + 16; ++l)
+              if (map[z * 64 + l] >= 0) mem[cnt++] = own_base + map[z * 64 + l];
+            add_group(mem, cnt);
+            for (int s = 0; s < steps; ++s) {
+              for (int l = 0; l < 16; ++l) {
+                const int32_t r = map[z * 64 + 16 * q + l];
+                mem[l] = (r >= 0 && s < ptr[r + 1] - ptr[r]) ? gather_base + idx[ptr[r] + s]
+                                                             : (int32_t)n;
+              }
+              add_group(mem, 16);
+            }
+          }
+        };
+        for (int64_t z = 0; z < mr * 16; ++z)
+          slot_groups(rmap, z, H.ptr, H.idx, (int32_t)(n + 1), 0);
+        for (int64_t z = 0; z < mc * 16; ++z)
+          slot_groups(cmap, z, H.cptr, H.cidx, 0, (int32_t)(n + 1));
+        lds_placement(n, m, gptr, gmem, ent);
+      }
       // chunk = 64 lanes x 4 entries: u32 LDS byte addresses, then the coefficients
       const size_t CB = 64 * 16 + 64 * 4 * sizeof(T);
       std::vector<unsigned char> stream;
@@ -417,7 +577,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       // columns (column pass); returns the chunk count
       auto put_slot = [&](const std::vector<int32_t>& map, int64_t z,
                           const std::vector<int32_t>& ptr, const std::vector<int32_t>& idx,
-                          const std::vector<T>& val, uint32_t base) -> int {
+                          const std::vector<T>& val, int32_t gather_base) -> int {
         int32_t width = 0;
         for (int l = 0; l < 64; ++l) {
           const int32_t r = map[z * 64 + l];
@@ -433,7 +593,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
             for (int u = 0; u < 4; ++u) {
               const int32_t q = 4 * ch + u;
               const bool has = r >= 0 && q < ptr[r + 1] - ptr[r];
-              off[4 * l + u] = has ? base + 16u * (uint32_t)idx[ptr[r] + q] : zero_off;
+              off[4 * l + u] = has ? 16u * (uint32_t)ent[gather_base + idx[ptr[r] + q]] : zero_off;
               v[4 * l + u] = has ? val[ptr[r] + q] : T(0);
             }
           }
@@ -445,9 +605,9 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         const int64_t first = nchunks;
         uint32_t rc = 0, cc = 0;
         for (int64_t r = 0; r < mr; ++r)
-          rc |= (uint32_t)put_slot(rmap, r * 16 + w, H.ptr, H.idx, H.val_s, 0u) << (8 * r);
+          rc |= (uint32_t)put_slot(rmap, r * 16 + w, H.ptr, H.idx, H.val_s, 0) << (8 * r);
         for (int64_t c = 0; c < mc; ++c)
-          cc |= (uint32_t)put_slot(cmap, c * 16 + w, H.cptr, H.cidx, H.cval_s, gd_off) << (8 * c);
+          cc |= (uint32_t)put_slot(cmap, c * 16 + w, H.cptr, H.cidx, H.cval_s, (int32_t)(n + 1)) << (8 * c);
         // the wrap chunk: a copy of the wave's first chunk (or zero padding),
         // prefetched at the end of each iteration for the next one
         if (nchunks > first) {
@@ -499,8 +659,15 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         int rc2;
 #define UPR(dst, vec) \
   if ((rc2 = upr((void**)&(dst), (vec).empty() ? nullptr : (vec).data(), (vec).size() * sizeof((vec)[0]))) != PURIN_CP_OK) return rc2
+        // each slot's own LDS entry: the (slot, thread) maps' entities placed
+        std::vector<int32_t> rent(rmap.size()), cent(cmap.size());
+        for (size_t k = 0; k < rmap.size(); ++k)
+          rent[k] = rmap[k] >= 0 ? ent[n + 1 + rmap[k]] : -1;
+        for (size_t k = 0; k < cmap.size(); ++k) cent[k] = cmap[k] >= 0 ? ent[cmap[k]] : -1;
         UPR(p->res_rowmap, rmap);
         UPR(p->res_colmap, cmap);
+        UPR(p->res_rowent, rent);
+        UPR(p->res_colent, cent);
         UPR(p->res_stream, stream);
         UPR(p->res_wtab, wtab);
 #undef UPR

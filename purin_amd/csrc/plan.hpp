@@ -85,6 +85,8 @@ struct purin_cp_plan {
   int32_t res_mr = 0, res_mc = 0;    // row / column slots per thread (1..kResMaxSlots)
   int32_t* res_rowmap = nullptr;     // Kr = mr * threads: kept row of each slot or -1
   int32_t* res_colmap = nullptr;     // Kc = mc * threads: column of each slot or -1
+  int32_t* res_rowent = nullptr;     // Kr: LDS entry (16-byte units) of each row slot's d, or -1
+  int32_t* res_colent = nullptr;     // Kc: LDS entry of each column slot's ybar / y, or -1
   unsigned char* res_stream = nullptr;  // per-wavefront chunk streams of the matrix
   int32_t* res_wtab = nullptr;       // [16][4] first chunk and packed chunk counts
   int64_t res_stream_bytes = 0;

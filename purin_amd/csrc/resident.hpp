@@ -67,6 +67,11 @@ struct Res {
   int Kr, Kc;                          // slot-ordered strides: SLR*1024, SLC*1024
   const int32_t* __restrict__ rowmap;  // [Kr] kept row of each (slot, thread) or -1
   const int32_t* __restrict__ colmap;  // [Kc] column of each (slot, thread) or -1
+  // [Kr] / [Kc] LDS entry (16-byte units) of each slot's row / column, or -1:
+  // the plan places the entries so that a quarter wavefront's accesses spread
+  // over the 16 entry classes (the stream's gather addresses use the same map)
+  const int32_t* __restrict__ rowent;
+  const int32_t* __restrict__ colent;
   const unsigned char* __restrict__ stream;  // the chunks
   const int32_t* __restrict__ wtab;    // [16][4]: first chunk, row chunk counts
                                        // (4 x u8), column chunk counts (4 x u8), 0
@@ -206,7 +211,6 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   const int64_t tile = blockIdx.x;
   const uint32_t lane16 = (uint32_t)lane * 16u;
   const V vzero = V(T(0));
-  const uint32_t gd_off = (uint32_t)(A.n + 1) * 16u;
   const uint32_t trash_off = (uint32_t)(A.n + 1 + A.m) * 16u;
 
   const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave]);
@@ -231,7 +235,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
       if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
     }
-    soff_c[c] = j >= 0 ? (uint32_t)j * 16u : trash_off;
+    soff_c[c] = j >= 0 ? (uint32_t)A.colent[c * NT + t] * 16u : trash_off;
     const V t0 = j >= 0 ? Ts[c * NT + t] : vzero;
     if constexpr (kHoldTarget) tg[c] = t0;
     y[c] = t0;  // y0 = ybar0 = yhat (kernels.py:229-231)
@@ -240,7 +244,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 #pragma unroll
   for (int r = 0; r < SLR; ++r) {
     const int i = A.rowmap[r * NT + t];
-    soff_r[r] = i >= 0 ? gd_off + (uint32_t)i * 16u : trash_off;
+    soff_r[r] = i >= 0 ? (uint32_t)A.rowent[r * NT + t] * 16u : trash_off;
     rr[r] = i >= 0 ? Rs[r * NT + t] : vzero;
     if (i >= A.me) ineq |= 1u << r;  // kept rows: equalities first
     lds_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
@@ -435,7 +439,6 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const uint32_t lane16 = (uint32_t)lane * 16u;
   const V vzero = V(T(0));
   const T zero = T(0), half = T(0.5), inf = T(__builtin_inf());
-  const uint32_t gd_off = (uint32_t)(A.n + 1) * 16u;
   const uint32_t trash_off = (uint32_t)(A.n + 1 + A.m) * 16u;
   const uint32_t red_off = trash_off + 16u;
   const uint32_t dec_off = red_off + 16u * 4u * kResQ * 16u;  // [BT] verdicts
@@ -463,7 +466,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
     }
     if (j >= 0) cvalid |= 1u << c;
-    soff_c[c] = j >= 0 ? (uint32_t)j * 16u : trash_off;
+    soff_c[c] = j >= 0 ? (uint32_t)A.colent[c * NT + t] * 16u : trash_off;
     // y0 = ybar0 = yhat (kernels.py:229-231)
     lds_write<V>(soff_c[c],
                  j >= 0 ? reinterpret_cast<const V*>(A.Ts)[tile * (int64_t)A.Kc + c * NT + t] : vzero);
@@ -472,7 +475,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   for (int r = 0; r < SLR; ++r) {
     const int i = A.rowmap[r * NT + t];
     if (i >= 0) rvalid |= 1u << r;
-    soff_r[r] = i >= 0 ? gd_off + (uint32_t)i * 16u : trash_off;
+    soff_r[r] = i >= 0 ? (uint32_t)A.rowent[r * NT + t] * 16u : trash_off;
     if (i >= A.me) ineq |= 1u << r;  // kept rows: equalities first
     lds_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
   }
