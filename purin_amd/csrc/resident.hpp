@@ -227,6 +227,12 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   constexpr bool kHoldTarget = SB || SLR + SLC < 8;
   V y[SLC], tg[kHoldTarget ? SLC : 1], rr[SLR];
   uint32_t ineq = 0, nanb = 0;
+  // shared bounds equal on every column of a wavefront's slots (box bounds,
+  // e.g. [-1, 1]): its column pass then takes them from registers instead of
+  // re-reading them from L2 every iteration.  The test is per wavefront (a
+  // ballot; the kernel uses no LDS beyond its own dynamic layout).
+  const T lo0 = A.Ls[0], hi0 = A.Hs[0];
+  int same = SB && lo0 == lo0 && hi0 == hi0;
 #pragma unroll
   for (int c = 0; c < SLC; ++c) {
     const int j = A.colmap[c * NT + t];
@@ -234,6 +240,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
     for (int s = 0; s < BT; ++s) {
       const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
       if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
+      if (SB && j >= 0 && (A.Ls[e] != lo0 || A.Hs[e] != hi0)) same = 0;
     }
     soff_c[c] = j >= 0 ? (uint32_t)A.colent[c * NT + t] * 16u : trash_off;
     const V t0 = j >= 0 ? Ts[c * NT + t] : vzero;
@@ -250,6 +257,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
     lds_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
   }
   if (t == 0) lds_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
+  const bool uni = __builtin_amdgcn_ballot_w64(same != 0) == ~0ull;  // all 64 lanes
   __syncthreads();
 
   constexpr uint32_t CB = res_chunk_bytes<T>();
@@ -289,7 +297,10 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       GP hb = (GP)A.Hs;
       asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
-      if (SB) {
+      if (SB && uni) {
+        lo = V(lo0);
+        hi = V(hi0);
+      } else if (SB) {
         lo = V(lb[c * NT + t]);
         hi = V(hb[c * NT + t]);
       } else {
@@ -457,6 +468,10 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   uint32_t soff_r[SLR], soff_c[SLC];
   V ky[SLR], dn[SLR];
   uint32_t ineq = 0, nanb = 0, rvalid = 0, cvalid = 0;
+  // shared bounds equal on every column of the wavefront's slots: taken from
+  // registers in the loop (as in k_resident; a ballot, no LDS)
+  const T lo0 = A.Ls[0], hi0 = A.Hs[0];
+  int same = SB && lo0 == lo0 && hi0 == hi0;
 #pragma unroll
   for (int c = 0; c < SLC; ++c) {
     const int j = A.colmap[c * NT + t];
@@ -464,6 +479,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     for (int s = 0; s < BT; ++s) {
       const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
       if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
+      if (SB && j >= 0 && (A.Ls[e] != lo0 || A.Hs[e] != hi0)) same = 0;
     }
     if (j >= 0) cvalid |= 1u << c;
     soff_c[c] = j >= 0 ? (uint32_t)A.colent[c * NT + t] * 16u : trash_off;
@@ -480,6 +496,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     lds_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
   }
   if (t == 0) lds_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
+  const bool uni = __builtin_amdgcn_ballot_w64(same != 0) == ~0ull;  // all 64 lanes
   // samples of the tile: the padding samples beyond the batch never run
   const int64_t bs0 = tile * BT;
   uint32_t act = 0;
@@ -549,7 +566,10 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
       asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
-      if (SB) {
+      if (SB && uni) {
+        lo = V(lo0);
+        hi = V(hi0);
+      } else if (SB) {
         lo = V(lb[c * NT + t]);
         hi = V(hb[c * NT + t]);
       } else {

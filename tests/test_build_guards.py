@@ -104,3 +104,66 @@ def test_the_guard_detects_packed_fp32_and_the_flag_removes_it(tmp_path):
                    check=True, capture_output=True)
     assert PACKED_F32.search(plain.read_text()), "control: expected packed FP32 without the flag"
     assert not PACKED_F32.search(guarded.read_text())
+
+
+def _kernel_metadata(obj, tmp_path, name):
+    """(kernel name, group_segment_fixed_size) of every kernel in a code object."""
+    f = tmp_path / f"{name}.co"
+    f.write_bytes(obj)
+    notes = subprocess.run([f"{LLVM}/llvm-readelf", "--notes", str(f)], check=True,
+                           capture_output=True, text=True).stdout
+    out, lds = [], None
+    for line in notes.splitlines():
+        m = re.search(r"\.group_segment_fixed_size:\s+(\d+)", line)
+        if m:
+            lds = int(m.group(1))
+        m = re.search(r"\.name:\s+(\S+)", line)
+        if m and lds is not None:
+            out.append((m.group(1), lds))
+            lds = None
+    return out
+
+
+def test_resident_kernels_have_no_static_lds(tmp_path):
+    """The resident kernels address LDS by absolute byte offsets held in the
+    matrix stream (their dynamic LDS must start at address 0), so no static LDS
+    may enter them, including through a library helper such as a workgroup
+    reduction."""
+    _need_tools()
+    if not os.path.exists(f"{LLVM}/llvm-readelf"):
+        pytest.skip("llvm-readelf not available")
+    if not os.path.exists(B.LIB):
+        pytest.skip("libpurin_cp.so is not built")
+    seen = 0
+    for k, obj in enumerate(_code_objects(B.LIB)):
+        for name, lds in _kernel_metadata(obj, tmp_path, f"m{k}"):
+            if "k_resident" in name:
+                seen += 1
+                assert lds == 0, f"{name}: {lds} bytes of static LDS"
+    assert seen > 0, "no resident kernel found"
+
+
+def test_the_static_lds_guard_sees_a_workgroup_reduction(tmp_path):
+    """Control: __syncthreads_and brings static LDS into a kernel, and the
+    metadata read above reports it."""
+    _need_tools()
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    if not os.path.exists(hipcc) or not os.path.exists(f"{LLVM}/llvm-readelf"):
+        pytest.skip("hipcc or llvm-readelf not available")
+    src = tmp_path / "red.hip"
+    src.write_text(
+        "#include <hip/hip_runtime.h>\n"
+        "__global__ void k_with_and(const int* a, int* b) {\n"
+        "  b[threadIdx.x] = __syncthreads_and(a[threadIdx.x]);\n"
+        "}\n"
+        "__global__ void k_without(const int* a, int* b) { b[threadIdx.x] = a[threadIdx.x]; }\n")
+    lib = tmp_path / "red.so"
+    subprocess.run([hipcc, "-O3", "-fPIC", "-shared", f"--offload-arch={B.ARCH}", str(src),
+                    "-o", str(lib)], check=True, capture_output=True)
+    meta = {}
+    for k, obj in enumerate(_code_objects(str(lib))):
+        meta.update(dict(_kernel_metadata(obj, tmp_path, f"red{k}")))
+    with_and = [v for n, v in meta.items() if "k_with_and" in n]
+    without = [v for n, v in meta.items() if "k_without" in n]
+    assert with_and and with_and[0] > 0
+    assert without and without[0] == 0
