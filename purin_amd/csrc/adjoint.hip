@@ -500,7 +500,10 @@ __global__ __launch_bounds__(kBlock) void k_gs_dots(const T* __restrict__ basis,
   for (int j = 0; j < NW; ++j) acc[j] = vsplat<T>(T(0));
   const int64_t r_begin = (int64_t)c * rpb;
   const int64_t r_end = std::min<int64_t>(W, r_begin + rpb);
-  for (int64_t r = r_begin; r < r_end; ++r) {
+  // rows last to first: the update-and-dot pass that follows walks the same
+  // chunks first to last, so it starts on the rows read last here, which the
+  // MALL still holds
+  for (int64_t r = r_end - 1; r >= r_begin; --r) {
     const size_t off = (size_t)r * ld + b0;
     const V xr = vload(x + off);
     V v[NW];
@@ -1532,11 +1535,11 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                                                                     part, (int)chunks, rpb, zld);
     return PURIN_CP_OK;
   };
-  // the dot pass: two blocks per CU over the batch tiles, one from 16 prefix
-  // vectors on (as fast, with each wavefront holding 4+ vectors' loads in
-  // flight, and half the chunk partials for the per-sample reduction)
+  // the dot pass: two blocks per CU over the batch tiles, the same chunks as
+  // the update-and-dot pass (launch_gs), so that pass B begins each chunk on
+  // the rows this pass read last (k_gs_dots walks its chunk backwards)
   auto launch_dots = [&](auto kern, int nv, const T* img) -> int {
-    const int64_t per_cu = nv >= 16 ? 1 : 2;
+    const int64_t per_cu = 2;
     const int64_t chunks = std::max<int64_t>(
         1, std::min<int64_t>({per_cu * cus / tiles0, (W + 3) / 4, (int64_t)nchunk2}));
     const int64_t rpb = (W + chunks - 1) / chunks;
