@@ -221,7 +221,10 @@ __global__ __launch_bounds__(kBlock) void k_lin_cols(Adj<T> S, const T* __restri
 }
 
 // ---------------------------------------------------------------------------
-// operator out = v - pullback(v) in three passes; v and out are W x Bp
+// operator out = v - pullback(v) in three passes; v and out are W x Bp.  The
+// input, the masks and the output are streamed nontemporally, so that the
+// prefix rows the last Gram--Schmidt pass read stay in the MALL for the next
+// dot pass (which starts on them); u and w, gathered, stay cacheable.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_op_cols1(Adj<T> S, const T* __restrict__ v,
@@ -238,12 +241,12 @@ __global__ __launch_bounds__(kBlock) void k_op_cols1(Adj<T> S, const T* __restri
     const size_t off = (size_t)j * S.Bp + b0;
     const size_t voff = (size_t)j * S.ldv + b0;
     const size_t boff = (size_t)(S.n + S.m + j) * S.ldv + b0;
-    V gy = vload(v + voff), gb = vload(v + boff);
+    V gy = vload_once(v + voff), gb = vload_once(v + boff);
     if (S.vsc) {
       gy = gy * sc;
       gb = gb * sc;
     }
-    const V u = vload(S.Cm + off) * (gy + T(2) * gb);
+    const V u = vload_once(S.Cm + off) * (gy + T(2) * gb);
     if (S.dg) {
       V du, o;
 #pragma unroll
@@ -252,10 +255,10 @@ __global__ __launch_bounds__(kBlock) void k_op_cols1(Adj<T> S, const T* __restri
         o[s] = gy[s] - (adj_a(S, j, b0 + s) * u[s] - gb[s]);
       }
       vstore(S.U + off, du);
-      vstore(out + voff, o);
+      vstore_once(out + voff, o);
     } else {
       vstore(S.U + off, u);
-      vstore(out + voff, gy - (S.a * u - gb));
+      vstore_once(out + voff, gy - (S.a * u - gb));
     }
   }
 }
@@ -285,11 +288,11 @@ __global__ __launch_bounds__(kBlock) void k_op_rows(Adj<T> S, const T* __restric
 #pragma unroll
       for (int s = 0; s < Sn; ++s) sg[s] = adj_sig(S, i, b0 + s);
       vstore(S.Wv + off, sg * w);
-      vstore(out + voff, gd - w);
+      vstore_once(out + voff, gd - w);
     } else {
       const V w = vload_once(S.Dm + off) * (gd - S.delta * acc);
       vstore(S.Wv + off, w);
-      vstore(out + voff, gd - w);
+      vstore_once(out + voff, gd - w);
     }
   }
 }
@@ -310,12 +313,12 @@ __global__ __launch_bounds__(kBlock) void k_op_cols2(Adj<T> S, const T* __restri
     for (int k = S.K.cptr[j]; k < S.K.cptr[j + 1]; ++k)
       acc += col_coef(S.K, k, b0) * vload(S.Wv + (size_t)S.K.cidx[k] * S.Bp + b0);
     const size_t off = (size_t)(S.n + S.m + j) * S.ldv + b0;
-    V gb = vload(v + off);
+    V gb = vload_once(v + off);
     if (S.vsc) gb = gb * vload(S.vsc + b0);
     if (S.dg)
-      vstore(out + off, gb - acc);
+      vstore_once(out + off, gb - acc);
     else
-      vstore(out + off, gb - S.sigma * acc);
+      vstore_once(out + off, gb - S.sigma * acc);
   }
 }
 
