@@ -318,7 +318,8 @@ typedef struct {
   double diag_ms;       /* summed residual + decide time (stop test) */
   double loop_ms;       /* first iteration kernel start to last end */
   int32_t resident;     /* 1: the iterations ran in the resident kernel (one launch) */
-  int32_t reserved;
+  int32_t linear_kybar; /* 1: the streaming passes formed K ybar = (1 + theta) K y -
+                           theta K y_prev instead of storing ybar (n > 2 m) */
 } purin_cp_timing;
 
 int purin_cp_last_timing(const purin_cp_plan* plan, purin_cp_timing* timing);

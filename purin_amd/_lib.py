@@ -95,7 +95,7 @@ class Timing(C.Structure):
         ("diag_ms", C.c_double),
         ("loop_ms", C.c_double),
         ("resident", C.c_int32),
-        ("reserved", C.c_int32),
+        ("linear_kybar", C.c_int32),
     ]
 
 

@@ -496,6 +496,16 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   // the MALL hits of the next iteration's reads instead).
   const bool col_nt =
       (double)((A.Q ? 4 : 3) * (int64_t)n + 2 * (int64_t)m) * (double)Bp * sizeof(T) > kMallBytes;
+  // K ybar by linearity (kernels.hpp, Iter::lin) where it moves fewer bytes:
+  // with n > 2m the ybar stream the column pass writes (n per sample) outweighs
+  // the two m-vectors of K y the row pass then reads and writes (fixed
+  // iterations), and with the stop test the row pass needs no gathers at all
+  // (the residual pass computes K y+).  Scalar schedule only (one theta for the
+  // batch), not for the dense adapter's unfrozen loop.  The two K y buffers
+  // take the ybar buffer's place (n x Bp >= 2 m x Bp).
+  const bool lin = m > 0 && (int64_t)n > 2 * (int64_t)m && !A.th_b && !A.nofreeze;
+  T* kyb[2] = {A.YB, A.YB + (size_t)m * Bp};
+  T theta_prev = T(0);
   // optional event timing: events[3k] before the row pass, [3k+1] between the
   // passes, [3k+2] after the column pass (and the stop test) of iteration k
   const bool timing = o.timing != 0;
@@ -516,8 +526,20 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     A.delta = tau * A.a;
     A.theta = theta;
     if (timing) PURIN_HIP(hipEventRecord(ev[3 * it], st));
+    if (lin) {  // this iteration's K y lands in kyb[it & 1]; kyb[(it + 1) & 1] holds the previous one
+      A.lin = 1;
+      A.thp = it == 0 ? T(0) : theta_prev;
+      A.KYc = kyb[it & 1];
+      A.KYp = kyb[(it + 1) & 1];
+    }
     if (!early) {
-      if (m) k_row_pass<T, false><<<grow, kBlock, 0, st>>>(A);
+      if (lin) {
+        A.KYo = kyb[it & 1];
+        k_row_pass<T, false, 1><<<grow, kBlock, 0, st>>>(A);
+        A.KYo = nullptr;
+      } else if (m) {
+        k_row_pass<T, false><<<grow, kBlock, 0, st>>>(A);
+      }
       if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 1], st));
       if (col_nt)
         k_col_pass<T, 0, kRowsPerWaveFixed, true><<<gcol, kBlock, 0, st>>>(A);
@@ -539,15 +561,26 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
                                                    nullptr, nullptr, nullptr, nullptr, nullptr);
     } else {
       A.done = done;
-      if (m) k_row_pass<T, true><<<grow, kBlock, 0, st>>>(A);
+      if (lin && it == 0) {  // K y0 (= K ybar0) by one gather of y0
+        A.KYo = kyb[0];
+        k_row_pass<T, true, 1><<<grow, kBlock, 0, st>>>(A);
+        A.KYo = nullptr;
+      } else if (lin) {  // K y from the previous residual pass: no gathers
+        k_row_pass<T, true, 2><<<grow, kBlock, 0, st>>>(A);
+      } else if (m) {
+        k_row_pass<T, true><<<grow, kBlock, 0, st>>>(A);
+      }
       if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 1], st));
       k_col_pass<T, 1, kRowsPerWaveEarly><<<gcolE, kBlock, 0, st>>>(A);
       if (timing) PURIN_HIP(hipEventRecord(evd[it], st));
+      if (lin) A.KYo = kyb[(it + 1) & 1];  // K y+ for the next iteration's row pass
       if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres, kBlock, 0, st>>>(A);
+      A.KYo = nullptr;
       k_decide<T, false><<<gdec, 64 * kDecideGroups, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
                                                    nullptr, nullptr, nullptr, nullptr, nullptr);
     }
     if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 2], st));
+    theta_prev = theta;  // the theta of this iteration's ybar update
     if (p->opts.accelerated && A.th_b) {
       // the same update, per sample: the column pass wrote the next steps into
       // the other buffer; swap (kernels.py:279-283)
@@ -588,6 +621,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     float total = 0;
     if (it > 0) PURIN_HIP(hipEventElapsedTime(&total, ev[0], ev[3 * (it - 1) + 2]));
     t.loop_ms = total;
+    t.linear_kybar = lin ? 1 : 0;
     p->timing = t;
     for (auto& e : ev) (void)hipEventDestroy(e);
     for (auto& e : evd) (void)hipEventDestroy(e);

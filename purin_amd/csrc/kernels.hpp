@@ -101,6 +101,17 @@ struct Iter {
   // return at once when *stop (the accepted count) has reached nstop
   const int32_t* stop;
   int64_t nstop;
+  // K ybar by linearity (lin != 0): ybar = y + theta (y - y_prev)
+  // (kernels.py:149) gives K~ybar = (1 + thp) K~y - thp K~y_prev, with thp the
+  // previous iteration's theta (0 at the first, where ybar = y).  The row pass
+  // takes K~y from a gather of Y (row pass template LIN 1, which stores it at
+  // KYo) or from the previous residual pass (LIN 2, no gathers; the residual
+  // pass stores K~y+ at KYo); ybar itself is not kept (YB is not written).
+  const T* __restrict__ KYc;  // m x Bp: K~y of the current y (LIN 2)
+  const T* __restrict__ KYp;  // m x Bp: K~y of the previous y (read when thp != 0)
+  T* KYo;                     // m x Bp: K~y stored by the row pass (LIN 1) / residual pass
+  T thp;
+  int lin;
   T* colpart;                 // [5][ncb][Bp]: primal, dual, stat, bound, finite
   T* rowpart;                 // [3][nrb][Bp]: residual max, r.d, finite
   int ncb, nrb;
@@ -152,7 +163,7 @@ __device__ __forceinline__ typename Lane<T>::V step_theta(const Iter<T>& A, int6
 // ---------------------------------------------------------------------------
 // row pass: d <- P(d + sigma (K ybar - r)) for samples not yet done
 // ---------------------------------------------------------------------------
-template <typename T, bool MASKED>
+template <typename T, bool MASKED, int LIN = 0>
 __global__ __launch_bounds__(kBlock) void k_row_pass(Iter<T> A) {
   if (A.stop && *A.stop >= A.nstop) return;
   using V = typename Lane<T>::V;
@@ -168,17 +179,25 @@ __global__ __launch_bounds__(kBlock) void k_row_pass(Iter<T> A) {
   for (int rb = blockIdx.y; rb * 4 < A.K.m; rb += gridDim.y) {
     const int i = rb * 4 + wave;
     if (i >= A.K.m) continue;
-    const int s0 = A.K.rptr[i], s1 = A.K.rptr[i + 1];
+    const size_t roff = (size_t)i * A.Bp + b0;
     V acc = vsplat<T>(T(0));
-    // unrolled: four independent gathers in flight per wave (rows are short)
+    if (LIN == 2) {
+      acc = vload(A.KYc + roff);
+    } else {
+      const int s0 = A.K.rptr[i], s1 = A.K.rptr[i + 1];
+      const T* src = LIN ? A.Y : A.YB;
+      // unrolled: four independent gathers in flight per wave (rows are short)
 #pragma unroll 4
-    for (int k = s0; k < s1; ++k) {
-      const V x = vload(A.YB + (size_t)A.K.ridx[k] * A.Bp + b0);
-      acc += row_coef(A.K, k, b0) * x;
+      for (int k = s0; k < s1; ++k) {
+        const V x = vload(src + (size_t)A.K.ridx[k] * A.Bp + b0);
+        acc += row_coef(A.K, k, b0) * x;
+      }
+      if (LIN == 1) vstore(A.KYo + roff, acc);
     }
-    T* dp = A.D + (size_t)i * A.Bp + b0;
+    if (LIN && A.thp != T(0)) acc = (T(1) + A.thp) * acc - A.thp * vload(A.KYp + roff);
+    T* dp = A.D + roff;
     const V d = vload(dp);
-    const V r = vload(A.R + (size_t)i * A.Bp + b0);
+    const V r = vload(A.R + roff);
     V p = d + step_sigma(A, i, b0) * (acc - r);
     if (i >= A.K.me) {
 #pragma unroll
@@ -277,7 +296,7 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
         V yb = yn + step_theta(A, b0) * (yn - y);
         if (MODE == 1) {
           const V yo = y;
-          const V ybo = vload(A.YB + off);
+          const V ybo = A.lin ? yo : vload(A.YB + off);
 #pragma unroll
           for (int s = 0; s < S; ++s) {
             if (keep[s] != zero && !A.nofreeze) {
@@ -287,7 +306,7 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
           }
         }
         vstore_s<NT>(A.Y + off, yn);
-        vstore_s<NT>(A.YB + off, yb);
+        if (!A.lin) vstore_s<NT>(A.YB + off, yb);  // with lin the row pass forms K ybar
       }
       if (MODE != 0 && A.Q) {
         // diagnostics (kernels.py:158-174, 272-274) with general q, c
@@ -365,6 +384,7 @@ __global__ __launch_bounds__(kBlock) void k_res_pass(Iter<T> A) {
       for (int k = s0; k < s1; ++k)
         acc += row_coef(A.K, k, b0) * vload(A.Y + (size_t)A.K.ridx[k] * A.Bp + b0);
       const size_t off = (size_t)i * A.Bp + b0;
+      if (A.KYo) vstore(A.KYo + off, acc);  // K~y+ for the next row pass (lin)
       const V r = vload(A.R + off);
       const V d = vload(A.D + off);
       const V e = acc - r;

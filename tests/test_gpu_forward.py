@@ -313,3 +313,48 @@ def test_resident_early_stop_matches_streaming_and_oracle(dtype, accelerated):
             np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
             assert rel_err(to_np(res.y)[sub], want.y) <= TOL[dtype], n
     assert stopped > 0  # the stop test fired
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("accelerated", [False, True])
+@pytest.mark.parametrize("early_stop", [False, True])
+def test_streaming_linear_kybar_matches_oracle(dtype, accelerated, early_stop):
+    """Wide problems (n > 2m): the streaming passes form K ybar as
+    (1 + theta) K y - theta K y_prev (kernels.py:149 applied under K) instead of
+    storing ybar; with the stop test the row pass takes K y from the residual
+    pass and gathers nothing.  Against the oracle (which forms ybar and
+    gathers it) at the parity bar, with the oracle's iteration counts and
+    statuses in fp64, and against the resident kernel on the same inputs."""
+    torch = require_gpu()
+    bar = TOL[dtype]
+    # tolerances at which the oracle stops these samples within the limit
+    # (fixed step: all of them at both sizes; accelerated: the n = 200 ones)
+    tol = 1e-3 if accelerated else 1e-4
+    stopped = 0
+    for n, me, mi, width, B in ((200, 20, 60, 4, 37), (3000, 300, 900, 6, 40)):
+        w = workloads.small_random(21 + n, n=n, me=me, mi=mi, width=width, batch=B,
+                                   accelerated=accelerated, target_sd=0.5)
+        canon = canonical_from_workload(w)
+        rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+        target = w.target.astype(dtype)
+        plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
+        iters = 400
+        kw = dict(max_iterations=iters, early_stop=early_stop, tolerance=tol)
+        st = plan.project(target, rhs, streaming=True, timing=True, **kw)
+        t = plan.last_timing()
+        assert t["resident"] == 0 and t["linear_kybar"] == 1, n
+        res = plan.project(target, rhs, timing=True, **kw)
+        assert plan.last_timing()["resident"] == 1
+        sub = slice(0, 6)
+        cfg = op.Config(accelerated=accelerated, max_iterations=iters, early_stop=early_stop,
+                        tolerance=tol)
+        want = op.solve(canon, target[sub], rhs[sub], cfg, dtype=dtype)
+        assert rel_err(to_np(st.y)[sub], want.y) <= bar, n
+        if dtype == np.float64:
+            np.testing.assert_array_equal(to_np(st.iterations)[sub], want.iterations)
+            np.testing.assert_array_equal(to_np(st.status)[sub], want.status)
+            np.testing.assert_array_equal(to_np(st.iterations), to_np(res.iterations))
+        assert rel_err(to_np(st.y), to_np(res.y)) <= bar
+        stopped += int(np.sum(to_np(st.iterations) < iters))
+    if early_stop:
+        assert stopped > 0  # the stop test fired
