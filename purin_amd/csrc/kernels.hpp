@@ -431,7 +431,30 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
   const T zero = T(0);
   const size_t cplane = (size_t)A.ncb * A.Bp, rplane = (size_t)A.nrb * A.Bp;
   T q[8] = {zero, zero, zero, zero, T(1), zero, zero, T(1)};  // primal, dual, stat, bnd, fin, res, rd, fin_d
-  for (int c = g; c < A.ncb; c += G) {
+  // Chunks c = g, g + G, ... in increasing order.  The loads of U chunks are
+  // issued before they are folded in (a chain of dependent waits otherwise:
+  // a small batch has few lanes and many chunks per lane); the order of the
+  // folds is unchanged.
+  constexpr int U = 8;
+  int c = g;
+  for (; c + (U - 1) * G < A.ncb; c += U * G) {
+    T v[5][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const T* p = A.colpart + (size_t)(c + u * G) * A.Bp + b;
+#pragma unroll
+      for (int k = 0; k < 5; ++k) v[k][u] = p[k * cplane];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      q[0] += v[0][u];
+      q[1] += v[1][u];
+      q[2] = maxp(q[2], v[2][u]);
+      q[3] = maxp(q[3], v[3][u]);
+      if (v[4][u] == zero) q[4] = zero;
+    }
+  }
+  for (; c < A.ncb; c += G) {
     const T* p = A.colpart + (size_t)c * A.Bp + b;
     q[0] += p[0];
     q[1] += p[cplane];
@@ -439,7 +462,23 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
     q[3] = maxp(q[3], p[3 * cplane]);
     if (p[4 * cplane] == zero) q[4] = zero;
   }
-  for (int r = g; r < A.nrb; r += G) {
+  int r = g;
+  for (; r + (U - 1) * G < A.nrb; r += U * G) {
+    T v[3][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const T* p = A.rowpart + (size_t)(r + u * G) * A.Bp + b;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) v[k][u] = p[k * rplane];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      q[5] = maxp(q[5], v[0][u]);
+      q[6] += v[1][u];
+      if (v[2][u] == zero) q[7] = zero;
+    }
+  }
+  for (; r < A.nrb; r += G) {
     const T* p = A.rowpart + (size_t)r * A.Bp + b;
     q[5] = maxp(q[5], p[0]);
     q[6] += p[rplane];
