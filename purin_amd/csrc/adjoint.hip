@@ -103,6 +103,15 @@ __device__ __forceinline__ T adj_sig(const Adj<T>& S, int64_t i, int64_t b) {
   return S.sig_r ? S.sig_r[i] : S.sigma;
 }
 
+// sigma of row i for the S samples from b0 (adj_sig as one vector: the
+// per-sample arrays hold a lane's samples contiguously)
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V adj_sig_v(const Adj<T>& S, int64_t i, int64_t b0) {
+  if (S.sig_rb) return vload(S.sig_rb + (size_t)i * S.Bp + b0);
+  if (S.sig_b) return vload(S.sig_b + b0);
+  return vsplat<T>(S.sig_r ? S.sig_r[i] : S.sigma);
+}
+
 // d/dx of max(x, y) and min(x, y) with JAX's balanced tie rule.
 template <typename T>
 __device__ __forceinline__ T dmax_dx(T x, T y) {
@@ -134,9 +143,7 @@ __global__ __launch_bounds__(kBlock) void k_lin_rows(Adj<T> S, const T* __restri
     for (int k = S.K.rptr[i]; k < S.K.rptr[i + 1]; ++k)
       acc += row_coef(S.K, k, b0) * vload(Y + (size_t)S.K.ridx[k] * S.Bp + b0);
     const size_t off = (size_t)i * S.Bp + b0;
-    V sg;
-#pragma unroll
-    for (int s = 0; s < Sn; ++s) sg[s] = adj_sig(S, i, b0 + s);
+    const V sg = adj_sig_v(S, i, b0);
     const V p = vload(Dd + off) + sg * (acc - vload(R + off));
     V dm, dp;
 #pragma unroll
@@ -284,9 +291,7 @@ __global__ __launch_bounds__(kBlock) void k_op_rows(Adj<T> S, const T* __restric
     if (S.vsc) gd = gd * vload(S.vsc + b0);
     if (S.dg) {
       const V w = vload_once(S.Dm + off) * (gd - acc);
-      V sg;
-#pragma unroll
-      for (int s = 0; s < Sn; ++s) sg[s] = adj_sig(S, i, b0 + s);
+      const V sg = adj_sig_v(S, i, b0);
       vstore(S.Wv + off, sg * w);
       vstore_once(out + voff, gd - w);
     } else {
@@ -1021,13 +1026,14 @@ __global__ __launch_bounds__(kBlock) void k_final_w(Adj<T> S, const T* __restric
       acc += row_coef(S.K, k, b0) * vload(S.U + (size_t)S.K.ridx[k] * S.Bp + b0);
     const size_t off = (size_t)i * S.Bp + b0;
     const V gd = vload(lam + (size_t)(S.n + i) * S.Bp + b0);
+    const V sg = adj_sig_v(S, i, b0);
     V out, swv;
 #pragma unroll
     for (int s = 0; s < Sn; ++s) {
       const T lw = lam_w[b0 + s];
       const T w = S.dg ? S.Dm[off + s] * ((lw != T(0) ? gd[s] : T(0)) - acc[s])
                        : S.Dm[off + s] * ((lw != T(0) ? gd[s] : T(0)) - S.delta * acc[s]);
-      const T r = adj_sig(S, i, b0 + s) * w;
+      const T r = sg[s] * w;
       swv[s] = r;
       out[s] = finite(r) ? -r : T(0);
     }
