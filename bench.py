@@ -388,6 +388,11 @@ def run_mode(args, torch):
     # these entry points take per-sample bounds: the column pass reads lower and upper (2n)
     bytes_row = B * ws * (n + 3 * m + coef_nnz)               # gather ybar, d, r, d+, per-sample entries
     bytes_col = B * ws * ((6 + extra_n) * n + m + coef_nnz)   # y, yhat (or q, c), bounds, writes, d+, entries
+    if tm["linear_kybar"]:
+        # K ybar formed from K y: the row pass reads and writes K y (2m), the column
+        # pass writes no ybar (n)
+        bytes_row += B * ws * 2 * m
+        bytes_col -= B * ws * n
     dominant = "k_col_pass" if col_ms >= row_ms else "k_row_pass"
     dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == "k_col_pass" else (bytes_row, row_ms)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
@@ -462,7 +467,7 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
     ap.add_argument("--mode", default="project", choices=("project", "values", "qp", "dense"),
                     help="project: the headline (default); values / qp / dense: the widened "
@@ -531,8 +536,15 @@ def main():
     torch.cuda.synchronize()
     tm = plan.last_timing()
     iters = max(int(tm["iterations"]), 1)
-    bytes_row = B * ws * (n + 3 * m)        # gather ybar (n), read d, r (2m), write d (m)
-    bytes_col = B * ws * (4 * n + m)        # gather d+ (m), read y, yhat (2n), write y, ybar (2n)
+    if tm["linear_kybar"]:
+        # K ybar formed from K y: the row pass gathers y (n), reads d, r and the
+        # previous K y (3m), writes d and K y (2m); the column pass gathers d+ (m),
+        # reads y, yhat (2n) and writes y (n), with no ybar vector
+        bytes_row = B * ws * (n + 5 * m)
+        bytes_col = B * ws * (3 * n + m)
+    else:
+        bytes_row = B * ws * (n + 3 * m)    # gather ybar (n), read d, r (2m), write d (m)
+        bytes_col = B * ws * (4 * n + m)    # gather d+ (m), read y, yhat (2n), write y, ybar (2n)
     bytes_iter = B * ws * (5 * n + 3 * m)   # the per-iteration contract figure
     iter_ms = tm["loop_ms"] / iters
     if tm["resident"]:
@@ -602,6 +614,10 @@ def main():
             "traffic": traffic,
             "bytes_per_launch": dom_bytes,
             "avg_launch_ms": dom_ms,
+            "what": (f"algorithmic bytes of one {dominant} launch (one pass of one "
+                     "iteration): "
+                     + ("K ybar formed from K y (no ybar stream; the row pass reads and "
+                        "writes K y)" if tm["linear_kybar"] else "ybar streamed")),
         }
     # the streaming two-pass path on the same inputs, for comparison
     streaming_ms = None
@@ -657,6 +673,7 @@ def main():
         "iteration": {
             "cp_iterations_per_s": w.iterations * 1e3 / ms_per_step,
             "resident_kernel": bool(tm["resident"]),
+            "linear_kybar": bool(tm["linear_kybar"]),
             "streaming_passes_ms_per_step": streaming_ms,
             "row_pass_ms": row_ms,
             "col_pass_ms": col_ms,

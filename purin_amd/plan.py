@@ -41,6 +41,13 @@ def _stream():
     return C.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+def _flags(t):
+    """A 0/1 uint8 flag array returned by the library, seen as bool without a copy
+    (every flag the kernels write is exactly 0 or 1), so a call launches no
+    conversion kernel after the library's own work."""
+    return t.view(torch.bool)
+
+
 @dataclass
 class CPOutput:
     """Inner solve result (reference src/purin/solvers/chambolle_pock/kernels.py:15-23)."""
@@ -235,7 +242,7 @@ class Plan:
             self.handle, _stream(), batch, _ptr(rhs), _ptr(target), _ptr(dual0), _ptr(lower),
             _ptr(upper), _ptr(tol), _u8(feasible), C.byref(o), _ptr(y), _ptr(dual), _i32(it),
             _ptr(res), _ptr(gap), _u8(conv), _ptr(saved)))
-        out = CPOutput(y, dual, it, res, gap, conv.bool())
+        out = CPOutput(y, dual, it, res, gap, _flags(conv))
         return (out, saved) if save else out
 
     def last_timing(self):
@@ -300,14 +307,14 @@ class Plan:
                 self.handle, _stream(), batch, _ptr(values), _ptr(target), _ptr(rhs),
                 _ptr(mult0), C.byref(o), _ptr(y), _ptr(mult), _ptr(slacks), _i32(status),
                 _i32(it), _ptr(res), _u8(fin), _u8(elig), _ptr(saved)))
-            return ProjectOutput(y, mult, slacks, status, it, res, fin.bool(), elig.bool(),
+            return ProjectOutput(y, mult, slacks, status, it, res, _flags(fin), _flags(elig),
                                  saved)
         entry = self.lib.purin_cp_project_noalloc if noalloc else self.lib.purin_cp_project
         _lib.check(entry(
             self.handle, _stream(), batch, _ptr(target), _ptr(rhs), _ptr(mult0), C.byref(o),
             _ptr(y), _ptr(mult), _ptr(slacks), _i32(status), _i32(it), _ptr(res), _u8(fin),
             _u8(elig), _ptr(saved)))
-        return ProjectOutput(y, mult, slacks, status, it, res, fin.bool(), elig.bool(), saved)
+        return ProjectOutput(y, mult, slacks, status, it, res, _flags(fin), _flags(elig), saved)
 
     def qp_solve(self, q, c, rhs, lower, upper, *, values=None, y0=None, dual0=None,
                  tolerance=1e-9, max_iterations=10000, early_stop=True, check_every=32,
@@ -343,7 +350,7 @@ class Plan:
             self.handle, _stream(), batch, _ptr(q), _ptr(c), _ptr(values), _ptr(rhs),
             _ptr(lower), _ptr(upper), _ptr(y0), _ptr(dual0), C.byref(o), _ptr(y), _ptr(mult),
             _ptr(slacks), _i32(status), _i32(it), _ptr(res), _u8(fin), _u8(conv), _ptr(saved)))
-        return QPOutput(y, mult, slacks, status, it, res, fin.bool(), conv.bool(), saved)
+        return QPOutput(y, mult, slacks, status, it, res, _flags(fin), _flags(conv), saved)
 
     def dense_solve(self, q, c, rhs, lower, upper, *, values=None, y0=None, dual0=None,
                     tolerance=1e-9, max_iterations=5000, early_stop=True, check_every=32,
@@ -429,7 +436,7 @@ class Plan:
             self.handle, _stream(), batch, _ptr(saved), _ptr(q), _ptr(c), _ptr(values), _ptr(cot),
             _ptr(cotd), C.byref(o), _ptr(gq), _ptr(gc), _ptr(gv), _ptr(gr), _ptr(gl), _ptr(gu),
             _u8(valid), _i32(info), _ptr(res)))
-        return QPAdjointOutput(gq, gc, gv, gr, gl, gu, valid.bool(), info, res)
+        return QPAdjointOutput(gq, gc, gv, gr, gl, gu, _flags(valid), info, res)
 
     def adjoint(self, saved, target, rhs, cot_y, *, tolerance=1e-9, atol=0.0, restart=30,
                 max_iterations=100, adjoint_tolerance=1e-8, force_eligible=False,
@@ -466,9 +473,9 @@ class Plan:
             _lib.check(self.lib.purin_cp_adjoint_values(
                 self.handle, _stream(), batch, _ptr(saved), _ptr(values), _ptr(cot), C.byref(o),
                 _ptr(gt), _ptr(gr), _ptr(gv), _u8(valid), _i32(info), _ptr(res)))
-            return AdjointOutput(gt, gr, None, None, valid.bool(), info, res, gv)
+            return AdjointOutput(gt, gr, None, None, _flags(valid), info, res, gv)
         _lib.check(self.lib.purin_cp_adjoint(
             self.handle, _stream(), batch, _ptr(saved), _ptr(target), _ptr(rhs), _ptr(cot),
             C.byref(o), _ptr(gt), _ptr(gr), _ptr(gl), _ptr(gu), _u8(valid), _i32(info),
             _ptr(res)))
-        return AdjointOutput(gt, gr, gl, gu, valid.bool(), info, res)
+        return AdjointOutput(gt, gr, gl, gu, _flags(valid), info, res)

@@ -96,9 +96,9 @@ class _ProjectFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, y_hat, rhs, values, layer, multipliers0):
+    def forward(ctx, y_hat, rhs, values, layer, multipliers0, save):
         vals = None if values is None else values.detach().contiguous()
-        out = layer.plan.project(y_hat, rhs, multipliers0=multipliers0, save=True, values=vals,
+        out = layer.plan.project(y_hat, rhs, multipliers0=multipliers0, save=save, values=vals,
                                  **layer._solve_kwargs())
         ctx.layer = layer
         ctx.saved_state = out.saved
@@ -113,7 +113,7 @@ class _ProjectFn(torch.autograd.Function):
     def backward(ctx, cot_y, *unused):
         layer = ctx.layer
         if cot_y is None:
-            return None, None, None, None, None
+            return None, None, None, None, None, None
         lin = layer.config.linear_solver
         adj = layer.plan.adjoint(ctx.saved_state, None, None, cot_y.contiguous(),
                                  tolerance=lin.tolerance, atol=lin.atol, restart=lin.restart,
@@ -122,7 +122,7 @@ class _ProjectFn(torch.autograd.Function):
                                  rhs_rows=layer.plan.me + layer.plan.mi, values=ctx.values)
         g_rhs = adj.g_rhs if ctx.needs_input_grad[1] else None
         g_values = adj.g_values if ctx.needs_input_grad[2] else None
-        return adj.g_target, g_rhs, g_values, None, None
+        return adj.g_target, g_rhs, g_values, None, None, None
 
 
 @dataclass(eq=False)
@@ -258,8 +258,11 @@ class PreparedChambollePockProjection:
         rhs = self._rhs(theta)
         values = self._values(theta)
         mult0 = self._multipliers0(multipliers_eq, multipliers_ineq)
+        # the state the backward pass reads is saved only when a backward pass can run
+        save = torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (target, rhs, values))
         y, mult, slacks, status, iters, res, fin, elig = _ProjectFn.apply(target, rhs, values,
-                                                                          self, mult0)
+                                                                          self, mult0, save)
         me = self.equality_size
         return ProjectionResult(y, mult[:, :me], mult[:, me:], slacks, status, iters, res, fin,
                                 elig)
