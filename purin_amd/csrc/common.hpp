@@ -17,6 +17,11 @@ namespace purin {
 
 constexpr int kWave = 64;
 constexpr int kBlock = 256;  // 4 wavefronts
+// ints per wavefront of the resident kernels' wave table: first chunk; the
+// chunk counts of the row slots and of the column slots (4 x u8 each); the
+// slots' entries in their last chunk, rows and columns (4 x u8 each); the row
+// and column section chunk counts; 0
+constexpr int kResWtab = 8;
 
 template <typename T>
 struct Lane;

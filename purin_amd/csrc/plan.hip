@@ -469,7 +469,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       // they form groups of 64 of nearly equal length (one group per slot of
       // one wavefront).  Within each slot the groups are dealt to the
       // wavefronts longest first to the wavefront with the least work so far,
-      // which evens out the chunks each wavefront walks between barriers.
+      // which evens out the entries each wavefront walks between barriers.
       auto assign = [&](int64_t K, int64_t count, const std::vector<int32_t>& ptr,
                         std::vector<int32_t>& map) {
         std::vector<int32_t> order(count);
@@ -478,9 +478,9 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
           return ptr[a + 1] - ptr[a] > ptr[b + 1] - ptr[b];
         });
         const int64_t groups = K / 64;
-        std::vector<int32_t> gch(groups, 0);  // chunks of each sorted group
+        std::vector<int32_t> gch(groups, 0);  // entries per lane of each sorted group
         for (int64_t g = 0; g < groups; ++g)
-          if (g * 64 < count) gch[g] = (ptr[order[g * 64] + 1] - ptr[order[g * 64]] + 3) / 4;
+          if (g * 64 < count) gch[g] = ptr[order[g * 64] + 1] - ptr[order[g * 64]];
         std::vector<int64_t> load(16, 0);
         std::vector<int64_t> slice_of(groups);
         for (int64_t slot = 0; slot < groups / 16; ++slot) {
@@ -527,7 +527,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
             const int32_t r = map[z * 64 + l];
             if (r >= 0) width = std::max(width, ptr[r + 1] - ptr[r]);
           }
-          const int steps = (width + 3) / 4 * 4;
+          const int steps = width;  // slots are packed: no chunk padding past the widest
           int32_t mem[16];
           for (int q = 0; q < 4; ++q) {
             int cnt = 0;
@@ -553,7 +553,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       // chunk = 64 lanes x 4 entries: u32 LDS byte addresses, then the coefficients
       const size_t CB = 64 * 16 + 64 * 4 * sizeof(T);
       std::vector<unsigned char> stream;
-      std::vector<int32_t> wtab(4 * 16, 0);
+      std::vector<int32_t> wtab((size_t)kResWtab * 16, 0);
       int64_t nchunks = 0;
       auto put_chunk = [&](const uint32_t* off, const T* val) {  // off, val: [64][4]
         const size_t at = stream.size();
@@ -573,41 +573,99 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         ++nchunks;
       };
       bool too_wide = false;
-      // one slot of one wavefront: chunks of the 64 lanes' rows (row pass) or
-      // columns (column pass); returns the chunk count
-      auto put_slot = [&](const std::vector<int32_t>& map, int64_t z,
-                          const std::vector<int32_t>& ptr, const std::vector<int32_t>& idx,
-                          const std::vector<T>& val, int32_t gather_base) -> int {
-        int32_t width = 0;
-        for (int l = 0; l < 64; ++l) {
-          const int32_t r = map[z * 64 + l];
-          if (r >= 0) width = std::max(width, ptr[r + 1] - ptr[r]);
-        }
-        const int nch = (width + 3) / 4;
-        if (nch > 255) too_wide = true;
-        uint32_t off[64 * 4];
-        T v[64 * 4];
-        for (int ch = 0; ch < nch; ++ch) {
+      // One pass of one wavefront (its row slots or its column slots): the
+      // slots' entries packed back to back, slot s taking W_s entries per lane
+      // (W_s = the longest row / column of its 64 lanes; shorter ones padded
+      // with the zero entry), so a slot may start inside the chunk where the
+      // one before it ends.  A chunk is shared by two slots at most: a slot
+      // that would start and end inside a shared chunk starts on the next
+      // chunk instead (the previous slot is padded to the boundary), and the
+      // section's end is padded to a whole chunk.  Writes to width[] each
+      // slot's entries from its first whole chunk on (W_s less the head it
+      // has in the chunk it shares with the slot before) and returns the
+      // section's chunk count.
+      auto put_section = [&](const std::vector<int32_t>& map, int64_t slots, int w,
+                             const std::vector<int32_t>& ptr, const std::vector<int32_t>& idx,
+                             const std::vector<T>& val, int32_t gather_base,
+                             int32_t* width) -> int64_t {
+        std::vector<int32_t> W(slots, 0);
+        for (int64_t s2 = 0; s2 < slots; ++s2)
           for (int l = 0; l < 64; ++l) {
-            const int32_t r = map[z * 64 + l];
-            for (int u = 0; u < 4; ++u) {
-              const int32_t q = 4 * ch + u;
-              const bool has = r >= 0 && q < ptr[r + 1] - ptr[r];
-              off[4 * l + u] = has ? 16u * (uint32_t)ent[gather_base + idx[ptr[r] + q]] : zero_off;
-              v[4 * l + u] = has ? val[ptr[r] + q] : T(0);
+            const int32_t r = map[(s2 * 16 + w) * 64 + l];
+            if (r >= 0) W[s2] = std::max(W[s2], ptr[r + 1] - ptr[r]);
+          }
+        // entry positions: slot s2 starts at at[s2]; pads are zero entries
+        std::vector<int64_t> at(slots, 0);
+        int64_t E = 0;
+        for (int64_t s2 = 0; s2 < slots; ++s2) {
+          int64_t u = E % 4;
+          if (u > 0 && W[s2] < 4 - u) {  // would start and end inside the shared chunk
+            width[s2 - 1] += (int32_t)(4 - u);
+            E += 4 - u;
+            u = 0;
+          }
+          const int64_t h = u > 0 ? 4 - u : 0;  // head in the chunk shared with s2 - 1
+          width[s2] = (int32_t)(W[s2] - h);
+          at[s2] = E;
+          E += W[s2];
+        }
+        if (slots > 0) {
+          const int64_t pad = (4 - E % 4) % 4;
+          width[slots - 1] += (int32_t)pad;
+          E += pad;
+        }
+        const int64_t nch = E / 4;
+        if (nch >= (int64_t)1 << 20) {
+          too_wide = true;
+          return 0;
+        }
+        std::vector<uint32_t> off((size_t)64 * E, zero_off);
+        std::vector<T> v((size_t)64 * E, T(0));
+        for (int l = 0; l < 64; ++l)
+          for (int64_t s2 = 0; s2 < slots; ++s2) {
+            const int32_t r = map[(s2 * 16 + w) * 64 + l];
+            if (r < 0) continue;
+            for (int32_t q = 0; q < ptr[r + 1] - ptr[r]; ++q) {
+              off[(size_t)l * E + at[s2] + q] = 16u * (uint32_t)ent[gather_base + idx[ptr[r] + q]];
+              v[(size_t)l * E + at[s2] + q] = val[ptr[r] + q];
             }
           }
-          put_chunk(off, v);
+        uint32_t co[64 * 4];
+        T cv[64 * 4];
+        for (int64_t ch = 0; ch < nch; ++ch) {
+          for (int l = 0; l < 64; ++l)
+            for (int u = 0; u < 4; ++u) {
+              co[4 * l + u] = off[(size_t)l * E + 4 * ch + u];
+              cv[4 * l + u] = v[(size_t)l * E + 4 * ch + u];
+            }
+          put_chunk(co, cv);
         }
         return nch;
       };
+      // per slot: its whole chunks and the entries of the last one, 8 bits each
+      auto pack_slots = [&](const int32_t* width, int64_t slots, int32_t& cnt, int32_t& last) {
+        uint32_t c = 0, l = 0;
+        for (int64_t s2 = 0; s2 < slots; ++s2) {
+          const int32_t R = width[s2];
+          const int32_t nch = (R + 3) / 4;
+          const int32_t e = nch > 0 ? R - 4 * (nch - 1) : 4;
+          if (nch > 255) too_wide = true;
+          c |= (uint32_t)(nch & 255) << (8 * s2);
+          l |= (uint32_t)e << (8 * s2);
+        }
+        cnt = (int32_t)c;
+        last = (int32_t)l;
+      };
+      int64_t iter_chunks = 0;
       for (int w = 0; w < 16; ++w) {
         const int64_t first = nchunks;
-        uint32_t rc = 0, cc = 0;
-        for (int64_t r = 0; r < mr; ++r)
-          rc |= (uint32_t)put_slot(rmap, r * 16 + w, H.ptr, H.idx, H.val_s, 0) << (8 * r);
-        for (int64_t c = 0; c < mc; ++c)
-          cc |= (uint32_t)put_slot(cmap, c * 16 + w, H.cptr, H.cidx, H.cval_s, (int32_t)(n + 1)) << (8 * c);
+        int32_t* wt = &wtab[(size_t)kResWtab * w];
+        int32_t rw[kResMaxSlots] = {0, 0, 0, 0}, cw[kResMaxSlots] = {0, 0, 0, 0};
+        const int64_t rch = put_section(rmap, mr, w, H.ptr, H.idx, H.val_s, 0, rw);
+        const int64_t cch =
+            put_section(cmap, mc, w, H.cptr, H.cidx, H.cval_s, (int32_t)(n + 1), cw);
+        pack_slots(rw, mr, wt[1], wt[3]);
+        pack_slots(cw, mc, wt[2], wt[4]);
         // the wrap chunk: a copy of the wave's first chunk (or zero padding),
         // prefetched at the end of each iteration for the next one
         if (nchunks > first) {
@@ -624,23 +682,17 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
           }
           put_chunk(off, v);
         }
-        wtab[4 * w] = (int32_t)first;
-        wtab[4 * w + 1] = (int32_t)rc;
-        wtab[4 * w + 2] = (int32_t)cc;
+        wt[0] = (int32_t)first;
+        wt[5] = (int32_t)rch;
+        wt[6] = (int32_t)cch;
+        iter_chunks += rch + cch;
       }
       if (too_wide || nchunks >= (int64_t)1 << 30) p->res_ok = false;
       if (p->res_ok) {
         // matrix-stream bytes one workgroup reads per iteration: every
         // wavefront's row and column chunks (the early-stop kernel reads the
         // same, plus one closing row sweep per launch)
-        auto chunks_of = [](int32_t packed) {
-          int total = 0;
-          for (int k = 0; k < 4; ++k) total += (packed >> (8 * k)) & 255;
-          return (int64_t)total;
-        };
-        int64_t chunks = 0;
-        for (int w = 0; w < 16; ++w) chunks += chunks_of(wtab[4 * w + 1]) + chunks_of(wtab[4 * w + 2]);
-        p->res_iter_bytes = chunks * (int64_t)CB;
+        p->res_iter_bytes = iter_chunks * (int64_t)CB;
         p->res_iter_bytes_e = p->res_iter_bytes;
       }
       if (p->res_ok) {

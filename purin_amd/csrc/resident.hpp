@@ -14,8 +14,10 @@
 //            stream of chunks per wavefront (row slots, column slots, then a
 //            copy of the first chunk), a chunk being 4 entries per lane stored
 //            as {LDS byte address of the gathered element, coefficient}.  The
-//            loads take an SGPR base and a constant lane offset, and the next
-//            chunk is always in flight while the current one is gathered,
+//            slots of a pass are packed back to back (a slot may begin and end
+//            inside a chunk; only each pass's end is padded to a whole chunk).
+//            The loads take an SGPR base and a constant lane offset, and the
+//            next chunk is always in flight while the current one is gathered,
 //            across slot, pass and iteration boundaries.
 // Rows and columns are assigned to (slot, thread) in decreasing-degree order
 // so the lanes of a wavefront walk rows / columns of (almost) equal length.
@@ -86,8 +88,9 @@ struct Res {
   const int32_t* __restrict__ rowent;
   const int32_t* __restrict__ colent;
   const unsigned char* __restrict__ stream;  // the chunks
-  const int32_t* __restrict__ wtab;    // [16][4]: first chunk, row chunk counts
-                                       // (4 x u8), column chunk counts (4 x u8), 0
+  const int32_t* __restrict__ wtab;    // [16][kResWtab]: first chunk; per row slot
+                                       // and per column slot (4 x u8 each) its
+                                       // chunks and the entries of its last chunk
   const T* __restrict__ Ts;   // [tiles][Kc][BT] targets in slot order
   const T* __restrict__ Rs;   // [tiles][Kr][BT] scaled rhs in slot order
   const T* __restrict__ D0s;  // [tiles][Kr][BT] initial duals in slot order
@@ -169,21 +172,93 @@ __device__ __forceinline__ void consume_chunk(const Chunk<T>& c, V& acc) {
   for (int u = 0; u < kResChunk; ++u) acc += c.v[u] * x[u];
 }
 
-// Sum over the ``nch`` chunks of one slot.  On entry b0 holds (or is loading)
-// the slot's first chunk and ``pos`` indexes the next chunk of the wave's
-// stream; on exit b0 holds the chunk after the slot's last one.  The chunks
-// are taken in pairs by a loop whose every pass issues the same loads (the
-// next chunk into b1, then the one after into b0), so the compiler waits only
-// for the chunk being consumed (the later chunk stays in flight); an odd last
-// chunk is consumed after the loop.  Summation order: the slot's chunks in
-// stream order, entries in order.
+// Entries [0, e) of the chunk to acc and entries [e, 4) to carry, in order:
+// the chunk's last entries open the next slot (e is wave-uniform).
 template <typename T, typename V>
-__device__ __forceinline__ V slot_sum(int nch, Chunk<T>& b0, Chunk<T>& b1, uint32_t& pos,
-                                      const unsigned char* __restrict__ stream, uint32_t lane16) {
+__device__ __forceinline__ void consume_split(const Chunk<T>& c, int e, V& acc, V& carry) {
+  V x[kResChunk];
+#pragma unroll
+  for (int u = 0; u < kResChunk; ++u) x[u] = lds_read<V>(c.o[u]);
+  // one straight-line block per split point; the empty asm keeps the compiler
+  // from merging the blocks into selects over both sums
+  if (e == 1) {
+    asm volatile("");
+    acc += c.v[0] * x[0];
+    carry += c.v[1] * x[1];
+    carry += c.v[2] * x[2];
+    carry += c.v[3] * x[3];
+  } else if (e == 2) {
+    asm volatile("");
+    acc += c.v[0] * x[0];
+    acc += c.v[1] * x[1];
+    carry += c.v[2] * x[2];
+    carry += c.v[3] * x[3];
+  } else {
+    asm volatile("");
+    acc += c.v[0] * x[0];
+    acc += c.v[1] * x[1];
+    acc += c.v[2] * x[2];
+    carry += c.v[3] * x[3];
+  }
+}
+
+// A slot's last chunk: its own, or shared with the next slot (e < 4).
+template <typename T, typename V>
+__device__ __forceinline__ void consume_last(const Chunk<T>& c, int e, V& acc, V& carry) {
+  if (e == kResChunk) {
+    asm volatile("");
+    consume_chunk(c, acc);
+  } else {
+    consume_split(c, e, acc, carry);
+  }
+}
+
+// Sum over one slot.  The slots of a pass are packed: a slot may open inside
+// the previous slot's last chunk (at most two slots share a chunk), and those
+// head entries arrive summed in ``carry``, from the previous call, which
+// consumed the shared chunk once.  The call then takes the slot's R entries
+// from the next whole chunk on, and leaves in ``carry`` the head of the next
+// slot when the slot's last chunk is shared (R and the split are
+// wave-uniform: ``nch`` whole chunks, the last with ``e`` entries of the
+// slot).  On entry b0 holds (or is loading) the slot's first whole
+// chunk and ``pos`` indexes the next chunk of the wave's stream; on exit b0
+// holds the chunk after the slot's last one.  The chunks are taken in pairs
+// by a loop whose every pass issues the same loads (the next chunk into b1,
+// then the one after into b0), so the compiler waits only for the chunk being
+// consumed (the later chunk stays in flight); the last one or two chunks are
+// taken after the loop, the last one whole or split.  Summation order: the
+// slot's entries in stream order, its head first.  SPLIT false: the pass has
+// one slot, which owns every chunk it walks (no head, no split).
+template <typename T, typename V, bool SPLIT>
+__device__ __forceinline__ V slot_sum(int nch, int e, V& carry, Chunk<T>& b0, Chunk<T>& b1,
+                                      uint32_t& pos, const unsigned char* __restrict__ stream,
+                                      uint32_t lane16) {
   constexpr uint64_t CB = res_chunk_bytes<T>();
-  V acc = V(T(0));
+  if constexpr (!SPLIT) {
+    // one slot per pass: it owns all its chunks (the pass's end is padded)
+    V acc = V(T(0));
+    int k = 0;
+    for (; k + 1 < nch; k += 2) {
+      load_chunk(b1, stream, pos * CB, lane16);
+      ++pos;
+      __builtin_amdgcn_sched_barrier(0);
+      consume_chunk(b0, acc);
+      load_chunk(b0, stream, pos * CB, lane16);
+      ++pos;
+      __builtin_amdgcn_sched_barrier(0);
+      consume_chunk(b1, acc);
+    }
+    if (k < nch) {
+      consume_chunk(b0, acc);
+      load_chunk(b0, stream, pos * CB, lane16);
+      ++pos;
+    }
+    return acc;
+  }
+  V acc = carry;
+  carry = V(T(0));
   int k = 0;
-  for (; k + 1 < nch; k += 2) {
+  for (; k + 2 < nch; k += 2) {
     load_chunk(b1, stream, pos * CB, lane16);
     ++pos;
     // keep the load ahead of the consumption it overlaps (the scheduler would
@@ -195,12 +270,26 @@ __device__ __forceinline__ V slot_sum(int nch, Chunk<T>& b0, Chunk<T>& b1, uint3
     __builtin_amdgcn_sched_barrier(0);
     consume_chunk(b1, acc);
   }
-  if (k < nch) {
+  if (k + 1 < nch) {
+    load_chunk(b1, stream, pos * CB, lane16);
+    ++pos;
+    __builtin_amdgcn_sched_barrier(0);
     consume_chunk(b0, acc);
+    load_chunk(b0, stream, pos * CB, lane16);
+    ++pos;
+    __builtin_amdgcn_sched_barrier(0);
+    consume_last(b1, e, acc, carry);
+  } else if (k < nch) {
+    consume_last(b0, e, acc, carry);
     load_chunk(b0, stream, pos * CB, lane16);
     ++pos;
   }
   return acc;
+}
+
+// Field k (8 bits) of a wave-table word of per-slot counts.
+__device__ __forceinline__ int slot_field(uint32_t word, int k) {
+  return (int)((word >> (8 * k)) & 255u);
 }
 
 // jnp.clip(x, lo, hi) for bounds that are not NaN: (x <= lo) is false for a
@@ -226,9 +315,14 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
   const V vzero = V(T(0));
   const uint32_t trash_off = (uint32_t)(A.n + 1 + A.m) * 16u;
 
-  const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave]);
-  const uint32_t rcnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave + 1]);
-  const uint32_t ccnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave + 2]);
+  const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave]);
+  // per slot (8 bits each): whole chunks from the slot's first whole chunk on,
+  // and the slot's entries in the last of them (4, or 1-3 when the next slot
+  // opens inside it)
+  const uint32_t rcnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 1]);
+  const uint32_t ccnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 2]);
+  const uint32_t rlast = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 3]);
+  const uint32_t clast = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 4]);
 
   const V* Ts = reinterpret_cast<const V*>(A.Ts) + tile * (int64_t)A.Kc;
   const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)A.Kr;
@@ -283,12 +377,17 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
         (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
     const T sigma = sc[0], a = sc[1], delta = sc[2], theta = sc[3];
     uint32_t pos = first + 1;
+    V carry = vzero;  // the head of the next slot (a chunk shared by two slots)
+    // the slot tables, opaque to the loop so that their fields are decoded at
+    // each slot rather than held decoded in SGPRs across the iteration
+    uint32_t rc = rcnt, rl = rlast, cc = ccnt, cl = clast;
+    asm volatile("" : "+s"(rc), "+s"(rl), "+s"(cc), "+s"(cl));
     // ---- row pass (reads Gy and the thread's own Gd entries, writes Gd) -------
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
-      const int nch = (int)((rcnt >> (8 * r)) & 255u);
       const V dold = lds_read<V>(soff_r[r]);
-      const V acc = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
+                                              b0, b1, pos, A.stream, lane16);
       V p = dold + sigma * (acc - rr[r]);
       if (ineq & (1u << r)) {
 #pragma unroll
@@ -298,9 +397,9 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
     }
     __syncthreads();
     // ---- column pass (reads Gd, writes Gy) --------------------------------------
+    carry = vzero;
 #pragma unroll
     for (int c = 0; c < SLC; ++c) {
-      const int nch = (int)((ccnt >> (8 * c)) & 255u);
       // bounds are re-read each iteration (L2-resident when shared) rather
       // than held in registers: the opaque base keeps them inside the loop;
       // they are loaded before the gathers, which hide their latency
@@ -329,7 +428,8 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
         asm volatile("" : "+s"(tb));
         tgc = tb[tile * (int64_t)A.Kc + c * NT + t];
       }
-      const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      const V tt = slot_sum<T, V, (SLC > 1)>(slot_field(cc, c), slot_field(cl, c), carry,
+                                             b0, b1, pos, A.stream, lane16);
       const V sv = a * y[c] - delta * tt + delta * tgc;
       V yn;
       if (nanb & (1u << c)) {  // a NaN bound on this lane: the exact NaN-propagating clip
@@ -467,9 +567,14 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const uint32_t red_off = trash_off + 16u;
   const uint32_t dec_off = red_off + 16u * 4u * kResQ * 16u;  // [BT] verdicts
 
-  const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave]);
-  const uint32_t rcnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave + 1]);
-  const uint32_t ccnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[4 * wave + 2]);
+  const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave]);
+  // per slot (8 bits each): whole chunks from the slot's first whole chunk on,
+  // and the slot's entries in the last of them (4, or 1-3 when the next slot
+  // opens inside it)
+  const uint32_t rcnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 1]);
+  const uint32_t ccnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 2]);
+  const uint32_t rlast = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 3]);
+  const uint32_t clast = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 4]);
 
   const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)A.Kr;
   const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)A.Kr;
@@ -532,11 +637,13 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   // holds the first column chunk
   {
     const T sigma0 = A.sched[0];
+    V carry = vzero;  // the head of the next slot (a chunk shared by two slots)
+    const uint32_t rc = rcnt, rl = rlast;
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
-      const int nch = (int)((rcnt >> (8 * r)) & 255u);
       const V rr = Rs[r * NT + t];
-      ky[r] = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      ky[r] = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
+                                        b0, b1, pos, A.stream, lane16);
       V p = lds_read<V>(soff_r[r]) + sigma0 * (ky[r] - rr);
       if (ineq & (1u << r)) {
 #pragma unroll
@@ -565,9 +672,13 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     __syncthreads();
     // ---- column pass, masked, with the column diagnostics ------------------------------
     V qp = vzero, qd = vzero, qc = vzero;
+    V carry = vzero;  // the head of the next slot (a chunk shared by two slots)
+    // the slot tables, opaque to the loop so that their fields are decoded at
+    // each slot rather than held decoded in SGPRs across the iteration
+    uint32_t rc = rcnt, rl = rlast, cc = ccnt, cl = clast;
+    asm volatile("" : "+s"(rc), "+s"(rl), "+s"(cc), "+s"(cl));
 #pragma unroll
     for (int c = 0; c < SLC; ++c) {
-      const int nch = (int)((ccnt >> (8 * c)) & 255u);
       typedef const __attribute__((address_space(1))) T* GP;
       GP lb = (GP)A.Ls;
       GP hb = (GP)A.Hs;
@@ -576,7 +687,8 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       // latency; the bounds after them (register pressure)
       asm volatile("" : "+s"(tb));
       const V tg = ((GV)tb)[tile * (int64_t)A.Kc + c * NT + t];
-      const V tt = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      const V tt = slot_sum<T, V, (SLC > 1)>(slot_field(cc, c), slot_field(cl, c), carry,
+                                             b0, b1, pos, A.stream, lane16);
       asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
       if (SB && uni) {
@@ -654,11 +766,12 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     asm volatile("" : "+s"(rb));
     const T tp1 = T(1) + theta;
     V qr = qd, qm = qc;  // the thread's dual terms and maxima of both passes
+    carry = vzero;
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
-      const int nch = (int)((rcnt >> (8 * r)) & 255u);
       const V rr = rb[r * NT + t];
-      const V acc = slot_sum<T, V>(nch, b0, b1, pos, A.stream, lane16);
+      const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
+                                              b0, b1, pos, A.stream, lane16);
       const V d = lds_read<V>(soff_r[r]);
       if (rvalid & (1u << r)) {  // kernels.py:158-166
         // e = K y+ - r; equality rows |e|, inequality rows max(e, 0): max(e, w e)

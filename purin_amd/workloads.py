@@ -103,6 +103,28 @@ def random_rows(*, seed, n, me, mi, width, value_sd, x0_half, bound, batch, targ
                     info=dict(mi_general=mi, width=width, bound=bound))
 
 
+def ragged_rows(seed, *, n, me, mi, wmin, wmax, batch, bound=1.0, dtype=np.float64,
+                accelerated=False, iterations=200, target_sd=2.0):
+    """Random sparse rows of ragged widths (uniform in [wmin, wmax], wmin >= 2 so
+    no general row is a singleton) with a feasible point, for parity tests of
+    schedules whose slots hold rows and columns of unequal length."""
+    rng = np.random.default_rng(seed)
+    rows, vals = [], []
+    for _ in range(me + mi):
+        w = int(rng.integers(wmin, wmax + 1))
+        rows.append(np.sort(rng.choice(n, w, replace=False)).tolist())
+        vals.append(rng.normal(0.0, 1.0, w).tolist())
+    x0 = rng.uniform(-0.5 * bound, 0.5 * bound, n)
+    Kx = np.array([np.dot(v, x0[c]) for c, v in zip(rows, vals)])
+    rhs = list(Kx[:me]) + list(Kx[me:] + rng.uniform(0.0, 1.0, mi))
+    _append_bounds(rows, vals, rhs, np.full(n, -bound), np.full(n, bound))
+    target = rng.normal(0.0, target_sd, (batch, n))
+    indptr, indices, data = _csr_from_rows(rows, vals)
+    return Workload(f"ragged{seed}", n, me, indptr, indices, data, np.asarray(rhs),
+                    target.astype(dtype), np.dtype(dtype), accelerated, iterations,
+                    info=dict(mi_general=mi, width=(wmin, wmax), bound=bound))
+
+
 def config1(batch=32):
     """Plumbing: n=64, 16 eq + 32 ineq rows of 4 columns, fp64, fixed-step, 1000 iterations."""
     return random_rows(seed=1, n=64, me=16, mi=32, width=4, value_sd=1.0, x0_half=0.5,

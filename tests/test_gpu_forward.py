@@ -260,6 +260,51 @@ def test_resident_kernel_matches_streaming_and_oracle(dtype, accelerated):
         np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
 
 
+# ragged rows: (n, me, mi, wmin, wmax, B).  The resident schedule packs each
+# wavefront's slots back to back, so a chunk may hold the end of one slot and
+# the start of the next: these shapes give split chunks in the row pass (3 and
+# 4 row slots of unequal widths) and in the column pass, and slots narrower
+# than a chunk (mostly empty columns: widths 0-2)
+RAGGED = ((2500, 700, 1800, 2, 11, 20), (4000, 100, 400, 2, 5, 9), (1000, 1200, 2800, 2, 9, 33))
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_resident_packed_slots_ragged_rows(dtype, accelerated):
+    """The resident kernels on rows and columns of unequal lengths (packed slots,
+    chunks shared by two slots) against the streaming passes and the oracle, in
+    fixed-iteration and early-stop mode."""
+    require_gpu()
+    for k, (n, me, mi, wmin, wmax, B) in enumerate(RAGGED):
+        w = workloads.ragged_rows(50 + k, n=n, me=me, mi=mi, wmin=wmin, wmax=wmax, batch=B,
+                                  accelerated=accelerated)
+        canon = canonical_from_workload(w)
+        rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+        target = w.target.astype(dtype)
+        plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
+        bar = TOL[dtype]
+        iters = 150
+        res = plan.project(target, rhs, max_iterations=iters, early_stop=False, timing=True)
+        assert plan.last_timing()["resident"] == 1, n
+        st = plan.project(target, rhs, max_iterations=iters, early_stop=False, streaming=True)
+        assert rel_err(to_np(res.y), to_np(st.y)) <= bar / 10, n
+        assert rel_err(to_np(res.multipliers), to_np(st.multipliers)) <= bar, n
+        np.testing.assert_array_equal(to_np(res.status), to_np(st.status))
+        sub = slice(0, 2)
+        cfg = op.Config(accelerated=accelerated, max_iterations=iters, early_stop=False)
+        want = op.solve(canon, target[sub], rhs[sub], cfg, dtype=dtype)
+        assert rel_err(to_np(res.y)[sub], want.y) <= bar, n
+        np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
+        if dtype == np.float64:  # early stop: identical iteration counts in fp64
+            kw = dict(max_iterations=600, early_stop=True, tolerance=1e-5 if accelerated else 1e-4)
+            re_ = plan.project(target, rhs, timing=True, **kw)
+            assert plan.last_timing()["resident"] == 1, n
+            se = plan.project(target, rhs, streaming=True, **kw)
+            np.testing.assert_array_equal(to_np(re_.iterations), to_np(se.iterations))
+            np.testing.assert_array_equal(to_np(re_.status), to_np(se.status))
+            assert rel_err(to_np(re_.y), to_np(se.y)) <= bar, n
+
+
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
 @pytest.mark.parametrize("accelerated", [False, True])
 def test_resident_early_stop_matches_streaming_and_oracle(dtype, accelerated):
