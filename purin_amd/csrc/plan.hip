@@ -152,6 +152,39 @@ int ensure_schedule(purin_cp_plan* p, int64_t iters, hipStream_t stream, bool at
   return PURIN_CP_OK;
 }
 
+// Layout of one wavefront's pass in the resident kernels' matrix stream: slots
+// of W[s] entries per lane packed back to back, a chunk being 4 entries.  A
+// slot that would start and end inside a chunk it shares with the slot before
+// starts on the next chunk instead (the previous slot is padded to the
+// boundary), so a chunk holds two slots at most, and the pass's end is padded
+// to a whole chunk.  Fills at[s] (the slot's first entry) and from[s] (its
+// entries from its first whole chunk on, pads included) when given; returns
+// the pass's chunk count.
+static int64_t pass_layout(const int32_t* W, int64_t slots, int64_t* at, int32_t* from) {
+  int64_t E = 0;
+  int32_t prev = 0;  // entries of the previous slot from its first whole chunk
+  for (int64_t s = 0; s < slots; ++s) {
+    int64_t u = E % 4;
+    if (u > 0 && W[s] < 4 - u) {
+      prev += (int32_t)(4 - u);
+      if (from) from[s - 1] = prev;
+      E += 4 - u;
+      u = 0;
+    }
+    const int64_t h = u > 0 ? 4 - u : 0;  // head in the chunk shared with slot s - 1
+    prev = (int32_t)(W[s] - h);
+    if (from) from[s] = prev;
+    if (at) at[s] = E;
+    E += W[s];
+  }
+  if (slots > 0) {
+    const int64_t pad = (4 - E % 4) % 4;
+    if (from) from[slots - 1] = prev + (int32_t)pad;
+    E += pad;
+  }
+  return E / 4;
+}
+
 // splitmix64 start vector in [-1, 1) (the oracle's start_vector restates it).
 static double start_value(uint64_t seed, uint64_t j) {
   uint64_t z = (seed << 32) + j + 0x9E3779B97F4A7C15ULL;
@@ -470,6 +503,10 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       // one wavefront).  Within each slot the groups are dealt to the
       // wavefronts longest first to the wavefront with the least work so far,
       // which evens out the entries each wavefront walks between barriers.
+      // (Dealing all groups widest-first to the least-loaded wavefront and
+      // ordering each wavefront's slots for the fewest packed chunks took the
+      // config 2 column pass's widest wavefront from 8 to 7 chunks and made no
+      // measurable difference, so the simpler dealing stays.)
       auto assign = [&](int64_t K, int64_t count, const std::vector<int32_t>& ptr,
                         std::vector<int32_t>& map) {
         std::vector<int32_t> order(count);
@@ -596,25 +633,8 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
           }
         // entry positions: slot s2 starts at at[s2]; pads are zero entries
         std::vector<int64_t> at(slots, 0);
-        int64_t E = 0;
-        for (int64_t s2 = 0; s2 < slots; ++s2) {
-          int64_t u = E % 4;
-          if (u > 0 && W[s2] < 4 - u) {  // would start and end inside the shared chunk
-            width[s2 - 1] += (int32_t)(4 - u);
-            E += 4 - u;
-            u = 0;
-          }
-          const int64_t h = u > 0 ? 4 - u : 0;  // head in the chunk shared with s2 - 1
-          width[s2] = (int32_t)(W[s2] - h);
-          at[s2] = E;
-          E += W[s2];
-        }
-        if (slots > 0) {
-          const int64_t pad = (4 - E % 4) % 4;
-          width[slots - 1] += (int32_t)pad;
-          E += pad;
-        }
-        const int64_t nch = E / 4;
+        const int64_t nch = pass_layout(W.data(), slots, at.data(), width);
+        const int64_t E = nch * 4;
         if (nch >= (int64_t)1 << 20) {
           too_wide = true;
           return 0;
