@@ -13,6 +13,7 @@
 // the plan's precision.
 
 #include <algorithm>
+#include <functional>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -315,6 +316,96 @@ static void lds_placement(int64_t n, int64_t m, const std::vector<int32_t>& gptr
   }
 }
 
+// One gathered item of a lane's slot: its entry offset q in the row / column
+// (-1: padding, the zero entry), the gathered entity (-1: the zero entry) and
+// the entity's LDS entry class (its entry index mod 16).
+struct GatherItem {
+  int32_t q, e, cls;
+};
+
+// Order of one slot's gathers for the 16 lanes of a quarter wavefront, which
+// gather together at each step (one ds_read_b128 serves 16 lanes, and entries
+// of one class at distinct addresses conflict; equal addresses broadcast).
+// Step by step, a maximum matching of lanes to classes (lanes with fewer
+// classes left first; classes with more items left tried first) gives each
+// matched lane an item of its own class; an unmatched lane takes the item
+// that adds the fewest addresses to a class this step.  Writes each lane's W
+// items in step order to out[l * W + s] (the item's q).  The sums then run in
+// this order instead of the row's / column's index order.
+static void schedule_quarter(std::vector<GatherItem> (&lanes)[16], int W, int32_t* out) {
+  for (int s = 0; s < W; ++s) {
+    int left[16] = {0};
+    for (int l = 0; l < 16; ++l)
+      for (const GatherItem& it : lanes[l]) left[it.cls]++;
+    int nopt[16], opt[16][16];
+    for (int l = 0; l < 16; ++l) {
+      bool has[16] = {false};
+      for (const GatherItem& it : lanes[l]) has[it.cls] = true;
+      nopt[l] = 0;
+      for (int c = 0; c < 16; ++c)
+        if (has[c]) opt[l][nopt[l]++] = c;
+      std::stable_sort(opt[l], opt[l] + nopt[l], [&](int a, int b) { return left[a] > left[b]; });
+    }
+    int owner[16], lane_cls[16];
+    for (int c = 0; c < 16; ++c) owner[c] = -1;
+    for (int l = 0; l < 16; ++l) lane_cls[l] = -1;
+    // Kuhn's augmenting paths over at most 16 x 16
+    std::function<bool(int, bool*)> augment = [&](int l, bool* seen) -> bool {
+      for (int k = 0; k < nopt[l]; ++k) {
+        const int c = opt[l][k];
+        if (seen[c]) continue;
+        seen[c] = true;
+        if (owner[c] < 0 || augment(owner[c], seen)) {
+          owner[c] = l;
+          lane_cls[l] = c;
+          return true;
+        }
+      }
+      return false;
+    };
+    int lorder[16];
+    for (int l = 0; l < 16; ++l) lorder[l] = l;
+    std::stable_sort(lorder, lorder + 16, [&](int a, int b) { return nopt[a] < nopt[b]; });
+    for (int k = 0; k < 16; ++k) {
+      if (lanes[lorder[k]].empty()) continue;
+      bool seen[16] = {false};
+      augment(lorder[k], seen);
+    }
+    for (int c = 0; c < 16; ++c)
+      if (owner[c] >= 0) lane_cls[owner[c]] = c;
+    // the step's addresses per class so far (entities; -1 the zero entry)
+    std::vector<int32_t> picked[16];
+    auto add_cost = [&](const GatherItem& it) {
+      for (int32_t e : picked[it.cls])
+        if (e == it.e) return 0;
+      return (int)picked[it.cls].size() + 1;
+    };
+    auto take = [&](int l, size_t k) {
+      const GatherItem it = lanes[l][k];
+      lanes[l].erase(lanes[l].begin() + (std::ptrdiff_t)k);
+      picked[it.cls].push_back(it.e);
+      out[(size_t)l * W + s] = it.q;
+    };
+    for (int l = 0; l < 16; ++l) {
+      if (lane_cls[l] < 0 || lanes[l].empty()) continue;
+      for (size_t k = 0; k < lanes[l].size(); ++k)
+        if (lanes[l][k].cls == lane_cls[l]) {
+          take(l, k);
+          break;
+        }
+    }
+    for (int l = 0; l < 16; ++l) {
+      if (lane_cls[l] >= 0 || lanes[l].empty()) continue;
+      size_t best = 0;
+      for (size_t k = 1; k < lanes[l].size(); ++k) {
+        const int a = add_cost(lanes[l][k]), b = add_cost(lanes[l][best]);
+        if (a < b || (a == b && left[lanes[l][k].cls] > left[lanes[l][best].cls])) best = k;
+      }
+      take(l, best);
+    }
+  }
+}
+
 template <typename T>
 static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices,
                  const double* values) {
@@ -544,9 +635,9 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       std::vector<int32_t> ent;
       {
         std::vector<int32_t> gptr(1, 0), gmem;
-        auto add_group = [&](const int32_t* mem, int count) {
+        auto add_group = [&](const int32_t* mem, size_t count) {
           const size_t at = gmem.size();
-          for (int k = 0; k < count; ++k) {
+          for (size_t k = 0; k < count; ++k) {
             bool seen = false;
             for (size_t q = at; q < gmem.size(); ++q) seen |= gmem[q] == mem[k];
             if (!seen) gmem.push_back(mem[k]);
@@ -554,8 +645,12 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
           if (gmem.size() - at > 1) gptr.push_back((int32_t)gmem.size());
           else gmem.resize(at);  // a single entity cannot conflict
         };
-        // slot z of a pass: lanes l own map[z * 64 + l]; the gathered entity of
-        // step s is ent_of(idx[ptr[r] + s]), or the zero entry past the row's end
+        // slot z of a pass: lanes l own map[z * 64 + l].  A quarter wavefront
+        // reads its own entries together, and gathers its rows' / columns'
+        // entities in an order scheduled after the placement (schedule_quarter)
+        // that spreads each step over the classes as far as the quarter's
+        // class counts allow, so the placement balances the classes of all the
+        // entities a quarter gathers (the zero entry when a lane pads)
         auto slot_groups = [&](const std::vector<int32_t>& map, int64_t z,
                                const std::vector<int32_t>& ptr, const std::vector<int32_t>& idx,
                                int32_t own_base, int32_t gather_base) {
@@ -564,21 +659,20 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
             const int32_t r = map[z * 64 + l];
             if (r >= 0) width = std::max(width, ptr[r + 1] - ptr[r]);
           }
-          const int steps = width;  // slots are packed: no chunk padding past the widest
-          int32_t mem[16];
+          std::vector<int32_t> mem;
           for (int q = 0; q < 4; ++q) {
-            int cnt = 0;
+            mem.clear();
             for (int l = 16 * q; l < 16 * q + 16; ++l)
-              if (map[z * 64 + l] >= 0) mem[cnt++] = own_base + map[z * 64 + l];
-            add_group(mem, cnt);
-            for (int s = 0; s < steps; ++s) {
-              for (int l = 0; l < 16; ++l) {
-                const int32_t r = map[z * 64 + 16 * q + l];
-                mem[l] = (r >= 0 && s < ptr[r + 1] - ptr[r]) ? gather_base + idx[ptr[r] + s]
-                                                             : (int32_t)n;
-              }
-              add_group(mem, 16);
+              if (map[z * 64 + l] >= 0) mem.push_back(own_base + map[z * 64 + l]);
+            add_group(mem.data(), mem.size());
+            mem.clear();
+            for (int l = 0; l < 16; ++l) {
+              const int32_t r = map[z * 64 + 16 * q + l];
+              const int32_t d = r >= 0 ? ptr[r + 1] - ptr[r] : 0;
+              for (int32_t k = 0; k < d; ++k) mem.push_back(gather_base + idx[ptr[r] + k]);
+              if (d < width) mem.push_back((int32_t)n);
             }
+            add_group(mem.data(), mem.size());
           }
         };
         for (int64_t z = 0; z < mr * 16; ++z)
@@ -641,15 +735,36 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         }
         std::vector<uint32_t> off((size_t)64 * E, zero_off);
         std::vector<T> v((size_t)64 * E, T(0));
-        for (int l = 0; l < 64; ++l)
-          for (int64_t s2 = 0; s2 < slots; ++s2) {
-            const int32_t r = map[(s2 * 16 + w) * 64 + l];
-            if (r < 0) continue;
-            for (int32_t q = 0; q < ptr[r + 1] - ptr[r]; ++q) {
-              off[(size_t)l * E + at[s2] + q] = 16u * (uint32_t)ent[gather_base + idx[ptr[r] + q]];
-              v[(size_t)l * E + at[s2] + q] = val[ptr[r] + q];
+        const int32_t zcls = (int32_t)(n & 15);
+        for (int64_t s2 = 0; s2 < slots; ++s2) {
+          const int32_t Wd = W[s2];
+          if (Wd == 0) continue;
+          std::vector<int32_t> sched((size_t)16 * Wd);
+          for (int q4 = 0; q4 < 4; ++q4) {
+            std::vector<GatherItem> lanes[16];
+            for (int l = 0; l < 16; ++l) {
+              const int32_t r = map[(s2 * 16 + w) * 64 + 16 * q4 + l];
+              const int32_t d = r >= 0 ? ptr[r + 1] - ptr[r] : 0;
+              for (int32_t k = 0; k < d; ++k) {
+                const int32_t e = gather_base + idx[ptr[r] + k];
+                lanes[l].push_back({k, e, ent[e] & 15});
+              }
+              for (int32_t k = d; k < Wd; ++k) lanes[l].push_back({-1, -1, zcls});
+            }
+            schedule_quarter(lanes, Wd, sched.data());
+            for (int l = 0; l < 16; ++l) {
+              const int lane = 16 * q4 + l;
+              const int32_t r = map[(s2 * 16 + w) * 64 + lane];
+              for (int32_t st2 = 0; st2 < Wd; ++st2) {
+                const int32_t k = sched[(size_t)l * Wd + st2];
+                if (k < 0) continue;  // padding: the zero entry, coefficient 0
+                off[(size_t)lane * E + at[s2] + st2] =
+                    16u * (uint32_t)ent[gather_base + idx[ptr[r] + k]];
+                v[(size_t)lane * E + at[s2] + st2] = val[ptr[r] + k];
+              }
             }
           }
+        }
         uint32_t co[64 * 4];
         T cv[64 * 4];
         for (int64_t ch = 0; ch < nch; ++ch) {

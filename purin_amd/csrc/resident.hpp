@@ -28,10 +28,11 @@
 //   col pass   y+ = clip(a y - delta K^T d+ + delta yhat, lo, hi);
 //              Gy <- y+ + theta (y+ - y); y <- y+            (reads Gd only)
 //   barrier
-// The arithmetic (operand order, fused multiply-adds, slot order of every
-// sum) is that of the streaming passes in kernels.hpp, so the two paths give
-// identical iterates.  Only the fixed-iteration mode runs here; the
-// per-sample stop test uses the streaming passes.
+// The arithmetic (operand order, fused multiply-adds) is that of the
+// streaming passes in kernels.hpp; each row's and column's sum runs in the
+// order the plan scheduled its gathers (for LDS classes), so the two paths
+// agree to rounding.  k_resident runs the fixed-iteration mode;
+// k_resident_early (below) adds the per-sample stop test.
 #pragma once
 
 #include "common.hpp"

@@ -290,6 +290,10 @@ def test_resident_packed_slots_ragged_rows(dtype, accelerated):
         assert rel_err(to_np(res.y), to_np(st.y)) <= bar / 10, n
         assert rel_err(to_np(res.multipliers), to_np(st.multipliers)) <= bar, n
         np.testing.assert_array_equal(to_np(res.status), to_np(st.status))
+        # the shared-bounds kernel (bounds from registers) gives the same bits
+        sh = plan.project(target, rhs, max_iterations=iters, early_stop=False,
+                          shared_bounds=True)
+        np.testing.assert_array_equal(to_np(sh.y), to_np(res.y))
         sub = slice(0, 2)
         cfg = op.Config(accelerated=accelerated, max_iterations=iters, early_stop=False)
         want = op.solve(canon, target[sub], rhs[sub], cfg, dtype=dtype)
@@ -343,8 +347,12 @@ def test_resident_early_stop_matches_streaming_and_oracle(dtype, accelerated):
         # accelerated fp32: the stop iteration itself moves by up to a few hundred
         # iterations under rounding-level changes of the iterate (measured: the
         # streaming passes and the oracle differ as much at n = 48), so the counts
-        # are not compared there; every sample's projected point still is
-        assert rel_err(to_np(res.y), to_np(st.y)) <= TOL[dtype]
+        # are not compared there.  Samples stopped at the same iteration agree to
+        # the parity bar; two points that each passed the stop test at tolerance
+        # tol but at different iterations agree to that tolerance's scale, 2 tol
+        yr, ys = to_np(res.y), to_np(st.y)
+        assert rel_err(yr[same], ys[same]) <= TOL[dtype]
+        assert rel_err(yr, ys) <= (2 * tol if dtype == np.float32 and accelerated else TOL[dtype])
         assert rel_err(to_np(res.multipliers)[same], to_np(st.multipliers)[same]) <= TOL[dtype] * 10
         if dtype == np.float64 or not accelerated:
             np.testing.assert_array_equal(to_np(res.status)[same], to_np(st.status)[same])
