@@ -204,18 +204,20 @@ struct HostMatrix {
   std::vector<T> cval_s, cval_o;
 };
 
-// LDS placement of the resident kernels' vectors.  A ds_read_b128 or
-// ds_write_b128 serves 16 consecutive lanes at a time and is free of bank
-// conflicts when their 16-byte entries differ mod 16 (lanes on one entry are a
-// broadcast).  Each gather step of the row pass reads, per quarter wavefront,
-// the entries of 16 columns; a step of the column pass those of 16 rows; a
-// quarter's own-entry reads and writes touch its 16 rows or columns.  Those
-// sets are the groups (gptr/gmem: distinct entities per group; entities are
-// columns [0, n), the zero entry n, rows n + 1 + [0, m)).  The entries of the
-// columns and of the rows are permuted among themselves (so every entry class
-// keeps its size and the LDS image its length) by a greedy swap search that
-// lowers the number of same-class pairs summed over the groups; ent[e] is
-// entity e's entry.  The search is deterministic (fixed seed) and bounded.
+// LDS placement of the resident kernels' vectors.  A ds_read_b128 serves a
+// wavefront's lanes in four cycle groups of 16 (kCycleLane) and is free of
+// bank conflicts when a group's 16-byte entries differ mod 16 (lanes on one
+// entry are a broadcast).  Over a slot, a group gathers the entries of its 16
+// rows' columns (row pass) or columns' rows (column pass), and reads and
+// writes its own 16 entries.  Those sets are the groups here (gptr/gmem:
+// distinct entities per group; entities are columns [0, n), the zero entry n,
+// rows n + 1 + [0, m)).  The entries of the columns and of the rows are
+// permuted among themselves (so every entry class keeps its size and the LDS
+// image its length) by a greedy swap search that lowers the number of
+// same-class pairs summed over the groups, balancing the classes each group
+// gathers; the gathers of a slot are then ordered step by step
+// (schedule_group).  ent[e] is entity e's entry.  The search is deterministic
+// (fixed seed) and bounded.
 static void lds_placement(int64_t n, int64_t m, const std::vector<int32_t>& gptr,
                           const std::vector<int32_t>& gmem, std::vector<int32_t>& ent) {
   const int64_t E = n + 1 + m;
@@ -316,6 +318,18 @@ static void lds_placement(int64_t n, int64_t m, const std::vector<int32_t>& gptr
   }
 }
 
+// The lanes a ds_read_b128 serves together: the wavefront's 64 lanes take four
+// cycles of 16, a cycle serving, within one half wavefront, lanes 0-3 and
+// 12-15 of one quarter with lanes 4-11 of the other (measured on gfx950:
+// 16-byte entries in distinct classes, entry index mod 16, within each of
+// these groups read at the full rate whatever the other groups do; a class
+// read at k distinct addresses in a group costs about k cycles).
+static const int kCycleLane[4][16] = {
+    {0, 1, 2, 3, 12, 13, 14, 15, 20, 21, 22, 23, 24, 25, 26, 27},
+    {4, 5, 6, 7, 8, 9, 10, 11, 16, 17, 18, 19, 28, 29, 30, 31},
+    {32, 33, 34, 35, 44, 45, 46, 47, 52, 53, 54, 55, 56, 57, 58, 59},
+    {36, 37, 38, 39, 40, 41, 42, 43, 48, 49, 50, 51, 60, 61, 62, 63}};
+
 // One gathered item of a lane's slot: its entry offset q in the row / column
 // (-1: padding, the zero entry), the gathered entity (-1: the zero entry) and
 // the entity's LDS entry class (its entry index mod 16).
@@ -323,16 +337,16 @@ struct GatherItem {
   int32_t q, e, cls;
 };
 
-// Order of one slot's gathers for the 16 lanes of a quarter wavefront, which
-// gather together at each step (one ds_read_b128 serves 16 lanes, and entries
-// of one class at distinct addresses conflict; equal addresses broadcast).
+// Order of one slot's gathers for the 16 lanes of a cycle group (kCycleLane),
+// which gather together at each step (entries of one class at distinct
+// addresses conflict; equal addresses broadcast).
 // Step by step, a maximum matching of lanes to classes (lanes with fewer
 // classes left first; classes with more items left tried first) gives each
 // matched lane an item of its own class; an unmatched lane takes the item
 // that adds the fewest addresses to a class this step.  Writes each lane's W
 // items in step order to out[l * W + s] (the item's q).  The sums then run in
 // this order instead of the row's / column's index order.
-static void schedule_quarter(std::vector<GatherItem> (&lanes)[16], int W, int32_t* out) {
+static void schedule_group(std::vector<GatherItem> (&lanes)[16], int W, int32_t* out) {
   for (int s = 0; s < W; ++s) {
     int left[16] = {0};
     for (int l = 0; l < 16; ++l)
@@ -630,8 +644,8 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       assign(mr * NT, m, H.ptr, rmap);
       assign(mc * NT, n, H.cptr, cmap);
       // LDS entries: columns in [0, n), the zero entry n, rows in n + 1 + [0, m),
-      // placed to spread each quarter wavefront's accesses over the 16 entry
-      // classes (lds_placement)
+      // placed to spread each cycle group's accesses over the 16 entry classes
+      // (lds_placement)
       std::vector<int32_t> ent;
       {
         std::vector<int32_t> gptr(1, 0), gmem;
@@ -645,12 +659,12 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
           if (gmem.size() - at > 1) gptr.push_back((int32_t)gmem.size());
           else gmem.resize(at);  // a single entity cannot conflict
         };
-        // slot z of a pass: lanes l own map[z * 64 + l].  A quarter wavefront
-        // reads its own entries together, and gathers its rows' / columns'
-        // entities in an order scheduled after the placement (schedule_quarter)
-        // that spreads each step over the classes as far as the quarter's
-        // class counts allow, so the placement balances the classes of all the
-        // entities a quarter gathers (the zero entry when a lane pads)
+        // slot z of a pass: lanes l own map[z * 64 + l].  A cycle group
+        // (kCycleLane) reads its own entries together, and gathers its rows' /
+        // columns' entities in an order scheduled after the placement
+        // (schedule_group) that spreads each step over the classes as far as
+        // the group's class counts allow, so the placement balances the classes
+        // of all the entities a group gathers (the zero entry when a lane pads)
         auto slot_groups = [&](const std::vector<int32_t>& map, int64_t z,
                                const std::vector<int32_t>& ptr, const std::vector<int32_t>& idx,
                                int32_t own_base, int32_t gather_base) {
@@ -660,14 +674,15 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
             if (r >= 0) width = std::max(width, ptr[r + 1] - ptr[r]);
           }
           std::vector<int32_t> mem;
-          for (int q = 0; q < 4; ++q) {
+          for (int g = 0; g < 4; ++g) {
             mem.clear();
-            for (int l = 16 * q; l < 16 * q + 16; ++l)
-              if (map[z * 64 + l] >= 0) mem.push_back(own_base + map[z * 64 + l]);
+            for (int i = 0; i < 16; ++i)
+              if (map[z * 64 + kCycleLane[g][i]] >= 0)
+                mem.push_back(own_base + map[z * 64 + kCycleLane[g][i]]);
             add_group(mem.data(), mem.size());
             mem.clear();
-            for (int l = 0; l < 16; ++l) {
-              const int32_t r = map[z * 64 + 16 * q + l];
+            for (int i = 0; i < 16; ++i) {
+              const int32_t r = map[z * 64 + kCycleLane[g][i]];
               const int32_t d = r >= 0 ? ptr[r + 1] - ptr[r] : 0;
               for (int32_t k = 0; k < d; ++k) mem.push_back(gather_base + idx[ptr[r] + k]);
               if (d < width) mem.push_back((int32_t)n);
@@ -740,10 +755,10 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
           const int32_t Wd = W[s2];
           if (Wd == 0) continue;
           std::vector<int32_t> sched((size_t)16 * Wd);
-          for (int q4 = 0; q4 < 4; ++q4) {
+          for (int g = 0; g < 4; ++g) {
             std::vector<GatherItem> lanes[16];
             for (int l = 0; l < 16; ++l) {
-              const int32_t r = map[(s2 * 16 + w) * 64 + 16 * q4 + l];
+              const int32_t r = map[(s2 * 16 + w) * 64 + kCycleLane[g][l]];
               const int32_t d = r >= 0 ? ptr[r + 1] - ptr[r] : 0;
               for (int32_t k = 0; k < d; ++k) {
                 const int32_t e = gather_base + idx[ptr[r] + k];
@@ -751,9 +766,9 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
               }
               for (int32_t k = d; k < Wd; ++k) lanes[l].push_back({-1, -1, zcls});
             }
-            schedule_quarter(lanes, Wd, sched.data());
+            schedule_group(lanes, Wd, sched.data());
             for (int l = 0; l < 16; ++l) {
-              const int lane = 16 * q4 + l;
+              const int lane = kCycleLane[g][l];
               const int32_t r = map[(s2 * 16 + w) * 64 + lane];
               for (int32_t st2 = 0; st2 < Wd; ++st2) {
                 const int32_t k = sched[(size_t)l * Wd + st2];
