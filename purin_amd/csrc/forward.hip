@@ -442,6 +442,11 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
       k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);
     }
     A.done = nullptr;
+    // free after the loop: the final passes leave K~^T d in the ybar buffer and
+    // K~y at the kept rows' places of the multiplier buffer
+    A.TK = A.YB;
+    A.KYo = (T*)(ws + L.DF);
+    A.kyrow = p->dkept;
     const dim3 gcolE0 = tile_grid(Bp, TS, L.ncb);
     const dim3 gres0 = tile_grid(Bp, TS, std::max(L.nrb, 1));
     const dim3 gdec0((unsigned)(Bp / 64));  // k_decide: 64 samples per block
@@ -631,9 +636,14 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     const int32_t cnt = (int32_t)o.max_iterations;
     k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);
   }
-  // final diagnostics on the returned state (kernels.py:291-305)
+  // final diagnostics on the returned state (kernels.py:291-305); the ybar /
+  // K y buffers are free now: the final passes leave K~^T d there and K~y at
+  // the kept rows' places of the multiplier buffer
   A.done = nullptr;
   A.stop = nullptr;
+  A.TK = A.YB;
+  A.KYo = (T*)(ws + L.DF);
+  A.kyrow = p->dkept;
   k_col_pass<T, 2, kRowsPerWaveEarly><<<gcolE, kBlock, 0, st>>>(A);
   if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres, kBlock, 0, st>>>(A);
   k_decide<T, true><<<gdec, 64 * kDecideGroups, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
@@ -887,6 +897,8 @@ static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T
   P.brow = p->brow;
   P.bcoef = (const T*)p->dbcoef;
   P.tgt = (const T*)(sv + L.Tt);
+  P.TK = (const T*)(ws + L.YB);  // K~^T d of the final diagnostics pass
+  P.KY = true;                   // and its K~y, in DF
   P.Y = (const T*)(sv + L.Y);
   P.D = (const T*)(sv + L.D);
   P.RF = RF;

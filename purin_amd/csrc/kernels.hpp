@@ -110,6 +110,9 @@ struct Iter {
   const T* __restrict__ KYc;  // m x Bp: K~y of the current y (LIN 2)
   const T* __restrict__ KYp;  // m x Bp: K~y of the previous y (read when thp != 0)
   T* KYo;                     // m x Bp: K~y stored by the row pass (LIN 1) / residual pass
+  T* TK;                      // n x Bp or nullptr: K~^T d stored by the final pass (MODE 2)
+  const int32_t* __restrict__ kyrow;  // with KYo: the residual pass stores row i at
+                                      // KYo + kyrow[i] * Bp (its full-row position)
   T thp;
   int lin;
   T* colpart;                 // [5][ncb][Bp]: primal, dual, stat, bound, finite
@@ -272,6 +275,7 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
       V yn;
       if (MODE == 2) {
         yn = y;
+        if (A.TK) vstore(A.TK + off, t);  // for the multiplier recovery (post.hpp)
       } else {
         V sv;
         if (A.Q) {
@@ -384,7 +388,8 @@ __global__ __launch_bounds__(kBlock) void k_res_pass(Iter<T> A) {
       for (int k = s0; k < s1; ++k)
         acc += row_coef(A.K, k, b0) * vload(A.Y + (size_t)A.K.ridx[k] * A.Bp + b0);
       const size_t off = (size_t)i * A.Bp + b0;
-      if (A.KYo) vstore(A.KYo + off, acc);  // K~y+ for the next row pass (lin)
+      if (A.KYo)  // K~y+ for the next row pass (lin), or for the multiplier recovery
+        vstore(A.KYo + (A.kyrow ? (size_t)A.kyrow[i] * A.Bp + b0 : off), acc);
       const V r = vload(A.R + off);
       const V d = vload(A.D + off);
       const V e = acc - r;

@@ -24,6 +24,12 @@ struct Post {
   const T* __restrict__ Q;
   const T* __restrict__ Cc;
   const T* __restrict__ tgt;     // n x Bp
+  // n x Bp or nullptr: K~^T d of the final diagnostics pass (k_col_pass MODE 2),
+  // the same sum K^T (d * scale) with the scale folded into the coefficients
+  const T* __restrict__ TK;
+  // with KY set: K~y of the final diagnostics pass, stored at each kept row's
+  // full-row position of DF (read there before the multiplier overwrites it)
+  bool KY;
   const T* __restrict__ Y;       // n x Bp
   const T* __restrict__ D;       // m x Bp (scaled duals)
   const T* __restrict__ RF;      // M x Bp (original rhs)
@@ -62,11 +68,15 @@ __global__ __launch_bounds__(kBlock) void k_post_rows(Post<T> P) {
     for (int c = 0; c < RPW; ++c) {
       const int i = (rb * 4 + wave) * RPW + c;
       if (i >= P.K.m) break;
-      const int s0 = P.K.rptr[i], s1 = P.K.rptr[i + 1];
-      V acc = vsplat<T>(zero);
-      for (int k = s0; k < s1; ++k)
-        acc += row_coef(P.K, k, b0) * vload(P.Y + (size_t)P.K.ridx[k] * P.Bp + b0);
       const int64_t row = P.kept[i];
+      V acc = vsplat<T>(zero);
+      if (P.KY) {  // K y = K~y / scale
+        acc = vload(P.DF + (size_t)row * P.Bp + b0) / post_scale(P, i, b0);
+      } else {
+        const int s0 = P.K.rptr[i], s1 = P.K.rptr[i + 1];
+        for (int k = s0; k < s1; ++k)
+          acc += row_coef(P.K, k, b0) * vload(P.Y + (size_t)P.K.ridx[k] * P.Bp + b0);
+      }
       const V d = vload(P.D + (size_t)i * P.Bp + b0);
       const V full = d * post_scale(P, i, b0);
       vstore(P.DF + (size_t)row * P.Bp + b0, full);
@@ -114,13 +124,17 @@ __global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
     for (int c = 0; c < CPW; ++c) {
       const int j = (cb * 4 + wave) * CPW + c;
       if (j >= P.K.n) break;
-      const int s0 = P.K.cptr[j], s1 = P.K.cptr[j + 1];
-      V tk = vsplat<T>(zero);
-      for (int k = s0; k < s1; ++k) {
-        const int i = P.K.cidx[k];
-        tk += col_coef(P.K, k, b0) * (vload(P.D + (size_t)i * P.Bp + b0) * post_scale(P, i, b0));
-      }
       const size_t off = (size_t)j * P.Bp + b0;
+      V tk = vsplat<T>(zero);
+      if (P.TK) {
+        tk = vload(P.TK + off);
+      } else {
+        const int s0 = P.K.cptr[j], s1 = P.K.cptr[j + 1];
+        for (int k = s0; k < s1; ++k) {
+          const int i = P.K.cidx[k];
+          tk += col_coef(P.K, k, b0) * (vload(P.D + (size_t)i * P.Bp + b0) * post_scale(P, i, b0));
+        }
+      }
       const V y = vload(P.Y + off);
       V lo, hi;
       if (P.shared_bounds) {
