@@ -23,6 +23,25 @@ constexpr int kBlock = 256;  // 4 wavefronts
 // and column section chunk counts; 0
 constexpr int kResWtab = 8;
 
+// Batch tile and first row / column block of a block of a (tiles x blocks)
+// grid.  Blocks are dealt to the 8 XCDs round-robin in launch order (x
+// fastest).  With more than 8 batch tiles (a multiple of 8), an XCD's
+// consecutive blocks walk one tile's row / column blocks before the next
+// tile's, so the few tiles an XCD holds at once keep their gathered vectors in
+// its L2; otherwise blockIdx.x is the tile (every tile stays on one XCD).
+__device__ __forceinline__ void tile_block(int64_t& tile, int& blk) {
+  const unsigned X = gridDim.x, Y = gridDim.y;
+  if (X > 8 && (X & 7u) == 0) {
+    const unsigned L = blockIdx.y * X + blockIdx.x;
+    const unsigned j = L >> 3;
+    tile = (int64_t)((L & 7u) + 8u * (j / Y));
+    blk = (int)(j % Y);
+  } else {
+    tile = blockIdx.x;
+    blk = (int)blockIdx.y;
+  }
+}
+
 template <typename T>
 struct Lane;
 template <>

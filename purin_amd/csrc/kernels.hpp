@@ -173,13 +173,16 @@ __global__ __launch_bounds__(kBlock) void k_row_pass(Iter<T> A) {
   constexpr int S = Lane<T>::S;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  int64_t tile;
+  int blk0;
+  tile_block(tile, blk0);
+  const int64_t b0 = (tile * kWave + lane) * S;
   V keep = vsplat<T>(T(0));
   if (MASKED) {
 #pragma unroll
     for (int s = 0; s < S; ++s) keep[s] = A.done[b0 + s] ? T(1) : T(0);
   }
-  for (int rb = blockIdx.y; rb * 4 < A.K.m; rb += gridDim.y) {
+  for (int rb = blk0; rb * 4 < A.K.m; rb += gridDim.y) {
     const int i = rb * 4 + wave;
     if (i >= A.K.m) continue;
     const size_t roff = (size_t)i * A.Bp + b0;
@@ -228,11 +231,14 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
   constexpr int S = Lane<T>::S;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  int64_t tile;
+  int blk0;
+  tile_block(tile, blk0);
+  const int64_t b0 = (tile * kWave + lane) * S;
   const T half = T(0.5), zero = T(0);
   // the per-sample schedule advances for every sample (done or not), once per
   // tile: wavefront 0 of the tile's first column block
-  if (MODE != 2 && A.sch_next && blockIdx.y == 0 && wave == 0) {
+  if (MODE != 2 && A.sch_next && blk0 == 0 && wave == 0) {
 #pragma unroll
     for (int s = 0; s < S; ++s)
       sched_next(A.gam ? A.gam[b0 + s] : T(1), A.tau_b[b0 + s], A.sig_b[b0 + s], A.sch_next,
@@ -245,7 +251,7 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
   }
   V primal = vsplat<T>(zero), dualo = vsplat<T>(zero), stat = vsplat<T>(zero),
     bnd = vsplat<T>(zero), fin = vsplat<T>(T(1));
-  for (int cb = blockIdx.y; cb * 4 * CPW < A.K.n; cb += gridDim.y) {
+  for (int cb = blk0; cb * 4 * CPW < A.K.n; cb += gridDim.y) {
     for (int c = 0; c < CPW; ++c) {
       const int j = (cb * 4 + wave) * CPW + c;
       if (j >= A.K.n) break;
@@ -375,9 +381,12 @@ __global__ __launch_bounds__(kBlock) void k_res_pass(Iter<T> A) {
   constexpr int S = Lane<T>::S;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  int64_t tile;
+  int blk0;
+  tile_block(tile, blk0);
+  const int64_t b0 = (tile * kWave + lane) * S;
   const T zero = T(0);
-  for (int rb = blockIdx.y; rb * 4 * RPW < A.K.m; rb += gridDim.y) {
+  for (int rb = blk0; rb * 4 * RPW < A.K.m; rb += gridDim.y) {
     V res = vsplat<T>(zero), rd = vsplat<T>(zero), fin = vsplat<T>(T(1));
     for (int c = 0; c < RPW; ++c) {
       const int i = (rb * 4 + wave) * RPW + c;

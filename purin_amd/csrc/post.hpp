@@ -53,6 +53,16 @@ __device__ __forceinline__ typename Lane<T>::V post_bcoef(const Post<T>& P, int 
   return P.bcoef_b ? vload(P.bcoef_b + (size_t)k * P.Bp + b0) : vsplat<T>(P.bcoef[k]);
 }
 
+// Right-hand side of bound row ``row`` for the S samples from b0: with shared
+// bounds the caller promises every sample's bound rows are equal and only
+// sample 0 is read (include/purin_cp.h, shared_bounds).
+template <typename T>
+__device__ __forceinline__ typename Lane<T>::V post_bound_rhs(const Post<T>& P, int64_t row,
+                                                              int64_t b0) {
+  const T* r = P.RF + (size_t)row * P.Bp;
+  return P.shared_bounds ? vsplat<T>(r[0]) : vload(r + b0);
+}
+
 // Kept rows: multiplier = d * scale (bounds.py:247), r = K y - rhs (285-289),
 // slack = max(-r, 0) for inequality rows (311).
 template <typename T, int RPW>
@@ -61,9 +71,12 @@ __global__ __launch_bounds__(kBlock) void k_post_rows(Post<T> P) {
   constexpr int S = Lane<T>::S;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  int64_t tile;
+  int blk0;
+  tile_block(tile, blk0);
+  const int64_t b0 = (tile * kWave + lane) * S;
   const T zero = T(0);
-  for (int rb = blockIdx.y; rb * 4 * RPW < P.K.m; rb += gridDim.y) {
+  for (int rb = blk0; rb * 4 * RPW < P.K.m; rb += gridDim.y) {
     V res = vsplat<T>(zero), fin = vsplat<T>(T(1));
     for (int c = 0; c < RPW; ++c) {
       const int i = (rb * 4 + wave) * RPW + c;
@@ -117,9 +130,12 @@ __global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
   constexpr int S = Lane<T>::S;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t b0 = ((int64_t)blockIdx.x * kWave + lane) * S;
+  int64_t tile;
+  int blk0;
+  tile_block(tile, blk0);
+  const int64_t b0 = (tile * kWave + lane) * S;
   const T zero = T(0), one = T(1);
-  for (int cb = blockIdx.y; cb * 4 * CPW < P.K.n; cb += gridDim.y) {
+  for (int cb = blk0; cb * 4 * CPW < P.K.n; cb += gridDim.y) {
     V res = vsplat<T>(zero), stat = vsplat<T>(zero), fin = vsplat<T>(one);
     for (int c = 0; c < CPW; ++c) {
       const int j = (cb * 4 + wave) * CPW + c;
@@ -160,7 +176,7 @@ __global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
       V lc = vsplat<T>(zero), uc = vsplat<T>(zero);
       for (int k = k0; k < k1; ++k) {
         const V cfv = post_bcoef(P, k, b0);
-        const V rr = vload(P.RF + (size_t)P.brow[k] * P.Bp + b0);
+        const V rr = post_bound_rhs(P, P.brow[k], b0);
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           const T cf = cfv[s];
@@ -173,7 +189,7 @@ __global__ __launch_bounds__(kBlock) void k_post_cols(Post<T> P) {
       for (int k = k0; k < k1; ++k) {
         const V cfv = post_bcoef(P, k, b0);
         const int64_t row = P.brow[k];
-        const V rr = vload(P.RF + (size_t)row * P.Bp + b0);
+        const V rr = post_bound_rhs(P, row, b0);
         V bd, sl;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
