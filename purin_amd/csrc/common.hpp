@@ -20,7 +20,8 @@ constexpr int kBlock = 256;  // 4 wavefronts
 // ints per wavefront of the resident kernels' wave table: first chunk; the
 // chunk counts of the row slots and of the column slots (4 x u8 each); the
 // slots' entries in their last chunk, rows and columns (4 x u8 each); the row
-// and column section chunk counts; 0
+// and column section chunk counts; flags: bit 0 (1) when the first row slot
+// spans two or more chunks, bit 1 (2) when the first column slot does
 constexpr int kResWtab = 8;
 
 // Batch tile and first row / column block of a block of a (tiles x blocks)

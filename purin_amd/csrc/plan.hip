@@ -835,6 +835,9 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         wt[0] = (int32_t)first;
         wt[5] = (int32_t)rch;
         wt[6] = (int32_t)cch;
+        // a pass whose first slot spans two chunks has both of them loaded
+        // before the barrier that opens it (k_resident)
+        wt[7] = (mr > 0 && rw[0] > 4 ? 1 : 0) | (mc > 0 && cw[0] > 4 ? 2 : 0);
         iter_chunks += rch + cch;
       }
       if (too_wide || nchunks >= (int64_t)1 << 30) p->res_ok = false;

@@ -88,7 +88,7 @@ struct purin_cp_plan {
   int32_t* res_rowent = nullptr;     // Kr: LDS entry (16-byte units) of each row slot's d, or -1
   int32_t* res_colent = nullptr;     // Kc: LDS entry of each column slot's ybar / y, or -1
   unsigned char* res_stream = nullptr;  // per-wavefront chunk streams of the matrix
-  int32_t* res_wtab = nullptr;       // [16][kResWtab] first chunk, slot widths, section chunks
+  int32_t* res_wtab = nullptr;       // [16][kResWtab] first chunk, slot widths, section chunks, flags
   int64_t res_stream_bytes = 0;
   int64_t res_iter_bytes = 0;        // matrix-stream bytes a workgroup reads per iteration
   int64_t res_iter_bytes_e = 0;      // the same for the early-stop kernel

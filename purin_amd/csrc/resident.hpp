@@ -227,18 +227,30 @@ __device__ __forceinline__ void consume_last(const Chunk<T>& c, int e, V& acc, V
 // by a loop whose every pass issues the same loads (the next chunk into b1,
 // then the one after into b0), so the compiler waits only for the chunk being
 // consumed (the later chunk stays in flight); the last one or two chunks are
-// taken after the loop, the last one whole or split.  Summation order: the
-// slot's entries in stream order, its head first.  SPLIT false: the pass has
-// one slot, which owns every chunk it walks (no head, no split).
+// taken after the loop, the last one whole or split.  ``pro`` (the first slot
+// of a pass, spanning two or more chunks): b1 holds (or is loading) the
+// slot's second chunk as well, loaded before the barrier that opened the pass
+// so that the stream stays busy while the wavefronts wait there; the first
+// two chunks are taken before the loop.  Summation order: the slot's entries
+// in stream order, its head first.  SPLIT false: the pass has one slot, which
+// owns every chunk it walks (no head, no split).
 template <typename T, typename V, bool SPLIT>
 __device__ __forceinline__ V slot_sum(int nch, int e, V& carry, Chunk<T>& b0, Chunk<T>& b1,
                                       uint32_t& pos, const unsigned char* __restrict__ stream,
-                                      uint32_t lane16) {
+                                      uint32_t lane16, bool pro) {
   constexpr uint64_t CB = res_chunk_bytes<T>();
   if constexpr (!SPLIT) {
     // one slot per pass: it owns all its chunks (the pass's end is padded)
     V acc = V(T(0));
     int k = 0;
+    if (pro) {  // nch >= 2
+      consume_chunk(b0, acc);
+      load_chunk(b0, stream, pos * CB, lane16);
+      ++pos;
+      __builtin_amdgcn_sched_barrier(0);
+      consume_chunk(b1, acc);
+      k = 2;
+    }
     for (; k + 1 < nch; k += 2) {
       load_chunk(b1, stream, pos * CB, lane16);
       ++pos;
@@ -259,6 +271,18 @@ __device__ __forceinline__ V slot_sum(int nch, int e, V& carry, Chunk<T>& b0, Ch
   V acc = carry;
   carry = V(T(0));
   int k = 0;
+  if (pro) {  // nch >= 2, no head (the pass's first slot)
+    consume_chunk(b0, acc);
+    load_chunk(b0, stream, pos * CB, lane16);
+    ++pos;
+    __builtin_amdgcn_sched_barrier(0);
+    if (nch == 2) {
+      consume_last(b1, e, acc, carry);
+      return acc;
+    }
+    consume_chunk(b1, acc);
+    k = 2;
+  }
   for (; k + 2 < nch; k += 2) {
     load_chunk(b1, stream, pos * CB, lane16);
     ++pos;
@@ -324,6 +348,9 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
   const uint32_t ccnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 2]);
   const uint32_t rlast = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 3]);
   const uint32_t clast = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 4]);
+  // bit 0 / bit 1: the first row / column slot spans two or more chunks, so
+  // the pass's first two chunks are loaded before the barrier that opens it
+  const uint32_t pro = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 7]);
 
   const V* Ts = reinterpret_cast<const V*>(A.Ts) + tile * (int64_t)A.Kc;
   const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)A.Kr;
@@ -371,13 +398,14 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
   constexpr uint32_t CB = res_chunk_bytes<T>();
   Chunk<T> b0, b1;
   load_chunk(b0, A.stream, (uint64_t)first * CB, lane16);
+  if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16);
 
   for (int64_t it = 0; it < A.iters; ++it) {
     // wave-uniform schedule scalars: scalar loads through the constant address space
     const __attribute__((address_space(4))) T* sc =
         (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
     const T sigma = sc[0], a = sc[1], delta = sc[2], theta = sc[3];
-    uint32_t pos = first + 1;
+    uint32_t pos = first + 1 + (pro & 1u);
     V carry = vzero;  // the head of the next slot (a chunk shared by two slots)
     // the slot tables, opaque to the loop so that their fields are decoded at
     // each slot rather than held decoded in SGPRs across the iteration
@@ -388,13 +416,18 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
     for (int r = 0; r < SLR; ++r) {
       const V dold = lds_read<V>(soff_r[r]);
       const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
-                                              b0, b1, pos, A.stream, lane16);
+                                              b0, b1, pos, A.stream, lane16,
+                                              r == 0 && (pro & 1u));
       V p = dold + sigma * (acc - rr[r]);
       if (ineq & (1u << r)) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
       }
       lds_write<V>(soff_r[r], p);
+    }
+    if (pro & 2u) {  // the column pass's second chunk (its first is in b0)
+      load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16);
+      ++pos;
     }
     __syncthreads();
     // ---- column pass (reads Gd, writes Gy) --------------------------------------
@@ -430,7 +463,8 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
         tgc = tb[tile * (int64_t)A.Kc + c * NT + t];
       }
       const V tt = slot_sum<T, V, (SLC > 1)>(slot_field(cc, c), slot_field(cl, c), carry,
-                                             b0, b1, pos, A.stream, lane16);
+                                             b0, b1, pos, A.stream, lane16,
+                                             c == 0 && (pro & 2u));
       const V sv = a * y[c] - delta * tt + delta * tgc;
       V yn;
       if (nanb & (1u << c)) {  // a NaN bound on this lane: the exact NaN-propagating clip
@@ -443,6 +477,8 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
       lds_write<V>(soff_c[c], yn + theta * (yn - y[c]));
       y[c] = yn;
     }
+    // the next row pass's second chunk (b0 holds the copy of its first)
+    if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16);
     __syncthreads();
   }
   // ---- hand the state to the batch-minor layout ---------------------------------
@@ -644,7 +680,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     for (int r = 0; r < SLR; ++r) {
       const V rr = Rs[r * NT + t];
       ky[r] = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
-                                        b0, b1, pos, A.stream, lane16);
+                                        b0, b1, pos, A.stream, lane16, false);
       V p = lds_read<V>(soff_r[r]) + sigma0 * (ky[r] - rr);
       if (ineq & (1u << r)) {
 #pragma unroll
@@ -689,7 +725,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       asm volatile("" : "+s"(tb));
       const V tg = ((GV)tb)[tile * (int64_t)A.Kc + c * NT + t];
       const V tt = slot_sum<T, V, (SLC > 1)>(slot_field(cc, c), slot_field(cl, c), carry,
-                                             b0, b1, pos, A.stream, lane16);
+                                             b0, b1, pos, A.stream, lane16, false);
       asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
       if (SB && uni) {
@@ -772,7 +808,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     for (int r = 0; r < SLR; ++r) {
       const V rr = rb[r * NT + t];
       const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
-                                              b0, b1, pos, A.stream, lane16);
+                                              b0, b1, pos, A.stream, lane16, false);
       const V d = lds_read<V>(soff_r[r]);
       if (rvalid & (1u << r)) {  // kernels.py:158-166
         // e = K y+ - r; equality rows |e|, inequality rows max(e, 0): max(e, w e)
