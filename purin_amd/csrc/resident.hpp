@@ -612,6 +612,9 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const uint32_t ccnt = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 2]);
   const uint32_t rlast = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 3]);
   const uint32_t clast = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 4]);
+  // bit 0 / bit 1: the first row / column slot spans two or more chunks, so
+  // a sweep's first two chunks are loaded before the barrier that opens it
+  const uint32_t pro = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave + 7]);
 
   const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)A.Kr;
   const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)A.Kr;
@@ -668,7 +671,8 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   constexpr uint32_t CB = res_chunk_bytes<T>();
   Chunk<T> b0, b1;
   load_chunk(b0, A.stream, (uint64_t)first * CB, lane16);
-  uint32_t pos = first + 1;
+  if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16);
+  uint32_t pos = first + 1 + (pro & 1u);
   typedef const __attribute__((address_space(1))) V* GV;
   // K y0 (= K ybar0) by one row sweep, and the first candidate duals; b0 then
   // holds the first column chunk
@@ -680,13 +684,17 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     for (int r = 0; r < SLR; ++r) {
       const V rr = Rs[r * NT + t];
       ky[r] = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
-                                        b0, b1, pos, A.stream, lane16, false);
+                                        b0, b1, pos, A.stream, lane16, r == 0 && (pro & 1u));
       V p = lds_read<V>(soff_r[r]) + sigma0 * (ky[r] - rr);
       if (ineq & (1u << r)) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
       }
       dn[r] = p;
+    }
+    if (pro & 2u) {  // the column pass's second chunk (its first is in b0)
+      load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16);
+      ++pos;
     }
   }
 
@@ -725,7 +733,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       asm volatile("" : "+s"(tb));
       const V tg = ((GV)tb)[tile * (int64_t)A.Kc + c * NT + t];
       const V tt = slot_sum<T, V, (SLC > 1)>(slot_field(cc, c), slot_field(cl, c), carry,
-                                             b0, b1, pos, A.stream, lane16, false);
+                                             b0, b1, pos, A.stream, lane16, c == 0 && (pro & 2u));
       asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
       if (SB && uni) {
@@ -791,9 +799,12 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     for (int s = 0; s < BT; ++s) qp[s] = row16_combine(qp[s], OpAdd());
     if (red_lead) lds_write<V>(red_at, qp);
     // qd and qc stay in registers: the sweep folds its own terms into them
+    // b0 holds the copy of the stream's first (row) chunk; its second chunk
+    // goes into b1 before the barrier when the first row slot spans two
+    if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16);
     __syncthreads();
     // ---- residual sweep (gathers Gy = y+; own Gd entries = d+) ---------------------
-    pos = first + 1;  // b0 holds the copy of the stream's first (row) chunk
+    pos = first + 1 + (pro & 1u);
     // the next iteration's sigma (the candidates are formed only when it runs)
     const bool more = it + 1 < A.iters;
     const T sigma_n = more ? A.sched[4 * (it + 1)] : zero;
@@ -808,7 +819,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     for (int r = 0; r < SLR; ++r) {
       const V rr = rb[r * NT + t];
       const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
-                                              b0, b1, pos, A.stream, lane16, false);
+                                              b0, b1, pos, A.stream, lane16, r == 0 && (pro & 1u));
       const V d = lds_read<V>(soff_r[r]);
       if (rvalid & (1u << r)) {  // kernels.py:158-166
         // e = K y+ - r; equality rows |e|, inequality rows max(e, 0): max(e, w e)
@@ -831,6 +842,10 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         dn[r] = p;
       }
       ky[r] = acc;
+    }
+    if (pro & 2u) {  // the next column pass's second chunk (its first is in b0)
+      load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16);
+      ++pos;
     }
 #pragma unroll
     for (int s = 0; s < BT; ++s) qr[s] = row16_combine(qr[s], OpAdd());
@@ -878,8 +893,9 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       }
       act = (uint32_t)__builtin_amdgcn_readfirstlane((int)(act & ~accept));
     }
-    // b0 holds the first column chunk again and pos follows it; the partials
-    // are rewritten only after the next barrier
+    // b0 (and b1 when the first column slot spans two chunks) hold the first
+    // column chunks again and pos follows them; the partials are rewritten
+    // only after the next barrier
   }
   // ---- hand the state to the batch-minor layout ---------------------------------
 #pragma unroll
