@@ -393,8 +393,9 @@ def run_mode(args, torch):
         # pass writes no ybar (n)
         bytes_row += B * ws * 2 * m
         bytes_col -= B * ws * n
-    dominant = "k_col_pass" if col_ms >= row_ms else "k_row_pass"
-    dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == "k_col_pass" else (bytes_row, row_ms)
+    col_kernel = "k_col_pass_q" if tm["narrow_columns"] else "k_col_pass"
+    dominant = col_kernel if col_ms >= row_ms else "k_row_pass"
+    dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == col_kernel else (bytes_row, row_ms)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
     bytes_iter = B * ws * ((7 + extra_n) * n + 3 * m + 2 * coef_nnz)
     iter_ms = tm["loop_ms"] / it
@@ -553,8 +554,11 @@ def main():
         row_ms = col_ms = None
     else:
         row_ms, col_ms = tm["row_ms"] / iters, tm["col_ms"] / iters
-        dominant = "k_col_pass" if col_ms >= row_ms else "k_row_pass"
-        dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == "k_col_pass" else (bytes_row, row_ms)
+        # a quarter wavefront per column (k_col_pass_q) where the wide tile's
+        # gathered slice of d+ exceeds an XCD's L2
+        col_kernel = "k_col_pass_q" if tm["narrow_columns"] else "k_col_pass"
+        dominant = col_kernel if col_ms >= row_ms else "k_row_pass"
+        dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == col_kernel else (bytes_row, row_ms)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
     traffic = traffic_from_profiles(args.config, dominant, B, w.iterations)
     if tm["resident"]:
@@ -674,6 +678,7 @@ def main():
             "cp_iterations_per_s": w.iterations * 1e3 / ms_per_step,
             "resident_kernel": bool(tm["resident"]),
             "linear_kybar": bool(tm["linear_kybar"]),
+            "narrow_columns": bool(tm["narrow_columns"]),
             "streaming_passes_ms_per_step": streaming_ms,
             "row_pass_ms": row_ms,
             "col_pass_ms": col_ms,

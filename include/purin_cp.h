@@ -320,6 +320,9 @@ typedef struct {
   int32_t resident;     /* 1: the iterations ran in the resident kernel (one launch) */
   int32_t linear_kybar; /* 1: the streaming passes formed K ybar = (1 + theta) K y -
                            theta K y_prev instead of storing ybar (n > 2 m) */
+  int32_t narrow_columns; /* 1: the fixed-iteration column pass took a quarter
+                             wavefront per column (batch tiles of 16 lanes: the
+                             gathered d+ slice of a tile fits an XCD's L2) */
 } purin_cp_timing;
 
 int purin_cp_last_timing(const purin_cp_plan* plan, purin_cp_timing* timing);

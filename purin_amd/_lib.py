@@ -96,6 +96,7 @@ class Timing(C.Structure):
         ("loop_ms", C.c_double),
         ("resident", C.c_int32),
         ("linear_kybar", C.c_int32),
+        ("narrow_columns", C.c_int32),
     ]
 
 

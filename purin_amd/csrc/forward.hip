@@ -492,15 +492,21 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   const dim3 grow = tile_grid(Bp, TS, (m + 3) / 4);
   const dim3 gcol = tile_grid(Bp, TS, (n + 3) / 4);
   const dim3 gcolE = tile_grid(Bp, TS, L.ncb);
+  // The fixed-iteration column pass takes a quarter wavefront per column
+  // (k_col_pass_q: batch tiles of TS / 4 samples) where the slice of d+ a
+  // wide tile gathers exceeds an XCD's L2 and the narrow tile's fits with
+  // room for the streams, and the narrow tiles come in multiples of the 8 XCDs
+  // (config 3: 10.2 MB -> 2.6 MB per tile).  The plain projection only.  Its
+  // streams stay cached (no nontemporal hint): the row pass that follows
+  // gathers the y it stores (config 3: column pass 59.2 us with the hint,
+  // 51.0 us without; row pass 44.8 -> 42.0 us).
+  const bool col_q = !A.Q && !A.sch_next && m > 0 &&
+                     (double)m * TS * sizeof(T) > kL2Bytes &&
+                     (double)m * (TS / 4) * sizeof(T) <= 0.625 * kL2Bytes &&
+                     (Bp / (TS / 4)) % 8 == 0;
+  const dim3 gcolq = tile_grid(Bp, TS / 4, (n + 15) / 16);
   const dim3 gres = tile_grid(Bp, TS, std::max(L.nrb, 1));
   const dim3 gdec((unsigned)(Bp / 64));  // k_decide: 64 samples per block
-  // The fixed-iteration column pass streams its per-column vectors past the
-  // caches when one iteration's per-sample vectors (y, ybar, and yhat or q
-  // and c; d, r) exceed the 256 MB MALL, so that the gathered rows of d+ stay
-  // cached (config 3: 287 MB, 4.6 % faster; where they fit, the hint loses
-  // the MALL hits of the next iteration's reads instead).
-  const bool col_nt =
-      (double)((A.Q ? 4 : 3) * (int64_t)n + 2 * (int64_t)m) * (double)Bp * sizeof(T) > kMallBytes;
   // K ybar by linearity (kernels.hpp, Iter::lin) where it moves fewer bytes:
   // with n > 2m the ybar stream the column pass writes (n per sample) outweighs
   // the two m-vectors of K y the row pass then reads and writes (fixed
@@ -509,6 +515,15 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   // batch), not for the dense adapter's unfrozen loop.  The two K y buffers
   // take the ybar buffer's place (n x Bp >= 2 m x Bp).
   const bool lin = m > 0 && (int64_t)n > 2 * (int64_t)m && !A.th_b && !A.nofreeze;
+  // The fixed-iteration (wide) column pass streams its per-column vectors past
+  // the caches when one iteration's per-sample vectors (y, ybar, and yhat or q
+  // and c; d, r) exceed the 256 MB MALL and it stores ybar, so that the
+  // gathered rows of d+ stay cached (measured at config 3's shape with ybar
+  // streamed: 4.6 % faster).  With K ybar from K y the row pass gathers the y
+  // the column pass stores, and caching it wins (config 3, wide tiles: 822 ->
+  // 869 projections/s without the hint).
+  const bool col_nt = !lin &&
+      (double)((A.Q ? 4 : 3) * (int64_t)n + 2 * (int64_t)m) * (double)Bp * sizeof(T) > kMallBytes;
   T* kyb[2] = {A.YB, A.YB + (size_t)m * Bp};
   T theta_prev = T(0);
   // optional event timing: events[3k] before the row pass, [3k+1] between the
@@ -546,7 +561,9 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
         k_row_pass<T, false><<<grow, kBlock, 0, st>>>(A);
       }
       if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 1], st));
-      if (col_nt)
+      if (col_q)
+        k_col_pass_q<T, false><<<gcolq, kBlock, 0, st>>>(A);
+      else if (col_nt)
         k_col_pass<T, 0, kRowsPerWaveFixed, true><<<gcol, kBlock, 0, st>>>(A);
       else
         k_col_pass<T, 0, kRowsPerWaveFixed><<<gcol, kBlock, 0, st>>>(A);
@@ -627,6 +644,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     if (it > 0) PURIN_HIP(hipEventElapsedTime(&total, ev[0], ev[3 * (it - 1) + 2]));
     t.loop_ms = total;
     t.linear_kybar = lin ? 1 : 0;
+    t.narrow_columns = col_q && !early ? 1 : 0;
     p->timing = t;
     for (auto& e : ev) (void)hipEventDestroy(e);
     for (auto& e : evd) (void)hipEventDestroy(e);

@@ -371,6 +371,62 @@ __global__ __launch_bounds__(kBlock) void k_col_pass(Iter<T> A) {
 }
 
 // ---------------------------------------------------------------------------
+// Column pass of the fixed-iteration loop with a quarter wavefront per column:
+// a batch tile is 16 lanes x S samples (32 in fp64), so the slice of d+ that a
+// tile's columns gather, m x 16 S values, is a quarter of k_col_pass's.  With
+// 8 such tiles (or a multiple of 8), each XCD walks one tile's columns at a
+// time (tile_block), and where the wide tile's slice exceeds an XCD's 4 MB L2
+// while the narrow one fits, the gathers hit L2 instead of re-reading d+ from
+// beyond it.  The streams (y, yhat, bounds, y and ybar stores) are 256-byte
+// runs per quarter wavefront.  Same arithmetic, in the same order, as
+// k_col_pass<MODE 0> (bit-identical results); the plain projection only (no
+// QP terms, no per-sample schedule advance).
+// ---------------------------------------------------------------------------
+template <typename T, bool NT, int P = 16>
+__global__ __launch_bounds__(kBlock) void k_col_pass_q(Iter<T> A) {
+  if (A.stop && *A.stop >= A.nstop) return;
+  using V = typename Lane<T>::V;
+  constexpr int S = Lane<T>::S;
+  constexpr int CW = kWave / P;  // columns per wavefront
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int64_t tile;
+  int blk0;
+  tile_block(tile, blk0);
+  const int64_t b0 = (tile * P + lane % P) * S;
+  const int q = lane / P;
+  for (int cb = blk0; cb * 4 * CW < A.K.n; cb += gridDim.y) {
+    const int j = (cb * 4 + wave) * CW + q;
+    if (j >= A.K.n) break;
+    const int s0 = A.K.cptr[j], s1 = A.K.cptr[j + 1];
+    V t = vsplat<T>(T(0));
+    for (int k = s0; k < s1; ++k) {
+      const V dd = vload(A.D + (size_t)A.K.cidx[k] * A.Bp + b0);
+      t += col_coef(A.K, k, b0) * dd;
+    }
+    const size_t off = (size_t)j * A.Bp + b0;
+    const V y = vload_s<NT>(A.Y + off);
+    const V tg = vload_s<NT>(A.tgt + off);
+    V lo, hi;
+    if (A.shared_bounds) {
+      lo = vsplat<T>(A.LO[j]);
+      hi = vsplat<T>(A.HI[j]);
+    } else {
+      lo = vload_s<NT>(A.LO + off);
+      hi = vload_s<NT>(A.HI + off);
+    }
+    const V aj = step_a(A, j, b0), dj = step_delta(A, j, b0);
+    const V sv = aj * y - dj * t + dj * tg;
+    V yn;
+#pragma unroll
+    for (int s = 0; s < S; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
+    const V yb = yn + step_theta(A, b0) * (yn - y);
+    vstore_s<NT>(A.Y + off, yn);
+    if (!A.lin) vstore_s<NT>(A.YB + off, yb);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // residual pass: per kept row r = K y - rhs -> |r| (eq) / max(r,0) (ineq);
 // r.d and finite(d) for the dual objective and the finiteness test.
 // ---------------------------------------------------------------------------

@@ -17,6 +17,7 @@ constexpr int64_t kSavedMagic = 0x5055524e43503031LL;  // "PURNCP01"
 constexpr int kResThreads = 1024;   // threads of a resident workgroup
 constexpr int kResMaxSlots = 4;     // rows / columns per thread (n, m <= 4096)
 constexpr double kMallBytes = 256.0 * 1024 * 1024;  // MI355X Infinity Cache (MALL)
+constexpr double kL2Bytes = 4.0 * 1024 * 1024;      // L2 of one MI355X XCD
 constexpr int kPinnedBytes = 4096;  // host-pinned flag words: counters and per-step counts
 // Iterations of the step schedule built with the plan (the schedule of k
 // iterations is a prefix of any longer one, so calls up to this count read it

@@ -237,3 +237,42 @@ def test_full_size_default_stopping_rule_matches_oracle_fixture():
     res = to_np(out.residual)[s]
     assert np.all(np.abs(res - g["residual"]) <= 1e-3 * np.abs(g["residual"]))
     assert np.all(status == 1) and int(to_np(out.eligible).sum()) == 0
+
+
+@pytest.mark.parametrize("edges,dtype", [(12000, np.float64), (9000, np.float64),
+                                         (12000, np.float32)])
+def test_narrow_column_tiles(edges, dtype):
+    """Network flow with 5000 nodes: a wide batch tile's slice of d+ (5000 x 128
+    fp64 or x 256 fp32 samples, 5.1 MB) exceeds an XCD's L2, so with 8 narrow
+    tiles (B = 256 fp64 / 512 fp32) the fixed-iteration column pass takes a
+    quarter wavefront per column.  Checked against the C loop on samples from
+    both ends of the batch, and bit-identical to the wide column pass, which a
+    batch of 64 / 128 samples runs (samples are independent and both passes
+    sum in the same order).  9000 edges (n < 2m) keeps ybar streamed; 12000
+    forms K ybar from K y."""
+    torch = require_gpu()
+    B = 256 if dtype == np.float64 else 512
+    w = workloads.config3(batch=B, nodes=5000, edges=edges)
+    w.iterations = 200
+    w.dtype = np.dtype(dtype)
+    w.target = w.target.astype(dtype)
+    p, values, root = full_plan(w)
+    rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+    for shared in (True, False):
+        kw = dict(max_iterations=w.iterations, early_stop=False, shared_bounds=shared)
+        print(f"edges={edges} dtype={np.dtype(dtype).name} B={B} shared={shared}", flush=True)
+        out = p.project(w.target, rhs, timing=True, **kw)
+        t = p.last_timing()
+        assert t["resident"] == 0 and t["narrow_columns"] == 1
+        assert t["linear_kybar"] == (1 if edges > 2 * 5000 else 0)
+        y = to_np(out.y)
+        bar = 1e-10 if dtype == np.float64 else 1e-4
+        want = checker_y(w, values, root, PICK)
+        assert rel_err(y[PICK] * root.astype(dtype), want) <= bar
+        k = B // 4
+        wide = p.project(w.target[:k], rhs[:k], timing=True, **kw)
+        assert p.last_timing()["narrow_columns"] == 0
+        np.testing.assert_array_equal(to_np(wide.y), y[:k])
+        np.testing.assert_array_equal(to_np(wide.multipliers), to_np(out.multipliers)[:k])
+        del out, wide
+    torch.cuda.empty_cache()
