@@ -261,3 +261,40 @@ def test_values_saved_state_and_option_errors():
     with pytest.raises(_lib.PurinError, match="shared"):
         plan.project(x, np.array([[1.0]]), values=vals, shared_bounds=True)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("mode", ["scalar", "diagonal"])
+def test_values_narrow_column_tiles(mode):
+    """Per-sample coefficients on a network-flow problem (5000 nodes, 12000
+    edges) whose wide column tile gathers more of d+ than an XCD's L2 holds:
+    with B = 256 the fixed-iteration column pass takes a quarter wavefront per
+    column, reading the per-sample coefficients and steps (scalar or diagonal)
+    per lane.  The first 64 samples alone, a batch that runs the wide pass,
+    give bit-identical results, and samples from both ends match the oracle."""
+    require_gpu()
+    B, k = 256, 64
+    w = workloads.config3(batch=B, nodes=5000, edges=12000)
+    canon = canonical_from_workload(w)
+    support, mask, shared = canon.ell(np.float64)
+    rng = np.random.default_rng(12)
+    csr = shared[mask]
+    vals = csr[None] * (1 + 0.3 * rng.uniform(-1, 1, (B, csr.size)))
+    target = np.ascontiguousarray(w.target, np.float64)
+    rhs = np.tile(w.rhs, (B, 1))
+    kw = dict(diagonal_preconditioning=True) if mode == "diagonal" else {}
+    plan = plan_for(canon, dtype=np.float64, **kw)
+    opts = dict(max_iterations=120, early_stop=False)
+    got = plan.project(target, rhs, values=vals, timing=True, **opts)
+    t = plan.last_timing()
+    assert t["resident"] == 0 and t["narrow_columns"] == 1
+    wide = plan.project(target[:k], rhs[:k], values=np.ascontiguousarray(vals[:k]), timing=True,
+                        **opts)
+    assert plan.last_timing()["narrow_columns"] == 0
+    np.testing.assert_array_equal(to_np(wide.y), to_np(got.y)[:k])
+    np.testing.assert_array_equal(to_np(wide.multipliers), to_np(got.multipliers)[:k])
+    pick = [0, B - 1]
+    ell = np.zeros((len(pick),) + shared.shape)
+    ell[:, mask] = vals[pick]
+    cfg = op.Config(max_iterations=120, early_stop=False, **kw)
+    want = op.solve(canon, target[pick], rhs[pick], cfg, dtype=np.float64, values=ell)
+    assert rel_err(to_np(got.y)[pick], want.y) <= TOL[np.float64]
