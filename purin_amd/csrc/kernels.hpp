@@ -615,20 +615,38 @@ __global__ __launch_bounds__(kBlock) void k_to_minor(const T* __restrict__ src, 
   __shared__ T tile[64][65];
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   const int64_t c0 = (int64_t)blockIdx.x * 64, b0 = (int64_t)blockIdx.y * 64;
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t b = b0 + r, c = c0 + tx;
-    T v = T(0);
-    if (b < B && c < C) {
-      v = src[b * ld + c];
-      if (mode == 1) v = v * colmul[c];
-      else if (mode == 2) v = v / colmul[c];
+  const int64_t c = c0 + tx;
+  // the thread's 16 loads are issued together (unrolled; unguarded in a tile
+  // inside the batch and the columns)
+  T v[16];
+  if (b0 + 64 <= B && c0 + 64 <= C) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = src[(b0 + ty + 4 * k) * ld + c];
+    if (mode != 0) {
+      const T f = colmul[c];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = mode == 1 ? v[k] * f : v[k] / f;
     }
-    tile[r][tx] = v;
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int64_t b = b0 + ty + 4 * k;
+      v[k] = T(0);
+      if (b < B && c < C) {
+        v[k] = src[b * ld + c];
+        if (mode == 1) v[k] = v[k] * colmul[c];
+        else if (mode == 2) v[k] = v[k] / colmul[c];
+      }
+    }
   }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) tile[ty + 4 * k][tx] = v[k];
   __syncthreads();
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t c = c0 + r, b = b0 + tx;
-    if (c < C && b < Bp) dst[c * Bp + b] = tile[tx][r];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int r = ty + 4 * k;
+    const int64_t cc = c0 + r, b = b0 + tx;
+    if (cc < C && b < Bp) dst[cc * Bp + b] = tile[tx][r];
   }
 }
 
@@ -641,20 +659,39 @@ __global__ __launch_bounds__(kBlock) void k_to_major(const T* __restrict__ src, 
   __shared__ T tile[64][65];
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   const int64_t c0 = (int64_t)blockIdx.x * 64, b0 = (int64_t)blockIdx.y * 64;
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t c = c0 + r, b = b0 + tx;
-    T v = T(0);
-    if (c < C && b < B) {
-      v = src[c * Bp + b];
-      if (mode == 1) v = v * colmul[c];
-      else if (mode == 2) v = v / colmul[c];
+  const int64_t b = b0 + tx;
+  // the thread's 16 loads are issued together (unrolled; unguarded in a tile
+  // inside the batch and the columns)
+  T v[16];
+  if (b0 + 64 <= B && c0 + 64 <= C) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = src[(c0 + ty + 4 * k) * Bp + b];
+    if (mode != 0) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const T f = colmul[c0 + ty + 4 * k];
+        v[k] = mode == 1 ? v[k] * f : v[k] / f;
+      }
     }
-    tile[r][tx] = v;
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int64_t c = c0 + ty + 4 * k;
+      v[k] = T(0);
+      if (c < C && b < B) {
+        v[k] = src[c * Bp + b];
+        if (mode == 1) v[k] = v[k] * colmul[c];
+        else if (mode == 2) v[k] = v[k] / colmul[c];
+      }
+    }
   }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) tile[ty + 4 * k][tx] = v[k];
   __syncthreads();
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t b = b0 + r, c = c0 + tx;
-    if (b < B && c < C) dst[b * ld + c] = tile[tx][r];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t bb = b0 + ty + 4 * k, c = c0 + tx;
+    if (bb < B && c < C) dst[bb * ld + c] = tile[tx][ty + 4 * k];
   }
 }
 
