@@ -325,16 +325,19 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   T* D0s = (T*)(ws + L.RD0);
   T* Ls = (T*)(ws + L.RLs);
   T* Hs = (T*)(ws + L.RHs);
-  const unsigned gb = 2048;
-  k_res_gather<T, BT><<<gb, 256, 0, st>>>((const T*)(sv + L.Tt), Bp, p->res_colmap, Kc, tiles, Ts);
-  k_res_gather<T, BT><<<gb, 256, 0, st>>>((const T*)(sv + L.R), Bp, p->res_rowmap, Kr, tiles, Rs);
-  k_res_gather<T, BT><<<gb, 256, 0, st>>>((const T*)(sv + L.D), Bp, p->res_rowmap, Kr, tiles, D0s);
+  // slot-ordered copies per tile (k_res_gather: 64 slots x 64 samples per block;
+  // tiles and the slot counts are multiples of 64)
+  const dim3 gc((unsigned)(tiles / (64 / BT)), (unsigned)(Kc / 64));
+  const dim3 gr((unsigned)(tiles / (64 / BT)), (unsigned)(Kr / 64));
+  k_res_gather<T, BT><<<gc, 256, 0, st>>>((const T*)(sv + L.Tt), Bp, p->res_colmap, Kc, tiles, Ts);
+  k_res_gather<T, BT><<<gr, 256, 0, st>>>((const T*)(sv + L.R), Bp, p->res_rowmap, Kr, tiles, Rs);
+  k_res_gather<T, BT><<<gr, 256, 0, st>>>((const T*)(sv + L.D), Bp, p->res_rowmap, Kr, tiles, D0s);
   if (o.shared_bounds) {
     k_res_gather_shared<T><<<(Kc + 255) / 256, 256, 0, st>>>((const T*)(sv + L.LO), p->res_colmap, Kc, Ls);
     k_res_gather_shared<T><<<(Kc + 255) / 256, 256, 0, st>>>((const T*)(sv + L.HI), p->res_colmap, Kc, Hs);
   } else {
-    k_res_gather<T, BT><<<gb, 256, 0, st>>>((const T*)(sv + L.LO), Bp, p->res_colmap, Kc, tiles, Ls);
-    k_res_gather<T, BT><<<gb, 256, 0, st>>>((const T*)(sv + L.HI), Bp, p->res_colmap, Kc, tiles, Hs);
+    k_res_gather<T, BT><<<gc, 256, 0, st>>>((const T*)(sv + L.LO), Bp, p->res_colmap, Kc, tiles, Ls);
+    k_res_gather<T, BT><<<gc, 256, 0, st>>>((const T*)(sv + L.HI), Bp, p->res_colmap, Kc, tiles, Hs);
   }
   R.Ts = Ts;
   R.Rs = Rs;

@@ -925,19 +925,37 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   }
 }
 
-// dst[(tile*K + k)*BT + s] = src[map[k]*Bp + tile*BT + s] (0 for empty slots)
+// dst[(tile*K + k)*BT + s] = src[map[k]*Bp + tile*BT + s] (0 for empty slots).
+// A block moves 64 slots x 64 samples (64 / BT tiles) through LDS: it reads
+// each slot's 64 samples as one contiguous run of the batch-minor source and
+// writes each tile's 64 slots x BT values as one contiguous run.  Launch:
+// grid (tiles / (64 / BT), K / 64), 256 threads; tiles and K are multiples of
+// 64 (the padded batch and the slot counts are).
 template <typename T, int BT>
-__global__ void k_res_gather(const T* __restrict__ src, int64_t Bp, const int32_t* __restrict__ map,
-                             int K, int64_t tiles, T* __restrict__ dst) {
-  const int64_t total = tiles * K * BT;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int s = (int)(e % BT);
-    const int64_t rest = e / BT;
-    const int k = (int)(rest % K);
-    const int64_t tile = rest / K;
-    const int32_t j = map[k];
-    dst[e] = j >= 0 ? src[(int64_t)j * Bp + tile * BT + s] : T(0);
+__global__ __launch_bounds__(256) void k_res_gather(const T* __restrict__ src, int64_t Bp,
+                                                    const int32_t* __restrict__ map, int K,
+                                                    int64_t tiles, T* __restrict__ dst) {
+  constexpr int TT = 64 / BT;  // tiles of the block
+  __shared__ T buf[64][65];    // [slot][sample of the block]
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * TT;
+  const int k0 = blockIdx.y * 64;
+  const int64_t b = t0 * BT + tx;
+  T v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int j = map[k0 + ty + 4 * i];
+    v[i] = j >= 0 ? src[(int64_t)j * Bp + b] : T(0);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) buf[ty + 4 * i][tx] = v[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int e = threadIdx.x + 256 * i;  // (tile of the block, slot, sample): 64 * BT per tile
+    const int tt = e / (64 * BT), rem = e % (64 * BT);
+    const int kk = rem / BT, s = rem % BT;
+    dst[((t0 + tt) * K + k0 + kk) * BT + s] = buf[kk][tt * BT + s];
   }
 }
 
