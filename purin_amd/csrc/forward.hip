@@ -54,6 +54,7 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values, int extra
   L.SL = take(mi * Bp * es);
   L.colpart = take((size_t)5 * std::max(L.ncb, 1) * Bp * es);
   L.rowpart = take((size_t)3 * std::max(L.nrb, 1) * Bp * es);
+  L.decpart = take((size_t)8 * kDecideSplit * Bp * es);  // k_decide's split pre-pass
   L.done = take(Bp * 4);
   L.count = take(Bp * 4);
   L.ndone = take(256);
@@ -510,6 +511,32 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   const dim3 gcolq = tile_grid(Bp, TS / 4, (n + 15) / 16);
   const dim3 gres = tile_grid(Bp, TS, std::max(L.nrb, 1));
   const dim3 gdec((unsigned)(Bp / 64));  // k_decide: 64 samples per block
+  // With fewer than 16 such blocks the per-sample stop test folds its chunk
+  // partials in two passes: (Bp / 64) x kDecideSplit blocks each fold every
+  // kDecideSplit-th chunk, then the decision folds those partials (config 3,
+  // B = 256: 4 blocks folding 1250 column chunks each otherwise)
+  const bool dec_split = Bp / 64 < 16;
+  const dim3 gdecp((unsigned)(Bp / 64), (unsigned)kDecideSplit);
+  T* const decpart = (T*)(ws + L.decpart);
+  auto decide = [&]() {
+    if (dec_split) {
+      k_decide<T, false, true><<<gdecp, 64 * kDecideGroups, 0, st>>>(
+          A, batch, tol_scalar, tolv, done, count, ndone, nullptr, nullptr, nullptr, nullptr,
+          nullptr, decpart);
+      Iter<T> A2 = A;
+      A2.colpart = decpart;
+      A2.ncb = kDecideSplit;
+      A2.rowpart = decpart + (size_t)5 * kDecideSplit * Bp;
+      A2.nrb = kDecideSplit;
+      k_decide<T, false><<<gdec, 64 * kDecideGroups, 0, st>>>(A2, batch, tol_scalar, tolv, done,
+                                                              count, ndone, nullptr, nullptr,
+                                                              nullptr, nullptr, nullptr);
+    } else {
+      k_decide<T, false><<<gdec, 64 * kDecideGroups, 0, st>>>(A, batch, tol_scalar, tolv, done,
+                                                              count, ndone, nullptr, nullptr,
+                                                              nullptr, nullptr, nullptr);
+    }
+  };
   // K ybar by linearity (kernels.hpp, Iter::lin) where it moves fewer bytes:
   // with n > 2m the ybar stream the column pass writes (n per sample) outweighs
   // the two m-vectors of K y the row pass then reads and writes (fixed
@@ -582,8 +609,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
       k_col_pass<T, 1, kRowsPerWaveEarly><<<gcolE, kBlock, 0, st>>>(A);
       if (timing) PURIN_HIP(hipEventRecord(evd[it], st));
       if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres, kBlock, 0, st>>>(A);
-      k_decide<T, false><<<gdec, 64 * kDecideGroups, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
-                                                   nullptr, nullptr, nullptr, nullptr, nullptr);
+      decide();
     } else {
       A.done = done;
       if (lin && it == 0) {  // K y0 (= K ybar0) by one gather of y0
@@ -601,8 +627,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
       if (lin) A.KYo = kyb[(it + 1) & 1];  // K y+ for the next iteration's row pass
       if (m) k_res_pass<T, kRowsPerWaveEarly><<<gres, kBlock, 0, st>>>(A);
       A.KYo = nullptr;
-      k_decide<T, false><<<gdec, 64 * kDecideGroups, 0, st>>>(A, batch, tol_scalar, tolv, done, count, ndone,
-                                                   nullptr, nullptr, nullptr, nullptr, nullptr);
+      decide();
     }
     if (timing) PURIN_HIP(hipEventRecord(ev[3 * it + 2], st));
     theta_prev = theta;  // the theta of this iteration's ybar update

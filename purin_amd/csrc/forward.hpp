@@ -14,7 +14,7 @@ struct Layout {
   // saved region
   size_t hdr, Tt, Y, D, R, LO, HI, RF, conv, feas, saved_end;
   // forward workspace
-  size_t YB, MF, DF, SL, colpart, rowpart, done, count, ndone, ores, ogap, ofin, X, Z;
+  size_t YB, MF, DF, SL, colpart, rowpart, decpart, done, count, ndone, ores, ogap, ofin, X, Z;
   size_t RTs, RRs, RD0, RLs, RHs;  // resident path (slot-ordered inputs)
   // per-sample coefficients (values given per call): entry values in the
   // caller's order (VF), the kept CSR / CSC entries original (RVo, CVo) and

@@ -486,13 +486,20 @@ __global__ __launch_bounds__(kBlock) void k_res_pass(Iter<T> A) {
 // samples: group g reduces the column chunks c = g, g + G, ... and the row
 // chunks likewise, in increasing order; the groups then combine in LDS in
 // group order.  Grid: Bp / 64 blocks.
+//
+// PRE (small batches, few blocks): a first pass of (Bp / 64) x kDecideSplit
+// blocks folds, per sample, the chunks c = y, y + P, y + 2P, ... (y =
+// blockIdx.y, P = gridDim.y) the same way and writes the P partials in the
+// chunk-partial layout ([5][P][Bp] column totals, then [3][P][Bp] row totals
+// at ``pre``); the decision pass then folds those P chunks.
 constexpr int kDecideGroups = 16;
+constexpr int kDecideSplit = 16;
 
-template <typename T, bool FINAL>
+template <typename T, bool FINAL, bool PRE = false>
 __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
     Iter<T> A, int64_t batch, T tol_scalar, const T* __restrict__ tolv, int32_t* done,
     int32_t* count, int32_t* ndone, const int32_t* feasible, T* out_res, T* out_gap,
-    int32_t* out_conv, int32_t* out_fin) {
+    int32_t* out_conv, int32_t* out_fin, T* pre = nullptr) {
   if (!FINAL && A.stop && *A.stop >= A.nstop) return;
   constexpr int G = kDecideGroups;
   __shared__ T buf[G][64];
@@ -500,6 +507,10 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
   const int64_t b = (int64_t)blockIdx.x * 64 + lane;  // < Bp by the grid
   const T zero = T(0);
   const size_t cplane = (size_t)A.ncb * A.Bp, rplane = (size_t)A.nrb * A.Bp;
+  // this block's chunk subsequence: chunk c0 + cs * c for c < nc (nr for rows)
+  const int cs = PRE ? (int)gridDim.y : 1, c0 = PRE ? (int)blockIdx.y : 0;
+  const int nc = PRE ? (A.ncb > c0 ? (A.ncb - c0 + cs - 1) / cs : 0) : A.ncb;
+  const int nr = PRE ? (A.nrb > c0 ? (A.nrb - c0 + cs - 1) / cs : 0) : A.nrb;
   T q[8] = {zero, zero, zero, zero, T(1), zero, zero, T(1)};  // primal, dual, stat, bnd, fin, res, rd, fin_d
   // Chunks c = g, g + G, ... in increasing order.  The loads of U chunks are
   // issued before they are folded in (a chain of dependent waits otherwise:
@@ -507,11 +518,11 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
   // folds is unchanged.
   constexpr int U = 8;
   int c = g;
-  for (; c + (U - 1) * G < A.ncb; c += U * G) {
+  for (; c + (U - 1) * G < nc; c += U * G) {
     T v[5][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const T* p = A.colpart + (size_t)(c + u * G) * A.Bp + b;
+      const T* p = A.colpart + (size_t)(c0 + cs * (c + u * G)) * A.Bp + b;
 #pragma unroll
       for (int k = 0; k < 5; ++k) v[k][u] = p[k * cplane];
     }
@@ -524,8 +535,8 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
       if (v[4][u] == zero) q[4] = zero;
     }
   }
-  for (; c < A.ncb; c += G) {
-    const T* p = A.colpart + (size_t)c * A.Bp + b;
+  for (; c < nc; c += G) {
+    const T* p = A.colpart + (size_t)(c0 + cs * c) * A.Bp + b;
     q[0] += p[0];
     q[1] += p[cplane];
     q[2] = maxp(q[2], p[2 * cplane]);
@@ -533,11 +544,11 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
     if (p[4 * cplane] == zero) q[4] = zero;
   }
   int r = g;
-  for (; r + (U - 1) * G < A.nrb; r += U * G) {
+  for (; r + (U - 1) * G < nr; r += U * G) {
     T v[3][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const T* p = A.rowpart + (size_t)(r + u * G) * A.Bp + b;
+      const T* p = A.rowpart + (size_t)(c0 + cs * (r + u * G)) * A.Bp + b;
 #pragma unroll
       for (int k = 0; k < 3; ++k) v[k][u] = p[k * rplane];
     }
@@ -548,8 +559,8 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
       if (v[2][u] == zero) q[7] = zero;
     }
   }
-  for (; r < A.nrb; r += G) {
-    const T* p = A.rowpart + (size_t)r * A.Bp + b;
+  for (; r < nr; r += G) {
+    const T* p = A.rowpart + (size_t)(c0 + cs * r) * A.Bp + b;
     q[5] = maxp(q[5], p[0]);
     q[6] += p[rplane];
     if (p[2 * rplane] == zero) q[7] = zero;
@@ -570,6 +581,16 @@ __global__ __launch_bounds__(64 * kDecideGroups) void k_decide(
       q[k] = v;
     }
     __syncthreads();
+  }
+  if (PRE) {
+    if (g == 0) {
+      const size_t P = gridDim.y, Bp = (size_t)A.Bp, y = blockIdx.y;
+#pragma unroll
+      for (int k = 0; k < 5; ++k) pre[((size_t)k * P + y) * Bp + b] = q[k];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) pre[((size_t)(5 + k) * P + y) * Bp + b] = q[5 + k];
+    }
+    return;
   }
   if (g != 0 || b >= batch) return;
   if (!FINAL && done[b]) {
