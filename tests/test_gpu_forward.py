@@ -421,3 +421,30 @@ def test_streaming_linear_kybar_matches_oracle(dtype, accelerated, early_stop):
         stopped += int(np.sum(to_np(st.iterations) < iters))
     if early_stop:
         assert stopped > 0  # the stop test fired
+
+
+def test_streaming_early_stop_two_pass_fold():
+    """The streaming passes' stop test at B = 256 (4 blocks of 64 samples),
+    where the chunk partials are folded in two passes (every 16th chunk per
+    block of the first pass, then the 16 partials), on a problem whose
+    fixed-iteration column pass takes quarter-wavefront tiles (m = 4500 kept
+    rows).  Against the oracle's early stop on samples from both ends of the
+    batch: identical iteration counts and statuses, y at the fp64 bar."""
+    require_gpu()
+    B = 256
+    w = workloads.small_random(77, n=10000, me=1500, mi=3000, width=4, batch=B,
+                               accelerated=True, target_sd=0.5)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (B, 1))
+    target = np.ascontiguousarray(w.target, np.float64)
+    plan = plan_for(canon, dtype=np.float64, accelerated=True)
+    kw = dict(max_iterations=800, early_stop=True, tolerance=1e-2)
+    got = plan.project(target, rhs, timing=True, **kw)
+    t = plan.last_timing()
+    assert t["resident"] == 0
+    pick = [0, 1, B - 2, B - 1]
+    cfg = op.Config(accelerated=True, max_iterations=800, early_stop=True, tolerance=1e-2)
+    want = op.solve(canon, target[pick], rhs[pick], cfg, dtype=np.float64)
+    np.testing.assert_array_equal(to_np(got.iterations)[pick], want.iterations)
+    np.testing.assert_array_equal(to_np(got.status)[pick], want.status)
+    assert rel_err(to_np(got.y)[pick], want.y) <= TOL[np.float64]
