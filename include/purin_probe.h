@@ -36,15 +36,6 @@ int purin_probe_lds(void* stream, int32_t iters, int32_t groups, int32_t lds_byt
                     int32_t unroll, int32_t reps, void* sink, int64_t sink_bytes,
                     double* ms_per_launch);
 
-/* LDS reads at a lane pattern: lane l of every wavefront reads the 16-byte
- * entries pattern[l] + 1024 u, u = 0..3 (pattern[l] in [0, 1024); a host
- * array of 64), ``iters`` times (lds_bytes >= 65536).  Comparing patterns
- * shows which lanes a ds_read_b128 serves together and what a bank conflict
- * costs.  Bytes per launch: groups * 1024 * 64 * iters. */
-int purin_probe_lds_pattern(void* stream, const int32_t* pattern, int32_t iters, int32_t groups,
-                            int32_t lds_bytes, int32_t reps, void* sink, int64_t sink_bytes,
-                            double* ms_per_launch);
-
 #ifdef __cplusplus
 }
 #endif

@@ -240,37 +240,19 @@ constexpr int res_tile() {
   return ResVec<T>::BT;  // 16 bytes of samples per gathered element
 }
 
-template <typename T, int SLR, int SLC>
-static int launch_resident_sl(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
-                              bool early) {
-  auto kern = early ? (sb ? k_resident_early<T, SLR, SLC, true> : k_resident_early<T, SLR, SLC, false>)
-                    : (sb ? k_resident<T, SLR, SLC, true> : k_resident<T, SLR, SLC, false>);
-  PURIN_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds));
-  kern<<<dim3((unsigned)tiles), dim3(kResThreads), lds, st>>>(R);
-  return PURIN_CP_OK;
-}
-
+// One translation unit per (element type, row slots): resident_launch.hip.
 template <typename T, int SLR>
-static int launch_resident_c(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
-                             bool sb, bool early) {
-  switch (slc) {
-    case 1: return launch_resident_sl<T, SLR, 1>(R, st, tiles, lds, sb, early);
-    case 2: return launch_resident_sl<T, SLR, 2>(R, st, tiles, lds, sb, early);
-    case 3: return launch_resident_sl<T, SLR, 3>(R, st, tiles, lds, sb, early);
-    case 4: return launch_resident_sl<T, SLR, 4>(R, st, tiles, lds, sb, early);
-    default: return set_error(PURIN_CP_ERR_ARG, "resident column slot count out of range");
-  }
-}
+int launch_resident_rows(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
+                         bool sb, bool early);
 
 template <typename T>
 static int launch_resident(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slr,
                            int slc, bool sb, bool early) {
   switch (slr) {
-    case 1: return launch_resident_c<T, 1>(R, st, tiles, lds, slc, sb, early);
-    case 2: return launch_resident_c<T, 2>(R, st, tiles, lds, slc, sb, early);
-    case 3: return launch_resident_c<T, 3>(R, st, tiles, lds, slc, sb, early);
-    case 4: return launch_resident_c<T, 4>(R, st, tiles, lds, slc, sb, early);
+    case 1: return launch_resident_rows<T, 1>(R, st, tiles, lds, slc, sb, early);
+    case 2: return launch_resident_rows<T, 2>(R, st, tiles, lds, slc, sb, early);
+    case 3: return launch_resident_rows<T, 3>(R, st, tiles, lds, slc, sb, early);
+    case 4: return launch_resident_rows<T, 4>(R, st, tiles, lds, slc, sb, early);
     default: return set_error(PURIN_CP_ERR_ARG, "resident row slot count out of range");
   }
 }

@@ -84,70 +84,9 @@ __global__ __launch_bounds__(1024) void k_probe_lds(int iters, uint32_t span_mas
   if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9E3779B9u) sink[t] = acc.x;
 }
 
-struct LanePattern {
-  uint32_t entry[64];  // the 16-byte LDS entry each lane reads, < 1024
-};
-
-// LDS reads at a given lane -> entry pattern: every lane reads 16 bytes at
-// entries pattern[lane] + 1024 u (u = 0..3, so the bank of each read is the
-// pattern's), all within a 64 KiB span.
-__global__ __launch_bounds__(1024) void k_probe_lds_pattern(int iters, LanePattern pat,
-                                                            uint32_t* __restrict__ sink) {
-  extern __shared__ __align__(16) unsigned char lds[];
-  const uint32_t t = threadIdx.x;
-  U4* l4 = reinterpret_cast<U4*>(lds);
-  for (uint32_t i = t; i < 4096u; i += 1024u) l4[i] = U4{i, i ^ 1u, i ^ 2u, i ^ 3u};
-  __syncthreads();
-  uint32_t e = pat.entry[t & 63u] & 1023u;
-  U4 acc = {0u, 0u, 0u, 0u};
-  for (int it = 0; it < iters; ++it) {
-    asm volatile("" : "+v"(e));  // the address is opaque each iteration: no hoisting
-    U4 v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = l4[(e + 1024u * (uint32_t)u) & 4095u];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) acc ^= v[u];
-  }
-  if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9E3779B9u) sink[t] = acc.x;
-}
-
 }  // namespace
 
 extern "C" {
-
-int purin_probe_lds_pattern(void* stream, const int32_t* pattern, int32_t iters, int32_t groups,
-                            int32_t lds_bytes, int32_t reps, void* sink, int64_t sink_bytes,
-                            double* ms_per_launch) {
-  if (!pattern || !sink || !ms_per_launch || iters < 1 || groups < 1 || reps < 1 ||
-      lds_bytes < 65536 || lds_bytes > 160 * 1024 || sink_bytes < 4096)
-    return 1;
-  LanePattern pat;
-  for (int l = 0; l < 64; ++l) {
-    if (pattern[l] < 0 || pattern[l] >= 1024) return 1;
-    pat.entry[l] = (uint32_t)pattern[l];
-  }
-  hipStream_t st = (hipStream_t)stream;
-  if (hipFuncSetAttribute((const void*)k_probe_lds_pattern,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes) != hipSuccess)
-    return 2;
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return 2;
-  hipError_t e = hipEventRecord(e0, st);
-  for (int r = 0; r < reps && e == hipSuccess; ++r) {
-    k_probe_lds_pattern<<<dim3((unsigned)groups), dim3(1024), (size_t)lds_bytes, st>>>(
-        iters, pat, (uint32_t*)sink);
-    e = hipGetLastError();
-  }
-  if (e == hipSuccess) e = hipEventRecord(e1, st);
-  if (e == hipSuccess) e = hipEventSynchronize(e1);
-  float ms = 0.f;
-  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  if (e != hipSuccess) return 2;
-  *ms_per_launch = (double)ms / reps;
-  return 0;
-}
 
 int purin_probe_stream(void* stream, const void* buf, int64_t buf_bytes, int64_t wave_chunks,
                        int32_t iters, int32_t groups, int32_t lds_bytes, int32_t unroll,

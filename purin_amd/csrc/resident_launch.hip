@@ -1,0 +1,48 @@
+// Launches of the resident (on-chip) CP kernels for one element type and one
+// row-slot count.  The build compiles this file once per (type, row slots)
+// pair, selected by PURIN_RES_F64 (1: double, 0: float) and PURIN_RES_SLR
+// (1..4), so that the 128 kernel variants (4 column-slot counts, shared or
+// per-sample bounds, fixed-iteration or early-stop, per pair) compile in
+// parallel translation units.  forward.hip dispatches to them.
+
+#include "plan.hpp"
+#include "resident.hpp"
+
+#ifndef PURIN_RES_F64
+#error "compile with -DPURIN_RES_F64=0|1 -DPURIN_RES_SLR=1..4"
+#endif
+
+namespace purin {
+
+template <typename T, int SLR, int SLC>
+static int launch_one(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
+                      bool early) {
+  auto kern = early ? (sb ? k_resident_early<T, SLR, SLC, true> : k_resident_early<T, SLR, SLC, false>)
+                    : (sb ? k_resident<T, SLR, SLC, true> : k_resident<T, SLR, SLC, false>);
+  PURIN_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+  kern<<<dim3((unsigned)tiles), dim3(kResThreads), lds, st>>>(R);
+  return PURIN_CP_OK;
+}
+
+template <typename T, int SLR>
+int launch_resident_rows(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
+                         bool sb, bool early) {
+  switch (slc) {
+    case 1: return launch_one<T, SLR, 1>(R, st, tiles, lds, sb, early);
+    case 2: return launch_one<T, SLR, 2>(R, st, tiles, lds, sb, early);
+    case 3: return launch_one<T, SLR, 3>(R, st, tiles, lds, sb, early);
+    case 4: return launch_one<T, SLR, 4>(R, st, tiles, lds, sb, early);
+    default: return set_error(PURIN_CP_ERR_ARG, "resident column slot count out of range");
+  }
+}
+
+#if PURIN_RES_F64
+template int launch_resident_rows<double, PURIN_RES_SLR>(const Res<double>&, hipStream_t, int64_t,
+                                                         size_t, int, bool, bool);
+#else
+template int launch_resident_rows<float, PURIN_RES_SLR>(const Res<float>&, hipStream_t, int64_t,
+                                                        size_t, int, bool, bool);
+#endif
+
+}  // namespace purin
