@@ -371,11 +371,7 @@ def sparse_cp(q, c, values, rhs, support, mask, me, lower, upper, *,
         if early_stop:
             done = done | accepted
         if accelerated:
-            one = dtype.type(1)
-            nt = one / np.sqrt(one + gamma * tau)
-            tau = nt * tau
-            sigma = sigma / nt
-            theta = nt
+            tau, sigma, theta = accelerated_update(tau, sigma, gamma)
         iteration += 1
     residual, gap = diagnostics(y, dual, q, c, rhs, lower, upper, mv, tmv, me)
     finite = (np.all(np.isfinite(y), axis=1) & np.all(np.isfinite(dual), axis=1)
@@ -388,22 +384,32 @@ def sparse_cp(q, c, values, rhs, support, mask, me, lower, upper, *,
     return CPOutput(y, dual, counts, residual, gap, converged)
 
 
+def accelerated_update(tau, sigma, gamma):
+    """One accelerated step update; kernels.py:279-283.
+
+    ``nu = 1/sqrt(1 + gamma tau)``; returns ``(nu tau, sigma/nu, nu)`` (the next
+    tau, sigma and theta), in the dtype of ``tau``.
+    """
+    tau = np.asarray(tau)
+    one = tau.dtype.type(1)
+    nt = one / np.sqrt(one + np.asarray(gamma, tau.dtype) * tau)
+    return nt * tau, np.asarray(sigma, tau.dtype) / nt, nt
+
+
 def accelerated_schedule(tau0, sigma0, iterations, dtype, gamma=1.0):
     """Per-iteration ``(tau, sigma, theta)`` of the accelerated update; kernels.py:279-283.
 
-    Row ``k`` holds the scalars iteration ``k`` uses (theta_0 = 1).
+    Row ``k`` holds the scalars iteration ``k`` uses (theta_0 = 1); each row
+    follows from the previous by ``accelerated_update``, the update the loop of
+    ``sparse_cp`` applies.
     """
     dtype = np.dtype(dtype)
-    one = dtype.type(1)
     g = dtype.type(gamma)
     tau = dtype.type(tau0)
     sigma = dtype.type(sigma0)
-    theta = one
+    theta = dtype.type(1)
     out = np.empty((iterations, 3), dtype)
     for k in range(iterations):
         out[k] = (tau, sigma, theta)
-        nt = one / np.sqrt(one + g * tau)
-        tau = nt * tau
-        sigma = sigma / nt
-        theta = nt
+        tau, sigma, theta = accelerated_update(tau, sigma, g)
     return out

@@ -135,12 +135,90 @@ def test_fixed_iteration_mode_runs_every_iteration():
     assert np.all(early.iterations < 37)
 
 
-def test_accelerated_schedule_matches_loop_update():
-    sched = cp.accelerated_schedule(0.3, 0.2, 5, np.float64)
-    tau, sigma, theta = 0.3, 0.2, 1.0
-    for k in range(5):
-        np.testing.assert_array_equal(sched[k], [tau, sigma, theta])
-        nt = 1 / np.sqrt(1 + tau)
-        tau, sigma, theta = nt * tau, sigma / nt, nt
-    s32 = cp.accelerated_schedule(0.3, 0.2, 5, np.float32)
+def _schedule_violations(sched, tau0, sigma0, gamma):
+    """Which relations fixed by the accelerated update (kernels.py:279-283:
+    nu = 1/sqrt(1 + gamma tau), tau <- nu tau, sigma <- sigma/nu, theta <- nu)
+    a schedule ``(tau_k, sigma_k, theta_k)`` breaks."""
+    tau, sigma, theta = (np.asarray(c, np.float64) for c in np.asarray(sched).T)
+    k = np.arange(len(tau), dtype=np.float64)
+    bad = []
+    if not (tau[0] == tau0 and sigma[0] == sigma0 and theta[0] == 1.0):
+        bad.append("start")
+    # the step product tau sigma is invariant (sigma is divided by what tau is multiplied by)
+    if not np.allclose(tau * sigma, tau0 * sigma0, rtol=1e-12, atol=0):
+        bad.append("tau*sigma")
+    # theta_{k+1} is the factor that took tau_k to tau_{k+1}
+    if not np.allclose(theta[1:], tau[1:] / tau[:-1], rtol=1e-14, atol=0):
+        bad.append("theta")
+    # squaring nu: 1/tau_{k+1}^2 = 1/tau_k^2 + gamma/tau_k
+    if not np.allclose(1 / tau[1:] ** 2 - 1 / tau[:-1] ** 2, gamma / tau[:-1], rtol=1e-9, atol=0):
+        bad.append("recursion")
+    # hence 1/tau_k grows like gamma k / 2: gamma tau_k k -> 2
+    if not abs(gamma * tau[-1] * k[-1] - 2.0) < 1e-2:
+        bad.append("asymptote")
+    return bad
+
+
+@pytest.mark.parametrize("gamma", [1.0, 0.25, 3.0])
+def test_accelerated_schedule_invariants(gamma):
+    """Pins ``accelerated_schedule`` by what the recurrence fixes, not by restating
+    it: the invariant step product, theta as the step ratio, the squared
+    recursion and the 2/(gamma k) decay (20000 steps)."""
+    tau0, sigma0 = 0.3, 0.2
+    sched = cp.accelerated_schedule(tau0, sigma0, 20000, np.float64, gamma=gamma)
+    assert _schedule_violations(sched, tau0, sigma0, gamma) == []
+    s32 = cp.accelerated_schedule(tau0, sigma0, 5, np.float32, gamma=gamma)
     assert s32.dtype == np.float32
+
+
+def test_schedule_invariants_reject_planted_mistakes():
+    """Each plausible slip in the update fails at least one relation: sigma
+    multiplied instead of divided, a doubled gamma, theta the inverse factor."""
+    tau0, sigma0, gamma = 0.3, 0.2, 1.0
+
+    def planted(kind, iters=20000):
+        out = np.empty((iters, 3))
+        tau, sigma, theta = tau0, sigma0, 1.0
+        for k in range(iters):
+            out[k] = (tau, sigma, theta)
+            nu = 1 / np.sqrt(1 + (2 * gamma if kind == "2gamma" else gamma) * tau)
+            tau = nu * tau
+            sigma = sigma * nu if kind == "sigma" else sigma / nu
+            theta = 1 / nu if kind == "theta" else nu
+        return out
+
+    assert _schedule_violations(planted("none"), tau0, sigma0, gamma) == []
+    assert "tau*sigma" in _schedule_violations(planted("sigma"), tau0, sigma0, gamma)
+    assert {"recursion", "asymptote"} <= set(_schedule_violations(planted("2gamma"), tau0,
+                                                                  sigma0, gamma))
+    assert "theta" in _schedule_violations(planted("theta"), tau0, sigma0, gamma)
+
+
+def test_sparse_cp_takes_the_schedule_steps(monkeypatch):
+    """The accelerated loop of ``sparse_cp`` updates its steps through
+    ``accelerated_update`` once per iteration, so it walks exactly the
+    ``accelerated_schedule`` pinned above."""
+    canon = _cases.sum_equals_b()
+    support, mask, values = canon.ell(np.float64)
+    yhat = np.array([[0.8, 0.7], [2.0, 0.0]])
+    q = np.ones_like(yhat)
+    inf = np.inf * np.ones_like(yhat)
+    seen = []
+    real = cp.accelerated_update
+
+    def spy(tau, sigma, gamma):
+        seen.append((np.array(tau, copy=True), np.array(sigma, copy=True), np.array(gamma)))
+        return real(tau, sigma, gamma)
+
+    monkeypatch.setattr(cp, "accelerated_update", spy)
+    cp.sparse_cp(q, -yhat, values, np.ones((2, 1)), support, mask, 1, -inf, inf,
+                 accelerated=True, max_iterations=7, y0=yhat, freeze_converged=True,
+                 check_stationarity=True, norm_bound=True, early_stop=False)
+    monkeypatch.setattr(cp, "accelerated_update", real)
+    assert len(seen) == 7
+    tau0, sigma0 = seen[0][0][0], seen[0][1][0]
+    sched = cp.accelerated_schedule(tau0, sigma0, 7, np.float64)
+    for k, (tau, sigma, gamma) in enumerate(seen):
+        np.testing.assert_array_equal(gamma, [1.0, 1.0])  # gamma = min q
+        np.testing.assert_array_equal(tau, [sched[k, 0]] * 2)
+        np.testing.assert_array_equal(sigma, [sched[k, 1]] * 2)
