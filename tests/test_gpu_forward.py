@@ -5,6 +5,8 @@ projected points and multipliers; identical iteration counts, status codes and
 active-set masks.  Relative error is ``max|a-b| / max|b|``.
 """
 
+from dataclasses import replace
+
 import numpy as np
 import pytest
 
@@ -13,6 +15,7 @@ from oracle import projection as op
 from purin_amd import workloads
 from tests import _cases
 from tests._gpu import canonical_from_workload, plan_for, rel_err, require_gpu, to_np
+from tests._margins import Margins, check_counts, check_iterates
 
 pytestmark = pytest.mark.gpu
 
@@ -58,40 +61,34 @@ def test_solve_matches_oracle(dtype, accelerated, early_stop):
     ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
     iters = 400
     tol = 1e-6 if dtype == np.float64 else 1e-4
-    want = ocp.sparse_cp(np.ones_like(target), -target, pre.kept_values[0], pre.kept_rhs, ksup,
-                         kmask, canon.me, pre.lower, pre.upper, accelerated=accelerated,
-                         max_iterations=iters, tolerance=tol, y0=target,
-                         freeze_converged=True, check_stationarity=True, norm_bound=True,
-                         early_stop=early_stop)
+    mg = Margins(lambda safety, tr: ocp.sparse_cp(
+        np.ones_like(target), -target, pre.kept_values[0], pre.kept_rhs, ksup, kmask, canon.me,
+        pre.lower, pre.upper, accelerated=accelerated, safety=safety, max_iterations=iters,
+        tolerance=tol, y0=target, freeze_converged=True, check_stationarity=True,
+        norm_bound=True, early_stop=early_stop, trace=tr), dtype)
+    want = mg.want
     plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
     got = plan.solve(pre.kept_rhs, target, pre.lower, pre.upper, tolerance=tol,
                      max_iterations=iters, early_stop=early_stop, check_every=7)
     bar = TOL[dtype]
-    assert rel_err(to_np(got.y), want.y) <= bar
-    assert rel_err(to_np(got.dual), want.dual) <= bar
-    it_g = to_np(got.iterations)
-    if dtype == np.float64:
-        np.testing.assert_array_equal(it_g, want.iterations)
-        np.testing.assert_array_equal(to_np(got.converged), want.converged)
-    else:
-        # fp32: the resident kernel sums each row and column in its scheduled
-        # gather order, not the oracle's index order, so a sample whose stop
-        # margin sits on the tolerance may stop one iteration apart (at most 1 in 10)
-        same = it_g == want.iterations
-        assert (~same).sum() * 10 <= B, (it_g[~same], want.iterations[~same])
-        assert np.all(np.abs(it_g - want.iterations) <= 1)
-        np.testing.assert_array_equal(to_np(got.converged)[same], want.converged[same])
+    # counts: identical in fp64; in fp32 a sample may stop elsewhere only where
+    # the oracle's own stop is borderline (tests/_margins.py)
+    same = check_counts(to_np(got.iterations), mg)
+    check_iterates(to_np(got.y), mg, same, bar)
+    assert rel_err(to_np(got.dual)[same], want.dual[same]) <= bar
+    np.testing.assert_array_equal(to_np(got.converged)[same], want.converged[same])
     # diagnostics of a nearly converged iterate sit near the rounding floor in fp32
     dtol = dict(rtol=1e-6, atol=1e-12) if dtype == np.float64 else dict(rtol=1e-2, atol=2e-5)
-    np.testing.assert_allclose(to_np(got.residual), want.residual, **dtol)
-    np.testing.assert_allclose(to_np(got.gap), want.gap, **dtol)
+    np.testing.assert_allclose(to_np(got.residual)[same], want.residual[same], **dtol)
+    np.testing.assert_allclose(to_np(got.gap)[same], want.gap[same], **dtol)
     if early_stop and not accelerated:
         assert np.any(want.iterations < iters), "the stop test should fire for some samples"
-    # active sets: bound activity and positive inequality duals
-    y, d = to_np(got.y), to_np(got.dual)
-    np.testing.assert_array_equal(y == pre.lower, want.y == pre.lower)
-    np.testing.assert_array_equal(y == pre.upper, want.y == pre.upper)
-    np.testing.assert_array_equal(d[:, canon.me:] > 0, want.dual[:, canon.me:] > 0)
+    # active sets on same-count samples: bound activity and positive inequality duals
+    y, d = to_np(got.y)[same], to_np(got.dual)[same]
+    lo, hi = pre.lower[same], pre.upper[same]
+    np.testing.assert_array_equal(y == lo, want.y[same] == lo)
+    np.testing.assert_array_equal(y == hi, want.y[same] == hi)
+    np.testing.assert_array_equal(d[:, canon.me:] > 0, want.dual[same][:, canon.me:] > 0)
 
 
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
@@ -330,9 +327,19 @@ def test_resident_early_stop_matches_streaming_and_oracle(dtype, accelerated):
     another fixed order, so its iterates differ from the streaming passes' by
     rounding: same-count samples agree to the parity bar; fp64 counts are
     identical; in fp32 a sample whose margin sits on the tolerance may stop
-    one iteration apart (at most 1 in 10)."""
+    one iteration apart (at most 1 in 10).
+
+    Oracle leg, fp64 and fp32: on the first samples of each batch the
+    resident kernel's counts are the oracle's under the rule of
+    tests/_margins.py (identical in fp64; in fp32 a different count only at a
+    borderline stop), same-count iterates at the parity bar and statuses
+    equal; the others within the oracle's own spread under a 1e-6 change of
+    the steps (accelerated fp32 moves some stops by tens of iterations)."""
     torch = require_gpu()
     tol = (1e-6 if dtype == np.float64 else 1e-3) if not accelerated else 1e-4
+    # oracle samples per size (the NumPy oracle's per-iteration diagnostics
+    # dominate the test's time at the larger sizes)
+    n_oracle = {48: 8, 700: 6, 1500: 4, 4096: 2}
     stopped = 0
     for n, me, mi, width, B in ((48, 8, 20, 4, 37), (700, 100, 300, 5, 64), (1500, 300, 700, 6, 40),
                                 (4096, 1024, 2048, 8, 16)):
@@ -367,14 +374,19 @@ def test_resident_early_stop_matches_streaming_and_oracle(dtype, accelerated):
         if dtype == np.float64 or not accelerated:
             np.testing.assert_array_equal(to_np(res.status)[same], to_np(st.status)[same])
         stopped += int(np.sum(it_r < kw["max_iterations"]))
-        if dtype == np.float64:
-            sub = slice(0, 6)
-            cfg = op.Config(accelerated=accelerated, max_iterations=kw["max_iterations"],
-                            tolerance=tol)
-            want = op.solve(canon, target[sub], rhs[sub], cfg, dtype=dtype)
-            np.testing.assert_array_equal(it_r[sub], want.iterations)
-            np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
-            assert rel_err(to_np(res.y)[sub], want.y) <= TOL[dtype], n
+        sub = np.arange(n_oracle[n])
+        cfg = op.Config(accelerated=accelerated, max_iterations=kw["max_iterations"],
+                        tolerance=tol)
+        print(f"n={n} {np.dtype(dtype).name} accelerated={accelerated}: oracle on "
+              f"{sub.size} samples", flush=True)
+        mg = Margins(lambda safety, tr: op.solve(canon, target[sub], rhs[sub],
+                                                 replace(cfg, safety=safety), dtype=dtype,
+                                                 trace=tr), dtype)
+        print(f"  counts gpu {it_r[sub].tolist()} oracle {mg.want.iterations.tolist()}",
+              flush=True)
+        same_o = check_counts(it_r, mg, samples=sub)
+        check_iterates(to_np(res.y), mg, same_o, TOL[dtype], samples=sub)
+        np.testing.assert_array_equal(to_np(res.status)[sub][same_o], mg.want.status[same_o])
     assert stopped > 0  # the stop test fired
 
 

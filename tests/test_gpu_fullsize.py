@@ -43,44 +43,135 @@ def full_plan(w):
     return p, values, root
 
 
+class Checked:
+    """The C loop's fixed-iteration state on a few samples, and the oracle's
+    recovery of the projection outputs from it (bounds.py:247-317)."""
+
+    def __init__(self, w, values, root, samples):
+        from oracle import cp as ocp
+
+        rows = [list(w.indices[w.indptr[i]:w.indptr[i + 1]]) for i in range(w.rows_total)]
+        coef = [list(values[w.indptr[i]:w.indptr[i + 1]]) for i in range(w.rows_total)]
+        self.canon = op.Canonical(n=w.n, me=w.me, rows=rows, coef=coef)
+        dt = np.dtype(w.dtype)
+        target = np.asarray(w.target[samples], dt)
+        if root is not None:  # the plan's variables z = sqrt(D) y (metric.py:102-108)
+            target = target * root.astype(dt)
+        self.target = target
+        self.rhs = np.tile(w.rhs, (len(samples), 1)).astype(dt)
+        self.cfg = op.Config(accelerated=w.accelerated, max_iterations=w.iterations,
+                             early_stop=False)
+        self.y, self.d, _ = cloop.run(cloop.prepare(self.canon, target, self.rhs, self.cfg, dt),
+                                      w.iterations, w.accelerated, threads=8)
+        # final diagnostics (kernels.py:291-305) and recovery, as oracle.cp.sparse_cp and
+        # oracle.projection.solve finish a fixed-iteration run
+        pre = op.presolve(self.canon, self.rhs, self.cfg, dt)
+        self.pre = pre
+        ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
+        mv, tmv = ocp.operators(pre.kept_values[0], ksup, kmask, w.n)
+        q, c = np.ones_like(target), -target
+        res, gap = ocp.diagnostics(self.y, self.d, q, c, pre.kept_rhs, pre.lower, pre.upper, mv,
+                                   tmv, w.me)
+        stat = ocp.stationarity(self.y, self.d, q, c, pre.lower, pre.upper, tmv)
+        finite = (np.all(np.isfinite(self.y), axis=1) & np.all(np.isfinite(self.d), axis=1)
+                  & np.isfinite(gap) & np.isfinite(res))
+        conv = finite & (res <= pre.tolerance) & (gap <= pre.tolerance) & (stat <= pre.tolerance)
+        iters = np.full(len(samples), w.iterations, np.int32)
+        out = ocp.CPOutput(self.y, self.d, iters, np.maximum(res, stat), gap,
+                           conv & pre.feasible)
+        self.rec = op.recover(self.canon, pre, out, target, self.rhs, self.cfg)
+        self.multipliers = np.concatenate((self.rec.multipliers_eq, self.rec.multipliers_ineq),
+                                          axis=1)
+
+
 def checker_y(w, values, root, samples):
     """y of the C loop for ``samples`` (in the metric's variables when there is one)."""
-    rows = [list(w.indices[w.indptr[i]:w.indptr[i + 1]]) for i in range(w.rows_total)]
-    coef = [list(values[w.indptr[i]:w.indptr[i + 1]]) for i in range(w.rows_total)]
-    canon = op.Canonical(n=w.n, me=w.me, rows=rows, coef=coef)
-    target = np.asarray(w.target[samples], w.dtype)
-    if root is not None:
-        target = target * root.astype(w.dtype)
-    rhs = np.tile(w.rhs, (len(samples), 1)).astype(w.dtype)
-    cfg = op.Config(accelerated=w.accelerated, max_iterations=w.iterations, early_stop=False)
-    y, _, _ = cloop.run(cloop.prepare(canon, target, rhs, cfg, w.dtype), w.iterations,
-                        w.accelerated, threads=4)
-    return y
+    return Checked(w, values, root, samples).y
 
 
-@pytest.mark.parametrize("config", [2, 3, 4])
-def test_full_size_projection(config):
-    torch = require_gpu()
-    w = {2: workloads.config2, 3: workloads.config3, 4: workloads.config4}[config]()
-    B = w.target.shape[0]
-    p, values, root = full_plan(w)
-    rhs = np.tile(w.rhs, (B, 1)).astype(w.dtype)
-    kw = dict(max_iterations=w.iterations, early_stop=False, shared_bounds=True)
-    print(f"config{config}: B={B} n={w.n} iterations={w.iterations}", flush=True)
-    out = p.project(w.target, rhs, **kw)
-    y = to_np(out.y)
-    bar = 1e-10 if w.dtype == np.float64 else 1e-4
-    want = checker_y(w, values, root, PICK)
-    got = y[PICK] * (root if root is not None else 1.0)
-    assert rel_err(got, want) <= bar
-    # independence of samples: the leading half alone is bit-identical
-    k = B // 2
-    alone = p.project(w.target[:k], rhs[:k], **kw)
-    np.testing.assert_array_equal(to_np(alone.y), y[:k])
-    np.testing.assert_array_equal(to_np(alone.status), to_np(out.status)[:k])
-    np.testing.assert_array_equal(to_np(alone.multipliers), to_np(out.multipliers)[:k])
-    del out, alone
-    torch.cuda.empty_cache()
+def spread(B, k):
+    """Both ends of the batch and ``k`` samples spread over it."""
+    return np.unique(np.r_[[0, 1, 2, B - 3, B - 2, B - 1],
+                           np.linspace(0, B - 1, k).astype(int)])
+
+
+def test_full_size_duals_and_active_sets():
+    """Kept-row duals, recovered multipliers, slacks, status and the active-set
+    masks at the full benchmark sizes, against the checker on samples spread
+    over the batch (configs 2, 3, 4: fp64 1e-10 and fp32 1e-4 on values; masks
+    identical).  The masks are the reference's: ``y == lower`` and
+    ``y == upper`` as the dual recovery tests them (bounds.py:252-261), in the
+    plan's variables (config 3's metric variables z = sqrt(D) y), ``d_I > 0`` on
+    the kept inequality rows (kernels.py:133-136), and positive recovered bound
+    multipliers.  ``solve`` gives the kept-row duals and z directly;
+    ``project`` the multipliers (original units), slacks and status."""
+    import torch
+
+    require_gpu()
+    for config, k in ((2, 26), (3, 10), (4, 58)):
+        w = {2: workloads.config2, 3: workloads.config3, 4: workloads.config4}[config]()
+        B = w.target.shape[0]
+        samples = spread(B, k)
+        p, values, root = full_plan(w)
+        dt = np.dtype(w.dtype)
+        bar = 1e-10 if dt == np.float64 else 1e-4
+        print(f"config{config}: B={B} n={w.n} iterations={w.iterations}, "
+              f"{len(samples)} checked samples", flush=True)
+        ck = Checked(w, values, root, samples)
+        pre = ck.pre
+        rhs = np.tile(w.rhs, (B, 1)).astype(dt)
+        kw = dict(max_iterations=w.iterations, early_stop=False, shared_bounds=True)
+        # the inner solve in the plan's variables and scaled units
+        target_z = w.target.astype(dt) * (root.astype(dt) if root is not None else 1)
+        o = p.solve(np.tile(pre.kept_rhs[0], (B, 1)), target_z, pre.lower[0], pre.upper[0], **kw)
+        yz, d = to_np(o.y)[samples], to_np(o.dual)[samples]
+        del o
+        me = w.me
+        lo, hi = pre.lower, pre.upper
+        print(f"  solve: y {rel_err(yz, ck.y):.2e} dual {rel_err(d, ck.d):.2e}; "
+              f"at lower {int((ck.y == lo).sum())} (gpu {int((yz == lo).sum())}), at upper "
+              f"{int((ck.y == hi).sum())} (gpu {int((yz == hi).sum())}), active inequalities "
+              f"{int((ck.d[:, me:] > 0).sum())} (gpu {int((d[:, me:] > 0).sum())})", flush=True)
+        # the whole projection
+        out = p.project(w.target, rhs, **kw)
+        y = to_np(out.y)[samples]
+        mult = to_np(out.multipliers)[samples]
+        slacks = to_np(out.slacks)[samples]
+        status = to_np(out.status)[samples]
+        residual = to_np(out.residual)[samples]
+        del out
+        kept, bnd = pre.rows, pre.bounds
+        print(f"  project: y {rel_err(y * (root if root is not None else 1), ck.y):.2e} "
+              f"kept multipliers {rel_err(mult[:, kept], ck.multipliers[:, kept]):.2e} "
+              f"bound multipliers {rel_err(mult[:, bnd], ck.multipliers[:, bnd]):.2e} "
+              f"slacks {rel_err(slacks, ck.rec.slacks):.2e} status {np.unique(status)} "
+              f"residual {residual.min():.3e}..{residual.max():.3e} vs "
+              f"{ck.rec.residual_inf_norm.min():.3e}..{ck.rec.residual_inf_norm.max():.3e}, "
+              f"positive bound multipliers {int((ck.multipliers[:, bnd] > 0).sum())} "
+              f"(gpu {int((mult[:, bnd] > 0).sum())})", flush=True)
+        # values at the parity bar
+        assert rel_err(yz, ck.y) <= bar
+        assert rel_err(d, ck.d) <= bar
+        assert rel_err(mult[:, kept], ck.multipliers[:, kept]) <= bar
+        if len(bnd):
+            assert rel_err(mult[:, bnd], ck.multipliers[:, bnd]) <= bar
+        assert rel_err(slacks, ck.rec.slacks) <= bar
+        np.testing.assert_array_equal(status, ck.rec.status)
+        # the original-unit residual; with a metric it is the z-space residual times
+        # max(1, sqrt(max D)) (metric.py:161-165)
+        factor = max(1.0, float(np.max(root))) if root is not None else 1.0
+        np.testing.assert_allclose(residual, ck.rec.residual_inf_norm * factor,
+                                   rtol=1e-8 if dt == np.float64 else 1e-3)
+        # the active sets, identical
+        np.testing.assert_array_equal(yz == lo, ck.y == lo)
+        np.testing.assert_array_equal(yz == hi, ck.y == hi)
+        np.testing.assert_array_equal(d[:, me:] > 0, ck.d[:, me:] > 0)
+        np.testing.assert_array_equal(mult[:, bnd] > 0, ck.multipliers[:, bnd] > 0)
+        # the non-vacuous part: bounds are attained and inequalities active
+        assert (ck.y == lo).any() or (ck.y == hi).any()
+        assert config == 3 or (ck.d[:, me:] > 0).any()
+        del p
+        torch.cuda.empty_cache()
 
 
 def test_full_size_resident_and_streaming_agree():

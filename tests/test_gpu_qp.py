@@ -15,7 +15,7 @@ from oracle import diagonal_qp as dq
 from oracle.cp import layout
 from oracle.projection import Config
 from tests._gpu import rel_err, require_gpu, to_np
-from tests.test_gpu_values import _check_counts
+from tests._margins import Margins, check_counts
 
 pytestmark = pytest.mark.gpu
 
@@ -68,19 +68,14 @@ def test_qp_solve_matches_oracle(dtype, early_stop, accelerated):
     # 1e-3 keeps them meaningful
     cfg = Config(accelerated=accelerated, max_iterations=iters, early_stop=early_stop,
                  tolerance=1e-6 if dtype == np.float64 else 1e-3)
-    trace, others = [], []
-    want = dq.solve(support, mask, me, data, cfg, trace=trace)
-    if dtype == np.float32 and early_stop:
-        for f in (1 + 1e-6, 1 - 1e-6):
-            other = []
-            dq.solve(support, mask, me, data, replace(cfg, safety=0.95 * f), trace=other)
-            others.append(np.asarray(other, np.float64))
+    mg = Margins(lambda safety, tr: dq.solve(support, mask, me, data,
+                                             replace(cfg, safety=safety), trace=tr), dtype)
+    want = mg.want
     plan = _plan(rows, me, mi, n, dtype, accelerated=accelerated)
     got = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper,
                         values=data.values[:, mask], tolerance=cfg.tolerance,
                         max_iterations=iters, early_stop=early_stop, check_every=6)
-    _check_counts(to_np(got.iterations), want.iterations, dtype,
-                  np.asarray(trace, np.float64), others)
+    check_counts(to_np(got.iterations), mg)
     same = to_np(got.iterations) == want.iterations
     bar = TOL[dtype]
     assert rel_err(to_np(got.y)[same], want.y[same]) <= bar

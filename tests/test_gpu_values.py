@@ -17,6 +17,7 @@ import pytest
 from oracle import projection as op
 from purin_amd import workloads
 from tests._gpu import canonical_from_workload, plan_for, rel_err, require_gpu, to_np
+from tests._margins import Margins, check_counts
 
 pytestmark = pytest.mark.gpu
 
@@ -41,47 +42,6 @@ def _per_sample(w, B, seed, spread=0.3):
     return canon, values, rhs, mask
 
 
-def _oracle_with_margins(solve, dtype):
-    """The oracle's result, its stop margins max(residual, gap, stationarity) /
-    tol per iteration (T, B), and (fp32) the margins of two runs whose steps
-    differ by 1e-6 relative (safety scaled by 1 +- 1e-6)."""
-    trace = []
-    want = solve(0.95, trace)
-    others = []
-    if dtype == np.float32:
-        for f in (1 + 1e-6, 1 - 1e-6):
-            other = []
-            solve(0.95 * f, other)
-            others.append(np.asarray(other, np.float64))
-    return want, np.asarray(trace, np.float64), others
-
-
-def _check_counts(got, want, dtype, trace, others):
-    """Per-sample iteration counts: identical in fp64.  In fp32 a sample may
-    stop at another iteration only where rounding-level changes move its stop
-    test across the tolerance: at the earlier of the two stop iterations k the
-    oracle's margin lies within max(1e-4, 2 s) of 1, with s the largest change
-    of that sample's margin over iterations k-2..k+2 when the steps change by
-    1e-6 relative (late accelerated fp32 iterations reach s ~ 5e-2), and at most
-    1 in 10 samples differ."""
-    diff = np.flatnonzero(got != want)
-    msg = (f"{diff.size} samples differ: {diff.tolist()[:8]} got {got[diff][:8].tolist()} "
-           f"want {want[diff][:8].tolist()}")
-    if dtype == np.float64 or diff.size == 0:
-        assert diff.size == 0, msg
-        return
-    assert diff.size * 10 <= got.size, msg
-    for b in diff:
-        k = min(got[b], want[b]) - 1
-        sens = 0.0
-        for other in others:
-            lo, hi = max(k - 2, 0), min(k + 3, len(trace), len(other))
-            if hi > lo:
-                sens = max(sens, float(np.max(np.abs(other[lo:hi, b] - trace[lo:hi, b]))))
-        assert abs(trace[k, b] - 1) <= max(1e-4, 2 * sens), (
-            f"{msg}; sample {b} margin {trace[k, b]!r} sensitivity {sens!r}")
-
-
 def _csr(values, mask):
     return np.ascontiguousarray(values[:, mask])
 
@@ -98,15 +58,16 @@ def test_values_project_matches_oracle(dtype, early_stop, accelerated):
     iters = 600
     cfg = op.Config(accelerated=accelerated, max_iterations=iters, early_stop=early_stop,
                     tolerance=1e-6 if dtype == np.float64 else 1e-4)
-    want, trace, others = _oracle_with_margins(
+    mg = Margins(
         lambda safety, tr: op.solve(canon, target, rhs.astype(dtype), replace(cfg, safety=safety),
                                     dtype=dtype, values=values.astype(dtype), trace=tr), dtype)
+    want = mg.want
     plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
     got = plan.project(target, rhs.astype(dtype), values=_csr(values, mask).astype(dtype),
                        tolerance=cfg.tolerance, max_iterations=iters, early_stop=early_stop,
                        check_every=7)
     bar = TOL[dtype]
-    _check_counts(to_np(got.iterations), want.iterations, dtype, trace, others)
+    check_counts(to_np(got.iterations), mg)
     same = to_np(got.iterations) == want.iterations
     assert rel_err(to_np(got.y)[same], want.y[same]) <= bar
     assert rel_err(to_np(got.y), want.y) <= 10 * bar
@@ -135,13 +96,14 @@ def test_values_steps_variants_match_oracle(dtype, mode):
     kw = dict(diagonal_preconditioning=True) if mode == "diagonal" else dict(norm_bound=False)
     cfg = op.Config(max_iterations=500, early_stop=True,
                     tolerance=1e-6 if dtype == np.float64 else 1e-4, **kw)
-    want, trace, others = _oracle_with_margins(
+    mg = Margins(
         lambda safety, tr: op.solve(canon, target, rhs.astype(dtype), replace(cfg, safety=safety),
                                     dtype=dtype, values=values.astype(dtype), trace=tr), dtype)
+    want = mg.want
     plan = plan_for(canon, dtype=dtype, **kw)
     got = plan.project(target, rhs.astype(dtype), values=_csr(values, mask).astype(dtype),
                        tolerance=cfg.tolerance, max_iterations=500, early_stop=True, check_every=5)
-    _check_counts(to_np(got.iterations), want.iterations, dtype, trace, others)
+    check_counts(to_np(got.iterations), mg)
     same = to_np(got.iterations) == want.iterations
     assert rel_err(to_np(got.y)[same], want.y[same]) <= TOL[dtype]
     assert rel_err(to_np(got.y), want.y) <= 10 * TOL[dtype]
