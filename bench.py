@@ -63,6 +63,12 @@ METRICS = {
 }
 
 
+# CPU-baseline samples (one core, all threads) for the headline configuration
+# and, smaller, for the configurations timed beside config2 in the default line
+CPU_SAMPLES = {2: (64, 512), 3: (4, 64), 4: (256, 4096)}
+CPU_SAMPLES_OTHER = {3: (2, 16), 4: (64, 1024)}
+
+
 def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -464,52 +470,17 @@ def time_calls(torch, fn, count):
     return e0.elapsed_time(e1) / count, out
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
-    ap.add_argument("--mode", default="project", choices=("project", "values", "qp", "dense"),
-                    help="project: the headline (default); values / qp / dense: the widened "
-                         "paths (per-sample coefficients, diagonal QP, dense adapter)")
-    ap.add_argument("--batch", type=int, default=None)
-    ap.add_argument("--iterations", type=int, default=None)
-    ap.add_argument("--cpu-samples", type=int, default=None,
-                    help="samples of the all-core CPU baseline leg")
-    ap.add_argument("--cpu-samples-one", type=int, default=None,
-                    help="samples of the one-core CPU baseline leg")
-    ap.add_argument("--cpu-adjoint-samples", type=int, default=32,
-                    help="samples of the one-thread CPU adjoint leg (config2)")
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-adjoint", action="store_true", help="skip the adjoint leg (config2)")
-    ap.add_argument("--no-streaming", action="store_true",
-                    help="skip the streaming two-pass comparison run")
-    ap.add_argument("--copy-calibration-mib", type=int, default=0,
-                    help="only run a plain device-to-device copy of this many MiB (3 times); "
-                         "its FETCH_SIZE / WRITE_SIZE counters calibrate the traffic figures")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: the batch shards across GPUs "
-                          "with no per-iteration communication, so run --gpus 1 per GPU"}))
-        sys.exit(2)
+def measure(args, torch, config, *, steps, warmup, headline):
+    """Time ``purin_cp_project`` on one configuration; returns (line, context).
 
-    import torch
-
-    if args.copy_calibration_mib:
-        copy_calibration(torch, args.copy_calibration_mib)
-        return
-
-    if args.mode != "project":
-        run_mode(args, torch)
-        return
-
+    ``headline``: the configuration of the driver's line (the command-line
+    batch / iteration overrides apply, and the extra legs run)."""
     from purin_amd import workloads
     from purin_amd.plan import Plan
 
-    make = {2: workloads.config2, 3: workloads.config3, 4: workloads.config4}[args.config]
-    w = make(args.batch) if args.batch else make()
-    if args.iterations:
+    make = {2: workloads.config2, 3: workloads.config3, 4: workloads.config4}[config]
+    w = make(args.batch) if (args.batch and headline) else make()
+    if args.iterations and headline:
         w.iterations = args.iterations
     B, n = w.target.shape
     tdtype = torch.float64 if w.dtype == np.float64 else torch.float32
@@ -524,11 +495,10 @@ def main():
     target = torch.as_tensor(w.target, device=dev)
     rhs = torch.as_tensor(np.tile(w.rhs, (B, 1)).astype(w.dtype), device=dev)
     kw = dict(max_iterations=w.iterations, early_stop=False, shared_bounds=True)
-    adjoint_leg = args.config == 2 and not args.no_adjoint
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         plan.project(target, rhs, **kw)
-    ms_per_step, out = time_calls(torch, lambda: plan.project(target, rhs, **kw), args.steps)
+    ms_per_step, out = time_calls(torch, lambda: plan.project(target, rhs, **kw), steps)
     value = B / (ms_per_step / 1e3)
     status = out.status.cpu().numpy()
 
@@ -560,7 +530,7 @@ def main():
         dominant = col_kernel if col_ms >= row_ms else "k_row_pass"
         dom_bytes, dom_ms = (bytes_col, col_ms) if dominant == col_kernel else (bytes_row, row_ms)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
-    traffic = traffic_from_profiles(args.config, dominant, B, w.iterations)
+    traffic = traffic_from_profiles(config, dominant, B, w.iterations)
     if tm["resident"]:
         # The iterate stays on chip: what the launch moves is the shared matrix's
         # chunk streams from L2 (every tile re-reads them each iteration) and the
@@ -625,31 +595,23 @@ def main():
         }
     # the streaming two-pass path on the same inputs, for comparison
     streaming_ms = None
-    if tm["resident"] and not args.no_streaming:
+    if headline and tm["resident"] and not args.no_streaming:
         streaming_ms, _ = time_calls(
             torch, lambda: plan.project(target, rhs, streaming=True, **kw), 1)
-    # per-sample bounds: the kernels of a caller whose bound rows depend on theta
-    kw_ps = dict(kw, shared_bounds=False)
-    plan.project(target, rhs, **kw_ps)
-    ps_ms, ps_out = time_calls(torch, lambda: plan.project(target, rhs, **kw_ps), args.steps)
-    same = bool(torch.equal(ps_out.y, out.y))
-    # the PURIN-API front end on the same problem (constant bound rows: it
-    # selects the shared-bounds kernels by itself)
-    api = purin_api_timing(torch, w, values, root, target, args.steps)
 
     line = {
-        "metric": METRICS[args.config],
+        "metric": METRICS[config],
         "value": value,
         "unit": "projections/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f64" if ws == 8 else "f32",
-        "data": f"synthetic ({w.name} generator, numpy default_rng seed {args.config})",
+        "data": f"synthetic ({w.name} generator, numpy default_rng seed {config})",
         "config": {
             "workload": {
                 2: "config2: n=4096, 1024 eq + 2048 ineq rows x 8 cols, 8192 bound rows, "
@@ -659,21 +621,12 @@ def main():
                    "fixed-step CP, fixed iterations, full projection",
                 4: "config4: n=1024, 256 eq + 512 ineq rows x 16 cols, bounds [-2,2], "
                    "batch 65536, fp32, accelerated CP, fixed iterations, full projection",
-            }[args.config],
+            }[config],
             "n": n, "kept_rows": m, "bound_rows": int(plan.info.bound_rows),
             "nnz_kept": int(plan.info.nnz_kept), "batch": B, "iterations": w.iterations,
             "parallelism": "1 GPU (batch-parallel)",
         },
         "roofline": roofline,
-        "per_sample_bounds": {
-            "ms_per_step": ps_ms,
-            "value": B / (ps_ms / 1e3),
-            "unit": "projections/s",
-            "y_bit_identical_to_shared": same,
-            "what": "the same purin_cp_project call with shared_bounds = 0 (lower/upper read "
-                    "per sample: the kernels of bound rows whose rhs depends on theta)",
-        },
-        "purin_api": api,
         "iteration": {
             "cp_iterations_per_s": w.iterations * 1e3 / ms_per_step,
             "resident_kernel": bool(tm["resident"]),
@@ -689,6 +642,73 @@ def main():
         },
         "statuses": {str(k): int(v) for k, v in zip(*np.unique(status, return_counts=True))},
     }
+    if headline:
+        # per-sample bounds: the kernels of a caller whose bound rows depend on theta
+        kw_ps = dict(kw, shared_bounds=False)
+        plan.project(target, rhs, **kw_ps)
+        ps_ms, ps_out = time_calls(torch, lambda: plan.project(target, rhs, **kw_ps), steps)
+        line["per_sample_bounds"] = {
+            "ms_per_step": ps_ms,
+            "value": B / (ps_ms / 1e3),
+            "unit": "projections/s",
+            "y_bit_identical_to_shared": bool(torch.equal(ps_out.y, out.y)),
+            "what": "the same purin_cp_project call with shared_bounds = 0 (lower/upper read "
+                    "per sample: the kernels of bound rows whose rhs depends on theta)",
+        }
+        # the PURIN-API front end on the same problem (constant bound rows: it
+        # selects the shared-bounds kernels by itself)
+        line["purin_api"] = purin_api_timing(torch, w, values, root, target, steps)
+    ctx = dict(w=w, plan=plan, target=target, rhs=rhs, kw=kw, B=B, n=n, m=m, ws=ws, dev=dev)
+    return line, ctx
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
+    ap.add_argument("--mode", default="project", choices=("project", "values", "qp", "dense"),
+                    help="project: the headline (default); values / qp / dense: the widened "
+                         "paths (per-sample coefficients, diagonal QP, dense adapter)")
+    ap.add_argument("--batch", type=int, default=None)
+    ap.add_argument("--iterations", type=int, default=None)
+    ap.add_argument("--cpu-samples", type=int, default=None,
+                    help="samples of the all-core CPU baseline leg")
+    ap.add_argument("--cpu-samples-one", type=int, default=None,
+                    help="samples of the one-core CPU baseline leg")
+    ap.add_argument("--cpu-adjoint-samples", type=int, default=32,
+                    help="samples of the one-thread CPU adjoint leg (config2)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-adjoint", action="store_true", help="skip the adjoint leg (config2)")
+    ap.add_argument("--no-others", action="store_true",
+                    help="skip the config3 / config4 sub-objects of the default (config2) line")
+    ap.add_argument("--no-streaming", action="store_true",
+                    help="skip the streaming two-pass comparison run")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run a plain device-to-device copy of this many MiB (3 times); "
+                         "its FETCH_SIZE / WRITE_SIZE counters calibrate the traffic figures")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: the batch shards across GPUs "
+                          "with no per-iteration communication, so run --gpus 1 per GPU"}))
+        sys.exit(2)
+
+    import torch
+
+    if args.copy_calibration_mib:
+        copy_calibration(torch, args.copy_calibration_mib)
+        return
+
+    if args.mode != "project":
+        run_mode(args, torch)
+        return
+
+    line, ctx = measure(args, torch, args.config, steps=args.steps, warmup=args.warmup,
+                        headline=True)
+    w, plan, target, rhs, kw = ctx["w"], ctx["plan"], ctx["target"], ctx["rhs"], ctx["kw"]
+    B, n, m, ws, dev = ctx["B"], ctx["n"], ctx["m"], ctx["ws"], ctx["dev"]
+    adjoint_leg = args.config == 2 and not args.no_adjoint
 
     if adjoint_leg:
         cot = torch.as_tensor(np.random.default_rng(5).normal(0.0, 1.0, (B, n)), device=dev)
@@ -749,7 +769,7 @@ def main():
         }
 
     if not args.no_cpu:
-        default_sample = {2: (64, 512), 3: (4, 64), 4: (256, 4096)}[args.config]
+        default_sample = CPU_SAMPLES[args.config]
         one = args.cpu_samples_one or default_sample[0]
         full = args.cpu_samples or default_sample[1]
         line["cpu_baseline"] = cpu_baseline(w, min(one, B), min(full, B))
@@ -769,6 +789,23 @@ def main():
             line["cpu_baseline_adjoint"] = cpu_baseline_adjoint(
                 w, plan, st.y.cpu().numpy(), st.dual.cpu().numpy(), pre.lower[0], pre.upper[0],
                 rhs_k, k)
+    # the other BASELINE configurations, each timed on its own plan after the
+    # headline's legs (3 steps after one warm-up call)
+    if args.config == 2 and not args.no_others and not args.batch and not args.iterations:
+        del ctx, plan, target, rhs
+        torch.cuda.empty_cache()
+        for c in (3, 4):
+            print(f"bench: config{c}", file=sys.stderr, flush=True)
+            sub, sctx = measure(args, torch, c, steps=max(1, min(args.steps, 3)), warmup=1,
+                                headline=False)
+            for k in ("n_gpus", "higher_is_better", "scaling", "vs_baseline"):
+                sub.pop(k, None)
+            if not args.no_cpu:
+                one, full = CPU_SAMPLES_OTHER[c]
+                sub["cpu_baseline"] = cpu_baseline(sctx["w"], one, full)
+            line[f"config{c}"] = sub
+            del sctx
+            torch.cuda.empty_cache()
     print(json.dumps(line), flush=True)
 
 

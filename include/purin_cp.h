@@ -36,14 +36,33 @@
  * finite, converged and valid arrays, as in the reference.
  * purin_cp_last_error() returns a message for the calling thread's last error.
  *
- * Threading: calls on one plan must be ordered (same stream or externally
- * synchronised); the plan owns one workspace.  All kernels are enqueued on the
- * given stream; project/solve/adjoint synchronise that stream only to read
- * their device-side stop flags.  A workspace that must grow is replaced
- * stream-ordered (hipMallocAsync / hipFreeAsync on the call's stream), and so
- * is the resident kernel's step schedule for a call of more than 65536
- * iterations; no entry point synchronises the device or other streams
- * (plan creation, destruction and set_metric are set-up calls and may).
+ * Workspaces and threading (the reference's layer is pure functional under
+ * jax.jit, bounds.py:33, 68-167): every compute entry point takes its device
+ * scratch either from the caller (the ``workspace`` / ``workspace_bytes``
+ * fields of its options struct; size from purin_cp_workspace_bytes) or, when
+ * that is NULL, from a workspace the plan owns.
+ *   - With a caller workspace a call allocates nothing and changes no plan
+ *     state its results depend on: calls on one plan may then run
+ *     concurrently, on different streams and from different threads, each
+ *     with its own workspace (and its own saved-state buffer).  The plan's
+ *     data is read-only to them.
+ *   - With the plan's workspace, calls on one plan must be ordered (same
+ *     stream or externally synchronised).  A workspace that must grow is
+ *     replaced stream-ordered (hipMallocAsync / hipFreeAsync on the call's
+ *     stream).
+ * All kernels are enqueued on the given stream.  project/solve read a device
+ * stop flag (a stream synchronisation) only on the streaming passes with
+ * early stop, every check_every iterations; the adjoints read their per-step
+ * counts likewise.  Such a call on a stream under capture returns
+ * PURIN_CP_ERR_ARG instead of breaking the capture; so does a call that would
+ * allocate (a plan workspace that must grow) or time itself under capture.
+ * A call of more than the 65536 iterations the resident kernel's step
+ * schedule holds extends the schedule once: it uploads the longer schedule on
+ * a stream of the plan's own and waits for that upload only.  No entry point
+ * synchronises the device or the caller's other streams (plan creation,
+ * destruction and set_metric are set-up calls and may).  The last_* queries
+ * report the last call that recorded them (timing: opts.timing; adjoint
+ * iterations: calls on the plan's workspace).
  */
 #ifndef PURIN_CP_H
 #define PURIN_CP_H
@@ -54,7 +73,7 @@
 extern "C" {
 #endif
 
-#define PURIN_CP_ABI_VERSION 1
+#define PURIN_CP_ABI_VERSION 2
 
 enum purin_cp_dtype { PURIN_CP_F32 = 0, PURIN_CP_F64 = 1 };
 
@@ -135,6 +154,11 @@ typedef struct {
   int64_t resident_stream_bytes_early;
   int64_t resident_row_slots;
   int64_t resident_col_slots;
+  /* Bytes the plan's own workspaces hold now (forward, adjoint); no reference
+   * counterpart.  Calls with a caller workspace, and the no-allocation entry,
+   * leave them unchanged. */
+  int64_t workspace_bytes;
+  int64_t adjoint_workspace_bytes;
 } purin_cp_plan_info;
 
 int purin_cp_plan_get_info(const purin_cp_plan* plan, purin_cp_plan_info* info);
@@ -154,7 +178,8 @@ int purin_cp_plan_set_metric(purin_cp_plan* plan, const double* sqrt_diagonal);
 
 /* First-kernel entry: out = K x (transpose = 0; x (B,n) -> out (B,m)) or
  * K^T x (transpose = 1; x (B,m) -> out (B,n)) over the kept rows, with the
- * row-scaled coefficients when scaled != 0. */
+ * row-scaled coefficients when scaled != 0.  Uses the plan's workspace
+ * (calls on one plan ordered). */
 int purin_cp_spmm(purin_cp_plan* plan, void* stream, int64_t batch, int32_t transpose,
                   int32_t scaled, const void* x, void* out);
 
@@ -172,6 +197,9 @@ typedef struct {
   int32_t streaming;       /* 1: force the streaming row/column passes even when the
                               resident on-chip kernel applies (fixed iterations) */
   int32_t reserved;
+  void* workspace;         /* caller device workspace (256-byte aligned) or NULL for the
+                              plan's own; see purin_cp_workspace_bytes */
+  int64_t workspace_bytes; /* its size in bytes */
 } purin_cp_solve_options;
 
 void purin_cp_default_solve_options(purin_cp_solve_options* opts);
@@ -338,9 +366,41 @@ typedef struct {
   int32_t force_eligible;    /* 1: treat every sample as converged (benchmark of
                                 a fixed-iteration state); 0: reference rule */
   int32_t reserved;
+  void* workspace;           /* caller device workspace (256-byte aligned) or NULL */
+  int64_t workspace_bytes;   /* its size in bytes */
+  int32_t* arnoldi_iterations; /* optional output, device int32 (B): per-sample Arnoldi
+                                  steps of this call (as purin_cp_last_adjoint_iterations;
+                                  the dense adjoint writes its BiCGSTAB iterations) */
 } purin_cp_adjoint_options;
 
 void purin_cp_default_adjoint_options(purin_cp_adjoint_options* opts);
+
+/* Compute entry points, for purin_cp_workspace_bytes. */
+enum purin_cp_entry {
+  PURIN_CP_ENTRY_SPMM = 0,
+  PURIN_CP_ENTRY_SOLVE = 1,
+  PURIN_CP_ENTRY_PROJECT = 2,          /* also purin_cp_project_noalloc */
+  PURIN_CP_ENTRY_PROJECT_VALUES = 3,
+  PURIN_CP_ENTRY_QP_SOLVE = 4,
+  PURIN_CP_ENTRY_DENSE_SOLVE = 5,
+  PURIN_CP_ENTRY_ADJOINT = 6,
+  PURIN_CP_ENTRY_ADJOINT_VALUES = 7,
+  PURIN_CP_ENTRY_QP_ADJOINT = 8,
+  PURIN_CP_ENTRY_DENSE_ADJOINT = 9
+};
+
+/*
+ * Bytes of caller workspace an entry point needs for ``batch`` samples: the
+ * largest over its optional arguments (a NULL ``saved``, whose state then
+ * lives in the workspace; warm-start multipliers or duals; a dual cotangent).
+ * For the adjoints ``adjoint_opts`` gives the GMRES restart length (NULL: the
+ * defaults).  Returns -1 for an invalid plan, entry or batch (message in
+ * purin_cp_last_error).  No reference counterpart (XLA sizes a custom call's
+ * scratch from such a query); replaces the plan-owned workspace of the
+ * jitted solve for callers that bring their own (bounds.py:33).
+ */
+int64_t purin_cp_workspace_bytes(const purin_cp_plan* plan, int32_t entry, int64_t batch,
+                                 const purin_cp_adjoint_options* adjoint_opts);
 
 /*
  * Implicit VJP at the state saved by project() (or solve()).

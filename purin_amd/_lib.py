@@ -16,6 +16,9 @@ LIB_PATH = os.path.join(HERE, "libpurin_cp.so")
 F32, F64 = 0, 1
 NOALLOC_SCRATCH_BYTES = 128 << 20  # PURIN_CP_NOALLOC_SCRATCH_BYTES
 OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM = 0, 1, 2, 3, 4
+# purin_cp_entry (purin_cp_workspace_bytes)
+ENTRY = dict(spmm=0, solve=1, project=2, project_values=3, qp_solve=4, dense_solve=5,
+             adjoint=6, adjoint_values=7, qp_adjoint=8, dense_adjoint=9)
 
 # every symbol the header declares (checked by tests/test_abi.py)
 SYMBOLS = (
@@ -28,6 +31,7 @@ SYMBOLS = (
     "purin_cp_spmm",
     "purin_cp_default_solve_options",
     "purin_cp_saved_bytes",
+    "purin_cp_workspace_bytes",
     "purin_cp_last_timing",
     "purin_cp_last_adjoint_stats",
     "purin_cp_last_adjoint_iterations",
@@ -71,6 +75,7 @@ class PlanInfo(C.Structure):
         ("tolerance_factor", C.c_double),
         ("resident_stream_bytes", C.c_int64), ("resident_stream_bytes_early", C.c_int64),
         ("resident_row_slots", C.c_int64), ("resident_col_slots", C.c_int64),
+        ("workspace_bytes", C.c_int64), ("adjoint_workspace_bytes", C.c_int64),
     ]
 
 
@@ -84,6 +89,8 @@ class SolveOptions(C.Structure):
         ("timing", C.c_int32),
         ("streaming", C.c_int32),
         ("reserved", C.c_int32),
+        ("workspace", C.c_void_p),
+        ("workspace_bytes", C.c_int64),
     ]
 
 
@@ -113,6 +120,9 @@ class AdjointOptions(C.Structure):
         ("adjoint_tolerance", C.c_double),
         ("force_eligible", C.c_int32),
         ("reserved", C.c_int32),
+        ("workspace", C.c_void_p),
+        ("workspace_bytes", C.c_int64),
+        ("arnoldi_iterations", C.POINTER(C.c_int32)),
     ]
 
 
@@ -158,6 +168,8 @@ def load(path: str = LIB_PATH):
     lib.purin_cp_default_solve_options.restype = None
     lib.purin_cp_saved_bytes.argtypes = [vp, i64]
     lib.purin_cp_saved_bytes.restype = C.c_int64
+    lib.purin_cp_workspace_bytes.argtypes = [vp, i32, i64, C.POINTER(AdjointOptions)]
+    lib.purin_cp_workspace_bytes.restype = C.c_int64
     lib.purin_cp_solve.argtypes = [vp, vp, i64, vp, vp, vp, vp, vp, vp, u8p, C.POINTER(SolveOptions),
                                    vp, vp, i32p, vp, vp, u8p, vp]
     lib.purin_cp_solve.restype = C.c_int

@@ -1269,16 +1269,20 @@ struct QPAdjArgs {
                       // no convergence masking
 };
 
+// ``size_only``: compute the workspace bytes of this call into *size_only and
+// return, touching neither the device nor the plan (purin_cp_workspace_bytes).
 template <typename T>
 static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const void* saved,
                         const T* cot_y, const purin_cp_adjoint_options& o, T* g_target, T* g_rhs,
                         T* g_lower, T* g_upper, uint8_t* valid, int32_t* info, T* gres,
                         const T* values = nullptr, T* g_values = nullptr,
-                        bool per_sample = false, const QPAdjArgs<T>* qa = nullptr) {
-  if (!saved || !cot_y) return set_error(PURIN_CP_ERR_ARG, "NULL saved state or cotangent");
-  if (per_sample && !qa && p->nnz_full && !values)
+                        bool per_sample = false, const QPAdjArgs<T>* qa = nullptr,
+                        int64_t* size_only = nullptr) {
+  if (!size_only && (!saved || !cot_y))
+    return set_error(PURIN_CP_ERR_ARG, "NULL saved state or cotangent");
+  if (!size_only && per_sample && !qa && p->nnz_full && !values)
     return set_error(PURIN_CP_ERR_ARG, "NULL values");
-  if (qa && (!qa->q || !qa->c)) return set_error(PURIN_CP_ERR_ARG, "NULL q or c");
+  if (!size_only && qa && (!qa->q || !qa->c)) return set_error(PURIN_CP_ERR_ARG, "NULL q or c");
   if (batch < 1) return set_error(PURIN_CP_ERR_ARG, "batch must be positive");
   if (o.restart < 1 || o.max_iterations < 1)
     return set_error(PURIN_CP_ERR_ARG, "linear iteration limits must be positive");
@@ -1292,38 +1296,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                           : (int)std::min<int64_t>({(int64_t)o.restart, (int64_t)o.max_iterations, W});
   if (restart > kMaxRestart) return set_error(PURIN_CP_ERR_UNSUPPORTED, "restart above 128");
   static_assert((kMaxRestart + 2) * 4 <= kPinnedBytes, "per-step counts must fit the pinned buffer");
-  // header written by the forward call
-  int64_t hdr[9];
-  PURIN_HIP(hipMemcpyAsync(hdr, saved, sizeof(hdr), hipMemcpyDeviceToHost, st));
-  PURIN_HIP(hipStreamSynchronize(st));
-  if (hdr[0] != kSavedMagic || hdr[1] != batch || hdr[2] != Bp || hdr[5] != p->dtype ||
-      hdr[6] != n || hdr[7] != m)
-    return set_error(PURIN_CP_ERR_ARG, "saved state does not belong to this plan and batch");
-  const int kind = (int)hdr[3];
-  const int shared = (int)hdr[4];
   const bool dense = qa && qa->dense;
-  if (dense ? kind != 4 : (qa ? kind != 3 : kind >= 3))
-    return set_error(PURIN_CP_ERR_ARG,
-                     dense ? "saved state is not from purin_cp_dense_solve"
-                           : (qa ? "saved state is not from purin_cp_qp_solve"
-                                 : "saved state is from purin_cp_qp_solve or purin_cp_dense_solve: "
-                                   "use purin_cp_qp_adjoint or purin_cp_dense_adjoint"));
-  if (!qa && per_sample != (kind == 2))
-    return set_error(PURIN_CP_ERR_ARG, per_sample
-                                           ? "saved state is not from purin_cp_project_values"
-                                           : "saved state is from purin_cp_project_values: use "
-                                             "purin_cp_adjoint_values");
-  const char* sv = (const char*)saved;
-  const T* Tt = (const T*)(sv + L.Tt);
-  const T* Y = (const T*)(sv + L.Y);
-  const T* Dd = (const T*)(sv + L.D);
-  const T* R = (const T*)(sv + L.R);
-  const T* LO = (const T*)(sv + L.LO);
-  const T* HI = (const T*)(sv + L.HI);
-  const T* RF = (const T*)(sv + L.RF);
-  const int32_t* conv = (const int32_t*)(sv + L.conv);
-  const T* metric = (kind == 1 || kind == 2) ? (const T*)p->metric : nullptr;
-
   // workspace
   const int nchunk = (int)((W + kChunk - 1) / kChunk);
   // Gram--Schmidt passes: about 1024 blocks of 4 wavefronts over the batch tiles
@@ -1332,11 +1305,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   // at most 8 resident blocks of 4 wavefronts per CU: the partial sums need at
   // most that many chunks per batch tile
   int cus = 0;
-  {
-    int dev = 0;
-    PURIN_HIP(hipGetDevice(&dev));
-    PURIN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  }
+  PURIN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device));
   const int nchunk2 = (int)std::max<int64_t>(
       1, std::min<int64_t>(((int64_t)8 * cus + tiles0 - 1) / tiles0, (W + 3) / 4));
   const size_t es = sizeof(T);
@@ -1373,9 +1342,61 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   const size_t oGq = qa ? take(n * Bp * es) : 0;    // g_q
   const size_t oCd = (qa && qa->cot_dual) ? take((size_t)std::max<int64_t>(M, 1) * Bp * es) : 0;
   const size_t oCds = (qa && qa->cot_dual) ? take((size_t)std::max<int64_t>(m, 1) * Bp * es) : 0;
+  if (size_only) {
+    *size_only = (int64_t)o_;
+    return PURIN_CP_OK;
+  }
+  // the adjoint reads the saved header and its per-step counts through stream
+  // synchronisations: not under capture
+  {
+    bool cap = false;
+    if (int rc = stream_capturing(st, &cap)) return rc;
+    if (cap)
+      return set_error(PURIN_CP_ERR_ARG,
+                       "the adjoint reads device-side counters (stream synchronisations): "
+                       "not under stream capture");
+  }
+  const bool own_ws = o.workspace == nullptr;
+  if (own_ws) {  // the last-call steps live in the plan's adjoint workspace, which may grow below
+    std::lock_guard<std::mutex> lock(p->mu);
+    p->adj_steps = nullptr;
+    p->adj_steps_batch = 0;
+  }
+  // header written by the forward call
+  int64_t hdr[9];
+  PURIN_HIP(hipMemcpyAsync(hdr, saved, sizeof(hdr), hipMemcpyDeviceToHost, st));
+  PURIN_HIP(hipStreamSynchronize(st));
+  if (hdr[0] != kSavedMagic || hdr[1] != batch || hdr[2] != Bp || hdr[5] != p->dtype ||
+      hdr[6] != n || hdr[7] != m)
+    return set_error(PURIN_CP_ERR_ARG, "saved state does not belong to this plan and batch");
+  const int kind = (int)hdr[3];
+  const int shared = (int)hdr[4];
+  if (dense ? kind != 4 : (qa ? kind != 3 : kind >= 3))
+    return set_error(PURIN_CP_ERR_ARG,
+                     dense ? "saved state is not from purin_cp_dense_solve"
+                           : (qa ? "saved state is not from purin_cp_qp_solve"
+                                 : "saved state is from purin_cp_qp_solve or purin_cp_dense_solve: "
+                                   "use purin_cp_qp_adjoint or purin_cp_dense_adjoint"));
+  if (!qa && per_sample != (kind == 2))
+    return set_error(PURIN_CP_ERR_ARG, per_sample
+                                           ? "saved state is not from purin_cp_project_values"
+                                           : "saved state is from purin_cp_project_values: use "
+                                             "purin_cp_adjoint_values");
+  const char* sv = (const char*)saved;
+  const T* Tt = (const T*)(sv + L.Tt);
+  const T* Y = (const T*)(sv + L.Y);
+  const T* Dd = (const T*)(sv + L.D);
+  const T* R = (const T*)(sv + L.R);
+  const T* LO = (const T*)(sv + L.LO);
+  const T* HI = (const T*)(sv + L.HI);
+  const T* RF = (const T*)(sv + L.RF);
+  const int32_t* conv = (const int32_t*)(sv + L.conv);
+  const T* metric = (kind == 1 || kind == 2) ? (const T*)p->metric : nullptr;
+
   int err = PURIN_CP_OK;
-  char* ws = (char*)workspace(p, o_, st, &err, true);
+  char* ws = (char*)workspace(p, o_, st, &err, true, o.workspace, o.workspace_bytes);
   if (!ws) return err;
+  HostWords hw(p);  // this call's host words for the counter reads
   T* Vb = (T*)(ws + oV);
   // GMRES basis: slot i, row r, sample b at r * zld + i * zs + b (the rows of all
   // slots interleaved, so a pass over the prefix reads one contiguous run per
@@ -1498,18 +1519,18 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
                                                                          out, opk);
   };
   auto read_counter = [&](int idx, int32_t* val) -> int {
-    PURIN_HIP(hipMemcpyAsync(p->pinned, G.counter, 2 * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+    PURIN_HIP(hipMemcpyAsync(hw.get(), G.counter, 2 * sizeof(int32_t), hipMemcpyDeviceToHost, st));
     PURIN_HIP(hipStreamSynchronize(st));
-    *val = p->pinned[idx];
+    *val = hw.get()[idx];
     return PURIN_CP_OK;
   };
   // active counts at the start of Arnoldi steps [0, upto] of the current cycle
   auto read_stepcnt = [&](int upto, std::vector<int32_t>& out) -> int {
     out.resize(upto + 1);
-    PURIN_HIP(hipMemcpyAsync(p->pinned, G.stepcnt, (upto + 1) * sizeof(int32_t),
+    PURIN_HIP(hipMemcpyAsync(hw.get(), G.stepcnt, (upto + 1) * sizeof(int32_t),
                              hipMemcpyDeviceToHost, st));
     PURIN_HIP(hipStreamSynchronize(st));
-    for (int i = 0; i <= upto; ++i) out[i] = p->pinned[i];
+    for (int i = 0; i <= upto; ++i) out[i] = hw.get()[i];
     return PURIN_CP_OK;
   };
   auto zero_counters = [&]() { k_fill<int32_t><<<1, 64, 0, st>>>(G.counter, 2, 0); };
@@ -1590,9 +1611,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   k_gm_rhs<T><<<eb, 256, 0, st>>>(n, m, W, Bp, batch, T1, cotd, conv,
                                   dense ? 1 : o.force_eligible, Gr);
   T* lam_w = (T*)(ws + oLw);
-  p->adjoint_stats = purin_cp_adjoint_stats{};
-  p->adj_steps = nullptr;  // set by the GMRES path below
-  p->adj_steps_batch = 0;
+  purin_cp_adjoint_stats stats{};
   if (dense) {
     // BiCGSTAB on (I - J^T) v = g over the whole batch (fixed_point.py:8-40)
     T* bpart = (T*)(ws + oBi);
@@ -1616,7 +1635,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     for (T* dst : {Rr, RH, Pv, Qv})
       PURIN_HIP(hipMemcpyAsync(dst, Gr, vec, hipMemcpyDeviceToDevice, st));
     int64_t iters = 0;
-    T* host = (T*)p->pinned;
+    T* host = (T*)hw.get();
     for (;;) {
       dot(Rr, Rr, kRS);
       PURIN_HIP(hipMemcpyAsync(host, bsc, kSlots * sizeof(T), hipMemcpyDeviceToHost, st));
@@ -1639,9 +1658,11 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
       k_bi_scalar<T><<<1, 64, 0, st>>>(bsc, 4, T(0), T(0));
       ++iters;
     }
-    p->adjoint_stats.arnoldi_steps = iters;
-    p->adjoint_stats.cycles = (int32_t)host[kK];  // iterations, or -10 / -11 at breakdown
+    stats.arnoldi_steps = iters;
+    stats.cycles = (int32_t)host[kK];  // iterations, or -10 / -11 at breakdown
     k_fill_weights<T><<<sb, 256, 0, st>>>(batch, Bp, lam_w);
+    if (o.arnoldi_iterations)
+      k_fill<int32_t><<<sb, 256, 0, st>>>(o.arnoldi_iterations, batch, (int32_t)iters);
   } else {
   // threshold = max(atol, tol * max|g|) and residual_inf = max|g - A 0| = max|g|
   k_gs<T, 4><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Gr, nullptr, W, Bp, part, nchunk, Bp);
@@ -1652,14 +1673,10 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
 
   const dim3 tri_grid((unsigned)(Bp / kTriS));
   const size_t tri_lds = (size_t)(5 * restart + 4) * kTriS * es;
-  PURIN_HIP(hipFuncSetAttribute((const void*)k_gm_tri<T, 1>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)tri_lds));
-  PURIN_HIP(hipFuncSetAttribute((const void*)k_gm_tri<T, 2>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)tri_lds));
+  if (int rc = raise_lds_cap((const void*)k_gm_tri<T, 1>, tri_lds)) return rc;
+  if (int rc = raise_lds_cap((const void*)k_gm_tri<T, 2>, tri_lds)) return rc;
   int64_t completed = 0;
   k_fill<int32_t><<<sb, 256, 0, st>>>(G.total, Bp, 0);
-  p->adj_steps = G.total;  // read by purin_cp_last_adjoint_iterations
-  p->adj_steps_batch = batch;
   while (completed < o.max_iterations) {
     zero_counters();
     k_gm_count_unconverged<T><<<sb, 256, 0, st>>>(G);
@@ -1667,7 +1684,7 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     if (int rc = read_counter(1, &unconverged)) return rc;
     if (unconverged == 0) break;
     const int cycle_limit = (int)std::min<int64_t>(restart, o.max_iterations - completed);
-    ++p->adjoint_stats.cycles;
+    ++stats.cycles;
     // beta = ||r||, V0 = r / max(beta, eps)
     k_gs<T, 3><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, Rr, nullptr, W, Bp, part, nchunk, Bp);
     reduce(1, S1, 0);
@@ -1729,7 +1746,15 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
     reduce(1, S1, 1);
     k_gm_cycle_end<T><<<sb, 256, 0, st>>>(G, S1);
     completed += it;
-    p->adjoint_stats.arnoldi_steps += it;
+    stats.arnoldi_steps += it;
+  }
+  if (o.arnoldi_iterations)
+    PURIN_HIP(hipMemcpyAsync(o.arnoldi_iterations, G.total, (size_t)batch * sizeof(int32_t),
+                             hipMemcpyDeviceToDevice, st));
+  if (own_ws) {  // read by purin_cp_last_adjoint_iterations until the next such call
+    std::lock_guard<std::mutex> lock(p->mu);
+    p->adj_steps = G.total;
+    p->adj_steps_batch = batch;
   }
   // finiteness of the solution, info, valid (operators.py:1119-1122, bounds.py:148-153)
   k_gs<T, 2><<<ggs, kBlock, 0, st>>>(nullptr, 0, 0, X, nullptr, W, Bp, part, nchunk, Bp);
@@ -1774,7 +1799,31 @@ static int adjoint_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const v
   if (g_lower) to_major<T>(st, glo, Bp, n, g_lower, batch, n, nullptr, 0);
   if (g_upper) to_major<T>(st, ghi, Bp, n, g_upper, batch, n, nullptr, 0);
   PURIN_HIP(hipGetLastError());
+  {
+    std::lock_guard<std::mutex> lock(p->mu);
+    p->adjoint_stats = stats;
+  }
   return PURIN_CP_OK;
+}
+
+template <typename T>
+static int adjoint_bytes_t(const purin_cp_plan* cp, int32_t entry, int64_t batch,
+                           const purin_cp_adjoint_options& o, int64_t* bytes) {
+  purin_cp_plan* p = const_cast<purin_cp_plan*>(cp);  // size_only touches nothing
+  const T dummy = T(0);
+  // the largest variant of each entry: a dual cotangent for the QP adjoints
+  const QPAdjArgs<T> qa{&dummy, &dummy, &dummy, nullptr, entry == PURIN_CP_ENTRY_DENSE_ADJOINT};
+  const bool per_sample = entry != PURIN_CP_ENTRY_ADJOINT;
+  const bool qp = entry == PURIN_CP_ENTRY_QP_ADJOINT || entry == PURIN_CP_ENTRY_DENSE_ADJOINT;
+  return adjoint_impl<T>(p, nullptr, batch, nullptr, nullptr, o, nullptr, nullptr, nullptr,
+                         nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, per_sample,
+                         qp ? &qa : nullptr, bytes);
+}
+
+int adjoint_workspace_bytes(const purin_cp_plan* p, int32_t entry, int64_t batch,
+                            const purin_cp_adjoint_options& o, int64_t* bytes) {
+  return p->dtype == PURIN_CP_F64 ? adjoint_bytes_t<double>(p, entry, batch, o, bytes)
+                                  : adjoint_bytes_t<float>(p, entry, batch, o, bytes);
 }
 
 }  // namespace purin

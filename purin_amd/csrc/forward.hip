@@ -284,7 +284,8 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
                      "max_iterations exceeds the plan's step schedule (" +
                          std::to_string(p->res_sched_len) +
                          " iterations) in the no-allocation entry point");
-  if (int rc = ensure_schedule(p, o.max_iterations, st, false)) return rc;
+  const void* sched = nullptr;
+  if (int rc = ensure_schedule(p, o.max_iterations, st, false, &sched)) return rc;
   Res<T> R{};
   R.n = (int)p->n;
   R.m = (int)p->m;
@@ -327,7 +328,7 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   R.D0s = D0s;
   R.Ls = Ls;
   R.Hs = Hs;
-  R.sched = (const T*)p->res_sched;
+  R.sched = (const T*)sched;
   R.iters = o.max_iterations;
   R.Y = (T*)(sv + L.Y);
   R.D = (T*)(sv + L.D);
@@ -349,7 +350,7 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     t.iterations = o.max_iterations;
     t.loop_ms = ms;
     t.resident = 1;
-    p->timing = t;
+    record_timing(p, t);
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
   }
@@ -551,6 +552,16 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     evd.resize((size_t)o.max_iterations);
     for (auto& e : evd) PURIN_HIP(hipEventCreate(&e));
   }
+  if (early) {  // the loop reads the device's all-done count every ``check`` iterations
+    bool cap = false;
+    if (int rc = stream_capturing(st, &cap)) return rc;
+    if (cap)
+      return set_error(PURIN_CP_ERR_ARG,
+                       "early stop on the streaming passes reads a device flag (a stream "
+                       "synchronisation): not under stream capture; capture fixed iterations "
+                       "(early_stop = 0) or a problem the resident kernel takes");
+  }
+  HostWords host(p);
   int64_t it = 0;
   for (; it < o.max_iterations; ++it) {
     A.sigma = sigma;
@@ -625,9 +636,9 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
       theta = nt;
     }
     if (early && ((it + 1) % check == 0)) {
-      PURIN_HIP(hipMemcpyAsync(p->pinned, ndone, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+      PURIN_HIP(hipMemcpyAsync(host.get(), ndone, sizeof(int32_t), hipMemcpyDeviceToHost, st));
       PURIN_HIP(hipStreamSynchronize(st));
-      if (p->pinned[0] >= batch) {
+      if (host.get()[0] >= batch) {
         ++it;
         break;
       }
@@ -655,7 +666,7 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
     t.loop_ms = total;
     t.linear_kybar = lin ? 1 : 0;
     t.narrow_columns = col_q && !early ? 1 : 0;
-    p->timing = t;
+    record_timing(p, t);
     for (auto& e : ev) (void)hipEventDestroy(e);
     for (auto& e : evd) (void)hipEventDestroy(e);
   }
@@ -720,17 +731,41 @@ int scratch_init_device(int device) {
   return PURIN_CP_OK;
 }
 
-// This call's buffers: the plan workspace (grown stream-ordered) or, for the
-// no-allocation entry, the device's scratch array.
+// A call that would synchronise its stream -- timing (HIP events), or early
+// stop on the streaming passes (the all-done flag read every check_every
+// iterations) -- is refused on a stream under capture before it enqueues
+// anything.  ``streaming_only``: the call cannot take the resident kernel
+// (per-sample coefficients, the QP).
+template <typename T>
+static int check_capture(purin_cp_plan* p, hipStream_t st, const purin_cp_solve_options& o,
+                         bool streaming_only) {
+  const bool early = o.early_stop != 0;
+  const bool resident = !streaming_only && resident_lds<T>(p, early) && !o.streaming && !p->diag;
+  if (!o.timing && !(early && !resident)) return PURIN_CP_OK;
+  bool cap = false;
+  if (int rc = stream_capturing(st, &cap)) return rc;
+  if (!cap) return PURIN_CP_OK;
+  return set_error(PURIN_CP_ERR_ARG,
+                   o.timing ? "timing synchronises the stream: not under stream capture"
+                            : "early stop on the streaming passes reads a device flag (a stream "
+                              "synchronisation): not under stream capture; capture fixed "
+                              "iterations (early_stop = 0) or a problem the resident kernel takes");
+}
+
+// This call's buffers: the caller's workspace, the plan workspace (grown
+// stream-ordered) or, for the no-allocation entry, the device's scratch array.
 template <typename T>
 static int prepare_buffers(purin_cp_plan* p, hipStream_t st, int64_t batch, void* saved,
                            Layout* L, char** sv, char** ws, bool values = false, int extras = 0,
-                           bool noalloc = false) {
+                           bool noalloc = false, const purin_cp_solve_options* o = nullptr) {
   *L = make_layout(p, batch, values, extras);
   int err = PURIN_CP_OK;
   const size_t need = L->ws_end + (saved ? 0 : L->saved_end);
   char* base = nullptr;
-  if (noalloc) {
+  if (o && o->workspace) {  // the caller's: nothing is allocated, nothing of the plan's changes
+    base = (char*)workspace(p, need, st, &err, false, o->workspace, o->workspace_bytes);
+    if (!base) return err;
+  } else if (noalloc) {
     int cur = -1;
     PURIN_HIP(hipGetDevice(&cur));
     if (cur != p->device)
@@ -804,9 +839,10 @@ static int solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T* 
   if (!target || !lower || !upper || (p->m && !rhs))
     return set_error(PURIN_CP_ERR_ARG, "NULL input array");
   if (o.max_iterations < 1) return set_error(PURIN_CP_ERR_ARG, "max_iterations must be a positive integer");
+  if ((rc = check_capture<T>(p, st, o, false))) return rc;
   Layout L;
   char *sv, *ws;
-  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws))) return rc;
+  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, false, 0, false, &o))) return rc;
   const int64_t Bp = L.Bp, n = p->n, m = p->m;
   write_header<T>(st, sv, batch, Bp, 0, o.shared_bounds, p);
   to_minor<T>(st, target, batch, n, n, (T*)(sv + L.Tt), Bp, nullptr, 0);
@@ -861,8 +897,9 @@ static int project_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const T
                      "max_iterations exceeds the plan's step schedule (" +
                          std::to_string(p->res_sched_len) +
                          " iterations) in the no-allocation entry point");
+  if ((rc = check_capture<T>(p, st, o, per_sample))) return rc;
   if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, per_sample,
-                               mult0 ? kLayoutWarm : 0, noalloc)))
+                               mult0 ? kLayoutWarm : 0, noalloc, &o)))
     return rc;
   const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
   constexpr int64_t TS = tile_samples<T>();
@@ -979,9 +1016,11 @@ static int qp_solve_impl(purin_cp_plan* p, hipStream_t st, int64_t batch, const 
   if (!(o.tolerance > 0.0) || !std::isfinite(o.tolerance))
     return set_error(PURIN_CP_ERR_ARG, "tolerance must be positive and finite");
   if (o.shared_bounds) return set_error(PURIN_CP_ERR_ARG, "the diagonal QP takes per-sample bounds");
+  if ((rc = check_capture<T>(p, st, o, true))) return rc;
   Layout L;
   char *sv, *ws;
-  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, true, dual0 ? kLayoutWarm : 0)))
+  if ((rc = prepare_buffers<T>(p, st, batch, saved, &L, &sv, &ws, true, dual0 ? kLayoutWarm : 0,
+                               false, &o)))
     return rc;
   const int64_t Bp = L.Bp, n = p->n, m = p->m, M = p->M;
   constexpr int64_t TS = tile_samples<T>();
@@ -1115,6 +1154,37 @@ int purin_cp_qp_solve(purin_cp_plan* p, void* stream, int64_t batch, const void*
                               converged, saved);
 }
 
+
+int64_t purin_cp_workspace_bytes(const purin_cp_plan* p, int32_t entry, int64_t batch,
+                                 const purin_cp_adjoint_options* aopts) {
+  if (!p) return set_error(PURIN_CP_ERR_ARG, "NULL plan"), -1;
+  if (batch < 1) return set_error(PURIN_CP_ERR_ARG, "batch must be positive"), -1;
+  auto forward = [&](bool values, int extras) -> int64_t {
+    const Layout L = make_layout(p, batch, values, extras);
+    return (int64_t)(L.ws_end + L.saved_end);  // saved == NULL puts the state in the workspace
+  };
+  switch (entry) {
+    case PURIN_CP_ENTRY_SPMM: return forward(false, kLayoutSpmm);
+    case PURIN_CP_ENTRY_SOLVE: return forward(false, 0);
+    case PURIN_CP_ENTRY_PROJECT: return forward(false, kLayoutWarm);
+    case PURIN_CP_ENTRY_PROJECT_VALUES:
+    case PURIN_CP_ENTRY_QP_SOLVE:
+    case PURIN_CP_ENTRY_DENSE_SOLVE: return forward(true, kLayoutWarm);
+    case PURIN_CP_ENTRY_ADJOINT:
+    case PURIN_CP_ENTRY_ADJOINT_VALUES:
+    case PURIN_CP_ENTRY_QP_ADJOINT:
+    case PURIN_CP_ENTRY_DENSE_ADJOINT: {
+      purin_cp_adjoint_options o;
+      purin_cp_default_adjoint_options(&o);
+      if (aopts) o = *aopts;
+      int64_t bytes = -1;
+      if (adjoint_workspace_bytes(p, entry, batch, o, &bytes) != PURIN_CP_OK) return -1;
+      return bytes;
+    }
+    default:
+      return set_error(PURIN_CP_ERR_ARG, "unknown entry point " + std::to_string(entry)), -1;
+  }
+}
 
 int64_t purin_cp_saved_bytes(const purin_cp_plan* p, int64_t batch) {
   if (!p || batch < 1) return -1;

@@ -31,6 +31,11 @@ constexpr int kLayoutWarm = 2;  // MF: warm-start multipliers / duals in batch-m
 
 Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values = false, int extras = 0);
 
+// Workspace bytes of an adjoint entry point (purin_cp_workspace_bytes; adjoint.hip):
+// the largest over its optional arguments.
+int adjoint_workspace_bytes(const purin_cp_plan* p, int32_t entry, int64_t batch,
+                            const purin_cp_adjoint_options& o, int64_t* bytes);
+
 // Per-sample coefficient arrays prepared for one call (see persample.hpp).
 template <typename T>
 struct PerSample {

@@ -14,6 +14,8 @@
 
 #include <algorithm>
 #include <functional>
+#include <map>
+#include <mutex>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -32,7 +34,21 @@ int set_error(int code, const std::string& msg) {
 }
 
 int hip_check(hipError_t e, const char* what) {
+  (void)hipGetLastError();  // reported here: do not leave it for a later call's launch check
   return set_error(PURIN_CP_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int raise_lds_cap(const void* kernel, size_t bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, size_t> caps;
+  int dev = 0;
+  PURIN_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  size_t& cap = caps[{dev, kernel}];
+  if (bytes <= cap) return PURIN_CP_OK;
+  PURIN_HIP(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+  cap = bytes;
+  return PURIN_CP_OK;
 }
 
 size_t elem_size(const purin_cp_plan* p) { return p->dtype == PURIN_CP_F64 ? 8 : 4; }
@@ -42,11 +58,65 @@ int64_t padded_batch(const purin_cp_plan* p, int64_t batch) {
   return round_up(std::max<int64_t>(batch, 1), tile);
 }
 
-void* workspace(purin_cp_plan* p, size_t bytes, hipStream_t stream, int* err, bool adjoint) {
+int stream_capturing(hipStream_t stream, bool* capturing) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  PURIN_HIP(hipStreamIsCapturing(stream, &cs));
+  *capturing = cs != hipStreamCaptureStatusNone;
+  return PURIN_CP_OK;
+}
+
+void record_timing(purin_cp_plan* p, const purin_cp_timing& t) {
+  std::lock_guard<std::mutex> lock(p->mu);
+  p->timing = t;
+}
+
+HostWords::HostWords(purin_cp_plan* p) : p_(p) {
+  uint32_t busy = p->pinned ? p->pinned_busy.load() : ~0u;
+  while (p->pinned) {
+    int s = 0;
+    while (s < kPinnedSlots && (busy >> s) & 1u) ++s;
+    if (s == kPinnedSlots) break;
+    if (p->pinned_busy.compare_exchange_weak(busy, busy | (1u << s))) {
+      slot_ = s;
+      ptr_ = p->pinned + (size_t)s * (kPinnedBytes / sizeof(int32_t));
+      return;
+    }
+  }
+  heap_.assign(kPinnedBytes / sizeof(int64_t), 0);
+  ptr_ = reinterpret_cast<int32_t*>(heap_.data());
+}
+
+HostWords::~HostWords() {
+  if (slot_ >= 0) p_->pinned_busy.fetch_and(~(1u << slot_));
+}
+
+void* workspace(purin_cp_plan* p, size_t bytes, hipStream_t stream, int* err, bool adjoint,
+                void* caller, int64_t caller_bytes) {
   *err = PURIN_CP_OK;
+  if (caller) {
+    if (caller_bytes < 0 || (size_t)caller_bytes < bytes) {
+      *err = set_error(PURIN_CP_ERR_ARG, "workspace too small: the call needs " +
+                                             std::to_string(bytes) + " bytes, " +
+                                             std::to_string(caller_bytes) + " given");
+      return nullptr;
+    }
+    if (reinterpret_cast<uintptr_t>(caller) % 256 != 0) {
+      *err = set_error(PURIN_CP_ERR_ARG, "workspace must be 256-byte aligned");
+      return nullptr;
+    }
+    return caller;
+  }
   void*& buf = adjoint ? p->aws : p->ws;
   size_t& have = adjoint ? p->aws_bytes : p->ws_bytes;
   if (bytes <= have && buf) return buf;
+  bool cap = false;
+  if ((*err = stream_capturing(stream, &cap))) return nullptr;
+  if (cap) {
+    *err = set_error(PURIN_CP_ERR_ARG,
+                     "the plan's workspace must grow, which allocates: under stream capture "
+                     "pass a workspace (purin_cp_workspace_bytes)");
+    return nullptr;
+  }
   // Stream-ordered growth: the new buffer is usable by work enqueued after it
   // on ``stream``, and the old one is released once the stream's earlier
   // kernels (which may still read it) are done.  No host or device-wide sync.
@@ -96,38 +166,27 @@ static std::vector<T> step_schedule(const purin_cp_plan* p, int64_t iters) {
   return h;
 }
 
-int ensure_schedule(purin_cp_plan* p, int64_t iters, hipStream_t stream, bool at_create) {
-  if (p->res_sched && p->res_sched_len >= iters) return PURIN_CP_OK;
+int ensure_schedule(purin_cp_plan* p, int64_t iters, hipStream_t stream, bool at_create,
+                    const void** sched) {
+  std::lock_guard<std::mutex> lock(p->mu);
+  if (p->res_sched && p->res_sched_len >= iters) {
+    if (sched) *sched = p->res_sched;
+    return PURIN_CP_OK;
+  }
+  if (!at_create) {
+    bool cap = false;
+    if (int rc = stream_capturing(stream, &cap)) return rc;
+    if (cap)
+      return set_error(PURIN_CP_ERR_ARG,
+                       "max_iterations exceeds the plan's step schedule (" +
+                           std::to_string(p->res_sched_len) +
+                           " iterations), whose extension allocates: not under stream capture");
+  }
   const int64_t len = std::max(iters, p->res_sched_len * 2);
   const size_t es = elem_size(p);
   const size_t bytes = (size_t)4 * len * es;
-  if (at_create) {
-    std::vector<unsigned char> h(bytes);
-    if (p->dtype == PURIN_CP_F64) {
-      auto v = step_schedule<double>(p, len);
-      std::memcpy(h.data(), v.data(), bytes);
-    } else {
-      auto v = step_schedule<float>(p, len);
-      std::memcpy(h.data(), v.data(), bytes);
-    }
-    // a stream-ordered allocation like the grown ones, so that every schedule
-    // buffer is released the same way (hipFreeAsync)
-    void* d = nullptr;
-    hipError_t e = hipMallocAsync(&d, bytes, nullptr);
-    if (e != hipSuccess) return set_error(PURIN_CP_ERR_NOMEM, "schedule hipMallocAsync failed");
-    e = hipMemcpyAsync(d, h.data(), bytes, hipMemcpyHostToDevice, nullptr);
-    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
-    if (e != hipSuccess) {
-      (void)hipFreeAsync(d, nullptr);
-      return hip_check(e, "schedule upload");
-    }
-    p->res_sched = d;
-    p->res_sched_len = len;
-    return PURIN_CP_OK;
-  }
-  // a longer call: a new pinned staging copy (kept until the plan is destroyed,
-  // so no host buffer is reused while a copy from it may be pending) and a
-  // stream-ordered replacement of the device buffer
+  // the host schedule in pinned staging (kept until the plan is destroyed: no
+  // host buffer is freed while a copy from it may be pending)
   void* staging = nullptr;
   hipError_t e = hipHostMalloc(&staging, bytes, hipHostMallocDefault);
   if (e != hipSuccess) return set_error(PURIN_CP_ERR_NOMEM, "schedule hipHostMalloc failed");
@@ -139,17 +198,22 @@ int ensure_schedule(purin_cp_plan* p, int64_t iters, hipStream_t stream, bool at
     auto v = step_schedule<float>(p, len);
     std::memcpy(staging, v.data(), bytes);
   }
+  // upload on the plan's own stream and wait for it alone: the buffer is
+  // complete before any call, on any stream, can read it
   void* d = nullptr;
-  e = hipMallocAsync(&d, bytes, stream);
+  e = hipMallocAsync(&d, bytes, p->upload);
   if (e != hipSuccess) return set_error(PURIN_CP_ERR_NOMEM, "schedule hipMallocAsync failed");
-  e = hipMemcpyAsync(d, staging, bytes, hipMemcpyHostToDevice, stream);
-  if (e != hipSuccess) return hip_check(e, "schedule upload");
-  if (p->res_sched) {
-    e = hipFreeAsync(p->res_sched, stream);
-    if (e != hipSuccess) return hip_check(e, "schedule hipFreeAsync");
+  e = hipMemcpyAsync(d, staging, bytes, hipMemcpyHostToDevice, p->upload);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->upload);
+  if (e != hipSuccess) {
+    (void)hipFreeAsync(d, p->upload);
+    return hip_check(e, "schedule upload");
   }
+  // kernels enqueued earlier (on any stream) may still read the old schedule
+  if (p->res_sched) p->sched_retired.push_back(p->res_sched);
   p->res_sched = d;
   p->res_sched_len = len;
+  if (sched) *sched = d;
   return PURIN_CP_OK;
 }
 
@@ -953,6 +1017,8 @@ void purin_cp_default_solve_options(purin_cp_solve_options* o) {
   o->timing = 0;
   o->streaming = 0;
   o->reserved = 0;
+  o->workspace = nullptr;
+  o->workspace_bytes = 0;
 }
 
 void purin_cp_default_adjoint_options(purin_cp_adjoint_options* o) {
@@ -964,12 +1030,15 @@ void purin_cp_default_adjoint_options(purin_cp_adjoint_options* o) {
   o->adjoint_tolerance = 1e-8;
   o->force_eligible = 0;
   o->reserved = 0;
+  o->workspace = nullptr;
+  o->workspace_bytes = 0;
+  o->arnoldi_iterations = nullptr;
 }
 
 const char* purin_cp_last_error(void) { return g_error.c_str(); }
 
 const char* purin_cp_build_info(void) {
-  return "purin_cp abi=1 target=gfx950 (CDNA4) kernels=HIP";
+  return "purin_cp abi=2 target=gfx950 (CDNA4) kernels=HIP";
 }
 
 int purin_cp_plan_create(purin_cp_plan** out, int32_t dtype, int64_t n, int64_t me, int64_t mi,
@@ -1020,8 +1089,13 @@ int purin_cp_plan_create(purin_cp_plan** out, int32_t dtype, int64_t n, int64_t 
   int rc = dtype == PURIN_CP_F64 ? build<double>(p, indptr, indices, values)
                                  : build<float>(p, indptr, indices, values);
   if (rc == PURIN_CP_OK) {
-    hipError_t e = hipHostMalloc((void**)&p->pinned, kPinnedBytes, hipHostMallocDefault);
+    hipError_t e = hipHostMalloc((void**)&p->pinned, (size_t)kPinnedSlots * kPinnedBytes,
+                                 hipHostMallocDefault);
     if (e != hipSuccess) rc = hip_check(e, "hipHostMalloc");
+  }
+  if (rc == PURIN_CP_OK) {  // default priority, not synchronising with the null stream
+    hipError_t e = hipStreamCreateWithFlags(&p->upload, hipStreamNonBlocking);
+    if (e != hipSuccess) rc = hip_check(e, "hipStreamCreateWithFlags");
   }
   // the resident kernel's step schedule, for calls of up to kSchedCapacity iterations
   if (rc == PURIN_CP_OK && p->res_ok) rc = ensure_schedule(p, kSchedCapacity, nullptr, true);
@@ -1044,9 +1118,11 @@ void purin_cp_plan_destroy(purin_cp_plan* p) {
   if (p->ws) (void)hipFreeAsync(p->ws, nullptr);
   if (p->aws) (void)hipFreeAsync(p->aws, nullptr);
   if (p->res_sched) (void)hipFreeAsync(p->res_sched, nullptr);
+  for (void* d : p->sched_retired) (void)hipFreeAsync(d, nullptr);
   (void)hipDeviceSynchronize();
   for (void* h : p->sched_staging) (void)hipHostFree(h);
   if (p->pinned) (void)hipHostFree(p->pinned);
+  if (p->upload) (void)hipStreamDestroy(p->upload);
   delete p;
 }
 
@@ -1070,17 +1146,21 @@ int purin_cp_plan_get_info(const purin_cp_plan* p, purin_cp_plan_info* info) {
   info->resident_stream_bytes_early = p->res_ok ? p->res_iter_bytes_e : 0;
   info->resident_row_slots = p->res_ok ? (int64_t)p->res_mr * kResThreads : 0;
   info->resident_col_slots = p->res_ok ? (int64_t)p->res_mc * kResThreads : 0;
+  info->workspace_bytes = (int64_t)p->ws_bytes;
+  info->adjoint_workspace_bytes = (int64_t)p->aws_bytes;
   return PURIN_CP_OK;
 }
 
 int purin_cp_last_timing(const purin_cp_plan* p, purin_cp_timing* t) {
   if (!p || !t) return set_error(PURIN_CP_ERR_ARG, "NULL argument");
+  std::lock_guard<std::mutex> lock(const_cast<purin_cp_plan*>(p)->mu);
   *t = p->timing;
   return PURIN_CP_OK;
 }
 
 int purin_cp_last_adjoint_stats(const purin_cp_plan* p, purin_cp_adjoint_stats* s) {
   if (!p || !s) return set_error(PURIN_CP_ERR_ARG, "NULL argument");
+  std::lock_guard<std::mutex> lock(const_cast<purin_cp_plan*>(p)->mu);
   *s = p->adjoint_stats;
   return PURIN_CP_OK;
 }
@@ -1088,8 +1168,10 @@ int purin_cp_last_adjoint_stats(const purin_cp_plan* p, purin_cp_adjoint_stats* 
 int purin_cp_last_adjoint_iterations(const purin_cp_plan* p, void* stream, int64_t batch,
                                      int32_t* iterations) {
   if (!p || !iterations) return set_error(PURIN_CP_ERR_ARG, "NULL argument");
+  std::lock_guard<std::mutex> lock(const_cast<purin_cp_plan*>(p)->mu);
   if (!p->adj_steps)
-    return set_error(PURIN_CP_ERR_ARG, "no GMRES adjoint call has run on this plan");
+    return set_error(PURIN_CP_ERR_ARG,
+                     "no GMRES adjoint call on the plan's workspace has run on this plan");
   if (batch != p->adj_steps_batch)
     return set_error(PURIN_CP_ERR_ARG, "batch differs from the last adjoint call's");
   PURIN_HIP(hipMemcpyAsync(iterations, p->adj_steps, (size_t)batch * sizeof(int32_t),

@@ -1,7 +1,9 @@
 // Plan object behind the opaque purin_cp_plan handle.
 #pragma once
 
+#include <atomic>
 #include <cstdint>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -18,7 +20,8 @@ constexpr int kResThreads = 1024;   // threads of a resident workgroup
 constexpr int kResMaxSlots = 4;     // rows / columns per thread (n, m <= 4096)
 constexpr double kMallBytes = 256.0 * 1024 * 1024;  // MI355X Infinity Cache (MALL)
 constexpr double kL2Bytes = 4.0 * 1024 * 1024;      // L2 of one MI355X XCD
-constexpr int kPinnedBytes = 4096;  // host-pinned flag words: counters and per-step counts
+constexpr int kPinnedBytes = 4096;  // host-pinned flag words of one call: counters, per-step counts
+constexpr int kPinnedSlots = 16;    // calls that may read device flags at once through pinned memory
 // Iterations of the step schedule built with the plan (the schedule of k
 // iterations is a prefix of any longer one, so calls up to this count read it
 // as it is; longer calls extend it stream-ordered).
@@ -77,7 +80,8 @@ struct purin_cp_plan {
   size_t ws_bytes = 0;
   void* aws = nullptr;        // adjoint workspace
   size_t aws_bytes = 0;
-  int32_t* pinned = nullptr;  // host-pinned flag words
+  int32_t* pinned = nullptr;  // host-pinned flag words: kPinnedSlots slots of kPinnedBytes
+  std::atomic<uint32_t> pinned_busy{0};  // bit s: slot s is held by a call (HostWords)
 
   // resident (on-chip) iteration schedule: degree-sorted rows/columns, one
   // thread per (slot, row) and (slot, column); built when n and m fit
@@ -96,6 +100,10 @@ struct purin_cp_plan {
   void* res_sched = nullptr;         // per-iteration (sigma, a, delta, theta)
   int64_t res_sched_len = 0;         // iterations the schedule holds
   std::vector<void*> sched_staging;  // pinned host copies of grown schedules (freed with the plan)
+  std::vector<void*> sched_retired;  // replaced schedules: kernels on other streams may still
+                                     // read them, so they are freed with the plan
+  hipStream_t upload = nullptr;      // the plan's own stream for schedule uploads
+  std::mutex mu;                     // guards the schedule, timing, adjoint stats and steps
 
   int device = 0;             // the device the plan was created on (its buffers live there)
 
@@ -112,11 +120,46 @@ int set_error(int code, const std::string& msg);
 int hip_check(hipError_t e, const char* what);
 int64_t padded_batch(const purin_cp_plan* p, int64_t batch);
 size_t elem_size(const purin_cp_plan* p);
-void* workspace(purin_cp_plan* p, size_t bytes, hipStream_t stream, int* err, bool adjoint = false);
-// Make the resident step schedule hold at least ``iters`` iterations: built on
-// the host and uploaded synchronously at plan creation (at_create), or grown
-// stream-ordered on ``stream`` (pinned staging, hipMallocAsync / hipFreeAsync).
-int ensure_schedule(purin_cp_plan* p, int64_t iters, hipStream_t stream, bool at_create);
+// The plan-owned workspace (adjoint: the adjoint's), grown stream-ordered on
+// ``stream``; or the caller's ``caller`` (``caller_bytes``), checked for size and
+// alignment.  Calls on the plan's workspace must be ordered; a stream under
+// capture cannot grow it.
+void* workspace(purin_cp_plan* p, size_t bytes, hipStream_t stream, int* err, bool adjoint = false,
+                void* caller = nullptr, int64_t caller_bytes = 0);
+// Make the resident step schedule hold at least ``iters`` iterations and return
+// the buffer this call reads (*sched): built on the host and uploaded at plan
+// creation (at_create), or extended once by a longer call, which uploads the
+// new schedule on the plan's own stream and waits for that upload alone.  The
+// replaced buffer is kept until the plan is destroyed.  Thread-safe.
+int ensure_schedule(purin_cp_plan* p, int64_t iters, hipStream_t stream, bool at_create,
+                    const void** sched = nullptr);
+// *capturing = whether ``stream`` is under graph capture.
+int stream_capturing(hipStream_t stream, bool* capturing);
+// Record the timing of a call (purin_cp_last_timing).
+void record_timing(purin_cp_plan* p, const purin_cp_timing& t);
+// Make ``kernel`` accept ``bytes`` of dynamic LDS on the current device.  The
+// cap only ever rises (under a lock), so a concurrent call on another plan or
+// thread cannot lower it between another call's raise and its launch.
+int raise_lds_cap(const void* kernel, size_t bytes);
+
+// Host-visible words for one call's reads of device flags: a slot of the
+// plan's pinned pool, or, when concurrent calls hold every slot, host memory
+// of the call's own (the reads are followed by a stream synchronisation, so
+// an ordinary host buffer serves, staged by the runtime).
+class HostWords {
+ public:
+  explicit HostWords(purin_cp_plan* p);
+  ~HostWords();
+  HostWords(const HostWords&) = delete;
+  HostWords& operator=(const HostWords&) = delete;
+  int32_t* get() { return ptr_; }
+
+ private:
+  purin_cp_plan* p_;
+  int slot_ = -1;
+  std::vector<int64_t> heap_;
+  int32_t* ptr_ = nullptr;
+};
 // The no-allocation entry's scratch (forward.hip): look up this device's copy
 // of the static array once, with the device current.
 int scratch_init_device(int device);

@@ -19,8 +19,7 @@ static int launch_one(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds
                       bool early) {
   auto kern = early ? (sb ? k_resident_early<T, SLR, SLC, true> : k_resident_early<T, SLR, SLC, false>)
                     : (sb ? k_resident<T, SLR, SLC, true> : k_resident<T, SLR, SLC, false>);
-  PURIN_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds));
+  if (int rc = raise_lds_cap((const void*)kern, lds)) return rc;
   kern<<<dim3((unsigned)tiles), dim3(kResThreads), lds, st>>>(R);
   return PURIN_CP_OK;
 }

@@ -41,6 +41,17 @@ def _stream():
     return C.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+def _set_workspace(o, workspace):
+    """Point an options struct at a caller workspace (a device tensor) or leave
+    the plan's own (None)."""
+    if workspace is None:
+        return
+    if not isinstance(workspace, torch.Tensor) or not workspace.is_cuda:
+        raise ValueError("workspace must be a device tensor")
+    o.workspace = C.c_void_p(workspace.data_ptr())
+    o.workspace_bytes = workspace.numel() * workspace.element_size()
+
+
 def _flags(t):
     """A 0/1 uint8 flag array returned by the library, seen as bool without a copy
     (every flag the kernels write is exactly 0 or 1), so a call launches no
@@ -83,6 +94,7 @@ class AdjointOutput:
     info: torch.Tensor
     residual: torch.Tensor
     g_values: torch.Tensor | None = None
+    steps: torch.Tensor | None = None  # per-sample Arnoldi steps (arnoldi_iterations)
 
 
 @dataclass
@@ -199,6 +211,30 @@ class Plan:
     def saved_bytes(self, batch):
         return int(self.lib.purin_cp_saved_bytes(self.handle, int(batch)))
 
+    def workspace_bytes(self, entry, batch, *, restart=30, max_iterations=100):
+        """Caller-workspace bytes of an entry point (``purin_cp_workspace_bytes``);
+        ``entry`` is a name of ``_lib.ENTRY``; restart / max_iterations are the
+        adjoints' GMRES settings."""
+        o = _lib.default_adjoint_options()
+        o.restart = int(restart)
+        o.max_iterations = int(max_iterations)
+        n = int(self.lib.purin_cp_workspace_bytes(self.handle, _lib.ENTRY[entry], int(batch),
+                                                   C.byref(o)))
+        if n < 0:
+            _lib.check(_lib.ERR_ARG)
+        return n
+
+    def new_workspace(self, entry, batch, **kw):
+        """A device buffer of ``workspace_bytes(entry, batch, **kw)`` bytes."""
+        return torch.empty(self.workspace_bytes(entry, batch, **kw), dtype=torch.uint8,
+                           device=self.device)
+
+    def current_info(self):
+        """The plan's info now (its own workspaces' sizes change as calls grow them)."""
+        info = _lib.PlanInfo()
+        _lib.check(self.lib.purin_cp_plan_get_info(self.handle, C.byref(info)))
+        return info
+
     # ------------------------------------------------------------------
     def spmm(self, x, *, transpose=False, scaled=True):
         """``K x`` (``(B, n) -> (B, m)``) or ``K^T x`` over the kept rows."""
@@ -211,7 +247,7 @@ class Plan:
 
     def solve(self, rhs, target, lower, upper, *, dual0=None, tol=None, feasible=None,
               tolerance=1e-9, max_iterations=10000, early_stop=True, check_every=32,
-              shared_bounds=False, save=False, streaming=False, timing=False):
+              shared_bounds=False, save=False, streaming=False, timing=False, workspace=None):
         """Inner CP solve on the kept rows (``purin_cp_solve``), scaled units."""
         batch = target.shape[0]
         target = self._tensor(target, (batch, self.n), "target")
@@ -231,6 +267,7 @@ class Plan:
         o.shared_bounds = int(bool(shared_bounds))
         o.streaming = int(bool(streaming))
         o.timing = int(bool(timing))
+        _set_workspace(o, workspace)
         y = self._empty(batch, self.n)
         dual = self._empty(batch, self.m)
         it = self._empty(batch, dtype=torch.int32)
@@ -266,7 +303,7 @@ class Plan:
 
     def project(self, target, rhs, *, multipliers0=None, tolerance=1e-9, max_iterations=10000,
                 early_stop=True, check_every=32, shared_bounds=False, save=False, timing=False,
-                streaming=False, values=None, noalloc=False):
+                streaming=False, values=None, noalloc=False, workspace=None, saved=None):
         """Full projection (``purin_cp_project``): BoundProjection.solve semantics.
 
         ``values`` (B, nnz): per-sample coefficients in the plan's CSR entry order
@@ -274,6 +311,10 @@ class Plan:
         ``noalloc``: run ``purin_cp_project_noalloc`` (the library allocates no
         device memory during the call; its buffers sit in a static per-GPU
         scratch array of ``_lib.NOALLOC_SCRATCH_BYTES``).
+        ``workspace``: a device buffer of at least ``workspace_bytes("project"
+        or "project_values", B)`` bytes for the call's scratch (calls with
+        their own workspaces may overlap on one plan); ``saved``: a buffer of
+        ``saved_bytes(B)`` to fill (``save=True`` allocates one).
         """
         batch = target.shape[0]
         M = self.me + self.mi
@@ -291,6 +332,7 @@ class Plan:
         o.shared_bounds = int(bool(shared_bounds))
         o.timing = int(bool(timing))
         o.streaming = int(bool(streaming))
+        _set_workspace(o, workspace)
         y = self._empty(batch, self.n)
         mult = self._empty(batch, M)
         slacks = self._empty(batch, self.mi)
@@ -299,7 +341,8 @@ class Plan:
         res = self._empty(batch)
         fin = self._empty(batch, dtype=torch.uint8)
         elig = self._empty(batch, dtype=torch.uint8)
-        saved = self._empty(self.saved_bytes(batch), dtype=torch.uint8) if save else None
+        if saved is None and save:
+            saved = self._empty(self.saved_bytes(batch), dtype=torch.uint8)
         if values is not None:
             if noalloc:
                 raise ValueError("the no-allocation entry takes the plan's own coefficients")
@@ -318,7 +361,7 @@ class Plan:
 
     def qp_solve(self, q, c, rhs, lower, upper, *, values=None, y0=None, dual0=None,
                  tolerance=1e-9, max_iterations=10000, early_stop=True, check_every=32,
-                 save=False, timing=False):
+                 save=False, timing=False, workspace=None):
         """General diagonal QP (``purin_cp_qp_solve``): PreparedDiagonalQP.solve
         semantics on a plan created with ``bound_presolve=False``."""
         batch = q.shape[0]
@@ -337,6 +380,7 @@ class Plan:
         o.early_stop = int(bool(early_stop))
         o.check_every = int(check_every)
         o.timing = int(bool(timing))
+        _set_workspace(o, workspace)
         y = self._empty(batch, self.n)
         mult = self._empty(batch, M)
         slacks = self._empty(batch, self.mi)
@@ -354,7 +398,7 @@ class Plan:
 
     def dense_solve(self, q, c, rhs, lower, upper, *, values=None, y0=None, dual0=None,
                     tolerance=1e-9, max_iterations=5000, early_stop=True, check_every=32,
-                    save=False, timing=False):
+                    save=False, timing=False, workspace=None):
         """The dense adapter's forward (``purin_cp_dense_solve``, solve_dense
         semantics) on a plan with bound_presolve, row_scaling, norm_bound and
         diagonal_preconditioning off.  Returns (y, multipliers, iterations, saved)."""
@@ -374,6 +418,7 @@ class Plan:
         o.early_stop = int(bool(early_stop))
         o.check_every = int(check_every)
         o.timing = int(bool(timing))
+        _set_workspace(o, workspace)
         y = self._empty(batch, self.n)
         mult = self._empty(batch, M)
         it = self._empty(batch, dtype=torch.int32)
@@ -385,7 +430,7 @@ class Plan:
         return y, mult, it, saved
 
     def dense_adjoint(self, saved, q, c, cot_y, *, values=None, cot_dual=None, tolerance=1e-6,
-                      max_iterations=50):
+                      max_iterations=50, workspace=None):
         """The dense layer's backward (``purin_cp_dense_adjoint``): BiCGSTAB over the
         batch with the frozen prox.  Returns a QPAdjointOutput (valid/info None)."""
         batch = cot_y.shape[0]
@@ -398,6 +443,7 @@ class Plan:
         o = _lib.default_adjoint_options()
         o.tolerance = float(tolerance)
         o.max_iterations = int(max_iterations)
+        _set_workspace(o, workspace)
         gq, gc = self._empty(batch, self.n), self._empty(batch, self.n)
         gv = self._empty(batch, self.nnz)
         gr = self._empty(batch, M)
@@ -409,7 +455,7 @@ class Plan:
 
     def qp_adjoint(self, saved, q, c, cot_y, *, values=None, cot_dual=None, tolerance=1e-9,
                    atol=0.0, restart=30, max_iterations=100, adjoint_tolerance=1e-8,
-                   force_eligible=False):
+                   force_eligible=False, workspace=None):
         """Implicit VJP of ``qp_solve`` (``purin_cp_qp_adjoint``)."""
         batch = cot_y.shape[0]
         M = self.me + self.mi
@@ -425,6 +471,7 @@ class Plan:
         o.max_iterations = int(max_iterations)
         o.adjoint_tolerance = float(adjoint_tolerance)
         o.force_eligible = int(bool(force_eligible))
+        _set_workspace(o, workspace)
         gq, gc = self._empty(batch, self.n), self._empty(batch, self.n)
         gv = self._empty(batch, self.nnz)
         gr = self._empty(batch, M)
@@ -440,11 +487,14 @@ class Plan:
 
     def adjoint(self, saved, target, rhs, cot_y, *, tolerance=1e-9, atol=0.0, restart=30,
                 max_iterations=100, adjoint_tolerance=1e-8, force_eligible=False,
-                bounds_grad=False, rhs_rows=None, values=None):
+                bounds_grad=False, rhs_rows=None, values=None, workspace=None,
+                return_steps=False):
         """Implicit VJP at a saved forward state (``purin_cp_adjoint``).
 
         ``values``: the per-sample coefficients of a ``project(..., values=...)``
         state (``purin_cp_adjoint_values``); the result then carries ``g_values``.
+        ``workspace``: a caller workspace (``workspace_bytes("adjoint", B)``);
+        ``return_steps``: fill ``steps`` with the per-sample Arnoldi steps.
         """
         batch = cot_y.shape[0]
         rows = rhs_rows if rhs_rows is not None else self.me + self.mi
@@ -460,6 +510,10 @@ class Plan:
         o.max_iterations = int(max_iterations)
         o.adjoint_tolerance = float(adjoint_tolerance)
         o.force_eligible = int(bool(force_eligible))
+        _set_workspace(o, workspace)
+        steps = self._empty(batch, dtype=torch.int32) if return_steps else None
+        if steps is not None:
+            o.arnoldi_iterations = _i32(steps)
         gt = self._empty(batch, self.n)
         gr = self._empty(batch, rows)
         gl = self._empty(batch, self.n) if bounds_grad else None
@@ -473,9 +527,9 @@ class Plan:
             _lib.check(self.lib.purin_cp_adjoint_values(
                 self.handle, _stream(), batch, _ptr(saved), _ptr(values), _ptr(cot), C.byref(o),
                 _ptr(gt), _ptr(gr), _ptr(gv), _u8(valid), _i32(info), _ptr(res)))
-            return AdjointOutput(gt, gr, None, None, _flags(valid), info, res, gv)
+            return AdjointOutput(gt, gr, None, None, _flags(valid), info, res, gv, steps)
         _lib.check(self.lib.purin_cp_adjoint(
             self.handle, _stream(), batch, _ptr(saved), _ptr(target), _ptr(rhs), _ptr(cot),
             C.byref(o), _ptr(gt), _ptr(gr), _ptr(gl), _ptr(gu), _u8(valid), _i32(info),
             _ptr(res)))
-        return AdjointOutput(gt, gr, gl, gu, _flags(valid), info, res)
+        return AdjointOutput(gt, gr, gl, gu, _flags(valid), info, res, None, steps)

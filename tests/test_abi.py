@@ -58,3 +58,52 @@ def test_invalid_plan_arguments_are_rejected_without_a_gpu():
     assert b"out of range" in lib.purin_cp_last_error()
     rc = lib.purin_cp_plan_create(ctypes.byref(handle), 7, 2, 1, 0, indptr, indices, values, None)
     assert rc == _lib.ERR_ARG
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """Every ctypes mirror of a header struct has the C compiler's size and
+    field offsets (the binding passes these structs by pointer)."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        import pytest
+
+        pytest.skip("no C compiler")
+    structs = {
+        "purin_cp_options": _lib.Options,
+        "purin_cp_plan_info": _lib.PlanInfo,
+        "purin_cp_solve_options": _lib.SolveOptions,
+        "purin_cp_timing": _lib.Timing,
+        "purin_cp_adjoint_stats": _lib.AdjointStats,
+        "purin_cp_adjoint_options": _lib.AdjointOptions,
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "purin_cp.h"',
+             "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'  printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True, capture_output=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    got = {}
+    for line in out.splitlines():
+        cname, what, value = line.split()
+        got[(cname, what)] = int(value)
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for field, _ in py._fields_:
+            assert got[(cname, field)] == getattr(py, field).offset, (cname, field)
+
+
+def test_entry_codes_match_the_header():
+    text = open(os.path.join(ROOT, "include", "purin_cp.h")).read()
+    codes = {m.group(1).lower(): int(m.group(2))
+             for m in re.finditer(r"PURIN_CP_ENTRY_(\w+)\s*=\s*(\d+)", text)}
+    assert codes == _lib.ENTRY

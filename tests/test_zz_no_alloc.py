@@ -93,3 +93,76 @@ def test_noalloc_rejects_what_does_not_fit():
     out = plan.project(small, rhs[:8], max_iterations=10, early_stop=False)
     torch.cuda.synchronize()
     assert np.all(np.isfinite(to_np(out.y)))
+
+
+def test_noalloc_allocates_nothing():
+    """On a fresh plan the no-allocation entry leaves the plan's workspace
+    unallocated, and after a regular call has sized it, a no-allocation call with
+    a larger batch leaves its size unchanged (purin_cp_plan_info.workspace_bytes)."""
+    torch = require_gpu()
+    w = workloads.small_random(23, n=300, me=40, mi=120, width=5, batch=96, accelerated=True,
+                               target_sd=0.5)
+    canon = canonical_from_workload(w)
+    plan = plan_for(canon, dtype=np.float64, accelerated=True)
+    rhs = np.tile(w.rhs, (96, 1))
+    for mode in ({}, dict(early_stop=True), dict(early_stop=True, streaming=True)):
+        kw = dict(max_iterations=300, tolerance=1e-3, early_stop=False)
+        kw.update(mode)
+        plan.project(w.target, rhs, noalloc=True, **kw)
+    torch.cuda.synchronize()
+    assert plan.current_info().workspace_bytes == 0
+    small = plan.project(w.target[:16], rhs[:16], max_iterations=300, early_stop=False)
+    torch.cuda.synchronize()
+    sized = plan.current_info().workspace_bytes
+    assert sized > 0
+    big = plan.project(w.target, rhs, max_iterations=300, early_stop=False, noalloc=True)
+    torch.cuda.synchronize()
+    assert plan.current_info().workspace_bytes == sized
+    np.testing.assert_array_equal(to_np(big.y)[:16], to_np(small.y))
+
+
+def test_noalloc_under_graph_capture():
+    """A fixed-iteration no-allocation projection captured into a graph and
+    replayed three times on new inputs (with eager calls and synchronisations
+    between the replays) gives the bits of purin_cp_project on each input.  An
+    early-stop call on the streaming passes, which would read a device flag, is
+    refused under capture before it enqueues anything."""
+    torch = require_gpu()
+    B = 64
+    w = workloads.small_random(24, n=300, me=40, mi=120, width=5, batch=B, accelerated=True,
+                               target_sd=0.5)
+    canon = canonical_from_workload(w)
+    plan = plan_for(canon, dtype=np.float64, accelerated=True)
+    rng = np.random.default_rng(6)
+    target = torch.as_tensor(w.target, device="cuda")
+    rhs = torch.as_tensor(np.tile(w.rhs, (B, 1)), device="cuda")
+    kw = dict(max_iterations=400, early_stop=False)
+    plan.project(target, rhs, noalloc=True, **kw)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    print("graph capture: capturing", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, capture_error_mode="relaxed"):
+        out = plan.project(target, rhs, noalloc=True, **kw)
+    torch.cuda.synchronize()
+    for k in range(3):
+        new_t = w.target + rng.normal(scale=0.2, size=w.target.shape)
+        target.copy_(torch.as_tensor(new_t, device="cuda"))
+        torch.cuda.synchronize()
+        print(f"graph capture: replay {k}", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        want = plan.project(torch.as_tensor(new_t, device="cuda"), rhs, **kw)
+        torch.cuda.synchronize()
+        _same(out, want, ("replay", k))
+    # refused before anything is enqueued
+    g2 = torch.cuda.CUDAGraph()
+    side = torch.zeros(4, device="cuda")
+    from purin_amd._lib import ERR_ARG, PurinError
+
+    with pytest.raises(PurinError) as err:
+        with torch.cuda.graph(g2, capture_error_mode="relaxed"):
+            side.add_(1.0)
+            plan.project(target, rhs, noalloc=True, max_iterations=50, early_stop=True,
+                         streaming=True)
+    assert err.value.code == ERR_ARG and "capture" in str(err.value)
+    torch.cuda.synchronize()
