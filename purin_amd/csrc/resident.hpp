@@ -619,12 +619,19 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)A.Kr;
   const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)A.Kr;
 
-  // registers: per row slot K y of the current iterate and the candidate
-  // dual of the next row update.  y lives in Gy (each thread reads its own
-  // entries); the targets and the scaled right-hand sides are re-read each
-  // iteration (L2), ahead of the gathers that hide their latency.
+  // registers: per row slot K y of the current iterate and, from the
+  // residual sweep to the decision, the committed dual the sweep replaced in
+  // Gd by the next candidate; the targets of the thread's columns and the
+  // scaled right-hand sides of its rows, loaded once (re-reading them each
+  // iteration from beyond L2 took 18.0 us per iteration at config 2's
+  // shape, holding them 15.3 us with a few spilled values, the floor without
+  // them 13.9 us).  y lives in Gy (each thread reads its own entries).
+  // With four row slots per thread (m > 3072) the held values would spill
+  // 116-228 bytes per lane, so those variants re-read them each iteration.
+  constexpr bool kHold = SLR <= 3;
   uint32_t soff_r[SLR], soff_c[SLC];
-  V ky[SLR], dn[SLR];
+  V ky[SLR], dk[SLR], tgh[kHold ? SLC : 1], rrh[kHold ? SLR : 1];
+  typedef const __attribute__((address_space(1))) V* GV;
   uint32_t ineq = 0, nanb = 0, rvalid = 0, cvalid = 0;
   // shared bounds equal on every column of the wavefront's slots: taken from
   // registers in the loop (as in k_resident; a ballot, no LDS)
@@ -641,9 +648,10 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     }
     if (j >= 0) cvalid |= 1u << c;
     soff_c[c] = j >= 0 ? (uint32_t)A.colent[c * NT + t] * 16u : trash_off;
-    // y0 = ybar0 = yhat (kernels.py:229-231)
-    lds_write<V>(soff_c[c],
-                 j >= 0 ? reinterpret_cast<const V*>(A.Ts)[tile * (int64_t)A.Kc + c * NT + t] : vzero);
+    // y0 = ybar0 = yhat (kernels.py:229-231); empty slots hold zeros
+    const V t0 = reinterpret_cast<const V*>(A.Ts)[tile * (int64_t)A.Kc + c * NT + t];
+    if constexpr (kHold) tgh[c] = t0;
+    lds_write<V>(soff_c[c], j >= 0 ? t0 : vzero);
   }
 #pragma unroll
   for (int r = 0; r < SLR; ++r) {
@@ -651,6 +659,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     if (i >= 0) rvalid |= 1u << r;
     soff_r[r] = i >= 0 ? (uint32_t)A.rowent[r * NT + t] * 16u : trash_off;
     if (i >= A.me) ineq |= 1u << r;  // kept rows: equalities first
+    if constexpr (kHold) rrh[r] = Rs[r * NT + t];  // zero on empty slots
     lds_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
   }
   if (t == 0) lds_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
@@ -673,7 +682,6 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   load_chunk(b0, A.stream, (uint64_t)first * CB, lane16);
   if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16);
   uint32_t pos = first + 1 + (pro & 1u);
-  typedef const __attribute__((address_space(1))) V* GV;
   // K y0 (= K ybar0) by one row sweep, and the first candidate duals; b0 then
   // holds the first column chunk
   {
@@ -682,7 +690,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     const uint32_t rc = rcnt, rl = rlast;
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
-      const V rr = Rs[r * NT + t];
+      const V rr = kHold ? rrh[kHold ? r : 0] : Rs[r * NT + t];
       ky[r] = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
                                         b0, b1, pos, A.stream, lane16, r == 0 && (pro & 1u));
       V p = lds_read<V>(soff_r[r]) + sigma0 * (ky[r] - rr);
@@ -690,32 +698,20 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
       }
-      dn[r] = p;
+      lds_write<V>(soff_r[r], p);  // the first iteration's d+ (every sample active)
     }
     if (pro & 2u) {  // the column pass's second chunk (its first is in b0)
       load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16);
       ++pos;
     }
   }
+  __syncthreads();
 
   for (int64_t it = 0; it < A.iters && act != 0u; ++it) {
     const __attribute__((address_space(4))) T* sc =
         (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
     const T a = sc[1], delta = sc[2], theta = sc[3];
-    // ---- row update: commit the candidate duals where the sample is active ----------
-#pragma unroll
-    for (int r = 0; r < SLR; ++r) {
-      V p = dn[r];
-      if (act != (1u << BT) - 1u) {
-        const V dold = lds_read<V>(soff_r[r]);
-#pragma unroll
-        for (int s = 0; s < BT; ++s)
-          if (!(act & (1u << s))) p[s] = dold[s];
-      }
-      lds_write<V>(soff_r[r], p);
-    }
-    __syncthreads();
-    // ---- column pass, masked, with the column diagnostics ------------------------------
+    // ---- column pass, masked, with the column diagnostics (Gd holds d+) ---------------
     V qp = vzero, qd = vzero, qc = vzero;
     V carry = vzero;  // the head of the next slot (a chunk shared by two slots)
     // the slot tables, opaque to the loop so that their fields are decoded at
@@ -727,11 +723,14 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       typedef const __attribute__((address_space(1))) T* GP;
       GP lb = (GP)A.Ls;
       GP hb = (GP)A.Hs;
-      GP tb = (GP)A.Ts;
-      // the target (per tile, beyond L2) ahead of the gathers that hide its
-      // latency; the bounds after them (register pressure)
-      asm volatile("" : "+s"(tb));
-      const V tg = ((GV)tb)[tile * (int64_t)A.Kc + c * NT + t];
+      V tg;
+      if constexpr (kHold) {
+        tg = tgh[kHold ? c : 0];
+      } else {  // per tile, beyond L2: loaded ahead of the gathers that hide its latency
+        GP tb = (GP)A.Ts;
+        asm volatile("" : "+s"(tb));
+        tg = ((GV)tb)[tile * (int64_t)A.Kc + c * NT + t];
+      }
       const V tt = slot_sum<T, V, (SLC > 1)>(slot_field(cc, c), slot_field(cl, c), carry,
                                              b0, b1, pos, A.stream, lane16, c == 0 && (pro & 2u));
       asm volatile("" : "+s"(lb), "+s"(hb));
@@ -808,16 +807,16 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     // the next iteration's sigma (the candidates are formed only when it runs)
     const bool more = it + 1 < A.iters;
     const T sigma_n = more ? A.sched[4 * (it + 1)] : zero;
-    // the slot-ordered rhs (zero on empty slots) through an opaque base, so the
-    // loads stay inside the loop
+    const T tp1 = T(1) + theta;
+    // the slot-ordered rhs when not held: through an opaque base, so the loads
+    // stay inside the loop
     GV rb = (GV)Rs;
     asm volatile("" : "+s"(rb));
-    const T tp1 = T(1) + theta;
     V qr = qd, qm = qc;  // the thread's dual terms and maxima of both passes
     carry = vzero;
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
-      const V rr = rb[r * NT + t];
+      const V rr = kHold ? rrh[kHold ? r : 0] : rb[r * NT + t];
       const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
                                               b0, b1, pos, A.stream, lane16, r == 0 && (pro & 1u));
       const V d = lds_read<V>(soff_r[r]);
@@ -833,14 +832,24 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
           qr[s] = (qr[s] - rr[s] * d[s]) - d[s] * zero;
         }
       }
-      if (more) {  // d+ of the next iteration from K ybar = (1 + theta) K y+ - theta K y
+      if (more) {
+        // d+ of the next iteration from K ybar = (1 + theta) K y+ - theta K y, into
+        // Gd where the sample is active (no thread gathers Gd in this sweep; the
+        // next column pass does, after the barriers below).  The committed d+
+        // stays in dk until the decision: a sample accepted now gets it back.
         V p = d + sigma_n * ((tp1 * acc - theta * ky[r]) - rr);
         if (ineq & (1u << r)) {
 #pragma unroll
           for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
         }
-        dn[r] = p;
+        if (act != (1u << BT) - 1u) {
+#pragma unroll
+          for (int s = 0; s < BT; ++s)
+            if (!(act & (1u << s))) p[s] = d[s];  // a frozen sample keeps its dual
+        }
+        lds_write<V>(soff_r[r], p);
       }
+      dk[r] = d;
       ky[r] = acc;
     }
     if (pro & 2u) {  // the next column pass's second chunk (its first is in b0)
@@ -890,6 +899,22 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       for (int s = 0; s < BT; ++s) {
         if (lds_read<uint32_t>(dec_off + 4u * (uint32_t)s) && (act & (1u << s))) accept |= 1u << s;
         if (act & (1u << s)) ++cnt[s];  // this iteration ran for the sample
+      }
+      accept = (uint32_t)__builtin_amdgcn_readfirstlane((int)accept);
+      if (accept && more) {
+        // accepted now: the sample keeps (y+, d+) of this iteration.  Its Gd
+        // entries hold the candidate the sweep wrote; restore d+ (own entries).
+        // The next column pass may gather either value for this sample only,
+        // whose update and diagnostics are masked from here on, so no barrier
+        // is needed before it.
+#pragma unroll
+        for (int r = 0; r < SLR; ++r) {
+          V p = lds_read<V>(soff_r[r]);
+#pragma unroll
+          for (int s = 0; s < BT; ++s)
+            if (accept & (1u << s)) p[s] = dk[r][s];
+          lds_write<V>(soff_r[r], p);
+        }
       }
       act = (uint32_t)__builtin_amdgcn_readfirstlane((int)(act & ~accept));
     }
