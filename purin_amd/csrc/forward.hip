@@ -263,7 +263,10 @@ template <typename T>
 static size_t resident_lds(const purin_cp_plan* p, bool early = false) {
   if (!p->res_ok) return 0;
   // Gy (n) | zero | Gd (m) | trash, 16 bytes each
-  const size_t lds = (size_t)(p->n + 1 + p->m + 1) * 16 + (early ? kResEarlyExtra : 0);
+  const size_t lds = (size_t)(p->n + 1 + p->m + 1) * 16 +
+                     (early ? kResEarlyExtra + (size_t)res_early_kyl(p->res_mr, p->res_mc) *
+                                                   kResThreads * 16
+                            : 0);
   return lds <= 160 * 1024 ? lds : 0;
 }
 

@@ -538,9 +538,23 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
 // kernels.py:172).  On lanes whose bounds are not NaN, y+ lies in [lo, hi]
 // (bound violation 0) and the stationarity clip equals the dual term's.
 // LDS: the fixed kernel's, then the partials [16 waves][4 rows][kResQ] and
-// the BT verdicts.
+// the BT verdicts, then K y of the first res_early_kyl(SLR, SLC) row slots.
 constexpr int kResQ = 3;  // primal; dual objective (terms - r.d); max(stationarity, residual)
 constexpr uint32_t kResEarlyExtra = 16u * 4u * kResQ * 16u + 16u;
+
+// Row slots whose K y the early-stop kernel keeps in LDS instead of registers:
+// as many as the largest LDS image of the (SLR, SLC) variant leaves room for
+// beside the partials, in variants with five or more slots per thread (the
+// smaller ones have registers to spare).  Measured at config 2's (3, 4): two
+// slots, 14.9 -> 13.7 us per iteration (the registers they free remove most
+// of the loop's spill traffic); one slot 14.1 us.
+constexpr int res_early_kyl(int SLR, int SLC) {
+  if (SLR + SLC < 5) return 0;
+  const long image = (long)(SLR + SLC) * 1024 * 16 + 32;
+  const long free_b = 160L * 1024 - image - (long)kResEarlyExtra;
+  const long k = free_b / (1024L * 16);
+  return (int)(k < 0 ? 0 : (k > SLR ? SLR : k));
+}
 
 // One DPP move of a 32- or 64-bit value (all lanes active, full row/bank masks).
 template <int CTRL, typename T>
@@ -603,6 +617,8 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const uint32_t trash_off = (uint32_t)(A.n + 1 + A.m) * 16u;
   const uint32_t red_off = trash_off + 16u;
   const uint32_t dec_off = red_off + 16u * 4u * kResQ * 16u;  // [BT] verdicts
+  constexpr int KYL = res_early_kyl(SLR, SLC);
+  const uint32_t kyl_off = dec_off + 16u;  // [KYL][1024] K y of the first row slots
 
   const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave]);
   // per slot (8 bits each): whole chunks from the slot's first whole chunk on,
@@ -619,7 +635,8 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const V* Rs = reinterpret_cast<const V*>(A.Rs) + tile * (int64_t)A.Kr;
   const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)A.Kr;
 
-  // registers: per row slot K y of the current iterate and, from the
+  // registers: per row slot K y of the current iterate (in LDS for the first
+  // KYL slots) and, from the
   // residual sweep to the decision, the committed dual the sweep replaced in
   // Gd by the next candidate; the targets of the thread's columns and the
   // scaled right-hand sides of its rows, loaded once (re-reading them each
@@ -691,9 +708,13 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
       const V rr = kHold ? rrh[kHold ? r : 0] : Rs[r * NT + t];
-      ky[r] = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
-                                        b0, b1, pos, A.stream, lane16, r == 0 && (pro & 1u));
-      V p = lds_read<V>(soff_r[r]) + sigma0 * (ky[r] - rr);
+      const V k0 = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
+                                             b0, b1, pos, A.stream, lane16, r == 0 && (pro & 1u));
+      if (r < KYL)
+        lds_write<V>(kyl_off + (uint32_t)(r * NT + t) * 16u, k0);
+      else
+        ky[r] = k0;
+      V p = lds_read<V>(soff_r[r]) + sigma0 * (k0 - rr);
       if (ineq & (1u << r)) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
@@ -837,7 +858,8 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         // Gd where the sample is active (no thread gathers Gd in this sweep; the
         // next column pass does, after the barriers below).  The committed d+
         // stays in dk until the decision: a sample accepted now gets it back.
-        V p = d + sigma_n * ((tp1 * acc - theta * ky[r]) - rr);
+        const V kyo = r < KYL ? lds_read<V>(kyl_off + (uint32_t)(r * NT + t) * 16u) : ky[r];
+        V p = d + sigma_n * ((tp1 * acc - theta * kyo) - rr);
         if (ineq & (1u << r)) {
 #pragma unroll
           for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
@@ -850,7 +872,10 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         lds_write<V>(soff_r[r], p);
       }
       dk[r] = d;
-      ky[r] = acc;
+      if (r < KYL)
+        lds_write<V>(kyl_off + (uint32_t)(r * NT + t) * 16u, acc);
+      else
+        ky[r] = acc;
     }
     if (pro & 2u) {  // the next column pass's second chunk (its first is in b0)
       load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16);
