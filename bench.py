@@ -536,13 +536,18 @@ def measure(args, torch, config, *, steps, warmup, headline):
         # chunk streams from L2 (every tile re-reads them each iteration) and the
         # LDS gathers.  Price it against the probes' ceilings at the same shape.
         info = plan.info
-        bt = 2 if ws == 8 else 4                        # samples per workgroup (16 bytes)
-        tiles = -(-B // (64 * bt)) * 64                 # the padded batch's tiles
+        # samples per workgroup: 16 bytes of samples per LDS entry (2 fp64, 4
+        # fp32), or 8 fp32 in two LDS planes where n, m <= 1024
+        bt = int(info.resident_tile_samples)
+        pad = 64 * (2 if ws == 8 else 4)                # the batch's padding unit
+        tiles = -(-B // pad) * pad // bt                # the padded batch's tiles
         l2_bytes = tiles * iters * int(info.resident_stream_bytes)
         entries = int(info.resident_stream_bytes) // (12 if ws == 8 else 8)
-        lds_iter = 16 * (entries + 2 * int(info.resident_row_slots) + int(info.resident_col_slots))
+        planes = bt * ws // 16                          # 16-byte LDS reads per gathered entry
+        lds_iter = 16 * planes * (entries + 2 * int(info.resident_row_slots)
+                                  + int(info.resident_col_slots))
         lds_launch = tiles * iters * lds_iter
-        lds_alloc = (n + 1 + m + 1) * 16
+        lds_alloc = (n + 1 + m + 1) * 16 if planes == 1 else 2 * 32800
         ceil = probe_ceilings(torch, tiles, lds_alloc, int(info.resident_stream_bytes))
         l2_rate = l2_bytes / (dom_ms / 1e3) / 1e9
         lds_rate = lds_launch / (dom_ms / 1e3) / 1e9
@@ -565,9 +570,9 @@ def measure(args, torch, config, *, steps, warmup, headline):
                            f"{ceil['l2']['unroll']} in flight, {ceil['l2']['lds_bytes']} B LDS",
             "lds": {"achieved": lds_rate, "peak": ceil["lds"]["GBs"],
                     "frac": lds_rate / ceil["lds"]["GBs"], "bytes_per_launch": lds_launch,
-                    "what": f"16 B per gathered entry ({entries} per workgroup per iteration, "
-                            "padding included) + the slots' own entries (2 per row, 1 per "
-                            "column)",
+                    "what": f"{16 * planes} B per gathered entry ({entries} per workgroup "
+                            "per iteration, padding included) + the slots' own entries (2 per "
+                            "row, 1 per column)",
                     "peak_source": "measured in this run: best rate of k_probe_lds "
                                    "(conflict-free ds_read_b128)"},
             "hbm": {"achieved": achieved, "peak": HBM_PEAK_GBS, "frac": achieved / HBM_PEAK_GBS,

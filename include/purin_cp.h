@@ -159,6 +159,10 @@ typedef struct {
    * leave them unchanged. */
   int64_t workspace_bytes;
   int64_t adjoint_workspace_bytes;
+  /* Samples of one resident workgroup (tile): 2 in fp64, 4 in fp32, or 8 in
+   * fp32 where n and m fit one slot per thread (two LDS planes); 0 when the
+   * resident kernel does not apply.  No reference counterpart. */
+  int64_t resident_tile_samples;
 } purin_cp_plan_info;
 
 int purin_cp_plan_get_info(const purin_cp_plan* plan, purin_cp_plan_info* info);

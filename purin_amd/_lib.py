@@ -76,6 +76,7 @@ class PlanInfo(C.Structure):
         ("resident_stream_bytes", C.c_int64), ("resident_stream_bytes_early", C.c_int64),
         ("resident_row_slots", C.c_int64), ("resident_col_slots", C.c_int64),
         ("workspace_bytes", C.c_int64), ("adjoint_workspace_bytes", C.c_int64),
+        ("resident_tile_samples", C.c_int64),
     ]
 
 

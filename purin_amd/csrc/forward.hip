@@ -235,24 +235,28 @@ template int prepare_values<float>(purin_cp_plan*, hipStream_t, int64_t, const L
                                    const float*, float, int, const float*, const float*,
                                    PerSample<float>*);
 
-template <typename T>
-constexpr int res_tile() {
-  return ResVec<T>::BT;  // 16 bytes of samples per gathered element
+// Samples per resident tile: 16 bytes of samples per gathered element, or 8
+// fp32 samples in two LDS planes where one row and one column slot per thread
+// hold the problem (resident.hpp, ResV): each tile's pass over the shared
+// matrix stream then serves twice the samples.
+int res_tile_samples(const purin_cp_plan* p) {
+  if (p->dtype == PURIN_CP_F32 && p->res_mr == 1 && p->res_mc == 1) return 8;
+  return p->dtype == PURIN_CP_F64 ? ResVec<double>::BT : ResVec<float>::BT;
 }
 
 // One translation unit per (element type, row slots): resident_launch.hip.
 template <typename T, int SLR>
 int launch_resident_rows(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
-                         bool sb, bool early);
+                         bool sb, bool early, int nb);
 
 template <typename T>
 static int launch_resident(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slr,
-                           int slc, bool sb, bool early) {
+                           int slc, bool sb, bool early, int nb) {
   switch (slr) {
-    case 1: return launch_resident_rows<T, 1>(R, st, tiles, lds, slc, sb, early);
-    case 2: return launch_resident_rows<T, 2>(R, st, tiles, lds, slc, sb, early);
-    case 3: return launch_resident_rows<T, 3>(R, st, tiles, lds, slc, sb, early);
-    case 4: return launch_resident_rows<T, 4>(R, st, tiles, lds, slc, sb, early);
+    case 1: return launch_resident_rows<T, 1>(R, st, tiles, lds, slc, sb, early, nb);
+    case 2: return launch_resident_rows<T, 2>(R, st, tiles, lds, slc, sb, early, nb);
+    case 3: return launch_resident_rows<T, 3>(R, st, tiles, lds, slc, sb, early, nb);
+    case 4: return launch_resident_rows<T, 4>(R, st, tiles, lds, slc, sb, early, nb);
     default: return set_error(PURIN_CP_ERR_ARG, "resident row slot count out of range");
   }
 }
@@ -262,6 +266,8 @@ static int launch_resident(const Res<T>& R, hipStream_t st, int64_t tiles, size_
 template <typename T>
 static size_t resident_lds(const purin_cp_plan* p, bool early = false) {
   if (!p->res_ok) return 0;
+  if (res_tile_samples(p) == 8)  // two planes of the largest one-slot image
+    return (size_t)2 * kResPlane + (early ? res_early_extra(32u, 8u) : 0);
   // Gy (n) | zero | Gd (m) | trash, 16 bytes each
   const size_t lds = (size_t)(p->n + 1 + p->m + 1) * 16 +
                      (early ? kResEarlyExtra + (size_t)res_early_kyl(p->res_mr, p->res_mc) *
@@ -277,7 +283,7 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
                         const purin_cp_solve_options& o, size_t lds, bool early = false,
                         int64_t batch = 0, T tol = T(0), const T* tolv = nullptr,
                         int32_t* done = nullptr, int32_t* count = nullptr, bool noalloc = false) {
-  constexpr int BT = res_tile<T>();
+  const int BT = res_tile_samples(p);
   const int64_t Bp = L.Bp, tiles = Bp / BT;
   const int Kr = p->res_mr * kResThreads, Kc = p->res_mc * kResThreads;
   // the step schedule built with the plan covers kSchedCapacity iterations;
@@ -316,15 +322,21 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   // tiles and the slot counts are multiples of 64)
   const dim3 gc((unsigned)(tiles / (64 / BT)), (unsigned)(Kc / 64));
   const dim3 gr((unsigned)(tiles / (64 / BT)), (unsigned)(Kr / 64));
-  k_res_gather<T, BT><<<gc, 256, 0, st>>>((const T*)(sv + L.Tt), Bp, p->res_colmap, Kc, tiles, Ts);
-  k_res_gather<T, BT><<<gr, 256, 0, st>>>((const T*)(sv + L.R), Bp, p->res_rowmap, Kr, tiles, Rs);
-  k_res_gather<T, BT><<<gr, 256, 0, st>>>((const T*)(sv + L.D), Bp, p->res_rowmap, Kr, tiles, D0s);
+  auto gather = [&](dim3 g, const T* src, const int32_t* map, int K, T* dst) {
+    if (BT == 8)
+      k_res_gather<T, 8><<<g, 256, 0, st>>>(src, Bp, map, K, tiles, dst);
+    else
+      k_res_gather<T, ResVec<T>::BT><<<g, 256, 0, st>>>(src, Bp, map, K, tiles, dst);
+  };
+  gather(gc, (const T*)(sv + L.Tt), p->res_colmap, Kc, Ts);
+  gather(gr, (const T*)(sv + L.R), p->res_rowmap, Kr, Rs);
+  gather(gr, (const T*)(sv + L.D), p->res_rowmap, Kr, D0s);
   if (o.shared_bounds) {
     k_res_gather_shared<T><<<(Kc + 255) / 256, 256, 0, st>>>((const T*)(sv + L.LO), p->res_colmap, Kc, Ls);
     k_res_gather_shared<T><<<(Kc + 255) / 256, 256, 0, st>>>((const T*)(sv + L.HI), p->res_colmap, Kc, Hs);
   } else {
-    k_res_gather<T, BT><<<gc, 256, 0, st>>>((const T*)(sv + L.LO), Bp, p->res_colmap, Kc, tiles, Ls);
-    k_res_gather<T, BT><<<gc, 256, 0, st>>>((const T*)(sv + L.HI), Bp, p->res_colmap, Kc, tiles, Hs);
+    gather(gc, (const T*)(sv + L.LO), p->res_colmap, Kc, Ls);
+    gather(gc, (const T*)(sv + L.HI), p->res_colmap, Kc, Hs);
   }
   R.Ts = Ts;
   R.Rs = Rs;
@@ -342,7 +354,7 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     PURIN_HIP(hipEventRecord(e0, st));
   }
   if (int rc = launch_resident<T>(R, st, tiles, lds, p->res_mr, p->res_mc,
-                                  o.shared_bounds != 0, early)) return rc;
+                                  o.shared_bounds != 0, early, BT)) return rc;
   PURIN_HIP(hipGetLastError());
   if (o.timing) {
     PURIN_HIP(hipEventRecord(e1, st));

@@ -1148,6 +1148,7 @@ int purin_cp_plan_get_info(const purin_cp_plan* p, purin_cp_plan_info* info) {
   info->resident_col_slots = p->res_ok ? (int64_t)p->res_mc * kResThreads : 0;
   info->workspace_bytes = (int64_t)p->ws_bytes;
   info->adjoint_workspace_bytes = (int64_t)p->aws_bytes;
+  info->resident_tile_samples = p->res_ok ? res_tile_samples(p) : 0;
   return PURIN_CP_OK;
 }
 

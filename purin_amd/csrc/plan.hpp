@@ -141,6 +141,10 @@ void record_timing(purin_cp_plan* p, const purin_cp_timing& t);
 // cap only ever rises (under a lock), so a concurrent call on another plan or
 // thread cannot lower it between another call's raise and its launch.
 int raise_lds_cap(const void* kernel, size_t bytes);
+// Samples of one resident tile (forward.hip): 16 bytes of samples, or 8 fp32
+// samples in two LDS planes where one row and one column slot per thread hold
+// the problem.
+int res_tile_samples(const purin_cp_plan* p);
 
 // Host-visible words for one call's reads of device flags: a slot of the
 // plan's pinned pool, or, when concurrent calls hold every slot, host memory

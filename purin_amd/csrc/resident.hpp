@@ -51,8 +51,8 @@ constexpr int kResWaves = 16;     // wavefronts of a resident workgroup
 // (its registers then hold fewer chunks in flight), and the fp64 kernels
 // would spill 36-44 bytes.  So only the fp32 per-sample-bounds kernel asks.
 template <typename T>
-constexpr int res_min_waves(int SLR, int SLC, bool SB) {
-  return sizeof(T) == 4 && SLR + SLC <= 2 && !SB ? 8 : 1;
+constexpr int res_min_waves(int SLR, int SLC, bool SB, int NB) {
+  return sizeof(T) == 4 && NB == 4 && SLR + SLC <= 2 && !SB ? 8 : 1;
 }
 
 template <typename T>
@@ -67,6 +67,30 @@ struct ResVec<float> {
   static constexpr int BT = 4;
   typedef float V __attribute__((ext_vector_type(4)));
 };
+
+// NB samples of a tile: one 16-byte LDS entry per gathered element (NB = 16 /
+// sizeof(T)), or, for fp32 tiles of 8 samples, two 16-byte entries in two
+// planes kResPlane bytes apart.  The second plane's read takes the first's
+// address plus an immediate offset, so the matrix stream (plane-0 addresses),
+// the LDS placement and its bank-class schedule serve both planes unchanged.
+// Two planes are used where one row and one column slot per thread hold the
+// problem (n, m <= 1024): the plane stride is then a constant that fits the
+// instruction's offset field, and the registers have room for 8 samples.
+template <typename T, int NB>
+struct ResV;
+template <>
+struct ResV<double, 2> {
+  typedef double V __attribute__((ext_vector_type(2)));
+};
+template <>
+struct ResV<float, 4> {
+  typedef float V __attribute__((ext_vector_type(4)));
+};
+template <>
+struct ResV<float, 8> {
+  typedef float V __attribute__((ext_vector_type(8)));
+};
+constexpr uint32_t kResPlane = (1024u + 1u + 1024u + 1u) * 16u;  // 32,800 B
 
 // Bytes of one chunk of one wavefront: the offsets block (64 lanes x 4 u32 LDS
 // byte addresses), then the coefficient blocks (64 lanes x 16 bytes each; 2
@@ -126,6 +150,33 @@ __device__ __forceinline__ void lds_write(uint32_t addr, V v) {
   *reinterpret_cast<__attribute__((address_space(3))) V*>(addr) = v;
 }
 
+// One gathered element (an entry of Gy, Gd, the zero or the trash entry) at its
+// plane-0 address: 16 bytes, or 32 bytes split over the two planes.
+template <typename V>
+__device__ __forceinline__ V ent_read(uint32_t addr) {
+  if constexpr (sizeof(V) == 32) {
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    typedef const __attribute__((address_space(3))) F4* P4;
+    const P4 p = reinterpret_cast<P4>(addr);
+    const F4 lo = p[0], hi = p[kResPlane / 16];
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  } else {
+    return lds_read<V>(addr);
+  }
+}
+template <typename V>
+__device__ __forceinline__ void ent_write(uint32_t addr, V v) {
+  if constexpr (sizeof(V) == 32) {
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) F4* P4;
+    const P4 p = reinterpret_cast<P4>(addr);
+    p[0] = __builtin_shufflevector(v, v, 0, 1, 2, 3);
+    p[kResPlane / 16] = __builtin_shufflevector(v, v, 4, 5, 6, 7);
+  } else {
+    lds_write<V>(addr, v);
+  }
+}
+
 // The chunk at byte ``cbyte`` of the stream; the base is made wave-uniform
 // explicitly so the loads take an SGPR base plus the lane's 16-byte offset.
 template <typename T>
@@ -168,7 +219,7 @@ template <typename T, typename V>
 __device__ __forceinline__ void consume_chunk(const Chunk<T>& c, V& acc) {
   V x[kResChunk];
 #pragma unroll
-  for (int u = 0; u < kResChunk; ++u) x[u] = lds_read<V>(c.o[u]);
+  for (int u = 0; u < kResChunk; ++u) x[u] = ent_read<V>(c.o[u]);
 #pragma unroll
   for (int u = 0; u < kResChunk; ++u) acc += c.v[u] * x[u];
 }
@@ -179,7 +230,7 @@ template <typename T, typename V>
 __device__ __forceinline__ void consume_split(const Chunk<T>& c, int e, V& acc, V& carry) {
   V x[kResChunk];
 #pragma unroll
-  for (int u = 0; u < kResChunk; ++u) x[u] = lds_read<V>(c.o[u]);
+  for (int u = 0; u < kResChunk; ++u) x[u] = ent_read<V>(c.o[u]);
   // one straight-line block per split point; the empty asm keeps the compiler
   // from merging the blocks into selects over both sums
   if (e == 1) {
@@ -326,11 +377,11 @@ __device__ __forceinline__ T clip_nonnan_bounds(T x, T lo, T hi) {
   return r >= hi ? hi : r;
 }
 
-template <typename T, int SLR, int SLC, bool SB>
-__global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_resident(Res<T> A) {
+template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT>
+__global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB, NB)) void k_resident(Res<T> A) {
   constexpr int NT = 1024;
-  constexpr int BT = ResVec<T>::BT;
-  using V = typename ResVec<T>::V;
+  constexpr int BT = NB;
+  using V = typename ResV<T, NB>::V;
   extern __shared__ __align__(16) unsigned char lds[];  // at LDS address 0 (no static LDS)
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -381,7 +432,7 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
     const V t0 = j >= 0 ? Ts[c * NT + t] : vzero;
     if constexpr (kHoldTarget) tg[c] = t0;
     y[c] = t0;  // y0 = ybar0 = yhat (kernels.py:229-231)
-    lds_write<V>(soff_c[c], y[c]);
+    ent_write<V>(soff_c[c], y[c]);
   }
 #pragma unroll
   for (int r = 0; r < SLR; ++r) {
@@ -389,9 +440,9 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
     soff_r[r] = i >= 0 ? (uint32_t)A.rowent[r * NT + t] * 16u : trash_off;
     rr[r] = i >= 0 ? Rs[r * NT + t] : vzero;
     if (i >= A.me) ineq |= 1u << r;  // kept rows: equalities first
-    lds_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
+    ent_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
   }
-  if (t == 0) lds_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
+  if (t == 0) ent_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
   const bool uni = __builtin_amdgcn_ballot_w64(same != 0) == ~0ull;  // all 64 lanes
   __syncthreads();
 
@@ -414,7 +465,7 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
     // ---- row pass (reads Gy and the thread's own Gd entries, writes Gd) -------
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
-      const V dold = lds_read<V>(soff_r[r]);
+      const V dold = ent_read<V>(soff_r[r]);
       const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
                                               b0, b1, pos, A.stream, lane16,
                                               r == 0 && (pro & 1u));
@@ -423,7 +474,7 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
       }
-      lds_write<V>(soff_r[r], p);
+      ent_write<V>(soff_r[r], p);
     }
     if (pro & 2u) {  // the column pass's second chunk (its first is in b0)
       load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16);
@@ -474,7 +525,7 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
 #pragma unroll
         for (int s = 0; s < BT; ++s) yn[s] = clip_nonnan_bounds(sv[s], lo[s], hi[s]);
       }
-      lds_write<V>(soff_c[c], yn + theta * (yn - y[c]));
+      ent_write<V>(soff_c[c], yn + theta * (yn - y[c]));
       y[c] = yn;
     }
     // the next row pass's second chunk (b0 holds the copy of its first)
@@ -494,7 +545,7 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
   for (int r = 0; r < SLR; ++r) {
     const int i = A.rowmap[r * NT + t];
     if (i >= 0) {
-      const V d = lds_read<V>(soff_r[r]);
+      const V d = ent_read<V>(soff_r[r]);
 #pragma unroll
       for (int s = 0; s < BT; ++s) A.D[(int64_t)i * A.Bp + b0s + s] = d[s];
     }
@@ -540,7 +591,14 @@ __global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB)) void k_reside
 // LDS: the fixed kernel's, then the partials [16 waves][4 rows][kResQ] and
 // the BT verdicts, then K y of the first res_early_kyl(SLR, SLC) row slots.
 constexpr int kResQ = 3;  // primal; dual objective (terms - r.d); max(stationarity, residual)
-constexpr uint32_t kResEarlyExtra = 16u * 4u * kResQ * 16u + 16u;
+
+// LDS bytes of the early-stop kernel beyond the tile's image, for vectors of
+// vb bytes (16, or 32 for two-plane tiles of nb = 8 samples): the partials
+// [16 waves][4 rows][kResQ] and the verdicts (4 bytes per sample, 16-aligned).
+constexpr uint32_t res_early_extra(uint32_t vb, uint32_t nb) {
+  return 16u * 4u * kResQ * vb + ((4u * nb + 15u) / 16u) * 16u;
+}
+constexpr uint32_t kResEarlyExtra = res_early_extra(16u, 4u);  // one-plane tiles
 
 // Row slots whose K y the early-stop kernel keeps in LDS instead of registers:
 // as many as the largest LDS image of the (SLR, SLC) variant leaves room for
@@ -601,11 +659,11 @@ __device__ __forceinline__ T read_lane(T v, int l) {
   }
 }
 
-template <typename T, int SLR, int SLC, bool SB>
+template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT>
 __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   constexpr int NT = 1024;
-  constexpr int BT = ResVec<T>::BT;
-  using V = typename ResVec<T>::V;
+  constexpr int BT = NB;
+  using V = typename ResV<T, NB>::V;
   extern __shared__ __align__(16) unsigned char lds[];  // at LDS address 0 (no static LDS)
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -615,10 +673,13 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   const V vzero = V(T(0));
   const T zero = T(0), half = T(0.5), inf = T(__builtin_inf());
   const uint32_t trash_off = (uint32_t)(A.n + 1 + A.m) * 16u;
-  const uint32_t red_off = trash_off + 16u;
-  const uint32_t dec_off = red_off + 16u * 4u * kResQ * 16u;  // [BT] verdicts
-  constexpr int KYL = res_early_kyl(SLR, SLC);
-  const uint32_t kyl_off = dec_off + 16u;  // [KYL][1024] K y of the first row slots
+  // the partials after the image (after both planes of a two-plane tile)
+  constexpr uint32_t VB = (uint32_t)sizeof(V);
+  const uint32_t red_off = VB == 32 ? 2u * kResPlane : trash_off + 16u;
+  const uint32_t dec_off = red_off + 16u * 4u * kResQ * VB;  // [BT] verdicts
+  constexpr int KYL = VB == 32 ? 0 : res_early_kyl(SLR, SLC);
+  // [KYL][1024] K y of the first row slots, after the verdicts
+  const uint32_t kyl_off = red_off + res_early_extra(VB, BT);
 
   const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave]);
   // per slot (8 bits each): whole chunks from the slot's first whole chunk on,
@@ -668,7 +729,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     // y0 = ybar0 = yhat (kernels.py:229-231); empty slots hold zeros
     const V t0 = reinterpret_cast<const V*>(A.Ts)[tile * (int64_t)A.Kc + c * NT + t];
     if constexpr (kHold) tgh[c] = t0;
-    lds_write<V>(soff_c[c], j >= 0 ? t0 : vzero);
+    ent_write<V>(soff_c[c], j >= 0 ? t0 : vzero);
   }
 #pragma unroll
   for (int r = 0; r < SLR; ++r) {
@@ -677,9 +738,9 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     soff_r[r] = i >= 0 ? (uint32_t)A.rowent[r * NT + t] * 16u : trash_off;
     if (i >= A.me) ineq |= 1u << r;  // kept rows: equalities first
     if constexpr (kHold) rrh[r] = Rs[r * NT + t];  // zero on empty slots
-    lds_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
+    ent_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
   }
-  if (t == 0) lds_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
+  if (t == 0) ent_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
   const bool uni = __builtin_amdgcn_ballot_w64(same != 0) == ~0ull;  // all 64 lanes
   // samples of the tile: the padding samples beyond the batch never run
   const int64_t bs0 = tile * BT;
@@ -690,7 +751,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   int32_t cnt[BT];
 #pragma unroll
   for (int s = 0; s < BT; ++s) cnt[s] = 0;
-  const uint32_t red_at = red_off + (uint32_t)((wave * 4 + (lane >> 4)) * kResQ) * 16u;
+  const uint32_t red_at = red_off + (uint32_t)((wave * 4 + (lane >> 4)) * kResQ) * VB;
   const bool red_lead = (lane & 15) == 0;
   __syncthreads();
 
@@ -711,15 +772,15 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       const V k0 = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
                                              b0, b1, pos, A.stream, lane16, r == 0 && (pro & 1u));
       if (r < KYL)
-        lds_write<V>(kyl_off + (uint32_t)(r * NT + t) * 16u, k0);
+        ent_write<V>(kyl_off + (uint32_t)(r * NT + t) * 16u, k0);
       else
         ky[r] = k0;
-      V p = lds_read<V>(soff_r[r]) + sigma0 * (k0 - rr);
+      V p = ent_read<V>(soff_r[r]) + sigma0 * (k0 - rr);
       if (ineq & (1u << r)) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
       }
-      lds_write<V>(soff_r[r], p);  // the first iteration's d+ (every sample active)
+      ent_write<V>(soff_r[r], p);  // the first iteration's d+ (every sample active)
     }
     if (pro & 2u) {  // the column pass's second chunk (its first is in b0)
       load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16);
@@ -766,7 +827,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         lo = ((GV)lb)[tile * (int64_t)A.Kc + c * NT + t];
         hi = ((GV)hb)[tile * (int64_t)A.Kc + c * NT + t];
       }
-      const V yo = lds_read<V>(soff_c[c]);
+      const V yo = ent_read<V>(soff_c[c]);
       const V sv = a * yo - delta * tt + delta * tg;
       V yn;
       if (nanb & (1u << c)) {
@@ -813,7 +874,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
           }
         }
       }
-      lds_write<V>(soff_c[c], yn);  // Gy <- y+
+      ent_write<V>(soff_c[c], yn);  // Gy <- y+
     }
 #pragma unroll
     for (int s = 0; s < BT; ++s) qp[s] = row16_combine(qp[s], OpAdd());
@@ -840,7 +901,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       const V rr = kHold ? rrh[kHold ? r : 0] : rb[r * NT + t];
       const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
                                               b0, b1, pos, A.stream, lane16, r == 0 && (pro & 1u));
-      const V d = lds_read<V>(soff_r[r]);
+      const V d = ent_read<V>(soff_r[r]);
       if (rvalid & (1u << r)) {  // kernels.py:158-166
         // e = K y+ - r; equality rows |e|, inequality rows max(e, 0): max(e, w e)
         // with w = -1 / 0.  d * 0 is NaN for a non-finite d: it makes the
@@ -858,7 +919,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         // Gd where the sample is active (no thread gathers Gd in this sweep; the
         // next column pass does, after the barriers below).  The committed d+
         // stays in dk until the decision: a sample accepted now gets it back.
-        const V kyo = r < KYL ? lds_read<V>(kyl_off + (uint32_t)(r * NT + t) * 16u) : ky[r];
+        const V kyo = r < KYL ? ent_read<V>(kyl_off + (uint32_t)(r * NT + t) * 16u) : ky[r];
         V p = d + sigma_n * ((tp1 * acc - theta * kyo) - rr);
         if (ineq & (1u << r)) {
 #pragma unroll
@@ -869,11 +930,11 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
           for (int s = 0; s < BT; ++s)
             if (!(act & (1u << s))) p[s] = d[s];  // a frozen sample keeps its dual
         }
-        lds_write<V>(soff_r[r], p);
+        ent_write<V>(soff_r[r], p);
       }
       dk[r] = d;
       if (r < KYL)
-        lds_write<V>(kyl_off + (uint32_t)(r * NT + t) * 16u, acc);
+        ent_write<V>(kyl_off + (uint32_t)(r * NT + t) * 16u, acc);
       else
         ky[r] = acc;
     }
@@ -883,16 +944,16 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     }
 #pragma unroll
     for (int s = 0; s < BT; ++s) qr[s] = row16_combine(qr[s], OpAdd());
-    if (red_lead) lds_write<V>(red_at + 16u, qr);
+    if (red_lead) lds_write<V>(red_at + VB, qr);
 #pragma unroll
     for (int s = 0; s < BT; ++s) qm[s] = row16_combine(qm[s], OpFMax());
-    if (red_lead) lds_write<V>(red_at + 32u, qm);
+    if (red_lead) lds_write<V>(red_at + 2u * VB, qm);
     __syncthreads();
     // ---- the stop test of sample s, on wavefront s: lane l combines partial l
     // (wave l/4, DPP row l%4) in one fixed order; the verdicts go through LDS
     if (wave < BT) {
-      const uint32_t pl = red_off + (uint32_t)(lane * kResQ) * 16u;
-      const V pp = lds_read<V>(pl), pd = lds_read<V>(pl + 16u), pm = lds_read<V>(pl + 32u);
+      const uint32_t pl = red_off + (uint32_t)(lane * kResQ) * VB;
+      const V pp = lds_read<V>(pl), pd = lds_read<V>(pl + VB), pm = lds_read<V>(pl + 2u * VB);
       T vp = pp[0], vd = pd[0], vm = pm[0];
 #pragma unroll
       for (int u = 1; u < BT; ++u)
@@ -934,11 +995,11 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         // is needed before it.
 #pragma unroll
         for (int r = 0; r < SLR; ++r) {
-          V p = lds_read<V>(soff_r[r]);
+          V p = ent_read<V>(soff_r[r]);
 #pragma unroll
           for (int s = 0; s < BT; ++s)
             if (accept & (1u << s)) p[s] = dk[r][s];
-          lds_write<V>(soff_r[r], p);
+          ent_write<V>(soff_r[r], p);
         }
       }
       act = (uint32_t)__builtin_amdgcn_readfirstlane((int)(act & ~accept));
@@ -952,7 +1013,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   for (int c = 0; c < SLC; ++c) {
     const int j = A.colmap[c * NT + t];
     if (j >= 0) {
-      const V yv = lds_read<V>(soff_c[c]);
+      const V yv = ent_read<V>(soff_c[c]);
 #pragma unroll
       for (int s = 0; s < BT; ++s) A.Y[(int64_t)j * A.Bp + bs0 + s] = yv[s];
     }
@@ -961,7 +1022,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   for (int r = 0; r < SLR; ++r) {
     const int i = A.rowmap[r * NT + t];
     if (i >= 0) {
-      const V d = lds_read<V>(soff_r[r]);
+      const V d = ent_read<V>(soff_r[r]);
 #pragma unroll
       for (int s = 0; s < BT; ++s) A.D[(int64_t)i * A.Bp + bs0 + s] = d[s];
     }

@@ -14,34 +14,47 @@
 
 namespace purin {
 
-template <typename T, int SLR, int SLC>
-static int launch_one(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
-                      bool early) {
-  auto kern = early ? (sb ? k_resident_early<T, SLR, SLC, true> : k_resident_early<T, SLR, SLC, false>)
-                    : (sb ? k_resident<T, SLR, SLC, true> : k_resident<T, SLR, SLC, false>);
+template <typename T, int SLR, int SLC, int NB>
+static int launch_nb(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
+                     bool early) {
+  auto kern = early ? (sb ? k_resident_early<T, SLR, SLC, true, NB>
+                          : k_resident_early<T, SLR, SLC, false, NB>)
+                    : (sb ? k_resident<T, SLR, SLC, true, NB> : k_resident<T, SLR, SLC, false, NB>);
   if (int rc = raise_lds_cap((const void*)kern, lds)) return rc;
   kern<<<dim3((unsigned)tiles), dim3(kResThreads), lds, st>>>(R);
   return PURIN_CP_OK;
 }
 
+// nb: samples per tile (resident.hpp, ResV); 8 only for fp32 with one row and
+// one column slot per thread (two LDS planes)
+template <typename T, int SLR, int SLC>
+static int launch_one(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
+                      bool early, int nb) {
+  if constexpr (sizeof(T) == 4 && SLR == 1 && SLC == 1) {
+    if (nb == 8) return launch_nb<T, SLR, SLC, 8>(R, st, tiles, lds, sb, early);
+  }
+  if (nb != ResVec<T>::BT) return set_error(PURIN_CP_ERR_ARG, "resident tile size out of range");
+  return launch_nb<T, SLR, SLC, ResVec<T>::BT>(R, st, tiles, lds, sb, early);
+}
+
 template <typename T, int SLR>
 int launch_resident_rows(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
-                         bool sb, bool early) {
+                         bool sb, bool early, int nb) {
   switch (slc) {
-    case 1: return launch_one<T, SLR, 1>(R, st, tiles, lds, sb, early);
-    case 2: return launch_one<T, SLR, 2>(R, st, tiles, lds, sb, early);
-    case 3: return launch_one<T, SLR, 3>(R, st, tiles, lds, sb, early);
-    case 4: return launch_one<T, SLR, 4>(R, st, tiles, lds, sb, early);
+    case 1: return launch_one<T, SLR, 1>(R, st, tiles, lds, sb, early, nb);
+    case 2: return launch_one<T, SLR, 2>(R, st, tiles, lds, sb, early, nb);
+    case 3: return launch_one<T, SLR, 3>(R, st, tiles, lds, sb, early, nb);
+    case 4: return launch_one<T, SLR, 4>(R, st, tiles, lds, sb, early, nb);
     default: return set_error(PURIN_CP_ERR_ARG, "resident column slot count out of range");
   }
 }
 
 #if PURIN_RES_F64
 template int launch_resident_rows<double, PURIN_RES_SLR>(const Res<double>&, hipStream_t, int64_t,
-                                                         size_t, int, bool, bool);
+                                                         size_t, int, bool, bool, int);
 #else
 template int launch_resident_rows<float, PURIN_RES_SLR>(const Res<float>&, hipStream_t, int64_t,
-                                                        size_t, int, bool, bool);
+                                                        size_t, int, bool, bool, int);
 #endif
 
 }  // namespace purin
