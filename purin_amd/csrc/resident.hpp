@@ -42,18 +42,11 @@ namespace purin {
 constexpr int kResChunk = 4;      // matrix entries per lane in one stream chunk
 constexpr int kResWaves = 16;     // wavefronts of a resident workgroup
 
-// Minimum wavefronts per SIMD the compiler must allow.  With one row and one
-// column slot per thread (n, m <= 1024) the tile's LDS image is at most 33 KB,
-// so two workgroups fit a CU when each wavefront keeps to 64 VGPRs (8 waves
-// per SIMD).  Measured at config 4 (fp32, one slot each): the per-sample-bounds
-// kernel, whose bound loads miss L2, gains from the second workgroup (90.7 ->
-// 79.7 ms per call, with a 12-byte spill); the shared-bounds kernel loses 2 %
-// (its registers then hold fewer chunks in flight), and the fp64 kernels
-// would spill 36-44 bytes.  So only the fp32 per-sample-bounds kernel asks.
-template <typename T>
-constexpr int res_min_waves(int SLR, int SLC, bool SB, int NB) {
-  return sizeof(T) == 4 && NB == 4 && SLR + SLC <= 2 && !SB ? 8 : 1;
-}
+// One workgroup per CU, four wavefronts per SIMD, up to 128 VGPRs each.  (With
+// one row and one column slot per thread the 8-sample fp32 tile's two LDS
+// planes, 64 KB, would let two workgroups share a CU at 64 VGPRs per
+// wavefront; the kernels then spill 164-180 bytes per lane and run 3x slower
+// at config 4: 157 against 51 ms per 500-iteration launch.)
 
 template <typename T>
 struct ResVec;
@@ -378,7 +371,7 @@ __device__ __forceinline__ T clip_nonnan_bounds(T x, T lo, T hi) {
 }
 
 template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT>
-__global__ __launch_bounds__(1024, res_min_waves<T>(SLR, SLC, SB, NB)) void k_resident(Res<T> A) {
+__global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   constexpr int NT = 1024;
   constexpr int BT = NB;
   using V = typename ResV<T, NB>::V;

@@ -30,11 +30,9 @@ static int launch_nb(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds,
 template <typename T, int SLR, int SLC>
 static int launch_one(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
                       bool early, int nb) {
-  if constexpr (sizeof(T) == 4 && SLR == 1 && SLC == 1) {
-    if (nb == 8) return launch_nb<T, SLR, SLC, 8>(R, st, tiles, lds, sb, early);
-  }
-  if (nb != ResVec<T>::BT) return set_error(PURIN_CP_ERR_ARG, "resident tile size out of range");
-  return launch_nb<T, SLR, SLC, ResVec<T>::BT>(R, st, tiles, lds, sb, early);
+  constexpr int NB = sizeof(T) == 4 && SLR == 1 && SLC == 1 ? 8 : ResVec<T>::BT;
+  if (nb != NB) return set_error(PURIN_CP_ERR_ARG, "resident tile size out of range");
+  return launch_nb<T, SLR, SLC, NB>(R, st, tiles, lds, sb, early);
 }
 
 template <typename T, int SLR>
