@@ -222,6 +222,73 @@ def test_ragged_batches(batch):
     np.testing.assert_array_equal(to_np(got.status), want.status)
 
 
+def _same_nonfinite(got, want, bar, what):
+    """NaN and infinite entries in the same places (infinities with the same
+    sign); the finite entries within ``bar`` (relative to the largest)."""
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want), err_msg=what)
+    inf = np.isinf(want)
+    np.testing.assert_array_equal(np.isinf(got), inf, err_msg=what)
+    np.testing.assert_array_equal(got[inf], want[inf], err_msg=what)
+    fin = np.isfinite(want)
+    assert rel_err(got[fin], want[fin]) <= bar, what
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("early_stop", [False, True])
+def test_nonfinite_bounds_and_targets(dtype, early_stop):
+    """Per-sample bounds with NaN entries (the lanes whose clip propagates NaN,
+    kernels.py:133-147's jnp.clip), infinite bounds, a tied box, and NaN and
+    infinite targets, in some samples of a batch: the resident kernel (fixed
+    and early stop) and the streaming passes each against the oracle.  NaN
+    and infinity land in the same places; the other samples keep the parity
+    bar and, in fp64, the oracle's iteration counts (a sample with a
+    non-finite iterate never passes the stop test)."""
+    torch = require_gpu()
+    B = 40
+    w = workloads.small_random(13, n=48, me=8, mi=20, width=4, batch=B)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+    target = w.target.astype(dtype).copy()
+    pre = _kept(canon, rhs, dtype)
+    ksup, kmask = pre.support[pre.rows], pre.mask[pre.rows]
+    lower, upper = pre.lower.astype(dtype).copy(), pre.upper.astype(dtype).copy()
+    lower[3, 5] = np.nan
+    upper[7, 11] = np.nan
+    lower[9, :10], upper[9, :10] = -np.inf, np.inf
+    lower[20, 7] = upper[20, 7] = 0.3
+    target[12, 2] = np.nan
+    target[15, 4] = np.inf
+    target[18, 6] = -np.inf
+    iters, tol = 300, (1e-6 if dtype == np.float64 else 1e-3)
+    with np.errstate(invalid="ignore", over="ignore"):
+        mg = Margins(lambda safety, tr: ocp.sparse_cp(
+            np.ones_like(target), -target, pre.kept_values[0], pre.kept_rhs, ksup, kmask,
+            canon.me, lower, upper, accelerated=False, safety=safety, max_iterations=iters,
+            tolerance=tol, y0=target, freeze_converged=True, check_stationarity=True,
+            norm_bound=True, early_stop=early_stop, trace=tr), dtype)
+    want = mg.want
+    assert np.isnan(want.y[3]).any() and np.isnan(want.y[12]).any()
+    plan = plan_for(canon, dtype=dtype)
+    bar = TOL[dtype]
+    for streaming in (False, True):
+        got = plan.solve(pre.kept_rhs, target, lower, upper, tolerance=tol, max_iterations=iters,
+                         early_stop=early_stop, check_every=5, streaming=streaming, timing=True)
+        assert plan.last_timing()["resident"] == (0 if streaming else 1)
+        what = f"streaming={streaming}"
+        print(f"non-finite inputs: {np.dtype(dtype).name} early_stop={early_stop} {what}",
+              flush=True)
+        it = to_np(got.iterations)
+        same = check_counts(it, mg)
+        bad = ~np.all(np.isfinite(want.y), axis=1)  # samples with a non-finite iterate
+        assert np.all(it[bad] == iters), what
+        y, d = to_np(got.y), to_np(got.dual)
+        _same_nonfinite(y[same], want.y[same], bar, what)
+        _same_nonfinite(d[same], want.dual[same], bar, what)
+        np.testing.assert_array_equal(to_np(got.converged)[same], want.converged[same])
+        # tied box: the variable sits on it
+        assert np.all(y[20, 7] == dtype(0.3)), what
+
+
 def test_invalid_arguments_raise():
     torch = require_gpu()
     from purin_amd._lib import PurinError
