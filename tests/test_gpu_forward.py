@@ -334,6 +334,54 @@ def test_resident_kernel_matches_streaming_and_oracle(dtype, accelerated):
         np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
 
 
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_resident_largest_tile(dtype):
+    """The largest problem the resident kernels take: n = m = 4096, four row
+    and four column slots per thread, a 131,104-byte LDS image (150,576 bytes
+    in the early-stop kernel, which keeps K y of one row slot in LDS and
+    re-reads targets and right-hand sides each iteration).  Fixed iterations
+    with per-sample and with shared bounds (bit-identical), against the
+    streaming passes and, on two samples, the oracle; early stop in fp64 with
+    the streaming passes' iteration counts."""
+    require_gpu()
+    n, me, mi, B = 4096, 1024, 3072, 10
+    w = workloads.small_random(91, n=n, me=me, mi=mi, width=6, batch=B, accelerated=True)
+    canon = canonical_from_workload(w)
+    rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+    target = w.target.astype(dtype)
+    plan = plan_for(canon, dtype=dtype, accelerated=True)
+    info = plan.info
+    assert info.resident_row_slots == 4096 and info.resident_col_slots == 4096
+    bar = TOL[dtype]
+    iters = 120
+    res = plan.project(target, rhs, max_iterations=iters, early_stop=False, timing=True)
+    assert plan.last_timing()["resident"] == 1
+    st = plan.project(target, rhs, max_iterations=iters, early_stop=False, streaming=True)
+    assert rel_err(to_np(res.y), to_np(st.y)) <= bar / 10
+    assert rel_err(to_np(res.multipliers), to_np(st.multipliers)) <= bar
+    np.testing.assert_array_equal(to_np(res.status), to_np(st.status))
+    sh = plan.project(target, rhs, max_iterations=iters, early_stop=False, shared_bounds=True)
+    np.testing.assert_array_equal(to_np(sh.y), to_np(res.y))
+    sub = slice(0, 2)
+    cfg = op.Config(accelerated=True, max_iterations=iters, early_stop=False)
+    want = op.solve(canon, target[sub], rhs[sub], cfg, dtype=dtype)
+    assert rel_err(to_np(res.y)[sub], want.y) <= bar
+    np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
+    if dtype == np.float64:
+        # this problem converges slowly: at tolerance 0.3 the samples stop at
+        # different iterations (about 430-580), so tiles freeze samples one by one
+        kw = dict(max_iterations=700, early_stop=True, tolerance=0.3)
+        for shared in (False, True):
+            re_ = plan.project(target, rhs, timing=True, shared_bounds=shared, **kw)
+            assert plan.last_timing()["resident"] == 1
+            se = plan.project(target, rhs, streaming=True, shared_bounds=shared, **kw)
+            it = to_np(re_.iterations)
+            np.testing.assert_array_equal(it, to_np(se.iterations))
+            np.testing.assert_array_equal(to_np(re_.status), to_np(se.status))
+            assert rel_err(to_np(re_.y), to_np(se.y)) <= bar
+        assert np.all(it < kw["max_iterations"]) and len(np.unique(it)) > 2
+
+
 # ragged rows: (n, me, mi, wmin, wmax, B).  The resident schedule packs each
 # wavefront's slots back to back, so a chunk may hold the end of one slot and
 # the start of the next: these shapes give split chunks in the row pass (3 and
