@@ -64,8 +64,7 @@ def test_dense_solve_matches_oracle(dtype, accelerated, early_stop):
     if early_stop and dtype == np.float64 and not accelerated:
         assert it[0] < iters  # the stop test fired (accelerated fp64 stalls above 1e-7)
     assert rel_err(to_np(gy), y) <= TOL[dtype]
-    assert rel_err(to_np(gm), np.concatenate((lam, mu), axis=1)) <= (
-        1e-9 if dtype == np.float64 else 1e-3)
+    assert rel_err(to_np(gm), np.concatenate((lam, mu), axis=1)) <= TOL[dtype]
 
 
 def test_dense_packed_inequality_support():

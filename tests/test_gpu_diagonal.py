@@ -79,7 +79,7 @@ def test_diagonal_project_matches_oracle(dtype):
     np.testing.assert_array_equal(to_np(got.status), want.status)
     mult = to_np(got.multipliers)
     want_mult = np.concatenate([want.multipliers_eq, want.multipliers_ineq], axis=1)
-    assert rel_err(mult, want_mult) <= (1e-9 if dtype == np.float64 else 1e-3)
+    assert rel_err(mult, want_mult) <= TOL[dtype]
 
 
 def test_diagonal_vjp_matches_oracle_at_the_same_state():

@@ -81,9 +81,8 @@ def test_qp_solve_matches_oracle(dtype, early_stop, accelerated):
     assert rel_err(to_np(got.y)[same], want.y[same]) <= bar
     mult = to_np(got.multipliers)
     want_mult = np.concatenate([want.multipliers_eq, want.multipliers_ineq], axis=1)
-    assert rel_err(mult[same], want_mult[same]) <= (1e-9 if dtype == np.float64 else 1e-3)
-    assert rel_err(to_np(got.slacks)[same], want.slacks[same]) <= (
-        1e-9 if dtype == np.float64 else 1e-3)
+    assert rel_err(mult[same], want_mult[same]) <= TOL[dtype]
+    assert rel_err(to_np(got.slacks)[same], want.slacks[same]) <= TOL[dtype]
     np.testing.assert_array_equal(to_np(got.status), want.status)
     np.testing.assert_array_equal(to_np(got.converged), want.gradient_eligible)
     # the residual decides the status against the tolerance: fp64 agrees to 1e-6

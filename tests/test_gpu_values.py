@@ -74,9 +74,8 @@ def test_values_project_matches_oracle(dtype, early_stop, accelerated):
     np.testing.assert_array_equal(to_np(got.status), want.status)
     mult = to_np(got.multipliers)
     want_mult = np.concatenate([want.multipliers_eq, want.multipliers_ineq], axis=1)
-    assert rel_err(mult[same], want_mult[same]) <= (1e-9 if dtype == np.float64 else 1e-3)
-    assert rel_err(to_np(got.slacks)[same], want.slacks[same]) <= (
-        1e-9 if dtype == np.float64 else 1e-3)
+    assert rel_err(mult[same], want_mult[same]) <= TOL[dtype]
+    assert rel_err(to_np(got.slacks)[same], want.slacks[same]) <= TOL[dtype]
     # the per-sample matrices differ: so do the per-sample iteration counts (the
     # accelerated fp64 case stays above the tolerance for the whole run)
     if early_stop and not accelerated:
