@@ -72,6 +72,10 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values, int extra
     L.RD0 = take(Kr * Bp * es);
     L.RLs = take(Kc * Bp * es);
     L.RHs = take(Kc * Bp * es);
+    if (values) {  // the diagonal QP on the resident kernel
+      L.RQs = take(Kc * Bp * es);
+      L.RY0 = take(Kc * Bp * es);
+    }
   }
   if (values) {
     const size_t nnz = p->nnz, nb = p->bound.size();
@@ -247,16 +251,16 @@ int res_tile_samples(const purin_cp_plan* p) {
 // One translation unit per (element type, row slots): resident_launch.hip.
 template <typename T, int SLR>
 int launch_resident_rows(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
-                         bool sb, bool early, int nb);
+                         bool sb, bool early, int nb, bool qp);
 
 template <typename T>
 static int launch_resident(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slr,
-                           int slc, bool sb, bool early, int nb) {
+                           int slc, bool sb, bool early, int nb, bool qp) {
   switch (slr) {
-    case 1: return launch_resident_rows<T, 1>(R, st, tiles, lds, slc, sb, early, nb);
-    case 2: return launch_resident_rows<T, 2>(R, st, tiles, lds, slc, sb, early, nb);
-    case 3: return launch_resident_rows<T, 3>(R, st, tiles, lds, slc, sb, early, nb);
-    case 4: return launch_resident_rows<T, 4>(R, st, tiles, lds, slc, sb, early, nb);
+    case 1: return launch_resident_rows<T, 1>(R, st, tiles, lds, slc, sb, early, nb, qp);
+    case 2: return launch_resident_rows<T, 2>(R, st, tiles, lds, slc, sb, early, nb, qp);
+    case 3: return launch_resident_rows<T, 3>(R, st, tiles, lds, slc, sb, early, nb, qp);
+    case 4: return launch_resident_rows<T, 4>(R, st, tiles, lds, slc, sb, early, nb, qp);
     default: return set_error(PURIN_CP_ERR_ARG, "resident row slot count out of range");
   }
 }
@@ -277,12 +281,15 @@ static size_t resident_lds(const purin_cp_plan* p, bool early = false) {
 }
 
 // The CP loop on the resident kernel; fills Y and D like the passes (and, with
-// early stop, the per-sample done flags and iteration counts).
+// early stop, the per-sample done flags and iteration counts).  qp (with ps):
+// the diagonal QP's fixed-iteration loop, q and c per sample, y0 from Y, the
+// per-sample steps of ps.
 template <typename T>
 static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char* sv, char* ws,
                         const purin_cp_solve_options& o, size_t lds, bool early = false,
                         int64_t batch = 0, T tol = T(0), const T* tolv = nullptr,
-                        int32_t* done = nullptr, int32_t* count = nullptr, bool noalloc = false) {
+                        int32_t* done = nullptr, int32_t* count = nullptr, bool noalloc = false,
+                        const QPRun<T>* qp = nullptr, const PerSample<T>* ps = nullptr) {
   const int BT = res_tile_samples(p);
   const int64_t Bp = L.Bp, tiles = Bp / BT;
   const int Kr = p->res_mr * kResThreads, Kc = p->res_mc * kResThreads;
@@ -293,8 +300,9 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
                      "max_iterations exceeds the plan's step schedule (" +
                          std::to_string(p->res_sched_len) +
                          " iterations) in the no-allocation entry point");
-  const void* sched = nullptr;
-  if (int rc = ensure_schedule(p, o.max_iterations, st, false, &sched)) return rc;
+  const void* sched = p->res_sched;  // the QP kernel reads per-sample steps instead
+  if (!qp)
+    if (int rc = ensure_schedule(p, o.max_iterations, st, false, &sched)) return rc;
   Res<T> R{};
   R.n = (int)p->n;
   R.m = (int)p->m;
@@ -328,7 +336,19 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     else
       k_res_gather<T, ResVec<T>::BT><<<g, 256, 0, st>>>(src, Bp, map, K, tiles, dst);
   };
-  gather(gc, (const T*)(sv + L.Tt), p->res_colmap, Kc, Ts);
+  if (qp) {  // c in the target's place, q, and the start y0
+    T* Qs = (T*)(ws + L.RQs);
+    T* Y0s = (T*)(ws + L.RY0);
+    gather(gc, qp->Cc, p->res_colmap, Kc, Ts);
+    gather(gc, qp->Q, p->res_colmap, Kc, Qs);
+    gather(gc, (const T*)(sv + L.Y), p->res_colmap, Kc, Y0s);
+    R.Qs = Qs;
+    R.Y0s = Y0s;
+    R.step0 = ps->tau_b;  // [5][Bp]: tau, sigma, a, delta, theta of iteration 0
+    R.gam = p->opts.accelerated ? qp->gamma : nullptr;
+  } else {
+    gather(gc, (const T*)(sv + L.Tt), p->res_colmap, Kc, Ts);
+  }
   gather(gr, (const T*)(sv + L.R), p->res_rowmap, Kr, Rs);
   gather(gr, (const T*)(sv + L.D), p->res_rowmap, Kr, D0s);
   if (o.shared_bounds) {
@@ -354,7 +374,7 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     PURIN_HIP(hipEventRecord(e0, st));
   }
   if (int rc = launch_resident<T>(R, st, tiles, lds, p->res_mr, p->res_mc,
-                                  o.shared_bounds != 0, early, BT)) return rc;
+                                  o.shared_bounds != 0, early, BT, qp != nullptr)) return rc;
   PURIN_HIP(hipGetLastError());
   if (o.timing) {
     PURIN_HIP(hipEventRecord(e1, st));
@@ -435,10 +455,14 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   const int m = A.K.m, n = A.K.n;
   const bool early = o.early_stop != 0;
   const size_t lds = resident_lds<T>(p, early);
-  // the resident kernel takes one schedule of scalar steps for the whole tile
-  if (lds && !o.streaming && !p->diag && !ps && !qp) {
+  // the resident kernel takes one schedule of scalar steps for the whole tile,
+  // or, for the diagonal QP's fixed iterations with the plan's own
+  // coefficients (one shared copy), per-sample steps it advances itself
+  const bool res_qp = qp && !qp->dense && ps && ps->RVs && !early && !o.shared_bounds;
+  if (lds && !o.streaming && !p->diag && ((!ps && !qp) || res_qp)) {
     if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds, early, batch, tol_scalar, tolv, done,
-                                 count, noalloc)) return rc;
+                                 count, noalloc, res_qp ? qp : nullptr, res_qp ? ps : nullptr))
+      return rc;
     if (!early) {
       const int32_t cnt = (int32_t)o.max_iterations;
       k_fill<int32_t><<<(unsigned)((Bp + 255) / 256), 256, 0, st>>>(count, Bp, cnt);

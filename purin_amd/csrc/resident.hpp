@@ -124,6 +124,14 @@ struct Res {
   const T* __restrict__ tolv;
   int32_t* done;               // [Bp] accepted (1) or not (0)
   int32_t* count;              // [Bp] iterations committed
+  // diagonal QP (k_resident with QP): Ts holds c; q and y0 in slot order; the
+  // per-sample steps of iteration 0, [5][Bp] = tau, sigma, a, delta, theta
+  // (only tau, sigma and, when accelerated, theta are read); gamma = min q
+  // per sample for the accelerated update, or nullptr (fixed steps, theta 1)
+  const T* __restrict__ Qs;
+  const T* __restrict__ Y0s;
+  const T* __restrict__ step0;
+  const T* __restrict__ gam;
 };
 
 template <typename T>
@@ -370,7 +378,39 @@ __device__ __forceinline__ T clip_nonnan_bounds(T x, T lo, T hi) {
   return r >= hi ? hi : r;
 }
 
-template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT>
+// A wave-uniform value kept in SGPRs (its lanes are equal: the first lane's).
+template <typename T>
+__device__ __forceinline__ T res_uniform(T x) {
+  if constexpr (sizeof(T) == 8) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+  }
+}
+
+// The accelerated update of the diagonal QP's per-sample steps after an
+// iteration (kernels.py:279-283, gamma = min q): nu = 1/sqrt(1 + gamma tau);
+// tau <- nu tau; sigma <- sigma / nu; theta <- nu; every product and quotient
+// rounded, as the streaming passes' sched_next forms them.  The steps are the
+// same in every thread and stay in SGPRs.
+template <typename T, int BT>
+__device__ __forceinline__ void res_qp_schedule(const T (&gam)[BT], T (&tau)[BT], T (&sig)[BT],
+                                                T (&th)[BT]) {
+#pragma clang fp contract(off)
+  const T one = T(1);
+#pragma unroll
+  for (int s = 0; s < BT; ++s) {
+    const T nu = one / (T)__builtin_sqrt(one + gam[s] * tau[s]);
+    tau[s] = res_uniform(nu * tau[s]);
+    sig[s] = res_uniform(sig[s] / nu);
+    th[s] = res_uniform(nu);
+  }
+}
+
+template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT, bool QP = false>
 __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   constexpr int NT = 1024;
   constexpr int BT = NB;
@@ -401,17 +441,47 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   const V* D0 = reinterpret_cast<const V*>(A.D0s) + tile * (int64_t)A.Kr;
 
   uint32_t soff_r[SLR], soff_c[SLC];
-  // the targets stay in registers except in the variant with four row and
-  // four column slots and per-sample bounds, which would spill them
+  // the targets (QP: c) stay in registers except in the variants with four
+  // row and four column slots and per-sample bounds, which would spill them
   constexpr bool kHoldTarget = SB || SLR + SLC < 8;
   V y[SLC], tg[kHoldTarget ? SLC : 1], rr[SLR];
+  // QP: q of the thread's columns, and the tile's per-sample steps (the same
+  // in every thread): tau, sigma, theta of the current iteration, gamma
+  V qh[QP ? SLC : 1];
+  T tau_s[BT], sig_s[BT], th_s[BT], gam_s[BT];
+  if constexpr (QP) {
+    const int64_t bq = tile * BT;
+#pragma unroll
+    for (int s = 0; s < BT; ++s) {
+      tau_s[s] = res_uniform(A.step0[bq + s]);
+      sig_s[s] = res_uniform(A.step0[A.Bp + bq + s]);
+      th_s[s] = res_uniform(A.gam ? A.step0[4 * A.Bp + bq + s] : T(1));
+      gam_s[s] = res_uniform(A.gam ? A.gam[bq + s] : T(0));
+    }
+  }
   uint32_t ineq = 0, nanb = 0;
   // shared bounds equal on every column of a wavefront's slots (box bounds,
   // e.g. [-1, 1]): its column pass then takes them from registers instead of
   // re-reading them from L2 every iteration.  The test is per wavefront (a
   // ballot; the kernel uses no LDS beyond its own dynamic layout).
-  const T lo0 = A.Ls[0], hi0 = A.Hs[0];
-  int same = SB && lo0 == lo0 && hi0 == hi0;
+  // The QP takes per-sample bounds; a box the same for every sample and
+  // column of the wavefront's slots (e.g. [-1, 1]) is held the same way, with
+  // the reference pair from the first lane's first column slot.
+  T lo0 = A.Ls[0], hi0 = A.Hs[0];
+  if constexpr (QP) {
+    T rl = T(0), rh = T(0);
+#pragma unroll
+    for (int c = SLC - 1; c >= 0; --c) {  // ends on the first valid slot
+      const int64_t e0 = (tile * (int64_t)A.Kc + c * NT + t) * BT;
+      if (A.colmap[c * NT + t] >= 0) {
+        rl = A.Ls[e0];
+        rh = A.Hs[e0];
+      }
+    }
+    lo0 = res_uniform(rl);
+    hi0 = res_uniform(rh);
+  }
+  int same = (SB || QP) && lo0 == lo0 && hi0 == hi0;
 #pragma unroll
   for (int c = 0; c < SLC; ++c) {
     const int j = A.colmap[c * NT + t];
@@ -419,12 +489,17 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
     for (int s = 0; s < BT; ++s) {
       const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
       if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
-      if (SB && j >= 0 && (A.Ls[e] != lo0 || A.Hs[e] != hi0)) same = 0;
+      if ((SB || QP) && j >= 0 && (A.Ls[e] != lo0 || A.Hs[e] != hi0)) same = 0;
     }
     soff_c[c] = j >= 0 ? (uint32_t)A.colent[c * NT + t] * 16u : trash_off;
     const V t0 = j >= 0 ? Ts[c * NT + t] : vzero;
     if constexpr (kHoldTarget) tg[c] = t0;
-    y[c] = t0;  // y0 = ybar0 = yhat (kernels.py:229-231)
+    if constexpr (QP) {  // y0 = ybar0: the caller's start or zero (diagonal_qp.py:257-262)
+      qh[c] = j >= 0 ? reinterpret_cast<const V*>(A.Qs)[tile * (int64_t)A.Kc + c * NT + t] : vzero;
+      y[c] = j >= 0 ? reinterpret_cast<const V*>(A.Y0s)[tile * (int64_t)A.Kc + c * NT + t] : vzero;
+    } else {
+      y[c] = t0;  // y0 = ybar0 = yhat (kernels.py:229-231)
+    }
     ent_write<V>(soff_c[c], y[c]);
   }
 #pragma unroll
@@ -446,9 +521,15 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 
   for (int64_t it = 0; it < A.iters; ++it) {
     // wave-uniform schedule scalars: scalar loads through the constant address space
-    const __attribute__((address_space(4))) T* sc =
-        (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
-    const T sigma = sc[0], a = sc[1], delta = sc[2], theta = sc[3];
+    T sigma = T(0), a = T(0), delta = T(0), theta = T(0);
+    if constexpr (!QP) {  // QP: the per-sample steps in registers instead
+      const __attribute__((address_space(4))) T* sc =
+          (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
+      sigma = sc[0];
+      a = sc[1];
+      delta = sc[2];
+      theta = sc[3];
+    }
     uint32_t pos = first + 1 + (pro & 1u);
     V carry = vzero;  // the head of the next slot (a chunk shared by two slots)
     // the slot tables, opaque to the loop so that their fields are decoded at
@@ -462,7 +543,14 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
                                               b0, b1, pos, A.stream, lane16,
                                               r == 0 && (pro & 1u));
-      V p = dold + sigma * (acc - rr[r]);
+      V p;
+      if constexpr (QP) {
+        const V e = acc - rr[r];
+#pragma unroll
+        for (int s = 0; s < BT; ++s) p[s] = dold[s] + sig_s[s] * e[s];
+      } else {
+        p = dold + sigma * (acc - rr[r]);
+      }
       if (ineq & (1u << r)) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
@@ -487,7 +575,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       GP hb = (GP)A.Hs;
       asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
-      if (SB && uni) {
+      if ((SB || QP) && uni) {
         lo = V(lo0);
         hi = V(hi0);
       } else if (SB) {
@@ -509,7 +597,18 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       const V tt = slot_sum<T, V, (SLC > 1)>(slot_field(cc, c), slot_field(cl, c), carry,
                                              b0, b1, pos, A.stream, lane16,
                                              c == 0 && (pro & 2u));
-      const V sv = a * y[c] - delta * tt + delta * tgc;
+      V sv;
+      if constexpr (QP) {  // the general-q prox (kernels.py:68-73), as the streaming pass forms it
+#pragma unroll
+        for (int s = 0; s < BT; ++s) {
+          const T aj = T(1) / (T(1) + tau_s[s] * qh[c][s]);
+          const T dj = tau_s[s] * aj;
+          const T oj = -dj * tgc[s];
+          sv[s] = aj * y[c][s] - dj * tt[s] + oj;
+        }
+      } else {
+        sv = a * y[c] - delta * tt + delta * tgc;
+      }
       V yn;
       if (nanb & (1u << c)) {  // a NaN bound on this lane: the exact NaN-propagating clip
 #pragma unroll
@@ -518,8 +617,17 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) yn[s] = clip_nonnan_bounds(sv[s], lo[s], hi[s]);
       }
-      ent_write<V>(soff_c[c], yn + theta * (yn - y[c]));
+      if constexpr (QP) {
+        V yb;
+#pragma unroll
+        for (int s = 0; s < BT; ++s) yb[s] = yn[s] + th_s[s] * (yn[s] - y[c][s]);
+        ent_write<V>(soff_c[c], yb);
+      } else
+        ent_write<V>(soff_c[c], yn + theta * (yn - y[c]));
       y[c] = yn;
+    }
+    if constexpr (QP) {
+      if (A.gam) res_qp_schedule<T, BT>(gam_s, tau_s, sig_s, th_s);
     }
     // the next row pass's second chunk (b0 holds the copy of its first)
     if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16);

@@ -16,10 +16,14 @@ namespace purin {
 
 template <typename T, int SLR, int SLC, int NB>
 static int launch_nb(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
-                     bool early) {
-  auto kern = early ? (sb ? k_resident_early<T, SLR, SLC, true, NB>
-                          : k_resident_early<T, SLR, SLC, false, NB>)
-                    : (sb ? k_resident<T, SLR, SLC, true, NB> : k_resident<T, SLR, SLC, false, NB>);
+                     bool early, bool qp) {
+  // the diagonal QP: fixed iterations, per-sample bounds
+  if (qp && (sb || early)) return set_error(PURIN_CP_ERR_ARG, "resident QP variant out of range");
+  auto kern = qp ? k_resident<T, SLR, SLC, false, NB, true>
+              : early ? (sb ? k_resident_early<T, SLR, SLC, true, NB>
+                            : k_resident_early<T, SLR, SLC, false, NB>)
+                      : (sb ? k_resident<T, SLR, SLC, true, NB>
+                            : k_resident<T, SLR, SLC, false, NB>);
   if (int rc = raise_lds_cap((const void*)kern, lds)) return rc;
   kern<<<dim3((unsigned)tiles), dim3(kResThreads), lds, st>>>(R);
   return PURIN_CP_OK;
@@ -29,30 +33,30 @@ static int launch_nb(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds,
 // one column slot per thread (two LDS planes)
 template <typename T, int SLR, int SLC>
 static int launch_one(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
-                      bool early, int nb) {
+                      bool early, int nb, bool qp) {
   constexpr int NB = sizeof(T) == 4 && SLR == 1 && SLC == 1 ? 8 : ResVec<T>::BT;
   if (nb != NB) return set_error(PURIN_CP_ERR_ARG, "resident tile size out of range");
-  return launch_nb<T, SLR, SLC, NB>(R, st, tiles, lds, sb, early);
+  return launch_nb<T, SLR, SLC, NB>(R, st, tiles, lds, sb, early, qp);
 }
 
 template <typename T, int SLR>
 int launch_resident_rows(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
-                         bool sb, bool early, int nb) {
+                         bool sb, bool early, int nb, bool qp) {
   switch (slc) {
-    case 1: return launch_one<T, SLR, 1>(R, st, tiles, lds, sb, early, nb);
-    case 2: return launch_one<T, SLR, 2>(R, st, tiles, lds, sb, early, nb);
-    case 3: return launch_one<T, SLR, 3>(R, st, tiles, lds, sb, early, nb);
-    case 4: return launch_one<T, SLR, 4>(R, st, tiles, lds, sb, early, nb);
+    case 1: return launch_one<T, SLR, 1>(R, st, tiles, lds, sb, early, nb, qp);
+    case 2: return launch_one<T, SLR, 2>(R, st, tiles, lds, sb, early, nb, qp);
+    case 3: return launch_one<T, SLR, 3>(R, st, tiles, lds, sb, early, nb, qp);
+    case 4: return launch_one<T, SLR, 4>(R, st, tiles, lds, sb, early, nb, qp);
     default: return set_error(PURIN_CP_ERR_ARG, "resident column slot count out of range");
   }
 }
 
 #if PURIN_RES_F64
 template int launch_resident_rows<double, PURIN_RES_SLR>(const Res<double>&, hipStream_t, int64_t,
-                                                         size_t, int, bool, bool, int);
+                                                         size_t, int, bool, bool, int, bool);
 #else
 template int launch_resident_rows<float, PURIN_RES_SLR>(const Res<float>&, hipStream_t, int64_t,
-                                                        size_t, int, bool, bool, int);
+                                                        size_t, int, bool, bool, int, bool);
 #endif
 
 }  // namespace purin

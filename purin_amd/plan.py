@@ -361,9 +361,11 @@ class Plan:
 
     def qp_solve(self, q, c, rhs, lower, upper, *, values=None, y0=None, dual0=None,
                  tolerance=1e-9, max_iterations=10000, early_stop=True, check_every=32,
-                 save=False, timing=False, workspace=None):
+                 save=False, timing=False, workspace=None, streaming=False):
         """General diagonal QP (``purin_cp_qp_solve``): PreparedDiagonalQP.solve
-        semantics on a plan created with ``bound_presolve=False``."""
+        semantics on a plan created with ``bound_presolve=False``.  Fixed
+        iterations with the plan's own coefficients run on the resident kernel
+        where it applies; ``streaming`` forces the streaming passes."""
         batch = q.shape[0]
         M = self.me + self.mi
         q = self._tensor(q, (batch, self.n), "q")
@@ -380,6 +382,7 @@ class Plan:
         o.early_stop = int(bool(early_stop))
         o.check_every = int(check_every)
         o.timing = int(bool(timing))
+        o.streaming = int(bool(streaming))
         _set_workspace(o, workspace)
         y = self._empty(batch, self.n)
         mult = self._empty(batch, M)

@@ -98,6 +98,76 @@ def test_qp_solve_matches_oracle(dtype, early_stop, accelerated):
 
 
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_qp_resident_matches_streaming_and_oracle(dtype, accelerated):
+    """Fixed iterations of the diagonal QP with the plan's own coefficients run
+    on the resident kernel (per-sample q and c in registers, per-sample steps
+    advanced in the kernel as the streaming passes' schedule does,
+    kernels.py:279-283 with gamma = min q): against the streaming passes on
+    the whole batch and the oracle on two samples, for every slot count of the
+    resident schedule (1, 2, 4 and 8 per thread), with a warm start."""
+    require_gpu()
+    for n, me, mi, width, B in ((30, 4, 10, 4, 33), (700, 100, 300, 5, 40),
+                                (1500, 300, 700, 6, 24), (4096, 1024, 2048, 8, 12)):
+        rng = np.random.default_rng(n + 7)
+        rows = [sorted(rng.choice(n, width, replace=False).tolist()) for _ in range(me + mi)]
+        support, mask = layout(rows, n)
+        coef = np.where(mask, rng.normal(size=mask.shape), 0)  # shared by the batch
+        values = np.broadcast_to(coef, (B,) + mask.shape)
+        q = rng.uniform(0.5, 3.0, (B, n))
+        c = rng.normal(size=(B, n)) * 2
+        x0 = rng.uniform(-0.4, 0.4, (B, n))
+        rhs = np.einsum("bmw,bmw->bm", values, x0[:, support])
+        rhs[:, me:] += rng.uniform(0.1, 1.0, (B, mi))
+        lower = np.where(rng.uniform(size=(B, n)) < 0.2, -np.inf, -0.8)
+        upper = np.where(rng.uniform(size=(B, n)) < 0.2, np.inf, 0.8)
+        y0 = rng.uniform(-0.5, 0.5, (B, n))
+        data = _cast(dq.QPData(q, c, values, rhs, lower, upper), dtype)
+        y0 = y0.astype(dtype)
+        import torch
+        from purin_amd.plan import Plan
+
+        indptr = np.zeros(len(rows) + 1, np.int64)
+        indptr[1:] = np.cumsum([len(r) for r in rows])
+        indices = np.asarray([j for r in rows for j in r], np.int32)
+        plan = Plan(n, me, mi, indptr, indices, coef[mask], bound_presolve=False,
+                    dtype=torch.float64 if dtype == np.float64 else torch.float32,
+                    accelerated=accelerated, device="cuda")
+        iters = 300
+        kw = dict(max_iterations=iters, early_stop=False, y0=y0, timing=True)
+        print(f"QP resident n={n} {np.dtype(dtype).name} accelerated={accelerated}", flush=True)
+        res = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, **kw)
+        assert plan.last_timing()["resident"] == 1, n
+        st = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, streaming=True, **kw)
+        assert plan.last_timing()["resident"] == 0, n
+        bar = TOL[dtype]
+        assert rel_err(to_np(res.y), to_np(st.y)) <= bar, n
+        assert rel_err(to_np(res.multipliers), to_np(st.multipliers)) <= bar, n
+        assert rel_err(to_np(res.slacks), to_np(st.slacks)) <= bar, n
+        np.testing.assert_array_equal(to_np(res.status), to_np(st.status))
+        np.testing.assert_array_equal(to_np(res.iterations), iters)
+        sub = slice(0, 2)
+        cfg = Config(accelerated=accelerated, max_iterations=iters, early_stop=False)
+        want = dq.solve(support, mask, me, dq.QPData(*(x[sub] for x in data)), cfg,
+                        y0=y0[sub])
+        assert rel_err(to_np(res.y)[sub], want.y) <= bar, n
+        want_mult = np.concatenate([want.multipliers_eq, want.multipliers_ineq], axis=1)
+        assert rel_err(to_np(res.multipliers)[sub], want_mult) <= bar, n
+        np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
+        y, lo, hi = to_np(res.y)[sub], data.lower[sub], data.upper[sub]
+        np.testing.assert_array_equal(y == lo, want.y == lo)
+        np.testing.assert_array_equal(y == hi, want.y == hi)
+        # one box for every sample and column: the kernel holds it in registers
+        box = np.full((B, n), 0.8, dtype)
+        rb = plan.qp_solve(data.q, data.c, data.rhs, -box, box, **kw)
+        assert plan.last_timing()["resident"] == 1, n
+        sb = plan.qp_solve(data.q, data.c, data.rhs, -box, box, streaming=True, **kw)
+        assert rel_err(to_np(rb.y), to_np(sb.y)) <= bar, n
+        assert rel_err(to_np(rb.multipliers), to_np(sb.multipliers)) <= bar, n
+        np.testing.assert_array_equal(to_np(rb.y) == 0.8, to_np(sb.y) == 0.8)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
 @pytest.mark.parametrize("mode", ["diagonal", "power"])
 def test_qp_step_variants_match_oracle(dtype, mode):
     """Per-variable diagonal steps (q does not enter them, kernels.py:76-88) and
@@ -121,8 +191,11 @@ def test_qp_step_variants_match_oracle(dtype, mode):
 def test_qp_shared_values_and_warm_start(early_stop):
     """values = None uses the plan's coefficients for every sample; a warm start
     (y0, dual0) enters the iteration like the oracle's (diagonal_qp.py:240-273).
-    The shared path reads one copy of the scaled entries, the same bits as every
-    sample's copy when the values are passed per sample, so the two agree exactly."""
+    The shared streaming path reads one copy of the scaled entries, the same
+    bits as every sample's copy when the values are passed per sample, so the
+    two agree exactly.  (Fixed iterations with shared values run on the
+    resident kernel by default, which sums in its own scheduled order: held to
+    the oracle at the parity bar.)"""
     require_gpu()
     rows, me, mi, n, support, mask, data = _problem(43, B=17)
     shared = data.values[0]
@@ -147,11 +220,14 @@ def test_qp_shared_values_and_warm_start(early_stop):
     got = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, y0=y0, dual0=d0,
                         max_iterations=iters, early_stop=early_stop)
     assert rel_err(to_np(got.y), want.y) <= 1e-10
+    got_s = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, y0=y0, dual0=d0,
+                          max_iterations=iters, early_stop=early_stop, streaming=True)
+    assert rel_err(to_np(got_s.y), want.y) <= 1e-10
     got2 = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, y0=y0, dual0=d0,
                          values=data.values[:, mask], max_iterations=iters,
                          early_stop=early_stop)
-    np.testing.assert_array_equal(to_np(got2.y), to_np(got.y))
-    np.testing.assert_array_equal(to_np(got2.iterations), to_np(got.iterations))
+    np.testing.assert_array_equal(to_np(got2.y), to_np(got_s.y))
+    np.testing.assert_array_equal(to_np(got2.iterations), to_np(got_s.iterations))
 
 
 @pytest.mark.parametrize("mode", ["scalar", "diagonal"])
