@@ -313,7 +313,10 @@ int purin_cp_project_values(purin_cp_plan* plan, void* stream, int64_t batch,
  * rhs (B, me+mi); y0 (B, n) or NULL for zero; dual0 (B, me+mi) or NULL.
  * Outputs y (B, n), multipliers (B, me+mi), slacks (B, mi), status,
  * iterations, residual (original units), finite, converged (B); each but y
- * may be NULL.  opts->shared_bounds must be 0.
+ * may be NULL.  opts->shared_bounds must be 0.  Fixed iterations
+ * (early_stop = 0) with the plan's own coefficients (values NULL) run on the
+ * resident kernel where the problem fits it (opts->streaming = 1 forces the
+ * streaming passes); the results agree to rounding.
  */
 int purin_cp_qp_solve(purin_cp_plan* plan, void* stream, int64_t batch, const void* q,
                       const void* c, const void* values, const void* rhs, const void* lower,
