@@ -456,9 +456,9 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   const bool early = o.early_stop != 0;
   const size_t lds = resident_lds<T>(p, early);
   // the resident kernel takes one schedule of scalar steps for the whole tile,
-  // or, for the diagonal QP's fixed iterations with the plan's own
-  // coefficients (one shared copy), per-sample steps it advances itself
-  const bool res_qp = qp && !qp->dense && ps && ps->RVs && !early && !o.shared_bounds;
+  // or, for the diagonal QP with the plan's own coefficients (one shared
+  // copy), per-sample steps it advances itself
+  const bool res_qp = qp && !qp->dense && ps && ps->RVs && !o.shared_bounds;
   if (lds && !o.streaming && !p->diag && ((!ps && !qp) || res_qp)) {
     if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds, early, batch, tol_scalar, tolv, done,
                                  count, noalloc, res_qp ? qp : nullptr, res_qp ? ps : nullptr))

@@ -760,7 +760,7 @@ __device__ __forceinline__ T read_lane(T v, int l) {
   }
 }
 
-template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT>
+template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT, bool QP = false>
 __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   constexpr int NT = 1024;
   constexpr int BT = NB;
@@ -810,12 +810,40 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   constexpr bool kHold = SLR <= 3;
   uint32_t soff_r[SLR], soff_c[SLC];
   V ky[SLR], dk[SLR], tgh[kHold ? SLC : 1], rrh[kHold ? SLR : 1];
+  // QP (as in k_resident): q of the thread's columns (Ts holds c), and the
+  // tile's per-sample steps in SGPRs
+  V qh[QP ? SLC : 1];
+  T tau_s[BT], sig_s[BT], th_s[BT], gam_s[BT];
+  if constexpr (QP) {
+#pragma unroll
+    for (int s = 0; s < BT; ++s) {
+      const int64_t b = tile * BT + s;
+      tau_s[s] = res_uniform(A.step0[b]);
+      sig_s[s] = res_uniform(A.step0[A.Bp + b]);
+      th_s[s] = res_uniform(A.gam ? A.step0[4 * A.Bp + b] : T(1));
+      gam_s[s] = res_uniform(A.gam ? A.gam[b] : T(0));
+    }
+  }
   typedef const __attribute__((address_space(1))) V* GV;
   uint32_t ineq = 0, nanb = 0, rvalid = 0, cvalid = 0;
   // shared bounds equal on every column of the wavefront's slots: taken from
-  // registers in the loop (as in k_resident; a ballot, no LDS)
-  const T lo0 = A.Ls[0], hi0 = A.Hs[0];
-  int same = SB && lo0 == lo0 && hi0 == hi0;
+  // registers in the loop (as in k_resident; a ballot, no LDS); for the QP's
+  // per-sample bounds, one box for every column and sample of those slots
+  T lo0 = A.Ls[0], hi0 = A.Hs[0];
+  if constexpr (QP) {
+    T rl = T(0), rh = T(0);
+#pragma unroll
+    for (int c = SLC - 1; c >= 0; --c) {  // ends on the first valid slot
+      const int64_t e0 = (tile * (int64_t)A.Kc + c * NT + t) * BT;
+      if (A.colmap[c * NT + t] >= 0) {
+        rl = A.Ls[e0];
+        rh = A.Hs[e0];
+      }
+    }
+    lo0 = res_uniform(rl);
+    hi0 = res_uniform(rh);
+  }
+  int same = (SB || QP) && lo0 == lo0 && hi0 == hi0;
 #pragma unroll
   for (int c = 0; c < SLC; ++c) {
     const int j = A.colmap[c * NT + t];
@@ -823,14 +851,22 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     for (int s = 0; s < BT; ++s) {
       const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
       if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
-      if (SB && j >= 0 && (A.Ls[e] != lo0 || A.Hs[e] != hi0)) same = 0;
+      if ((SB || QP) && j >= 0 && (A.Ls[e] != lo0 || A.Hs[e] != hi0)) same = 0;
     }
     if (j >= 0) cvalid |= 1u << c;
     soff_c[c] = j >= 0 ? (uint32_t)A.colent[c * NT + t] * 16u : trash_off;
-    // y0 = ybar0 = yhat (kernels.py:229-231); empty slots hold zeros
+    // y0 = ybar0 = yhat (kernels.py:229-231), for the QP the caller's start or
+    // zero (diagonal_qp.py:257-262); empty slots hold zeros
     const V t0 = reinterpret_cast<const V*>(A.Ts)[tile * (int64_t)A.Kc + c * NT + t];
     if constexpr (kHold) tgh[c] = t0;
-    ent_write<V>(soff_c[c], j >= 0 ? t0 : vzero);
+    if constexpr (QP) {
+      qh[c] = j >= 0 ? reinterpret_cast<const V*>(A.Qs)[tile * (int64_t)A.Kc + c * NT + t] : vzero;
+      ent_write<V>(soff_c[c],
+                   j >= 0 ? reinterpret_cast<const V*>(A.Y0s)[tile * (int64_t)A.Kc + c * NT + t]
+                          : vzero);
+    } else {
+      ent_write<V>(soff_c[c], j >= 0 ? t0 : vzero);
+    }
   }
 #pragma unroll
   for (int r = 0; r < SLR; ++r) {
@@ -864,7 +900,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   // K y0 (= K ybar0) by one row sweep, and the first candidate duals; b0 then
   // holds the first column chunk
   {
-    const T sigma0 = A.sched[0];
+    const T sigma0 = QP ? T(0) : A.sched[0];
     V carry = vzero;  // the head of the next slot (a chunk shared by two slots)
     const uint32_t rc = rcnt, rl = rlast;
 #pragma unroll
@@ -876,7 +912,14 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         ent_write<V>(kyl_off + (uint32_t)(r * NT + t) * 16u, k0);
       else
         ky[r] = k0;
-      V p = ent_read<V>(soff_r[r]) + sigma0 * (k0 - rr);
+      V p;
+      if constexpr (QP) {
+        const V dd = ent_read<V>(soff_r[r]), e = k0 - rr;
+#pragma unroll
+        for (int s = 0; s < BT; ++s) p[s] = dd[s] + sig_s[s] * e[s];
+      } else {
+        p = ent_read<V>(soff_r[r]) + sigma0 * (k0 - rr);
+      }
       if (ineq & (1u << r)) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
@@ -891,9 +934,14 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   __syncthreads();
 
   for (int64_t it = 0; it < A.iters && act != 0u; ++it) {
-    const __attribute__((address_space(4))) T* sc =
-        (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
-    const T a = sc[1], delta = sc[2], theta = sc[3];
+    T a = T(0), delta = T(0), theta = T(0);
+    if constexpr (!QP) {
+      const __attribute__((address_space(4))) T* sc =
+          (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
+      a = sc[1];
+      delta = sc[2];
+      theta = sc[3];
+    }
     // ---- column pass, masked, with the column diagnostics (Gd holds d+) ---------------
     V qp = vzero, qd = vzero, qc = vzero;
     V carry = vzero;  // the head of the next slot (a chunk shared by two slots)
@@ -918,7 +966,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
                                              b0, b1, pos, A.stream, lane16, c == 0 && (pro & 2u));
       asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
-      if (SB && uni) {
+      if ((SB || QP) && uni) {
         lo = V(lo0);
         hi = V(hi0);
       } else if (SB) {
@@ -929,7 +977,18 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         hi = ((GV)hb)[tile * (int64_t)A.Kc + c * NT + t];
       }
       const V yo = ent_read<V>(soff_c[c]);
-      const V sv = a * yo - delta * tt + delta * tg;
+      V sv;
+      if constexpr (QP) {  // the general-q prox (kernels.py:68-73), as in k_resident
+#pragma unroll
+        for (int s = 0; s < BT; ++s) {
+          const T aj = T(1) / (T(1) + tau_s[s] * qh[c][s]);
+          const T dj = tau_s[s] * aj;
+          const T oj = -dj * tg[s];
+          sv[s] = aj * yo[s] - dj * tt[s] + oj;
+        }
+      } else {
+        sv = a * yo - delta * tt + delta * tg;
+      }
       V yn;
       if (nanb & (1u << c)) {
 #pragma unroll
@@ -943,7 +1002,23 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         for (int s = 0; s < BT; ++s)
           if (!(act & (1u << s))) yn[s] = yo[s];  // a frozen sample keeps its state
       }
-      if (cvalid & (1u << c)) {  // diagnostics with q = 1, c = -yhat (kernels.py:158-174, 272-274)
+      if (QP && (cvalid & (1u << c))) {
+        // diagnostics with general q, c (kernels.py:158-174, 272-274), the
+        // streaming column pass's expressions; a non-finite stationarity term
+        // counts as infinite, as in the NaN-bound branch below
+#pragma unroll
+        for (int s = 0; s < BT; ++s) {
+          const T yv = yn[s], q = qh[QP ? c : 0][s], cq = tg[s];
+          qp[s] += half * q * yv * yv + cq * yv;
+          const T tf = cq + tt[s];
+          const T mz = q > T(1e-12) ? clipp(-tf / q, lo[s], hi[s]) : (tf >= zero ? lo[s] : hi[s]);
+          qd[s] += half * q * (mz * mz) + tf * mz;
+          T g = maxp(absv(yv - clipp(yv - ((q * yv + cq) + tt[s]), lo[s], hi[s])),
+                     maxp(maxp(lo[s] - yv, zero), maxp(yv - hi[s], zero)));
+          if (!finite(g)) g = inf;
+          qc[s] = __builtin_fmax(qc[s], g);
+        }
+      } else if (cvalid & (1u << c)) {  // diagnostics with q = 1, c = -yhat (kernels.py:158-174, 272-274)
         if (!(nanb & (1u << c))) {
           // Bounds without NaN (the usual lane): y+ is a clip to [lo, hi], so
           // its bound violation is 0; y - (y + c + K^T d) = -c - K^T d, so the
@@ -989,8 +1064,15 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     pos = first + 1 + (pro & 1u);
     // the next iteration's sigma (the candidates are formed only when it runs)
     const bool more = it + 1 < A.iters;
-    const T sigma_n = more ? A.sched[4 * (it + 1)] : zero;
+    const T sigma_n = (more && !QP) ? A.sched[4 * (it + 1)] : zero;
     const T tp1 = T(1) + theta;
+    // QP: this iteration's theta (of K ybar), then the steps of the next one
+    T thq[BT];
+    if constexpr (QP) {
+#pragma unroll
+      for (int s = 0; s < BT; ++s) thq[s] = th_s[s];
+      if (A.gam) res_qp_schedule<T, BT>(gam_s, tau_s, sig_s, th_s);
+    }
     // the slot-ordered rhs when not held: through an opaque base, so the loads
     // stay inside the loop
     GV rb = (GV)Rs;
@@ -1021,7 +1103,14 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         // next column pass does, after the barriers below).  The committed d+
         // stays in dk until the decision: a sample accepted now gets it back.
         const V kyo = r < KYL ? ent_read<V>(kyl_off + (uint32_t)(r * NT + t) * 16u) : ky[r];
-        V p = d + sigma_n * ((tp1 * acc - theta * kyo) - rr);
+        V p;
+        if constexpr (QP) {
+#pragma unroll
+          for (int s = 0; s < BT; ++s)
+            p[s] = d[s] + sig_s[s] * (((T(1) + thq[s]) * acc[s] - thq[s] * kyo[s]) - rr[s]);
+        } else {
+          p = d + sigma_n * ((tp1 * acc - theta * kyo) - rr);
+        }
         if (ineq & (1u << r)) {
 #pragma unroll
           for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));

@@ -17,9 +17,10 @@ namespace purin {
 template <typename T, int SLR, int SLC, int NB>
 static int launch_nb(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
                      bool early, bool qp) {
-  // the diagonal QP: fixed iterations, per-sample bounds
-  if (qp && (sb || early)) return set_error(PURIN_CP_ERR_ARG, "resident QP variant out of range");
-  auto kern = qp ? k_resident<T, SLR, SLC, false, NB, true>
+  // the diagonal QP takes per-sample bounds
+  if (qp && sb) return set_error(PURIN_CP_ERR_ARG, "resident QP variant out of range");
+  auto kern = qp ? (early ? k_resident_early<T, SLR, SLC, false, NB, true>
+                          : k_resident<T, SLR, SLC, false, NB, true>)
               : early ? (sb ? k_resident_early<T, SLR, SLC, true, NB>
                             : k_resident_early<T, SLR, SLC, false, NB>)
                       : (sb ? k_resident<T, SLR, SLC, true, NB>

@@ -22,7 +22,11 @@ scaled by 1 +- 1e-6) and
   others to max(10 bar, 2 d), with d the sample's distance (relative to the
   batch's largest entry) between the oracle and its perturbed runs.
 
-The perturbed runs are computed only when some count differs.
+A caller may add further perturbed runs (``alternates``): the same problem
+solved another way, e.g. the oracle in fp64 on the fp32 inputs, whose margins
+then measure the fp32 rounding noise of the margin itself (the objective sums
+behind the gap carry rounding error of their own, which a change of the steps
+does not show).  The perturbed runs are computed only when some count differs.
 """
 
 from __future__ import annotations
@@ -35,13 +39,16 @@ class Margins:
 
     ``solve(safety, trace)`` runs the oracle at the given safety factor,
     appending each iteration's (B,) margins to ``trace``, and returns its
-    result (with ``.iterations`` and ``.y``).
+    result (with ``.iterations`` and ``.y``).  ``alternates``: further
+    callables ``alt(trace)`` solving the same problem another way (results
+    and traces as ``solve``'s), counted among the perturbed runs.
     """
 
-    def __init__(self, solve, dtype, safety=0.95):
+    def __init__(self, solve, dtype, safety=0.95, alternates=()):
         self._solve = solve
         self.dtype = np.dtype(dtype)
         self.safety = safety
+        self._alternates = tuple(alternates)
         trace = []
         self.want = solve(safety, trace)
         self.trace = np.asarray(trace, np.float64)
@@ -49,12 +56,17 @@ class Margins:
 
     @property
     def others(self):
-        """[(result, trace)] of the runs with safety * (1 + 1e-6) and * (1 - 1e-6)."""
+        """[(result, trace)] of the runs with safety * (1 + 1e-6) and * (1 - 1e-6),
+        then of the alternates."""
         if self._others is None:
             self._others = []
             for f in (1 + 1e-6, 1 - 1e-6):
                 tr = []
                 res = self._solve(self.safety * f, tr)
+                self._others.append((res, np.asarray(tr, np.float64)))
+            for alt in self._alternates:
+                tr = []
+                res = alt(tr)
                 self._others.append((res, np.asarray(tr, np.float64)))
         return self._others
 

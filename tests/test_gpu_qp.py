@@ -15,7 +15,7 @@ from oracle import diagonal_qp as dq
 from oracle.cp import layout
 from oracle.projection import Config
 from tests._gpu import rel_err, require_gpu, to_np
-from tests._margins import Margins, check_counts
+from tests._margins import Margins, check_counts, check_iterates
 
 pytestmark = pytest.mark.gpu
 
@@ -97,6 +97,41 @@ def test_qp_solve_matches_oracle(dtype, early_stop, accelerated):
         assert len(np.unique(want.iterations)) > 1
 
 
+# sizes (n, me, mi, width, B) covering every slot count of the resident
+# schedule (1, 2, 4 and 8 row and column slots per thread)
+RESIDENT_QP_SIZES = ((30, 4, 10, 4, 33), (700, 100, 300, 5, 40), (1500, 300, 700, 6, 24),
+                     (4096, 1024, 2048, 8, 12))
+
+
+def _shared_qp(n, me, mi, width, B, dtype, accelerated):
+    """A QP whose coefficients are the plan's own (one set for the batch):
+    per-sample q, c, rhs, bounds (some infinite) and a warm start y0."""
+    import torch
+    from purin_amd.plan import Plan
+
+    rng = np.random.default_rng(n + 7)
+    rows = [sorted(rng.choice(n, width, replace=False).tolist()) for _ in range(me + mi)]
+    support, mask = layout(rows, n)
+    coef = np.where(mask, rng.normal(size=mask.shape), 0)
+    values = np.broadcast_to(coef, (B,) + mask.shape)
+    q = rng.uniform(0.5, 3.0, (B, n))
+    c = rng.normal(size=(B, n)) * 2
+    x0 = rng.uniform(-0.4, 0.4, (B, n))
+    rhs = np.einsum("bmw,bmw->bm", values, x0[:, support])
+    rhs[:, me:] += rng.uniform(0.1, 1.0, (B, mi))
+    lower = np.where(rng.uniform(size=(B, n)) < 0.2, -np.inf, -0.8)
+    upper = np.where(rng.uniform(size=(B, n)) < 0.2, np.inf, 0.8)
+    y0 = rng.uniform(-0.5, 0.5, (B, n)).astype(dtype)
+    data = _cast(dq.QPData(q, c, values, rhs, lower, upper), dtype)
+    indptr = np.zeros(len(rows) + 1, np.int64)
+    indptr[1:] = np.cumsum([len(r) for r in rows])
+    indices = np.asarray([j for r in rows for j in r], np.int32)
+    plan = Plan(n, me, mi, indptr, indices, coef[mask], bound_presolve=False,
+                dtype=torch.float64 if dtype == np.float64 else torch.float32,
+                accelerated=accelerated, device="cuda")
+    return support, mask, data, y0, plan
+
+
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
 @pytest.mark.parametrize("accelerated", [False, True])
 def test_qp_resident_matches_streaming_and_oracle(dtype, accelerated):
@@ -105,34 +140,10 @@ def test_qp_resident_matches_streaming_and_oracle(dtype, accelerated):
     advanced in the kernel as the streaming passes' schedule does,
     kernels.py:279-283 with gamma = min q): against the streaming passes on
     the whole batch and the oracle on two samples, for every slot count of the
-    resident schedule (1, 2, 4 and 8 per thread), with a warm start."""
+    resident schedule, with a warm start, random boxes and one shared box."""
     require_gpu()
-    for n, me, mi, width, B in ((30, 4, 10, 4, 33), (700, 100, 300, 5, 40),
-                                (1500, 300, 700, 6, 24), (4096, 1024, 2048, 8, 12)):
-        rng = np.random.default_rng(n + 7)
-        rows = [sorted(rng.choice(n, width, replace=False).tolist()) for _ in range(me + mi)]
-        support, mask = layout(rows, n)
-        coef = np.where(mask, rng.normal(size=mask.shape), 0)  # shared by the batch
-        values = np.broadcast_to(coef, (B,) + mask.shape)
-        q = rng.uniform(0.5, 3.0, (B, n))
-        c = rng.normal(size=(B, n)) * 2
-        x0 = rng.uniform(-0.4, 0.4, (B, n))
-        rhs = np.einsum("bmw,bmw->bm", values, x0[:, support])
-        rhs[:, me:] += rng.uniform(0.1, 1.0, (B, mi))
-        lower = np.where(rng.uniform(size=(B, n)) < 0.2, -np.inf, -0.8)
-        upper = np.where(rng.uniform(size=(B, n)) < 0.2, np.inf, 0.8)
-        y0 = rng.uniform(-0.5, 0.5, (B, n))
-        data = _cast(dq.QPData(q, c, values, rhs, lower, upper), dtype)
-        y0 = y0.astype(dtype)
-        import torch
-        from purin_amd.plan import Plan
-
-        indptr = np.zeros(len(rows) + 1, np.int64)
-        indptr[1:] = np.cumsum([len(r) for r in rows])
-        indices = np.asarray([j for r in rows for j in r], np.int32)
-        plan = Plan(n, me, mi, indptr, indices, coef[mask], bound_presolve=False,
-                    dtype=torch.float64 if dtype == np.float64 else torch.float32,
-                    accelerated=accelerated, device="cuda")
+    for n, me, mi, width, B in RESIDENT_QP_SIZES:
+        support, mask, data, y0, plan = _shared_qp(n, me, mi, width, B, dtype, accelerated)
         iters = 300
         kw = dict(max_iterations=iters, early_stop=False, y0=y0, timing=True)
         print(f"QP resident n={n} {np.dtype(dtype).name} accelerated={accelerated}", flush=True)
@@ -165,6 +176,67 @@ def test_qp_resident_matches_streaming_and_oracle(dtype, accelerated):
         assert rel_err(to_np(rb.y), to_np(sb.y)) <= bar, n
         assert rel_err(to_np(rb.multipliers), to_np(sb.multipliers)) <= bar, n
         np.testing.assert_array_equal(to_np(rb.y) == 0.8, to_np(sb.y) == 0.8)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_qp_resident_early_stop(dtype, accelerated):
+    """PreparedDiagonalQP.solve's default loop (early stop, freezing,
+    stationarity; kernels.py:238-290 with general q, c) on the resident
+    kernel: each sample stops on its own.  fp64 iteration counts equal the
+    streaming passes' and the oracle's; fp32 counts follow the oracle under
+    the rule of tests/_margins.py, with the oracle's fp64 run on the same
+    inputs among the perturbed runs; same-count iterates and multipliers at
+    the parity bar; statuses equal."""
+    require_gpu()
+    # fp32 at 1e-2: there the oracle's fp32 and fp64 runs stop every sample at
+    # the same iteration, with margins 1e-4 to 1e-3 apart at the stop.  At 1e-3
+    # the accelerated n = 4096 samples' margins fall by ~10 % per iteration
+    # through 1 and sit ~1.5 % apart between the oracle's fp32 and fp64 runs
+    # and ~6 % between the oracle and this kernel (its K ybar from K y, its sums
+    # in scheduled order), so rounding, not the recurrence, picks the
+    # iteration there.
+    tol = 1e-6 if dtype == np.float64 else 1e-2
+    n_oracle = {30: 8, 700: 4, 1500: 3, 4096: 2}
+    stopped = 0
+    for n, me, mi, width, B in RESIDENT_QP_SIZES:
+        support, mask, data, y0, plan = _shared_qp(n, me, mi, width, B, dtype, accelerated)
+        kw = dict(max_iterations=2000, early_stop=True, tolerance=tol, y0=y0, check_every=7,
+                  timing=True)
+        print(f"QP resident early stop n={n} {np.dtype(dtype).name} accelerated={accelerated}",
+              flush=True)
+        res = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, **kw)
+        assert plan.last_timing()["resident"] == 1, n
+        st = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, streaming=True, **kw)
+        assert plan.last_timing()["resident"] == 0, n
+        it_r, it_s = to_np(res.iterations), to_np(st.iterations)
+        bar = TOL[dtype]
+        same = it_r == it_s
+        if dtype == np.float64:
+            np.testing.assert_array_equal(it_r, it_s)
+        assert rel_err(to_np(res.y)[same], to_np(st.y)[same]) <= bar, n
+        assert rel_err(to_np(res.multipliers)[same], to_np(st.multipliers)[same]) <= bar, n
+        np.testing.assert_array_equal(to_np(res.status)[same], to_np(st.status)[same])
+        stopped += int(np.sum(it_r < kw["max_iterations"]))
+        sub = np.arange(n_oracle[n])
+        cfg = Config(accelerated=accelerated, max_iterations=kw["max_iterations"],
+                     early_stop=True, tolerance=tol)
+        part = dq.QPData(*(x[sub] for x in data))
+        # fp32: the oracle in fp64 on the same (fp32) inputs measures the
+        # rounding noise of the stop margin (the gap's objective sums)
+        part64 = dq.QPData(*(np.asarray(x, np.float64) for x in part))
+        alt = () if dtype == np.float64 else (
+            lambda tr: dq.solve(support, mask, me, part64, cfg,
+                                y0=y0[sub].astype(np.float64), trace=tr),)
+        mg = Margins(lambda safety, tr: dq.solve(support, mask, me, part,
+                                                 replace(cfg, safety=safety), y0=y0[sub],
+                                                 trace=tr), dtype, alternates=alt)
+        print(f"  counts gpu {it_r[sub].tolist()} oracle {mg.want.iterations.tolist()}",
+              flush=True)
+        same_o = check_counts(it_r, mg, samples=sub)
+        check_iterates(to_np(res.y), mg, same_o, bar, samples=sub)
+        np.testing.assert_array_equal(to_np(res.status)[sub][same_o], mg.want.status[same_o])
+    assert stopped > 0  # the stop test fired
 
 
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
@@ -267,7 +339,8 @@ def test_qp_vjp_matches_oracle_at_the_same_state(mode):
 def test_qp_adjoint_shared_values_equal_per_sample(mode):
     """The QP's VJP with the plan's own coefficients (values = None: one shared
     copy of the scaled entries) equals, bit for bit, the VJP with those
-    coefficients passed per sample."""
+    coefficients passed per sample (both forwards on the streaming passes,
+    which read the shared copy in the per-sample order)."""
     require_gpu()
     rows, me, mi, n, support, mask, data = _problem(45, n=16, me=2, mi=5, width=3, B=20)
     shared = data.values[0]
@@ -290,7 +363,7 @@ def test_qp_adjoint_shared_values_equal_per_sample(mode):
     outs = []
     for vals in (None, data.values[:, mask]):
         fwd = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, values=vals,
-                            tolerance=1e-9, max_iterations=20000, save=True)
+                            tolerance=1e-9, max_iterations=20000, save=True, streaming=True)
         adj = plan.qp_adjoint(fwd.saved, data.q, data.c, cot, values=vals, cot_dual=cot_dual,
                               tolerance=1e-12, max_iterations=200)
         outs.append((fwd, adj))
