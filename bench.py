@@ -342,9 +342,9 @@ def run_mode(args, torch):
             rhs = torch.as_tensor(np.tile(w.rhs[:general], (B, 1)), device=dev)
             lo = torch.full((B, w.n), -1.0, dtype=torch.float64, device=dev)
             hi = torch.full((B, w.n), 1.0, dtype=torch.float64, device=dev)
-            call = lambda timing=False, streaming=False: plan.qp_solve(
-                q, c, rhs, lo, hi, max_iterations=iters, early_stop=False, timing=timing,
-                streaming=streaming)
+            call = lambda timing=False, streaming=False, early=False: plan.qp_solve(
+                q, c, rhs, lo, hi, max_iterations=iters, early_stop=early, tolerance=1e-9,
+                timing=timing, streaming=streaming)
             extra_n = 1  # q and c replace the candidates: one more n-vector per iteration
         n, m, nnz = w.n, plan.m, int(plan.info.nnz_kept)
         # the QP with the plan's own coefficients reads one shared copy of them
@@ -447,6 +447,13 @@ def resident_qp_line(args, torch, plan, call, tm, B, n, m, nnz, ws, iters, ms_pe
     # q, c (2n) replace the candidates: B ws ((7 + 1) n + 3 m) per iteration
     bytes_iter = B * ws * (8 * n + 3 * m)
     streaming_ms, _ = time_calls(torch, lambda: call(streaming=True), 1)
+    # PreparedDiagonalQP.solve's default loop (early stop at tolerance 1e-9,
+    # freezing, stationarity) on the same inputs, resident and streaming
+    call(early=True)
+    early_ms, res = time_calls(torch, lambda: call(early=True, timing=True), 1)
+    early_resident = plan.last_timing()["resident"]
+    early_iters = int(res.iterations.max().item())
+    early_streaming_ms, _ = time_calls(torch, lambda: call(early=True, streaming=True), 1)
     line = {
         "metric": MODES[args.mode], "value": B / (ms_per_step / 1e3), "unit": "solves/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
@@ -470,6 +477,12 @@ def resident_qp_line(args, torch, plan, call, tm, B, n, m, nnz, ws, iters, ms_pe
         "iteration": {"resident_kernel": True, "iteration_ms": loop_ms / iters,
                       "streaming_passes_ms_per_step": streaming_ms,
                       "streaming_passes_value": B / (streaming_ms / 1e3)},
+        "early_stop": {"what": "the same solve with early stop at tolerance 1e-9 (the stop "
+                               "test every iteration, freezing, stationarity)",
+                       "ms_per_step": early_ms, "value": B / (early_ms / 1e3),
+                       "resident_kernel": bool(early_resident), "iterations_max": early_iters,
+                       "streaming_passes_ms_per_step": early_streaming_ms,
+                       "streaming_passes_value": B / (early_streaming_ms / 1e3)},
     }
     print(json.dumps(line), flush=True)
 
