@@ -327,8 +327,8 @@ def run_mode(args, torch):
             target = torch.as_tensor(w.target, device=dev)
             rhs = torch.as_tensor(np.tile(w.rhs, (B, 1)), device=dev)
             kw = dict(max_iterations=iters, early_stop=False)
-            call = lambda timing=False: plan.project(target, rhs, values=values, timing=timing,
-                                                     **kw)
+            call = lambda timing=False, streaming=False: plan.project(
+                target, rhs, values=values, timing=timing, streaming=streaming, **kw)
             extra_n = 0
         else:
             general = w.me + int(w.info["mi_general"])
@@ -392,7 +392,7 @@ def run_mode(args, torch):
     tm = plan.last_timing()
     it = max(int(tm["iterations"]), 1)
     if tm["resident"]:  # the diagonal QP's fixed iterations on the resident kernel
-        resident_qp_line(args, torch, plan, call, tm, B, n, m, nnz, ws, iters, ms_per_step,
+        resident_mode_line(args, torch, plan, call, tm, B, n, m, nnz, ws, iters, ms_per_step,
                          workload)
         return
     row_ms, col_ms = tm["row_ms"] / it, tm["col_ms"] / it
@@ -429,61 +429,87 @@ def run_mode(args, torch):
     print(json.dumps(line), flush=True)
 
 
-def resident_qp_line(args, torch, plan, call, tm, B, n, m, nnz, ws, iters, ms_per_step,
-                     workload):
-    """The ``--mode qp`` line when the QP runs on the resident kernel: priced,
-    like the headline, on the L2 -> CU matrix stream against the same-run stream
-    probe, with the state bytes on HBM terms as context and the streaming passes
-    on the same inputs beside it."""
+def resident_mode_line(args, torch, plan, call, tm, B, n, m, nnz, ws, iters, ms_per_step,
+                       workload):
+    """The ``--mode qp`` / ``--mode values`` line when the fixed iterations run on
+    the resident kernel.  The diagonal QP (the plan's shared coefficients) is
+    priced, like the headline, on the L2 -> CU matrix stream against the
+    same-run stream probe; per-sample coefficients on the HBM bytes of the
+    tiles' coefficient streams (each tile reads its samples' coefficients once
+    per iteration, in the plan's stream order) against the HBM peak.  The
+    state bytes on HBM terms are context; the streaming passes on the same
+    inputs are timed beside it."""
     info = plan.info
     bt = int(info.resident_tile_samples)
     pad = 64 * (2 if ws == 8 else 4)
     tiles = -(-B // pad) * pad // bt
     sbytes = int(info.resident_stream_bytes)
+    chunk = 64 * 16 + 64 * 4 * ws
     loop_ms = tm["loop_ms"]
-    l2_bytes = tiles * iters * sbytes
-    ceil = probe_ceilings(torch, tiles, (n + 1 + m + 1) * 16, sbytes)
-    l2_rate = l2_bytes / (loop_ms / 1e3) / 1e9
-    # q, c (2n) replace the candidates: B ws ((7 + 1) n + 3 m) per iteration
-    bytes_iter = B * ws * (8 * n + 3 * m)
     streaming_ms, _ = time_calls(torch, lambda: call(streaming=True), 1)
-    # PreparedDiagonalQP.solve's default loop (early stop at tolerance 1e-9,
-    # freezing, stationarity) on the same inputs, resident and streaming
-    call(early=True)
-    early_ms, res = time_calls(torch, lambda: call(early=True, timing=True), 1)
-    early_resident = plan.last_timing()["resident"]
-    early_iters = int(res.iterations.max().item())
-    early_streaming_ms, _ = time_calls(torch, lambda: call(early=True, streaming=True), 1)
+    if args.mode == "qp":
+        l2_bytes = tiles * iters * sbytes
+        ceil = probe_ceilings(torch, tiles, (n + 1 + m + 1) * 16, sbytes)
+        l2_rate = l2_bytes / (loop_ms / 1e3) / 1e9
+        # q, c (2n) replace the candidates: B ws ((7 + 1) n + 3 m) per iteration
+        bytes_iter = B * ws * (8 * n + 3 * m)
+        roofline = {"bound": "l2", "kernel": "k_resident (diagonal QP)", "achieved": l2_rate,
+                    "peak": ceil["l2"]["GBs"], "unit": "GB/s",
+                    "frac": l2_rate / ceil["l2"]["GBs"], "traffic": None,
+                    "bytes_per_launch": l2_bytes, "avg_launch_ms": loop_ms,
+                    "what": f"L2 -> CU bytes of the shared matrix's chunk streams: {sbytes} B "
+                            f"per workgroup per iteration x {tiles} workgroups x {iters} "
+                            "iterations",
+                    "peak_source": "measured in this run: best rate of the k_probe_stream "
+                                   f"ceiling probe at {tiles} workgroups of 1024 threads"}
+    else:
+        # every tile reads its coefficient stream once per iteration: 4 entries per
+        # lane per chunk, bt samples each
+        cbytes = tiles * iters * (sbytes // chunk) * 256 * bt * ws
+        rate = cbytes / (loop_ms / 1e3) / 1e9
+        bytes_iter = B * ws * (7 * n + 3 * m + 2 * nnz)
+        roofline = {"bound": "hbm", "kernel": "k_resident (per-sample coefficients)",
+                    "achieved": rate, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": rate / HBM_PEAK_GBS, "traffic": None, "bytes_per_launch": cbytes,
+                    "avg_launch_ms": loop_ms,
+                    "what": f"HBM bytes of the tiles' coefficient streams: {sbytes // chunk} "
+                            f"chunks x 256 entries x {bt} samples x {ws} B per workgroup per "
+                            f"iteration x {tiles} workgroups x {iters} iterations (the "
+                            "iterate stays on chip)"}
+    roofline["hbm_context"] = {
+        "achieved": bytes_iter * iters / (loop_ms / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
+        "bytes_per_launch": bytes_iter * iters,
+        "note": "algorithmic bytes of the streaming formulation per iteration (state "
+                "vectors" + (" and per-sample coefficients" if args.mode == "values" else "")
+                + "); the state stays on chip (context only)"}
     line = {
-        "metric": MODES[args.mode], "value": B / (ms_per_step / 1e3), "unit": "solves/s",
+        "metric": MODES[args.mode], "value": B / (ms_per_step / 1e3),
+        "unit": "solves/s" if args.mode == "qp" else "projections/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64",
         "data": "synthetic (numpy default_rng)",
         "config": {"workload": workload, "n": n, "rows": m, "nnz": nnz, "batch": B,
                    "iterations": iters, "parallelism": "1 GPU (batch-parallel)"},
-        "roofline": {"bound": "l2", "kernel": "k_resident (diagonal QP)", "achieved": l2_rate,
-                     "peak": ceil["l2"]["GBs"], "unit": "GB/s",
-                     "frac": l2_rate / ceil["l2"]["GBs"], "traffic": None,
-                     "bytes_per_launch": l2_bytes, "avg_launch_ms": loop_ms,
-                     "what": f"L2 -> CU bytes of the shared matrix's chunk streams: {sbytes} B "
-                             f"per workgroup per iteration x {tiles} workgroups x {iters} "
-                             "iterations",
-                     "peak_source": "measured in this run: best rate of the k_probe_stream "
-                                    f"ceiling probe at {tiles} workgroups of 1024 threads",
-                     "hbm": {"achieved": bytes_iter * iters / (loop_ms / 1e3) / 1e9,
-                             "peak": HBM_PEAK_GBS, "bytes_per_launch": bytes_iter * iters,
-                             "note": "algorithmic state bytes B*ws*(8n+3m) per iteration; "
-                                     "they stay on chip (context only)"}},
+        "roofline": roofline,
         "iteration": {"resident_kernel": True, "iteration_ms": loop_ms / iters,
                       "streaming_passes_ms_per_step": streaming_ms,
                       "streaming_passes_value": B / (streaming_ms / 1e3)},
-        "early_stop": {"what": "the same solve with early stop at tolerance 1e-9 (the stop "
-                               "test every iteration, freezing, stationarity)",
-                       "ms_per_step": early_ms, "value": B / (early_ms / 1e3),
-                       "resident_kernel": bool(early_resident), "iterations_max": early_iters,
-                       "streaming_passes_ms_per_step": early_streaming_ms,
-                       "streaming_passes_value": B / (early_streaming_ms / 1e3)},
     }
+    if args.mode == "qp":
+        # PreparedDiagonalQP.solve's default loop (early stop at tolerance 1e-9,
+        # freezing, stationarity) on the same inputs, resident and streaming
+        call(early=True)
+        early_ms, res = time_calls(torch, lambda: call(early=True, timing=True), 1)
+        early_resident = plan.last_timing()["resident"]
+        early_iters = int(res.iterations.max().item())
+        early_streaming_ms, _ = time_calls(torch, lambda: call(early=True, streaming=True), 1)
+        line["early_stop"] = {
+            "what": "the same solve with early stop at tolerance 1e-9 (the stop test every "
+                    "iteration, freezing, stationarity)",
+            "ms_per_step": early_ms, "value": B / (early_ms / 1e3),
+            "resident_kernel": bool(early_resident), "iterations_max": early_iters,
+            "streaming_passes_ms_per_step": early_streaming_ms,
+            "streaming_passes_value": B / (early_streaming_ms / 1e3)}
     print(json.dumps(line), flush=True)
 
 

@@ -292,7 +292,10 @@ int purin_cp_project_noalloc(purin_cp_plan* plan, void* stream, int64_t batch,
  *   values (B, nnz) in the plan's CSR entry order (indptr/indices given to
  *   plan_create; the plan's own values are not used by this call).
  * Other arguments and outputs as purin_cp_project(); opts->shared_bounds must
- * be 0.  The saved state is for purin_cp_adjoint_values() only.
+ * be 0.  The saved state is for purin_cp_adjoint_values() only.  Fixed
+ * iterations (early_stop = 0) run on the resident kernel where the problem
+ * fits it (each workgroup streams its samples' coefficients; opts->streaming
+ * = 1 forces the streaming passes); the results agree to rounding.
  */
 int purin_cp_project_values(purin_cp_plan* plan, void* stream, int64_t batch,
                             const void* values, const void* target, const void* rhs,

@@ -72,9 +72,12 @@ Layout make_layout(const purin_cp_plan* p, int64_t batch, bool values, int extra
     L.RD0 = take(Kr * Bp * es);
     L.RLs = take(Kc * Bp * es);
     L.RHs = take(Kc * Bp * es);
-    if (values) {  // the diagonal QP on the resident kernel
+    if (values) {  // the diagonal QP and per-sample coefficients on the resident kernel
       L.RQs = take(Kc * Bp * es);
       L.RY0 = take(Kc * Bp * es);
+      const size_t chunks = (size_t)p->res_stream_bytes /
+                            (64 * 16 + 64 * 4 * (size_t)es);  // the plan's stream chunks
+      L.RCS = take(chunks * 256 * Bp * es);
     }
   }
   if (values) {
@@ -249,18 +252,19 @@ int res_tile_samples(const purin_cp_plan* p) {
 }
 
 // One translation unit per (element type, row slots): resident_launch.hip.
+// kind: 0 the projection, 1 the diagonal QP, 2 per-sample coefficients
 template <typename T, int SLR>
 int launch_resident_rows(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
-                         bool sb, bool early, int nb, bool qp);
+                         bool sb, bool early, int nb, int kind);
 
 template <typename T>
 static int launch_resident(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slr,
-                           int slc, bool sb, bool early, int nb, bool qp) {
+                           int slc, bool sb, bool early, int nb, int kind) {
   switch (slr) {
-    case 1: return launch_resident_rows<T, 1>(R, st, tiles, lds, slc, sb, early, nb, qp);
-    case 2: return launch_resident_rows<T, 2>(R, st, tiles, lds, slc, sb, early, nb, qp);
-    case 3: return launch_resident_rows<T, 3>(R, st, tiles, lds, slc, sb, early, nb, qp);
-    case 4: return launch_resident_rows<T, 4>(R, st, tiles, lds, slc, sb, early, nb, qp);
+    case 1: return launch_resident_rows<T, 1>(R, st, tiles, lds, slc, sb, early, nb, kind);
+    case 2: return launch_resident_rows<T, 2>(R, st, tiles, lds, slc, sb, early, nb, kind);
+    case 3: return launch_resident_rows<T, 3>(R, st, tiles, lds, slc, sb, early, nb, kind);
+    case 4: return launch_resident_rows<T, 4>(R, st, tiles, lds, slc, sb, early, nb, kind);
     default: return set_error(PURIN_CP_ERR_ARG, "resident row slot count out of range");
   }
 }
@@ -282,8 +286,9 @@ static size_t resident_lds(const purin_cp_plan* p, bool early = false) {
 
 // The CP loop on the resident kernel; fills Y and D like the passes (and, with
 // early stop, the per-sample done flags and iteration counts).  qp (with ps):
-// the diagonal QP's fixed-iteration loop, q and c per sample, y0 from Y, the
-// per-sample steps of ps.
+// the diagonal QP, q and c per sample, y0 from Y, the per-sample steps of ps.
+// ps alone: per-sample coefficients (ps's RV, CV laid out in the plan's stream
+// order per tile) and per-sample steps.
 template <typename T>
 static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char* sv, char* ws,
                         const purin_cp_solve_options& o, size_t lds, bool early = false,
@@ -300,8 +305,8 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
                      "max_iterations exceeds the plan's step schedule (" +
                          std::to_string(p->res_sched_len) +
                          " iterations) in the no-allocation entry point");
-  const void* sched = p->res_sched;  // the QP kernel reads per-sample steps instead
-  if (!qp)
+  const void* sched = p->res_sched;  // per-sample steps (QP, coefficients) instead
+  if (!ps)
     if (int rc = ensure_schedule(p, o.max_iterations, st, false, &sched)) return rc;
   Res<T> R{};
   R.n = (int)p->n;
@@ -346,8 +351,26 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     R.Y0s = Y0s;
     R.step0 = ps->tau_b;  // [5][Bp]: tau, sigma, a, delta, theta of iteration 0
     R.gam = p->opts.accelerated ? qp->gamma : nullptr;
+    R.accel = p->opts.accelerated;
   } else {
     gather(gc, (const T*)(sv + L.Tt), p->res_colmap, Kc, Ts);
+  }
+  if (ps && !qp) {  // per-sample coefficients: each tile's stream of them
+    const int64_t entries = p->res_stream_bytes / (int64_t)res_chunk_bytes<T>() * 256;
+    T* CS = (T*)(ws + L.RCS);
+    const int64_t threads = entries * tiles;
+    const unsigned blocks = (unsigned)((threads + 255) / 256);
+    if (BT == 8)
+      k_res_coef_stream<T, 8><<<blocks, 256, 0, st>>>(p->res_srcmap, entries, ps->RV, ps->CV, Bp,
+                                                      tiles, CS);
+    else
+      k_res_coef_stream<T, ResVec<T>::BT><<<blocks, 256, 0, st>>>(p->res_srcmap, entries, ps->RV,
+                                                                  ps->CV, Bp, tiles, CS);
+    R.Cs = CS;
+    R.cs_tile = entries;
+    R.step0 = ps->tau_b;
+    R.gam = nullptr;  // gamma = min q = 1
+    R.accel = p->opts.accelerated;
   }
   gather(gr, (const T*)(sv + L.R), p->res_rowmap, Kr, Rs);
   gather(gr, (const T*)(sv + L.D), p->res_rowmap, Kr, D0s);
@@ -374,7 +397,8 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     PURIN_HIP(hipEventRecord(e0, st));
   }
   if (int rc = launch_resident<T>(R, st, tiles, lds, p->res_mr, p->res_mc,
-                                  o.shared_bounds != 0, early, BT, qp != nullptr)) return rc;
+                                  o.shared_bounds != 0, early, BT, qp ? 1 : (ps ? 2 : 0)))
+    return rc;
   PURIN_HIP(hipGetLastError());
   if (o.timing) {
     PURIN_HIP(hipEventRecord(e1, st));
@@ -459,9 +483,12 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   // or, for the diagonal QP with the plan's own coefficients (one shared
   // copy), per-sample steps it advances itself
   const bool res_qp = qp && !qp->dense && ps && ps->RVs && !o.shared_bounds;
-  if (lds && !o.streaming && !p->diag && ((!ps && !qp) || res_qp)) {
+  // per-sample coefficients (fixed iterations): each tile streams its own
+  const bool res_vals = !qp && ps && !ps->RVs && !early;
+  if (lds && !o.streaming && !p->diag && ((!ps && !qp) || res_qp || res_vals)) {
     if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds, early, batch, tol_scalar, tolv, done,
-                                 count, noalloc, res_qp ? qp : nullptr, res_qp ? ps : nullptr))
+                                 count, noalloc, res_qp ? qp : nullptr,
+                                 (res_qp || res_vals) ? ps : nullptr))
       return rc;
     if (!early) {
       const int32_t cnt = (int32_t)o.max_iterations;

@@ -17,6 +17,7 @@ struct Layout {
   size_t YB, MF, DF, SL, colpart, rowpart, decpart, done, count, ndone, ores, ogap, ofin, X, Z;
   size_t RTs, RRs, RD0, RLs, RHs;  // resident path (slot-ordered inputs)
   size_t RQs, RY0;                 // resident diagonal QP: q and y0 in slot order
+  size_t RCS;                      // resident per-sample coefficients: the tiles' coefficient streams
   // per-sample coefficients (values given per call): entry values in the
   // caller's order (VF), the kept CSR / CSC entries original (RVo, CVo) and
   // row-scaled (RV, CV), bound-row coefficients (BC), row scales (SC), steps

@@ -763,9 +763,16 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
       // chunk = 64 lanes x 4 entries: u32 LDS byte addresses, then the coefficients
       const size_t CB = 64 * 16 + 64 * 4 * sizeof(T);
       std::vector<unsigned char> stream;
+      // per stream entry, [chunk][lane][4]: the kept CSR entry it takes its
+      // coefficient from (row sections), the kept CSC entry | kResSrcCol
+      // (column sections), or -1 (padding): the map that lays per-sample
+      // coefficients out in stream order
+      std::vector<int32_t> srcmap;
       std::vector<int32_t> wtab((size_t)kResWtab * 16, 0);
       int64_t nchunks = 0;
-      auto put_chunk = [&](const uint32_t* off, const T* val) {  // off, val: [64][4]
+      auto put_chunk = [&](const uint32_t* off, const T* val,
+                           const int32_t* src) {  // off, val, src: [64][4]
+        srcmap.insert(srcmap.end(), src, src + 64 * 4);
         const size_t at = stream.size();
         stream.resize(at + CB);
         std::memcpy(&stream[at], off, 64 * 16);
@@ -814,6 +821,8 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         }
         std::vector<uint32_t> off((size_t)64 * E, zero_off);
         std::vector<T> v((size_t)64 * E, T(0));
+        std::vector<int32_t> src((size_t)64 * E, -1);
+        const int32_t colflag = gather_base == 0 ? 0 : kResSrcCol;  // column sections gather rows
         const int32_t zcls = (int32_t)(n & 15);
         for (int64_t s2 = 0; s2 < slots; ++s2) {
           const int32_t Wd = W[s2];
@@ -840,19 +849,22 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
                 off[(size_t)lane * E + at[s2] + st2] =
                     16u * (uint32_t)ent[gather_base + idx[ptr[r] + k]];
                 v[(size_t)lane * E + at[s2] + st2] = val[ptr[r] + k];
+                src[(size_t)lane * E + at[s2] + st2] = (ptr[r] + k) | colflag;
               }
             }
           }
         }
         uint32_t co[64 * 4];
         T cv[64 * 4];
+        int32_t cs[64 * 4];
         for (int64_t ch = 0; ch < nch; ++ch) {
           for (int l = 0; l < 64; ++l)
             for (int u = 0; u < 4; ++u) {
               co[4 * l + u] = off[(size_t)l * E + 4 * ch + u];
               cv[4 * l + u] = v[(size_t)l * E + 4 * ch + u];
+              cs[4 * l + u] = src[(size_t)l * E + 4 * ch + u];
             }
-          put_chunk(co, cv);
+          put_chunk(co, cv, cs);
         }
         return nch;
       };
@@ -886,15 +898,21 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
           const size_t at = stream.size();
           stream.resize(at + CB);
           std::memcpy(&stream[at], &stream[(size_t)first * CB], CB);
+          const size_t sat = srcmap.size();
+          srcmap.resize(sat + 64 * 4);
+          std::copy(srcmap.begin() + (size_t)first * 256, srcmap.begin() + (size_t)first * 256 + 256,
+                    srcmap.begin() + sat);
           ++nchunks;
         } else {
           uint32_t off[64 * 4];
           T v[64 * 4];
+          int32_t src[64 * 4];
           for (int e = 0; e < 64 * 4; ++e) {
             off[e] = zero_off;
             v[e] = T(0);
+            src[e] = -1;
           }
-          put_chunk(off, v);
+          put_chunk(off, v, src);
         }
         wt[0] = (int32_t)first;
         wt[5] = (int32_t)rch;
@@ -938,6 +956,7 @@ static int build(purin_cp_plan* p, const int64_t* indptr, const int32_t* indices
         UPR(p->res_rowent, rent);
         UPR(p->res_colent, cent);
         UPR(p->res_stream, stream);
+        UPR(p->res_srcmap, srcmap);
         UPR(p->res_wtab, wtab);
 #undef UPR
       }

@@ -18,6 +18,7 @@ constexpr int kSavedHeader = 256;     // bytes of the saved-state header
 constexpr int64_t kSavedMagic = 0x5055524e43503031LL;  // "PURNCP01"
 constexpr int kResThreads = 1024;   // threads of a resident workgroup
 constexpr int kResMaxSlots = 4;     // rows / columns per thread (n, m <= 4096)
+constexpr int32_t kResSrcCol = 1 << 30;  // stream-entry map: a column section's (CSC) entry
 constexpr double kMallBytes = 256.0 * 1024 * 1024;  // MI355X Infinity Cache (MALL)
 constexpr double kL2Bytes = 4.0 * 1024 * 1024;      // L2 of one MI355X XCD
 constexpr int kPinnedBytes = 4096;  // host-pinned flag words of one call: counters, per-step counts
@@ -93,6 +94,7 @@ struct purin_cp_plan {
   int32_t* res_rowent = nullptr;     // Kr: LDS entry (16-byte units) of each row slot's d, or -1
   int32_t* res_colent = nullptr;     // Kc: LDS entry of each column slot's ybar / y, or -1
   unsigned char* res_stream = nullptr;  // per-wavefront chunk streams of the matrix
+  int32_t* res_srcmap = nullptr;     // per stream entry: kept CSR / CSC (| kResSrcCol) entry, or -1
   int32_t* res_wtab = nullptr;       // [16][kResWtab] first chunk, slot widths, section chunks, flags
   int64_t res_stream_bytes = 0;
   int64_t res_iter_bytes = 0;        // matrix-stream bytes a workgroup reads per iteration

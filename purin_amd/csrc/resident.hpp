@@ -35,6 +35,8 @@
 // k_resident_early (below) adds the per-sample stop test.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace purin {
@@ -132,12 +134,23 @@ struct Res {
   const T* __restrict__ Y0s;
   const T* __restrict__ step0;
   const T* __restrict__ gam;
+  int accel;  // per-sample steps (QP, per-sample coefficients): the accelerated update runs
+  // per-sample coefficients (k_resident with VALS): each tile's coefficient
+  // stream, [tiles][cs_tile] vectors of the tile's samples ([chunk][4][64] per
+  // tile, the plan's stream order); the steps are per sample as for the QP,
+  // with gamma 1 and the prox a, delta of q = 1 from step0's rows 2 and 3
+  const T* __restrict__ Cs;
+  int64_t cs_tile;
 };
 
-template <typename T>
+// One chunk of a wavefront's stream in registers: the lane's 4 LDS addresses
+// and coefficients, shared by the tile's samples (CV = T), or per sample (CV =
+// the tile's vector type, from the per-tile coefficient stream of per-sample
+// coefficients).
+template <typename T, typename CV = T>
 struct Chunk {
   uint32_t o[kResChunk];
-  T v[kResChunk];
+  CV v[kResChunk];
 };
 
 // LDS accesses by absolute byte address: the kernel declares no static LDS, so
@@ -180,9 +193,12 @@ __device__ __forceinline__ void ent_write(uint32_t addr, V v) {
 
 // The chunk at byte ``cbyte`` of the stream; the base is made wave-uniform
 // explicitly so the loads take an SGPR base plus the lane's 16-byte offset.
-template <typename T>
-__device__ __forceinline__ void load_chunk(Chunk<T>& c, const unsigned char* __restrict__ stream,
-                                           uint64_t cbyte, uint32_t lane16) {
+// Per-sample coefficients (CV a vector): the offsets from the stream, the
+// coefficients from ``cs``, the tile's coefficient stream, [chunk][4][64] CV.
+template <typename T, typename CV = T>
+__device__ __forceinline__ void load_chunk(Chunk<T, CV>& c, const unsigned char* __restrict__ stream,
+                                           uint64_t cbyte, uint32_t lane16,
+                                           const CV* __restrict__ cs = nullptr) {
   const uint64_t a = (uint64_t)(uintptr_t)stream + cbyte;
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
@@ -195,7 +211,13 @@ __device__ __forceinline__ void load_chunk(Chunk<T>& c, const unsigned char* __r
   c.o[1] = o.y;
   c.o[2] = o.z;
   c.o[3] = o.w;
-  if constexpr (sizeof(T) == 8) {
+  if constexpr (!std::is_same<CV, T>::value) {
+    const uint64_t k = cbyte / res_chunk_bytes<T>();  // the chunk's index in the stream
+    typedef const __attribute__((address_space(1))) CV* CVP;
+    const CVP cp = (CVP)cs + (size_t)k * (4 * 64) + (lane16 >> 4);
+#pragma unroll
+    for (int u = 0; u < kResChunk; ++u) c.v[u] = cp[u * 64];
+  } else if constexpr (sizeof(T) == 8) {
     typedef double D2 __attribute__((ext_vector_type(2)));
     typedef const __attribute__((address_space(1))) D2* D2P;
     const D2 x = *reinterpret_cast<D2P>(base + 1024u + lane16);
@@ -216,8 +238,8 @@ __device__ __forceinline__ void load_chunk(Chunk<T>& c, const unsigned char* __r
 }
 
 // acc += sum over the chunk's 4 entries of coefficient * gathered element, in order
-template <typename T, typename V>
-__device__ __forceinline__ void consume_chunk(const Chunk<T>& c, V& acc) {
+template <typename T, typename V, typename CV>
+__device__ __forceinline__ void consume_chunk(const Chunk<T, CV>& c, V& acc) {
   V x[kResChunk];
 #pragma unroll
   for (int u = 0; u < kResChunk; ++u) x[u] = ent_read<V>(c.o[u]);
@@ -227,8 +249,8 @@ __device__ __forceinline__ void consume_chunk(const Chunk<T>& c, V& acc) {
 
 // Entries [0, e) of the chunk to acc and entries [e, 4) to carry, in order:
 // the chunk's last entries open the next slot (e is wave-uniform).
-template <typename T, typename V>
-__device__ __forceinline__ void consume_split(const Chunk<T>& c, int e, V& acc, V& carry) {
+template <typename T, typename V, typename CV>
+__device__ __forceinline__ void consume_split(const Chunk<T, CV>& c, int e, V& acc, V& carry) {
   V x[kResChunk];
 #pragma unroll
   for (int u = 0; u < kResChunk; ++u) x[u] = ent_read<V>(c.o[u]);
@@ -256,8 +278,8 @@ __device__ __forceinline__ void consume_split(const Chunk<T>& c, int e, V& acc, 
 }
 
 // A slot's last chunk: its own, or shared with the next slot (e < 4).
-template <typename T, typename V>
-__device__ __forceinline__ void consume_last(const Chunk<T>& c, int e, V& acc, V& carry) {
+template <typename T, typename V, typename CV>
+__device__ __forceinline__ void consume_last(const Chunk<T, CV>& c, int e, V& acc, V& carry) {
   if (e == kResChunk) {
     asm volatile("");
     consume_chunk(c, acc);
@@ -286,10 +308,11 @@ __device__ __forceinline__ void consume_last(const Chunk<T>& c, int e, V& acc, V
 // two chunks are taken before the loop.  Summation order: the slot's entries
 // in stream order, its head first.  SPLIT false: the pass has one slot, which
 // owns every chunk it walks (no head, no split).
-template <typename T, typename V, bool SPLIT>
-__device__ __forceinline__ V slot_sum(int nch, int e, V& carry, Chunk<T>& b0, Chunk<T>& b1,
-                                      uint32_t& pos, const unsigned char* __restrict__ stream,
-                                      uint32_t lane16, bool pro) {
+template <typename T, typename V, bool SPLIT, typename CV = T>
+__device__ __forceinline__ V slot_sum(int nch, int e, V& carry, Chunk<T, CV>& b0,
+                                      Chunk<T, CV>& b1, uint32_t& pos,
+                                      const unsigned char* __restrict__ stream, uint32_t lane16,
+                                      bool pro, const CV* __restrict__ cs = nullptr) {
   constexpr uint64_t CB = res_chunk_bytes<T>();
   if constexpr (!SPLIT) {
     // one slot per pass: it owns all its chunks (the pass's end is padded)
@@ -297,25 +320,25 @@ __device__ __forceinline__ V slot_sum(int nch, int e, V& carry, Chunk<T>& b0, Ch
     int k = 0;
     if (pro) {  // nch >= 2
       consume_chunk(b0, acc);
-      load_chunk(b0, stream, pos * CB, lane16);
+      load_chunk(b0, stream, pos * CB, lane16, cs);
       ++pos;
       __builtin_amdgcn_sched_barrier(0);
       consume_chunk(b1, acc);
       k = 2;
     }
     for (; k + 1 < nch; k += 2) {
-      load_chunk(b1, stream, pos * CB, lane16);
+      load_chunk(b1, stream, pos * CB, lane16, cs);
       ++pos;
       __builtin_amdgcn_sched_barrier(0);
       consume_chunk(b0, acc);
-      load_chunk(b0, stream, pos * CB, lane16);
+      load_chunk(b0, stream, pos * CB, lane16, cs);
       ++pos;
       __builtin_amdgcn_sched_barrier(0);
       consume_chunk(b1, acc);
     }
     if (k < nch) {
       consume_chunk(b0, acc);
-      load_chunk(b0, stream, pos * CB, lane16);
+      load_chunk(b0, stream, pos * CB, lane16, cs);
       ++pos;
     }
     return acc;
@@ -325,7 +348,7 @@ __device__ __forceinline__ V slot_sum(int nch, int e, V& carry, Chunk<T>& b0, Ch
   int k = 0;
   if (pro) {  // nch >= 2, no head (the pass's first slot)
     consume_chunk(b0, acc);
-    load_chunk(b0, stream, pos * CB, lane16);
+    load_chunk(b0, stream, pos * CB, lane16, cs);
     ++pos;
     __builtin_amdgcn_sched_barrier(0);
     if (nch == 2) {
@@ -336,29 +359,29 @@ __device__ __forceinline__ V slot_sum(int nch, int e, V& carry, Chunk<T>& b0, Ch
     k = 2;
   }
   for (; k + 2 < nch; k += 2) {
-    load_chunk(b1, stream, pos * CB, lane16);
+    load_chunk(b1, stream, pos * CB, lane16, cs);
     ++pos;
     // keep the load ahead of the consumption it overlaps (the scheduler would
     // otherwise sink it, leaving one chunk in flight)
     __builtin_amdgcn_sched_barrier(0);
     consume_chunk(b0, acc);
-    load_chunk(b0, stream, pos * CB, lane16);
+    load_chunk(b0, stream, pos * CB, lane16, cs);
     ++pos;
     __builtin_amdgcn_sched_barrier(0);
     consume_chunk(b1, acc);
   }
   if (k + 1 < nch) {
-    load_chunk(b1, stream, pos * CB, lane16);
+    load_chunk(b1, stream, pos * CB, lane16, cs);
     ++pos;
     __builtin_amdgcn_sched_barrier(0);
     consume_chunk(b0, acc);
-    load_chunk(b0, stream, pos * CB, lane16);
+    load_chunk(b0, stream, pos * CB, lane16, cs);
     ++pos;
     __builtin_amdgcn_sched_barrier(0);
     consume_last(b1, e, acc, carry);
   } else if (k < nch) {
     consume_last(b0, e, acc, carry);
-    load_chunk(b0, stream, pos * CB, lane16);
+    load_chunk(b0, stream, pos * CB, lane16, cs);
     ++pos;
   }
   return acc;
@@ -398,19 +421,24 @@ __device__ __forceinline__ T res_uniform(T x) {
 // same in every thread and stay in SGPRs.
 template <typename T, int BT>
 __device__ __forceinline__ void res_qp_schedule(const T (&gam)[BT], T (&tau)[BT], T (&sig)[BT],
-                                                T (&th)[BT]) {
+                                                T (&th)[BT], T (&pa)[BT], T (&pd)[BT]) {
 #pragma clang fp contract(off)
   const T one = T(1);
 #pragma unroll
   for (int s = 0; s < BT; ++s) {
     const T nu = one / (T)__builtin_sqrt(one + gam[s] * tau[s]);
-    tau[s] = res_uniform(nu * tau[s]);
+    const T nt = nu * tau[s];
+    const T a = one / (one + nt);  // the prox of q = 1 (per-sample coefficients)
+    tau[s] = res_uniform(nt);
     sig[s] = res_uniform(sig[s] / nu);
     th[s] = res_uniform(nu);
+    pa[s] = res_uniform(a);
+    pd[s] = res_uniform(nt * a);
   }
 }
 
-template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT, bool QP = false>
+template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT, bool QP = false,
+          bool VALS = false>
 __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   constexpr int NT = 1024;
   constexpr int BT = NB;
@@ -445,20 +473,28 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   // row and four column slots and per-sample bounds, which would spill them
   constexpr bool kHoldTarget = SB || SLR + SLC < 8;
   V y[SLC], tg[kHoldTarget ? SLC : 1], rr[SLR];
-  // QP: q of the thread's columns, and the tile's per-sample steps (the same
-  // in every thread): tau, sigma, theta of the current iteration, gamma
+  // QP: q of the thread's columns.  QP and per-sample coefficients (VALS):
+  // the tile's per-sample steps (the same in every thread): tau, sigma,
+  // theta, the prox a, delta of q = 1 (VALS) of the current iteration, gamma
+  constexpr bool kPS = QP || VALS;
   V qh[QP ? SLC : 1];
-  T tau_s[BT], sig_s[BT], th_s[BT], gam_s[BT];
-  if constexpr (QP) {
+  T tau_s[BT], sig_s[BT], th_s[BT], gam_s[BT], pa_s[BT], pd_s[BT];
+  if constexpr (kPS) {
     const int64_t bq = tile * BT;
 #pragma unroll
     for (int s = 0; s < BT; ++s) {
       tau_s[s] = res_uniform(A.step0[bq + s]);
       sig_s[s] = res_uniform(A.step0[A.Bp + bq + s]);
-      th_s[s] = res_uniform(A.gam ? A.step0[4 * A.Bp + bq + s] : T(1));
-      gam_s[s] = res_uniform(A.gam ? A.gam[bq + s] : T(0));
+      pa_s[s] = res_uniform(A.step0[2 * A.Bp + bq + s]);
+      pd_s[s] = res_uniform(A.step0[3 * A.Bp + bq + s]);
+      th_s[s] = res_uniform(A.accel ? A.step0[4 * A.Bp + bq + s] : T(1));
+      gam_s[s] = res_uniform(A.gam ? A.gam[bq + s] : T(1));
     }
   }
+  // per-sample coefficients: this tile's coefficient stream
+  using CV = typename std::conditional<VALS, V, T>::type;
+  const CV* cs = nullptr;
+  if constexpr (VALS) cs = reinterpret_cast<const CV*>(A.Cs) + tile * A.cs_tile;
   uint32_t ineq = 0, nanb = 0;
   // shared bounds equal on every column of a wavefront's slots (box bounds,
   // e.g. [-1, 1]): its column pass then takes them from registers instead of
@@ -515,14 +551,14 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   __syncthreads();
 
   constexpr uint32_t CB = res_chunk_bytes<T>();
-  Chunk<T> b0, b1;
-  load_chunk(b0, A.stream, (uint64_t)first * CB, lane16);
-  if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16);
+  Chunk<T, CV> b0, b1;
+  load_chunk(b0, A.stream, (uint64_t)first * CB, lane16, cs);
+  if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16, cs);
 
   for (int64_t it = 0; it < A.iters; ++it) {
     // wave-uniform schedule scalars: scalar loads through the constant address space
     T sigma = T(0), a = T(0), delta = T(0), theta = T(0);
-    if constexpr (!QP) {  // QP: the per-sample steps in registers instead
+    if constexpr (!kPS) {  // QP, VALS: the per-sample steps in registers instead
       const __attribute__((address_space(4))) T* sc =
           (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
       sigma = sc[0];
@@ -540,11 +576,11 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
       const V dold = ent_read<V>(soff_r[r]);
-      const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
-                                              b0, b1, pos, A.stream, lane16,
-                                              r == 0 && (pro & 1u));
+      const V acc = slot_sum<T, V, (SLR > 1), CV>(slot_field(rc, r), slot_field(rl, r), carry,
+                                                  b0, b1, pos, A.stream, lane16,
+                                                  r == 0 && (pro & 1u), cs);
       V p;
-      if constexpr (QP) {
+      if constexpr (kPS) {
         const V e = acc - rr[r];
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = dold[s] + sig_s[s] * e[s];
@@ -558,7 +594,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       ent_write<V>(soff_r[r], p);
     }
     if (pro & 2u) {  // the column pass's second chunk (its first is in b0)
-      load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16);
+      load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16, cs);
       ++pos;
     }
     __syncthreads();
@@ -594,9 +630,9 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
         asm volatile("" : "+s"(tb));
         tgc = tb[tile * (int64_t)A.Kc + c * NT + t];
       }
-      const V tt = slot_sum<T, V, (SLC > 1)>(slot_field(cc, c), slot_field(cl, c), carry,
-                                             b0, b1, pos, A.stream, lane16,
-                                             c == 0 && (pro & 2u));
+      const V tt = slot_sum<T, V, (SLC > 1), CV>(slot_field(cc, c), slot_field(cl, c), carry,
+                                                 b0, b1, pos, A.stream, lane16,
+                                                 c == 0 && (pro & 2u), cs);
       V sv;
       if constexpr (QP) {  // the general-q prox (kernels.py:68-73), as the streaming pass forms it
 #pragma unroll
@@ -606,6 +642,9 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
           const T oj = -dj * tgc[s];
           sv[s] = aj * y[c][s] - dj * tt[s] + oj;
         }
+      } else if constexpr (VALS) {  // per-sample a, delta of q = 1
+#pragma unroll
+        for (int s = 0; s < BT; ++s) sv[s] = pa_s[s] * y[c][s] - pd_s[s] * tt[s] + pd_s[s] * tgc[s];
       } else {
         sv = a * y[c] - delta * tt + delta * tgc;
       }
@@ -617,7 +656,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 #pragma unroll
         for (int s = 0; s < BT; ++s) yn[s] = clip_nonnan_bounds(sv[s], lo[s], hi[s]);
       }
-      if constexpr (QP) {
+      if constexpr (kPS) {
         V yb;
 #pragma unroll
         for (int s = 0; s < BT; ++s) yb[s] = yn[s] + th_s[s] * (yn[s] - y[c][s]);
@@ -626,11 +665,11 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
         ent_write<V>(soff_c[c], yn + theta * (yn - y[c]));
       y[c] = yn;
     }
-    if constexpr (QP) {
-      if (A.gam) res_qp_schedule<T, BT>(gam_s, tau_s, sig_s, th_s);
+    if constexpr (kPS) {
+      if (A.accel) res_qp_schedule<T, BT>(gam_s, tau_s, sig_s, th_s, pa_s, pd_s);
     }
     // the next row pass's second chunk (b0 holds the copy of its first)
-    if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16);
+    if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16, cs);
     __syncthreads();
   }
   // ---- hand the state to the batch-minor layout ---------------------------------
@@ -813,15 +852,16 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   // QP (as in k_resident): q of the thread's columns (Ts holds c), and the
   // tile's per-sample steps in SGPRs
   V qh[QP ? SLC : 1];
-  T tau_s[BT], sig_s[BT], th_s[BT], gam_s[BT];
+  T tau_s[BT], sig_s[BT], th_s[BT], gam_s[BT], pa_s[BT], pd_s[BT];
   if constexpr (QP) {
 #pragma unroll
     for (int s = 0; s < BT; ++s) {
       const int64_t b = tile * BT + s;
       tau_s[s] = res_uniform(A.step0[b]);
       sig_s[s] = res_uniform(A.step0[A.Bp + b]);
-      th_s[s] = res_uniform(A.gam ? A.step0[4 * A.Bp + b] : T(1));
-      gam_s[s] = res_uniform(A.gam ? A.gam[b] : T(0));
+      pa_s[s] = pd_s[s] = T(0);
+      th_s[s] = res_uniform(A.accel ? A.step0[4 * A.Bp + b] : T(1));
+      gam_s[s] = res_uniform(A.gam ? A.gam[b] : T(1));
     }
   }
   typedef const __attribute__((address_space(1))) V* GV;
@@ -1071,7 +1111,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     if constexpr (QP) {
 #pragma unroll
       for (int s = 0; s < BT; ++s) thq[s] = th_s[s];
-      if (A.gam) res_qp_schedule<T, BT>(gam_s, tau_s, sig_s, th_s);
+      if (A.accel) res_qp_schedule<T, BT>(gam_s, tau_s, sig_s, th_s, pa_s, pd_s);
     }
     // the slot-ordered rhs when not held: through an opaque base, so the loads
     // stay inside the loop
@@ -1223,6 +1263,36 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       A.count[bs0 + s] = cnt[s];
       A.done[bs0 + s] = (bs0 + s < A.batch && !(act & (1u << s))) ? 1 : 0;
     }
+  }
+}
+
+// Per-sample coefficients in the plan's stream order: out[tile][k][u][lane]
+// (BT values, the tile's samples) = the coefficient of stream entry (chunk k,
+// lane, entry u): RV (kept CSR, [nnz][Bp]) for row sections, CV (kept CSC)
+// for column sections, 0 for padding (srcmap: the plan's map, [chunk][lane][4]).
+// One thread per (stream entry, tile), tiles fastest (the reads of one entry
+// run along the batch).
+template <typename T, int BT>
+__global__ __launch_bounds__(256) void k_res_coef_stream(const int32_t* __restrict__ srcmap,
+                                                         int64_t entries,
+                                                         const T* __restrict__ RV,
+                                                         const T* __restrict__ CV, int64_t Bp,
+                                                         int64_t tiles, T* __restrict__ out) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= entries * tiles) return;
+  const int64_t tile = gid % tiles, e = gid / tiles;
+  const int64_t k = e >> 8;
+  const int lane = (int)((e >> 2) & 63), u = (int)(e & 3);
+  const int32_t src = srcmap[e];
+  const int64_t o = (((tile * (entries >> 8) + k) * 4 + u) * 64 + lane) * BT;
+  const int64_t b = tile * BT;
+#pragma unroll
+  for (int s = 0; s < BT; ++s) {
+    T v = T(0);
+    if (src >= 0)
+      v = (src & kResSrcCol) ? CV[(int64_t)(src & ~kResSrcCol) * Bp + b + s]
+                             : RV[(int64_t)src * Bp + b + s];
+    out[o + s] = v;
   }
 }
 

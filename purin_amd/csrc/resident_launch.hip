@@ -14,13 +14,17 @@
 
 namespace purin {
 
+// kind: 0 the projection, 1 the diagonal QP (per-sample bounds), 2
+// per-sample coefficients (fixed iterations)
 template <typename T, int SLR, int SLC, int NB>
 static int launch_nb(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
-                     bool early, bool qp) {
-  // the diagonal QP takes per-sample bounds
-  if (qp && sb) return set_error(PURIN_CP_ERR_ARG, "resident QP variant out of range");
-  auto kern = qp ? (early ? k_resident_early<T, SLR, SLC, false, NB, true>
-                          : k_resident<T, SLR, SLC, false, NB, true>)
+                     bool early, int kind) {
+  if ((kind == 1 && sb) || (kind == 2 && early) || kind < 0 || kind > 2)
+    return set_error(PURIN_CP_ERR_ARG, "resident kernel variant out of range");
+  auto kern = kind == 1 ? (early ? k_resident_early<T, SLR, SLC, false, NB, true>
+                                 : k_resident<T, SLR, SLC, false, NB, true>)
+              : kind == 2 ? (sb ? k_resident<T, SLR, SLC, true, NB, false, true>
+                                : k_resident<T, SLR, SLC, false, NB, false, true>)
               : early ? (sb ? k_resident_early<T, SLR, SLC, true, NB>
                             : k_resident_early<T, SLR, SLC, false, NB>)
                       : (sb ? k_resident<T, SLR, SLC, true, NB>
@@ -34,30 +38,30 @@ static int launch_nb(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds,
 // one column slot per thread (two LDS planes)
 template <typename T, int SLR, int SLC>
 static int launch_one(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
-                      bool early, int nb, bool qp) {
+                      bool early, int nb, int kind) {
   constexpr int NB = sizeof(T) == 4 && SLR == 1 && SLC == 1 ? 8 : ResVec<T>::BT;
   if (nb != NB) return set_error(PURIN_CP_ERR_ARG, "resident tile size out of range");
-  return launch_nb<T, SLR, SLC, NB>(R, st, tiles, lds, sb, early, qp);
+  return launch_nb<T, SLR, SLC, NB>(R, st, tiles, lds, sb, early, kind);
 }
 
 template <typename T, int SLR>
 int launch_resident_rows(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
-                         bool sb, bool early, int nb, bool qp) {
+                         bool sb, bool early, int nb, int kind) {
   switch (slc) {
-    case 1: return launch_one<T, SLR, 1>(R, st, tiles, lds, sb, early, nb, qp);
-    case 2: return launch_one<T, SLR, 2>(R, st, tiles, lds, sb, early, nb, qp);
-    case 3: return launch_one<T, SLR, 3>(R, st, tiles, lds, sb, early, nb, qp);
-    case 4: return launch_one<T, SLR, 4>(R, st, tiles, lds, sb, early, nb, qp);
+    case 1: return launch_one<T, SLR, 1>(R, st, tiles, lds, sb, early, nb, kind);
+    case 2: return launch_one<T, SLR, 2>(R, st, tiles, lds, sb, early, nb, kind);
+    case 3: return launch_one<T, SLR, 3>(R, st, tiles, lds, sb, early, nb, kind);
+    case 4: return launch_one<T, SLR, 4>(R, st, tiles, lds, sb, early, nb, kind);
     default: return set_error(PURIN_CP_ERR_ARG, "resident column slot count out of range");
   }
 }
 
 #if PURIN_RES_F64
 template int launch_resident_rows<double, PURIN_RES_SLR>(const Res<double>&, hipStream_t, int64_t,
-                                                         size_t, int, bool, bool, int, bool);
+                                                         size_t, int, bool, bool, int, int);
 #else
 template int launch_resident_rows<float, PURIN_RES_SLR>(const Res<float>&, hipStream_t, int64_t,
-                                                        size_t, int, bool, bool, int, bool);
+                                                        size_t, int, bool, bool, int, int);
 #endif
 
 }  // namespace purin

@@ -83,6 +83,49 @@ def test_values_project_matches_oracle(dtype, early_stop, accelerated):
 
 
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_values_resident_matches_streaming_and_oracle(dtype, accelerated):
+    """Fixed iterations with per-sample coefficients on the resident kernel:
+    the iterate stays on chip and each tile streams its samples' scaled
+    coefficients in the plan's stream order, with per-sample steps advanced in
+    the kernel (kernels.py:209-227, 279-283).  Against the streaming passes on
+    the whole batch and the oracle on two samples, for every slot count of the
+    resident schedule (1, 2, 4 and 8 per thread)."""
+    require_gpu()
+    for k, (n, me, mi, width, B) in enumerate(((48, 8, 20, 4, 37), (700, 100, 300, 5, 40),
+                                               (1500, 300, 700, 6, 24),
+                                               (4096, 1024, 2048, 8, 12))):
+        w = workloads.small_random(60 + k, n=n, me=me, mi=mi, width=width, batch=B,
+                                   accelerated=accelerated)
+        canon, values, rhs, mask = _per_sample(w, B, 70 + k)
+        target = w.target.astype(dtype)
+        rhs = rhs.astype(dtype)
+        vals = _csr(values, mask).astype(dtype)
+        plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
+        iters = 200
+        kw = dict(values=vals, max_iterations=iters, early_stop=False, timing=True)
+        print(f"values resident n={n} {np.dtype(dtype).name} accelerated={accelerated}",
+              flush=True)
+        res = plan.project(target, rhs, **kw)
+        assert plan.last_timing()["resident"] == 1, n
+        st = plan.project(target, rhs, streaming=True, **kw)
+        assert plan.last_timing()["resident"] == 0, n
+        bar = TOL[dtype]
+        assert rel_err(to_np(res.y), to_np(st.y)) <= bar, n
+        assert rel_err(to_np(res.multipliers), to_np(st.multipliers)) <= bar, n
+        assert rel_err(to_np(res.slacks), to_np(st.slacks)) <= bar, n
+        np.testing.assert_array_equal(to_np(res.status), to_np(st.status))
+        sub = slice(0, 2)
+        cfg = op.Config(accelerated=accelerated, max_iterations=iters, early_stop=False)
+        want = op.solve(canon, target[sub], rhs[sub], cfg, dtype=dtype,
+                        values=values[sub].astype(dtype))
+        assert rel_err(to_np(res.y)[sub], want.y) <= bar, n
+        want_mult = np.concatenate([want.multipliers_eq, want.multipliers_ineq], axis=1)
+        assert rel_err(to_np(res.multipliers)[sub], want_mult) <= bar, n
+        np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
 @pytest.mark.parametrize("mode", ["diagonal", "power"])
 def test_values_steps_variants_match_oracle(dtype, mode):
     """Per-sample diagonal steps (kernels.py:76-88) and the per-sample
