@@ -483,8 +483,8 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   // or, for the diagonal QP with the plan's own coefficients (one shared
   // copy), per-sample steps it advances itself
   const bool res_qp = qp && !qp->dense && ps && ps->RVs && !o.shared_bounds;
-  // per-sample coefficients (fixed iterations): each tile streams its own
-  const bool res_vals = !qp && ps && !ps->RVs && !early;
+  // per-sample coefficients: each tile streams its own
+  const bool res_vals = !qp && ps && !ps->RVs;
   if (lds && !o.streaming && !p->diag && ((!ps && !qp) || res_qp || res_vals)) {
     if (int rc = run_resident<T>(p, st, L, sv, ws, o, lds, early, batch, tol_scalar, tolv, done,
                                  count, noalloc, res_qp ? qp : nullptr,

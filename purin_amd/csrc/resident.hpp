@@ -799,7 +799,8 @@ __device__ __forceinline__ T read_lane(T v, int l) {
   }
 }
 
-template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT, bool QP = false>
+template <typename T, int SLR, int SLC, bool SB, int NB = ResVec<T>::BT, bool QP = false,
+          bool VALS = false>
 __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   constexpr int NT = 1024;
   constexpr int BT = NB;
@@ -849,21 +850,27 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   constexpr bool kHold = SLR <= 3;
   uint32_t soff_r[SLR], soff_c[SLC];
   V ky[SLR], dk[SLR], tgh[kHold ? SLC : 1], rrh[kHold ? SLR : 1];
-  // QP (as in k_resident): q of the thread's columns (Ts holds c), and the
-  // tile's per-sample steps in SGPRs
+  // QP (as in k_resident): q of the thread's columns (Ts holds c).  QP and
+  // per-sample coefficients (VALS): the tile's per-sample steps in SGPRs
+  constexpr bool kPS = QP || VALS;
   V qh[QP ? SLC : 1];
   T tau_s[BT], sig_s[BT], th_s[BT], gam_s[BT], pa_s[BT], pd_s[BT];
-  if constexpr (QP) {
+  if constexpr (kPS) {
 #pragma unroll
     for (int s = 0; s < BT; ++s) {
       const int64_t b = tile * BT + s;
       tau_s[s] = res_uniform(A.step0[b]);
       sig_s[s] = res_uniform(A.step0[A.Bp + b]);
-      pa_s[s] = pd_s[s] = T(0);
+      pa_s[s] = res_uniform(A.step0[2 * A.Bp + b]);
+      pd_s[s] = res_uniform(A.step0[3 * A.Bp + b]);
       th_s[s] = res_uniform(A.accel ? A.step0[4 * A.Bp + b] : T(1));
       gam_s[s] = res_uniform(A.gam ? A.gam[b] : T(1));
     }
   }
+  // per-sample coefficients: this tile's coefficient stream
+  using CV = typename std::conditional<VALS, V, T>::type;
+  const CV* cs = nullptr;
+  if constexpr (VALS) cs = reinterpret_cast<const CV*>(A.Cs) + tile * A.cs_tile;
   typedef const __attribute__((address_space(1))) V* GV;
   uint32_t ineq = 0, nanb = 0, rvalid = 0, cvalid = 0;
   // shared bounds equal on every column of the wavefront's slots: taken from
@@ -933,27 +940,28 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   __syncthreads();
 
   constexpr uint32_t CB = res_chunk_bytes<T>();
-  Chunk<T> b0, b1;
-  load_chunk(b0, A.stream, (uint64_t)first * CB, lane16);
-  if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16);
+  Chunk<T, CV> b0, b1;
+  load_chunk(b0, A.stream, (uint64_t)first * CB, lane16, cs);
+  if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16, cs);
   uint32_t pos = first + 1 + (pro & 1u);
   // K y0 (= K ybar0) by one row sweep, and the first candidate duals; b0 then
   // holds the first column chunk
   {
-    const T sigma0 = QP ? T(0) : A.sched[0];
+    const T sigma0 = kPS ? T(0) : A.sched[0];
     V carry = vzero;  // the head of the next slot (a chunk shared by two slots)
     const uint32_t rc = rcnt, rl = rlast;
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
       const V rr = kHold ? rrh[kHold ? r : 0] : Rs[r * NT + t];
-      const V k0 = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
-                                             b0, b1, pos, A.stream, lane16, r == 0 && (pro & 1u));
+      const V k0 = slot_sum<T, V, (SLR > 1), CV>(slot_field(rc, r), slot_field(rl, r), carry,
+                                                 b0, b1, pos, A.stream, lane16,
+                                                 r == 0 && (pro & 1u), cs);
       if (r < KYL)
         ent_write<V>(kyl_off + (uint32_t)(r * NT + t) * 16u, k0);
       else
         ky[r] = k0;
       V p;
-      if constexpr (QP) {
+      if constexpr (kPS) {
         const V dd = ent_read<V>(soff_r[r]), e = k0 - rr;
 #pragma unroll
         for (int s = 0; s < BT; ++s) p[s] = dd[s] + sig_s[s] * e[s];
@@ -967,7 +975,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       ent_write<V>(soff_r[r], p);  // the first iteration's d+ (every sample active)
     }
     if (pro & 2u) {  // the column pass's second chunk (its first is in b0)
-      load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16);
+      load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16, cs);
       ++pos;
     }
   }
@@ -975,7 +983,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
 
   for (int64_t it = 0; it < A.iters && act != 0u; ++it) {
     T a = T(0), delta = T(0), theta = T(0);
-    if constexpr (!QP) {
+    if constexpr (!kPS) {
       const __attribute__((address_space(4))) T* sc =
           (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
       a = sc[1];
@@ -1002,8 +1010,9 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         asm volatile("" : "+s"(tb));
         tg = ((GV)tb)[tile * (int64_t)A.Kc + c * NT + t];
       }
-      const V tt = slot_sum<T, V, (SLC > 1)>(slot_field(cc, c), slot_field(cl, c), carry,
-                                             b0, b1, pos, A.stream, lane16, c == 0 && (pro & 2u));
+      const V tt = slot_sum<T, V, (SLC > 1), CV>(slot_field(cc, c), slot_field(cl, c), carry,
+                                                 b0, b1, pos, A.stream, lane16,
+                                                 c == 0 && (pro & 2u), cs);
       asm volatile("" : "+s"(lb), "+s"(hb));
       V lo, hi;
       if ((SB || QP) && uni) {
@@ -1026,6 +1035,9 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
           const T oj = -dj * tg[s];
           sv[s] = aj * yo[s] - dj * tt[s] + oj;
         }
+      } else if constexpr (VALS) {  // per-sample a, delta of q = 1
+#pragma unroll
+        for (int s = 0; s < BT; ++s) sv[s] = pa_s[s] * yo[s] - pd_s[s] * tt[s] + pd_s[s] * tg[s];
       } else {
         sv = a * yo - delta * tt + delta * tg;
       }
@@ -1098,17 +1110,18 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     // qd and qc stay in registers: the sweep folds its own terms into them
     // b0 holds the copy of the stream's first (row) chunk; its second chunk
     // goes into b1 before the barrier when the first row slot spans two
-    if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16);
+    if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16, cs);
     __syncthreads();
     // ---- residual sweep (gathers Gy = y+; own Gd entries = d+) ---------------------
     pos = first + 1 + (pro & 1u);
     // the next iteration's sigma (the candidates are formed only when it runs)
     const bool more = it + 1 < A.iters;
-    const T sigma_n = (more && !QP) ? A.sched[4 * (it + 1)] : zero;
+    const T sigma_n = (more && !kPS) ? A.sched[4 * (it + 1)] : zero;
     const T tp1 = T(1) + theta;
-    // QP: this iteration's theta (of K ybar), then the steps of the next one
+    // per-sample steps: this iteration's theta (of K ybar), then the steps of
+    // the next one
     T thq[BT];
-    if constexpr (QP) {
+    if constexpr (kPS) {
 #pragma unroll
       for (int s = 0; s < BT; ++s) thq[s] = th_s[s];
       if (A.accel) res_qp_schedule<T, BT>(gam_s, tau_s, sig_s, th_s, pa_s, pd_s);
@@ -1122,8 +1135,9 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
 #pragma unroll
     for (int r = 0; r < SLR; ++r) {
       const V rr = kHold ? rrh[kHold ? r : 0] : rb[r * NT + t];
-      const V acc = slot_sum<T, V, (SLR > 1)>(slot_field(rc, r), slot_field(rl, r), carry,
-                                              b0, b1, pos, A.stream, lane16, r == 0 && (pro & 1u));
+      const V acc = slot_sum<T, V, (SLR > 1), CV>(slot_field(rc, r), slot_field(rl, r), carry,
+                                                  b0, b1, pos, A.stream, lane16,
+                                                  r == 0 && (pro & 1u), cs);
       const V d = ent_read<V>(soff_r[r]);
       if (rvalid & (1u << r)) {  // kernels.py:158-166
         // e = K y+ - r; equality rows |e|, inequality rows max(e, 0): max(e, w e)
@@ -1144,7 +1158,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         // stays in dk until the decision: a sample accepted now gets it back.
         const V kyo = r < KYL ? ent_read<V>(kyl_off + (uint32_t)(r * NT + t) * 16u) : ky[r];
         V p;
-        if constexpr (QP) {
+        if constexpr (kPS) {
 #pragma unroll
           for (int s = 0; s < BT; ++s)
             p[s] = d[s] + sig_s[s] * (((T(1) + thq[s]) * acc[s] - thq[s] * kyo[s]) - rr[s]);
@@ -1169,7 +1183,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         ky[r] = acc;
     }
     if (pro & 2u) {  // the next column pass's second chunk (its first is in b0)
-      load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16);
+      load_chunk(b1, A.stream, (uint64_t)pos * CB, lane16, cs);
       ++pos;
     }
 #pragma unroll

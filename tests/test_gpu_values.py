@@ -17,7 +17,7 @@ import pytest
 from oracle import projection as op
 from purin_amd import workloads
 from tests._gpu import canonical_from_workload, plan_for, rel_err, require_gpu, to_np
-from tests._margins import Margins, check_counts
+from tests._margins import Margins, check_counts, check_iterates
 
 pytestmark = pytest.mark.gpu
 
@@ -123,6 +123,66 @@ def test_values_resident_matches_streaming_and_oracle(dtype, accelerated):
         want_mult = np.concatenate([want.multipliers_eq, want.multipliers_ineq], axis=1)
         assert rel_err(to_np(res.multipliers)[sub], want_mult) <= bar, n
         np.testing.assert_array_equal(to_np(res.status)[sub], want.status)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("accelerated", [False, True])
+def test_values_resident_early_stop(dtype, accelerated):
+    """BoundProjection.solve's default loop (early stop, freezing,
+    stationarity; kernels.py:238-290) with per-sample coefficients on the
+    resident early-stop kernel.  fp64 counts equal the streaming passes' and
+    the oracle's; fp32 counts follow the oracle under the rule of
+    tests/_margins.py with the oracle's fp64 run on the same inputs among the
+    perturbed runs, at tolerance 1e-2 (where the oracle's fp32 and fp64 runs
+    stop every checked sample at the same iteration); same-count iterates at
+    the parity bar, statuses equal."""
+    require_gpu()
+    tol = 1e-4 if dtype == np.float64 else 1e-2
+    n_oracle = {48: 8, 700: 4, 1500: 3, 4096: 2}
+    stopped = 0
+    for k, (n, me, mi, width, B) in enumerate(((48, 8, 20, 4, 37), (700, 100, 300, 5, 40),
+                                               (1500, 300, 700, 6, 24),
+                                               (4096, 1024, 2048, 8, 12))):
+        w = workloads.small_random(60 + k, n=n, me=me, mi=mi, width=width, batch=B,
+                                   accelerated=accelerated)
+        canon, values, rhs, mask = _per_sample(w, B, 70 + k)
+        target = w.target.astype(dtype)
+        rhs = rhs.astype(dtype)
+        vals = _csr(values, mask).astype(dtype)
+        plan = plan_for(canon, dtype=dtype, accelerated=accelerated)
+        kw = dict(values=vals, max_iterations=2000, early_stop=True, tolerance=tol,
+                  check_every=7, timing=True)
+        print(f"values resident early stop n={n} {np.dtype(dtype).name} "
+              f"accelerated={accelerated}", flush=True)
+        res = plan.project(target, rhs, **kw)
+        assert plan.last_timing()["resident"] == 1, n
+        st = plan.project(target, rhs, streaming=True, **kw)
+        assert plan.last_timing()["resident"] == 0, n
+        it_r, it_s = to_np(res.iterations), to_np(st.iterations)
+        bar = TOL[dtype]
+        same = it_r == it_s
+        if dtype == np.float64:
+            np.testing.assert_array_equal(it_r, it_s)
+        assert rel_err(to_np(res.y)[same], to_np(st.y)[same]) <= bar, n
+        np.testing.assert_array_equal(to_np(res.status)[same], to_np(st.status)[same])
+        stopped += int(np.sum(it_r < kw["max_iterations"]))
+        sub = np.arange(n_oracle[n])
+        cfg = op.Config(accelerated=accelerated, max_iterations=2000, early_stop=True,
+                        tolerance=tol)
+        v32 = values[sub].astype(dtype)
+        alt = () if dtype == np.float64 else (
+            lambda tr: op.solve(canon, target[sub].astype(np.float64),
+                                rhs[sub].astype(np.float64), cfg, dtype=np.float64,
+                                values=v32.astype(np.float64), trace=tr),)
+        mg = Margins(lambda safety, tr: op.solve(canon, target[sub], rhs[sub],
+                                                 replace(cfg, safety=safety), dtype=dtype,
+                                                 values=v32, trace=tr), dtype, alternates=alt)
+        print(f"  counts gpu {it_r[sub].tolist()} oracle {mg.want.iterations.tolist()}",
+              flush=True)
+        same_o = check_counts(it_r, mg, samples=sub)
+        check_iterates(to_np(res.y), mg, same_o, bar, samples=sub)
+        np.testing.assert_array_equal(to_np(res.status)[sub][same_o], mg.want.status[same_o])
+    assert stopped > 0  # the stop test fired
 
 
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
