@@ -326,9 +326,9 @@ def run_mode(args, torch):
             values = torch.as_tensor(w.data[None, :] * scale, device=dev)
             target = torch.as_tensor(w.target, device=dev)
             rhs = torch.as_tensor(np.tile(w.rhs, (B, 1)), device=dev)
-            kw = dict(max_iterations=iters, early_stop=False)
-            call = lambda timing=False, streaming=False: plan.project(
-                target, rhs, values=values, timing=timing, streaming=streaming, **kw)
+            call = lambda timing=False, streaming=False, early=False: plan.project(
+                target, rhs, values=values, timing=timing, streaming=streaming,
+                max_iterations=iters, early_stop=early, tolerance=1e-9)
             extra_n = 0
         else:
             general = w.me + int(w.info["mi_general"])
@@ -495,21 +495,20 @@ def resident_mode_line(args, torch, plan, call, tm, B, n, m, nnz, ws, iters, ms_
                       "streaming_passes_ms_per_step": streaming_ms,
                       "streaming_passes_value": B / (streaming_ms / 1e3)},
     }
-    if args.mode == "qp":
-        # PreparedDiagonalQP.solve's default loop (early stop at tolerance 1e-9,
-        # freezing, stationarity) on the same inputs, resident and streaming
-        call(early=True)
-        early_ms, res = time_calls(torch, lambda: call(early=True, timing=True), 1)
-        early_resident = plan.last_timing()["resident"]
-        early_iters = int(res.iterations.max().item())
-        early_streaming_ms, _ = time_calls(torch, lambda: call(early=True, streaming=True), 1)
-        line["early_stop"] = {
-            "what": "the same solve with early stop at tolerance 1e-9 (the stop test every "
-                    "iteration, freezing, stationarity)",
-            "ms_per_step": early_ms, "value": B / (early_ms / 1e3),
-            "resident_kernel": bool(early_resident), "iterations_max": early_iters,
-            "streaming_passes_ms_per_step": early_streaming_ms,
-            "streaming_passes_value": B / (early_streaming_ms / 1e3)}
+    # the default loop (early stop at tolerance 1e-9, freezing,
+    # stationarity) on the same inputs, resident and streaming
+    call(early=True)
+    early_ms, res = time_calls(torch, lambda: call(early=True, timing=True), 1)
+    early_resident = plan.last_timing()["resident"]
+    early_iters = int(res.iterations.max().item())
+    early_streaming_ms, _ = time_calls(torch, lambda: call(early=True, streaming=True), 1)
+    line["early_stop"] = {
+        "what": "the same solve with early stop at tolerance 1e-9 (the stop test every "
+                "iteration, freezing, stationarity)",
+        "ms_per_step": early_ms, "value": B / (early_ms / 1e3),
+        "resident_kernel": bool(early_resident), "iterations_max": early_iters,
+        "streaming_passes_ms_per_step": early_streaming_ms,
+        "streaming_passes_value": B / (early_streaming_ms / 1e3)}
     print(json.dumps(line), flush=True)
 
 
