@@ -292,10 +292,10 @@ int purin_cp_project_noalloc(purin_cp_plan* plan, void* stream, int64_t batch,
  *   values (B, nnz) in the plan's CSR entry order (indptr/indices given to
  *   plan_create; the plan's own values are not used by this call).
  * Other arguments and outputs as purin_cp_project(); opts->shared_bounds must
- * be 0.  The saved state is for purin_cp_adjoint_values() only.  Fixed
- * iterations (early_stop = 0) run on the resident kernel where the problem
- * fits it (each workgroup streams its samples' coefficients; opts->streaming
- * = 1 forces the streaming passes); the results agree to rounding.
+ * be 0.  The saved state is for purin_cp_adjoint_values() only.  The
+ * iterations run on the resident kernel where the problem fits it (each
+ * workgroup streams its samples' coefficients; opts->streaming = 1 forces the
+ * streaming passes); the results agree to rounding.
  */
 int purin_cp_project_values(purin_cp_plan* plan, void* stream, int64_t batch,
                             const void* values, const void* target, const void* rhs,
@@ -316,8 +316,7 @@ int purin_cp_project_values(purin_cp_plan* plan, void* stream, int64_t batch,
  * rhs (B, me+mi); y0 (B, n) or NULL for zero; dual0 (B, me+mi) or NULL.
  * Outputs y (B, n), multipliers (B, me+mi), slacks (B, mi), status,
  * iterations, residual (original units), finite, converged (B); each but y
- * may be NULL.  opts->shared_bounds must be 0.  Fixed iterations
- * (early_stop = 0) with the plan's own coefficients (values NULL) run on the
+ * may be NULL.  opts->shared_bounds must be 0.  The iterations run on the
  * resident kernel where the problem fits it (opts->streaming = 1 forces the
  * streaming passes); the results agree to rounding.
  */

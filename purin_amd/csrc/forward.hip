@@ -252,7 +252,8 @@ int res_tile_samples(const purin_cp_plan* p) {
 }
 
 // One translation unit per (element type, row slots): resident_launch.hip.
-// kind: 0 the projection, 1 the diagonal QP, 2 per-sample coefficients
+// kind: 0 the projection, 1 the diagonal QP, 2 per-sample coefficients, 3 the
+// diagonal QP with per-sample coefficients
 template <typename T, int SLR>
 int launch_resident_rows(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, int slc,
                          bool sb, bool early, int nb, int kind);
@@ -355,7 +356,7 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   } else {
     gather(gc, (const T*)(sv + L.Tt), p->res_colmap, Kc, Ts);
   }
-  if (ps && !qp) {  // per-sample coefficients: each tile's stream of them
+  if (ps && !ps->RVs) {  // per-sample coefficients: each tile's stream of them
     const int64_t entries = p->res_stream_bytes / (int64_t)res_chunk_bytes<T>() * 256;
     T* CS = (T*)(ws + L.RCS);
     const int64_t threads = entries * tiles;
@@ -368,9 +369,11 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
                                                                   ps->CV, Bp, tiles, CS);
     R.Cs = CS;
     R.cs_tile = entries;
-    R.step0 = ps->tau_b;
-    R.gam = nullptr;  // gamma = min q = 1
-    R.accel = p->opts.accelerated;
+    if (!qp) {
+      R.step0 = ps->tau_b;
+      R.gam = nullptr;  // gamma = min q = 1
+      R.accel = p->opts.accelerated;
+    }
   }
   gather(gr, (const T*)(sv + L.R), p->res_rowmap, Kr, Rs);
   gather(gr, (const T*)(sv + L.D), p->res_rowmap, Kr, D0s);
@@ -397,7 +400,8 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     PURIN_HIP(hipEventRecord(e0, st));
   }
   if (int rc = launch_resident<T>(R, st, tiles, lds, p->res_mr, p->res_mc,
-                                  o.shared_bounds != 0, early, BT, qp ? 1 : (ps ? 2 : 0)))
+                                  o.shared_bounds != 0, early, BT,
+                                  qp ? (ps->RVs ? 1 : 3) : (ps ? 2 : 0)))
     return rc;
   PURIN_HIP(hipGetLastError());
   if (o.timing) {
@@ -480,9 +484,8 @@ int run_iterations(purin_cp_plan* p, hipStream_t st, int64_t batch, const Layout
   const bool early = o.early_stop != 0;
   const size_t lds = resident_lds<T>(p, early);
   // the resident kernel takes one schedule of scalar steps for the whole tile,
-  // or, for the diagonal QP with the plan's own coefficients (one shared
-  // copy), per-sample steps it advances itself
-  const bool res_qp = qp && !qp->dense && ps && ps->RVs && !o.shared_bounds;
+  // or, for the diagonal QP, per-sample steps it advances itself
+  const bool res_qp = qp && !qp->dense && ps && !o.shared_bounds;
   // per-sample coefficients: each tile streams its own
   const bool res_vals = !qp && ps && !ps->RVs;
   if (lds && !o.streaming && !p->diag && ((!ps && !qp) || res_qp || res_vals)) {

@@ -15,14 +15,16 @@
 namespace purin {
 
 // kind: 0 the projection, 1 the diagonal QP (per-sample bounds), 2
-// per-sample coefficients
+// per-sample coefficients, 3 the diagonal QP with per-sample coefficients
 template <typename T, int SLR, int SLC, int NB>
 static int launch_nb(const Res<T>& R, hipStream_t st, int64_t tiles, size_t lds, bool sb,
                      bool early, int kind) {
-  if ((kind == 1 && sb) || kind < 0 || kind > 2)
+  if (((kind == 1 || kind == 3) && sb) || kind < 0 || kind > 3)
     return set_error(PURIN_CP_ERR_ARG, "resident kernel variant out of range");
   auto kern = kind == 1 ? (early ? k_resident_early<T, SLR, SLC, false, NB, true>
                                  : k_resident<T, SLR, SLC, false, NB, true>)
+              : kind == 3 ? (early ? k_resident_early<T, SLR, SLC, false, NB, true, true>
+                                   : k_resident<T, SLR, SLC, false, NB, true, true>)
               : kind == 2 ? (early ? (sb ? k_resident_early<T, SLR, SLC, true, NB, false, true>
                                          : k_resident_early<T, SLR, SLC, false, NB, false, true>)
                                    : (sb ? k_resident<T, SLR, SLC, true, NB, false, true>

@@ -135,12 +135,12 @@ def _shared_qp(n, me, mi, width, B, dtype, accelerated):
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
 @pytest.mark.parametrize("accelerated", [False, True])
 def test_qp_resident_matches_streaming_and_oracle(dtype, accelerated):
-    """Fixed iterations of the diagonal QP with the plan's own coefficients run
-    on the resident kernel (per-sample q and c in registers, per-sample steps
-    advanced in the kernel as the streaming passes' schedule does,
-    kernels.py:279-283 with gamma = min q): against the streaming passes on
-    the whole batch and the oracle on two samples, for every slot count of the
-    resident schedule, with a warm start, random boxes and one shared box."""
+    """Fixed iterations of the diagonal QP on the resident kernel (per-sample q
+    and c in registers, per-sample steps advanced in the kernel as the
+    streaming passes' schedule does, kernels.py:279-283 with gamma = min q):
+    against the streaming passes on the whole batch and the oracle on two
+    samples, for every slot count of the resident schedule, with a warm
+    start, random boxes, one shared box, and per-sample coefficients."""
     require_gpu()
     for n, me, mi, width, B in RESIDENT_QP_SIZES:
         support, mask, data, y0, plan = _shared_qp(n, me, mi, width, B, dtype, accelerated)
@@ -176,6 +176,20 @@ def test_qp_resident_matches_streaming_and_oracle(dtype, accelerated):
         assert rel_err(to_np(rb.y), to_np(sb.y)) <= bar, n
         assert rel_err(to_np(rb.multipliers), to_np(sb.multipliers)) <= bar, n
         np.testing.assert_array_equal(to_np(rb.y) == 0.8, to_np(sb.y) == 0.8)
+        # per-sample coefficients (the front end's call): each tile streams its
+        # samples' coefficients
+        scale = np.random.default_rng(n).uniform(0.8, 1.2, data.values.shape)
+        pv = (data.values * scale).astype(dtype)
+        rv = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, values=pv[:, mask],
+                           **kw)
+        assert plan.last_timing()["resident"] == 1, n
+        sv = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, values=pv[:, mask],
+                           streaming=True, **kw)
+        assert rel_err(to_np(rv.y), to_np(sv.y)) <= bar, n
+        assert rel_err(to_np(rv.multipliers), to_np(sv.multipliers)) <= bar, n
+        wantv = dq.solve(support, mask, me, dq.QPData(*(x[sub] for x in data._replace(values=pv))),
+                         cfg, y0=y0[sub])
+        assert rel_err(to_np(rv.y)[sub], wantv.y) <= bar, n
 
 
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
@@ -265,9 +279,8 @@ def test_qp_shared_values_and_warm_start(early_stop):
     (y0, dual0) enters the iteration like the oracle's (diagonal_qp.py:240-273).
     The shared streaming path reads one copy of the scaled entries, the same
     bits as every sample's copy when the values are passed per sample, so the
-    two agree exactly.  (Fixed iterations with shared values run on the
-    resident kernel by default, which sums in its own scheduled order: held to
-    the oracle at the parity bar.)"""
+    two agree exactly.  (By default both run on the resident kernel, which
+    sums in its own scheduled order: held to the oracle at the parity bar.)"""
     require_gpu()
     rows, me, mi, n, support, mask, data = _problem(43, B=17)
     shared = data.values[0]
@@ -297,7 +310,7 @@ def test_qp_shared_values_and_warm_start(early_stop):
     assert rel_err(to_np(got_s.y), want.y) <= 1e-10
     got2 = plan.qp_solve(data.q, data.c, data.rhs, data.lower, data.upper, y0=y0, dual0=d0,
                          values=data.values[:, mask], max_iterations=iters,
-                         early_stop=early_stop)
+                         early_stop=early_stop, streaming=True)
     np.testing.assert_array_equal(to_np(got2.y), to_np(got_s.y))
     np.testing.assert_array_equal(to_np(got2.iterations), to_np(got_s.iterations))
 
