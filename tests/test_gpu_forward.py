@@ -335,6 +335,54 @@ def test_resident_kernel_matches_streaming_and_oracle(dtype, accelerated):
 
 
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_resident_random_shapes(dtype):
+    """Fourteen shapes drawn from a fixed seed over the resident kernel's range:
+    n and m from 1 to 4096 (one to four row and column slots, up to the
+    largest tile), no general rows at all, ragged rows of 2 to 12 entries
+    (columns of width 0, chunks shared by two slots), batches that leave the
+    last tile partly empty; fixed iterations and early stop against the
+    streaming passes on the whole batch (fp64 counts identical)."""
+    require_gpu()
+    rng = np.random.default_rng(2024)
+    shapes = [(1, 0, 0), (3, 1, 1), (4096, 0, 0)]
+    while len(shapes) < 14:
+        n = int(rng.integers(2, 4097))
+        m = int(rng.integers(1, 4097))
+        me = int(rng.integers(0, m + 1)) // 3
+        shapes.append((n, me, m - me))
+    bar = TOL[dtype]
+    for k, (n, me, mi) in enumerate(shapes):
+        B = int(rng.integers(1, 300))
+        wmax = min(12, n)
+        wmin = min(2, wmax)
+        w = workloads.ragged_rows(400 + k, n=n, me=me, mi=mi, wmin=wmin, wmax=wmax, batch=B,
+                                  accelerated=bool(k % 2))
+        canon = canonical_from_workload(w)
+        rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+        target = w.target.astype(dtype)
+        plan = plan_for(canon, dtype=dtype, accelerated=bool(k % 2))
+        print(f"random shape {k}: n={n} me={me} mi={mi} B={B} {np.dtype(dtype).name}",
+              flush=True)
+        kw = dict(max_iterations=60, early_stop=False, timing=True)
+        res = plan.project(target, rhs, **kw)
+        assert plan.last_timing()["resident"] == 1, (k, n, me, mi)
+        st = plan.project(target, rhs, streaming=True, **kw)
+        assert rel_err(to_np(res.y), to_np(st.y)) <= bar / 10, (k, n, me, mi)
+        assert rel_err(to_np(res.multipliers), to_np(st.multipliers)) <= bar, (k, n, me, mi)
+        np.testing.assert_array_equal(to_np(res.status), to_np(st.status))
+        kw = dict(max_iterations=300, early_stop=True, tolerance=1e-3, timing=True)
+        re_ = plan.project(target, rhs, **kw)
+        assert plan.last_timing()["resident"] == 1, (k, n, me, mi)
+        se = plan.project(target, rhs, streaming=True, **kw)
+        it_r, it_s = to_np(re_.iterations), to_np(se.iterations)
+        same = it_r == it_s
+        if dtype == np.float64:
+            np.testing.assert_array_equal(it_r, it_s)
+        assert rel_err(to_np(re_.y)[same], to_np(se.y)[same]) <= bar, (k, n, me, mi)
+        np.testing.assert_array_equal(to_np(re_.status)[same], to_np(se.status)[same])
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
 def test_resident_largest_tile(dtype):
     """The largest problem the resident kernels take: n = m = 4096, four row
     and four column slots per thread, a 131,104-byte LDS image (150,576 bytes
