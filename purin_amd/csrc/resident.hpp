@@ -237,6 +237,19 @@ __device__ __forceinline__ void load_chunk(Chunk<T, CV>& c, const unsigned char*
   }
 }
 
+// acc <- fma(coefficient, gathered element, acc), per sample: the fused step of
+// every sum over the stream.  Written as one intrinsic (not a product and a sum
+// left to contraction), so no transformation can separate the product from its
+// sum, e.g. hoist the products that the blocks of a split chunk share.
+template <typename V, typename CV>
+__device__ __forceinline__ void fma_acc(V& acc, CV c, V x) {
+  if constexpr (std::is_same<CV, V>::value) {
+    acc = __builtin_elementwise_fma(c, x, acc);
+  } else {
+    acc = __builtin_elementwise_fma(V(c), x, acc);
+  }
+}
+
 // acc += sum over the chunk's 4 entries of coefficient * gathered element, in order
 template <typename T, typename V, typename CV>
 __device__ __forceinline__ void consume_chunk(const Chunk<T, CV>& c, V& acc) {
@@ -244,7 +257,7 @@ __device__ __forceinline__ void consume_chunk(const Chunk<T, CV>& c, V& acc) {
 #pragma unroll
   for (int u = 0; u < kResChunk; ++u) x[u] = ent_read<V>(c.o[u]);
 #pragma unroll
-  for (int u = 0; u < kResChunk; ++u) acc += c.v[u] * x[u];
+  for (int u = 0; u < kResChunk; ++u) fma_acc(acc, c.v[u], x[u]);
 }
 
 // Entries [0, e) of the chunk to acc and entries [e, 4) to carry, in order:
@@ -258,22 +271,22 @@ __device__ __forceinline__ void consume_split(const Chunk<T, CV>& c, int e, V& a
   // from merging the blocks into selects over both sums
   if (e == 1) {
     asm volatile("");
-    acc += c.v[0] * x[0];
-    carry += c.v[1] * x[1];
-    carry += c.v[2] * x[2];
-    carry += c.v[3] * x[3];
+    fma_acc(acc, c.v[0], x[0]);
+    fma_acc(carry, c.v[1], x[1]);
+    fma_acc(carry, c.v[2], x[2]);
+    fma_acc(carry, c.v[3], x[3]);
   } else if (e == 2) {
     asm volatile("");
-    acc += c.v[0] * x[0];
-    acc += c.v[1] * x[1];
-    carry += c.v[2] * x[2];
-    carry += c.v[3] * x[3];
+    fma_acc(acc, c.v[0], x[0]);
+    fma_acc(acc, c.v[1], x[1]);
+    fma_acc(carry, c.v[2], x[2]);
+    fma_acc(carry, c.v[3], x[3]);
   } else {
     asm volatile("");
-    acc += c.v[0] * x[0];
-    acc += c.v[1] * x[1];
-    acc += c.v[2] * x[2];
-    carry += c.v[3] * x[3];
+    fma_acc(acc, c.v[0], x[0]);
+    fma_acc(acc, c.v[1], x[1]);
+    fma_acc(acc, c.v[2], x[2]);
+    fma_acc(carry, c.v[3], x[3]);
   }
 }
 
