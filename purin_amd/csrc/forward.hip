@@ -399,7 +399,17 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     PURIN_HIP(hipEventCreate(&e1));
     PURIN_HIP(hipEventRecord(e0, st));
   }
-  if (int rc = launch_resident<T>(R, st, tiles, lds, p->res_mr, p->res_mc,
+  // per-sample bounds (fixed iterations): the leading column slots' bounds
+  // held in the LDS the image leaves free, so the rest stay in L2 (config 2
+  // shape: one slot of four)
+  size_t lds_all = lds;
+  if (!o.shared_bounds && !early) {
+    const size_t slot_lds = (size_t)2 * kResThreads * BT * sizeof(T);
+    const size_t room = (size_t)160 * 1024 - lds;
+    R.lb_slots = (int)std::min<size_t>((size_t)p->res_mc, room / slot_lds);
+    lds_all += (size_t)R.lb_slots * slot_lds;
+  }
+  if (int rc = launch_resident<T>(R, st, tiles, lds_all, p->res_mr, p->res_mc,
                                   o.shared_bounds != 0, early, BT,
                                   qp ? (ps->RVs ? 1 : 3) : (ps ? 2 : 0)))
     return rc;

@@ -141,6 +141,9 @@ struct Res {
   // with gamma 1 and the prox a, delta of q = 1 from step0's rows 2 and 3
   const T* __restrict__ Cs;
   int64_t cs_tile;
+  // per-sample bounds (k_resident): the leading column slots whose bounds the
+  // kernel holds in LDS after the image (the launch's LDS includes them)
+  int lb_slots;
 };
 
 // One chunk of a wavefront's stream in registers: the lane's 4 LDS addresses
@@ -186,6 +189,32 @@ __device__ __forceinline__ void ent_write(uint32_t addr, V v) {
     const P4 p = reinterpret_cast<P4>(addr);
     p[0] = __builtin_shufflevector(v, v, 0, 1, 2, 3);
     p[kResPlane / 16] = __builtin_shufflevector(v, v, 4, 5, 6, 7);
+  } else {
+    lds_write<V>(addr, v);
+  }
+}
+
+// A tile vector in LDS as 16-byte granules ``stride`` bytes apart (one granule,
+// or two for a 32-byte vector): the per-sample bounds held on chip, laid out
+// so that consecutive lanes read consecutive granules (no bank conflicts).
+template <typename V>
+__device__ __forceinline__ V lds_read_split(uint32_t addr, uint32_t stride) {
+  if constexpr (sizeof(V) == 32) {
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    const F4 lo = lds_read<F4>(addr), hi = lds_read<F4>(addr + stride);
+    return __builtin_bit_cast(V, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  } else {
+    return lds_read<V>(addr);
+  }
+}
+template <typename V>
+__device__ __forceinline__ void lds_write_split(uint32_t addr, uint32_t stride, V v) {
+  if constexpr (sizeof(V) == 32) {
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    typedef float F8 __attribute__((ext_vector_type(8)));
+    const F8 f = __builtin_bit_cast(F8, v);
+    lds_write<F4>(addr, __builtin_shufflevector(f, f, 0, 1, 2, 3));
+    lds_write<F4>(addr + stride, __builtin_shufflevector(f, f, 4, 5, 6, 7));
   } else {
     lds_write<V>(addr, v);
   }
@@ -561,6 +590,27 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   }
   if (t == 0) ent_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
   const bool uni = __builtin_amdgcn_ballot_w64(same != 0) == ~0ull;  // all 64 lanes
+  // per-sample bounds of the leading lb_slots column slots, held in LDS after
+  // the image: slot c's lower bounds, then its upper bounds, each as 16-byte
+  // granules of consecutive threads (two granule rows for a 32-byte vector).
+  // Each thread reads back only what it wrote, so no barrier orders them.
+  // Held on chip they leave the L2 to the other slots' bounds, which then
+  // stay there instead of being re-read from beyond it every iteration.
+  constexpr uint32_t VB = (uint32_t)sizeof(V);
+  constexpr uint32_t GS = NT * 16u;  // bytes of one granule row
+  const uint32_t lb_off = (VB == 32 ? 2u * kResPlane : trash_off + 16u) + (uint32_t)t * 16u;
+  const int lbs = SB ? 0 : __builtin_amdgcn_readfirstlane(A.lb_slots);
+  if constexpr (!SB) {
+#pragma unroll
+    for (int c = 0; c < SLC; ++c) {
+      if (c < lbs) {
+        const int64_t e = tile * (int64_t)A.Kc + c * NT + t;
+        const uint32_t at = lb_off + (uint32_t)c * 2u * (VB / 16u) * GS;
+        lds_write_split<V>(at, GS, reinterpret_cast<const V*>(A.Ls)[e]);
+        lds_write_split<V>(at + (VB / 16u) * GS, GS, reinterpret_cast<const V*>(A.Hs)[e]);
+      }
+    }
+  }
   __syncthreads();
 
   constexpr uint32_t CB = res_chunk_bytes<T>();
@@ -630,6 +680,10 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       } else if (SB) {
         lo = V(lb[c * NT + t]);
         hi = V(hb[c * NT + t]);
+      } else if (c < lbs) {
+        const uint32_t at = lb_off + (uint32_t)c * 2u * (VB / 16u) * GS;
+        lo = lds_read_split<V>(at, GS);
+        hi = lds_read_split<V>(at + (VB / 16u) * GS, GS);
       } else {
         lo = ((GV)lb)[tile * (int64_t)A.Kc + c * NT + t];
         hi = ((GV)hb)[tile * (int64_t)A.Kc + c * NT + t];
