@@ -430,6 +430,70 @@ def test_resident_largest_tile(dtype):
         assert np.all(it < kw["max_iterations"]) and len(np.unique(it)) > 2
 
 
+# (n, me, mi, dtype, the column slots whose per-sample bounds the fixed-iteration
+# resident kernel holds in LDS: what fits of 160 KB beside the image, at most
+# the column slot count)
+LDS_BOUNDS = ((1000, 100, 200, np.float64, 1), (2000, 200, 400, np.float64, 2),
+              (3000, 300, 500, np.float64, 3), (4096, 200, 400, np.float64, 2),
+              (4096, 1024, 2048, np.float64, 1), (3000, 300, 500, np.float32, 3),
+              (800, 100, 200, np.float32, 1))
+
+
+def _lds_bound_slots(info, dtype):
+    """The kernel's rule, restated: 16-byte entries (n + 1 + m + 1), or two
+    planes of 32,800 bytes for 8-sample fp32 tiles; a slot's bounds take
+    2 x 1024 x 16 bytes per 16 bytes of tile samples."""
+    samples = info.resident_tile_samples
+    vb = samples * np.dtype(dtype).itemsize
+    image = 2 * 32800 if samples == 8 else (info.n + 1 + info.kept_rows + 1) * 16
+    return min(info.resident_col_slots // 1024, (160 * 1024 - image) // (2 * 1024 * vb))
+
+
+@pytest.mark.parametrize("case", range(len(LDS_BOUNDS)))
+def test_resident_per_sample_bounds_held_in_lds(case):
+    """Per-sample bounds with one to three column slots held in LDS by the
+    fixed-iteration resident kernel (the rest read from memory): bounds equal
+    in every sample give the shared-bounds bits; bounds scaled per sample
+    (upper f_b, lower -f_b, f_b in [0.5, 1.5]) match the streaming passes on
+    the whole batch and the oracle on two samples, at the parity bars."""
+    require_gpu()
+    n, me, mi, dtype, want_slots = LDS_BOUNDS[case]
+    B = 37
+    w = workloads.small_random(700 + case, n=n, me=me, mi=mi, width=5, batch=B,
+                               accelerated=True)
+    canon = canonical_from_workload(w)
+    plan = plan_for(canon, dtype=dtype, accelerated=True)
+    assert _lds_bound_slots(plan.info, dtype) == want_slots, case
+    bar = TOL[dtype]
+    target = w.target.astype(dtype)
+    rhs = np.tile(w.rhs, (B, 1)).astype(dtype)
+    kw = dict(max_iterations=150, early_stop=False)
+    print(f"bounds in LDS: n={n} m={me + mi} {np.dtype(dtype).name} slots={want_slots}",
+          flush=True)
+    ps = plan.project(target, rhs, timing=True, **kw)
+    assert plan.last_timing()["resident"] == 1
+    sh = plan.project(target, rhs, shared_bounds=True, **kw)
+    np.testing.assert_array_equal(to_np(ps.y), to_np(sh.y))
+    np.testing.assert_array_equal(to_np(ps.multipliers), to_np(sh.multipliers))
+    # the last 2n rows are the bound rows (y <= 1, then -y <= 1)
+    f = np.random.default_rng(case).uniform(0.5, 1.5, B)
+    rhs_v = np.tile(w.rhs, (B, 1))
+    rhs_v[:, -2 * n:] *= f[:, None]
+    rhs_v = rhs_v.astype(dtype)
+    got = plan.project(target, rhs_v, timing=True, **kw)
+    assert plan.last_timing()["resident"] == 1
+    st = plan.project(target, rhs_v, streaming=True, **kw)
+    assert rel_err(to_np(got.y), to_np(st.y)) <= bar / 10, case
+    assert rel_err(to_np(got.multipliers), to_np(st.multipliers)) <= bar, case
+    np.testing.assert_array_equal(to_np(got.status), to_np(st.status))
+    assert not np.array_equal(to_np(got.y), to_np(ps.y))  # the bounds bind differently
+    sub = slice(0, 2)
+    cfg = op.Config(accelerated=True, max_iterations=150, early_stop=False)
+    want = op.solve(canon, target[sub], rhs_v[sub], cfg, dtype=dtype)
+    assert rel_err(to_np(got.y)[sub], want.y) <= bar, case
+    np.testing.assert_array_equal(to_np(got.status)[sub], want.status)
+
+
 # ragged rows: (n, me, mi, wmin, wmax, B).  The resident schedule packs each
 # wavefront's slots back to back, so a chunk may hold the end of one slot and
 # the start of the next: these shapes give split chunks in the row pass (3 and
