@@ -399,13 +399,16 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
     PURIN_HIP(hipEventCreate(&e1));
     PURIN_HIP(hipEventRecord(e0, st));
   }
-  // per-sample bounds (fixed iterations): the leading column slots' bounds
-  // held in the LDS the image leaves free, so the rest stay in L2 (config 2
-  // shape: one slot of four)
+  // per-sample bounds: the leading column slots' bounds held in the LDS the
+  // image leaves free, so the rest stay in L2 (config 2 shape: one slot of
+  // four).  The early-stop kernel does so for the projection (not the QP),
+  // in the room where it would otherwise keep K y of its first row slots.
   size_t lds_all = lds;
-  if (!o.shared_bounds && !early) {
+  if (!o.shared_bounds && (!early || !qp)) {
+    if (early && BT != 8)
+      lds_all -= (size_t)res_early_kyl(p->res_mr, p->res_mc) * kResThreads * 16;
     const size_t slot_lds = (size_t)2 * kResThreads * BT * sizeof(T);
-    const size_t room = (size_t)160 * 1024 - lds;
+    const size_t room = (size_t)160 * 1024 - lds_all;
     R.lb_slots = (int)std::min<size_t>((size_t)p->res_mc, room / slot_lds);
     lds_all += (size_t)R.lb_slots * slot_lds;
   }

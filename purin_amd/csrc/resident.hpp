@@ -885,9 +885,16 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   constexpr uint32_t VB = (uint32_t)sizeof(V);
   const uint32_t red_off = VB == 32 ? 2u * kResPlane : trash_off + 16u;
   const uint32_t dec_off = red_off + 16u * 4u * kResQ * VB;  // [BT] verdicts
-  constexpr int KYL = VB == 32 ? 0 : res_early_kyl(SLR, SLC);
+  // per-sample bounds of the projection (plan or per-sample coefficients):
+  // the leading column slots' bounds are held in LDS after the verdicts, in
+  // the room K y would take (k_resident's layout), so K y stays in registers
+  constexpr bool kLB = !SB && !QP;
+  constexpr int KYL = (VB == 32 || kLB) ? 0 : res_early_kyl(SLR, SLC);
   // [KYL][1024] K y of the first row slots, after the verdicts
   const uint32_t kyl_off = red_off + res_early_extra(VB, BT);
+  constexpr uint32_t GS = NT * 16u;  // bytes of one granule row of held bounds
+  const uint32_t lb_off = kyl_off + (uint32_t)t * 16u;
+  const int lbs = kLB ? __builtin_amdgcn_readfirstlane(A.lb_slots) : 0;
 
   const uint32_t first = (uint32_t)__builtin_amdgcn_readfirstlane(A.wtab[kResWtab * wave]);
   // per slot (8 bits each): whole chunks from the slot's first whole chunk on,
@@ -992,6 +999,17 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
     ent_write<V>(soff_r[r], i >= 0 ? D0[r * NT + t] : vzero);
   }
   if (t == 0) ent_write<V>((uint32_t)A.n * 16u, vzero);  // the zero slot
+  if constexpr (kLB) {  // each thread reads back only what it writes here
+#pragma unroll
+    for (int c = 0; c < SLC; ++c) {
+      if (c < lbs) {
+        const int64_t e = tile * (int64_t)A.Kc + c * NT + t;
+        const uint32_t at = lb_off + (uint32_t)c * 2u * (VB / 16u) * GS;
+        lds_write_split<V>(at, GS, reinterpret_cast<const V*>(A.Ls)[e]);
+        lds_write_split<V>(at + (VB / 16u) * GS, GS, reinterpret_cast<const V*>(A.Hs)[e]);
+      }
+    }
+  }
   const bool uni = __builtin_amdgcn_ballot_w64(same != 0) == ~0ull;  // all 64 lanes
   // samples of the tile: the padding samples beyond the batch never run
   const int64_t bs0 = tile * BT;
@@ -1088,6 +1106,10 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       } else if (SB) {
         lo = V(lb[c * NT + t]);
         hi = V(hb[c * NT + t]);
+      } else if (kLB && c < lbs) {
+        const uint32_t at = lb_off + (uint32_t)c * 2u * (VB / 16u) * GS;
+        lo = lds_read_split<V>(at, GS);
+        hi = lds_read_split<V>(at + (VB / 16u) * GS, GS);
       } else {
         lo = ((GV)lb)[tile * (int64_t)A.Kc + c * NT + t];
         hi = ((GV)hb)[tile * (int64_t)A.Kc + c * NT + t];
