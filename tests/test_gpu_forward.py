@@ -386,8 +386,10 @@ def test_resident_random_shapes(dtype):
 def test_resident_largest_tile(dtype):
     """The largest problem the resident kernels take: n = m = 4096, four row
     and four column slots per thread, a 131,104-byte LDS image (150,576 bytes
-    in the early-stop kernel, which keeps K y of one row slot in LDS and
-    re-reads targets and right-hand sides each iteration).  Fixed iterations
+    in the early-stop kernel with shared bounds, which keeps K y of one row
+    slot in LDS; with per-sample bounds it keeps K y in registers, and no
+    slot of bounds fits beside the image; either re-reads targets and
+    right-hand sides each iteration).  Fixed iterations
     with per-sample and with shared bounds (bit-identical), against the
     streaming passes and, on two samples, the oracle; early stop in fp64 with
     the streaming passes' iteration counts."""
