@@ -457,7 +457,9 @@ def test_resident_per_sample_bounds_held_in_lds(case):
     fixed-iteration resident kernel (the rest read from memory): bounds equal
     in every sample give the shared-bounds bits; bounds scaled per sample
     (upper f_b, lower -f_b, f_b in [0.5, 1.5]) match the streaming passes on
-    the whole batch and the oracle on two samples, at the parity bars."""
+    the whole batch and the oracle on two samples, at the parity bars; early
+    stop (the early-stop kernel holds the bounds in place of K y) matches the
+    streaming passes' counts (identical in fp64) and iterates."""
     require_gpu()
     n, me, mi, dtype, want_slots = LDS_BOUNDS[case]
     B = 37
@@ -494,6 +496,18 @@ def test_resident_per_sample_bounds_held_in_lds(case):
     want = op.solve(canon, target[sub], rhs_v[sub], cfg, dtype=dtype)
     assert rel_err(to_np(got.y)[sub], want.y) <= bar, case
     np.testing.assert_array_equal(to_np(got.status)[sub], want.status)
+    # the early-stop kernel holds the same slots' bounds in place of K y
+    ke = dict(max_iterations=400, early_stop=True, tolerance=1e-3)
+    ge = plan.project(target, rhs_v, timing=True, **ke)
+    assert plan.last_timing()["resident"] == 1
+    se = plan.project(target, rhs_v, streaming=True, **ke)
+    it_g, it_s = to_np(ge.iterations), to_np(se.iterations)
+    same = it_g == it_s
+    if dtype == np.float64:
+        np.testing.assert_array_equal(it_g, it_s)
+    assert same.mean() >= 0.9, case
+    assert rel_err(to_np(ge.y)[same], to_np(se.y)[same]) <= bar, case
+    np.testing.assert_array_equal(to_np(ge.status)[same], to_np(se.status)[same])
 
 
 # ragged rows: (n, me, mi, wmin, wmax, B).  The resident schedule packs each
