@@ -443,6 +443,30 @@ __device__ __forceinline__ T clip_nonnan_bounds(T x, T lo, T hi) {
   return r >= hi ? hi : r;
 }
 
+// The resident kernels' clip for bounds that are not NaN and projection onto
+// x >= 0.  fp32: gfx950's NaN-propagating v_maximum3_f32 / v_minimum3_f32
+// (IEEE 754-2019 maximum and minimum), one instruction each where the
+// compare-and-select forms take two per side; the values are jnp.clip's and
+// jnp.maximum's, a NaN x passing through.  They differ from clipp / maxp
+// only in the sign of a zero at a tie of +0 with -0 (these order -0 below
+// +0).  fp64 (no such instruction): the compare-and-select forms.
+template <typename T>
+__device__ __forceinline__ T res_clip(T x, T lo, T hi) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_elementwise_minimum(__builtin_elementwise_maximum(x, lo), hi);
+  } else {
+    return clip_nonnan_bounds(x, lo, hi);
+  }
+}
+template <typename T>
+__device__ __forceinline__ T res_pos(T x) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_elementwise_maximum(x, T(0));
+  } else {
+    return maxp(x, T(0));
+  }
+}
+
 // A wave-uniform value kept in SGPRs (its lanes are equal: the first lane's).
 template <typename T>
 __device__ __forceinline__ T res_uniform(T x) {
@@ -652,7 +676,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
       }
       if (ineq & (1u << r)) {
 #pragma unroll
-        for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
+        for (int s = 0; s < BT; ++s) p[s] = res_pos(p[s]);
       }
       ent_write<V>(soff_r[r], p);
     }
@@ -721,7 +745,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
         for (int s = 0; s < BT; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
       } else {
 #pragma unroll
-        for (int s = 0; s < BT; ++s) yn[s] = clip_nonnan_bounds(sv[s], lo[s], hi[s]);
+        for (int s = 0; s < BT; ++s) yn[s] = res_clip(sv[s], lo[s], hi[s]);
       }
       if constexpr (kPS) {
         V yb;
@@ -1055,7 +1079,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
       }
       if (ineq & (1u << r)) {
 #pragma unroll
-        for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
+        for (int s = 0; s < BT; ++s) p[s] = res_pos(p[s]);
       }
       ent_write<V>(soff_r[r], p);  // the first iteration's d+ (every sample active)
     }
@@ -1136,7 +1160,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         for (int s = 0; s < BT; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
       } else {
 #pragma unroll
-        for (int s = 0; s < BT; ++s) yn[s] = clip_nonnan_bounds(sv[s], lo[s], hi[s]);
+        for (int s = 0; s < BT; ++s) yn[s] = res_clip(sv[s], lo[s], hi[s]);
       }
       if (act != (1u << BT) - 1u) {
 #pragma unroll
@@ -1256,7 +1280,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         }
         if (ineq & (1u << r)) {
 #pragma unroll
-          for (int s = 0; s < BT; ++s) p[s] = maxp(p[s], T(0));
+          for (int s = 0; s < BT; ++s) p[s] = res_pos(p[s]);
         }
         if (act != (1u << BT) - 1u) {
 #pragma unroll
