@@ -467,7 +467,9 @@ __device__ __forceinline__ T res_pos(T x) {
   }
 }
 
-// 1 / x for the QP prox's x = 1 + tau q >= 1 (q >= 0, tau > 0): the hardware
+// 1 / x for the QP prox's x = 1 + tau q, which lies in [1, 2) (q >= 0 and
+// tau <= s / (max q + L) with s < 1, decreasing under the accelerated update,
+// kernels.py:209-227): the hardware
 // reciprocal estimate refined by two Newton-Raphson steps r <- r + r (1 - x r)
 // (each with fused multiply-adds), within an ulp of the correctly rounded
 // quotient, in 5 instructions where the IEEE division sequence takes about
