@@ -228,14 +228,15 @@ template <typename T, typename CV = T>
 __device__ __forceinline__ void load_chunk(Chunk<T, CV>& c, const unsigned char* __restrict__ stream,
                                            uint64_t cbyte, uint32_t lane16,
                                            const CV* __restrict__ cs = nullptr) {
-  const uint64_t a = (uint64_t)(uintptr_t)stream + cbyte;
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
-  const __attribute__((address_space(1))) unsigned char* base =
-      (const __attribute__((address_space(1))) unsigned char*)(((uint64_t)hi << 32) | lo);
+  // raw buffer loads: the stream's base in a buffer resource (SGPRs, built
+  // once per launch), the chunk's byte offset as the scalar offset and the
+  // lane's 16 bytes as the vector offset, so a chunk costs no address
+  // arithmetic beyond one scalar add per load (the stream is far below 2 GB)
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)stream, 0, 0x7fffffff, 0x00020000);
+  const uint32_t cb = (uint32_t)cbyte;
   typedef uint32_t U4 __attribute__((ext_vector_type(4)));
-  typedef const __attribute__((address_space(1))) U4* U4P;
-  const U4 o = *reinterpret_cast<U4P>(base + lane16);
+  const U4 o = __builtin_amdgcn_raw_buffer_load_b128(rs, lane16, cb, 0);
   c.o[0] = o.x;
   c.o[1] = o.y;
   c.o[2] = o.z;
@@ -248,17 +249,15 @@ __device__ __forceinline__ void load_chunk(Chunk<T, CV>& c, const unsigned char*
     for (int u = 0; u < kResChunk; ++u) c.v[u] = cp[u * 64];
   } else if constexpr (sizeof(T) == 8) {
     typedef double D2 __attribute__((ext_vector_type(2)));
-    typedef const __attribute__((address_space(1))) D2* D2P;
-    const D2 x = *reinterpret_cast<D2P>(base + 1024u + lane16);
-    const D2 y = *reinterpret_cast<D2P>(base + 2048u + lane16);
+    const D2 x = __builtin_bit_cast(D2, __builtin_amdgcn_raw_buffer_load_b128(rs, lane16, cb + 1024u, 0));
+    const D2 y = __builtin_bit_cast(D2, __builtin_amdgcn_raw_buffer_load_b128(rs, lane16, cb + 2048u, 0));
     c.v[0] = x.x;
     c.v[1] = x.y;
     c.v[2] = y.x;
     c.v[3] = y.y;
   } else {
     typedef float F4 __attribute__((ext_vector_type(4)));
-    typedef const __attribute__((address_space(1))) F4* F4P;
-    const F4 x = *reinterpret_cast<F4P>(base + 1024u + lane16);
+    const F4 x = __builtin_bit_cast(F4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane16, cb + 1024u, 0));
     c.v[0] = x.x;
     c.v[1] = x.y;
     c.v[2] = x.z;
