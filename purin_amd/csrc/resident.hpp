@@ -16,7 +16,8 @@
 //            as {LDS byte address of the gathered element, coefficient}.  The
 //            slots of a pass are packed back to back (a slot may begin and end
 //            inside a chunk; only each pass's end is padded to a whole chunk).
-//            The loads take an SGPR base and a constant lane offset, and the
+//            The loads are raw buffer loads (the stream in a buffer resource,
+//            the chunk's offset scalar, the lane's vector), and the
 //            next chunk is always in flight while the current one is gathered,
 //            across slot, pass and iteration boundaries.
 // Rows and columns are assigned to (slot, thread) in decreasing-degree order
@@ -220,8 +221,8 @@ __device__ __forceinline__ void lds_write_split(uint32_t addr, uint32_t stride, 
   }
 }
 
-// The chunk at byte ``cbyte`` of the stream; the base is made wave-uniform
-// explicitly so the loads take an SGPR base plus the lane's 16-byte offset.
+// The chunk at byte ``cbyte`` of the stream (wave-uniform), loaded by each
+// lane at its 16-byte offset.
 // Per-sample coefficients (CV a vector): the offsets from the stream, the
 // coefficients from ``cs``, the tile's coefficient stream, [chunk][4][64] CV.
 template <typename T, typename CV = T>
