@@ -665,17 +665,25 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
   load_chunk(b0, A.stream, (uint64_t)first * CB, lane16, cs);
   if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16, cs);
 
-  for (int64_t it = 0; it < A.iters; ++it) {
-    // wave-uniform schedule scalars: scalar loads through the constant address space
-    T sigma = T(0), a = T(0), delta = T(0), theta = T(0);
-    if constexpr (!kPS) {  // QP, VALS: the per-sample steps in registers instead
+  // wave-uniform schedule scalars (QP, VALS: the per-sample steps in registers
+  // instead), scalar loads through the constant address space.  Each
+  // iteration's are loaded before the barrier that ends the previous one,
+  // whose wait covers them, so no scalar load is outstanding in the passes
+  // (one would make every wait on an LDS gather there wait for all of them)
+  T sigma = T(0), a = T(0), delta = T(0), theta = T(0);
+  auto load_sched = [&](int64_t i) {
+    if constexpr (!kPS) {
       const __attribute__((address_space(4))) T* sc =
-          (const __attribute__((address_space(4))) T*)(A.sched + 4 * it);
+          (const __attribute__((address_space(4))) T*)(A.sched + 4 * i);
       sigma = sc[0];
       a = sc[1];
       delta = sc[2];
       theta = sc[3];
+      asm volatile("" : "+s"(sigma), "+s"(a), "+s"(delta), "+s"(theta));
     }
+  };
+  load_sched(0);
+  for (int64_t it = 0; it < A.iters; ++it) {
     uint32_t pos = first + 1 + (pro & 1u);
     V carry = vzero;  // the head of the next slot (a chunk shared by two slots)
     // the slot tables, opaque to the loop so that their fields are decoded at
@@ -784,6 +792,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
     }
     // the next row pass's second chunk (b0 holds the copy of its first)
     if (pro & 1u) load_chunk(b1, A.stream, (uint64_t)(first + 1) * CB, lane16, cs);
+    if (it + 1 < A.iters) load_sched(it + 1);
     __syncthreads();
   }
   // ---- hand the state to the batch-minor layout ---------------------------------
