@@ -340,8 +340,9 @@ def test_resident_random_shapes(dtype):
     n and m from 1 to 4096 (one to four row and column slots, up to the
     largest tile), no general rows at all, ragged rows of 2 to 12 entries
     (columns of width 0, chunks shared by two slots), batches that leave the
-    last tile partly empty; fixed iterations and early stop against the
-    streaming passes on the whole batch (fp64 counts identical)."""
+    last tile partly empty; fixed iterations (with bounds shared by the
+    samples and scaled per sample) and early stop against the streaming
+    passes on the whole batch (fp64 counts identical)."""
     require_gpu()
     rng = np.random.default_rng(2024)
     shapes = [(1, 0, 0), (3, 1, 1), (4096, 0, 0)]
@@ -370,6 +371,17 @@ def test_resident_random_shapes(dtype):
         assert rel_err(to_np(res.y), to_np(st.y)) <= bar / 10, (k, n, me, mi)
         assert rel_err(to_np(res.multipliers), to_np(st.multipliers)) <= bar, (k, n, me, mi)
         np.testing.assert_array_equal(to_np(res.status), to_np(st.status))
+        # bounds scaled per sample (the last 2n rows: y <= 1, -y <= 1); the
+        # kernel holds the leading column slots' bounds that fit in LDS
+        f = np.random.default_rng(600 + k).uniform(0.5, 1.5, B)
+        rv = np.tile(w.rhs, (B, 1))
+        rv[:, -2 * n:] *= f[:, None]
+        rv = rv.astype(dtype)
+        rp = plan.project(target, rv, **kw)
+        assert plan.last_timing()["resident"] == 1, (k, n, me, mi)
+        sp = plan.project(target, rv, streaming=True, **kw)
+        assert rel_err(to_np(rp.y), to_np(sp.y)) <= bar / 10, (k, n, me, mi)
+        assert rel_err(to_np(rp.multipliers), to_np(sp.multipliers)) <= bar, (k, n, me, mi)
         kw = dict(max_iterations=300, early_stop=True, tolerance=1e-3, timing=True)
         re_ = plan.project(target, rhs, **kw)
         assert plan.last_timing()["resident"] == 1, (k, n, me, mi)
