@@ -613,7 +613,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 #pragma unroll
     for (int s = 0; s < BT; ++s) {
       const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
-      if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
+      if (!(A.Ls[e] <= A.Hs[e])) nanb |= 1u << c;  // a NaN or crossed bound
       if ((SB || QP) && j >= 0 && (A.Ls[e] != lo0 || A.Hs[e] != hi0)) same = 0;
     }
     soff_c[c] = j >= 0 ? (uint32_t)A.colent[c * NT + t] * 16u : trash_off;
@@ -771,7 +771,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
         sv = a * y[c] - delta * tt + delta * tgc;
       }
       V yn;
-      if (nanb & (1u << c)) {  // a NaN bound on this lane: the exact NaN-propagating clip
+      if (nanb & (1u << c)) {  // a NaN or crossed bound on this lane: the exact NaN-propagating clip
 #pragma unroll
         for (int s = 0; s < BT; ++s) yn[s] = clipp(sv[s], lo[s], hi[s]);
       } else {
@@ -849,8 +849,9 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 // iterates differ from the fixed kernel's (which gathers ybar) by rounding.
 // A non-finite y+ or d+ makes the primal or the dual sum non-finite, so the
 // gap is not finite and the sample is not accepted (the finiteness flag of
-// kernels.py:172).  On lanes whose bounds are not NaN, y+ lies in [lo, hi]
-// (bound violation 0) and the stationarity clip equals the dual term's.
+// kernels.py:172).  On lanes whose bounds are neither NaN nor crossed
+// (lo <= hi), y+ lies in [lo, hi] (bound violation 0) and the stationarity
+// clip equals the dual term's; the other lanes take the full expressions.
 // LDS: the fixed kernel's, then the partials [16 waves][4 rows][kResQ] and
 // the BT verdicts, then K y of the first res_early_kyl(SLR, SLC) row slots.
 constexpr int kResQ = 3;  // primal; dual objective (terms - r.d); max(stationarity, residual)
@@ -1027,7 +1028,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
 #pragma unroll
     for (int s = 0; s < BT; ++s) {
       const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
-      if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e]) nanb |= 1u << c;
+      if (!(A.Ls[e] <= A.Hs[e])) nanb |= 1u << c;  // a NaN or crossed bound
       if ((SB || QP) && j >= 0 && (A.Ls[e] != lo0 || A.Hs[e] != hi0)) same = 0;
     }
     if (j >= 0) cvalid |= 1u << c;
@@ -1217,8 +1218,10 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
         }
       } else if (cvalid & (1u << c)) {  // diagnostics with q = 1, c = -yhat (kernels.py:158-174, 272-274)
         if (!(nanb & (1u << c))) {
-          // Bounds without NaN (the usual lane): y+ is a clip to [lo, hi], so
-          // its bound violation is 0; y - (y + c + K^T d) = -c - K^T d, so the
+          // Bounds neither NaN nor crossed (the usual lane): y+ is a clip to
+          // [lo, hi], so its bound violation is 0 (with lo > hi it is lo - hi,
+          // which keeps an infeasible sample running to max_iterations, so
+          // such lanes take the full expressions below); y - (y + c + K^T d) = -c - K^T d, so the
           // stationarity clip is the dual term's clip m.  A non-finite y+
           // makes the primal sum non-finite, which the stop test rejects
           // through the gap (kernels.py:172's finiteness).
@@ -1231,7 +1234,7 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
             qd[s] += half * mz * mz + tf * mz;
             qc[s] = __builtin_fmax(qc[s], absv(yv - mz));
           }
-        } else {  // a NaN bound on this lane: the reference's expressions, NaN-propagating
+        } else {  // a NaN or crossed bound on this lane: the reference's expressions, NaN-propagating
 #pragma unroll
           for (int s = 0; s < BT; ++s) {
             const T yv = yn[s], cq = -tg[s];

@@ -184,6 +184,39 @@ def test_known_answer_status_codes():
     assert abs(float(to_np(got.y).sum()) * 1000 - 1000) <= 1e-9
 
 
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_crossed_bounds_keep_running_under_early_stop(dtype):
+    """Samples whose bound rows cross (y0 <= 0 and y0 >= 1: lower > upper) are
+    infeasible; the reference's stop test sees their bound violation
+    (kernels.py:158-175) and never accepts them, so they run to
+    max_iterations with status 1, beside feasible samples of the same batch
+    (y0 in [-1, 1]) that stop on their own.  The resident early-stop kernel
+    (which drops the violation term on lanes whose bounds cannot be violated)
+    and the streaming passes against the oracle."""
+    require_gpu()
+    canon = _cases.canonical_from_dense([[1.0, 1.0]], [[1.0, 0.0], [-1.0, 0.0]], 2)
+    B = 6
+    target = np.array([[0.3, 0.2], [0.5, -0.1], [2.0, 1.0], [-1.0, 0.4], [0.9, 0.9],
+                       [-2.0, 0.5]], dtype)
+    rhs = np.array([[0.5, 0.0, -1.0] if s % 2 == 0 else [0.5, 1.0, 1.0] for s in range(B)],
+                   dtype)
+    crossed = np.arange(B) % 2 == 0
+    cfg = op.Config(max_iterations=500, tolerance=1e-6)
+    want = op.solve(canon, target, rhs, cfg, dtype=dtype)
+    assert np.all(want.iterations[crossed] == 500)
+    assert np.all(want.iterations[~crossed] < 500)
+    plan = plan_for(canon, dtype=dtype)
+    for streaming in (False, True):
+        got = plan.project(target, rhs, max_iterations=500, tolerance=1e-6,
+                           streaming=streaming, timing=True)
+        assert plan.last_timing()["resident"] == (0 if streaming else 1)
+        it = to_np(got.iterations)
+        np.testing.assert_array_equal(it[crossed], 500)
+        np.testing.assert_array_equal(to_np(got.status), want.status)
+        if dtype == np.float64:
+            np.testing.assert_array_equal(it, want.iterations)
+
+
 def test_known_answer_no_constraints_identity():
     """Reference tests/test_regression_chambolle_pock.py:88-95."""
     canon = op.Canonical(n=2, me=0, rows=[], coef=[])
