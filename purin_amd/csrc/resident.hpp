@@ -613,7 +613,7 @@ __global__ __launch_bounds__(1024) void k_resident(Res<T> A) {
 #pragma unroll
     for (int s = 0; s < BT; ++s) {
       const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
-      if (!(A.Ls[e] <= A.Hs[e])) nanb |= 1u << c;  // a NaN or crossed bound
+      if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e] || A.Ls[e] > A.Hs[e]) nanb |= 1u << c;  // NaN or crossed bound
       if ((SB || QP) && j >= 0 && (A.Ls[e] != lo0 || A.Hs[e] != hi0)) same = 0;
     }
     soff_c[c] = j >= 0 ? (uint32_t)A.colent[c * NT + t] * 16u : trash_off;
@@ -1028,7 +1028,10 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
 #pragma unroll
     for (int s = 0; s < BT; ++s) {
       const int64_t e = SB ? (int64_t)(c * NT + t) : (tile * (int64_t)A.Kc + c * NT + t) * BT + s;
-      if (!(A.Ls[e] <= A.Hs[e])) nanb |= 1u << c;  // a NaN or crossed bound
+      // a NaN or crossed bound (written as the two NaN tests and lo > hi: the
+      // single !(lo <= hi) made the per-sample-bounds variant spill 56 B more
+      // per lane and run 24 % slower)
+      if (A.Ls[e] != A.Ls[e] || A.Hs[e] != A.Hs[e] || A.Ls[e] > A.Hs[e]) nanb |= 1u << c;
       if ((SB || QP) && j >= 0 && (A.Ls[e] != lo0 || A.Hs[e] != hi0)) same = 0;
     }
     if (j >= 0) cvalid |= 1u << c;
