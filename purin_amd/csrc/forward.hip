@@ -401,10 +401,13 @@ static int run_resident(purin_cp_plan* p, hipStream_t st, const Layout& L, char*
   }
   // per-sample bounds: the leading column slots' bounds held in the LDS the
   // image leaves free, so the rest stay in L2 (config 2 shape: one slot of
-  // four).  The early-stop kernel does so for the projection (not the QP),
-  // in the room where it would otherwise keep K y of its first row slots.
+  // four).  The early-stop kernel does so for the projection with the plan's
+  // coefficients where four column slots' bounds would crowd the L2 (up to
+  // three row slots), in the room where it would otherwise keep K y of its
+  // first row slots, and in two-plane tiles (the rule of k_resident_early).
   size_t lds_all = lds;
-  if (!o.shared_bounds && (!early || !qp)) {
+  const bool early_lb = !qp && !ps && (BT == 8 || (p->res_mc == 4 && p->res_mr <= 3));
+  if (!o.shared_bounds && (!early || early_lb)) {
     if (early && BT != 8)
       lds_all -= (size_t)res_early_kyl(p->res_mr, p->res_mc) * kResThreads * 16;
     const size_t slot_lds = (size_t)2 * kResThreads * BT * sizeof(T);

@@ -942,10 +942,13 @@ __global__ __launch_bounds__(1024) void k_resident_early(Res<T> A) {
   constexpr uint32_t VB = (uint32_t)sizeof(V);
   const uint32_t red_off = VB == 32 ? 2u * kResPlane : trash_off + 16u;
   const uint32_t dec_off = red_off + 16u * 4u * kResQ * VB;  // [BT] verdicts
-  // per-sample bounds of the projection (plan or per-sample coefficients):
-  // the leading column slots' bounds are held in LDS after the verdicts, in
-  // the room K y would take (k_resident's layout), so K y stays in registers
-  constexpr bool kLB = !SB && !QP;
+  // per-sample bounds of the projection: the leading column slots' bounds are
+  // held in LDS after the verdicts, in the room K y would take (k_resident's
+  // layout), so K y stays in registers.  Only where four column slots'
+  // bounds (4 MB per XCD) would crowd the L2 and the freed room takes a slot
+  // of them (up to three row slots), or where K y is not in LDS anyway
+  // (two-plane tiles); elsewhere the bounds stay in L2 and K y in LDS.
+  constexpr bool kLB = !SB && !QP && !VALS && (VB == 32 || (SLC == 4 && SLR <= 3));
   constexpr int KYL = (VB == 32 || kLB) ? 0 : res_early_kyl(SLR, SLC);
   // [KYL][1024] K y of the first row slots, after the verdicts
   const uint32_t kyl_off = red_off + res_early_extra(VB, BT);
